@@ -1,0 +1,145 @@
+/*
+ * llapis_moe.h -- the MI355X dual-precision MoE expert FFN: entry points
+ * beside the moert island ABI (moert_hip.h).
+ *
+ * All device entry points take device pointers and a hipStream_t passed as
+ * void*, never allocate (scratch comes from the caller: a workspace pointer
+ * and its size, or the island's host->pool_alloc), and launch asynchronously
+ * on that stream.  Functions returning int32_t return 0 on success and a
+ * negative code on a refused call; llapis_last_error() then says why.
+ *
+ * Weight pools hold ggml blocks byte-for-byte (ggml-common.h layouts):
+ * an expert is a contiguous [d_out rows][row_size(type, d_in)] slab and a
+ * pool is slabs back to back.  Type tags are ggml's (ggml.h:390-412).
+ */
+#ifndef LLAPIS_MOE_H
+#define LLAPIS_MOE_H
+
+#include <stdint.h>
+
+#include "moert_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LLAPIS_T_F32 = 0, LLAPIS_T_Q5_0 = 6, LLAPIS_T_Q8_0 = 8, LLAPIS_T_Q8_1 = 9,
+    LLAPIS_T_Q4_K = 12, LLAPIS_T_Q8_K = 15, LLAPIS_T_IQ4_NL = 20, LLAPIS_T_IQ2_S = 22,
+};
+
+/* Activation format of the integer dot products.
+ *  LLAPIS_ACT_CPU:  what the reference CPU path quantises to -- q8_K for
+ *                   256-wide blocks, q8_0 for 32-wide blocks (ggml-cpu.c:
+ *                   250-373 vec_dot_type; quants.c / arch/x86/quants.c).
+ *  LLAPIS_ACT_Q8_1: q8_1 and the per-block arithmetic of ggml-cuda's
+ *                   vec_dot_*_q8_1 (quantize.cu:5-50, vecdotq.cuh). */
+enum { LLAPIS_ACT_CPU = 0, LLAPIS_ACT_Q8_1 = 1 };
+/* GELU of the GEGLU: the CPU's fp16 table (vec.h:1414-1428) or exact tanh
+ * (ggml-cuda unary.cuh:101-104). */
+enum { LLAPIS_GELU_TABLE = 0, LLAPIS_GELU_TANH = 1 };
+
+const char * llapis_last_error(void);
+
+/* Modes used by moert_ffn_moe's matmuls (the island ABI has no field for
+ * them).  Defaults: LLAPIS_ACT_CPU, LLAPIS_GELU_TABLE. */
+void llapis_set_modes(int32_t act_mode, int32_t gelu_mode);
+
+/* ------------------------------------------------------------ host side */
+
+/* Bytes of a row of n values of `type`; 0 if unsupported. */
+uint64_t llapis_row_size(int32_t type, int64_t n);
+
+/* Replaces ggml_quantize_chunk (ggml.c:7761-7800) for Q4_K, Q5_0 (imatrix
+ * NULL), IQ2_S and IQ4_NL (imatrix or NULL), byte-identical output.
+ * Multithreaded on the host.  Returns bytes written, 0 if refused. */
+uint64_t llapis_quantize(int32_t type, const float * src, void * dst, int64_t nrow, int64_t n_per_row,
+                         const float * imatrix);
+
+/* Seeded N(mean, std) synthetic data; element i depends on (seed, offset+i) only. */
+void llapis_synth_normal(uint64_t seed, int64_t offset, int64_t n, float mean, float stddev, float * out);
+
+/* ---------------------------------------------------------- device side */
+
+/* The quantised mul_mat_id service for moert_ffn_moe_host.mm: replaces the
+ * trampoline's call of ggml_cuda_mul_mat_vec_q (ggml-cuda/moe-dual.cu:74-94,
+ * mmvq.cu:470-640).  For channel i < *ne_live (or < n_ids):
+ *   y[i*d_out + r] = W_{ids[i]}[r, :] . b[:, b_ncols == 1 ? 0 : i]
+ * with W_{j} = w_ptrs ? w_ptrs[j] : w_base + j * row_size(w_type, d_in) * d_out,
+ * activations quantised on the fly in the mode set by llapis_set_modes.
+ * Every expert slab must be a multiple of 16 bytes. */
+int32_t llapis_mul_mat_id(const moert_mm_call * call, int32_t w_type, const void * w_base, int64_t w_n,
+                          int32_t d_in, int32_t d_out, void * stream);
+
+/* A ggml tensor as the op sees it (ggml.h ggml_tensor: type, ne, nb, data). */
+typedef struct llapis_tensor {
+    int32_t  type;
+    int64_t  ne[4];
+    uint64_t nb[4];
+    void *   data;
+} llapis_tensor;
+
+/* Replaces ggml_cuda_moe_dual (ggml-cuda/moe-dual.cu:98-157): GGML_OP_MOE_DUAL
+ * with srcs {cur, ids, w_hot, w_cold, exp_slot, slot_exp, slot_state, s_hot,
+ * s_cold} and op_params {kind, top_k, il, cold_type, n_expert, w_cold_dev(2),
+ * s_cold_dev(2), planc_mode} (ggml.c:3322-3370), dst f32 [d_out, n_used, T].
+ * The island's LIFO scratch comes from `workspace` (see
+ * llapis_moe_dual_workspace_size). */
+typedef struct llapis_moe_dual_op {
+    const llapis_tensor * src[9];
+    int32_t op_params[10];
+    llapis_tensor * dst;
+} llapis_moe_dual_op;
+uint64_t llapis_moe_dual_workspace_size(const llapis_moe_dual_op * op);
+int32_t  llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace, uint64_t ws_bytes, void * stream);
+
+/* Router + selection (llama-graph.cpp:1548-1650; ggml-cuda topk-moe.cu:80):
+ * logits = W_r x_t (+ bias), p = softmax, ids = top_k of p (descending, ties
+ * to the lower index), w = p[ids] / max(sum p[ids], 6.103515625e-5).
+ * x [T][d], W_r [n_expert][d] (ggml ne0 = d), bias [n_expert] or NULL,
+ * ids/w [T][top_k], probs [T][n_expert] or NULL.  n_expert <= 256, top_k <= 16. */
+int32_t llapis_router_topk(const float * x, int32_t n_tokens, const float * w_r, const float * bias,
+                           int32_t d, int32_t n_expert, int32_t top_k,
+                           int32_t * ids, float * weights, float * probs, void * stream);
+
+/* GEGLU over the merged gate_up output (llama-graph.cpp:1687-1761):
+ * out[c][i] = gelu(gu[c][i]) * gu[c][n_ff + i] for n_cols columns of 2*n_ff. */
+int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float * out, int32_t gelu_mode,
+                     void * stream);
+
+/* One dual-precision MoE FFN layer: build_moe_ffn's merged gate_up path for
+ * gemma4-style MoE (llama-graph.cpp:1507-1850) with each routed pair computed
+ * at its tier.  Pools are device slabs (see the note at the top):
+ *   hot_gu  [k_slots][2 n_ff][row(hot_gu_type, d_model)]
+ *   hot_dn  [k_slots][d_model][row(hot_dn_type, n_ff)]
+ *   cold_gu [n_expert][2 n_ff][row(cold_gu_type, d_model)]
+ *   cold_dn [n_expert][d_model][row(cold_dn_type, n_ff)]
+ * A pair (t, e) is hot iff exp_slot[e] = s, 0 <= s < k_slots,
+ * slot_state[s] == 2 (READY) and slot_exp[s] == e (ffn_moe.cu:80-130). */
+typedef struct llapis_moe_layer {
+    int32_t d_model, n_ff, n_expert, top_k, k_slots;
+    int32_t hot_gu_type, hot_dn_type, cold_gu_type, cold_dn_type;
+    int32_t act_mode, gelu_mode;
+    const float * router_w;        /* [n_expert][d_model] */
+    const float * router_b;        /* [n_expert] or NULL */
+    const void * hot_gu;  const void * hot_dn;
+    const void * cold_gu; const void * cold_dn;
+    const int32_t * exp_slot;      /* [n_expert] */
+    const int32_t * slot_exp;      /* [k_slots] */
+    const int32_t * slot_state;    /* [k_slots] */
+    const float * s_hot;           /* [k_slots] down scale, or NULL */
+    const float * s_cold;          /* [n_expert] down scale, or NULL */
+} llapis_moe_layer;
+
+/* Device scratch the layer needs for n_tokens (bytes). */
+uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens);
+
+/* out [T][d_model] = the layer applied to x [T][d_model].  ids/weights
+ * ([T][top_k], optional) receive the routing. */
+int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
+                       int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

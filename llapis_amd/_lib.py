@@ -1,0 +1,138 @@
+"""ctypes binding of libllapis_moe.so (include/moert_hip.h + include/llapis_moe.h).
+
+The library is the product: loading fails loudly if it has not been built
+(python -m llapis_amd.build); there is no fallback implementation.
+"""
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libllapis_moe.so"
+
+# ggml type tags (ggml.h:390-412)
+F32, Q5_0, Q8_0, Q8_1, Q4_K, Q8_K, IQ4_NL, IQ2_S = 0, 6, 8, 9, 12, 15, 20, 22
+ACT_CPU, ACT_Q8_1 = 0, 1
+GELU_TABLE, GELU_TANH = 0, 1
+MM_W_HOT, MM_W_COLD_SRC, MM_W_RAW = 0, 1, 2
+SLOT_FREE, SLOT_FILLING, SLOT_READY = 0, 1, 2
+PMAX_MAX = 32
+
+vp, i32, i64, u64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64
+
+
+class MoertCudaConfig(C.Structure):
+    _fields_ = [("counted", i32), ("copy_stream", i32), ("coldcpu", i32), ("coldcpu_max", i32),
+                ("coldcpu_fn", u64), ("cold_guard_fn", u64), ("cold_ffn", i32),
+                ("coldffn_submit_fn", u64), ("coldffn_wait_fn", u64)]
+
+
+class MoertMmCall(C.Structure):
+    _fields_ = [("w_sel", i32), ("w_type_tag", i32), ("w_data", vp), ("w_n", i64), ("b", vp),
+                ("b_ncols", i64), ("ids", vp), ("n_ids", i64), ("y", vp), ("ne_live", vp), ("w_ptrs", vp)]
+
+
+POOL_ALLOC = C.CFUNCTYPE(vp, vp, u64)
+POOL_FREE = C.CFUNCTYPE(None, vp, vp)
+MM_FN = C.CFUNCTYPE(None, vp, C.POINTER(MoertMmCall))
+
+
+class MoertFfnMoeHost(C.Structure):
+    _fields_ = [("user", vp), ("pool_alloc", POOL_ALLOC), ("pool_free", POOL_FREE), ("mm", MM_FN)]
+
+
+class MoertFfnMoeArgs(C.Structure):
+    _fields_ = [("kind", i32), ("top_k", i32), ("il", i32), ("planc_mode", i32), ("n_used", i32),
+                ("n_tokens", i32), ("ids_s1", i32), ("d_in", i32), ("d_out", i32), ("n_expert", i32),
+                ("k", i32), ("cold_type_tag", i32), ("expert_bytes", u64), ("cur", vp), ("ids", vp),
+                ("exp_slot", vp), ("slot_exp", vp), ("slot_state", vp), ("s_hot", vp), ("s_cold", vp),
+                ("w_cold_dev", u64), ("s_cold_dev", u64), ("has_w_cold", i32), ("dst", vp), ("stream", vp)]
+
+
+class MoertCudaStats(C.Structure):
+    _fields_ = [(n, C.c_longlong) for n in ("fires", "op_host_ns", "seam_syncs", "seam_ns", "coldcpu_calls",
+                                            "coldcpu_pairs", "coldcpu_ns", "coldcpu_over_max")]
+
+
+class MoertCudaDirStats(C.Structure):
+    _fields_ = [(n, C.c_longlong) for n in ("async_copies", "async_marks", "bytes", "pub_calls", "pub_copies",
+                                            "sm_copies", "sm_fallback", "sm_timed", "sm_gpu_ns", "sm_gpu_ns_max",
+                                            "sm_ring_copies", "sm_ring_waits")] + \
+               [("sm_ring_wait_ms", C.c_double), ("sm_stage_ms", C.c_double)]
+
+
+class LlapisTensor(C.Structure):
+    _fields_ = [("type", i32), ("ne", i64 * 4), ("nb", u64 * 4), ("data", vp)]
+
+
+class LlapisMoeDualOp(C.Structure):
+    _fields_ = [("src", C.POINTER(LlapisTensor) * 9), ("op_params", i32 * 10), ("dst", C.POINTER(LlapisTensor))]
+
+
+class LlapisMoeLayer(C.Structure):
+    _fields_ = [("d_model", i32), ("n_ff", i32), ("n_expert", i32), ("top_k", i32), ("k_slots", i32),
+                ("hot_gu_type", i32), ("hot_dn_type", i32), ("cold_gu_type", i32), ("cold_dn_type", i32),
+                ("act_mode", i32), ("gelu_mode", i32),
+                ("router_w", vp), ("router_b", vp), ("hot_gu", vp), ("hot_dn", vp), ("cold_gu", vp),
+                ("cold_dn", vp), ("exp_slot", vp), ("slot_exp", vp), ("slot_state", vp), ("s_hot", vp),
+                ("s_cold", vp)]
+
+
+# every symbol the two public headers declare, with its signature
+SIGNATURES = {
+    # moert_hip.h
+    "moert_cuda_configure": (None, [C.POINTER(MoertCudaConfig)]),
+    "moert_ffn_moe": (None, [C.POINTER(MoertFfnMoeArgs), C.POINTER(MoertFfnMoeHost)]),
+    "moert_cuda_route_counts_enable": (i32, [i32, i32]),
+    "moert_cuda_route_counts_fetch": (i32, [vp, i32]),
+    "moert_cuda_host_register_pinned": (i32, [vp, u64]),
+    "moert_cuda_host_unregister": (None, [vp]),
+    "moert_cuda_host_register_mapped": (i32, [vp, u64]),
+    "moert_cuda_host_map": (vp, [vp, u64]),
+    "moert_cuda_stats_get": (None, [C.POINTER(MoertCudaStats)]),
+    "moert_cuda_dir_init": (i32, [i32, i32, i32]),
+    "moert_cuda_dir_async": (i32, [vp, vp, u64]),
+    "moert_cuda_dir_mark": (i64, []),
+    "moert_cuda_dir_poll": (i64, [i32]),
+    "moert_cuda_publish_h2d": (i32, [i32, vp, vp, vp]),
+    "moert_cuda_dir_stats_get": (None, [C.POINTER(MoertCudaDirStats)]),
+    "moert_cuda_dir_gate": (i64, [i32, i64]),
+    "moert_cuda_set_hot_table": (None, [i32, i32, vp, i32, i32]),
+    # llapis_moe.h
+    "llapis_last_error": (C.c_char_p, []),
+    "llapis_set_modes": (None, [i32, i32]),
+    "llapis_row_size": (u64, [i32, i64]),
+    "llapis_quantize": (u64, [i32, vp, vp, i64, i64, vp]),
+    "llapis_synth_normal": (None, [u64, i64, i64, C.c_float, C.c_float, vp]),
+    "llapis_mul_mat_id": (i32, [C.POINTER(MoertMmCall), i32, vp, i64, i32, i32, vp]),
+    "llapis_moe_dual_workspace_size": (u64, [C.POINTER(LlapisMoeDualOp)]),
+    "llapis_moe_dual_compute": (i32, [C.POINTER(LlapisMoeDualOp), vp, u64, vp]),
+    "llapis_router_topk": (i32, [vp, i32, vp, vp, i32, i32, i32, vp, vp, vp, vp]),
+    "llapis_geglu": (i32, [vp, i32, i32, vp, i32, vp]),
+    "llapis_moe_ffn_workspace_size": (u64, [C.POINTER(LlapisMoeLayer), i32]),
+    "llapis_moe_ffn": (i32, [C.POINTER(LlapisMoeLayer), vp, i32, vp, vp, vp, vp, u64, vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded once).  Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m llapis_amd.build` first")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class LlapisError(RuntimeError):
+    pass
+
+
+def check(rc, what):
+    if rc != 0:
+        raise LlapisError(f"{what}: {lib().llapis_last_error().decode()}")

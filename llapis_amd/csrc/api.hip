@@ -1,0 +1,561 @@
+// api.hip -- host side of the C ABI: the moert island (moert_hip.h) and the
+// llapis entry points (llapis_moe.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/llapis_moe.h"
+#include "device.h"
+#include "formats.h"
+#include "launch.h"
+
+using namespace llapis;
+
+namespace {
+
+// The island's error contract (ffn_moe.cu:38-46): a device-API failure prints
+// and aborts.
+#define MOERT_HIP_CHECK(expr)                                                                       \
+    do {                                                                                            \
+        const hipError_t err_ = (expr);                                                             \
+        if (err_ != hipSuccess) {                                                                   \
+            fprintf(stderr, "moert/hip: HIP error %s at %s:%d: %s\n", hipGetErrorName(err_), __FILE__, \
+                    __LINE__, hipGetErrorString(err_));                                             \
+            abort();                                                                                \
+        }                                                                                           \
+    } while (0)
+
+thread_local std::string g_err;
+
+int32_t fail(const std::string & msg) {
+    g_err = msg;
+    return -1;
+}
+
+#define LL_TRY(expr)                                                                 \
+    do {                                                                             \
+        const hipError_t e_ = (expr);                                                \
+        if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+std::atomic<int> g_act_mode{LLAPIS_ACT_CPU};
+std::atomic<int> g_gelu_mode{LLAPIS_GELU_TABLE};
+
+moert_cuda_config g_cfg = [] {
+    moert_cuda_config c;
+    moert_cuda_config_defaults(&c);
+    return c;
+}();
+
+// device routing counters: [n_layers][n_expert] then [n_layers][2]
+struct RouteCounters {
+    int32_t * dev = nullptr;
+    int32_t nl = 0, ne = 0;
+    bool on = false;
+    size_t n_ints() const { return (size_t)nl * ne + (size_t)nl * 2; }
+} g_rc;
+std::mutex g_rc_mu;
+
+std::atomic<long long> g_fires{0}, g_op_ns{0};
+
+struct HotTable {
+    const void * const * ptrs = nullptr;
+    int32_t n = 0, type = 0;
+};
+HotTable g_hot_tab[128][2];
+
+long long now_ns() {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+bool is_gu_type(int t) { return t == T_Q4_K || t == T_IQ2_S; }
+bool is_dn_type(int t) { return t == T_Q5_0 || t == T_IQ4_NL; }
+bool supported_w(int t) { return is_gu_type(t) || is_dn_type(t); }
+
+uint64_t rbytes(int t, int64_t n) { return (n % blk_elems(t)) ? 0 : row_bytes(t, n); }
+
+}  // namespace
+
+extern "C" {
+
+const char * llapis_last_error(void) { return g_err.c_str(); }
+
+void llapis_set_modes(int32_t act_mode, int32_t gelu_mode) {
+    g_act_mode = act_mode == LLAPIS_ACT_Q8_1 ? LLAPIS_ACT_Q8_1 : LLAPIS_ACT_CPU;
+    g_gelu_mode = gelu_mode == LLAPIS_GELU_TANH ? LLAPIS_GELU_TANH : LLAPIS_GELU_TABLE;
+}
+
+// ------------------------------------------------------------ mm service
+
+int32_t llapis_mul_mat_id(const moert_mm_call * c, int32_t w_type, const void * w_base, int64_t w_n, int32_t d_in,
+                          int32_t d_out, void * stream) {
+    if (!c) return fail("llapis_mul_mat_id: null call");
+    if (!supported_w(w_type)) return fail("llapis_mul_mat_id: unsupported weight type " + std::to_string(w_type));
+    const uint64_t rb = rbytes(w_type, d_in);
+    if (!rb || d_in > dev::MAX_D_IN) return fail("llapis_mul_mat_id: d_in does not fit the format");
+    const uint64_t eb = rb * (uint64_t)d_out;
+    if (eb % 16) return fail("llapis_mul_mat_id: expert slab is not a multiple of 16 bytes");
+    if (c->n_ids <= 0) return 0;
+    if (c->b_ncols != 1 && c->b_ncols != c->n_ids) return fail("llapis_mul_mat_id: b_ncols must be 1 or n_ids");
+    MmvParams p = {};
+    p.mode = MMV_COMPACT;
+    p.d_in = d_in;
+    p.d_out = d_out;
+    p.w0 = static_cast<const uint8_t *>(w_base);
+    p.stride0 = eb;
+    p.ptrs0 = c->w_ptrs;
+    p.n0 = w_n;
+    p.ids = static_cast<const int32_t *>(c->ids);
+    p.ne_live = c->ne_live;
+    p.b_ncols = (int)c->b_ncols;
+    p.act = static_cast<const float *>(c->b);
+    p.act_ld = d_in;
+    p.y = static_cast<float *>(c->y);
+    mmv_prepare(p, w_type, w_type);
+    LL_TRY(launch_mmv(p, w_type, w_type, g_act_mode.load(), dev::SRC_PLAIN, (int)c->n_ids, (hipStream_t)stream));
+    return 0;
+}
+
+// --------------------------------------------------------------- island
+
+void moert_cuda_configure(const moert_cuda_config * cfg) {
+    if (cfg) g_cfg = *cfg;
+}
+
+int32_t moert_cuda_route_counts_enable(int32_t n_layers, int32_t n_expert) {
+    if (n_layers <= 0 || n_expert <= 0) return 0;
+    std::lock_guard<std::mutex> lk(g_rc_mu);
+    if (g_rc.on && g_rc.nl == n_layers && g_rc.ne == n_expert) return 1;
+    if (g_rc.dev) {
+        MOERT_HIP_CHECK(hipFree(g_rc.dev));
+        g_rc.dev = nullptr;
+        g_rc.on = false;
+    }
+    g_rc.nl = n_layers;
+    g_rc.ne = n_expert;
+    const size_t bytes = g_rc.n_ints() * sizeof(int32_t);
+    if (hipMalloc(&g_rc.dev, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        g_rc.nl = g_rc.ne = 0;
+        g_rc.dev = nullptr;
+        return 0;
+    }
+    MOERT_HIP_CHECK(hipMemset(g_rc.dev, 0, bytes));
+    g_rc.on = true;
+    return 1;
+}
+
+int32_t moert_cuda_route_counts_fetch(int32_t * dst, int32_t reset) {
+    std::lock_guard<std::mutex> lk(g_rc_mu);
+    if (!g_rc.on || !dst) return 0;
+    const size_t n = g_rc.n_ints();
+    MOERT_HIP_CHECK(hipDeviceSynchronize());
+    MOERT_HIP_CHECK(hipMemcpy(dst, g_rc.dev, n * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (reset) MOERT_HIP_CHECK(hipMemset(g_rc.dev, 0, n * sizeof(int32_t)));
+    return (int32_t)n;
+}
+
+int32_t moert_cuda_host_register_pinned(void *, uint64_t) { return 0; }
+void moert_cuda_host_unregister(void *) {}
+int32_t moert_cuda_host_register_mapped(void *, uint64_t) { return 0; }
+void * moert_cuda_host_map(void *, uint64_t) { return nullptr; }
+
+void moert_cuda_stats_get(moert_cuda_stats * out) {
+    if (!out) return;
+    memset(out, 0, sizeof(*out));
+    out->fires = g_fires.load();
+    out->op_host_ns = g_op_ns.load();
+}
+
+int32_t moert_cuda_dir_init(int32_t, int32_t, int32_t) { return 0; }
+int32_t moert_cuda_dir_async(void *, const void *, uint64_t) { return 0; }
+int64_t moert_cuda_dir_mark(void) { return -1; }
+int64_t moert_cuda_dir_poll(int32_t) { return -1; }
+int32_t moert_cuda_publish_h2d(int32_t n, void * const * dsts, const void * const * srcs, const uint64_t * sizes) {
+    for (int32_t i = 0; i < n; ++i) MOERT_HIP_CHECK(hipMemcpy(dsts[i], srcs[i], sizes[i], hipMemcpyHostToDevice));
+    return 1;
+}
+void moert_cuda_dir_stats_get(moert_cuda_dir_stats * out) {
+    if (out) memset(out, 0, sizeof(*out));
+}
+int64_t moert_cuda_dir_gate(int32_t, int64_t) { return -1; }
+
+void moert_cuda_set_hot_table(int32_t il, int32_t kind, const void * const * dev_ptrs, int32_t n, int32_t type_tag) {
+    if (il < 0 || il >= 128 || kind < 0 || kind > 1) return;
+    g_hot_tab[il][kind].ptrs = n > 0 ? dev_ptrs : nullptr;
+    g_hot_tab[il][kind].n = n > 0 ? n : 0;
+    g_hot_tab[il][kind].type = type_tag;
+}
+
+// One (layer, kind) fire (ffn_moe.cu:892-1246 with the cold pool in HBM):
+// partition -> [gather] -> hot mm -> cold mm -> scatter, scratch from the
+// host's LIFO pool in a fixed order and released in reverse.
+void moert_ffn_moe(const moert_ffn_moe_args * a, const moert_ffn_moe_host * h) {
+    const long long t0 = now_ns();
+    const int kind = a->kind;
+    const int n_used = a->n_used, n_tokens = a->n_tokens;
+    const int Pmax = n_used * n_tokens;
+    const int D_in = a->d_in, D_out = a->d_out;
+    hipStream_t stream = (hipStream_t)a->stream;
+    if (a->planc_mode != 0 || !a->has_w_cold) {
+        fprintf(stderr, "moert/hip: planc_mode %d / has_w_cold %d: only an HBM-resident cold pool is supported\n",
+                a->planc_mode, a->has_w_cold);
+        abort();
+    }
+    if (Pmax <= 0 || Pmax > MOERT_COLDCPU_GS_PMAX_MAX) {
+        fprintf(stderr, "moert/hip: %d routed pairs per fire (max %d)\n", Pmax, MOERT_COLDCPU_GS_PMAX_MAX);
+        abort();
+    }
+    const bool gather_x = (kind != 0 || n_tokens > 1);
+
+    void * scratch[16];
+    int n_scratch = 0;
+    auto pool_alloc = [&](uint64_t nbytes) -> void * {
+        void * p = h->pool_alloc(h->user, nbytes);
+        scratch[n_scratch++] = p;
+        return p;
+    };
+    float * x_hot = (float *)pool_alloc((uint64_t)D_in * Pmax * sizeof(float));
+    float * x_cold = (float *)pool_alloc((uint64_t)D_in * Pmax * sizeof(float));
+    int32_t * ids_hot = (int32_t *)pool_alloc((uint64_t)Pmax * sizeof(int32_t));
+    int32_t * ids_cold = (int32_t *)pool_alloc((uint64_t)Pmax * sizeof(int32_t));
+    int32_t * hot_dst = (int32_t *)pool_alloc((uint64_t)Pmax * sizeof(int32_t));
+    int32_t * cold_dst = (int32_t *)pool_alloc((uint64_t)Pmax * sizeof(int32_t));
+    int32_t * counts = (int32_t *)pool_alloc(2 * sizeof(int32_t));
+    float * y_hot = (float *)pool_alloc((uint64_t)D_out * Pmax * sizeof(float));
+    float * y_cold = (float *)pool_alloc((uint64_t)D_out * Pmax * sizeof(float));
+
+    int32_t * rc_counts = nullptr, * rc_hits = nullptr;
+    if (g_rc.on && kind == 0 && a->il >= 0 && a->il < g_rc.nl) {
+        rc_counts = g_rc.dev + (size_t)a->il * g_rc.ne;
+        rc_hits = g_rc.dev + (size_t)g_rc.nl * g_rc.ne + (size_t)a->il * 2;
+    }
+    if (!g_cfg.counted) {          // padded channels read id 0 and, when gathered, x = 0
+        MOERT_HIP_CHECK(hipMemsetAsync(ids_hot, 0, (size_t)Pmax * sizeof(int32_t), stream));
+        MOERT_HIP_CHECK(hipMemsetAsync(ids_cold, 0, (size_t)Pmax * sizeof(int32_t), stream));
+        if (gather_x) {
+            MOERT_HIP_CHECK(hipMemsetAsync(x_hot, 0, (size_t)D_in * Pmax * sizeof(float), stream));
+            MOERT_HIP_CHECK(hipMemsetAsync(x_cold, 0, (size_t)D_in * Pmax * sizeof(float), stream));
+        }
+    }
+    MOERT_HIP_CHECK(launch_partition((const int32_t *)a->ids, n_used, a->ids_s1, Pmax, (const int32_t *)a->exp_slot,
+                                     (const int32_t *)a->slot_exp, (const int32_t *)a->slot_state, a->n_expert, a->k,
+                                     ids_hot, ids_cold, hot_dst, cold_dst, counts, rc_counts, rc_hits, stream));
+    if (gather_x)
+        MOERT_HIP_CHECK(launch_gather((const float *)a->cur, D_in, kind, n_used, counts, hot_dst, cold_dst, x_hot,
+                                      x_cold, Pmax, stream));
+    const int32_t * ne_hot = g_cfg.counted ? counts : nullptr;
+    const int32_t * ne_cold = g_cfg.counted ? counts + 1 : nullptr;
+    {
+        moert_mm_call c = {};
+        c.w_sel = MOERT_MM_W_HOT;
+        if (a->il >= 0 && a->il < 128 && (kind == 0 || kind == 1)) {
+            const HotTable & ht = g_hot_tab[a->il][kind];
+            if (ht.ptrs && ht.n == a->k) {
+                c.w_sel = MOERT_MM_W_RAW;
+                c.w_type_tag = ht.type;
+                c.w_n = a->k;
+                c.w_ptrs = ht.ptrs;
+                c.w_data = (const void *)ht.ptrs;
+            }
+        }
+        c.b = gather_x ? (const void *)x_hot : a->cur;
+        c.b_ncols = gather_x ? Pmax : 1;
+        c.ids = ids_hot;
+        c.n_ids = Pmax;
+        c.y = y_hot;
+        c.ne_live = ne_hot;
+        h->mm(h->user, &c);
+    }
+    {
+        moert_mm_call c = {};
+        c.w_sel = MOERT_MM_W_COLD_SRC;
+        c.b = gather_x ? (const void *)x_cold : a->cur;
+        c.b_ncols = gather_x ? Pmax : 1;
+        c.ids = ids_cold;
+        c.n_ids = Pmax;
+        c.y = y_cold;
+        c.ne_live = ne_cold;
+        h->mm(h->user, &c);
+    }
+    MOERT_HIP_CHECK(launch_scatter(y_hot, y_cold, D_out, kind, counts, ids_hot, hot_dst, ids_cold, cold_dst,
+                                   (const float *)a->s_hot, (const float *)a->s_cold, (float *)a->dst, Pmax, stream));
+    for (int i = n_scratch - 1; i >= 0; --i) h->pool_free(h->user, scratch[i]);
+    g_op_ns += now_ns() - t0;
+    ++g_fires;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------- trampoline
+
+namespace {
+
+// LIFO bump allocator over the caller's workspace (the ggml pool contract:
+// frees in exact reverse order of allocation within one fire).
+struct HostCtx {
+    uint8_t * base = nullptr;
+    uint64_t cap = 0, top = 0;
+    struct Rec { void * p; uint64_t prev_top; } stack[16];
+    int n = 0;
+    const llapis_tensor * w_hot = nullptr;
+    const llapis_tensor * w_cold = nullptr;
+    int32_t d_in = 0, d_out = 0;
+    bool failed = false;
+};
+
+void * host_pool_alloc(void * user, uint64_t nbytes) {
+    HostCtx * hc = (HostCtx *)user;
+    const uint64_t at = (hc->top + 255) & ~uint64_t(255);
+    if (hc->n >= 16 || at + nbytes > hc->cap) {
+        fprintf(stderr, "moert/hip: workspace exhausted (%llu + %llu > %llu)\n", (unsigned long long)at,
+                (unsigned long long)nbytes, (unsigned long long)hc->cap);
+        abort();
+    }
+    hc->stack[hc->n++] = {hc->base + at, hc->top};
+    hc->top = at + nbytes;
+    return hc->base + at;
+}
+
+void host_pool_free(void * user, void * ptr) {
+    HostCtx * hc = (HostCtx *)user;
+    if (hc->n <= 0 || hc->stack[hc->n - 1].p != ptr) {
+        fprintf(stderr, "moert/hip: pool free must be LIFO\n");
+        abort();
+    }
+    hc->top = hc->stack[--hc->n].prev_top;
+}
+
+thread_local hipStream_t g_tramp_stream = nullptr;
+
+void host_mm_stream(void * user, const moert_mm_call * c) {
+    HostCtx * hc = (HostCtx *)user;
+    int32_t type;
+    const void * base;
+    int64_t n;
+    if (c->w_sel == MOERT_MM_W_HOT) {
+        type = hc->w_hot->type; base = hc->w_hot->data; n = hc->w_hot->ne[2];
+    } else if (c->w_sel == MOERT_MM_W_COLD_SRC) {
+        type = hc->w_cold->type; base = hc->w_cold->data; n = hc->w_cold->ne[2];
+    } else {
+        type = c->w_type_tag; base = c->w_data; n = c->w_n;
+    }
+    moert_mm_call cc = *c;
+    if (c->w_sel != MOERT_MM_W_RAW) cc.w_ptrs = nullptr;
+    if (llapis_mul_mat_id(&cc, type, base, n, hc->d_in, hc->d_out, (void *)g_tramp_stream) != 0) {
+        fprintf(stderr, "moert/hip: mul_mat_id refused: %s\n", llapis_last_error());
+        abort();
+    }
+}
+
+uint64_t fire_scratch_bytes(int d_in, int d_out, int pmax) {
+    auto al = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
+    return 2 * al((uint64_t)d_in * pmax * 4) + 4 * al((uint64_t)pmax * 4) + al(8) + 2 * al((uint64_t)d_out * pmax * 4) +
+           256;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t llapis_moe_dual_workspace_size(const llapis_moe_dual_op * op) {
+    if (!op || !op->src[0] || !op->src[1] || !op->src[2]) return 0;
+    const int d_in = (int)op->src[0]->ne[0];
+    const int d_out = (int)op->src[2]->ne[1];
+    const int pmax = (int)(op->src[1]->ne[0] * op->src[1]->ne[1]);
+    return fire_scratch_bytes(d_in, d_out, pmax);
+}
+
+int32_t llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace, uint64_t ws_bytes, void * stream) {
+    if (!op || !op->dst) return fail("llapis_moe_dual_compute: null op");
+    for (int i : {0, 1, 2, 3, 4, 5, 6})
+        if (!op->src[i]) return fail("llapis_moe_dual_compute: missing src " + std::to_string(i));
+    const llapis_tensor * cur = op->src[0];
+    const llapis_tensor * ids = op->src[1];
+    const llapis_tensor * w_hot = op->src[2];
+    const llapis_tensor * w_cold = op->src[3];
+    const int32_t * prm = op->op_params;
+    moert_ffn_moe_args a = {};
+    a.kind = prm[0];
+    a.top_k = prm[1];
+    a.il = prm[2];
+    a.planc_mode = prm[9];
+    a.n_used = (int32_t)ids->ne[0];
+    a.n_tokens = (int32_t)ids->ne[1];
+    a.ids_s1 = (int32_t)(ids->nb[1] / sizeof(int32_t));
+    a.d_in = (int32_t)cur->ne[0];
+    a.d_out = (int32_t)w_hot->ne[1];
+    a.n_expert = (int32_t)w_cold->ne[2];
+    a.k = (int32_t)op->src[5]->ne[0];
+    a.cold_type_tag = w_cold->type;
+    a.expert_bytes = rbytes(w_cold->type, a.d_in) * (uint64_t)a.d_out;
+    a.cur = cur->data;
+    a.ids = ids->data;
+    a.exp_slot = op->src[4]->data;
+    a.slot_exp = op->src[5]->data;
+    a.slot_state = op->src[6]->data;
+    a.s_hot = op->src[7] ? op->src[7]->data : nullptr;
+    a.s_cold = op->src[8] ? op->src[8]->data : nullptr;
+    memcpy(&a.w_cold_dev, &prm[5], sizeof(uint64_t));
+    memcpy(&a.s_cold_dev, &prm[7], sizeof(uint64_t));
+    a.has_w_cold = 1;
+    a.dst = op->dst->data;
+    a.stream = stream;
+    if (a.n_used * a.n_tokens > MOERT_COLDCPU_GS_PMAX_MAX)
+        return fail("llapis_moe_dual_compute: more than 32 routed pairs per fire");
+    if (a.planc_mode != 0) return fail("llapis_moe_dual_compute: planc_mode must be 0 (cold pool in HBM)");
+    if (ws_bytes < fire_scratch_bytes(a.d_in, a.d_out, a.n_used * a.n_tokens))
+        return fail("llapis_moe_dual_compute: workspace too small");
+    if (!supported_w(w_hot->type) || w_hot->type == T_F32 || !supported_w(w_cold->type))
+        return fail("llapis_moe_dual_compute: unsupported pool type");
+
+    HostCtx hc;
+    hc.base = static_cast<uint8_t *>(workspace);
+    hc.cap = ws_bytes;
+    hc.w_hot = w_hot;
+    hc.w_cold = w_cold;
+    hc.d_in = a.d_in;
+    hc.d_out = a.d_out;
+    g_tramp_stream = (hipStream_t)stream;
+    moert_ffn_moe_host h;
+    h.user = &hc;
+    h.pool_alloc = &host_pool_alloc;
+    h.pool_free = &host_pool_free;
+    h.mm = &host_mm_stream;
+    moert_ffn_moe(&a, &h);
+    if (hc.n != 0) return fail("llapis_moe_dual_compute: island did not release its scratch");
+    return 0;
+}
+
+// -------------------------------------------------------- router / GEGLU
+
+int32_t llapis_router_topk(const float * x, int32_t n_tokens, const float * w_r, const float * bias, int32_t d,
+                           int32_t n_expert, int32_t top_k, int32_t * ids, float * weights, float * probs,
+                           void * stream) {
+    if (n_tokens <= 0) return 0;
+    if (!x || !w_r || !ids || !weights || !probs) return fail("llapis_router_topk: null pointer (probs is required)");
+    if (n_expert <= 0 || n_expert > 256 || top_k <= 0 || top_k > 16 || top_k > n_expert)
+        return fail("llapis_router_topk: need 0 < top_k <= 16, top_k <= n_expert <= 256");
+    hipStream_t s = (hipStream_t)stream;
+    LL_TRY(launch_router_logits(x, n_tokens, w_r, bias, d, n_expert, probs, s));
+    LL_TRY(launch_topk(probs, n_tokens, n_expert, top_k, ids, weights, s));
+    return 0;
+}
+
+int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float * out, int32_t gelu_mode,
+                     void * stream) {
+    if (n_cols <= 0 || n_ff <= 0) return 0;
+    LL_TRY(launch_geglu(gate_up, n_ff, n_cols, out, gelu_mode, (hipStream_t)stream));
+    return 0;
+}
+
+// ------------------------------------------------------------- fused layer
+
+namespace {
+struct FfnWs {
+    uint64_t probs, ids, w, ygu, ydn, total;
+};
+FfnWs ffn_ws(const llapis_moe_layer * L, int32_t T) {
+    auto al = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
+    const uint64_t P = (uint64_t)T * L->top_k;
+    FfnWs w;
+    w.probs = 0;
+    w.ids = w.probs + al((uint64_t)T * L->n_expert * 4);
+    w.w = w.ids + al(P * 4);
+    w.ygu = w.w + al(P * 4);
+    w.ydn = w.ygu + al(P * 2 * L->n_ff * 4);
+    w.total = w.ydn + al(P * L->d_model * 4);
+    return w;
+}
+}  // namespace
+
+uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
+    if (!L || n_tokens <= 0) return 0;
+    return ffn_ws(L, n_tokens).total;
+}
+
+int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
+                       float * w_out, void * workspace, uint64_t ws_bytes, void * stream) {
+    if (!L) return fail("llapis_moe_ffn: null layer");
+    if (T <= 0) return 0;
+    if (!is_gu_type(L->hot_gu_type) || !is_gu_type(L->cold_gu_type) || !is_dn_type(L->hot_dn_type) ||
+        !is_dn_type(L->cold_dn_type))
+        return fail("llapis_moe_ffn: gate_up pools must be Q4_K/IQ2_S and down pools Q5_0/IQ4_NL");
+    if (L->d_model % 256 || L->n_ff % 32 || L->d_model > dev::MAX_D_IN || L->n_ff > dev::MAX_D_IN)
+        return fail("llapis_moe_ffn: d_model must be a multiple of 256 and n_ff of 32");
+    if (L->k_slots > 0 && (!L->hot_gu || !L->hot_dn || !L->exp_slot || !L->slot_exp || !L->slot_state))
+        return fail("llapis_moe_ffn: hot pool or residency mirrors missing");
+    if (!L->cold_gu || !L->cold_dn || !L->router_w) return fail("llapis_moe_ffn: cold pool or router missing");
+    const uint64_t gu_hot = rbytes(L->hot_gu_type, L->d_model) * 2 * L->n_ff;
+    const uint64_t gu_cold = rbytes(L->cold_gu_type, L->d_model) * 2 * L->n_ff;
+    const uint64_t dn_hot = rbytes(L->hot_dn_type, L->n_ff) * L->d_model;
+    const uint64_t dn_cold = rbytes(L->cold_dn_type, L->n_ff) * L->d_model;
+    if ((gu_hot | gu_cold | dn_hot | dn_cold) % 16) return fail("llapis_moe_ffn: expert slabs must be multiples of 16 bytes");
+    const FfnWs ws = ffn_ws(L, T);
+    if (!workspace || ws_bytes < ws.total) return fail("llapis_moe_ffn: workspace too small");
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t * base = static_cast<uint8_t *>(workspace);
+    float * probs = (float *)(base + ws.probs);
+    int32_t * ids = ids_out ? ids_out : (int32_t *)(base + ws.ids);
+    float * w = w_out ? w_out : (float *)(base + ws.w);
+    float * ygu = (float *)(base + ws.ygu);
+    float * ydn = (float *)(base + ws.ydn);
+    const int P = T * L->top_k;
+
+    LL_TRY(launch_router_logits(x, T, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
+    LL_TRY(launch_topk(probs, T, L->n_expert, L->top_k, ids, w, s));
+
+    MmvParams p = {};
+    p.mode = MMV_ROUTED;
+    p.top_k = L->top_k;
+    p.ids_s1 = L->top_k;
+    p.n_expert = L->n_expert;
+    p.k_slots = L->k_slots;
+    p.exp_slot = L->exp_slot;
+    p.slot_exp = L->slot_exp;
+    p.slot_state = L->slot_state;
+    p.ids = ids;
+    // gate_up: activation column = token
+    p.d_in = L->d_model;
+    p.d_out = 2 * L->n_ff;
+    p.w0 = static_cast<const uint8_t *>(L->hot_gu);
+    p.stride0 = gu_hot;
+    p.n0 = L->k_slots;
+    p.w1 = static_cast<const uint8_t *>(L->cold_gu);
+    p.stride1 = gu_cold;
+    p.n1 = L->n_expert;
+    p.act = x;
+    p.act_ld = L->d_model;
+    p.act_by_token = 1;
+    p.y = ygu;
+    mmv_prepare(p, L->hot_gu_type, L->cold_gu_type);
+    LL_TRY(launch_mmv(p, L->hot_gu_type, L->cold_gu_type, L->act_mode, dev::SRC_PLAIN, P, s));
+    // down: activation column = pair, GEGLU of its gate_up output on the fly
+    p.d_in = L->n_ff;
+    p.d_out = L->d_model;
+    p.w0 = static_cast<const uint8_t *>(L->hot_dn);
+    p.stride0 = dn_hot;
+    p.w1 = static_cast<const uint8_t *>(L->cold_dn);
+    p.stride1 = dn_cold;
+    p.s0 = L->s_hot;
+    p.s1 = L->s_cold;
+    p.act = ygu;
+    p.act_ld = 2 * L->n_ff;
+    p.act_by_token = 0;
+    p.y = ydn;
+    mmv_prepare(p, L->hot_dn_type, L->cold_dn_type);
+    const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+    LL_TRY(launch_mmv(p, L->hot_dn_type, L->cold_dn_type, L->act_mode, src, P, s));
+    LL_TRY(launch_combine(ydn, w, T, L->top_k, L->d_model, out, s));
+    return 0;
+}
+
+}  // extern "C"

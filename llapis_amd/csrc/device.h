@@ -1,0 +1,442 @@
+// device.h -- device-side building blocks shared by the gfx950 kernels:
+// LDS addressing, activation quantisation into LDS, and the per-unit integer
+// dot products of the four weight formats against q8 activations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "formats.h"
+
+namespace llapis {
+namespace dev {
+
+constexpr int WG = 256;         // threads per workgroup (4 wave64)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // one 128-bit load/store
+constexpr int MAX_D_IN = 8192;  // longest activation column a workgroup quantises
+
+// Activation modes (llapis_moe.h LLAPIS_ACT_*) and activation sources.
+enum { AM_CPU = 0, AM_Q8_1 = 1 };
+enum { SRC_PLAIN = 0, SRC_GEGLU_TABLE = 1, SRC_GEGLU_TANH = 2 };
+
+// --------------------------------------------------------------- LDS views
+
+// Byte offsets inside the dynamic LDS block of one workgroup.
+struct LdsLayout {
+    int w;        // staged weight bytes (16-aligned)
+    int q;        // int8 activation values, d_in bytes
+    int d32;      // float per 32 values (q8_0 / q8_1 scale)
+    int s32;      // float per 32 values (q8_1 sum)
+    int dK;       // float per 256 values (q8_K scale)
+    int bsum;     // int per 16 values (q8_K block sums)
+    int grid;     // IQ2_S codebook, 1024 x uint2
+    int sign;     // IQ2_S sign masks, 256 x uint4
+    int total;
+};
+
+LL_HD inline int align16(int x) { return (x + 15) & ~15; }
+
+LL_HD inline LdsLayout lds_layout(int w_bytes, int d_in, bool iq2_tables) {
+    LdsLayout L;
+    L.w = 0;
+    L.q = align16(w_bytes + 16);            // +16: funnel reads may touch one dword past the end
+    L.d32 = align16(L.q + d_in + 16);
+    L.s32 = align16(L.d32 + (d_in / 32) * 4);
+    L.dK = align16(L.s32 + (d_in / 32) * 4);
+    L.bsum = align16(L.dK + (d_in / 256 + 1) * 4);
+    L.grid = align16(L.bsum + (d_in / 16) * 4);
+    L.sign = L.grid + (iq2_tables ? 1024 * 8 : 0);
+    L.total = L.sign + (iq2_tables ? 256 * 16 : 0);
+    return L;
+}
+
+#if defined(__HIPCC__)
+
+__device__ __forceinline__ uint32_t lds32(const uint8_t * smem, int off) {       // off % 4 == 0
+    return *reinterpret_cast<const uint32_t *>(smem + off);
+}
+// a dword at an even (2-aligned) byte offset
+__device__ __forceinline__ uint32_t lds32u(const uint8_t * smem, int off) {
+    const int a = off & ~3;
+    const uint32_t lo = *reinterpret_cast<const uint32_t *>(smem + a);
+    const uint32_t hi = *reinterpret_cast<const uint32_t *>(smem + a + 4);
+    return __builtin_amdgcn_alignbit(hi, lo, (off & 3) * 8);
+}
+
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    const uint16_t h = (uint16_t)h16;
+    _Float16 f;
+    __builtin_memcpy(&f, &h, 2);
+    return (float)f;
+}
+__device__ __forceinline__ float round_to_half(float x) { return (float)(_Float16)x; }
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w0, uint32_t w1, int i) {   // byte i (0..7) of w1:w0
+    const uint32_t w = i < 4 ? w0 : w1;
+    return (w >> ((i & 3) * 8)) & 0xFF;
+}
+
+// ----------------------------------------------------- GELU (exact tanh)
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float GELU_COEF_A = 0.044715f;
+    const float SQRT_2_OVER_PI = 0.79788456080286535587989211986876f;
+    return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
+}
+
+// GEGLU of one element in a given mode.  Table mode reproduces the CPU's
+// fp16 lookup (vec.h:1414-1428): gelu evaluated at fp16(g), rounded to fp16.
+template <int SRC>
+__device__ __forceinline__ float geglu1(float g, float u) {
+    if (SRC == SRC_GEGLU_TANH) return __fmul_rn(gelu_tanh(g), u);
+    if (g <= -10.0f) return 0.0f;
+    if (g >= 10.0f) return __fmul_rn(g, u);
+    return __fmul_rn(round_to_half(gelu_tanh(round_to_half(g))), u);
+}
+
+// ----------------------------------------------- wave reductions (wave64)
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---------------------------------------- activation quantisation into LDS
+
+// Source element k of activation column `col`.
+struct ActSrc {
+    const float * p;   // SRC_PLAIN: column base; GEGLU: merged gate_up column base
+    int n;             // d_in (GEGLU: n_ff; up half starts at p + n)
+};
+
+template <int SRC>
+__device__ __forceinline__ float act_at(const ActSrc & s, int k) {
+    if (SRC == SRC_PLAIN) return s.p[k];
+    return geglu1<SRC>(s.p[k], s.p[s.n + k]);
+}
+
+// q8_K of d_in values (ggml-quants.c:2696-2733): one wave per 256-block.
+// max is the first element of largest magnitude; iscale = -127/max;
+// q = min(127, nearest_int(iscale x)); d = 1/iscale; bsums over 16.
+template <int SRC>
+__device__ __forceinline__ void quantize_q8_K_lds(uint8_t * smem, const LdsLayout & L, const ActSrc & src, int d_in) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int8_t * q = reinterpret_cast<int8_t *>(smem + L.q);
+    float * dK = reinterpret_cast<float *>(smem + L.dK);
+    int * bsum = reinterpret_cast<int *>(smem + L.bsum);
+    for (int b = wave; b < d_in / 256; b += WG / 64) {
+        float v[4];
+        uint64_t key = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int pos = lane + 64 * j;
+            v[j] = act_at<SRC>(src, b * 256 + pos);
+            const uint64_t k = ((uint64_t)__float_as_uint(fabsf(v[j])) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)pos);
+            key = k > key ? k : key;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint64_t other = __shfl_xor(key, o, 64);
+            key = other > key ? other : key;
+        }
+        const float amax = __uint_as_float((uint32_t)(key >> 32));
+        const int pmax = (int)(0xFFFFFFFFu - (uint32_t)key);
+        const int jm = pmax >> 6;
+        const float mine = jm == 0 ? v[0] : jm == 1 ? v[1] : jm == 2 ? v[2] : v[3];
+        const float max = __shfl(mine, pmax & 63, 64);
+        int qi[4];
+        if (amax == 0.0f) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qi[j] = 0;
+            if (lane == 0) dK[b] = 0.0f;
+        } else {
+            const float iscale = -127.f / max;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = (int)rintf(__fmul_rn(iscale, v[j]));
+                qi[j] = r < 127 ? r : 127;
+            }
+            if (lane == 0) dK[b] = 1.0f / iscale;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[b * 256 + lane + 64 * j] = (int8_t)qi[j];
+            int s = qi[j];
+            for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+            if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
+        }
+    }
+}
+
+// q8_0 as the x86 CPU build computes it (arch/x86/quants.c:302-360):
+// d = amax/127 stored as fp16, id = 127/amax, q = round-to-nearest-even(x id).
+// q8_1 as ggml-cuda computes it (quantize.cu:5-50): d = amax/127,
+// q = roundf(x/d), s = butterfly sum of x; both stored as fp16.
+// One wave handles two 32-blocks per step.
+template <int SRC, int AM>
+__device__ __forceinline__ void quantize_q8_32_lds(uint8_t * smem, const LdsLayout & L, const ActSrc & src, int d_in) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int8_t * q = reinterpret_cast<int8_t *>(smem + L.q);
+    float * d32 = reinterpret_cast<float *>(smem + L.d32);
+    float * s32 = reinterpret_cast<float *>(smem + L.s32);
+    for (int base = wave * 64; base < d_in; base += WG) {
+        const int pos = base + lane;
+        const bool live = pos < d_in;          // d_in is a multiple of 32, not always of 64
+        const float v = live ? act_at<SRC>(src, pos) : 0.0f;
+        float amax = fabsf(v);
+        for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+        int qi;
+        float dstore;
+        if (AM == AM_CPU) {
+            const float d = amax / 127.f;
+            const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+            qi = (int)rintf(__fmul_rn(v, id));
+            qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+            dstore = round_to_half(d);
+        } else {
+            float s = v;
+            for (int o = 16; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 32));
+            const float d = amax / 127.0f;
+            qi = amax == 0.0f ? 0 : (int)roundf(v / d);
+            dstore = round_to_half(d);
+            if (live && (lane & 31) == 0) s32[pos >> 5] = round_to_half(s);
+        }
+        if (live) {
+            q[pos] = (int8_t)qi;
+            if ((lane & 31) == 0) d32[pos >> 5] = dstore;
+        }
+    }
+}
+
+// IQ2_S tables in LDS: the codebook as bytes {0x08,0x19,0x2b} per level, and
+// for each sign byte s the negation masks {m_lo, m_hi, m_lo & 1s, m_hi & 1s}
+// with m = 0xFF in every byte whose sign bit is set.
+__device__ __forceinline__ void build_iq2s_tables(uint8_t * smem, const LdsLayout & L, const uint16_t * codes) {
+    uint2 * grid = reinterpret_cast<uint2 *>(smem + L.grid);
+    uint4 * sign = reinterpret_cast<uint4 *>(smem + L.sign);
+    for (int k = threadIdx.x; k < 1024; k += WG) {
+        const uint32_t c = codes[k];
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t l = (c >> (2 * i)) & 3;
+            const uint32_t b = 8u + 17u * l + (l >> 1);     // 0x08, 0x19, 0x2b
+            if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+        }
+        grid[k] = make_uint2(lo, hi);
+    }
+    {
+        const uint32_t s = threadIdx.x;   // WG == 256 sign bytes
+        uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if ((s >> i) & 1) m0 |= 0xFFu << (8 * i);
+            if ((s >> (i + 4)) & 1) m1 |= 0xFFu << (8 * i);
+        }
+        sign[s] = make_uint4(m0, m1, m0 & 0x01010101u, m1 & 0x01010101u);
+    }
+}
+
+// ------------------------------------------------------------ unit dots
+//
+// A unit is the slice of a weight row one lane dots at a time:
+//   Q4_K, IQ2_S: a quarter super-block (64 values, two 32-sub-blocks)
+//   Q5_0, IQ4_NL: one 32-block
+// `wb` is the LDS byte offset of the row, u the unit index in the row.
+
+template <int T> struct Fmt;
+template <> struct Fmt<T_Q4_K>   { static constexpr int UNIT = 64; static constexpr int LPR = 16; };
+template <> struct Fmt<T_IQ2_S>  { static constexpr int UNIT = 64; static constexpr int LPR = 16; };
+template <> struct Fmt<T_Q5_0>   { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
+template <> struct Fmt<T_IQ4_NL> { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
+
+// Q4_K . q8_K   (ggml-cpu/quants.c:645-718): per super-block
+//   d_w dK sum_j sc_j dot_j  -  dmin_w dK sum_j m_j (bsum_2j + bsum_2j+1)
+// Q4_K . q8_1   (ggml-cuda/vecdotq.cuh:505-528): per 32-block b
+//   d_w d8_b sc_b dot_b  -  dmin_w d8_b m_b sum(q8_b)
+template <int AM>
+__device__ __forceinline__ float q4k_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+    const int sb = u >> 2, qq = u & 3;
+    const int blk = wb + sb * 144;                        // 16-aligned
+    const uint4 hdr = *reinterpret_cast<const uint4 *>(smem + blk);
+    const uint4 qa = *reinterpret_cast<const uint4 *>(smem + blk + 16 + 32 * qq);
+    const uint4 qb = *reinterpret_cast<const uint4 *>(smem + blk + 32 + 32 * qq);
+    // 6-bit scales/mins of sub-blocks j0 = 2qq, j1 = 2qq + 1 (get_scale_min_k4)
+    const uint32_t s03 = hdr.y, s47 = hdr.z, s8b = hdr.w;
+    int sc0, m0, sc1, m1;
+    if (qq < 2) {
+        const int sh0 = 16 * qq, sh1 = 16 * qq + 8;
+        sc0 = (s03 >> sh0) & 63; m0 = (s47 >> sh0) & 63;
+        sc1 = (s03 >> sh1) & 63; m1 = (s47 >> sh1) & 63;
+    } else {
+        const int sh0 = 16 * (qq - 2), sh1 = sh0 + 8;     // j-4 in 0..3
+        sc0 = ((s8b >> sh0) & 0xF) | (((s03 >> sh0) >> 6 & 3) << 4);
+        m0  = ((s8b >> sh0) >> 4 & 0xF) | (((s47 >> sh0) >> 6 & 3) << 4);
+        sc1 = ((s8b >> sh1) & 0xF) | (((s03 >> sh1) >> 6 & 3) << 4);
+        m1  = ((s8b >> sh1) >> 4 & 0xF) | (((s47 >> sh1) >> 6 & 3) << 4);
+    }
+    const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+    const int ao = L.q + sb * 256 + 64 * qq;
+    const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + ao);
+    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + ao + 16);
+    const uint4 a2 = *reinterpret_cast<const uint4 *>(smem + ao + 32);
+    const uint4 a3 = *reinterpret_cast<const uint4 *>(smem + ao + 48);
+    const uint32_t alo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint32_t ahi[8] = {a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    int dot1 = 0, dot2 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dot1 = dot4((int)(w[i] & 0x0F0F0F0Fu), (int)alo[i], dot1);
+        dot2 = dot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), (int)ahi[i], dot2);
+    }
+    if (AM == AM_CPU) {
+        const float dK = reinterpret_cast<const float *>(smem + L.dK)[sb];
+        const int * bs = reinterpret_cast<const int *>(smem + L.bsum) + sb * 16 + 4 * qq;
+        const int sumi = sc0 * dot1 + sc1 * dot2;
+        const int summ = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        return __fmul_rn(d * dK, (float)sumi) - __fmul_rn(dmin * dK, (float)summ);
+    } else {
+        int sq0 = 0, sq1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sq0 = dot4(0x01010101, (int)alo[i], sq0);
+            sq1 = dot4(0x01010101, (int)ahi[i], sq1);
+        }
+        const float * d32 = reinterpret_cast<const float *>(smem + L.d32) + (sb * 256 + 64 * qq) / 32;
+        const float sd = d32[0] * (float)(dot1 * sc0) + d32[1] * (float)(dot2 * sc1);
+        const float sm = d32[0] * (float)(sq0 * m0) + d32[1] * (float)(sq1 * m1);
+        return d * sd - dmin * sm;
+    }
+}
+
+// IQ2_S . q8_K  (ggml-cpu/quants.c:947-997): per super-block
+//   0.125 d_w dK sum_ib [(2 sc_lo + 1) s_1 + (2 sc_hi + 1) s_2]
+// IQ2_S . q8_1  (ggml-cuda/vecdotq.cuh:1061-1105): per 32-block
+//   d_w d8 ((s_1 sc_lo + s_2 sc_hi + (s_1 + s_2)/2) / 4)   (C integer division)
+template <int AM>
+__device__ __forceinline__ float iq2s_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+    const int sb = u >> 2, qq = u & 3;
+    const int blk = wb + sb * 82;                         // 2-aligned
+    const float d = h2f(lds32u(smem, blk));
+    const uint32_t qs0 = lds32u(smem, blk + 2 + 8 * qq), qs1 = lds32u(smem, blk + 6 + 8 * qq);
+    const uint32_t sg0 = lds32u(smem, blk + 34 + 8 * qq), sg1 = lds32u(smem, blk + 38 + 8 * qq);
+    const uint32_t qh2 = lds32u(smem, blk + 66 + 2 * qq);
+    const uint32_t sc2 = lds32u(smem, blk + 74 + 2 * qq);
+    const uint2 * grid = reinterpret_cast<const uint2 *>(smem + L.grid);
+    const uint4 * sign = reinterpret_cast<const uint4 *>(smem + L.sign);
+    const int ao = L.q + sb * 256 + 64 * qq;
+    int bsum = 0;
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t qhb = (qh2 >> (8 * h)) & 0xFF, scb = (sc2 >> (8 * h)) & 0xFF;
+        int s[2] = {0, 0};
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int g = 4 * h + l;
+            const uint32_t idx = byte_of(qs0, qs1, g) | (((qhb >> (2 * l)) & 3) << 8);
+            const uint2 gv = grid[idx];
+            const uint4 m = sign[byte_of(sg0, sg1, g)];
+            const int g0 = (int)((gv.x ^ m.x) + m.z);
+            const int g1 = (int)((gv.y ^ m.y) + m.w);
+            const uint2 a = *reinterpret_cast<const uint2 *>(smem + ao + 32 * h + 8 * l);
+            s[l >> 1] = dot4(g0, (int)a.x, s[l >> 1]);
+            s[l >> 1] = dot4(g1, (int)a.y, s[l >> 1]);
+        }
+        if (AM == AM_CPU) {
+            bsum += (2 * (int)(scb & 15) + 1) * s[0] + (2 * (int)(scb >> 4) + 1) * s[1];
+        } else {
+            const int sumi = (s[0] * (int)(scb & 15) + s[1] * (int)(scb >> 4) + (s[0] + s[1]) / 2) / 4;
+            const float d8 = reinterpret_cast<const float *>(smem + L.d32)[(sb * 256 + 64 * qq + 32 * h) / 32];
+            acc += (d * d8) * (float)sumi;
+        }
+    }
+    if (AM == AM_CPU) {
+        const float dK = reinterpret_cast<const float *>(smem + L.dK)[sb];
+        return 0.125f * __fmul_rn(d * dK, (float)bsum);
+    }
+    return acc;
+}
+
+// Q5_0 . q8_0  (ggml-cpu/quants.c:314-352):  d_w d8 sum (q - 16) a
+// Q5_0 . q8_1  (ggml-cuda/vecdotq.cuh:172-198): d_w (d8 sum q a - 16 s8)
+template <int AM>
+__device__ __forceinline__ float q5_0_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+    const int blk = wb + u * 22;                          // 2-aligned
+    const float d = h2f(lds32u(smem, blk));
+    const uint32_t qh = lds32u(smem, blk + 2);
+    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32);
+    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32 + 16);
+    const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
+    int sumi = 0, suma = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qsw = lds32u(smem, blk + 6 + 4 * i);
+        const uint32_t vh0 = qh >> (4 * i), vh1 = qh >> (16 + 4 * i);
+        uint32_t v0 = qsw & 0x0F0F0F0Fu;
+        v0 |= (vh0 << 4) & 0x10u; v0 |= (vh0 << 11) & 0x1000u; v0 |= (vh0 << 18) & 0x100000u; v0 |= (vh0 << 25) & 0x10000000u;
+        uint32_t v1 = (qsw >> 4) & 0x0F0F0F0Fu;
+        v1 |= (vh1 << 4) & 0x10u; v1 |= (vh1 << 11) & 0x1000u; v1 |= (vh1 << 18) & 0x100000u; v1 |= (vh1 << 25) & 0x10000000u;
+        sumi = dot4((int)v0, (int)alo[i], sumi);
+        sumi = dot4((int)v1, (int)ahi[i], sumi);
+        if (AM == AM_CPU) {
+            suma = dot4(0x01010101, (int)alo[i], suma);
+            suma = dot4(0x01010101, (int)ahi[i], suma);
+        }
+    }
+    const float d8 = reinterpret_cast<const float *>(smem + L.d32)[u];
+    if (AM == AM_CPU) return __fmul_rn(d * d8, (float)(sumi - 16 * suma));
+    const float s8 = reinterpret_cast<const float *>(smem + L.s32)[u];
+    return d * ((float)sumi * d8 - 16.0f * s8);
+}
+
+// 16-entry signed-byte table lookup of four nibble indices (one per byte).
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx, const uint32_t tab[4]) {
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(tab[1], tab[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(tab[3], tab[2], sel);
+    const uint32_t m = ((idx & 0x08080808u) >> 3) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+
+// IQ4_NL . q8_0 (ggml-cpu/quants.c:1203-1228) and . q8_1 (vecdotq.cuh:1270-1289):
+//   d_w d8 sum kvalues[q] a
+template <int AM>
+__device__ __forceinline__ float iq4nl_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+    // kvalues_iq4nl as little-endian bytes
+    const uint32_t tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+    const int blk = wb + u * 18;                          // 2-aligned
+    const float d = h2f(lds32u(smem, blk));
+    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32);
+    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32 + 16);
+    const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
+    int sumi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qsw = lds32u(smem, blk + 2 + 4 * i);
+        sumi = dot4((int)iq4nl_lookup(qsw & 0x0F0F0F0Fu, tab), (int)alo[i], sumi);
+        sumi = dot4((int)iq4nl_lookup((qsw >> 4) & 0x0F0F0F0Fu, tab), (int)ahi[i], sumi);
+    }
+    const float d8 = reinterpret_cast<const float *>(smem + L.d32)[u];
+    if (AM == AM_CPU) return __fmul_rn(d8 * d, (float)sumi);
+    return (d * d8) * (float)sumi;
+}
+
+template <int T, int AM>
+__device__ __forceinline__ float unit_dot_t(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+    if constexpr (T == T_Q4_K) return q4k_unit<AM>(smem, L, wb, u);
+    else if constexpr (T == T_IQ2_S) return iq2s_unit<AM>(smem, L, wb, u);
+    else if constexpr (T == T_Q5_0) return q5_0_unit<AM>(smem, L, wb, u);
+    else return iq4nl_unit<AM>(smem, L, wb, u);
+}
+
+#endif  // __HIPCC__
+
+}  // namespace dev
+}  // namespace llapis

@@ -1,0 +1,59 @@
+// launch.h -- host-visible launchers of the gfx950 kernels (defined in the
+// .hip translation units) and the parameter blocks they take.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llapis {
+
+// How a matvec channel (blockIdx.y) finds its weights, activation and output.
+enum { MMV_COMPACT = 0, MMV_ROUTED = 1 };
+
+struct MmvParams {
+    int mode;                    // MMV_COMPACT or MMV_ROUTED
+    int d_in, d_out;
+    int w_lds_bytes;             // LDS bytes reserved for staged weights (host computed)
+    // tier 0 (the hot pool, or the only pool) and tier 1 (the cold pool)
+    const uint8_t * w0; uint64_t stride0; const void * const * ptrs0; int64_t n0;
+    const uint8_t * w1; uint64_t stride1; int64_t n1;
+    // MMV_COMPACT: channel i uses expert/slot ids[i], column (b_ncols == 1 ? 0 : i)
+    const int32_t * ids; const int32_t * ne_live; int b_ncols;
+    // MMV_ROUTED: channel p is routed pair p of token p / top_k (ids row stride ids_s1)
+    int top_k, ids_s1, n_expert, k_slots;
+    const int32_t * exp_slot; const int32_t * slot_exp; const int32_t * slot_state;
+    const float * s0; const float * s1;      // per-slot / per-expert output scale, or NULL
+    int act_by_token;                        // activation column: token (1) or pair (0)
+    // activations: column c starts at act + c * act_ld
+    const float * act; int64_t act_ld;
+    float * y;                               // y[ch * d_out + r]
+};
+
+// rows of one workgroup for a weight type
+int mmv_rows_per_wg(int wtype);
+// dynamic LDS bytes of a matvec launch; 0 if the shape is not supported
+int mmv_lds_bytes(const MmvParams & p, int ht, int ct);
+// fill w_lds_bytes for the format pair
+void mmv_prepare(MmvParams & p, int ht, int ct);
+// launch over n_channels channels; returns hipSuccess or the launch error
+hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int act_mode, int src, int n_channels, hipStream_t s);
+
+hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
+                                float * logits, hipStream_t s);
+hipError_t launch_topk(float * probs_inout, int T, int E, int K, int32_t * ids, float * w, hipStream_t s);
+hipError_t launch_combine(const float * y, const float * w, int T, int K, int D, float * out, hipStream_t s);
+hipError_t launch_geglu(const float * gu, int F, int n_cols, float * out, int mode, hipStream_t s);
+
+hipError_t launch_partition(const int32_t * ids, int n_used, int ids_s1, int n_pairs, const int32_t * exp_slot,
+                            const int32_t * slot_exp, const int32_t * slot_state, int n_expert, int K,
+                            int32_t * ids_hot, int32_t * ids_cold, int32_t * hot_dst, int32_t * cold_dst,
+                            int32_t * counts, int32_t * rc_counts, int32_t * rc_hits, hipStream_t s);
+hipError_t launch_gather(const float * cur, int D_in, int kind, int n_used, const int32_t * counts,
+                         const int32_t * hot_dst, const int32_t * cold_dst, float * x_hot, float * x_cold,
+                         int Pmax, hipStream_t s);
+hipError_t launch_scatter(const float * y_hot, const float * y_cold, int D_out, int kind, const int32_t * counts,
+                          const int32_t * ids_hot, const int32_t * hot_dst, const int32_t * ids_cold,
+                          const int32_t * cold_dst, const float * s_hot, const float * s_cold, float * y_full,
+                          int Pmax, hipStream_t s);
+
+}  // namespace llapis

@@ -1,0 +1,277 @@
+// small_kernels.hip -- the path's small kernels on gfx950: router logits,
+// softmax/top-k selection, the island's residency partition / gather /
+// scatter, the weighted combine, and a standalone GEGLU.
+#include "device.h"
+#include "launch.h"
+
+namespace llapis {
+namespace dev {
+
+// ------------------------------------------------------------- router
+
+constexpr int ROUTER_TOK = 8;    // tokens per wave (the expert row stays in registers)
+
+// logits[t][e] = W_r[e] . x[t] (+ bias[e]); one wave per (expert, 8 tokens)
+// (build_lora_mm(gate_inp, cur), llama-graph.cpp:1541; ggml mul_mat f32).
+__global__ __launch_bounds__(WG) void k_router_logits(const float * __restrict__ x, int T,
+                                                      const float * __restrict__ w_r, const float * __restrict__ bias,
+                                                      int d, int E, float * __restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * (WG / 64) + (threadIdx.x >> 6);
+    if (e >= E) return;                         // whole wave leaves; no barriers below
+    const int t0 = blockIdx.y * ROUTER_TOK;
+    const int nt = min(ROUTER_TOK, T - t0);
+    const float * wrow = w_r + (int64_t)e * d;
+    float acc[ROUTER_TOK];
+#pragma unroll
+    for (int j = 0; j < ROUTER_TOK; ++j) acc[j] = 0.0f;
+    if ((d & 3) == 0) {
+        for (int k = 4 * lane; k < d; k += 256) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(wrow + k);
+#pragma unroll
+            for (int j = 0; j < ROUTER_TOK; ++j) {
+                if (j < nt) {
+                    const float4 x4 = *reinterpret_cast<const float4 *>(x + (int64_t)(t0 + j) * d + k);
+                    acc[j] += w4.x * x4.x + w4.y * x4.y + w4.z * x4.z + w4.w * x4.w;
+                }
+            }
+        }
+    } else {
+        for (int k = lane; k < d; k += 64) {
+            const float w = wrow[k];
+#pragma unroll
+            for (int j = 0; j < ROUTER_TOK; ++j)
+                if (j < nt) acc[j] += w * x[(int64_t)(t0 + j) * d + k];
+        }
+    }
+    const float b = bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < ROUTER_TOK; ++j) {
+        const float s = wave_sum(acc[j]);
+        if (lane == 0 && j < nt) logits[(int64_t)(t0 + j) * E + e] = s + b;
+    }
+}
+
+// In place: logits -> probabilities (ggml soft_max: exp(x - max), sum in
+// double, scaled by float(1/sum); ops.cpp:5344-5450), then top-K by
+// descending p with ties to the lower index (argsort_top_k), weights
+// p[ids] / max(sum, 6.103515625e-5) with the sum in double (sum_rows, clamp,
+// div: llama-graph.cpp:1636-1650).  One wave per token, E <= 256, K <= 16.
+__global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, int K,
+                                             int32_t * __restrict__ ids, float * __restrict__ w) {
+    const int lane = threadIdx.x, t = blockIdx.x;
+    float * row = probs + (int64_t)t * E;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? row[e] : -INFINITY;
+    }
+    const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    double ls = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? expf(v[j] - mx) : 0.0f;
+        ls += (double)v[j];
+    }
+    for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    const float inv = (float)(1.0 / ls);
+    bool taken[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = __fmul_rn(v[j], inv);
+        if (e < E) row[e] = v[j];
+        taken[j] = e >= E;
+    }
+    float sel = 0.0f;        // lane k (< K) keeps the k-th selected probability
+    for (int k = 0; k < K; ++k) {
+        uint64_t key = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = lane + 64 * j;
+            const uint64_t kk = taken[j] ? 0 : (((uint64_t)__float_as_uint(v[j]) << 32) | (0xFFFFFFFFu - e)) + 1;
+            key = kk > key ? kk : key;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint64_t other = __shfl_xor(key, o, 64);
+            key = other > key ? other : key;
+        }
+        key -= 1;
+        const uint32_t eb = 0xFFFFFFFFu - (uint32_t)key;
+        const float pb = __uint_as_float((uint32_t)(key >> 32));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) if ((uint32_t)(lane + 64 * j) == eb) taken[j] = true;
+        if (lane == k) sel = pb;
+        if (lane == 0) ids[(int64_t)t * K + k] = (int32_t)eb;
+    }
+    double s = lane < K ? (double)sel : 0.0;
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    float sf = (float)s;
+    if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
+    if (lane < K) w[(int64_t)t * K + lane] = sel / sf;
+}
+
+// out[t][r] = ((w0 y0 + w1 y1) + w2 y2) + ...   (llama-graph.cpp:1812-1840:
+// ggml_mul by the weights, then the views added in order)
+__global__ __launch_bounds__(WG) void k_combine(const float * __restrict__ y, const float * __restrict__ w, int K, int D,
+                                                float * __restrict__ out) {
+    const int r = blockIdx.x * WG + threadIdx.x, t = blockIdx.y;
+    if (r >= D) return;
+    const float * yp = y + (int64_t)t * K * D + r;
+    const float * wt = w + (int64_t)t * K;
+    float o = __fmul_rn(yp[0], wt[0]);
+    for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(yp[(int64_t)k * D], wt[k]));
+    out[(int64_t)t * D + r] = o;
+}
+
+template <int SRC>
+__global__ __launch_bounds__(WG) void k_geglu(const float * __restrict__ gu, int F, float * __restrict__ out) {
+    const int i = blockIdx.x * WG + threadIdx.x, c = blockIdx.y;
+    if (i >= F) return;
+    const float * col = gu + (int64_t)c * 2 * F;
+    out[(int64_t)c * F + i] = geglu1<SRC>(col[i], col[F + i]);
+}
+
+// ----------------------------------------------------------- island
+
+// Residency partition of the routed pairs of one fire, one lane per pair
+// (moert/cuda/ffn_moe.cu:80-130): pair p of token t = p / n_used reads
+// ids[t*ids_s1 + p - t*n_used]; hot iff the READY mirror predicate holds.
+// Compaction keeps ascending p on both sides (64-bit ballot + popcount).
+__global__ __launch_bounds__(64) void k_partition(const int32_t * __restrict__ ids, int n_used, int ids_s1, int n_pairs,
+                                                  const int32_t * __restrict__ exp_slot, const int32_t * __restrict__ slot_exp,
+                                                  const int32_t * __restrict__ slot_state, int n_expert, int K,
+                                                  int32_t * __restrict__ ids_hot, int32_t * __restrict__ ids_cold,
+                                                  int32_t * __restrict__ hot_dst, int32_t * __restrict__ cold_dst,
+                                                  int32_t * __restrict__ counts, int32_t * __restrict__ rc_counts,
+                                                  int32_t * __restrict__ rc_hits) {
+    const int lane = threadIdx.x;
+    const bool valid = lane < n_pairs;
+    int e = -1, slot = -1;
+    bool hot = false;
+    if (valid) {
+        const int t = lane / n_used;
+        e = ids[t * ids_s1 + (lane - t * n_used)];
+        if (e >= 0 && e < n_expert && K > 0) {
+            const int s = exp_slot[e];
+            if (s >= 0 && s < K && slot_state[s] == 2 && slot_exp[s] == e) { hot = true; slot = s; }
+        }
+    }
+    const uint64_t hm = __ballot(valid && hot), cm = __ballot(valid && !hot);
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    if (valid && hot) {
+        const int i = __popcll(hm & below);
+        ids_hot[i] = slot;
+        hot_dst[i] = lane;
+    } else if (valid) {
+        const int i = __popcll(cm & below);
+        ids_cold[i] = e;
+        cold_dst[i] = lane;
+    }
+    if (lane == 0) {
+        counts[0] = __popcll(hm);
+        counts[1] = __popcll(cm);
+    }
+    if (rc_counts && valid && e >= 0 && e < n_expert) atomicAdd(&rc_counts[e], 1);
+    if (rc_hits && lane == 0) {
+        atomicAdd(&rc_hits[0], (int)__popcll(hm));
+        atomicAdd(&rc_hits[1], (int)__popcll(cm));
+    }
+}
+
+// x_side[i] = activation column of compact pair i (ffn_moe.cu:135-153)
+__global__ __launch_bounds__(WG) void k_gather(const float * __restrict__ cur, int D_in, int kind, int n_used,
+                                               const int32_t * __restrict__ counts, const int32_t * __restrict__ hot_dst,
+                                               const int32_t * __restrict__ cold_dst, float * __restrict__ x_hot,
+                                               float * __restrict__ x_cold) {
+    const int i = blockIdx.x, side = blockIdx.y;
+    if (i >= counts[side]) return;
+    const int p = side == 0 ? hot_dst[i] : cold_dst[i];
+    const int src_col = kind == 0 ? p / n_used : p;
+    float * dst = (side == 0 ? x_hot : x_cold) + (int64_t)i * D_in;
+    const float * src = cur + (int64_t)src_col * D_in;
+    if ((D_in & 3) == 0) {
+        for (int k = threadIdx.x; k < (D_in >> 2); k += WG)
+            reinterpret_cast<float4 *>(dst)[k] = reinterpret_cast<const float4 *>(src)[k];
+    } else {
+        for (int k = threadIdx.x; k < D_in; k += WG) dst[k] = src[k];
+    }
+}
+
+// y_full[p] = y_side[i] * (kind == 1 ? scale : 1) (ffn_moe.cu:158-176)
+__global__ __launch_bounds__(WG) void k_scatter(const float * __restrict__ y_hot, const float * __restrict__ y_cold, int D_out,
+                                                int kind, const int32_t * __restrict__ counts,
+                                                const int32_t * __restrict__ ids_hot, const int32_t * __restrict__ hot_dst,
+                                                const int32_t * __restrict__ ids_cold, const int32_t * __restrict__ cold_dst,
+                                                const float * __restrict__ s_hot, const float * __restrict__ s_cold,
+                                                float * __restrict__ y_full) {
+    const int i = blockIdx.x;
+    if (i < counts[0]) {
+        const int p = hot_dst[i];
+        const float sc = (kind == 1 && s_hot) ? s_hot[ids_hot[i]] : 1.0f;
+        for (int o = threadIdx.x; o < D_out; o += WG) y_full[(int64_t)p * D_out + o] = y_hot[(int64_t)i * D_out + o] * sc;
+    }
+    if (i < counts[1]) {
+        const int p = cold_dst[i];
+        const float sc = (kind == 1 && s_cold) ? s_cold[ids_cold[i]] : 1.0f;
+        for (int o = threadIdx.x; o < D_out; o += WG) y_full[(int64_t)p * D_out + o] = y_cold[(int64_t)i * D_out + o] * sc;
+    }
+}
+
+}  // namespace dev
+
+using namespace dev;
+
+hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
+                                float * logits, hipStream_t s) {
+    dim3 grid((E + 3) / 4, (T + ROUTER_TOK - 1) / ROUTER_TOK);
+    hipLaunchKernelGGL(k_router_logits, grid, dim3(WG), 0, s, x, T, w_r, bias, d, E, logits);
+    return hipGetLastError();
+}
+
+hipError_t launch_topk(float * probs, int T, int E, int K, int32_t * ids, float * w, hipStream_t s) {
+    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, s, probs, E, K, ids, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float * y, const float * w, int T, int K, int D, float * out, hipStream_t s) {
+    hipLaunchKernelGGL(k_combine, dim3((D + WG - 1) / WG, T), dim3(WG), 0, s, y, w, K, D, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_geglu(const float * gu, int F, int n_cols, float * out, int mode, hipStream_t s) {
+    dim3 grid((F + WG - 1) / WG, n_cols);
+    if (mode == 1) hipLaunchKernelGGL(k_geglu<SRC_GEGLU_TANH>, grid, dim3(WG), 0, s, gu, F, out);
+    else hipLaunchKernelGGL(k_geglu<SRC_GEGLU_TABLE>, grid, dim3(WG), 0, s, gu, F, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_partition(const int32_t * ids, int n_used, int ids_s1, int n_pairs, const int32_t * exp_slot,
+                            const int32_t * slot_exp, const int32_t * slot_state, int n_expert, int K,
+                            int32_t * ids_hot, int32_t * ids_cold, int32_t * hot_dst, int32_t * cold_dst,
+                            int32_t * counts, int32_t * rc_counts, int32_t * rc_hits, hipStream_t s) {
+    hipLaunchKernelGGL(k_partition, dim3(1), dim3(64), 0, s, ids, n_used, ids_s1, n_pairs, exp_slot, slot_exp,
+                       slot_state, n_expert, K, ids_hot, ids_cold, hot_dst, cold_dst, counts, rc_counts, rc_hits);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const float * cur, int D_in, int kind, int n_used, const int32_t * counts,
+                         const int32_t * hot_dst, const int32_t * cold_dst, float * x_hot, float * x_cold,
+                         int Pmax, hipStream_t s) {
+    hipLaunchKernelGGL(k_gather, dim3(Pmax, 2), dim3(WG), 0, s, cur, D_in, kind, n_used, counts, hot_dst, cold_dst,
+                       x_hot, x_cold);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter(const float * y_hot, const float * y_cold, int D_out, int kind, const int32_t * counts,
+                          const int32_t * ids_hot, const int32_t * hot_dst, const int32_t * ids_cold,
+                          const int32_t * cold_dst, const float * s_hot, const float * s_cold, float * y_full,
+                          int Pmax, hipStream_t s) {
+    hipLaunchKernelGGL(k_scatter, dim3(Pmax), dim3(WG), 0, s, y_hot, y_cold, D_out, kind, counts, ids_hot, hot_dst,
+                       ids_cold, cold_dst, s_hot, s_cold, y_full);
+    return hipGetLastError();
+}
+
+}  // namespace llapis

@@ -1,0 +1,208 @@
+"""GPU parity: the HIP path against the CPU oracle on the same inputs.
+
+Tolerances (north star: max relative L2 1e-3 in fp32 accumulation):
+* matvecs: the integer dot products are exact on both sides and the
+  activation quantisation is bit-identical, so only fp32 summation order
+  differs: rel L2 <= 2e-6 per channel;
+* routing: ids identical, weights within 1e-5 relative;
+* whole layer against the oracle with the GPU's routing: rel L2 <= 1e-4;
+* whole layer against the reference's own ggml CPU graph: rel L2 <= 1e-3.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import llapis_amd as la
+from llapis_amd import _lib as L
+from helpers import FULL16, SMALL, layer, rel_l2, tokens
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def torch_mod():
+    import torch
+    return torch
+
+
+MM_CASES = [(la.Q4_K, 2816, 40), (la.IQ2_S, 2816, 40), (la.Q5_0, 704, 72), (la.IQ4_NL, 704, 72),
+            (la.Q4_K, 512, 33), (la.IQ2_S, 768, 24), (la.Q5_0, 96, 40), (la.IQ4_NL, 96, 40)]
+
+
+@pytest.mark.parametrize("wtype,d_in,d_out", MM_CASES)
+@pytest.mark.parametrize("act_mode", [la.ACT_CPU, la.ACT_Q8_1])
+def test_mul_mat_id_vs_oracle(gpu, oracle, wtype, d_in, d_out, act_mode):
+    torch = torch_mod()
+    say(f"mul_mat_id type={wtype} d_in={d_in} d_out={d_out} act={act_mode}")
+    n_pool, n_ids = 5, 6
+    rs = la.row_size(wtype, d_in)
+    w = np.concatenate([la.quantize(wtype, la.synth_normal(100 + e, d_out * d_in, 0, 0.02).reshape(d_out, d_in),
+                                    np.ones(d_in, np.float32) if wtype in (la.IQ2_S, la.IQ4_NL) else None)
+                        for e in range(n_pool)])
+    ids = np.array([3, 0, 4, 4, 1, 2], np.int32)
+    b = la.synth_normal(7, d_in * n_ids).reshape(n_ids, d_in)
+    b[2] *= 1e-3
+    b[3, : d_in // 2] = 0.0           # a zero half-column exercises amax == 0 blocks
+    dev = {k: torch.from_numpy(v).to(gpu) for k, v in dict(w=w, ids=ids, b=b).items()}
+    y = torch.full((n_ids, d_out), float("nan"), device=gpu)
+    ne_live = torch.tensor([n_ids - 1], dtype=torch.int32, device=gpu)
+    call = L.MoertMmCall(L.MM_W_HOT, 0, None, 0, dev["b"].data_ptr(), n_ids, dev["ids"].data_ptr(), n_ids,
+                         y.data_ptr(), ne_live.data_ptr(), None)
+    la.lib().llapis_set_modes(act_mode, la.GELU_TABLE)
+    s = torch.cuda.current_stream().cuda_stream
+    L.check(la.lib().llapis_mul_mat_id(C.byref(call), wtype, dev["w"].data_ptr(), n_pool, d_in, d_out, s), "mm")
+    torch.cuda.synchronize()
+    yg = y.cpu().numpy()
+    assert np.isnan(yg[n_ids - 1]).all(), "a channel past ne_live was written"
+    for i in range(n_ids - 1):
+        slab = w[ids[i] * rs * d_out:(ids[i] + 1) * rs * d_out]
+        yo = oracle.matvec(wtype, act_mode, slab, d_out, d_in, b[i])
+        assert rel_l2(yg[i], yo) <= 2e-6, (i, rel_l2(yg[i], yo))
+    la.lib().llapis_set_modes(la.ACT_CPU, la.GELU_TABLE)
+
+
+def test_mul_mat_id_refuses_unaligned_slab(gpu):
+    """An expert slab that is not a whole number of 16-byte chunks is refused
+    on the host (the kernel streams slabs in 128-bit loads)."""
+    torch = torch_mod()
+    d_in, d_out = 768, 17                      # 246 B rows x 17 = 4182 B
+    y = torch.empty(1, d_out, device=gpu)
+    ids = torch.zeros(1, dtype=torch.int32, device=gpu)
+    b = torch.zeros(d_in, device=gpu)
+    w = torch.zeros(la.row_size(la.IQ2_S, d_in) * d_out, dtype=torch.uint8, device=gpu)
+    call = L.MoertMmCall(L.MM_W_HOT, 0, None, 0, b.data_ptr(), 1, ids.data_ptr(), 1, y.data_ptr(), None, None)
+    rc = la.lib().llapis_mul_mat_id(C.byref(call), la.IQ2_S, w.data_ptr(), 1, d_in, d_out,
+                                    torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"16 bytes" in la.lib().llapis_last_error()
+
+
+def test_mul_mat_id_shared_column(gpu, oracle):
+    torch = torch_mod()
+    say("mul_mat_id shared column")
+    d_in, d_out, n_pool = 2816, 48, 3
+    w = np.concatenate([la.quantize(la.Q4_K, la.synth_normal(200 + e, d_out * d_in, 0, 0.02).reshape(d_out, d_in))
+                        for e in range(n_pool)])
+    ids = np.array([2, 1, 0], np.int32)
+    b = la.synth_normal(9, d_in)
+    wd, idd, bd = (torch.from_numpy(a).to(gpu) for a in (w, ids, b))
+    y = torch.empty(3, d_out, device=gpu)
+    call = L.MoertMmCall(L.MM_W_HOT, 0, None, 0, bd.data_ptr(), 1, idd.data_ptr(), 3, y.data_ptr(), None, None)
+    L.check(la.lib().llapis_mul_mat_id(C.byref(call), la.Q4_K, wd.data_ptr(), n_pool, d_in, d_out,
+                                       torch.cuda.current_stream().cuda_stream), "mm")
+    torch.cuda.synchronize()
+    rs = la.row_size(la.Q4_K, d_in) * d_out
+    for i in range(3):
+        yo = oracle.matvec(la.Q4_K, la.ACT_CPU, w[ids[i] * rs:(ids[i] + 1) * rs], d_out, d_in, b)
+        assert rel_l2(y[i].cpu().numpy(), yo) <= 2e-6
+
+
+@pytest.mark.parametrize("T", [1, 4, 37])
+def test_router_vs_oracle(gpu, oracle, T):
+    torch = torch_mod()
+    say(f"router T={T}")
+    lay = layer(SMALL, 11, [], router_bias=la.synth_normal(5, SMALL.n_expert, 0, 0.5))
+    dl = la.DeviceLayer(lay, gpu)
+    x = tokens(3, T, SMALL.d_model)
+    ids, w, probs = dl.router(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    ids_o, w_o, p_o = oracle.router(x, lay.router_w, lay.router_b, SMALL.top_k)
+    assert np.array_equal(ids.cpu().numpy(), ids_o)
+    assert np.allclose(w.cpu().numpy(), w_o, rtol=1e-5, atol=1e-7)
+    assert np.allclose(probs.cpu().numpy(), p_o, rtol=1e-5, atol=1e-8)
+    assert np.allclose(w.cpu().numpy().sum(1), 1.0, atol=1e-6)
+
+
+@pytest.mark.parametrize("mode", [la.GELU_TABLE, la.GELU_TANH])
+def test_geglu_vs_oracle(gpu, oracle, mode):
+    torch = torch_mod()
+    say(f"geglu mode={mode}")
+    F, n = 704, 9
+    gu = (3.0 * la.synth_normal(21, n * 2 * F)).reshape(n, 2 * F)
+    gu[0, :8] = [-12, -10, -9.99, 0, 9.99, 10, 11, np.float32(1e-8)]
+    out = la.geglu(torch.from_numpy(gu).to(gpu), F, mode)
+    torch.cuda.synchronize()
+    og = out.cpu().numpy()
+    oo = np.stack([oracle.geglu(gu[c, :F], gu[c, F:], mode) for c in range(n)])
+    # the device's tanhf may differ from glibc's by an ulp; in table mode that
+    # can move one fp16 rounding: allow it on a handful of elements
+    close = np.isclose(og, oo, rtol=2e-6 if mode == la.GELU_TANH else 0, atol=1e-7)
+    assert (~close).sum() <= max(2, og.size // 2000), (~close).sum()
+    assert rel_l2(og, oo) <= 1e-5
+
+
+def _layer_case(spec, seed, n_hot, scales):
+    rng = np.random.default_rng(seed)
+    hot = sorted(rng.choice(spec.n_expert, n_hot, replace=False).tolist()) if n_hot else []
+    return layer(spec, seed, hot, scales=scales)
+
+
+@pytest.mark.parametrize("spec_name,n_hot,T,scales", [("SMALL", 6, 3, True), ("SMALL", 16, 2, False),
+                                                      ("SMALL", 0, 5, True), ("FULL16", 7, 1, False),
+                                                      ("FULL16", 9, 4, True)])
+@pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
+def test_layer_vs_oracle(gpu, oracle, spec_name, n_hot, T, scales, act_mode, gelu_mode):
+    torch = torch_mod()
+    spec = {"SMALL": SMALL, "FULL16": FULL16}[spec_name]
+    say(f"layer {spec_name} hot={n_hot} T={T} scales={scales} act={act_mode} gelu={gelu_mode}")
+    lay = _layer_case(spec, 31 + n_hot, n_hot, scales)
+    dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
+    x = tokens(77 + T, T, spec.d_model)
+    out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    ids_g, w_g = ids.cpu().numpy(), w.cpu().numpy()
+    ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, spec.top_k)
+    assert np.array_equal(ids_g, ids_o)
+    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, act_mode, gelu_mode)
+    err = rel_l2(out.cpu().numpy(), out_o)
+    say(f"  rel_l2 vs oracle = {err:.3e}")
+    assert err <= 1e-4
+
+
+def test_island_fires_match_layer(gpu, oracle):
+    """gate_up and down through moert_ffn_moe (the reference's operator
+    boundary) give the oracle's per-pair matvecs."""
+    torch = torch_mod()
+    say("island fires")
+    spec = FULL16
+    lay = _layer_case(spec, 55, 5, True)
+    dl = la.DeviceLayer(lay, gpu)
+    T = 4
+    x = tokens(90, T, spec.d_model)
+    xd = torch.from_numpy(x).to(gpu)
+    ids, w, _ = dl.router(xd)
+    # a strided ids view, as argsort_top_k hands the op (row stride n_expert)
+    ids_full = torch.full((T, spec.n_expert), -7, dtype=torch.int32, device=gpu)
+    ids_full[:, : spec.top_k] = ids
+    gu = dl.moe_dual(0, xd, ids_full, il=0, ids_row_stride=spec.n_expert)
+    act = la.geglu(gu.reshape(-1, 2 * spec.n_ff).contiguous(), spec.n_ff)
+    dn = dl.moe_dual(1, act, ids_full, il=0, ids_row_stride=spec.n_expert)
+    torch.cuda.synchronize()
+    ids_h = ids.cpu().numpy()
+    gu_h, act_h, dn_h = gu.cpu().numpy(), act.cpu().numpy(), dn.cpu().numpy()
+    res = lay.residency
+    for t in range(T):
+        for k in range(spec.top_k):
+            e = int(ids_h[t, k])
+            hot = res.is_hot(e)
+            s = int(res.exp_slot[e])
+            gut = spec.hot_gu_type if hot else spec.cold_gu_type
+            dnt = spec.hot_dn_type if hot else spec.cold_dn_type
+            idx = s if hot else e
+            gpool = lay.hot_gu if hot else lay.cold_gu
+            dpool = lay.hot_dn if hot else lay.cold_dn
+            gb, db = spec.gu_bytes(gut), spec.dn_bytes(dnt)
+            yo = oracle.matvec(gut, la.ACT_CPU, gpool[idx * gb:(idx + 1) * gb], 2 * spec.n_ff, spec.d_model, x[t])
+            assert rel_l2(gu_h[t, k], yo) <= 2e-6
+            do = oracle.matvec(dnt, la.ACT_CPU, dpool[idx * db:(idx + 1) * db], spec.d_model, spec.n_ff,
+                               act_h[t * spec.top_k + k])
+            sc = (lay.s_hot[s] if hot else lay.s_cold[e])
+            assert rel_l2(dn_h[t, k], do * sc) <= 2e-6
+    st = L.MoertCudaStats()
+    la.lib().moert_cuda_stats_get(C.byref(st))
+    assert st.fires >= 2
