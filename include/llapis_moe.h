@@ -97,7 +97,8 @@ int32_t  llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace
  * logits = W_r x_t (+ bias), p = softmax, ids = top_k of p (descending, ties
  * to the lower index), w = p[ids] / max(sum p[ids], 6.103515625e-5).
  * x [T][d], W_r [n_expert][d] (ggml ne0 = d), bias [n_expert] or NULL,
- * ids/w [T][top_k], probs [T][n_expert] or NULL.  n_expert <= 256, top_k <= 16. */
+ * ids/w [T][top_k], probs [T][n_expert] (required: it also holds the logits
+ * between the two kernels).  n_expert <= 256, top_k <= 16. */
 int32_t llapis_router_topk(const float * x, int32_t n_tokens, const float * w_r, const float * bias,
                            int32_t d, int32_t n_expert, int32_t top_k,
                            int32_t * ids, float * weights, float * probs, void * stream);
@@ -138,6 +139,15 @@ uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tok
  * ([T][top_k], optional) receive the routing. */
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
                        int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
+
+/* Stage timing of llapis_moe_ffn for measurement: while enabled, every call
+ * records a hipEvent before and after each of its kernels on the call's
+ * stream.  llapis_profile_read waits for the recorded events, writes the
+ * summed milliseconds per stage {router, top-k, gate_up, down, combine} to
+ * ms[0..n) and returns the number of timed calls since the last read (-1 on
+ * a HIP error); reading resets the sums.  Disabled by default (no events). */
+void    llapis_profile_enable(int32_t on);
+int32_t llapis_profile_read(float * ms, int32_t n);
 
 #ifdef __cplusplus
 }

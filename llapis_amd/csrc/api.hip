@@ -457,6 +457,54 @@ int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float 
     return 0;
 }
 
+// ------------------------------------------------------------ profiling
+
+namespace {
+constexpr int PROF_STAGES = 5;
+constexpr int PROF_RING = 4096;
+struct Profiler {
+    std::mutex mu;
+    bool on = false;
+    hipEvent_t ev[PROF_RING][PROF_STAGES + 1] = {};
+    int n = 0;          // calls recorded since the last read
+    bool created = false;
+};
+Profiler g_prof;
+
+// record boundary `b` (0..PROF_STAGES) of call slot `c`
+hipError_t prof_mark(int c, int b, hipStream_t s) {
+    if (c < 0) return hipSuccess;
+    return hipEventRecord(g_prof.ev[c][b], s);
+}
+}  // namespace
+
+void llapis_profile_enable(int32_t on) {
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    if (on && !g_prof.created) {
+        for (auto & row : g_prof.ev)
+            for (auto & e : row) MOERT_HIP_CHECK(hipEventCreate(&e));
+        g_prof.created = true;
+    }
+    g_prof.on = on != 0;
+    g_prof.n = 0;
+}
+
+int32_t llapis_profile_read(float * ms, int32_t n) {
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    for (int i = 0; i < n; ++i) ms[i] = 0.0f;
+    const int calls = g_prof.n;
+    for (int c = 0; c < calls; ++c) {
+        if (hipEventSynchronize(g_prof.ev[c][PROF_STAGES]) != hipSuccess) return -1;
+        for (int st = 0; st < PROF_STAGES && st < n; ++st) {
+            float t = 0.0f;
+            if (hipEventElapsedTime(&t, g_prof.ev[c][st], g_prof.ev[c][st + 1]) != hipSuccess) return -1;
+            ms[st] += t;
+        }
+    }
+    g_prof.n = 0;
+    return calls;
+}
+
 // ------------------------------------------------------------- fused layer
 
 namespace {
@@ -510,8 +558,16 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     float * ydn = (float *)(base + ws.ydn);
     const int P = T * L->top_k;
 
+    int pc = -1;                       // profiling slot of this call
+    if (g_prof.on) {
+        std::lock_guard<std::mutex> lk(g_prof.mu);
+        if (g_prof.n < PROF_RING) pc = g_prof.n++;
+    }
+    LL_TRY(prof_mark(pc, 0, s));
     LL_TRY(launch_router_logits(x, T, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
+    LL_TRY(prof_mark(pc, 1, s));
     LL_TRY(launch_topk(probs, T, L->n_expert, L->top_k, ids, w, s));
+    LL_TRY(prof_mark(pc, 2, s));
 
     MmvParams p = {};
     p.mode = MMV_ROUTED;
@@ -538,6 +594,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     p.y = ygu;
     mmv_prepare(p, L->hot_gu_type, L->cold_gu_type);
     LL_TRY(launch_mmv(p, L->hot_gu_type, L->cold_gu_type, L->act_mode, dev::SRC_PLAIN, P, s));
+    LL_TRY(prof_mark(pc, 3, s));
     // down: activation column = pair, GEGLU of its gate_up output on the fly
     p.d_in = L->n_ff;
     p.d_out = L->d_model;
@@ -554,7 +611,9 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     mmv_prepare(p, L->hot_dn_type, L->cold_dn_type);
     const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
     LL_TRY(launch_mmv(p, L->hot_dn_type, L->cold_dn_type, L->act_mode, src, P, s));
+    LL_TRY(prof_mark(pc, 4, s));
     LL_TRY(launch_combine(ydn, w, T, L->top_k, L->d_model, out, s));
+    LL_TRY(prof_mark(pc, 5, s));
     return 0;
 }
 
