@@ -72,7 +72,7 @@ class Workload:
         self.w = torch.empty(T, sp.top_k, device=dev)
         self.descs = [l.desc() for l in self.layers]
         need = int(la.lib().llapis_moe_ffn_workspace_size(C.byref(self.descs[0]), T))
-        self.ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        self.ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         self.n_tok = n_tok
         self.fn = la.lib().llapis_moe_ffn
 

@@ -136,9 +136,20 @@ typedef struct llapis_moe_layer {
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens);
 
 /* out [T][d_model] = the layer applied to x [T][d_model].  ids/weights
- * ([T][top_k], optional) receive the routing. */
+ * ([T][top_k], optional) receive the routing.  Batches of up to 4 tokens
+ * take the three-kernel decode path, whose control block lives at the start
+ * of the workspace: zero the workspace before its first use (e.g. with
+ * llapis_moe_ffn_workspace_init); the library keeps it consistent after
+ * that.  Calls that share a workspace must not run concurrently. */
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
                        int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
+
+/* Zero the control block of a fused-layer workspace (a kernel on `stream`). */
+int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
+
+/* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
+ * (default 1), key 1 = down-slab prefetch during gate_up (default 1). */
+void llapis_set_tuning(int32_t key, int32_t value);
 
 /* Stage timing of llapis_moe_ffn for measurement: while enabled, every call
  * records a hipEvent before and after each of its kernels on the call's

@@ -508,26 +508,82 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
+std::atomic<int> g_decode_path{1}, g_prefetch{1};
+
+uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+uint64_t dec_ctl_bytes(const llapis_moe_layer * L) {
+    const int n_rb = (L->d_model + 31) / 32;
+    return al256(sizeof(DecCtl)) + al256((uint64_t)DEC_MAXT * n_rb * 4);
+}
+
+// generic path (any T): probs, ids, w, y_gu, y_dn -- after the decode path's
+// control block, which every layout reserves so the two paths can share a
+// workspace
 struct FfnWs {
     uint64_t probs, ids, w, ygu, ydn, total;
 };
 FfnWs ffn_ws(const llapis_moe_layer * L, int32_t T) {
-    auto al = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
     const uint64_t P = (uint64_t)T * L->top_k;
     FfnWs w;
-    w.probs = 0;
-    w.ids = w.probs + al((uint64_t)T * L->n_expert * 4);
-    w.w = w.ids + al(P * 4);
-    w.ygu = w.w + al(P * 4);
-    w.ydn = w.ygu + al(P * 2 * L->n_ff * 4);
-    w.total = w.ydn + al(P * L->d_model * 4);
+    w.probs = dec_ctl_bytes(L);
+    w.ids = w.probs + al256((uint64_t)T * L->n_expert * 4);
+    w.w = w.ids + al256(P * 4);
+    w.ygu = w.w + al256(P * 4);
+    w.ydn = w.ygu + al256(P * 2 * L->n_ff * 4);
+    w.total = w.ydn + al256(P * L->d_model * 4);
     return w;
+}
+
+// decode path (T <= DEC_MAXT): control block first (zero before first use)
+struct DecWs {
+    uint64_t ctl, comb, logits, ids, w, xq, ygu, aq, ydn, total, ctl_bytes;
+    int64_t xq_stride, aq_stride;
+    int n_rb;
+};
+DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
+    const uint64_t P = (uint64_t)T * L->top_k;
+    DecWs w;
+    w.n_rb = (L->d_model + 31) / 32;
+    w.xq_stride = dec_act_bytes(L->d_model);
+    w.aq_stride = dec_act_bytes(L->n_ff);
+    w.ctl = 0;
+    w.comb = al256(sizeof(DecCtl));
+    w.ctl_bytes = dec_ctl_bytes(L);
+    w.logits = w.ctl_bytes;
+    w.ids = w.logits + al256((uint64_t)T * L->n_expert * 4);
+    w.w = w.ids + al256(P * 4);
+    w.xq = w.w + al256(P * 4);
+    w.ygu = w.xq + al256((uint64_t)T * w.xq_stride);
+    w.aq = w.ygu + al256(P * 2 * L->n_ff * 4);
+    w.ydn = w.aq + al256(P * w.aq_stride);
+    w.total = w.ydn + al256(P * L->d_model * 4);
+    return w;
+}
+
+bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
+    return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && (L->d_model % 4) == 0;
 }
 }  // namespace
 
+void llapis_set_tuning(int32_t key, int32_t value) {
+    if (key == 0) g_decode_path = value != 0;
+    if (key == 1) g_prefetch = value != 0;
+}
+
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
     if (!L || n_tokens <= 0) return 0;
-    return ffn_ws(L, n_tokens).total;
+    uint64_t b = ffn_ws(L, n_tokens).total;
+    if (n_tokens <= DEC_MAXT) b = std::max(b, dec_ws(L, n_tokens).total);
+    return b;
+}
+
+int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream) {
+    if (!L || !workspace) return fail("llapis_moe_ffn_workspace_init: null argument");
+    const DecWs dw = dec_ws(L, 1);
+    const uint64_t n = std::min<uint64_t>(ws_bytes, dw.ctl_bytes);
+    LL_TRY(launch_zero_i32(static_cast<int *>(workspace), (int)(n / 4), (hipStream_t)stream));
+    return 0;
 }
 
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
@@ -547,10 +603,53 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     const uint64_t dn_hot = rbytes(L->hot_dn_type, L->n_ff) * L->d_model;
     const uint64_t dn_cold = rbytes(L->cold_dn_type, L->n_ff) * L->d_model;
     if ((gu_hot | gu_cold | dn_hot | dn_cold) % 16) return fail("llapis_moe_ffn: expert slabs must be multiples of 16 bytes");
-    const FfnWs ws = ffn_ws(L, T);
-    if (!workspace || ws_bytes < ws.total) return fail("llapis_moe_ffn: workspace too small");
     hipStream_t s = (hipStream_t)stream;
     uint8_t * base = static_cast<uint8_t *>(workspace);
+    if (decode_eligible(L, T)) {
+        const DecWs dw = dec_ws(L, T);
+        if (!workspace || ws_bytes < dw.total) return fail("llapis_moe_ffn: workspace too small");
+        DecParams p = {};
+        p.d_model = L->d_model; p.n_ff = L->n_ff; p.n_expert = L->n_expert; p.top_k = L->top_k;
+        p.k_slots = L->k_slots; p.T = T;
+        p.x = x; p.router_w = L->router_w; p.router_b = L->router_b;
+        p.hot_gu = static_cast<const uint8_t *>(L->hot_gu); p.hot_gu_stride = gu_hot;
+        p.cold_gu = static_cast<const uint8_t *>(L->cold_gu); p.cold_gu_stride = gu_cold;
+        p.hot_dn = static_cast<const uint8_t *>(L->hot_dn); p.hot_dn_stride = dn_hot;
+        p.cold_dn = static_cast<const uint8_t *>(L->cold_dn); p.cold_dn_stride = dn_cold;
+        p.exp_slot = L->exp_slot; p.slot_exp = L->slot_exp; p.slot_state = L->slot_state;
+        p.s_hot = L->s_hot; p.s_cold = L->s_cold;
+        p.ctl = reinterpret_cast<DecCtl *>(base + dw.ctl);
+        p.comb_count = reinterpret_cast<int *>(base + dw.comb);
+        p.logits = reinterpret_cast<float *>(base + dw.logits);
+        p.ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + dw.ids);
+        p.w = w_out ? w_out : reinterpret_cast<float *>(base + dw.w);
+        p.xq = base + dw.xq; p.xq_stride = dw.xq_stride;
+        p.ygu = reinterpret_cast<float *>(base + dw.ygu);
+        p.aq = base + dw.aq; p.aq_stride = dw.aq_stride;
+        p.ydn = reinterpret_cast<float *>(base + dw.ydn);
+        p.out = out;
+        const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
+        const int rbd = (int)std::max(rbytes(L->hot_dn_type, L->n_ff), rbytes(L->cold_dn_type, L->n_ff));
+        p.w_lds_gu = dev::align16(16 * rbg + 32);
+        p.w_lds_dn = dev::align16(32 * rbd + 32);
+        p.n_rb_down = dw.n_rb;
+        p.prefetch = g_prefetch.load();
+        p.never = 0;
+        if (dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) <= 65536 && dec_lds_down(p) <= 65536) {
+            int pc = -1;
+            if (g_prof.on) {
+                std::lock_guard<std::mutex> lk(g_prof.mu);
+                if (g_prof.n < PROF_RING) pc = g_prof.n++;
+            }
+            const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+            LL_TRY(prof_mark(pc, 0, s));
+            LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
+                                 src, s, pc >= 0 ? &g_prof.ev[pc][0] : nullptr));
+            return 0;
+        }
+    }
+    const FfnWs ws = ffn_ws(L, T);
+    if (!workspace || ws_bytes < ws.total) return fail("llapis_moe_ffn: workspace too small");
     float * probs = (float *)(base + ws.probs);
     int32_t * ids = ids_out ? ids_out : (int32_t *)(base + ws.ids);
     float * w = w_out ? w_out : (float *)(base + ws.w);

@@ -1,0 +1,513 @@
+// decode.hip -- the MoE layer for decode batches (1..4 tokens) in three
+// kernels on gfx950.
+//
+//   A  k_dec_route   router logits, one wave per expert over all tokens; the
+//                    last workgroup to finish does softmax + top-k per token,
+//                    resolves each routed expert's tier once (the residency
+//                    predicate of moert/cuda/ffn_moe.cu:80-130), groups the
+//                    routed pairs by expert (decode once, dot N: the tokens
+//                    that share an expert read its slab once) and quantises
+//                    the tokens' activations.
+//   B  k_dec_gate_up per (expert group, 16-row block): streams the gate_up
+//                    rows through LDS with 128-bit loads and dots them
+//                    against every member token; also prefetches a slice of
+//                    the same expert's down slab.  The last workgroup of a
+//                    group evaluates GEGLU and quantises each member pair's
+//                    down activation.
+//   C  k_dec_down    per (expert group, 32-row block): the down projection,
+//                    scaled by the expert's .scale; the last arrival of a
+//                    (token, row block) writes the weighted combine of the
+//                    token's top_k outputs for those rows.
+//
+// Cross-workgroup hand-offs use a device-scope fence then an atomic arrival
+// counter; the last arriver fences again before reading the others' data.
+// Kernel A clears the counters of B and C for the call; B clears A's.
+#include "device.h"
+#include "launch.h"
+
+namespace llapis {
+namespace dev {
+
+__constant__ uint16_t c_iq2s_codes_dec[1024] = {
+#include "iq2s_grid.inc"
+};
+
+template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
+static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
+
+// A group record read back from the control block, validated so that no
+// field can send a load or store out of bounds: tier 0/1 only, slot or
+// expert index inside its pool, member count <= DEC_MAXT, members < P.
+__device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
+    GroupInfo gi = p.ctl->groups[g];
+    const int P = p.T * p.top_k;
+    bool ok = (gi.tier == 0 && gi.idx >= 0 && gi.idx < p.k_slots) ||
+              (gi.tier == 1 && gi.idx >= 0 && gi.idx < p.n_expert);
+    gi.n_mem = max(0, min(gi.n_mem, DEC_MAXT));
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+        if (c < gi.n_mem && (gi.mem[c] < 0 || gi.mem[c] >= P)) ok = false;
+    if (!ok) {
+        gi.tier = 2;
+        gi.idx = 0;
+        gi.n_mem = 0;
+    }
+    return gi;
+}
+
+// groups of this call (never more than the launch has rows of workgroups)
+__device__ __forceinline__ int n_groups(const DecParams & p) {
+    return min(p.ctl->n_groups, (int)gridDim.y);
+}
+
+// member i of a group (select chain: keeps the record in registers)
+__device__ __forceinline__ int member(const GroupInfo & g, int i) {
+    return i == 0 ? g.mem[0] : i == 1 ? g.mem[1] : i == 2 ? g.mem[2] : g.mem[3];
+}
+
+__device__ __forceinline__ const uint8_t * group_slab(int tier, int idx, const uint8_t * hot, uint64_t hs,
+                                                      const uint8_t * cold, uint64_t cs) {
+    return tier == 0 ? hot + (uint64_t)idx * hs : cold + (uint64_t)idx * cs;
+}
+
+// ---------------------------------------------------------------- A
+
+// softmax (ggml soft_max: exp(x - max), sum in double, scaled by float(1/sum))
+// and top-K (descending, ties to the lower index) of one token, one wave.
+__device__ void topk_wave(const float * row, int E, int K, int32_t * ids, float * w, int * s_ids) {
+    const int lane = threadIdx.x & 63;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? row[e] : -INFINITY;
+    }
+    const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    double ls = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? expf(v[j] - mx) : 0.0f;
+        ls += (double)v[j];
+    }
+    for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    const float inv = (float)(1.0 / ls);
+    bool taken[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = __fmul_rn(v[j], inv);
+        taken[j] = lane + 64 * j >= E;
+    }
+    float sel = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        uint64_t key = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = lane + 64 * j;
+            const uint64_t kk = taken[j] ? 0 : (((uint64_t)__float_as_uint(v[j]) << 32) | (0xFFFFFFFFu - e)) + 1;
+            key = kk > key ? kk : key;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint64_t other = __shfl_xor(key, o, 64);
+            key = other > key ? other : key;
+        }
+        key -= 1;
+        const uint32_t eb = 0xFFFFFFFFu - (uint32_t)key;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) if ((uint32_t)(lane + 64 * j) == eb) taken[j] = true;
+        if (lane == k) sel = __uint_as_float((uint32_t)(key >> 32));
+        if (lane == 0) {
+            ids[k] = (int32_t)eb;
+            s_ids[k] = (int)eb;
+        }
+    }
+    double s = lane < K ? (double)sel : 0.0;
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    float sf = (float)s;
+    if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
+    if (lane < K) w[lane] = sel / sf;
+}
+
+template <int AM>
+__global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
+    __shared__ int s_last;
+    __shared__ int s_ids[DEC_PMAX];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = p.d_model, E = p.n_expert, T = p.T, K = p.top_k;
+    const int e = blockIdx.x * (WG / 64) + wave;
+    if (e < E) {
+        const float * wrow = p.router_w + (int64_t)e * d;
+        float acc[DEC_MAXT];
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
+        for (int k = 4 * lane; k < d; k += 256) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(wrow + k);
+#pragma unroll
+            for (int t = 0; t < DEC_MAXT; ++t) {
+                if (t < T) {
+                    const float4 x4 = *reinterpret_cast<const float4 *>(p.x + (int64_t)t * d + k);
+                    acc[t] += w4.x * x4.x + w4.y * x4.y + w4.z * x4.z + w4.w * x4.w;
+                }
+            }
+        }
+        const float b = p.router_b ? p.router_b[e] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t) {
+            const float s = wave_sum(acc[t]);
+            if (lane == 0 && t < T) p.logits[(int64_t)t * E + e] = s + b;
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(&p.ctl->route_count, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // ---- last workgroup: selection, groups, activation quantisation
+    if (wave < T) topk_wave(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
+    // counters of B and C for this call start at zero
+    for (int i = threadIdx.x; i < DEC_PMAX; i += WG) p.ctl->group_count[i] = 0;
+    for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
+    __syncthreads();
+    if (wave == 0) {
+        const int P = T * K;
+        const int pr = lane;
+        const bool live = pr < P;
+        const int ex = live ? s_ids[pr] : -1;
+        int leader = pr, slot = 0, nmem = 0;
+        for (int q = 0; q < P; ++q) {
+            const int eq = s_ids[q];
+            if (eq == ex) {
+                if (q < pr) ++slot;
+                if (q < leader) leader = q;
+                ++nmem;
+            }
+        }
+        const bool is_leader = live && leader == pr;
+        const uint64_t lm = __ballot(is_leader);
+        const int gid = __popcll(lm & (leader == 0 ? 0ull : (~0ull >> (64 - leader))));
+        if (is_leader) {
+            int tier = 2, idx = 0;
+            if (ex >= 0 && ex < E) {
+                tier = 1;
+                idx = ex;
+                if (p.k_slots > 0) {
+                    const int s = p.exp_slot[ex];
+                    if (s >= 0 && s < p.k_slots && p.slot_state[s] == 2 && p.slot_exp[s] == ex) {
+                        tier = 0;
+                        idx = s;
+                    }
+                }
+            }
+            p.ctl->groups[gid].tier = tier;
+            p.ctl->groups[gid].idx = idx;
+            p.ctl->groups[gid].n_mem = min(nmem, DEC_MAXT);
+        }
+        if (live && slot < DEC_MAXT) p.ctl->groups[gid].mem[slot] = pr;   // top-k ids of a token are distinct
+        if (lane == 0) p.ctl->n_groups = __popcll(lm);
+    }
+    ActView v;
+    act_layout(d, 0, &v);
+    for (int t = 0; t < T; ++t) {
+        ActSrc src;
+        src.p = p.x + (int64_t)t * d;
+        src.n = d;
+        quantize_act<T_Q4_K, AM, SRC_PLAIN>(p.xq + (int64_t)t * p.xq_stride, v, src, d);
+    }
+}
+
+// ---------------------------------------------------------------- B / C
+
+constexpr int MAXPER_DEC = 8;
+
+// Stage `nch` 16-byte chunks starting at g into LDS at offset `at` (issue
+// first, store after the caller's other work): part 1, the loads.
+struct Staged {
+    u32x4 r[MAXPER_DEC];
+};
+
+__device__ __forceinline__ void stage_load(Staged & s, const u32x4 * g, int nch) {
+    if (nch > 0) {
+#pragma unroll
+        for (int k = 0; k < MAXPER_DEC; ++k) s.r[k] = g[min((int)threadIdx.x + k * WG, nch - 1)];
+    }
+}
+__device__ __forceinline__ void stage_store(const Staged & s, const u32x4 * g, int nch, uint8_t * smem, int at) {
+    if (nch > 0) {
+#pragma unroll
+        for (int k = 0; k < MAXPER_DEC; ++k) {
+            const int i = threadIdx.x + k * WG;
+            if (i < nch) *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = s.r[k];
+        }
+    }
+    for (int i = threadIdx.x + MAXPER_DEC * WG; i < nch; i += WG) *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = g[i];
+}
+
+// copy n bytes (multiple of 16) from global to LDS
+__device__ __forceinline__ void copy16(uint8_t * smem, int at, const uint8_t * src, int n) {
+    for (int i = threadIdx.x; i < n / 16; i += WG)
+        *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = reinterpret_cast<const u32x4 *>(src)[i];
+}
+
+template <int HT, int CT, int AM, int GSRC>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_last;
+    constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
+    static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
+    const int g = blockIdx.y;
+    if (blockIdx.x == 0 && g == 0 && threadIdx.x == 0) p.ctl->route_count = 0;   // A is complete
+    if (g >= n_groups(p)) return;
+    const GroupInfo gi = load_group(p, g);
+    const int F2 = 2 * p.n_ff, d_in = p.d_model;
+    const bool valid = gi.tier < 2;
+    const int wtype = gi.tier == 0 ? HT : CT;
+    const int r0 = blockIdx.x * ROWS;
+    const int rows = min(ROWS, F2 - r0);
+    const int rb = (d_in / blk_elems(wtype)) * blk_bytes(wtype);
+    const uint64_t start = (uint64_t)r0 * rb;
+    const uint64_t c0 = start >> 4;
+    const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
+    const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_gu, p.hot_gu_stride, p.cold_gu, p.cold_gu_stride)
+                              : nullptr;
+    const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+    Staged st;
+    stage_load(st, gW, nch);
+
+    // prefetch this workgroup's slice of the expert's down slab (into L2/MALL)
+    uint32_t sink = 0;
+    if (p.prefetch && valid) {
+        const u32x4 * D = reinterpret_cast<const u32x4 *>(
+            group_slab(gi.tier, gi.idx, p.hot_dn, p.hot_dn_stride, p.cold_dn, p.cold_dn_stride));
+        const uint64_t dstride = gi.tier == 0 ? p.hot_dn_stride : p.cold_dn_stride;
+        const int dch = (int)(dstride >> 4);
+        const int per = (dch + gridDim.x - 1) / gridDim.x;
+        const int b0 = blockIdx.x * per, b1 = min(dch, b0 + per);
+        for (int i = b0 + threadIdx.x; i < b1; i += WG) {
+            const u32x4 v = D[i];
+            sink ^= v.x;
+        }
+    }
+
+    // member activations (quantised by A) and the codebook tables
+    ActView tmp;
+    const int abytes = act_layout(d_in, 0, &tmp);
+    const int a0 = p.w_lds_gu;
+    ActView av[DEC_MAXT];
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
+    const int n_mem = gi.n_mem;
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+        if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(gi.mem[c] / p.top_k) * p.xq_stride, abytes);
+    const int grid_off = align16i(a0 + DEC_MAXT * abytes), sign_off = grid_off + 1024 * 8;
+    if (wtype == T_IQ2_S) build_iq2s_tables(smem, grid_off, sign_off, c_iq2s_codes_dec);
+    stage_store(st, gW, nch, smem, 0);
+    __syncthreads();
+
+    const int rw = threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (valid && rw < rows) {
+        const int wb = (int)(start & 15) + rw * rb;
+        const int U = d_in / Fmt<HT>::UNIT;
+        if (gi.tier == 0) {
+            for (int u = lr; u < U; u += LPR)
+                unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+        } else {
+            for (int u = lr; u < U; u += LPR)
+                unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+#pragma unroll
+        for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
+    if (lr == 0 && rw < rows) {
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c)
+            if (c < n_mem) p.ygu[(int64_t)gi.mem[c] * F2 + r0 + rw] = acc[c];
+    }
+
+    // ---- group completion: the last workgroup builds the down activations
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(&p.ctl->group_count[g], 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (s_last) {
+        __threadfence();
+        ActView v;
+        act_layout(p.n_ff, 0, &v);
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c) {
+            if (c >= n_mem) break;
+            const int pr = gi.mem[c];
+            ActSrc src;
+            src.p = p.ygu + (int64_t)pr * F2;
+            src.n = p.n_ff;
+            quantize_act<T_Q5_0, AM, GSRC>(p.aq + (int64_t)pr * p.aq_stride, v, src, p.n_ff);
+        }
+    }
+    if (p.never) p.ygu[threadIdx.x] = (float)sink;        // keeps the prefetch loads alive
+}
+
+template <int HT, int CT, int AM>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_down(const DecParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_lastc[DEC_MAXT];
+    constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
+    static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && !k256<HT>() && !k256<CT>(), "down formats");
+    const int g = blockIdx.y;
+    if (g >= n_groups(p)) return;
+    const GroupInfo gi = load_group(p, g);
+    const int D = p.d_model, d_in = p.n_ff, K = p.top_k;
+    const bool valid = gi.tier < 2;
+    const int wtype = gi.tier == 0 ? HT : CT;
+    const int r0 = blockIdx.x * ROWS;
+    const int rows = min(ROWS, D - r0);
+    const int rb = (d_in / blk_elems(wtype)) * blk_bytes(wtype);
+    const uint64_t start = (uint64_t)r0 * rb;
+    const uint64_t c0 = start >> 4;
+    const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
+    const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_dn, p.hot_dn_stride, p.cold_dn, p.cold_dn_stride)
+                              : nullptr;
+    const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+    Staged st;
+    stage_load(st, gW, nch);
+
+    ActView tmp;
+    const int abytes = act_layout(d_in, 0, &tmp);
+    const int a0 = p.w_lds_dn;
+    ActView av[DEC_MAXT];
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
+    const int n_mem = gi.n_mem;
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+        if (c < n_mem) copy16(smem, a0 + c * abytes, p.aq + (int64_t)gi.mem[c] * p.aq_stride, abytes);
+    stage_store(st, gW, nch, smem, 0);
+    __syncthreads();
+
+    const int rw = threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (valid && rw < rows) {
+        const int wb = (int)(start & 15) + rw * rb;
+        const int U = d_in / Fmt<HT>::UNIT;
+        if (gi.tier == 0) {
+            for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+        } else {
+            for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+#pragma unroll
+        for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
+    const float sc = !valid ? 0.0f
+                   : gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f) : (p.s_cold ? p.s_cold[gi.idx] : 1.0f);
+    if (lr == 0 && rw < rows) {
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c)
+            if (c < n_mem) p.ydn[(int64_t)gi.mem[c] * D + r0 + rw] = valid ? acc[c] * sc : 0.0f;
+    }
+
+    // ---- combine: the last pair of a token to finish these rows sums them
+    __threadfence();
+    __syncthreads();
+    if ((int)threadIdx.x < n_mem) {
+        const int t = member(gi, threadIdx.x) / K;
+        s_lastc[threadIdx.x] = atomicAdd(&p.comb_count[t * p.n_rb_down + blockIdx.x], 1) == K - 1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) {
+        if (c >= n_mem) break;
+        if (!s_lastc[c]) continue;
+        __threadfence();
+        const int t = gi.mem[c] / K;
+        const float * yt = p.ydn + (int64_t)t * K * D + r0;
+        const float * wt = p.w + t * K;
+        for (int r = threadIdx.x; r < rows; r += WG) {
+            float o = __fmul_rn(yt[r], wt[0]);
+            for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(yt[(int64_t)k * D + r], wt[k]));
+            p.out[(int64_t)t * D + r0 + r] = o;
+        }
+    }
+}
+
+__global__ void k_zero(int * p, int n) {
+    for (int i = blockIdx.x * WG + threadIdx.x; i < n; i += gridDim.x * WG) p[i] = 0;
+}
+
+}  // namespace dev
+
+using namespace dev;
+
+int dec_act_bytes(int n) {
+    ActView v;
+    return act_layout(n, 0, &v);
+}
+
+int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
+    ActView v;
+    const int ab = act_layout(p.d_model, 0, &v);
+    const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
+    return align16i(p.w_lds_gu + DEC_MAXT * ab) + (iq2 ? 1024 * 8 + 256 * 16 : 0);
+}
+
+int dec_lds_down(const DecParams & p) {
+    ActView v;
+    const int ab = act_layout(p.n_ff, 0, &v);
+    return p.w_lds_dn + DEC_MAXT * ab;
+}
+
+hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
+                         hipEvent_t * ev) {
+    auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
+    const int P = p.T * p.top_k;
+    {
+        dim3 grid((p.n_expert + 3) / 4);
+        if (am == AM_CPU) hipLaunchKernelGGL(k_dec_route<AM_CPU>, grid, dim3(WG), 0, s, p);
+        else hipLaunchKernelGGL(k_dec_route<AM_Q8_1>, grid, dim3(WG), 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = mark(1);
+        if (e == hipSuccess) e = mark(2);
+        if (e != hipSuccess) return e;
+    }
+    {
+        dim3 grid((2 * p.n_ff + 15) / 16, P);
+        const int lds = dec_lds_gate_up(p, hgu, cgu);
+#define LL_GU(A, B, M, G) \
+        if (hgu == A && cgu == B && am == M && gelu == G) hipLaunchKernelGGL((k_dec_gate_up<A, B, M, G>), grid, dim3(WG), lds, s, p); else
+#define LL_GU2(A, B) LL_GU(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_GU(A, B, AM_CPU, SRC_GEGLU_TANH) \
+                     LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TANH)
+        LL_GU2(T_Q4_K, T_IQ2_S) LL_GU2(T_Q4_K, T_Q4_K) LL_GU2(T_IQ2_S, T_IQ2_S) LL_GU2(T_IQ2_S, T_Q4_K)
+        return hipErrorInvalidValue;
+#undef LL_GU2
+#undef LL_GU
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = mark(3);
+        if (e != hipSuccess) return e;
+    }
+    {
+        dim3 grid(p.n_rb_down, P);
+        const int lds = dec_lds_down(p);
+#define LL_DN(A, B, M) if (hdn == A && cdn == B && am == M) hipLaunchKernelGGL((k_dec_down<A, B, M>), grid, dim3(WG), lds, s, p); else
+#define LL_DN2(A, B) LL_DN(A, B, AM_CPU) LL_DN(A, B, AM_Q8_1)
+        LL_DN2(T_Q5_0, T_IQ4_NL) LL_DN2(T_Q5_0, T_Q5_0) LL_DN2(T_IQ4_NL, T_IQ4_NL) LL_DN2(T_IQ4_NL, T_Q5_0)
+        return hipErrorInvalidValue;
+#undef LL_DN2
+#undef LL_DN
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = mark(4);
+    if (e == hipSuccess) e = mark(5);
+    return e;
+}
+
+hipError_t launch_zero_i32(int * p, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_zero, dim3(std::min(1024, (n + WG - 1) / WG)), dim3(WG), 0, s, p, n);
+    return hipGetLastError();
+}
+
+}  // namespace llapis

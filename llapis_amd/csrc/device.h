@@ -21,6 +21,25 @@ enum { SRC_PLAIN = 0, SRC_GEGLU_TABLE = 1, SRC_GEGLU_TANH = 2 };
 
 // --------------------------------------------------------------- LDS views
 
+// Byte offsets of one quantised activation column (relative to some base):
+// int8 values, per-32 scale and sum, per-256 scale, per-16 block sums.  The
+// same layout is used in LDS and for columns stored in global memory.
+struct ActView {
+    int q, d32, s32, dK, bsum;
+};
+
+LL_HD inline int align16i(int x) { return (x + 15) & ~15; }
+
+// layout of an n-value column placed at byte offset `at`; returns its size
+LL_HD inline int act_layout(int n, int at, ActView * v) {
+    v->q = at;
+    v->d32 = align16i(at + n);
+    v->s32 = v->d32 + (n / 32) * 4;
+    v->dK = align16i(v->s32 + (n / 32) * 4);
+    v->bsum = align16i(v->dK + (n / 256 + 1) * 4);
+    return align16i(v->bsum + (n / 16) * 4 + 16) - at;
+}
+
 // Byte offsets inside the dynamic LDS block of one workgroup.
 struct LdsLayout {
     int w;        // staged weight bytes (16-aligned)
@@ -125,11 +144,11 @@ __device__ __forceinline__ float act_at(const ActSrc & s, int k) {
 // max is the first element of largest magnitude; iscale = -127/max;
 // q = min(127, nearest_int(iscale x)); d = 1/iscale; bsums over 16.
 template <int SRC>
-__device__ __forceinline__ void quantize_q8_K_lds(uint8_t * smem, const LdsLayout & L, const ActSrc & src, int d_in) {
+__device__ __forceinline__ void quantize_q8_K(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int8_t * q = reinterpret_cast<int8_t *>(smem + L.q);
-    float * dK = reinterpret_cast<float *>(smem + L.dK);
-    int * bsum = reinterpret_cast<int *>(smem + L.bsum);
+    int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
+    float * dK = reinterpret_cast<float *>(base + L.dK);
+    int * bsum = reinterpret_cast<int *>(base + L.bsum);
     for (int b = wave; b < d_in / 256; b += WG / 64) {
         float v[4];
         uint64_t key = 0;
@@ -179,11 +198,11 @@ __device__ __forceinline__ void quantize_q8_K_lds(uint8_t * smem, const LdsLayou
 // q = roundf(x/d), s = butterfly sum of x; both stored as fp16.
 // One wave handles two 32-blocks per step.
 template <int SRC, int AM>
-__device__ __forceinline__ void quantize_q8_32_lds(uint8_t * smem, const LdsLayout & L, const ActSrc & src, int d_in) {
+__device__ __forceinline__ void quantize_q8_32(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int8_t * q = reinterpret_cast<int8_t *>(smem + L.q);
-    float * d32 = reinterpret_cast<float *>(smem + L.d32);
-    float * s32 = reinterpret_cast<float *>(smem + L.s32);
+    int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
+    float * d32 = reinterpret_cast<float *>(base + L.d32);
+    float * s32 = reinterpret_cast<float *>(base + L.s32);
     for (int base = wave * 64; base < d_in; base += WG) {
         const int pos = base + lane;
         const bool live = pos < d_in;          // d_in is a multiple of 32, not always of 64
@@ -213,12 +232,19 @@ __device__ __forceinline__ void quantize_q8_32_lds(uint8_t * smem, const LdsLayo
     }
 }
 
+// Quantise an activation column into the format weight type T is dotted with.
+template <int T, int AM, int SRC>
+__device__ __forceinline__ void quantize_act(uint8_t * base, const ActView & v, const ActSrc & src, int n) {
+    if constexpr (AM == AM_CPU && (T == T_Q4_K || T == T_IQ2_S)) quantize_q8_K<SRC>(base, v, src, n);
+    else quantize_q8_32<SRC, AM>(base, v, src, n);
+}
+
 // IQ2_S tables in LDS: the codebook as bytes {0x08,0x19,0x2b} per level, and
 // for each sign byte s the negation masks {m_lo, m_hi, m_lo & 1s, m_hi & 1s}
 // with m = 0xFF in every byte whose sign bit is set.
-__device__ __forceinline__ void build_iq2s_tables(uint8_t * smem, const LdsLayout & L, const uint16_t * codes) {
-    uint2 * grid = reinterpret_cast<uint2 *>(smem + L.grid);
-    uint4 * sign = reinterpret_cast<uint4 *>(smem + L.sign);
+__device__ __forceinline__ void build_iq2s_tables(uint8_t * smem, int grid_off, int sign_off, const uint16_t * codes) {
+    uint2 * grid = reinterpret_cast<uint2 *>(smem + grid_off);
+    uint4 * sign = reinterpret_cast<uint4 *>(smem + sign_off);
     for (int k = threadIdx.x; k < 1024; k += WG) {
         const uint32_t c = codes[k];
         uint32_t lo = 0, hi = 0;
@@ -244,10 +270,13 @@ __device__ __forceinline__ void build_iq2s_tables(uint8_t * smem, const LdsLayou
 
 // ------------------------------------------------------------ unit dots
 //
-// A unit is the slice of a weight row one lane dots at a time:
+// A unit is the slice of a weight row one lane handles at a time:
 //   Q4_K, IQ2_S: a quarter super-block (64 values, two 32-sub-blocks)
 //   Q5_0, IQ4_NL: one 32-block
-// `wb` is the LDS byte offset of the row, u the unit index in the row.
+// Each unit is decoded from LDS once and dotted against up to NC activation
+// columns (decode once, dot N: the columns of the tokens that routed to the
+// same expert).  `wb` is the LDS byte offset of the row, `u` the unit index,
+// av[c] the LDS offsets of column c's quantised activation.
 
 template <int T> struct Fmt;
 template <> struct Fmt<T_Q4_K>   { static constexpr int UNIT = 64; static constexpr int LPR = 16; };
@@ -255,17 +284,22 @@ template <> struct Fmt<T_IQ2_S>  { static constexpr int UNIT = 64; static conste
 template <> struct Fmt<T_Q5_0>   { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
 template <> struct Fmt<T_IQ4_NL> { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
 
+__device__ __forceinline__ u32x4 lds128(const uint8_t * smem, int off) {   // off % 16 == 0
+    return *reinterpret_cast<const u32x4 *>(smem + off);
+}
+
 // Q4_K . q8_K   (ggml-cpu/quants.c:645-718): per super-block
 //   d_w dK sum_j sc_j dot_j  -  dmin_w dK sum_j m_j (bsum_2j + bsum_2j+1)
 // Q4_K . q8_1   (ggml-cuda/vecdotq.cuh:505-528): per 32-block b
 //   d_w d8_b sc_b dot_b  -  dmin_w d8_b m_b sum(q8_b)
-template <int AM>
-__device__ __forceinline__ float q4k_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+template <int AM, int NC>
+__device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
+                                         float * acc) {
     const int sb = u >> 2, qq = u & 3;
     const int blk = wb + sb * 144;                        // 16-aligned
-    const uint4 hdr = *reinterpret_cast<const uint4 *>(smem + blk);
-    const uint4 qa = *reinterpret_cast<const uint4 *>(smem + blk + 16 + 32 * qq);
-    const uint4 qb = *reinterpret_cast<const uint4 *>(smem + blk + 32 + 32 * qq);
+    const u32x4 hdr = lds128(smem, blk);
+    const u32x4 qa = lds128(smem, blk + 16 + 32 * qq);
+    const u32x4 qb = lds128(smem, blk + 32 + 32 * qq);
     // 6-bit scales/mins of sub-blocks j0 = 2qq, j1 = 2qq + 1 (get_scale_min_k4)
     const uint32_t s03 = hdr.y, s47 = hdr.z, s8b = hdr.w;
     int sc0, m0, sc1, m1;
@@ -281,37 +315,45 @@ __device__ __forceinline__ float q4k_unit(const uint8_t * smem, const LdsLayout 
         m1  = ((s8b >> sh1) >> 4 & 0xF) | (((s47 >> sh1) >> 6 & 3) << 4);
     }
     const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
-    const int ao = L.q + sb * 256 + 64 * qq;
     const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + ao);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + ao + 16);
-    const uint4 a2 = *reinterpret_cast<const uint4 *>(smem + ao + 32);
-    const uint4 a3 = *reinterpret_cast<const uint4 *>(smem + ao + 48);
-    const uint32_t alo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const uint32_t ahi[8] = {a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-    int dot1 = 0, dot2 = 0;
+    uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        dot1 = dot4((int)(w[i] & 0x0F0F0F0Fu), (int)alo[i], dot1);
-        dot2 = dot4((int)((w[i] >> 4) & 0x0F0F0F0Fu), (int)ahi[i], dot2);
+        lo[i] = w[i] & 0x0F0F0F0Fu;
+        hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
     }
-    if (AM == AM_CPU) {
-        const float dK = reinterpret_cast<const float *>(smem + L.dK)[sb];
-        const int * bs = reinterpret_cast<const int *>(smem + L.bsum) + sb * 16 + 4 * qq;
-        const int sumi = sc0 * dot1 + sc1 * dot2;
-        const int summ = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
-        return __fmul_rn(d * dK, (float)sumi) - __fmul_rn(dmin * dK, (float)summ);
-    } else {
-        int sq0 = 0, sq1 = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (c >= nc) break;
+        const int ao = av[c].q + sb * 256 + 64 * qq;
+        const u32x4 a0 = lds128(smem, ao), a1 = lds128(smem, ao + 16);
+        const u32x4 a2 = lds128(smem, ao + 32), a3 = lds128(smem, ao + 48);
+        const uint32_t alo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const uint32_t ahi[8] = {a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+        int dot1 = 0, dot2 = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            sq0 = dot4(0x01010101, (int)alo[i], sq0);
-            sq1 = dot4(0x01010101, (int)ahi[i], sq1);
+            dot1 = dot4((int)lo[i], (int)alo[i], dot1);
+            dot2 = dot4((int)hi[i], (int)ahi[i], dot2);
         }
-        const float * d32 = reinterpret_cast<const float *>(smem + L.d32) + (sb * 256 + 64 * qq) / 32;
-        const float sd = d32[0] * (float)(dot1 * sc0) + d32[1] * (float)(dot2 * sc1);
-        const float sm = d32[0] * (float)(sq0 * m0) + d32[1] * (float)(sq1 * m1);
-        return d * sd - dmin * sm;
+        if (AM == AM_CPU) {
+            const float dK = reinterpret_cast<const float *>(smem + av[c].dK)[sb];
+            const int * bs = reinterpret_cast<const int *>(smem + av[c].bsum) + sb * 16 + 4 * qq;
+            const int sumi = sc0 * dot1 + sc1 * dot2;
+            const int summ = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+            acc[c] += __fmul_rn(d * dK, (float)sumi) - __fmul_rn(dmin * dK, (float)summ);
+        } else {
+            int sq0 = 0, sq1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sq0 = dot4(0x01010101, (int)alo[i], sq0);
+                sq1 = dot4(0x01010101, (int)ahi[i], sq1);
+            }
+            const float * d32 = reinterpret_cast<const float *>(smem + av[c].d32) + (sb * 256 + 64 * qq) / 32;
+            const float sd = d32[0] * (float)(dot1 * sc0) + d32[1] * (float)(dot2 * sc1);
+            const float sm = d32[0] * (float)(sq0 * m0) + d32[1] * (float)(sq1 * m1);
+            acc[c] += d * sd - dmin * sm;
+        }
     }
 }
 
@@ -319,8 +361,10 @@ __device__ __forceinline__ float q4k_unit(const uint8_t * smem, const LdsLayout 
 //   0.125 d_w dK sum_ib [(2 sc_lo + 1) s_1 + (2 sc_hi + 1) s_2]
 // IQ2_S . q8_1  (ggml-cuda/vecdotq.cuh:1061-1105): per 32-block
 //   d_w d8 ((s_1 sc_lo + s_2 sc_hi + (s_1 + s_2)/2) / 4)   (C integer division)
-template <int AM>
-__device__ __forceinline__ float iq2s_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+// The codebook and sign masks are in LDS (tables at `grid`, `sign`).
+template <int AM, int NC>
+__device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
+                                          float * acc, int grid_off, int sign_off) {
     const int sb = u >> 2, qq = u & 3;
     const int blk = wb + sb * 82;                         // 2-aligned
     const float d = h2f(lds32u(smem, blk));
@@ -328,112 +372,147 @@ __device__ __forceinline__ float iq2s_unit(const uint8_t * smem, const LdsLayout
     const uint32_t sg0 = lds32u(smem, blk + 34 + 8 * qq), sg1 = lds32u(smem, blk + 38 + 8 * qq);
     const uint32_t qh2 = lds32u(smem, blk + 66 + 2 * qq);
     const uint32_t sc2 = lds32u(smem, blk + 74 + 2 * qq);
-    const uint2 * grid = reinterpret_cast<const uint2 *>(smem + L.grid);
-    const uint4 * sign = reinterpret_cast<const uint4 *>(smem + L.sign);
-    const int ao = L.q + sb * 256 + 64 * qq;
-    int bsum = 0;
-    float acc = 0.0f;
+    const uint2 * grid = reinterpret_cast<const uint2 *>(smem + grid_off);
+    const uint4 * sign = reinterpret_cast<const uint4 *>(smem + sign_off);
+    // signed codebook bytes of the unit's 8 groups of 8
+    uint32_t g0[8], g1[8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t qhb = (qh2 >> (8 * h)) & 0xFF, scb = (sc2 >> (8 * h)) & 0xFF;
-        int s[2] = {0, 0};
+    for (int g = 0; g < 8; ++g) {
+        const uint32_t qhb = (qh2 >> (8 * (g >> 2))) & 0xFF;
+        const uint32_t idx = byte_of(qs0, qs1, g) | (((qhb >> (2 * (g & 3))) & 3) << 8);
+        const uint2 gv = grid[idx];
+        const uint4 m = sign[byte_of(sg0, sg1, g)];
+        g0[g] = (gv.x ^ m.x) + m.z;
+        g1[g] = (gv.y ^ m.y) + m.w;
+    }
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const int g = 4 * h + l;
-            const uint32_t idx = byte_of(qs0, qs1, g) | (((qhb >> (2 * l)) & 3) << 8);
-            const uint2 gv = grid[idx];
-            const uint4 m = sign[byte_of(sg0, sg1, g)];
-            const int g0 = (int)((gv.x ^ m.x) + m.z);
-            const int g1 = (int)((gv.y ^ m.y) + m.w);
-            const uint2 a = *reinterpret_cast<const uint2 *>(smem + ao + 32 * h + 8 * l);
-            s[l >> 1] = dot4(g0, (int)a.x, s[l >> 1]);
-            s[l >> 1] = dot4(g1, (int)a.y, s[l >> 1]);
+    for (int c = 0; c < NC; ++c) {
+        if (c >= nc) break;
+        const int ao = av[c].q + sb * 256 + 64 * qq;
+        int bsum = 0;
+        float accf = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t scb = (sc2 >> (8 * h)) & 0xFF;
+            int s[2] = {0, 0};
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int g = 4 * h + l;
+                const uint2 a = *reinterpret_cast<const uint2 *>(smem + ao + 32 * h + 8 * l);
+                s[l >> 1] = dot4((int)g0[g], (int)a.x, s[l >> 1]);
+                s[l >> 1] = dot4((int)g1[g], (int)a.y, s[l >> 1]);
+            }
+            if (AM == AM_CPU) {
+                bsum += (2 * (int)(scb & 15) + 1) * s[0] + (2 * (int)(scb >> 4) + 1) * s[1];
+            } else {
+                const int sumi = (s[0] * (int)(scb & 15) + s[1] * (int)(scb >> 4) + (s[0] + s[1]) / 2) / 4;
+                const float d8 = reinterpret_cast<const float *>(smem + av[c].d32)[(sb * 256 + 64 * qq + 32 * h) / 32];
+                accf += (d * d8) * (float)sumi;
+            }
         }
         if (AM == AM_CPU) {
-            bsum += (2 * (int)(scb & 15) + 1) * s[0] + (2 * (int)(scb >> 4) + 1) * s[1];
+            const float dK = reinterpret_cast<const float *>(smem + av[c].dK)[sb];
+            acc[c] += 0.125f * __fmul_rn(d * dK, (float)bsum);
         } else {
-            const int sumi = (s[0] * (int)(scb & 15) + s[1] * (int)(scb >> 4) + (s[0] + s[1]) / 2) / 4;
-            const float d8 = reinterpret_cast<const float *>(smem + L.d32)[(sb * 256 + 64 * qq + 32 * h) / 32];
-            acc += (d * d8) * (float)sumi;
+            acc[c] += accf;
         }
     }
-    if (AM == AM_CPU) {
-        const float dK = reinterpret_cast<const float *>(smem + L.dK)[sb];
-        return 0.125f * __fmul_rn(d * dK, (float)bsum);
-    }
-    return acc;
 }
 
 // Q5_0 . q8_0  (ggml-cpu/quants.c:314-352):  d_w d8 sum (q - 16) a
 // Q5_0 . q8_1  (ggml-cuda/vecdotq.cuh:172-198): d_w (d8 sum q a - 16 s8)
-template <int AM>
-__device__ __forceinline__ float q5_0_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
+template <int AM, int NC>
+__device__ __forceinline__ void q5_0_unit(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
+                                          float * acc) {
     const int blk = wb + u * 22;                          // 2-aligned
     const float d = h2f(lds32u(smem, blk));
     const uint32_t qh = lds32u(smem, blk + 2);
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32 + 16);
-    const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
-    int sumi = 0, suma = 0;
+    uint32_t v0[4], v1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t qsw = lds32u(smem, blk + 6 + 4 * i);
         const uint32_t vh0 = qh >> (4 * i), vh1 = qh >> (16 + 4 * i);
-        uint32_t v0 = qsw & 0x0F0F0F0Fu;
-        v0 |= (vh0 << 4) & 0x10u; v0 |= (vh0 << 11) & 0x1000u; v0 |= (vh0 << 18) & 0x100000u; v0 |= (vh0 << 25) & 0x10000000u;
-        uint32_t v1 = (qsw >> 4) & 0x0F0F0F0Fu;
-        v1 |= (vh1 << 4) & 0x10u; v1 |= (vh1 << 11) & 0x1000u; v1 |= (vh1 << 18) & 0x100000u; v1 |= (vh1 << 25) & 0x10000000u;
-        sumi = dot4((int)v0, (int)alo[i], sumi);
-        sumi = dot4((int)v1, (int)ahi[i], sumi);
+        uint32_t a = qsw & 0x0F0F0F0Fu;
+        a |= (vh0 << 4) & 0x10u; a |= (vh0 << 11) & 0x1000u; a |= (vh0 << 18) & 0x100000u; a |= (vh0 << 25) & 0x10000000u;
+        uint32_t b = (qsw >> 4) & 0x0F0F0F0Fu;
+        b |= (vh1 << 4) & 0x10u; b |= (vh1 << 11) & 0x1000u; b |= (vh1 << 18) & 0x100000u; b |= (vh1 << 25) & 0x10000000u;
+        v0[i] = a;
+        v1[i] = b;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (c >= nc) break;
+        const u32x4 a0 = lds128(smem, av[c].q + u * 32), a1 = lds128(smem, av[c].q + u * 32 + 16);
+        const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
+        int sumi = 0, suma = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sumi = dot4((int)v0[i], (int)alo[i], sumi);
+            sumi = dot4((int)v1[i], (int)ahi[i], sumi);
+            if (AM == AM_CPU) {
+                suma = dot4(0x01010101, (int)alo[i], suma);
+                suma = dot4(0x01010101, (int)ahi[i], suma);
+            }
+        }
+        const float d8 = reinterpret_cast<const float *>(smem + av[c].d32)[u];
         if (AM == AM_CPU) {
-            suma = dot4(0x01010101, (int)alo[i], suma);
-            suma = dot4(0x01010101, (int)ahi[i], suma);
+            acc[c] += __fmul_rn(d * d8, (float)(sumi - 16 * suma));
+        } else {
+            const float s8 = reinterpret_cast<const float *>(smem + av[c].s32)[u];
+            acc[c] += d * ((float)sumi * d8 - 16.0f * s8);
         }
     }
-    const float d8 = reinterpret_cast<const float *>(smem + L.d32)[u];
-    if (AM == AM_CPU) return __fmul_rn(d * d8, (float)(sumi - 16 * suma));
-    const float s8 = reinterpret_cast<const float *>(smem + L.s32)[u];
-    return d * ((float)sumi * d8 - 16.0f * s8);
 }
 
 // 16-entry signed-byte table lookup of four nibble indices (one per byte).
-__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx, const uint32_t tab[4]) {
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx) {
+    // kvalues_iq4nl (ggml-common.h:1110) as little-endian bytes
+    const uint32_t t0 = 0xBFAD9881u, t1 = 0xF6EADDCFu, t2 = 0x26190D01u, t3 = 0x71594535u;
     const uint32_t sel = idx & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(tab[1], tab[0], sel);
-    const uint32_t hi = __builtin_amdgcn_perm(tab[3], tab[2], sel);
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
     const uint32_t m = ((idx & 0x08080808u) >> 3) * 0xFFu;
     return (hi & m) | (lo & ~m);
 }
 
 // IQ4_NL . q8_0 (ggml-cpu/quants.c:1203-1228) and . q8_1 (vecdotq.cuh:1270-1289):
 //   d_w d8 sum kvalues[q] a
-template <int AM>
-__device__ __forceinline__ float iq4nl_unit(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
-    // kvalues_iq4nl as little-endian bytes
-    const uint32_t tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+template <int AM, int NC>
+__device__ __forceinline__ void iq4nl_unit(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
+                                           float * acc) {
     const int blk = wb + u * 18;                          // 2-aligned
     const float d = h2f(lds32u(smem, blk));
-    const uint4 a0 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32);
-    const uint4 a1 = *reinterpret_cast<const uint4 *>(smem + L.q + u * 32 + 16);
-    const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
-    int sumi = 0;
+    uint32_t v0[4], v1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t qsw = lds32u(smem, blk + 2 + 4 * i);
-        sumi = dot4((int)iq4nl_lookup(qsw & 0x0F0F0F0Fu, tab), (int)alo[i], sumi);
-        sumi = dot4((int)iq4nl_lookup((qsw >> 4) & 0x0F0F0F0Fu, tab), (int)ahi[i], sumi);
+        v0[i] = iq4nl_lookup(qsw & 0x0F0F0F0Fu);
+        v1[i] = iq4nl_lookup((qsw >> 4) & 0x0F0F0F0Fu);
     }
-    const float d8 = reinterpret_cast<const float *>(smem + L.d32)[u];
-    if (AM == AM_CPU) return __fmul_rn(d8 * d, (float)sumi);
-    return (d * d8) * (float)sumi;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (c >= nc) break;
+        const u32x4 a0 = lds128(smem, av[c].q + u * 32), a1 = lds128(smem, av[c].q + u * 32 + 16);
+        const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
+        int sumi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sumi = dot4((int)v0[i], (int)alo[i], sumi);
+            sumi = dot4((int)v1[i], (int)ahi[i], sumi);
+        }
+        const float d8 = reinterpret_cast<const float *>(smem + av[c].d32)[u];
+        if (AM == AM_CPU) acc[c] += __fmul_rn(d8 * d, (float)sumi);
+        else acc[c] += (d * d8) * (float)sumi;
+    }
 }
 
-template <int T, int AM>
-__device__ __forceinline__ float unit_dot_t(const uint8_t * smem, const LdsLayout & L, int wb, int u) {
-    if constexpr (T == T_Q4_K) return q4k_unit<AM>(smem, L, wb, u);
-    else if constexpr (T == T_IQ2_S) return iq2s_unit<AM>(smem, L, wb, u);
-    else if constexpr (T == T_Q5_0) return q5_0_unit<AM>(smem, L, wb, u);
-    else return iq4nl_unit<AM>(smem, L, wb, u);
+template <int T, int AM, int NC>
+__device__ __forceinline__ void unit_dot_n(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
+                                           float * acc, int grid_off, int sign_off) {
+    if constexpr (T == T_Q4_K) q4k_unit<AM, NC>(smem, wb, u, av, nc, acc);
+    else if constexpr (T == T_IQ2_S) iq2s_unit<AM, NC>(smem, wb, u, av, nc, acc, grid_off, sign_off);
+    else if constexpr (T == T_Q5_0) q5_0_unit<AM, NC>(smem, wb, u, av, nc, acc);
+    else iq4nl_unit<AM, NC>(smem, wb, u, av, nc, acc);
 }
 
 #endif  // __HIPCC__

@@ -38,6 +38,65 @@ void mmv_prepare(MmvParams & p, int ht, int ct);
 // launch over n_channels channels; returns hipSuccess or the launch error
 hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int act_mode, int src, int n_channels, hipStream_t s);
 
+// ------------------------------------------------------------ decode path
+
+constexpr int DEC_MAXT = 4;     // tokens per decode call (a 3-deep MTP verify plus the token)
+constexpr int DEC_PMAX = 64;    // routed pairs per call (DEC_MAXT * top_k, top_k <= 16)
+
+// one routed expert of the call and the pairs that use it
+struct GroupInfo {
+    int tier;                   // 0 hot (idx = slot), 1 cold (idx = expert), 2 invalid id
+    int idx;
+    int n_mem;
+    int pad;
+    int mem[DEC_MAXT];          // routed-pair indices, one per member token
+};
+
+// control block at the start of the decode workspace (zero before first use)
+struct DecCtl {
+    int route_count;
+    int n_groups;
+    int pad[2];
+    int group_count[DEC_PMAX];
+    GroupInfo groups[DEC_PMAX];
+};
+
+struct DecParams {
+    int d_model, n_ff, n_expert, top_k, k_slots, T;
+    const float * x;
+    const float * router_w;
+    const float * router_b;
+    const uint8_t * hot_gu; uint64_t hot_gu_stride;
+    const uint8_t * cold_gu; uint64_t cold_gu_stride;
+    const uint8_t * hot_dn; uint64_t hot_dn_stride;
+    const uint8_t * cold_dn; uint64_t cold_dn_stride;
+    const int32_t * exp_slot; const int32_t * slot_exp; const int32_t * slot_state;
+    const float * s_hot; const float * s_cold;
+    DecCtl * ctl;
+    int * comb_count;           // [DEC_MAXT][n_rb_down]
+    float * logits;             // [T][n_expert]
+    int32_t * ids;              // [T][top_k]
+    float * w;                  // [T][top_k]
+    uint8_t * xq; int64_t xq_stride;     // quantised tokens
+    float * ygu;                // [P][2 n_ff]
+    uint8_t * aq; int64_t aq_stride;     // quantised down activations per pair
+    float * ydn;                // [P][d_model]
+    float * out;                // [T][d_model]
+    int w_lds_gu, w_lds_dn;     // LDS bytes for staged weights
+    int n_rb_down;              // 32-row blocks of the down projection
+    int prefetch;               // prefetch down slabs during gate_up
+    int never;                  // always 0 (keeps prefetch loads from being dropped)
+};
+
+int dec_act_bytes(int n);
+int dec_lds_gate_up(const DecParams & p, int ht, int ct);
+int dec_lds_down(const DecParams & p);
+// ev (optional): 6 events; ev[0] is recorded by the caller before the call,
+// ev[1..2] after kernel A, ev[3] after B, ev[4..5] after C
+hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
+                         hipStream_t s, hipEvent_t * ev);
+hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
+
 hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
                                 float * logits, hipStream_t s);
 hipError_t launch_topk(float * probs_inout, int T, int E, int K, int32_t * ids, float * w, hipStream_t s);

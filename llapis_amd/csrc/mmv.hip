@@ -93,13 +93,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     }
 
     // ---- 3. activation into LDS (+ IQ2_S tables)
-    if (wtype == T_IQ2_S) build_iq2s_tables(smem, L, c_iq2s_codes);
+    const ActView av = {L.q, L.d32, L.s32, L.dK, L.bsum};
+    if (wtype == T_IQ2_S) build_iq2s_tables(smem, L.grid, L.sign, c_iq2s_codes);
     if (valid) {
         ActSrc src;
         src.p = p.act + (int64_t)col * p.act_ld;
         src.n = p.d_in;
-        if constexpr (AM == AM_CPU && is_k256<HT>()) quantize_q8_K_lds<SRC>(smem, L, src, p.d_in);
-        else quantize_q8_32_lds<SRC, AM>(smem, L, src, p.d_in);
+        quantize_act<HT, AM, SRC>(smem, av, src, p.d_in);
     }
 
     // ---- 4. weights into LDS, then dot
@@ -121,9 +121,9 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         constexpr int UNIT = Fmt<HT>::UNIT;
         const int U = p.d_in / UNIT;
         if (tier == 0) {
-            for (int u = lr; u < U; u += LPR) acc += unit_dot_t<HT, AM>(smem, L, wb, u);
+            for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid, L.sign);
         } else {
-            for (int u = lr; u < U; u += LPR) acc += unit_dot_t<CT, AM>(smem, L, wb, u);
+            for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid, L.sign);
         }
     }
 #pragma unroll

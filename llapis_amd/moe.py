@@ -269,7 +269,8 @@ class DeviceLayer:
         d = self.desc()
         need = int(lib().llapis_moe_ffn_workspace_size(C.byref(d), n_tokens))
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            # zero-filled: the decode path keeps its control block here
+            self._ws = torch.zeros(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
     def forward(self, x, out=None, ids=None, weights=None, stream=None):

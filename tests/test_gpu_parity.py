@@ -206,3 +206,35 @@ def test_island_fires_match_layer(gpu, oracle):
     st = L.MoertCudaStats()
     la.lib().moert_cuda_stats_get(C.byref(st))
     assert st.fires >= 2
+
+
+@pytest.mark.parametrize("T,n_hot", [(1, 0), (1, 16), (2, 7), (4, 9), (4, 0)])
+def test_decode_path_matches_generic_path(gpu, T, n_hot):
+    """The three-kernel decode path (expert groups, fused GEGLU quantisation,
+    last-arrival combine) against the generic per-pair path, with and
+    without the down-slab prefetch, over several calls on one workspace."""
+    torch = torch_mod()
+    say(f"decode vs generic T={T} hot={n_hot}")
+    spec = FULL16
+    lay = _layer_case(spec, 60 + n_hot, n_hot, True)
+    dl = la.DeviceLayer(lay, gpu)
+    lib = la.lib()
+    outs = {}
+    try:
+        for name, dec, pf in (("generic", 0, 0), ("decode", 1, 1), ("decode_nopf", 1, 0)):
+            lib.llapis_set_tuning(0, dec)
+            lib.llapis_set_tuning(1, pf)
+            res = []
+            for rep in range(3):
+                x = tokens(300 + rep, T, spec.d_model)
+                out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+                res.append((out.cpu().numpy().copy(), ids.cpu().numpy().copy(), w.cpu().numpy().copy()))
+            outs[name] = res
+    finally:
+        lib.llapis_set_tuning(0, 1)
+        lib.llapis_set_tuning(1, 1)
+    for name in ("decode", "decode_nopf"):
+        for (o, i, w), (og, ig, wg) in zip(outs[name], outs["generic"]):
+            assert np.array_equal(i, ig)
+            assert np.allclose(w, wg, rtol=1e-6, atol=0)
+            assert rel_l2(o, og) <= 1e-6, rel_l2(o, og)
