@@ -19,8 +19,12 @@
 //                    (token, row block) writes the weighted combine of the
 //                    token's top_k outputs for those rows.
 //
-// Cross-workgroup hand-offs use a device-scope fence then an atomic arrival
-// counter; the last arriver fences again before reading the others' data.
+// Cross-workgroup hand-offs inside a kernel never touch the L2 as a whole:
+// the values another workgroup will read are written with device-scope
+// coherent stores (write-through past the per-XCD L2), each thread waits for
+// its stores to complete, then one thread bumps an arrival counter; the last
+// arriver reads with device-scope coherent loads.  (A device-scope fence
+// would write back and invalidate the XCD's whole L2 in every workgroup.)
 // Kernel A clears the counters of B and C for the call; B clears A's.
 #include "device.h"
 #include "launch.h"
@@ -33,6 +37,25 @@ __constant__ uint16_t c_iq2s_codes_dec[1024] = {
 };
 
 template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
+
+__device__ __forceinline__ void st_coh(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float * p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// this thread's outstanding vector memory operations have completed
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// all threads' coherent stores are complete; thread 0 arrives on `counter`;
+// returns (to every thread) whether this workgroup arrived last of `n`
+__device__ __forceinline__ bool arrive_last(int * counter, int n, int * s_flag) {
+    wait_vm();
+    __syncthreads();
+    if (threadIdx.x == 0) *s_flag = atomicAdd(counter, 1) == n - 1;
+    __syncthreads();
+    return *s_flag != 0;
+}
 static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
 
 // A group record read back from the control block, validated so that no
@@ -80,7 +103,7 @@ __device__ void topk_wave(const float * row, int E, int K, int32_t * ids, float 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? row[e] : -INFINITY;
+        v[j] = e < E ? ld_coh(row + e) : -INFINITY;
     }
     const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     double ls = 0.0;
@@ -154,15 +177,10 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
 #pragma unroll
         for (int t = 0; t < DEC_MAXT; ++t) {
             const float s = wave_sum(acc[t]);
-            if (lane == 0 && t < T) p.logits[(int64_t)t * E + e] = s + b;
+            if (lane == 0 && t < T) st_coh(p.logits + (int64_t)t * E + e, s + b);
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&p.ctl->route_count, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!arrive_last(&p.ctl->route_count, gridDim.x, &s_last)) return;
 
     // ---- last workgroup: selection, groups, activation quantisation
     if (wave < T) topk_wave(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
@@ -326,16 +344,18 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     if (lr == 0 && rw < rows) {
 #pragma unroll
         for (int c = 0; c < DEC_MAXT; ++c)
-            if (c < n_mem) p.ygu[(int64_t)gi.mem[c] * F2 + r0 + rw] = acc[c];
+            if (c < n_mem) st_coh(p.ygu + (int64_t)gi.mem[c] * F2 + r0 + rw, acc[c]);
     }
 
     // ---- group completion: the last workgroup builds the down activations
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&p.ctl->group_count[g], 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (s_last) {
-        __threadfence();
+    if (arrive_last(&p.ctl->group_count[g], gridDim.x, &s_last)) {
+        // the members' gate_up rows -> LDS (the weight staging area is free now)
+        float * gu = reinterpret_cast<float *>(smem);
+        for (int i = threadIdx.x; i < n_mem * F2; i += WG) {
+            const int c = i / F2, r = i - c * F2;
+            gu[i] = ld_coh(p.ygu + (int64_t)member(gi, c) * F2 + r);
+        }
+        __syncthreads();
         ActView v;
         act_layout(p.n_ff, 0, &v);
 #pragma unroll
@@ -343,7 +363,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             if (c >= n_mem) break;
             const int pr = gi.mem[c];
             ActSrc src;
-            src.p = p.ygu + (int64_t)pr * F2;
+            src.p = gu + c * F2;
             src.n = p.n_ff;
             quantize_act<T_Q5_0, AM, GSRC>(p.aq + (int64_t)pr * p.aq_stride, v, src, p.n_ff);
         }
@@ -408,11 +428,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     if (lr == 0 && rw < rows) {
 #pragma unroll
         for (int c = 0; c < DEC_MAXT; ++c)
-            if (c < n_mem) p.ydn[(int64_t)gi.mem[c] * D + r0 + rw] = valid ? acc[c] * sc : 0.0f;
+            if (c < n_mem) st_coh(p.ydn + (int64_t)gi.mem[c] * D + r0 + rw, valid ? acc[c] * sc : 0.0f);
     }
 
     // ---- combine: the last pair of a token to finish these rows sums them
-    __threadfence();
+    wait_vm();
     __syncthreads();
     if ((int)threadIdx.x < n_mem) {
         const int t = member(gi, threadIdx.x) / K;
@@ -423,13 +443,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     for (int c = 0; c < DEC_MAXT; ++c) {
         if (c >= n_mem) break;
         if (!s_lastc[c]) continue;
-        __threadfence();
         const int t = gi.mem[c] / K;
         const float * yt = p.ydn + (int64_t)t * K * D + r0;
         const float * wt = p.w + t * K;
         for (int r = threadIdx.x; r < rows; r += WG) {
-            float o = __fmul_rn(yt[r], wt[0]);
-            for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(yt[(int64_t)k * D + r], wt[k]));
+            float o = __fmul_rn(ld_coh(yt + r), wt[0]);
+            for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(ld_coh(yt + (int64_t)k * D + r), wt[k]));
             p.out[(int64_t)t * D + r0 + r] = o;
         }
     }

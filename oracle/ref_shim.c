@@ -48,7 +48,10 @@ float ref_vec_dot(int type, int64_t n, const void * w, const void * a) {
 }
 
 static struct ggml_context * mk_ctx(size_t extra) {
-    struct ggml_init_params p = { .mem_size = extra + 256u * 1024 * 1024, .mem_buffer = NULL, .no_alloc = false };
+    /* weights + activations + graph metadata + ggml's work buffer (also
+     * allocated in the context by ggml_graph_compute_with_ctx) */
+    struct ggml_init_params p = { .mem_size = extra + extra / 8 + 512u * 1024 * 1024, .mem_buffer = NULL,
+                                  .no_alloc = false };
     return ggml_init(p);
 }
 
