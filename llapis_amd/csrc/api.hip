@@ -630,8 +630,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.out = out;
         const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
         const int rbd = (int)std::max(rbytes(L->hot_dn_type, L->n_ff), rbytes(L->cold_dn_type, L->n_ff));
-        // the staging area also holds the members' gate_up rows for the GEGLU
-        p.w_lds_gu = dev::align16(std::max(16 * rbg + 32, DEC_MAXT * 2 * L->n_ff * 4));
+        p.w_lds_gu = dev::align16(16 * rbg + 32);
         p.w_lds_dn = dev::align16(32 * rbd + 32);
         p.n_rb_down = dw.n_rb;
         p.prefetch = g_prefetch.load();

@@ -1,31 +1,30 @@
 // decode.hip -- the MoE layer for decode batches (1..4 tokens) in three
-// kernels on gfx950.
+// kernels on gfx950:
 //
-//   A  k_dec_route   router logits, one wave per expert over all tokens; the
-//                    last workgroup to finish does softmax + top-k per token,
-//                    resolves each routed expert's tier once (the residency
-//                    predicate of moert/cuda/ffn_moe.cu:80-130), groups the
-//                    routed pairs by expert (decode once, dot N: the tokens
-//                    that share an expert read its slab once) and quantises
-//                    the tokens' activations.
-//   B  k_dec_gate_up per (expert group, 16-row block): streams the gate_up
-//                    rows through LDS with 128-bit loads and dots them
-//                    against every member token; also prefetches a slice of
-//                    the same expert's down slab.  The last workgroup of a
-//                    group evaluates GEGLU and quantises each member pair's
-//                    down activation.
-//   C  k_dec_down    per (expert group, 32-row block): the down projection,
-//                    scaled by the expert's .scale; the last arrival of a
-//                    (token, row block) writes the weighted combine of the
-//                    token's top_k outputs for those rows.
+//   A  k_dec_route   router logits (one wave per expert, all tokens) and the
+//                    tokens' activation quantisation spread over the
+//                    workgroups; the last workgroup to finish selects the
+//                    routing (softmax, top-k with DPP wave reductions, ties to
+//                    the lower index), groups the routed pairs by expert
+//                    (decode once, dot N: the tokens that share an expert read
+//                    its slab once) and resolves each group's tier (the
+//                    residency predicate of moert/cuda/ffn_moe.cu:80-130).
+//   B  k_dec_gate_up per (expert group, 16-row block): one record read, then
+//                    the expert's gate_up rows stream through LDS with 128-bit
+//                    loads, dotted against every member token; a slice of the
+//                    same expert's down slab is prefetched into L2/MALL.
+//   C  k_dec_down    per (expert group, 32-row block): GEGLU and down
+//                    activation quantisation of the group's pairs in the
+//                    prologue (while the weight loads are in flight), the down
+//                    projection with the expert's .scale, and the combine:
+//                    the last arrival of a (token, row block) writes the
+//                    weighted sum of the token's top_k outputs for those rows.
 //
-// Cross-workgroup hand-offs inside a kernel never touch the L2 as a whole:
-// the values another workgroup will read are written with device-scope
-// coherent stores (write-through past the per-XCD L2), each thread waits for
-// its stores to complete, then one thread bumps an arrival counter; the last
-// arriver reads with device-scope coherent loads.  (A device-scope fence
-// would write back and invalidate the XCD's whole L2 in every workgroup.)
-// Kernel A clears the counters of B and C for the call; B clears A's.
+// Hand-offs inside a kernel (A's logits, C's partial outputs) write with
+// device-scope coherent stores, wait for their completion, then count
+// arrivals with an atomic; the last arriver reads with device-scope coherent
+// loads -- no L2 writeback or invalidate.  Kernel A clears C's counters for
+// the call; B clears A's.
 #include "device.h"
 #include "launch.h"
 
@@ -37,6 +36,7 @@ __constant__ uint16_t c_iq2s_codes_dec[1024] = {
 };
 
 template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
+static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
 
 __device__ __forceinline__ void st_coh(float * p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -56,34 +56,23 @@ __device__ __forceinline__ bool arrive_last(int * counter, int n, int * s_flag) 
     __syncthreads();
     return *s_flag != 0;
 }
-static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
 
-// A group record read back from the control block, validated so that no
-// field can send a load or store out of bounds: tier 0/1 only, slot or
-// expert index inside its pool, member count <= DEC_MAXT, members < P.
-__device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
-    GroupInfo gi = p.ctl->groups[g];
-    const int P = p.T * p.top_k;
-    bool ok = (gi.tier == 0 && gi.idx >= 0 && gi.idx < p.k_slots) ||
-              (gi.tier == 1 && gi.idx >= 0 && gi.idx < p.n_expert);
-    gi.n_mem = max(0, min(gi.n_mem, DEC_MAXT));
-#pragma unroll
-    for (int c = 0; c < DEC_MAXT; ++c)
-        if (c < gi.n_mem && (gi.mem[c] < 0 || gi.mem[c] >= P)) ok = false;
-    if (!ok) {
-        gi.tier = 2;
-        gi.idx = 0;
-        gi.n_mem = 0;
-    }
-    return gi;
+// wave64 reductions on DPP lane moves (quad perms, row mirrors, row
+// broadcasts); the result is read from lane 63 and is wave-uniform
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWMASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v, v));          // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_mov<0x4E>(v, v));          // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_mov<0x141>(v, v));         // row_half_mirror
+    v = fmaxf(v, dpp_mov<0x140>(v, v));         // row_mirror
+    v = fmaxf(v, dpp_mov<0x142, 0xA>(v, v));    // row_bcast15
+    v = fmaxf(v, dpp_mov<0x143, 0xC>(v, v));    // row_bcast31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// groups of this call (never more than the launch has rows of workgroups)
-__device__ __forceinline__ int n_groups(const DecParams & p) {
-    return min(p.ctl->n_groups, (int)gridDim.y);
-}
-
-// member i of a group (select chain: keeps the record in registers)
 __device__ __forceinline__ int member(const GroupInfo & g, int i) {
     return i == 0 ? g.mem[0] : i == 1 ? g.mem[1] : i == 2 ? g.mem[2] : g.mem[3];
 }
@@ -95,17 +84,19 @@ __device__ __forceinline__ const uint8_t * group_slab(int tier, int idx, const u
 
 // ---------------------------------------------------------------- A
 
-// softmax (ggml soft_max: exp(x - max), sum in double, scaled by float(1/sum))
-// and top-K (descending, ties to the lower index) of one token, one wave.
-__device__ void topk_wave(const float * row, int E, int K, int32_t * ids, float * w, int * s_ids) {
+// Softmax + top-K of one token in one wave (ggml soft_max: exp(x - max), sum
+// in double, scaled by float(1/sum); argsort_top_k: descending, equal
+// probabilities in index order; weights p[ids] / max(sum, 6.103515625e-5)
+// with the sum accumulated in double in id order).  E <= 256.
+__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids) {
     const int lane = threadIdx.x & 63;
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? ld_coh(row + e) : -INFINITY;
+        v[j] = e < E ? ld_coh(logits + e) : -INFINITY;
     }
-    const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    const float mx = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     double ls = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -115,38 +106,29 @@ __device__ void topk_wave(const float * row, int E, int K, int32_t * ids, float 
     }
     for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
     const float inv = (float)(1.0 / ls);
-    bool taken[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[j] = __fmul_rn(v[j], inv);
-        taken[j] = lane + 64 * j >= E;
-    }
+    for (int j = 0; j < 4; ++j) v[j] = lane + 64 * j < E ? __fmul_rn(v[j], inv) : -1.0f;
+    // probabilities are >= 0; a taken entry drops to -1
     float sel = 0.0f;
+    double sum = 0.0;
     for (int k = 0; k < K; ++k) {
-        uint64_t key = 0;
+        const float m = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        int e = -1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64 * j;
-            const uint64_t kk = taken[j] ? 0 : (((uint64_t)__float_as_uint(v[j]) << 32) | (0xFFFFFFFFu - e)) + 1;
-            key = kk > key ? kk : key;
+            const uint64_t b = __ballot(v[j] == m);
+            if (e < 0 && b) e = 64 * j + __builtin_ctzll(b);
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const uint64_t other = __shfl_xor(key, o, 64);
-            key = other > key ? other : key;
-        }
-        key -= 1;
-        const uint32_t eb = 0xFFFFFFFFu - (uint32_t)key;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) if ((uint32_t)(lane + 64 * j) == eb) taken[j] = true;
-        if (lane == k) sel = __uint_as_float((uint32_t)(key >> 32));
+        for (int j = 0; j < 4; ++j) if (lane + 64 * j == e) v[j] = -1.0f;
+        sum += (double)m;
+        if (lane == k) sel = m;
         if (lane == 0) {
-            ids[k] = (int32_t)eb;
-            s_ids[k] = (int)eb;
+            ids[k] = e;
+            s_ids[k] = e;
         }
     }
-    double s = lane < K ? (double)sel : 0.0;
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-    float sf = (float)s;
+    float sf = (float)sum;
     if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
     if (lane < K) w[lane] = sel / sf;
 }
@@ -156,9 +138,11 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     __shared__ int s_last;
     __shared__ int s_ids[DEC_PMAX];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gw = blockIdx.x * (WG / 64) + wave;          // wave id in the grid
+    const int nw = gridDim.x * (WG / 64);
     const int d = p.d_model, E = p.n_expert, T = p.T, K = p.top_k;
-    const int e = blockIdx.x * (WG / 64) + wave;
-    if (e < E) {
+    if (gw < E) {
+        const int e = gw;
         const float * wrow = p.router_w + (int64_t)e * d;
         float acc[DEC_MAXT];
 #pragma unroll
@@ -180,29 +164,41 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
             if (lane == 0 && t < T) st_coh(p.logits + (int64_t)t * E + e, s + b);
         }
     }
+    // the tokens' gate_up activations: one wave per 256-block (q8_K) or per
+    // 64 values (q8_1)
+    {
+        ActView v;
+        act_layout(d, 0, &v);
+        const int per_tok = AM == AM_CPU ? d / 256 : (d + 63) / 64;
+        for (int j = gw; j < T * per_tok; j += nw) {
+            const int t = j / per_tok, b = j - t * per_tok;
+            ActSrc src;
+            src.p = p.x + (int64_t)t * d;
+            src.n = d;
+            uint8_t * col = p.xq + (int64_t)t * p.xq_stride;
+            if (AM == AM_CPU) q8K_block<SRC_PLAIN>(col, v, src, b);
+            else q8_32_step<SRC_PLAIN, AM_Q8_1>(col, v, src, d, 64 * b);
+        }
+    }
     if (!arrive_last(&p.ctl->route_count, gridDim.x, &s_last)) return;
 
-    // ---- last workgroup: selection, groups, activation quantisation
-    if (wave < T) topk_wave(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
-    // counters of B and C for this call start at zero
-    for (int i = threadIdx.x; i < DEC_PMAX; i += WG) p.ctl->group_count[i] = 0;
+    // ---- last workgroup: selection and groups
+    if (wave < T) select_token(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
     for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
     __syncthreads();
     if (wave == 0) {
         const int P = T * K;
-        const int pr = lane;
-        const bool live = pr < P;
-        const int ex = live ? s_ids[pr] : -1;
-        int leader = pr, slot = 0, nmem = 0;
+        const bool live = lane < P;
+        const int ex = live ? s_ids[lane] : -1;
+        int leader = lane, slot = 0, nmem = 0;
         for (int q = 0; q < P; ++q) {
-            const int eq = s_ids[q];
-            if (eq == ex) {
-                if (q < pr) ++slot;
+            if (s_ids[q] == ex) {
+                if (q < lane) ++slot;
                 if (q < leader) leader = q;
                 ++nmem;
             }
         }
-        const bool is_leader = live && leader == pr;
+        const bool is_leader = live && leader == lane;
         const uint64_t lm = __ballot(is_leader);
         const int gid = __popcll(lm & (leader == 0 ? 0ull : (~0ull >> (64 - leader))));
         if (is_leader) {
@@ -220,31 +216,48 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
             }
             p.ctl->groups[gid].tier = tier;
             p.ctl->groups[gid].idx = idx;
-            p.ctl->groups[gid].n_mem = min(nmem, DEC_MAXT);
+            p.ctl->groups[gid].n_mem = min(nmem, min(T, DEC_MAXT));     // one member per token at most
         }
-        if (live && slot < DEC_MAXT) p.ctl->groups[gid].mem[slot] = pr;   // top-k ids of a token are distinct
+        if (live && slot < DEC_MAXT) p.ctl->groups[gid].mem[slot] = lane;
         if (lane == 0) p.ctl->n_groups = __popcll(lm);
     }
-    ActView v;
-    act_layout(d, 0, &v);
-    for (int t = 0; t < T; ++t) {
-        ActSrc src;
-        src.p = p.x + (int64_t)t * d;
-        src.n = d;
-        quantize_act<T_Q4_K, AM, SRC_PLAIN>(p.xq + (int64_t)t * p.xq_stride, v, src, d);
+}
+
+// A group record written by A, validated so that no field can send a load
+// or store out of bounds: tier 0/1 only, slot or expert index inside its
+// pool, member count <= min(T, DEC_MAXT), members < P.
+__device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
+    GroupInfo gi = p.ctl->groups[g];
+    const int P = p.T * p.top_k;
+    bool ok = (gi.tier == 0 && gi.idx >= 0 && gi.idx < p.k_slots) ||
+              (gi.tier == 1 && gi.idx >= 0 && gi.idx < p.n_expert);
+    gi.n_mem = max(0, min(gi.n_mem, min(p.T, DEC_MAXT)));
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c)
+        if (c < gi.n_mem && (gi.mem[c] < 0 || gi.mem[c] >= P)) ok = false;
+    if (!ok) {
+        gi.tier = 2;
+        gi.idx = 0;
+        gi.n_mem = 0;
     }
+    return gi;
+}
+
+// groups of this call (never more than the launch has rows of workgroups)
+__device__ __forceinline__ int n_groups(const DecParams & p) {
+    return min(p.ctl->n_groups, (int)gridDim.y);
 }
 
 // ---------------------------------------------------------------- B / C
 
 constexpr int MAXPER_DEC = 8;
 
-// Stage `nch` 16-byte chunks starting at g into LDS at offset `at` (issue
-// first, store after the caller's other work): part 1, the loads.
 struct Staged {
     u32x4 r[MAXPER_DEC];
 };
 
+// loads of `nch` 16-byte chunks (issued now, stored to LDS later); lanes
+// past the end re-read the last chunk so the loads carry no condition
 __device__ __forceinline__ void stage_load(Staged & s, const u32x4 * g, int nch) {
     if (nch > 0) {
 #pragma unroll
@@ -262,16 +275,14 @@ __device__ __forceinline__ void stage_store(const Staged & s, const u32x4 * g, i
     for (int i = threadIdx.x + MAXPER_DEC * WG; i < nch; i += WG) *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = g[i];
 }
 
-// copy n bytes (multiple of 16) from global to LDS
 __device__ __forceinline__ void copy16(uint8_t * smem, int at, const uint8_t * src, int n) {
     for (int i = threadIdx.x; i < n / 16; i += WG)
         *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = reinterpret_cast<const u32x4 *>(src)[i];
 }
 
-template <int HT, int CT, int AM, int GSRC>
+template <int HT, int CT, int AM>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_last;
     constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
     static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
     const int g = blockIdx.y;
@@ -302,13 +313,9 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int dch = (int)(dstride >> 4);
         const int per = (dch + gridDim.x - 1) / gridDim.x;
         const int b0 = blockIdx.x * per, b1 = min(dch, b0 + per);
-        for (int i = b0 + threadIdx.x; i < b1; i += WG) {
-            const u32x4 v = D[i];
-            sink ^= v.x;
-        }
+        for (int i = b0 + threadIdx.x; i < b1; i += WG) sink ^= D[i].x;
     }
 
-    // member activations (quantised by A) and the codebook tables
     ActView tmp;
     const int abytes = act_layout(d_in, 0, &tmp);
     const int a0 = p.w_lds_gu;
@@ -318,8 +325,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     const int n_mem = gi.n_mem;
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c)
-        if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(gi.mem[c] / p.top_k) * p.xq_stride, abytes);
-    const int grid_off = align16i(a0 + DEC_MAXT * abytes), sign_off = grid_off + 1024 * 8;
+        if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride, abytes);
+    const int grid_off = align16i(a0 + min(p.T, DEC_MAXT) * abytes), sign_off = grid_off + 1024 * 8;
     if (wtype == T_IQ2_S) build_iq2s_tables(smem, grid_off, sign_off, c_iq2s_codes_dec);
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();
@@ -344,43 +351,21 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     if (lr == 0 && rw < rows) {
 #pragma unroll
         for (int c = 0; c < DEC_MAXT; ++c)
-            if (c < n_mem) st_coh(p.ygu + (int64_t)gi.mem[c] * F2 + r0 + rw, acc[c]);
-    }
-
-    // ---- group completion: the last workgroup builds the down activations
-    if (arrive_last(&p.ctl->group_count[g], gridDim.x, &s_last)) {
-        // the members' gate_up rows -> LDS (the weight staging area is free now)
-        float * gu = reinterpret_cast<float *>(smem);
-        for (int i = threadIdx.x; i < n_mem * F2; i += WG) {
-            const int c = i / F2, r = i - c * F2;
-            gu[i] = ld_coh(p.ygu + (int64_t)member(gi, c) * F2 + r);
-        }
-        __syncthreads();
-        ActView v;
-        act_layout(p.n_ff, 0, &v);
-#pragma unroll
-        for (int c = 0; c < DEC_MAXT; ++c) {
-            if (c >= n_mem) break;
-            const int pr = gi.mem[c];
-            ActSrc src;
-            src.p = gu + c * F2;
-            src.n = p.n_ff;
-            quantize_act<T_Q5_0, AM, GSRC>(p.aq + (int64_t)pr * p.aq_stride, v, src, p.n_ff);
-        }
+            if (c < n_mem) p.ygu[(int64_t)member(gi, c) * F2 + r0 + rw] = acc[c];
     }
     if (p.never) p.ygu[threadIdx.x] = (float)sink;        // keeps the prefetch loads alive
 }
 
-template <int HT, int CT, int AM>
+template <int HT, int CT, int AM, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_down(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_lastc[DEC_MAXT];
     constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
     static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && !k256<HT>() && !k256<CT>(), "down formats");
     const int g = blockIdx.y;
+    const int D = p.d_model, d_in = p.n_ff, K = p.top_k;
     if (g >= n_groups(p)) return;
     const GroupInfo gi = load_group(p, g);
-    const int D = p.d_model, d_in = p.n_ff, K = p.top_k;
     const bool valid = gi.tier < 2;
     const int wtype = gi.tier == 0 ? HT : CT;
     const int r0 = blockIdx.x * ROWS;
@@ -395,6 +380,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     Staged st;
     stage_load(st, gW, nch);
 
+    // GEGLU of the members' gate_up rows, quantised into LDS
     ActView tmp;
     const int abytes = act_layout(d_in, 0, &tmp);
     const int a0 = p.w_lds_dn;
@@ -403,8 +389,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     for (int c = 0; c < DEC_MAXT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
     const int n_mem = gi.n_mem;
 #pragma unroll
-    for (int c = 0; c < DEC_MAXT; ++c)
-        if (c < n_mem) copy16(smem, a0 + c * abytes, p.aq + (int64_t)gi.mem[c] * p.aq_stride, abytes);
+    for (int c = 0; c < DEC_MAXT; ++c) {
+        if (c >= n_mem) break;
+        ActSrc src;
+        src.p = p.ygu + (int64_t)member(gi, c) * 2 * d_in;
+        src.n = d_in;
+        quantize_act<T_Q5_0, AM, GSRC>(smem, av[c], src, d_in);
+    }
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();
 
@@ -428,7 +419,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     if (lr == 0 && rw < rows) {
 #pragma unroll
         for (int c = 0; c < DEC_MAXT; ++c)
-            if (c < n_mem) st_coh(p.ydn + (int64_t)gi.mem[c] * D + r0 + rw, valid ? acc[c] * sc : 0.0f);
+            if (c < n_mem) st_coh(p.ydn + (int64_t)member(gi, c) * D + r0 + rw, valid ? acc[c] * sc : 0.0f);
     }
 
     // ---- combine: the last pair of a token to finish these rows sums them
@@ -443,7 +434,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     for (int c = 0; c < DEC_MAXT; ++c) {
         if (c >= n_mem) break;
         if (!s_lastc[c]) continue;
-        const int t = gi.mem[c] / K;
+        const int t = member(gi, c) / K;
         const float * yt = p.ydn + (int64_t)t * K * D + r0;
         const float * wt = p.w + t * K;
         for (int r = threadIdx.x; r < rows; r += WG) {
@@ -467,17 +458,19 @@ int dec_act_bytes(int n) {
     return act_layout(n, 0, &v);
 }
 
+// dynamic LDS: staged weights, one activation column per token of the call
+// (a group has at most one member per token), IQ2_S tables when used
 int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
     ActView v;
     const int ab = act_layout(p.d_model, 0, &v);
     const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
-    return align16i(p.w_lds_gu + DEC_MAXT * ab) + (iq2 ? 1024 * 8 + 256 * 16 : 0);
+    return align16i(p.w_lds_gu + std::min(p.T, DEC_MAXT) * ab) + (iq2 ? 1024 * 8 + 256 * 16 : 0);
 }
 
 int dec_lds_down(const DecParams & p) {
     ActView v;
     const int ab = act_layout(p.n_ff, 0, &v);
-    return p.w_lds_dn + DEC_MAXT * ab;
+    return p.w_lds_dn + std::min(p.T, DEC_MAXT) * ab;
 }
 
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
@@ -485,7 +478,9 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
     const int P = p.T * p.top_k;
     {
-        dim3 grid((p.n_expert + 3) / 4);
+        const int per_tok = am == AM_CPU ? p.d_model / 256 : (p.d_model + 63) / 64;
+        const int waves = std::max(p.n_expert, p.T * per_tok);
+        dim3 grid((waves + 3) / 4);
         if (am == AM_CPU) hipLaunchKernelGGL(k_dec_route<AM_CPU>, grid, dim3(WG), 0, s, p);
         else hipLaunchKernelGGL(k_dec_route<AM_Q8_1>, grid, dim3(WG), 0, s, p);
         hipError_t e = hipGetLastError();
@@ -496,10 +491,9 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     {
         dim3 grid((2 * p.n_ff + 15) / 16, P);
         const int lds = dec_lds_gate_up(p, hgu, cgu);
-#define LL_GU(A, B, M, G) \
-        if (hgu == A && cgu == B && am == M && gelu == G) hipLaunchKernelGGL((k_dec_gate_up<A, B, M, G>), grid, dim3(WG), lds, s, p); else
-#define LL_GU2(A, B) LL_GU(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_GU(A, B, AM_CPU, SRC_GEGLU_TANH) \
-                     LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TANH)
+#define LL_GU(A, B, M) \
+        if (hgu == A && cgu == B && am == M) hipLaunchKernelGGL((k_dec_gate_up<A, B, M>), grid, dim3(WG), lds, s, p); else
+#define LL_GU2(A, B) LL_GU(A, B, AM_CPU) LL_GU(A, B, AM_Q8_1)
         LL_GU2(T_Q4_K, T_IQ2_S) LL_GU2(T_Q4_K, T_Q4_K) LL_GU2(T_IQ2_S, T_IQ2_S) LL_GU2(T_IQ2_S, T_Q4_K)
         return hipErrorInvalidValue;
 #undef LL_GU2
@@ -511,8 +505,10 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     {
         dim3 grid(p.n_rb_down, P);
         const int lds = dec_lds_down(p);
-#define LL_DN(A, B, M) if (hdn == A && cdn == B && am == M) hipLaunchKernelGGL((k_dec_down<A, B, M>), grid, dim3(WG), lds, s, p); else
-#define LL_DN2(A, B) LL_DN(A, B, AM_CPU) LL_DN(A, B, AM_Q8_1)
+#define LL_DN(A, B, M, G) \
+        if (hdn == A && cdn == B && am == M && gelu == G) hipLaunchKernelGGL((k_dec_down<A, B, M, G>), grid, dim3(WG), lds, s, p); else
+#define LL_DN2(A, B) LL_DN(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_DN(A, B, AM_CPU, SRC_GEGLU_TANH) \
+                     LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TANH)
         LL_DN2(T_Q5_0, T_IQ4_NL) LL_DN2(T_Q5_0, T_Q5_0) LL_DN2(T_IQ4_NL, T_IQ4_NL) LL_DN2(T_IQ4_NL, T_Q5_0)
         return hipErrorInvalidValue;
 #undef LL_DN2

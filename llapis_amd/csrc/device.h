@@ -140,96 +140,99 @@ __device__ __forceinline__ float act_at(const ActSrc & s, int k) {
     return geglu1<SRC>(s.p[k], s.p[s.n + k]);
 }
 
-// q8_K of d_in values (ggml-quants.c:2696-2733): one wave per 256-block.
+// q8_K of one 256-block b of a column (ggml-quants.c:2696-2733), one wave:
 // max is the first element of largest magnitude; iscale = -127/max;
 // q = min(127, nearest_int(iscale x)); d = 1/iscale; bsums over 16.
 template <int SRC>
-__device__ __forceinline__ void quantize_q8_K(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void q8K_block(uint8_t * base, const ActView & L, const ActSrc & src, int b) {
+    const int lane = threadIdx.x & 63;
     int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
     float * dK = reinterpret_cast<float *>(base + L.dK);
     int * bsum = reinterpret_cast<int *>(base + L.bsum);
-    for (int b = wave; b < d_in / 256; b += WG / 64) {
-        float v[4];
-        uint64_t key = 0;
+    float v[4];
+    float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int pos = lane + 64 * j;
-            v[j] = act_at<SRC>(src, b * 256 + pos);
-            const uint64_t k = ((uint64_t)__float_as_uint(fabsf(v[j])) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)pos);
-            key = k > key ? k : key;
-        }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const uint64_t other = __shfl_xor(key, o, 64);
-            key = other > key ? other : key;
-        }
-        const float amax = __uint_as_float((uint32_t)(key >> 32));
-        const int pmax = (int)(0xFFFFFFFFu - (uint32_t)key);
-        const int jm = pmax >> 6;
-        const float mine = jm == 0 ? v[0] : jm == 1 ? v[1] : jm == 2 ? v[2] : v[3];
-        const float max = __shfl(mine, pmax & 63, 64);
-        int qi[4];
-        if (amax == 0.0f) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) qi[j] = 0;
-            if (lane == 0) dK[b] = 0.0f;
-        } else {
-            const float iscale = -127.f / max;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = (int)rintf(__fmul_rn(iscale, v[j]));
-                qi[j] = r < 127 ? r : 127;
-            }
-            if (lane == 0) dK[b] = 1.0f / iscale;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            q[b * 256 + lane + 64 * j] = (int8_t)qi[j];
-            int s = qi[j];
-            for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
-            if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
-        }
+    for (int j = 0; j < 4; ++j) {
+        v[j] = act_at<SRC>(src, b * 256 + lane + 64 * j);
+        amax = fmaxf(amax, fabsf(v[j]));
     }
+    amax = wave_max(amax);
+    // first position holding |x| == amax: positions are lane + 64 j
+    float max = 0.0f;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+        const uint64_t m = __ballot(fabsf(v[j]) == amax);
+        if (m) max = __shfl(v[j], __builtin_ctzll(m), 64);
+    }
+    int qi[4];
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qi[j] = 0;
+        if (lane == 0) dK[b] = 0.0f;
+    } else {
+        const float iscale = -127.f / max;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (int)rintf(__fmul_rn(iscale, v[j]));
+            qi[j] = r < 127 ? r : 127;
+        }
+        if (lane == 0) dK[b] = 1.0f / iscale;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        q[b * 256 + lane + 64 * j] = (int8_t)qi[j];
+        int s = qi[j];
+        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+        if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
+    }
+}
+
+template <int SRC>
+__device__ __forceinline__ void quantize_q8_K(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
+    for (int b = threadIdx.x >> 6; b < d_in / 256; b += WG / 64) q8K_block<SRC>(base, L, src, b);
 }
 
 // q8_0 as the x86 CPU build computes it (arch/x86/quants.c:302-360):
 // d = amax/127 stored as fp16, id = 127/amax, q = round-to-nearest-even(x id).
 // q8_1 as ggml-cuda computes it (quantize.cu:5-50): d = amax/127,
 // q = roundf(x/d), s = butterfly sum of x; both stored as fp16.
-// One wave handles two 32-blocks per step.
+// One wave quantises the two 32-blocks starting at `at`.
 template <int SRC, int AM>
-__device__ __forceinline__ void quantize_q8_32(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void q8_32_step(uint8_t * base, const ActView & L, const ActSrc & src, int d_in, int at) {
+    const int lane = threadIdx.x & 63;
     int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
     float * d32 = reinterpret_cast<float *>(base + L.d32);
     float * s32 = reinterpret_cast<float *>(base + L.s32);
-    for (int base = wave * 64; base < d_in; base += WG) {
-        const int pos = base + lane;
-        const bool live = pos < d_in;          // d_in is a multiple of 32, not always of 64
-        const float v = live ? act_at<SRC>(src, pos) : 0.0f;
-        float amax = fabsf(v);
-        for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-        int qi;
-        float dstore;
-        if (AM == AM_CPU) {
-            const float d = amax / 127.f;
-            const float id = amax != 0.0f ? 127.f / amax : 0.0f;
-            qi = (int)rintf(__fmul_rn(v, id));
-            qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
-            dstore = round_to_half(d);
-        } else {
-            float s = v;
-            for (int o = 16; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 32));
-            const float d = amax / 127.0f;
-            qi = amax == 0.0f ? 0 : (int)roundf(v / d);
-            dstore = round_to_half(d);
-            if (live && (lane & 31) == 0) s32[pos >> 5] = round_to_half(s);
-        }
-        if (live) {
-            q[pos] = (int8_t)qi;
-            if ((lane & 31) == 0) d32[pos >> 5] = dstore;
-        }
+    const int pos = at + lane;
+    const bool live = pos < d_in;          // d_in is a multiple of 32, not always of 64
+    const float v = live ? act_at<SRC>(src, pos) : 0.0f;
+    float amax = fabsf(v);
+    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    int qi;
+    float dstore;
+    if (AM == AM_CPU) {
+        const float d = amax / 127.f;
+        const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+        qi = (int)rintf(__fmul_rn(v, id));
+        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+        dstore = round_to_half(d);
+    } else {
+        float s = v;
+        for (int o = 16; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 32));
+        const float d = amax / 127.0f;
+        qi = amax == 0.0f ? 0 : (int)roundf(v / d);
+        dstore = round_to_half(d);
+        if (live && (lane & 31) == 0) s32[pos >> 5] = round_to_half(s);
     }
+    if (live) {
+        q[pos] = (int8_t)qi;
+        if ((lane & 31) == 0) d32[pos >> 5] = dstore;
+    }
+}
+
+template <int SRC, int AM>
+__device__ __forceinline__ void quantize_q8_32(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
+    for (int at = (threadIdx.x >> 6) * 64; at < d_in; at += WG) q8_32_step<SRC, AM>(base, L, src, d_in, at);
 }
 
 // Quantise an activation column into the format weight type T is dotted with.

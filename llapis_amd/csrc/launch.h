@@ -52,12 +52,12 @@ struct GroupInfo {
     int mem[DEC_MAXT];          // routed-pair indices, one per member token
 };
 
-// control block at the start of the decode workspace (zero before first use)
+// control block at the start of the decode workspace (zero before first use):
+// kernel A's arrival counter and the expert groups it selected
 struct DecCtl {
     int route_count;
     int n_groups;
     int pad[2];
-    int group_count[DEC_PMAX];
     GroupInfo groups[DEC_PMAX];
 };
 
