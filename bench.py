@@ -100,7 +100,8 @@ class Workload:
 
 
 def time_graph(wl, steps, warmup):
-    """Capture R consecutive steps in one HIP graph and time replays of it."""
+    """Capture R consecutive steps (one pass over the replicas) in a HIP graph
+    and K mod R steps in a second one; time exactly K steps of replays."""
     torch = wl.torch
     R = wl.R
     stream = torch.cuda.Stream()
@@ -108,12 +109,18 @@ def time_graph(wl, steps, warmup):
         for i in range(max(warmup, 1)):
             wl.step(i, stream.cuda_stream)
     torch.cuda.synchronize()
+    reps, tail = divmod(steps, R)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for i in range(R):
             wl.step(i, stream.cuda_stream)
+    gt = None
+    if tail:
+        gt = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gt, stream=stream):
+            for i in range(tail):
+                wl.step(i, stream.cuda_stream)
     torch.cuda.synchronize()
-    reps = max(1, steps // R)
     for _ in range(max(1, warmup // R)):
         g.replay()
     torch.cuda.synchronize()
@@ -121,10 +128,12 @@ def time_graph(wl, steps, warmup):
     e0.record(torch.cuda.current_stream())
     for _ in range(reps):
         g.replay()
+    if gt is not None:
+        gt.replay()
     e1.record(torch.cuda.current_stream())
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
-    return ms / (reps * R), reps * R
+    return ms / steps, steps
 
 
 def time_eager(wl, steps, warmup):
@@ -190,6 +199,7 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     st = stage_times(wl, max(2 * R, 64))
     sb = stage_bytes(sp, n_hot, n_cold, T, pairs)
     dom = max(("gate_up", "down"), key=lambda k: st[k])
+    kernel = {"gate_up": "k_dec_gate_up", "down": "k_dec_down"}[dom] if T <= 4 else f"k_mmv ({dom})"
     res = {
         "tok_per_s": T * 1e3 / ms_graph,
         "ms_per_step": ms_graph,
@@ -201,6 +211,7 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
         "replicas": R,
         "stage_ms": st,
         "dominant": dom,
+        "dominant_kernel": kernel,
         "dominant_bytes": sb[dom],
         "dominant_gbs": sb[dom] / (st[dom] * 1e-3) / 1e9,
         "distinct_hot": n_hot,
@@ -254,6 +265,9 @@ def main():
     ap.add_argument("--configs", default="iq2s,q4k,dual", help="comma list of iq2s,q4k,dual")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 20 device-to-device copies of MIB MiB (scales the HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the path's multi-GPU "
@@ -266,7 +280,19 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
-    la.lib()
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 20}))
+        return
+    for kv in filter(None, args.tune.split(",")):
+        k, v = kv.split("=")
+        la.lib().llapis_set_tuning(int(k), int(v))
     cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
     spec = la.LayerSpec()
     t0 = time.time()
@@ -299,7 +325,7 @@ def main():
     head = results.get("iq2s") or next(iter(results.values()))
     roof = {"bound": "hbm", "achieved": head["dominant_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": head["dominant_gbs"] / HBM_PEAK_GBS, "traffic": None,
-            "kernel": f"k_mmv ({head['dominant']})", "algo_bytes_per_launch": head["dominant_bytes"],
+            "kernel": head["dominant_kernel"], "algo_bytes_per_launch": head["dominant_bytes"],
             "avg_launch_ms": head["stage_ms"][head["dominant"]]}
     cpu = None
     if not args.no_cpu_baseline and "iq2s" in cfgs:
@@ -315,7 +341,7 @@ def main():
         "value": head["tok_per_s"],
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": head["steps_timed"],
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,

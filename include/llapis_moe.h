@@ -148,15 +148,19 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
 
 /* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
- * (default 1), key 1 = down-slab prefetch during gate_up (default 1). */
+ * (default 1), key 1 = down-slab prefetch during gate_up (default 0). */
 void llapis_set_tuning(int32_t key, int32_t value);
 
-/* Stage timing of llapis_moe_ffn for measurement: while enabled, every call
- * records a hipEvent before and after each of its kernels on the call's
- * stream.  llapis_profile_read waits for the recorded events, writes the
- * summed milliseconds per stage {router, top-k, gate_up, down, combine} to
- * ms[0..n) and returns the number of timed calls since the last read (-1 on
- * a HIP error); reading resets the sums.  Disabled by default (no events). */
+/* Stage timing of llapis_moe_ffn for measurement (not under stream capture):
+ * while enabled, every call times its stages on the call's stream with HIP
+ * events -- a stage that is one kernel (gate_up and down on both paths; the
+ * decode path's router+top-k kernel, reported as the router stage) takes the
+ * dispatch's own begin/end timestamps, the generic path's router, top-k and
+ * combine kernels are bracketed by event records.  llapis_profile_read waits
+ * for the events, writes the summed milliseconds per stage {router, top-k,
+ * gate_up, down, combine} to ms[0..n) (0 for a stage the path does not have)
+ * and returns the number of timed calls since the last read (-1 on a HIP
+ * error); reading resets the sums.  Disabled by default (no events). */
 void    llapis_profile_enable(int32_t on);
 int32_t llapis_profile_read(float * ms, int32_t n);
 

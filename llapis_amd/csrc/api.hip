@@ -460,21 +460,40 @@ int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float 
 // ------------------------------------------------------------ profiling
 
 namespace {
-constexpr int PROF_STAGES = 5;
+constexpr int PROF_STAGES = 5;      // router, top-k, gate_up, down, combine
 constexpr int PROF_RING = 4096;
+// Per call and stage a begin/end event pair.  Single-kernel stages (the
+// decode path's kernels, the generic path's matvecs) get the dispatch's own
+// begin/end timestamps; multi-kernel or small stages are bracketed by event
+// records.  A stage a path does not have stays unrecorded and reads as 0.
 struct Profiler {
     std::mutex mu;
     bool on = false;
-    hipEvent_t ev[PROF_RING][PROF_STAGES + 1] = {};
+    hipEvent_t ev[PROF_RING][2 * PROF_STAGES] = {};
+    bool used[PROF_RING][PROF_STAGES] = {};
     int n = 0;          // calls recorded since the last read
     bool created = false;
 };
 Profiler g_prof;
 
-// record boundary `b` (0..PROF_STAGES) of call slot `c`
-hipError_t prof_mark(int c, int b, hipStream_t s) {
+// a profiling slot for this call, or -1
+int prof_slot() {
+    if (!g_prof.on) return -1;
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    if (g_prof.n >= PROF_RING) return -1;
+    const int c = g_prof.n++;
+    for (bool & u : g_prof.used[c]) u = false;
+    return c;
+}
+// the event pair of stage st of slot c (nullptrs when not profiling)
+hipEvent_t prof_ev(int c, int st, int end) {
+    if (c < 0) return nullptr;
+    g_prof.used[c][st] = true;
+    return g_prof.ev[c][2 * st + end];
+}
+hipError_t prof_record(int c, int st, int end, hipStream_t s) {
     if (c < 0) return hipSuccess;
-    return hipEventRecord(g_prof.ev[c][b], s);
+    return hipEventRecord(prof_ev(c, st, end), s);
 }
 }  // namespace
 
@@ -494,10 +513,11 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
     for (int i = 0; i < n; ++i) ms[i] = 0.0f;
     const int calls = g_prof.n;
     for (int c = 0; c < calls; ++c) {
-        if (hipEventSynchronize(g_prof.ev[c][PROF_STAGES]) != hipSuccess) return -1;
         for (int st = 0; st < PROF_STAGES && st < n; ++st) {
+            if (!g_prof.used[c][st]) continue;
             float t = 0.0f;
-            if (hipEventElapsedTime(&t, g_prof.ev[c][st], g_prof.ev[c][st + 1]) != hipSuccess) return -1;
+            if (hipEventSynchronize(g_prof.ev[c][2 * st + 1]) != hipSuccess) return -1;
+            if (hipEventElapsedTime(&t, g_prof.ev[c][2 * st], g_prof.ev[c][2 * st + 1]) != hipSuccess) return -1;
             ms[st] += t;
         }
     }
@@ -508,7 +528,7 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefetch{1};
+std::atomic<int> g_decode_path{1}, g_prefetch{0};
 
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
@@ -636,15 +656,12 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.prefetch = g_prefetch.load();
         p.never = 0;
         if (dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) <= 65536 && dec_lds_down(p) <= 65536) {
-            int pc = -1;
-            if (g_prof.on) {
-                std::lock_guard<std::mutex> lk(g_prof.mu);
-                if (g_prof.n < PROF_RING) pc = g_prof.n++;
-            }
+            const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
-            LL_TRY(prof_mark(pc, 0, s));
+            hipEvent_t ev[6] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0),
+                                prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
-                                 src, s, pc >= 0 ? &g_prof.ev[pc][0] : nullptr));
+                                 src, s, pc >= 0 ? ev : nullptr));
             return 0;
         }
     }
@@ -657,16 +674,13 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     float * ydn = (float *)(base + ws.ydn);
     const int P = T * L->top_k;
 
-    int pc = -1;                       // profiling slot of this call
-    if (g_prof.on) {
-        std::lock_guard<std::mutex> lk(g_prof.mu);
-        if (g_prof.n < PROF_RING) pc = g_prof.n++;
-    }
-    LL_TRY(prof_mark(pc, 0, s));
+    const int pc = prof_slot();        // profiling slot of this call
+    LL_TRY(prof_record(pc, 0, 0, s));
     LL_TRY(launch_router_logits(x, T, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
-    LL_TRY(prof_mark(pc, 1, s));
+    LL_TRY(prof_record(pc, 0, 1, s));
+    LL_TRY(prof_record(pc, 1, 0, s));
     LL_TRY(launch_topk(probs, T, L->n_expert, L->top_k, ids, w, s));
-    LL_TRY(prof_mark(pc, 2, s));
+    LL_TRY(prof_record(pc, 1, 1, s));
 
     MmvParams p = {};
     p.mode = MMV_ROUTED;
@@ -692,8 +706,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     p.act_by_token = 1;
     p.y = ygu;
     mmv_prepare(p, L->hot_gu_type, L->cold_gu_type);
-    LL_TRY(launch_mmv(p, L->hot_gu_type, L->cold_gu_type, L->act_mode, dev::SRC_PLAIN, P, s));
-    LL_TRY(prof_mark(pc, 3, s));
+    LL_TRY(launch_mmv(p, L->hot_gu_type, L->cold_gu_type, L->act_mode, dev::SRC_PLAIN, P, s, prof_ev(pc, 2, 0),
+                      prof_ev(pc, 2, 1)));
     // down: activation column = pair, GEGLU of its gate_up output on the fly
     p.d_in = L->n_ff;
     p.d_out = L->d_model;
@@ -709,10 +723,11 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     p.y = ydn;
     mmv_prepare(p, L->hot_dn_type, L->cold_dn_type);
     const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
-    LL_TRY(launch_mmv(p, L->hot_dn_type, L->cold_dn_type, L->act_mode, src, P, s));
-    LL_TRY(prof_mark(pc, 4, s));
+    LL_TRY(launch_mmv(p, L->hot_dn_type, L->cold_dn_type, L->act_mode, src, P, s, prof_ev(pc, 3, 0),
+                      prof_ev(pc, 3, 1)));
+    LL_TRY(prof_record(pc, 4, 0, s));
     LL_TRY(launch_combine(ydn, w, T, L->top_k, L->d_model, out, s));
-    LL_TRY(prof_mark(pc, 5, s));
+    LL_TRY(prof_record(pc, 4, 1, s));
     return 0;
 }
 

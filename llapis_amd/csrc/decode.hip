@@ -25,6 +25,8 @@
 // arrivals with an atomic; the last arriver reads with device-scope coherent
 // loads -- no L2 writeback or invalidate.  Kernel A clears C's counters for
 // the call; B clears A's.
+#include <hip/hip_ext.h>
+
 #include "device.h"
 #include "launch.h"
 
@@ -137,31 +139,50 @@ template <int AM>
 __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     __shared__ int s_last;
     __shared__ int s_ids[DEC_PMAX];
+    __shared__ float s_part[DEC_MAXT][WG / 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gw = blockIdx.x * (WG / 64) + wave;          // wave id in the grid
     const int nw = gridDim.x * (WG / 64);
     const int d = p.d_model, E = p.n_expert, T = p.T, K = p.top_k;
-    if (gw < E) {
-        const int e = gw;
-        const float * wrow = p.router_w + (int64_t)e * d;
+    // router: workgroup e computes expert e's logit for every token; each lane
+    // issues all of its row loads (RU float4 per pass) before any arithmetic
+    if ((int)blockIdx.x < E) {
+        constexpr int RU = 4;
+        const int e = blockIdx.x, n4 = d / 4;
+        const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
+        const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
         float acc[DEC_MAXT];
 #pragma unroll
         for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
-        for (int k = 4 * lane; k < d; k += 256) {
-            const float4 w4 = *reinterpret_cast<const float4 *>(wrow + k);
+        for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
+            // clamped indices (row end, last token): every load is unconditional
+            float4 w4[RU], xv[DEC_MAXT][RU];
 #pragma unroll
-            for (int t = 0; t < DEC_MAXT; ++t) {
-                if (t < T) {
-                    const float4 x4 = *reinterpret_cast<const float4 *>(p.x + (int64_t)t * d + k);
-                    acc[t] += w4.x * x4.x + w4.y * x4.y + w4.z * x4.z + w4.w * x4.w;
-                }
-            }
+            for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+            for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+                for (int u = 0; u < RU; ++u) xv[t][u] = x4[(int64_t)min(t, T - 1) * n4 + min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+            for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+                for (int u = 0; u < RU; ++u)
+                    if (t < T && k0 + u * WG < n4)
+                        acc[t] += w4[u].x * xv[t][u].x + w4[u].y * xv[t][u].y + w4[u].z * xv[t][u].z +
+                                  w4[u].w * xv[t][u].w;
         }
-        const float b = p.router_b ? p.router_b[e] : 0.0f;
 #pragma unroll
         for (int t = 0; t < DEC_MAXT; ++t) {
             const float s = wave_sum(acc[t]);
-            if (lane == 0 && t < T) st_coh(p.logits + (int64_t)t * E + e, s + b);
+            if (lane == 0) s_part[t][wave] = s;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < T) {
+            const int t = threadIdx.x;
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
+            st_coh(p.logits + (int64_t)t * E + e, s + (p.router_b ? p.router_b[e] : 0.0f));
         }
     }
     // the tokens' gate_up activations: one wave per 256-block (q8_K) or per
@@ -223,29 +244,29 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     }
 }
 
-// A group record written by A, validated so that no field can send a load
-// or store out of bounds: tier 0/1 only, slot or expert index inside its
-// pool, member count <= min(T, DEC_MAXT), members < P.
+// The group record g written by A, or an empty group when g is past the
+// call's groups.  Validated so that no field can send a load or store out of
+// bounds: member count <= min(T, DEC_MAXT) and members < P, else the group is
+// emptied; a tier other than 0/1 or an index outside its pool makes the group
+// invalid (tier 2: its members contribute zeros, their combine still counts).
+// The record and the count are read together (one round trip).
 __device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
     GroupInfo gi = p.ctl->groups[g];
+    const int ng = p.ctl->n_groups;
     const int P = p.T * p.top_k;
-    bool ok = (gi.tier == 0 && gi.idx >= 0 && gi.idx < p.k_slots) ||
-              (gi.tier == 1 && gi.idx >= 0 && gi.idx < p.n_expert);
+    bool ok = g < ng;
     gi.n_mem = max(0, min(gi.n_mem, min(p.T, DEC_MAXT)));
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c)
         if (c < gi.n_mem && (gi.mem[c] < 0 || gi.mem[c] >= P)) ok = false;
-    if (!ok) {
+    if (!ok) gi.n_mem = 0;
+    const bool idx_ok = (gi.tier == 0 && gi.idx >= 0 && gi.idx < p.k_slots) ||
+                        (gi.tier == 1 && gi.idx >= 0 && gi.idx < p.n_expert);
+    if (!idx_ok) {
         gi.tier = 2;
         gi.idx = 0;
-        gi.n_mem = 0;
     }
     return gi;
-}
-
-// groups of this call (never more than the launch has rows of workgroups)
-__device__ __forceinline__ int n_groups(const DecParams & p) {
-    return min(p.ctl->n_groups, (int)gridDim.y);
 }
 
 // ---------------------------------------------------------------- B / C
@@ -287,8 +308,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
     const int g = blockIdx.y;
     if (blockIdx.x == 0 && g == 0 && threadIdx.x == 0) p.ctl->route_count = 0;   // A is complete
-    if (g >= n_groups(p)) return;
     const GroupInfo gi = load_group(p, g);
+    if (gi.n_mem == 0) return;
     const int F2 = 2 * p.n_ff, d_in = p.d_model;
     const bool valid = gi.tier < 2;
     const int wtype = gi.tier == 0 ? HT : CT;
@@ -364,8 +385,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && !k256<HT>() && !k256<CT>(), "down formats");
     const int g = blockIdx.y;
     const int D = p.d_model, d_in = p.n_ff, K = p.top_k;
-    if (g >= n_groups(p)) return;
     const GroupInfo gi = load_group(p, g);
+    if (gi.n_mem == 0) return;
     const bool valid = gi.tier < 2;
     const int wtype = gi.tier == 0 ? HT : CT;
     const int r0 = blockIdx.x * ROWS;
@@ -473,40 +494,48 @@ int dec_lds_down(const DecParams & p) {
     return p.w_lds_dn + std::min(p.T, DEC_MAXT) * ab;
 }
 
+namespace {
+// launch with the dispatch's own begin/end timestamps recorded into e0/e1
+// when profiling (e0 != nullptr)
+template <typename F>
+void launch_timed(F k, dim3 grid, int lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const DecParams & p) {
+    if (e0) hipExtLaunchKernelGGL(k, grid, dim3(WG), (uint32_t)lds, s, e0, e1, 0u, p);
+    else hipLaunchKernelGGL(k, grid, dim3(WG), lds, s, p);
+}
+}  // namespace
+
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
                          hipEvent_t * ev) {
-    auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], s) : hipSuccess; };
+    hipEvent_t e[6] = {};
+    if (ev)
+        for (int i = 0; i < 6; ++i) e[i] = ev[i];
     const int P = p.T * p.top_k;
     {
         const int per_tok = am == AM_CPU ? p.d_model / 256 : (p.d_model + 63) / 64;
-        const int waves = std::max(p.n_expert, p.T * per_tok);
-        dim3 grid((waves + 3) / 4);
-        if (am == AM_CPU) hipLaunchKernelGGL(k_dec_route<AM_CPU>, grid, dim3(WG), 0, s, p);
-        else hipLaunchKernelGGL(k_dec_route<AM_Q8_1>, grid, dim3(WG), 0, s, p);
-        hipError_t e = hipGetLastError();
-        if (e == hipSuccess) e = mark(1);
-        if (e == hipSuccess) e = mark(2);
-        if (e != hipSuccess) return e;
+        dim3 grid(std::max(p.n_expert, (p.T * per_tok + 3) / 4));
+        if (am == AM_CPU) launch_timed(k_dec_route<AM_CPU>, grid, 0, s, e[0], e[1], p);
+        else launch_timed(k_dec_route<AM_Q8_1>, grid, 0, s, e[0], e[1], p);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
     }
     {
         dim3 grid((2 * p.n_ff + 15) / 16, P);
         const int lds = dec_lds_gate_up(p, hgu, cgu);
 #define LL_GU(A, B, M) \
-        if (hgu == A && cgu == B && am == M) hipLaunchKernelGGL((k_dec_gate_up<A, B, M>), grid, dim3(WG), lds, s, p); else
+        if (hgu == A && cgu == B && am == M) launch_timed(k_dec_gate_up<A, B, M>, grid, lds, s, e[2], e[3], p); else
 #define LL_GU2(A, B) LL_GU(A, B, AM_CPU) LL_GU(A, B, AM_Q8_1)
         LL_GU2(T_Q4_K, T_IQ2_S) LL_GU2(T_Q4_K, T_Q4_K) LL_GU2(T_IQ2_S, T_IQ2_S) LL_GU2(T_IQ2_S, T_Q4_K)
         return hipErrorInvalidValue;
 #undef LL_GU2
 #undef LL_GU
-        hipError_t e = hipGetLastError();
-        if (e == hipSuccess) e = mark(3);
-        if (e != hipSuccess) return e;
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
     }
     {
         dim3 grid(p.n_rb_down, P);
         const int lds = dec_lds_down(p);
 #define LL_DN(A, B, M, G) \
-        if (hdn == A && cdn == B && am == M && gelu == G) hipLaunchKernelGGL((k_dec_down<A, B, M, G>), grid, dim3(WG), lds, s, p); else
+        if (hdn == A && cdn == B && am == M && gelu == G) launch_timed(k_dec_down<A, B, M, G>, grid, lds, s, e[4], e[5], p); else
 #define LL_DN2(A, B) LL_DN(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_DN(A, B, AM_CPU, SRC_GEGLU_TANH) \
                      LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TANH)
         LL_DN2(T_Q5_0, T_IQ4_NL) LL_DN2(T_Q5_0, T_Q5_0) LL_DN2(T_IQ4_NL, T_IQ4_NL) LL_DN2(T_IQ4_NL, T_Q5_0)
@@ -514,10 +543,7 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
 #undef LL_DN2
 #undef LL_DN
     }
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = mark(4);
-    if (e == hipSuccess) e = mark(5);
-    return e;
+    return hipGetLastError();
 }
 
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s) {

@@ -36,7 +36,9 @@ int mmv_lds_bytes(const MmvParams & p, int ht, int ct);
 // fill w_lds_bytes for the format pair
 void mmv_prepare(MmvParams & p, int ht, int ct);
 // launch over n_channels channels; returns hipSuccess or the launch error
-hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int act_mode, int src, int n_channels, hipStream_t s);
+// e0/e1 (optional, profiling): receive the dispatch's begin and end timestamps
+hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int act_mode, int src, int n_channels, hipStream_t s,
+                      hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 // ------------------------------------------------------------ decode path
 
@@ -91,8 +93,8 @@ struct DecParams {
 int dec_act_bytes(int n);
 int dec_lds_gate_up(const DecParams & p, int ht, int ct);
 int dec_lds_down(const DecParams & p);
-// ev (optional): 6 events; ev[0] is recorded by the caller before the call,
-// ev[1..2] after kernel A, ev[3] after B, ev[4..5] after C
+// ev (optional, profiling): 6 events that receive the begin and end
+// timestamps of kernels A, B and C (ev[0..1], ev[2..3], ev[4..5])
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
                          hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);

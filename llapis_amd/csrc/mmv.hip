@@ -14,6 +14,8 @@
 //   4. store the weight bytes to LDS, then lanes in groups of LPR dot whole
 //      units (quarter super-blocks or 32-blocks) with v_dot4_i32_i8 and
 //      reduce with cross-lane shuffles.
+#include <hip/hip_ext.h>
+
 #include "device.h"
 #include "launch.h"
 
@@ -151,38 +153,42 @@ int mmv_lds_bytes(const MmvParams & p, int ht, int ct) {
     return lds_layout(p.w_lds_bytes, p.d_in, ht == T_IQ2_S || ct == T_IQ2_S).total;
 }
 
+using Ev = hipEvent_t;
+
 template <int HT, int CT, int AM, int SRC>
-static hipError_t go(const MmvParams & p, int n_channels, hipStream_t s) {
+static hipError_t go(const MmvParams & p, int n_channels, hipStream_t s, Ev e0, Ev e1) {
     const int rows = WG / Fmt<HT>::LPR;
     dim3 grid((p.d_out + rows - 1) / rows, n_channels);
     const int lds = mmv_lds_bytes(p, HT, CT);
-    hipLaunchKernelGGL((k_mmv<HT, CT, AM, SRC>), grid, dim3(WG), lds, s, p);
+    if (e0) hipExtLaunchKernelGGL((k_mmv<HT, CT, AM, SRC>), grid, dim3(WG), (uint32_t)lds, s, e0, e1, 0u, p);
+    else hipLaunchKernelGGL((k_mmv<HT, CT, AM, SRC>), grid, dim3(WG), lds, s, p);
     return hipGetLastError();
 }
 
 template <int HT, int CT, int SRC>
-static hipError_t go_am(const MmvParams & p, int am, int n, hipStream_t s) {
-    return am == AM_CPU ? go<HT, CT, AM_CPU, SRC>(p, n, s) : go<HT, CT, AM_Q8_1, SRC>(p, n, s);
+static hipError_t go_am(const MmvParams & p, int am, int n, hipStream_t s, Ev e0, Ev e1) {
+    return am == AM_CPU ? go<HT, CT, AM_CPU, SRC>(p, n, s, e0, e1) : go<HT, CT, AM_Q8_1, SRC>(p, n, s, e0, e1);
 }
 
 template <int HT, int CT>
-static hipError_t go_src(const MmvParams & p, int am, int src, int n, hipStream_t s) {
+static hipError_t go_src(const MmvParams & p, int am, int src, int n, hipStream_t s, Ev e0, Ev e1) {
     if constexpr (is_k256<HT>()) {
         if (src != SRC_PLAIN) return hipErrorInvalidValue;      // GEGLU feeds the 32-block down formats only
-        return go_am<HT, CT, SRC_PLAIN>(p, am, n, s);
+        return go_am<HT, CT, SRC_PLAIN>(p, am, n, s, e0, e1);
     } else {
         switch (src) {
-            case SRC_PLAIN: return go_am<HT, CT, SRC_PLAIN>(p, am, n, s);
-            case SRC_GEGLU_TABLE: return go_am<HT, CT, SRC_GEGLU_TABLE>(p, am, n, s);
-            case SRC_GEGLU_TANH: return go_am<HT, CT, SRC_GEGLU_TANH>(p, am, n, s);
+            case SRC_PLAIN: return go_am<HT, CT, SRC_PLAIN>(p, am, n, s, e0, e1);
+            case SRC_GEGLU_TABLE: return go_am<HT, CT, SRC_GEGLU_TABLE>(p, am, n, s, e0, e1);
+            case SRC_GEGLU_TANH: return go_am<HT, CT, SRC_GEGLU_TANH>(p, am, n, s, e0, e1);
         }
         return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int am, int src, int n_channels, hipStream_t s) {
+hipError_t launch_mmv(const MmvParams & p, int ht, int ct, int am, int src, int n_channels, hipStream_t s, Ev e0,
+                      Ev e1) {
     if (n_channels <= 0 || p.d_out <= 0) return hipSuccess;
-#define LL_PAIR(A, B) if (ht == A && ct == B) return go_src<A, B>(p, am, src, n_channels, s);
+#define LL_PAIR(A, B) if (ht == A && ct == B) return go_src<A, B>(p, am, src, n_channels, s, e0, e1);
     LL_PAIR(T_Q4_K, T_IQ2_S) LL_PAIR(T_Q4_K, T_Q4_K) LL_PAIR(T_IQ2_S, T_IQ2_S) LL_PAIR(T_IQ2_S, T_Q4_K)
     LL_PAIR(T_Q5_0, T_IQ4_NL) LL_PAIR(T_Q5_0, T_Q5_0) LL_PAIR(T_IQ4_NL, T_IQ4_NL) LL_PAIR(T_IQ4_NL, T_Q5_0)
 #undef LL_PAIR
