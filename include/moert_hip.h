@@ -43,6 +43,47 @@ typedef struct moert_cuda_config {
     uint64_t coldffn_wait_fn;
 } moert_cuda_config;
 
+/* Host callback types the config carries (cuda.h:70-119).  They are part of
+ * the interface the embedding host compiles against; this backend stores the
+ * config but never calls them (the cold tier is in HBM, so no fire takes the
+ * RAM-cold sidecar path). */
+typedef void (*moert_cold_guard_fn)(int32_t il, const int32_t * ids, int32_t n);
+
+/* cuda.h:80-94: one (layer, kind) cold matmul for the host sidecar */
+typedef struct moert_coldcpu_call {
+    int32_t         il, kind;
+    int32_t         n_cold;
+    const int32_t * cold_ids;      /* host, compaction order */
+    const float   * x;             /* host activations */
+    int32_t         x_per_pair;    /* 0: one shared column [d_in]; 1: [d_in, n_cold] */
+    const void    * w_host;        /* cold pool host base */
+    uint64_t        expert_bytes;
+    uint64_t        stride;        /* base + e * stride; 0 means expert_bytes */
+    int32_t         w_type_tag;
+    int32_t         d_in, d_out;
+    float         * y;             /* out [d_out, n_cold], host */
+    const int32_t * x_col;         /* optional per-pair column of x, or NULL */
+} moert_coldcpu_call;
+typedef void (*moert_coldcpu_fn)(const moert_coldcpu_call * call);
+
+/* cuda.h:102-115: one layer's whole cold FFN for the host */
+typedef struct moert_coldffn_job {
+    int32_t         il;
+    int32_t         n_used, n_tokens;
+    const int32_t * h_counts;      /* [0] n_hot, [1] n_cold */
+    const int32_t * h_ids;         /* cold expert ids, compaction order */
+    const int32_t * h_cdst;        /* cold pair index, same order */
+    const float   * x;             /* token columns [d_in, n_tokens] */
+    const void    * w_gu;          /* gate_up cold pool host base */
+    uint64_t        gu_bytes, gu_stride;
+    int32_t         gu_type, d_in, d_gu;
+    float         * y;             /* out */
+    void          (*wait_ready)(void * ev);
+    void          * ev;
+} moert_coldffn_job;
+typedef void    (*moert_coldffn_submit_fn)(const moert_coldffn_job * job);
+typedef int32_t (*moert_coldffn_wait_fn)(int32_t il, int64_t * cpu_ns);
+
 /* Replaces the header-inline moert_cuda_config_defaults (cuda.h:121-131). */
 static inline void moert_cuda_config_defaults(moert_cuda_config * cfg) {
     cfg->counted = 1;

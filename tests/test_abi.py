@@ -1,0 +1,134 @@
+"""The C ABI, CPU only: libllapis_moe.so loads, exports every function the
+public headers declare, and the plain-C structs have the byte layout of the
+reference's moert/include/moert/cuda.h (compiled and compared here when the
+reference tree is present) and of the ctypes mirror in llapis_amd/_lib.py."""
+import ctypes as C
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import llapis_amd as la
+from llapis_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+INCLUDE = ROOT / "include"
+REF_HEADER = Path("/root/reference/moert/include/moert/cuda.h")
+
+DECL = re.compile(r"^\s*(?!typedef|static|#|/\*|\*)[A-Za-z_][\w\s\*]*?\b((?:moert|llapis)_\w+)\s*\(", re.M)
+
+
+def declared_functions():
+    names = set()
+    for h in INCLUDE.glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
+        names.update(DECL.findall(text))
+    return names
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 30, sorted(names)
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes binding covers the same set
+    assert names == set(_lib.SIGNATURES), sorted(names ^ set(_lib.SIGNATURES))
+
+
+MIRRORS = {
+    "moert_cuda_config": _lib.MoertCudaConfig,
+    "moert_mm_call": _lib.MoertMmCall,
+    "moert_ffn_moe_host": _lib.MoertFfnMoeHost,
+    "moert_ffn_moe_args": _lib.MoertFfnMoeArgs,
+    "moert_cuda_stats": _lib.MoertCudaStats,
+    "moert_cuda_dir_stats": _lib.MoertCudaDirStats,
+    "llapis_tensor": _lib.LlapisTensor,
+    "llapis_moe_dual_op": _lib.LlapisMoeDualOp,
+    "llapis_moe_layer": _lib.LlapisMoeLayer,
+}
+# structs of the reference header with no ctypes mirror (host callback payloads)
+CALLBACK_STRUCTS = {
+    "moert_coldcpu_call": ["il", "kind", "n_cold", "cold_ids", "x", "x_per_pair", "w_host", "expert_bytes",
+                           "stride", "w_type_tag", "d_in", "d_out", "y", "x_col"],
+    "moert_coldffn_job": ["il", "n_used", "n_tokens", "h_counts", "h_ids", "h_cdst", "x", "w_gu", "gu_bytes",
+                          "gu_stride", "gu_type", "d_in", "d_gu", "y", "wait_ready", "ev"],
+}
+
+
+def layout_program(header, structs):
+    lines = ["#include <cstddef>", "#include <cstdio>", f'#include "{header}"', "int main() {"]
+    for s, fields in structs.items():
+        lines.append(f'  std::printf("{s} sizeof %zu\\n", sizeof({s}));')
+        for f in fields:
+            lines.append(f'  std::printf("{s} {f} %zu\\n", offsetof({s}, {f}));')
+    lines += ["  return 0;", "}"]
+    return "\n".join(lines)
+
+
+def compile_layouts(tmp_path, header, structs):
+    if not shutil.which("g++"):
+        pytest.skip("no host C++ compiler")
+    src = tmp_path / "layout.cpp"
+    src.write_text(layout_program(header, structs))
+    exe = tmp_path / "layout"
+    subprocess.run(["g++", "-std=c++17", "-I", str(INCLUDE), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True).stdout
+    return {tuple(l.split()[:2]): int(l.split()[2]) for l in out.splitlines()}
+
+
+def moert_structs():
+    out = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items() if k.startswith("moert_")}
+    out.update(CALLBACK_STRUCTS)
+    return out
+
+
+def test_ctypes_mirror_matches_headers(tmp_path):
+    structs = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items()}
+    prog_header = tmp_path / "both.h"
+    prog_header.write_text('#include "moert_hip.h"\n#include "llapis_moe.h"\n')
+    got = compile_layouts(tmp_path, str(prog_header), structs)
+    for s, cls in MIRRORS.items():
+        assert got[(s, "sizeof")] == C.sizeof(cls), s
+        for f in structs[s]:
+            assert got[(s, f)] == getattr(cls, f).offset, (s, f)
+
+
+@pytest.mark.skipif(not REF_HEADER.exists(), reason="reference tree not present")
+def test_moert_structs_match_reference_header(tmp_path):
+    ours = compile_layouts(tmp_path, str(INCLUDE / "moert_hip.h"), moert_structs())
+    (tmp_path / "r").mkdir()
+    theirs = compile_layouts(tmp_path / "r", str(REF_HEADER), moert_structs())
+    assert ours == theirs
+    assert ours[("moert_ffn_moe_args", "sizeof")] > 0
+
+
+def test_config_defaults_match():
+    """moert_cuda_config_defaults is header-inline in both; compare the values
+    ours sets with the reference's documented defaults."""
+    cfg = _lib.MoertCudaConfig()
+    la.lib().moert_cuda_configure(C.byref(cfg))      # accepted without a device
+    text = (INCLUDE / "moert_hip.h").read_text()
+    body = text[text.index("moert_cuda_config_defaults"):]
+    body = body[:body.index("}")]
+    vals = dict(re.findall(r"cfg->(\w+)\s*=\s*(\d+)", body))
+    assert vals == {"counted": "1", "copy_stream": "0", "coldcpu": "0", "coldcpu_max": "3", "coldcpu_fn": "0",
+                    "cold_guard_fn": "0", "cold_ffn": "0", "coldffn_submit_fn": "0", "coldffn_wait_fn": "0"}
+
+
+def test_refusing_services_without_a_device():
+    lib = la.lib()
+    assert lib.moert_cuda_host_register_pinned(None, 0) == 0
+    assert lib.moert_cuda_host_register_mapped(None, 0) == 0
+    assert lib.moert_cuda_host_map(None, 0) is None
+    assert lib.moert_cuda_dir_init(0, 0, 0) == 0
+    assert lib.moert_cuda_dir_mark() == -1
+    assert lib.moert_cuda_dir_poll(0) == -1
+    assert lib.moert_cuda_dir_gate(0, 0) == -1
+    st = _lib.MoertCudaDirStats()
+    lib.moert_cuda_dir_stats_get(C.byref(st))
+    assert st.async_copies == 0 and st.pub_calls == 0

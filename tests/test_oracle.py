@@ -1,0 +1,430 @@
+"""The oracle (oracle/oracle.c, the CPU restatement used as the checker) pinned
+before it is trusted.  CPU only.
+
+How each oracle function is pinned:
+
+  orc_dequantize (q4_K, iq2_s, q5_0, iq4_nl)
+      bit-exact against the reference ggml's dequantize_row_* on the golden
+      rows (quant.npz), and on blocks that enumerate all 1024 IQ2_S grid
+      indices with and without signs (iq2s_grid.npz); closed-form special
+      cases: a Q4_K block with unit scales and zero mins dequantises to its
+      nibbles in ggml's order; per-sub-block scales multiply the right 32.
+  orc_quantize_act (q8_K, q8_0)
+      byte-exact against the reference x86 build (act.npz), including
+      equal-magnitude maxima of opposite sign; invariants of q8_K: the first
+      largest-magnitude value maps to -127, d = -max/127, bsums are the
+      16-wide sums.
+  orc_quantize_act (q8_1)
+      parity unpinned against the reference (its quantiser is CUDA code that
+      cannot be compiled here); pinned by its definition's invariants: the
+      largest magnitude maps to +-127, d = amax/127, s = sum of x.
+  orc_vec_dot CPU mode
+      against the reference's vec_dot on the golden rows (dot.npz), and
+      against the float64 dot of the dequantised operands.
+  orc_vec_dot q8_1 mode
+      q4_K, q5_0, iq4_nl: equal to the float64 dot of the dequantised operands
+      (their q8_1 formulas are exact integer sums times scales); iq2_s: within
+      the truncation bound of its integer formula (at most one unit of
+      d*d8 per 32 values).  Parity with the reference's CUDA code itself is
+      unpinned (no CUDA compiler here).
+  orc_geglu
+      table mode bit-exact against the reference's geglu_split (geglu.npz),
+      including the +-10 clamps; tanh mode against the closed form in float64.
+  orc_router
+      the golden layers' ids and weights (layer.npz); closed forms: equal
+      logits give ids 0..k-1 and weights 1/k, Σw = 1, probabilities sum to 1,
+      ids ordered by descending probability.
+  orc_matvec, orc_moe_experts
+      the reference's mul_mat_id (mmid.npz) and whole single-tier layers
+      (layer.npz); the dual-precision mask by brute force: each routed pair
+      takes the hot pool exactly when the READY predicate holds, the down
+      .scale is applied once, and the combine is the weighted sum.
+  Live reference (oracle/_ref, where it is built): randomised cases of all
+      of the above.
+"""
+import math
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from oracle import (ACT_CPU, ACT_Q8_1, GELU_TABLE, GELU_TANH, IQ2_S, IQ4_NL, Q4_K, Q5_0, Q8_0, Q8_1, Q8_K,
+                    row_size)
+
+GOLD = Path(__file__).resolve().parent / "golden"
+WTYPES = {"q4_K": Q4_K, "iq2_s": IQ2_S, "q5_0": Q5_0, "iq4_nl": IQ4_NL}
+
+
+def load(name):
+    return np.load(GOLD / name, allow_pickle=False)
+
+
+def rows_of(q, t, n):
+    rs = row_size(t, n)
+    return [q[i * rs:(i + 1) * rs] for i in range(q.size // rs)]
+
+
+# ------------------------------------------------------------ dequantisation
+
+def test_dequant_matches_reference_goldens(oracle):
+    g = load("quant.npz")
+    keys = sorted(k[:-2] for k in g.files if k.endswith("_q"))
+    assert len(keys) >= 8
+    for key in keys:
+        t = WTYPES[key.rsplit("_", 1)[0]]
+        x, q, deq = g[key + "_x"], g[key + "_q"], g[key + "_deq"]
+        n = x.shape[1]
+        for r, blk in enumerate(rows_of(q, t, n)):
+            got = oracle.dequantize(t, blk, n)
+            assert np.array_equal(got.view(np.uint32), deq[r].view(np.uint32)), (key, r)
+
+
+def test_iq2s_every_grid_index(oracle):
+    g = load("iq2s_grid.npz")
+    plain = oracle.dequantize(IQ2_S, g["plain_q"], 32 * 256)
+    assert np.array_equal(plain, g["plain_deq"])
+    signed = oracle.dequantize(IQ2_S, g["signed_q"], 32 * 256)
+    assert np.array_equal(signed, g["signed_deq"])
+    table = g["plain_deq"].reshape(1024, 8)
+    # the codebook: bytes 0x08, 0x19, 0x2b; 1024 distinct entries
+    assert set(np.unique(table).tolist()) <= {8.0, 25.0, 43.0}
+    assert len({tuple(r) for r in table}) == 1024
+
+
+def test_iq2s_product_table_is_the_codebook():
+    """The product's 2-bit code table (llapis_amd/csrc/iq2s_grid.inc) expands
+    to the reference's codebook."""
+    src = (Path(__file__).resolve().parents[1] / "llapis_amd/csrc/iq2s_grid.inc").read_text()
+    body = " ".join(l.split("//")[0] for l in src.splitlines())
+    codes = [int(v, 0) for v in body.split(",") if v.strip()]
+    assert len(codes) == 1024
+    vals = np.array([8.0, 25.0, 43.0, np.nan])
+    table = np.array([[vals[(c >> (2 * k)) & 3] for k in range(8)] for c in codes])
+    assert np.array_equal(table, load("iq2s_grid.npz")["plain_deq"].reshape(1024, 8))
+
+
+def _q4k_block(d, dmin, sc, mn, qs):
+    """Q4_K block from 8 6-bit scales and mins (packing of ggml-common.h:
+    the inverse of get_scale_min_k4)."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    b[4:16] = s
+    b[16:144] = qs
+    return b
+
+
+def test_q4k_closed_form_nibble_order(oracle):
+    rng = np.random.default_rng(3)
+    qs = rng.integers(0, 256, 128, dtype=np.uint8)
+    blk = _q4k_block(1.0, 0.0, [1] * 8, [0] * 8, qs)
+    y = oracle.dequantize(Q4_K, blk, 256)
+    want = np.zeros(256)
+    for j in range(4):                         # 64 values per 32 bytes: low nibbles, then high
+        want[64 * j:64 * j + 32] = qs[32 * j:32 * j + 32] & 15
+        want[64 * j + 32:64 * j + 64] = qs[32 * j:32 * j + 32] >> 4
+    assert np.array_equal(y, want)
+
+
+def test_q4k_closed_form_scales_and_mins(oracle):
+    rng = np.random.default_rng(4)
+    qs = rng.integers(0, 256, 128, dtype=np.uint8)
+    sc = [3, 17, 63, 1, 40, 9, 62, 33]         # exercises both halves of the 6-bit packing
+    mn = [0, 5, 63, 12, 50, 7, 1, 31]
+    blk = _q4k_block(0.5, 0.25, sc, mn, qs)
+    y = oracle.dequantize(Q4_K, blk, 256)
+    nib = np.zeros(256)
+    for j in range(4):
+        nib[64 * j:64 * j + 32] = qs[32 * j:32 * j + 32] & 15
+        nib[64 * j + 32:64 * j + 64] = qs[32 * j:32 * j + 32] >> 4
+    want = np.array([0.5 * sc[i // 32] * nib[i] - 0.25 * mn[i // 32] for i in range(256)])
+    assert np.allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------------------ activations
+
+def test_act_quant_matches_reference(oracle):
+    g = load("act.npz")
+    for r, x in enumerate(g["x"]):
+        assert np.array_equal(oracle.quantize_act(Q8_K, x), g["q8_K"][r]), ("q8_K", r)
+        assert np.array_equal(oracle.quantize_act(Q8_0, x), g["q8_0"][r]), ("q8_0", r)
+
+
+def _q8k_fields(b, n):
+    nb = n // 256
+    blk = b.reshape(nb, 292)
+    d = blk[:, 0:4].copy().view(np.float32).ravel()
+    q = blk[:, 4:260].view(np.int8).astype(np.int64)
+    bs = blk[:, 260:292].copy().view(np.int16).astype(np.int64)
+    return d, q, bs
+
+
+def test_q8k_invariants(oracle):
+    rng = np.random.default_rng(5)
+    for trial in range(20):
+        x = (rng.standard_normal(512) * rng.uniform(0.01, 10)).astype(np.float32)
+        d, q, bs = _q8k_fields(oracle.quantize_act(Q8_K, x), 512)
+        for b in range(2):
+            xb = x[256 * b:256 * (b + 1)]
+            i = int(np.argmax(np.abs(xb)))          # first largest magnitude
+            assert q[b, i] == -127
+            assert np.float32(d[b]) == np.float32(1.0 / np.float32(-127.0 / xb[i]))
+            assert np.all(np.abs(q[b]) <= 127)
+            assert np.array_equal(bs[b], q[b].reshape(16, 16).sum(1))
+            assert np.max(np.abs(d[b] * q[b] - xb)) <= abs(d[b]) * 0.5 + 1e-6
+
+
+def test_q8_1_invariants(oracle):
+    """q8_1 (the GPU activation format): d = amax/127, q = round(x/d), s = Σx."""
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal(256) * 2).astype(np.float32)
+    b = oracle.quantize_act(Q8_1, x).reshape(8, 36)
+    for k in range(8):
+        xb = x[32 * k:32 * (k + 1)]
+        d = float(b[k, 0:2].copy().view(np.float16)[0])
+        s = float(b[k, 2:4].copy().view(np.float16)[0])
+        q = b[k, 4:36].view(np.int8).astype(np.int64)
+        amax = np.abs(xb).max()
+        assert abs(d - amax / 127) <= 1e-3 * amax / 127
+        assert abs(abs(q[np.argmax(np.abs(xb))]) - 127) == 0
+        assert abs(s - xb.sum(dtype=np.float64)) <= 2e-3 * max(1.0, abs(xb.sum()))
+        assert np.max(np.abs(q * (amax / 127) - xb)) <= amax / 127 * 0.5 + 1e-6
+
+
+# ------------------------------------------------------------ dots
+
+def test_vec_dot_matches_reference(oracle):
+    g = load("dot.npz")
+    for name, t in WTYPES.items():
+        n = int(g[f"{name}_n"])
+        at = int(g[f"{name}_act_type"])
+        assert oracle.act_type(t, ACT_CPU) == at
+        for r, w in enumerate(rows_of(g[f"{name}_w_q"], t, n)):
+            wf = np.abs(oracle.dequantize(t, w, n).astype(np.float64))
+            for j, a in enumerate(g[f"{name}_act_q"]):
+                want = float(g[f"{name}_dot"][r, j])
+                got = oracle.vec_dot(t, ACT_CPU, n, w, a)
+                # the reference's x86 dots accumulate in FMA lanes, the oracle
+                # in the generic order: equal up to rounding of the magnitude sum
+                scale = float(wf @ np.abs(_deq_act(oracle, at, a, n))) + 1e-30
+                assert abs(got - want) <= 2e-6 * scale, (name, r, j, got, want)
+
+
+def _deq_act(oracle, at, a, n):
+    if at == Q8_K:
+        d, q, _ = _q8k_fields(a, n)
+        return (d[:, None].astype(np.float64) * q).ravel()
+    blk = a.reshape(n // 32, -1)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+    off = 2 if at == Q8_0 else 4
+    q = blk[:, off:off + 32].view(np.int8).astype(np.float64)
+    return (d[:, None] * q).ravel()
+
+
+@pytest.mark.parametrize("name", list(WTYPES))
+@pytest.mark.parametrize("mode", [ACT_CPU, ACT_Q8_1])
+def test_vec_dot_equals_dequantised_dot(oracle, name, mode):
+    t = WTYPES[name]
+    g = load("quant.npz")
+    key = f"{name}_{'ones' if t == IQ2_S else 'none'}"
+    n = g[key + "_x"].shape[1]
+    rng = np.random.default_rng(7)
+    at = oracle.act_type(t, mode)
+    for r, w in enumerate(rows_of(g[key + "_q"], t, n)):
+        wf = oracle.dequantize(t, w, n).astype(np.float64)
+        x = rng.standard_normal(n).astype(np.float32)
+        a = oracle.quantize_act(at, x)
+        af = _deq_act(oracle, at, a, n)
+        exact = float(wf @ af)
+        got = oracle.vec_dot(t, mode, n, w, a)
+        scale = float(np.abs(wf) @ np.abs(af)) + 1e-30
+        if t == Q5_0 and mode == ACT_Q8_1:
+            # the q8_1 formula d_w (d8 Σ q a - 16 s) uses the block's stored sum s
+            # of the unquantised x in place of d8 Σ q_a: the difference is bounded
+            # by 16 |d_w| |s - d8 Σ q_a| per block
+            dw = np.abs(np.frombuffer(w.tobytes(), np.uint8).reshape(-1, 22)[:, 0:2].copy().view(np.float16)
+                        .astype(np.float64).ravel())
+            ab = a.reshape(n // 32, 36)
+            d8 = ab[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+            s8 = ab[:, 2:4].copy().view(np.float16).astype(np.float64).ravel()
+            sq = ab[:, 4:36].view(np.int8).astype(np.float64).sum(1)
+            bound = float(np.sum(16 * dw * np.abs(s8 - d8 * sq))) + 3e-6 * scale
+            assert abs(got - exact) <= bound, (r, got, exact, bound)
+        elif t == IQ2_S and mode == ACT_Q8_1:
+            # integer formula (s0*ls0 + s1*ls1 + (s0+s1)/2)/4 truncates: at most
+            # one unit of d*d8 per 32 values
+            dw = np.frombuffer(w.tobytes(), np.uint8).reshape(-1, 82)[:, 0:2].copy().view(np.float16).astype(np.float64)
+            d8 = np.abs(a.reshape(n // 32, 36)[:, 0:2].copy().view(np.float16).astype(np.float64).ravel())
+            bound = float(np.sum(np.repeat(np.abs(dw.ravel()), 8) * d8)) + 1e-6 * scale
+            assert abs(got - exact) <= bound, (r, got, exact, bound)
+        else:
+            assert abs(got - exact) <= 3e-6 * scale, (r, got, exact)
+
+
+# ------------------------------------------------------------ geglu
+
+def test_geglu_table_matches_reference(oracle):
+    g = load("geglu.npz")
+    got = oracle.geglu(g["g"], g["u"], GELU_TABLE)
+    assert np.array_equal(got.view(np.uint32), g["out"].view(np.uint32))
+
+
+def test_geglu_tanh_closed_form(oracle):
+    x = np.linspace(-8, 8, 4001).astype(np.float32)
+    u = np.ones_like(x)
+    got = oracle.geglu(x, u, GELU_TANH).astype(np.float64)
+    xd = x.astype(np.float64)
+    want = 0.5 * xd * (1 + np.tanh(math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    assert np.allclose(got, want, rtol=2e-6, atol=2e-7)
+    tab = oracle.geglu(x, u, GELU_TABLE).astype(np.float64)
+    assert np.allclose(tab, want, rtol=2e-3, atol=2e-3)      # fp16 table
+
+
+# ------------------------------------------------------------ router
+
+def test_router_closed_forms(oracle):
+    T, d, E, k = 2, 64, 16, 4
+    x = np.ones((T, d), np.float32)
+    ids, w, p = oracle.router(x, np.zeros((E, d), np.float32), None, k)
+    assert np.array_equal(ids, np.tile(np.arange(k), (T, 1)))      # ties go to the lower index
+    assert np.allclose(w, 1.0 / k, rtol=0, atol=1e-7)
+    bias = np.arange(E, dtype=np.float32) * 0.1
+    ids, w, p = oracle.router(x, np.zeros((E, d), np.float32), bias, k)
+    assert np.array_equal(ids[0], np.arange(E - 1, E - 1 - k, -1))
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    wr = (rng.standard_normal((E, d)) * 0.3).astype(np.float32)
+    ids, w, p = oracle.router(x, wr, None, k)
+    assert np.allclose(p.sum(1), 1.0, atol=1e-6)
+    for t in range(T):
+        assert len(set(ids[t])) == k
+        assert np.all(np.diff(p[t, ids[t]]) <= 0)
+        assert np.array_equal(np.sort(ids[t]), np.sort(np.argsort(-p[t], kind="stable")[:k]))
+        assert abs(w[t].sum() - 1.0) <= 1e-6
+        logits = x[t].astype(np.float64) @ wr.T.astype(np.float64)
+        ref_p = np.exp(logits - logits.max())
+        ref_p /= ref_p.sum()
+        assert np.allclose(p[t], ref_p, rtol=1e-5, atol=1e-7)
+
+
+# ------------------------------------------------------------ matvec / layer
+
+def test_mul_mat_id_matches_reference(oracle):
+    g = load("mmid.npz")
+    for name, t in WTYPES.items():
+        d_in, d_out, n_pool = (int(v) for v in g[f"{name}_shape"])
+        w = g[f"{name}_w"]
+        eb = row_size(t, d_in) * d_out
+        for i, e in enumerate(g[f"{name}_ids"]):
+            got = oracle.matvec(t, ACT_CPU, w[e * eb:(e + 1) * eb], d_out, d_in, g[f"{name}_x"][i])
+            want = g[f"{name}_y"][i]
+            assert np.max(np.abs(got - want)) <= 2e-6 * max(1.0, np.abs(want).max()), (name, i)
+
+
+def single_tier_layer(g, tag):
+    d, F, E, K, T = (int(v) for v in g[f"{tag}_shape"])
+    gt, dt = (int(v) for v in g[f"{tag}_types"])
+    hot = tag == "hot"
+    L = SimpleNamespace(d_model=d, n_ff=F, n_expert=E, top_k=K, k_slots=E if hot else 0,
+                        hot_gu_type=gt, hot_dn_type=dt, cold_gu_type=gt, cold_dn_type=dt,
+                        hot_gu=g[f"{tag}_gu"] if hot else None, hot_dn=g[f"{tag}_dn"] if hot else None,
+                        cold_gu=None if hot else g[f"{tag}_gu"], cold_dn=None if hot else g[f"{tag}_dn"],
+                        exp_slot=np.arange(E, dtype=np.int32) if hot else np.full(E, -1, np.int32),
+                        slot_exp=np.arange(E, dtype=np.int32) if hot else np.full(1, -1, np.int32),
+                        slot_state=np.full(E, 2, np.int32) if hot else np.zeros(1, np.int32),
+                        s_hot=None, s_cold=None)
+    return L
+
+
+@pytest.mark.parametrize("tag", ["cold", "hot"])
+def test_layer_matches_reference(oracle, tag):
+    g = load("layer.npz")
+    L = single_tier_layer(g, tag)
+    x = g[f"{tag}_x"]
+    ids, w, _ = oracle.router(x, g[f"{tag}_router_w"], g[f"{tag}_bias"], L.top_k)
+    assert np.array_equal(ids, g[f"{tag}_ids"])
+    assert np.allclose(w, g[f"{tag}_w"], rtol=1e-6, atol=1e-7)
+    out, _ = oracle.moe_experts(L, x, g[f"{tag}_ids"], g[f"{tag}_w"])
+    want = g[f"{tag}_out"]
+    err = np.linalg.norm(out - want) / np.linalg.norm(want)
+    assert err <= 1e-6, err
+
+
+def test_dual_mask_brute_force(oracle):
+    """Pairs read the hot pool exactly when the READY predicate holds."""
+    g = load("layer.npz")
+    hot = single_tier_layer(g, "hot")
+    cold = single_tier_layer(g, "cold")
+    E, K = hot.n_expert, hot.top_k
+    rng = np.random.default_rng(9)
+    # a dual layer: hot pool = the "hot" pools for slots, cold pool = the "cold" pools;
+    # slot s holds expert perm[s]; some slots not READY, one slot_exp mismatched
+    ks = 5
+    perm = rng.permutation(E)[:ks]
+    gb, db = row_size(hot.hot_gu_type, hot.d_model) * 2 * hot.n_ff, row_size(hot.hot_dn_type, hot.n_ff) * hot.d_model
+    hot_gu = np.concatenate([hot.hot_gu[e * gb:(e + 1) * gb] for e in perm])
+    hot_dn = np.concatenate([hot.hot_dn[e * db:(e + 1) * db] for e in perm])
+    exp_slot = np.full(E, -1, np.int32)
+    slot_exp = perm.astype(np.int32).copy()
+    state = np.array([2, 1, 2, 0, 2], np.int32)             # FILLING and FREE slots are cold
+    exp_slot[perm] = np.arange(ks)
+    slot_exp[4] = (perm[4] + 1) % E                          # mirror disagreement: cold
+    s_hot = (1 + rng.random(ks)).astype(np.float32)
+    s_cold = (1 + rng.random(E)).astype(np.float32)
+    dual = SimpleNamespace(**{**cold.__dict__, "k_slots": ks, "hot_gu_type": hot.hot_gu_type,
+                              "hot_dn_type": hot.hot_dn_type, "hot_gu": hot_gu, "hot_dn": hot_dn,
+                              "exp_slot": exp_slot, "slot_exp": slot_exp, "slot_state": state,
+                              "s_hot": s_hot, "s_cold": s_cold})
+    x = g["cold_x"]
+    T = x.shape[0]
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    ids[0, 0] = perm[0]; ids[1, 0] = perm[1]; ids[2, 0] = perm[4]    # READY, FILLING, mismatched
+    w = rng.random((T, K)).astype(np.float32)
+    out, yp = oracle.moe_experts(dual, x, ids, w)
+    _, y_hot = oracle.moe_experts(hot, x, ids, w)
+    _, y_cold = oracle.moe_experts(cold, x, ids, w)
+    want = np.zeros_like(out, dtype=np.float64)
+    for t in range(T):
+        for k in range(K):
+            e = int(ids[t, k])
+            s = int(exp_slot[e])
+            is_hot = 0 <= s < ks and state[s] == 2 and slot_exp[s] == e
+            y = y_hot[t * K + k] * s_hot[s] if is_hot else y_cold[t * K + k] * s_cold[e]
+            assert np.allclose(yp[t * K + k], y, rtol=1e-6, atol=1e-7), (t, k, is_hot)
+            want[t] += float(w[t, k]) * y.astype(np.float64)
+    assert np.allclose(out, want, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------ live reference
+
+@pytest.fixture(scope="module")
+def live_ref():
+    try:
+        from oracle import Ref
+        return Ref()
+    except (FileNotFoundError, OSError):
+        pytest.skip("oracle/_ref not built (needs the reference sources)")
+
+
+@pytest.mark.parametrize("name", list(WTYPES))
+def test_live_reference_random_rows(oracle, live_ref, name):
+    t = WTYPES[name]
+    n = 1024 if t in (Q4_K, IQ2_S) else 512
+    rng = np.random.default_rng(10 + t)
+    x = (rng.standard_normal((6, n)) * 0.02).astype(np.float32)
+    im = np.ones(n, np.float32) if t == IQ2_S else None
+    q = live_ref.quantize(t, x, im)
+    at = live_ref.vec_dot_type(t)
+    for r, w in enumerate(rows_of(q, t, n)):
+        assert np.array_equal(oracle.dequantize(t, w, n), live_ref.dequantize(t, w, n))
+        a = rng.standard_normal(n).astype(np.float32)
+        aq = live_ref.quantize_act(at, a)
+        assert np.array_equal(oracle.quantize_act(at, a), aq)
+        want = live_ref.vec_dot(t, n, w, aq)
+        assert abs(oracle.vec_dot(t, ACT_CPU, n, w, aq) - want) <= 2e-6 * max(1.0, abs(want))
