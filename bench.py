@@ -226,6 +226,17 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     return res
 
 
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes committed under profiles/ (scaled by a plain copy's
+    counts), or None when that kernel was not measured for this workload."""
+    try:
+        d = json.loads((ROOT / "profiles" / "pmc_traffic.json").read_text())
+        return d[workload][kernel]["traffic_bytes"]
+    except (OSError, KeyError, TypeError, ValueError):
+        return None
+
+
 def cpu_baseline(host_layer, T, budget_s=12.0):
     """The reference's ggml CPU graph (oracle/_ref) on a bounded sample."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -323,8 +334,10 @@ def main():
         results["dual"] = run_config(la, torch, "decode dual K=57 T=4", dual, 4, args.steps, args.warmup, dev)
 
     head = results.get("iq2s") or next(iter(results.values()))
+    workload = "decode_all_iq2s_1tok" if "iq2s" in results else None
     roof = {"bound": "hbm", "achieved": head["dominant_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": head["dominant_gbs"] / HBM_PEAK_GBS, "traffic": None,
+            "frac": head["dominant_gbs"] / HBM_PEAK_GBS,
+            "traffic": measured_traffic(workload, head["dominant_kernel"]),
             "kernel": head["dominant_kernel"], "algo_bytes_per_launch": head["dominant_bytes"],
             "avg_launch_ms": head["stage_ms"][head["dominant"]]}
     cpu = None

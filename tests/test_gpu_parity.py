@@ -6,7 +6,11 @@ Tolerances (north star: max relative L2 1e-3 in fp32 accumulation):
   differs: rel L2 <= 2e-6 per channel;
 * routing: ids identical, weights within 1e-5 relative;
 * whole layer against the oracle with the GPU's routing: rel L2 <= 1e-4;
-* whole layer against the reference's own ggml CPU graph: rel L2 <= 1e-3.
+* whole layer against the reference's own ggml CPU graph (the committed
+  golden fixtures, made from the compiled reference): rel L2 <= 1e-3, ids
+  identical;
+* HIP graph replays of the layer: identical to the eager calls, replay after
+  replay.
 """
 import ctypes as C
 import sys
@@ -14,9 +18,13 @@ import sys
 import numpy as np
 import pytest
 
+from pathlib import Path
+
 import llapis_amd as la
 from llapis_amd import _lib as L
 from helpers import FULL16, SMALL, layer, rel_l2, tokens
+
+GOLD = Path(__file__).resolve().parent / "golden"
 
 pytestmark = pytest.mark.gpu
 
@@ -232,9 +240,118 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot):
             outs[name] = res
     finally:
         lib.llapis_set_tuning(0, 1)
-        lib.llapis_set_tuning(1, 1)
+        lib.llapis_set_tuning(1, 0)
     for name in ("decode", "decode_nopf"):
         for (o, i, w), (og, ig, wg) in zip(outs[name], outs["generic"]):
             assert np.array_equal(i, ig)
             assert np.allclose(w, wg, rtol=1e-6, atol=0)
             assert rel_l2(o, og) <= 1e-6, rel_l2(o, og)
+
+
+def test_mul_mat_id_vs_reference_golden(gpu):
+    """llapis_mul_mat_id against ggml's own CPU mul_mat_id (golden fixtures)."""
+    torch = torch_mod()
+    g = np.load(GOLD / "mmid.npz", allow_pickle=False)
+    s = torch.cuda.current_stream().cuda_stream
+    for name, wtype in (("q4_K", la.Q4_K), ("iq2_s", la.IQ2_S), ("q5_0", la.Q5_0), ("iq4_nl", la.IQ4_NL)):
+        say(f"mul_mat_id golden {name}")
+        d_in, d_out, n_pool = (int(v) for v in g[f"{name}_shape"])
+        ids = g[f"{name}_ids"]
+        n = ids.size
+        wd = torch.from_numpy(g[f"{name}_w"]).to(gpu)
+        bd = torch.from_numpy(np.ascontiguousarray(g[f"{name}_x"])).to(gpu)
+        idd = torch.from_numpy(ids).to(gpu)
+        y = torch.empty(n, d_out, device=gpu)
+        call = L.MoertMmCall(L.MM_W_HOT, 0, None, 0, bd.data_ptr(), n, idd.data_ptr(), n, y.data_ptr(), None, None)
+        L.check(la.lib().llapis_mul_mat_id(C.byref(call), wtype, wd.data_ptr(), n_pool, d_in, d_out, s), "mm")
+        torch.cuda.synchronize()
+        want = g[f"{name}_y"]
+        for i in range(n):
+            assert rel_l2(y[i].cpu().numpy(), want[i]) <= 2e-6, (name, i)
+
+
+def _golden_layer(g, tag):
+    d, F, E, K, T = (int(v) for v in g[f"{tag}_shape"])
+    gt, dt = (int(v) for v in g[f"{tag}_types"])
+    hot = tag == "hot"
+    spec = la.LayerSpec(d_model=d, n_ff=F, n_expert=E, top_k=K, hot_gu_type=la.Q4_K, hot_dn_type=la.Q5_0,
+                        cold_gu_type=la.IQ2_S, cold_dn_type=la.IQ4_NL)
+    assert (gt, dt) == ((la.Q4_K, la.Q5_0) if hot else (la.IQ2_S, la.IQ4_NL))
+    res = la.Residency.from_hot(E, list(range(E)) if hot else [])
+    lay = la.DualLayer(spec, res, g[f"{tag}_router_w"], g[f"{tag}_bias"])
+    if hot:
+        lay.hot_gu, lay.hot_dn = g["hot_gu"], g["hot_dn"]
+        lay.cold_gu = np.zeros(E * spec.gu_bytes(la.IQ2_S), np.uint8)     # never read: every expert is hot
+        lay.cold_dn = np.zeros(E * spec.dn_bytes(la.IQ4_NL), np.uint8)
+    else:
+        lay.cold_gu, lay.cold_dn = g["cold_gu"], g["cold_dn"]
+        lay.hot_gu = np.zeros(spec.gu_bytes(la.Q4_K), np.uint8)
+        lay.hot_dn = np.zeros(spec.dn_bytes(la.Q5_0), np.uint8)
+    return lay, T
+
+
+@pytest.mark.parametrize("tag", ["cold", "hot"])
+@pytest.mark.parametrize("decode_path", [1, 0])
+def test_layer_vs_reference_golden(gpu, tag, decode_path):
+    """The whole layer against ggml's own CPU graph of it (router mul_mat,
+    soft_max, argsort_top_k, ..., mul_mat_id, geglu, combine)."""
+    torch = torch_mod()
+    say(f"layer golden {tag} decode_path={decode_path}")
+    g = np.load(GOLD / "layer.npz", allow_pickle=False)
+    lay, T = _golden_layer(g, tag)
+    dl = la.DeviceLayer(lay, gpu)
+    lib = la.lib()
+    try:
+        lib.llapis_set_tuning(0, decode_path)
+        out, ids, w = dl.forward(torch.from_numpy(g[f"{tag}_x"]).to(gpu))
+        torch.cuda.synchronize()
+    finally:
+        lib.llapis_set_tuning(0, 1)
+    assert np.array_equal(ids.cpu().numpy(), g[f"{tag}_ids"])
+    assert np.allclose(w.cpu().numpy(), g[f"{tag}_w"], rtol=1e-5, atol=1e-7)
+    err = rel_l2(out.cpu().numpy(), g[f"{tag}_out"])
+    say(f"  rel_l2 vs reference = {err:.3e}")
+    assert err <= 1e-3
+
+
+@pytest.mark.parametrize("T", [1, 4, 6])
+def test_graph_replays_match_eager(gpu, T):
+    """Three layer calls captured in one HIP graph: every replay, with eager
+    calls on the same workspace between replays, reproduces the eager
+    results exactly (the workspace's counters are reset by the kernels
+    themselves, never by memset nodes)."""
+    torch = torch_mod()
+    say(f"graph replays T={T}")
+    spec = FULL16
+    lay = _layer_case(spec, 70 + T, 5, True)
+    dl = la.DeviceLayer(lay, gpu)
+    xs = [torch.from_numpy(tokens(400 + i, T, spec.d_model)).to(gpu) for i in range(3)]
+    eager = []
+    for x in xs:
+        o, i, w = dl.forward(x)
+        eager.append((o.clone(), i.clone(), w.clone()))
+    torch.cuda.synchronize()
+    outs = [(torch.empty(T, spec.d_model, device=gpu), torch.empty(T, spec.top_k, dtype=torch.int32, device=gpu),
+             torch.empty(T, spec.top_k, device=gpu)) for _ in range(3)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for x, (o, i, w) in zip(xs, outs):
+            dl.forward(x, o, i, w, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for x, (o, i, w) in zip(xs, outs):
+            dl.forward(x, o, i, w, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for o, i, w in outs:
+            o.fill_(float("nan"))
+            i.fill_(-1)
+        dl.forward(xs[(rep + 1) % 3])          # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for (o, i, w), (oe, ie, we) in zip(outs, eager):
+            assert torch.equal(i, ie), rep
+            assert torch.equal(w, we), rep
+            assert torch.equal(o, oe), rep
