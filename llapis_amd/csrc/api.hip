@@ -528,7 +528,7 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefetch{0};
+std::atomic<int> g_decode_path{1}, g_prefetch{0}, g_prefill{1};
 
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
@@ -584,17 +584,55 @@ DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
 bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
     return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && (L->d_model % 4) == 0;
 }
+
+// prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
+// chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
+struct PfWs {
+    uint64_t probs, ids, w, ntiles, sorted, tiles, xh, xd, xm, ygu, ah, al, ae, ydn, total;
+    int Tc, max_tiles;
+};
+PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
+    PfWs w;
+    w.Tc = std::min<int>(T, PF_MAX_PAIRS / std::max(1, L->top_k));
+    const uint64_t P = (uint64_t)w.Tc * L->top_k;
+    const uint64_t D = L->d_model, F = L->n_ff, NSB = L->d_model / 256;
+    w.max_tiles = pf_max_tiles((int)P, L->n_expert);
+    w.probs = dec_ctl_bytes(L);
+    w.ids = w.probs + al256((uint64_t)w.Tc * L->n_expert * 4);
+    w.w = w.ids + al256(P * 4);
+    w.ntiles = w.w + al256(P * 4);
+    w.sorted = w.ntiles + 256;
+    w.tiles = w.sorted + al256(P * 4);
+    w.xh = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
+    w.xd = w.xh + al256((uint64_t)w.Tc * D * 2);
+    w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
+    w.ygu = w.xm + al256((uint64_t)w.Tc * NSB * 32);
+    w.ah = w.ygu + al256(P * 2 * F * 4);
+    w.al = w.ah + al256(P * F * 2);
+    w.ae = w.al + al256(P * F * 2);
+    w.ydn = w.ae + al256(P * 4);
+    w.total = w.ydn + al256(P * D * 4);
+    return w;
+}
+
+bool prefill_eligible(const llapis_moe_layer * L, int32_t T) {
+    return g_prefill.load() && T > DEC_MAXT && L->act_mode == LLAPIS_ACT_CPU && L->top_k >= 1 &&
+           L->top_k <= PF_MAX_PAIRS && L->n_expert <= 256 && L->n_ff <= PF_MAX_FF && L->d_model % 256 == 0 &&
+           L->n_ff % 32 == 0;
+}
 }  // namespace
 
 void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
     if (key == 1) g_prefetch = value != 0;
+    if (key == 2) g_prefill = value != 0;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
     if (!L || n_tokens <= 0) return 0;
     uint64_t b = ffn_ws(L, n_tokens).total;
     if (n_tokens <= DEC_MAXT) b = std::max(b, dec_ws(L, n_tokens).total);
+    if (n_tokens > DEC_MAXT) b = std::max(b, pf_ws(L, n_tokens).total);
     return b;
 }
 
@@ -664,6 +702,55 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
                                  src, s, pc >= 0 ? ev : nullptr));
             return 0;
         }
+    }
+    if (prefill_eligible(L, T)) {
+        const PfWs pw = pf_ws(L, T);
+        if (!workspace || ws_bytes < pw.total) return fail("llapis_moe_ffn: workspace too small");
+        const int K = L->top_k;
+        const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+        for (int t0 = 0; t0 < T; t0 += pw.Tc) {
+            const int Tc = std::min(pw.Tc, T - t0);
+            float * probs = (float *)(base + pw.probs);
+            int32_t * ids = ids_out ? ids_out + (int64_t)t0 * K : (int32_t *)(base + pw.ids);
+            float * w = w_out ? w_out + (int64_t)t0 * K : (float *)(base + pw.w);
+            const float * xc = x + (int64_t)t0 * L->d_model;
+            const int pc = prof_slot();
+            LL_TRY(prof_record(pc, 0, 0, s));
+            LL_TRY(launch_router_logits(xc, Tc, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
+            LL_TRY(prof_record(pc, 0, 1, s));
+            LL_TRY(prof_record(pc, 1, 0, s));
+            LL_TRY(launch_topk(probs, Tc, L->n_expert, K, ids, w, s));
+            LL_TRY(prof_record(pc, 1, 1, s));
+            PfParams p = {};
+            p.d_model = L->d_model; p.n_ff = L->n_ff; p.n_expert = L->n_expert; p.top_k = K;
+            p.k_slots = L->k_slots; p.T = Tc;
+            p.x = xc; p.ids = ids;
+            p.exp_slot = L->exp_slot; p.slot_exp = L->slot_exp; p.slot_state = L->slot_state;
+            p.hot_gu = static_cast<const uint8_t *>(L->hot_gu); p.hot_gu_stride = gu_hot;
+            p.cold_gu = static_cast<const uint8_t *>(L->cold_gu); p.cold_gu_stride = gu_cold;
+            p.hot_dn = static_cast<const uint8_t *>(L->hot_dn); p.hot_dn_stride = dn_hot;
+            p.cold_dn = static_cast<const uint8_t *>(L->cold_dn); p.cold_dn_stride = dn_cold;
+            p.s_hot = L->s_hot; p.s_cold = L->s_cold;
+            p.n_tiles = (int *)(base + pw.ntiles);
+            p.sorted = (int32_t *)(base + pw.sorted);
+            p.tiles = (PfTile *)(base + pw.tiles);
+            p.max_tiles = pw.max_tiles;
+            p.xh = (_Float16 *)(base + pw.xh);
+            p.xd = (float *)(base + pw.xd);
+            p.xm = (_Float16 *)(base + pw.xm);
+            p.ygu = (float *)(base + pw.ygu);
+            p.ah = (_Float16 *)(base + pw.ah);
+            p.al = (_Float16 *)(base + pw.al);
+            p.ae = (float *)(base + pw.ae);
+            p.ydn = (float *)(base + pw.ydn);
+            hipEvent_t ev[4] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
+            LL_TRY(launch_prefill(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, src, s,
+                                  pc >= 0 ? ev : nullptr));
+            LL_TRY(prof_record(pc, 4, 0, s));
+            LL_TRY(launch_combine(p.ydn, w, Tc, K, L->d_model, out + (int64_t)t0 * L->d_model, s));
+            LL_TRY(prof_record(pc, 4, 1, s));
+        }
+        return 0;
     }
     const FfnWs ws = ffn_ws(L, T);
     if (!workspace || ws_bytes < ws.total) return fail("llapis_moe_ffn: workspace too small");

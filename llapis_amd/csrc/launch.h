@@ -99,6 +99,50 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
                          hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 
+// ------------------------------------------------------------ prefill path
+
+constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)
+constexpr int PF_TOK = 32;            // routed pairs per tile
+constexpr int PF_MAX_PAIRS = 4096;    // routed pairs per prefill launch (T * top_k)
+constexpr int PF_MAX_FF = 4096;       // longest n_ff the down activation kernel stages
+
+// a run of up to PF_TOK pairs routed to one expert
+struct PfTile {
+    int tier;                   // 0 hot (idx = slot), 1 cold (idx = expert)
+    int idx;
+    int begin;                  // first entry in the sorted pair list
+    int n;
+};
+
+struct PfParams {
+    int d_model, n_ff, n_expert, top_k, k_slots, T;
+    const float * x;                     // [T][d_model]
+    const int32_t * ids;                 // [T][top_k]
+    const int32_t * exp_slot; const int32_t * slot_exp; const int32_t * slot_state;
+    const uint8_t * hot_gu; uint64_t hot_gu_stride;
+    const uint8_t * cold_gu; uint64_t cold_gu_stride;
+    const uint8_t * hot_dn; uint64_t hot_dn_stride;
+    const uint8_t * cold_dn; uint64_t cold_dn_stride;
+    const float * s_hot; const float * s_cold;
+    int * n_tiles;                       // [1]
+    int32_t * sorted;                    // [P] pair indices grouped by expert, ascending within
+    PfTile * tiles;                      // [max_tiles]
+    int max_tiles;
+    _Float16 * xh;                       // [T][d_model] q8_K values (exact fp16)
+    float * xd;                          // [T][d_model / 256] q8_K scales
+    _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
+    float * ygu;                         // [P][2 n_ff]
+    _Float16 * ah;                       // [P][n_ff] down activations d8 q 2^e, fp16 high part
+    _Float16 * al;                       // [P][n_ff] and the exact low part
+    float * ae;                          // [P] 2^-e
+    float * ydn;                         // [P][d_model]
+};
+
+int pf_max_tiles(int P, int n_expert);
+// ev (optional, profiling): begin/end timestamps of the gate_up and down GEMMs
+hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn, int gelu_src, hipStream_t s,
+                          hipEvent_t * ev);
+
 hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
                                 float * logits, hipStream_t s);
 hipError_t launch_topk(float * probs_inout, int T, int E, int K, int32_t * ids, float * w, hipStream_t s);

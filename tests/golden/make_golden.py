@@ -23,7 +23,8 @@ Files (numpy .npz, no pickled objects):
   layer.npz    whole single-tier MoE layers of the CPU graph (router mul_mat,
                soft_max, argsort_top_k, get_rows, sum_rows, clamp, div,
                mul_mat_id gate_up, geglu_split, mul_mat_id down, mul, adds;
-               llama-graph.cpp:1507-1850) for two tiers of formats.
+               llama-graph.cpp:1507-1850) for two tiers of formats, at 3 and
+               at 40 tokens.
 """
 import sys
 from pathlib import Path
@@ -170,14 +171,16 @@ def make_layer(ref, rng):
         cold = tag == "cold"
         gq = ref.quantize(gt, gu, np.ones(d, np.float32) if cold else None)
         dq = ref.quantize(dt, dn, np.ones(F, np.float32) if cold else None)
-        x = rng.standard_normal((T, d)).astype(np.float32)
-        rl = ref.layer(w_r, bias, K, gt, gq, dt, dq, F, T)
-        o, ids, w = rl.run(x, 1, True)
-        del rl
         out.update({f"{tag}_router_w": w_r, f"{tag}_bias": bias, f"{tag}_gu": gq, f"{tag}_dn": dq,
-                    f"{tag}_x": x, f"{tag}_out": o, f"{tag}_ids": ids, f"{tag}_w": w,
-                    f"{tag}_types": np.array([gt, dt], np.int32),
-                    f"{tag}_shape": np.array([d, F, E, K, T], np.int32)})
+                    f"{tag}_types": np.array([gt, dt], np.int32)})
+        # a decode batch and a prefill-sized batch through the same layer
+        for sfx, TT in (("", T), ("_long", 40)):
+            x = rng.standard_normal((TT, d)).astype(np.float32)
+            rl = ref.layer(w_r, bias, K, gt, gq, dt, dq, F, TT)
+            o, ids, w = rl.run(x, 1, True)
+            del rl
+            out.update({f"{tag}{sfx}_x": x, f"{tag}{sfx}_out": o, f"{tag}{sfx}_ids": ids, f"{tag}{sfx}_w": w,
+                        f"{tag}{sfx}_shape": np.array([d, F, E, K, TT], np.int32)})
     return out
 
 

@@ -270,8 +270,8 @@ def test_mul_mat_id_vs_reference_golden(gpu):
             assert rel_l2(y[i].cpu().numpy(), want[i]) <= 2e-6, (name, i)
 
 
-def _golden_layer(g, tag):
-    d, F, E, K, T = (int(v) for v in g[f"{tag}_shape"])
+def _golden_layer(g, tag, sfx=""):
+    d, F, E, K, T = (int(v) for v in g[f"{tag}{sfx}_shape"])
     gt, dt = (int(v) for v in g[f"{tag}_types"])
     hot = tag == "hot"
     spec = la.LayerSpec(d_model=d, n_ff=F, n_expert=E, top_k=K, hot_gu_type=la.Q4_K, hot_dn_type=la.Q5_0,
@@ -291,25 +291,28 @@ def _golden_layer(g, tag):
 
 
 @pytest.mark.parametrize("tag", ["cold", "hot"])
-@pytest.mark.parametrize("decode_path", [1, 0])
-def test_layer_vs_reference_golden(gpu, tag, decode_path):
+@pytest.mark.parametrize("sfx,path", [("", "decode"), ("", "generic"), ("_long", "prefill"), ("_long", "generic")])
+def test_layer_vs_reference_golden(gpu, tag, sfx, path):
     """The whole layer against ggml's own CPU graph of it (router mul_mat,
-    soft_max, argsort_top_k, ..., mul_mat_id, geglu, combine)."""
+    soft_max, argsort_top_k, ..., mul_mat_id, geglu, combine), through each
+    of the three paths (3 tokens: decode or generic; 40: prefill or generic)."""
     torch = torch_mod()
-    say(f"layer golden {tag} decode_path={decode_path}")
+    say(f"layer golden {tag}{sfx} path={path}")
     g = np.load(GOLD / "layer.npz", allow_pickle=False)
-    lay, T = _golden_layer(g, tag)
+    lay, T = _golden_layer(g, tag, sfx)
     dl = la.DeviceLayer(lay, gpu)
     lib = la.lib()
     try:
-        lib.llapis_set_tuning(0, decode_path)
-        out, ids, w = dl.forward(torch.from_numpy(g[f"{tag}_x"]).to(gpu))
+        lib.llapis_set_tuning(0, 1 if path == "decode" else 0)
+        lib.llapis_set_tuning(2, 1 if path == "prefill" else 0)
+        out, ids, w = dl.forward(torch.from_numpy(g[f"{tag}{sfx}_x"]).to(gpu))
         torch.cuda.synchronize()
     finally:
         lib.llapis_set_tuning(0, 1)
-    assert np.array_equal(ids.cpu().numpy(), g[f"{tag}_ids"])
-    assert np.allclose(w.cpu().numpy(), g[f"{tag}_w"], rtol=1e-5, atol=1e-7)
-    err = rel_l2(out.cpu().numpy(), g[f"{tag}_out"])
+        lib.llapis_set_tuning(2, 1)
+    assert np.array_equal(ids.cpu().numpy(), g[f"{tag}{sfx}_ids"])
+    assert np.allclose(w.cpu().numpy(), g[f"{tag}{sfx}_w"], rtol=1e-5, atol=1e-7)
+    err = rel_l2(out.cpu().numpy(), g[f"{tag}{sfx}_out"])
     say(f"  rel_l2 vs reference = {err:.3e}")
     assert err <= 1e-3
 
@@ -355,3 +358,63 @@ def test_graph_replays_match_eager(gpu, T):
             assert torch.equal(i, ie), rep
             assert torch.equal(w, we), rep
             assert torch.equal(o, oe), rep
+
+
+@pytest.mark.parametrize("T,n_hot,scales", [(5, 0, False), (37, 7, True), (64, 16, False), (200, 9, True)])
+def test_prefill_vs_oracle(gpu, oracle, T, n_hot, scales):
+    """The MFMA prefill path (bucketing, grouped gate_up and down GEMMs)
+    against the oracle at the benchmark's per-expert shapes."""
+    torch = torch_mod()
+    say(f"prefill T={T} hot={n_hot} scales={scales}")
+    spec = FULL16
+    lay = _layer_case(spec, 80 + n_hot, n_hot, scales)
+    dl = la.DeviceLayer(lay, gpu)
+    x = tokens(500 + T, T, spec.d_model)
+    out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    ids_g, w_g = ids.cpu().numpy(), w.cpu().numpy()
+    ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, spec.top_k)
+    assert np.array_equal(ids_g, ids_o)
+    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g)
+    check_flip_tolerant(out.cpu().numpy(), out_o)
+
+
+def check_flip_tolerant(got, want):
+    """Layer outputs whose gate_up values differ from the reference's in the
+    last bits (another fp32 summation order) can re-quantise a down
+    activation to the neighbouring q8_0 integer when x * id lies within
+    ~1e-5 of a rounding boundary: a few pairs per few hundred move by ~1e-3.
+    Bars: overall rel L2 <= 5e-4 (the requirement is 1e-3), the median token
+    <= 1e-5 (no flip), every token <= 3e-3."""
+    err = rel_l2(got, want)
+    per_tok = np.array([rel_l2(got[t], want[t]) for t in range(got.shape[0])])
+    say(f"  rel_l2 = {err:.3e}; tokens: median {np.median(per_tok):.1e} max {per_tok.max():.1e} "
+        f"({int((per_tok > 1e-5).sum())} of {per_tok.size} above 1e-5)")
+    assert err <= 5e-4
+    assert np.median(per_tok) <= 1e-5
+    assert per_tok.max() <= 3e-3
+
+
+def test_prefill_chunks_and_generic_agree(gpu, oracle):
+    """A batch longer than one prefill launch (split into chunks of
+    4096 / top_k tokens) against the generic path and the oracle."""
+    torch = torch_mod()
+    spec = SMALL                                 # top_k 4: chunks of 1024 tokens
+    T = 1100
+    say(f"prefill chunks T={T}")
+    lay = _layer_case(spec, 91, 6, True)
+    dl = la.DeviceLayer(lay, gpu)
+    x = tokens(600, T, spec.d_model)
+    xd = torch.from_numpy(x).to(gpu)
+    lib = la.lib()
+    out_p, ids_p, w_p = (t.clone() for t in dl.forward(xd))
+    try:
+        lib.llapis_set_tuning(2, 0)
+        out_g, ids_g, w_g = (t.clone() for t in dl.forward(xd))
+    finally:
+        lib.llapis_set_tuning(2, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(ids_p, ids_g)
+    check_flip_tolerant(out_p.cpu().numpy(), out_g.cpu().numpy())
+    out_o, _ = oracle.moe_experts(lay, x, ids_p.cpu().numpy(), w_p.cpu().numpy())
+    check_flip_tolerant(out_p.cpu().numpy(), out_o)

@@ -327,8 +327,8 @@ def test_mul_mat_id_matches_reference(oracle):
             assert np.max(np.abs(got - want)) <= 2e-6 * max(1.0, np.abs(want).max()), (name, i)
 
 
-def single_tier_layer(g, tag):
-    d, F, E, K, T = (int(v) for v in g[f"{tag}_shape"])
+def single_tier_layer(g, tag, sfx=""):
+    d, F, E, K, T = (int(v) for v in g[f"{tag}{sfx}_shape"])
     gt, dt = (int(v) for v in g[f"{tag}_types"])
     hot = tag == "hot"
     L = SimpleNamespace(d_model=d, n_ff=F, n_expert=E, top_k=K, k_slots=E if hot else 0,
@@ -343,15 +343,16 @@ def single_tier_layer(g, tag):
 
 
 @pytest.mark.parametrize("tag", ["cold", "hot"])
-def test_layer_matches_reference(oracle, tag):
+@pytest.mark.parametrize("sfx", ["", "_long"])
+def test_layer_matches_reference(oracle, tag, sfx):
     g = load("layer.npz")
-    L = single_tier_layer(g, tag)
-    x = g[f"{tag}_x"]
+    L = single_tier_layer(g, tag, sfx)
+    x = g[f"{tag}{sfx}_x"]
     ids, w, _ = oracle.router(x, g[f"{tag}_router_w"], g[f"{tag}_bias"], L.top_k)
-    assert np.array_equal(ids, g[f"{tag}_ids"])
-    assert np.allclose(w, g[f"{tag}_w"], rtol=1e-6, atol=1e-7)
-    out, _ = oracle.moe_experts(L, x, g[f"{tag}_ids"], g[f"{tag}_w"])
-    want = g[f"{tag}_out"]
+    assert np.array_equal(ids, g[f"{tag}{sfx}_ids"])
+    assert np.allclose(w, g[f"{tag}{sfx}_w"], rtol=1e-6, atol=1e-7)
+    out, _ = oracle.moe_experts(L, x, g[f"{tag}{sfx}_ids"], g[f"{tag}{sfx}_w"])
+    want = g[f"{tag}{sfx}_out"]
     err = np.linalg.norm(out - want) / np.linalg.norm(want)
     assert err <= 1e-6, err
 
