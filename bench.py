@@ -11,11 +11,14 @@ Inputs are resident in HBM before timing starts.  Each step reads a different
 layer replica (and token) so the bytes touched per cycle exceed the 256 MB
 MALL: the HBM rate is HBM, not cache.
 
-Also reported (extra): all-Q4_K decode and the dual-precision K=57 4-token
-decode, each with its own roofline; the dominant kernel's duration is timed
-live with HIP events on the stream it runs on; the reference's ggml CPU path
-(oracle/_ref, built from the reference's sources) is timed on a bounded sample
-of the same workload on the host cores.
+Also reported (extra): all-Q4_K decode, the dual-precision K=57 4-token
+decode, and the dual-precision 512-token prefill (grouped MFMA GEMMs; int8
+TOP/s = 2 x 11 894 784 ops per routed pair, against the int8 peak and against
+the attainable min(peak, arithmetic intensity x HBM)), each with its own
+roofline; the dominant kernel's duration is timed live with HIP events on the
+stream it runs on; the reference's ggml CPU path (oracle/_ref, built from the
+reference's sources) is timed on a bounded sample of the same workload on the
+host cores.
 """
 import argparse
 import ctypes as C
@@ -31,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E, GB/s
+OPS_PER_PAIR = 2 * (2816 * 1408 + 704 * 2816)   # int8 multiply-adds x 2 per routed pair (gate_up + down)
 INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
 METRIC = "MoE-layer decode tok/s + HBM TB/s (% peak); 512-tok prefill int8 TOPS (% peak)"
 
@@ -199,7 +203,8 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     st = stage_times(wl, max(2 * R, 64))
     sb = stage_bytes(sp, n_hot, n_cold, T, pairs)
     dom = max(("gate_up", "down"), key=lambda k: st[k])
-    kernel = {"gate_up": "k_dec_gate_up", "down": "k_dec_down"}[dom] if T <= 4 else f"k_mmv ({dom})"
+    kernel = ({"gate_up": "k_dec_gate_up", "down": "k_dec_down"} if T <= 4 else
+              {"gate_up": "k_pf_gate_up", "down": "k_pf_down"})[dom]
     res = {
         "tok_per_s": T * 1e3 / ms_graph,
         "ms_per_step": ms_graph,
@@ -218,6 +223,19 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
         "distinct_cold": n_cold,
         "pairs": pairs,
     }
+    if T > 4:
+        ops = pairs * OPS_PER_PAIR
+        ai = ops / max(bytes_step, 1)
+        tops = ops / (ms_graph * 1e-3) / 1e12
+        attain = min(INT8_PEAK_TOPS, ai * HBM_PEAK_GBS / 1e3)
+        gemm_ms = st["gate_up"] + st["down"]
+        res.update({"int8_tops": tops, "frac_int8_peak": tops / INT8_PEAK_TOPS, "ops_per_byte": ai,
+                    "attainable_tops": attain, "frac_attainable": tops / attain,
+                    "gemm_int8_tops": ops / (gemm_ms * 1e-3) / 1e12,
+                    "gemm_frac_int8_peak": ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS})
+        log(f"[{name}] {tops:.1f} int8 TOP/s = {100 * tops / INT8_PEAK_TOPS:.2f}% of peak, "
+            f"{100 * tops / attain:.1f}% of attainable {attain:.0f} (AI {ai:.0f} op/B); GEMMs alone "
+            f"{res['gemm_int8_tops']:.1f} TOP/s")
     log(f"[{name}] {res['tok_per_s']:.0f} tok/s, {ms_graph * 1e3:.1f} us/step (eager {ms_eager * 1e3:.1f} us), "
         f"step {res['hbm_gbs_step']:.0f} GB/s, {dom} {res['dominant_gbs']:.0f} GB/s, stages "
         + ", ".join(f"{k} {v * 1e3:.1f}us" for k, v in st.items()))
@@ -273,7 +291,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual", help="comma list of iq2s,q4k,dual")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill", help="comma list of iq2s,q4k,dual,prefill")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
@@ -309,7 +327,7 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = "q4k" in cfgs or "dual" in cfgs
+    need_hot = "q4k" in cfgs or "dual" in cfgs or "prefill" in cfgs
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -322,7 +340,7 @@ def main():
         results["iq2s"] = run_config(la, torch, "decode all-IQ2_S T=1", cold_only, 1, args.steps, args.warmup, dev)
     if "q4k" in cfgs:
         results["q4k"] = run_config(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev)
-    if "dual" in cfgs:
+    if "dual" in cfgs or "prefill" in cfgs:
         dual = copy.copy(full)
         gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
         dual.hot_gu = np.concatenate([full.hot_gu[e * gb:(e + 1) * gb] for e in hot57])
@@ -331,7 +349,11 @@ def main():
         bias, frac = la.tune_router_bias(full.router_w, prior, hot57, 0.85, 11)
         dual.router_b = bias
         log(f"dual: router bias puts {frac:.2f} of picks on the 57 hot experts")
-        results["dual"] = run_config(la, torch, "decode dual K=57 T=4", dual, 4, args.steps, args.warmup, dev)
+        if "dual" in cfgs:
+            results["dual"] = run_config(la, torch, "decode dual K=57 T=4", dual, 4, args.steps, args.warmup, dev)
+        if "prefill" in cfgs:
+            results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
+                                            max(10, args.steps // 40), max(2, args.warmup // 20), dev)
 
     head = results.get("iq2s") or next(iter(results.values()))
     workload = "decode_all_iq2s_1tok" if "iq2s" in results else None

@@ -588,7 +588,7 @@ bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
 // prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
 // chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
 struct PfWs {
-    uint64_t probs, ids, w, ntiles, sorted, tiles, xh, xd, xm, ygu, ah, al, ae, ydn, total;
+    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, ygu, aq, as, ae, ydn, total;
     int Tc, max_tiles;
 };
 PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
@@ -603,13 +603,13 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     w.ntiles = w.w + al256(P * 4);
     w.sorted = w.ntiles + 256;
     w.tiles = w.sorted + al256(P * 4);
-    w.xh = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
-    w.xd = w.xh + al256((uint64_t)w.Tc * D * 2);
+    w.xq = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
+    w.xd = w.xq + al256((uint64_t)w.Tc * D);
     w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
     w.ygu = w.xm + al256((uint64_t)w.Tc * NSB * 32);
-    w.ah = w.ygu + al256(P * 2 * F * 4);
-    w.al = w.ah + al256(P * F * 2);
-    w.ae = w.al + al256(P * F * 2);
+    w.aq = w.ygu + al256(P * 2 * F * 4);
+    w.as = w.aq + al256(P * F);
+    w.ae = w.as + al256(P * (F / 32) * 2);
     w.ydn = w.ae + al256(P * 4);
     w.total = w.ydn + al256(P * D * 4);
     return w;
@@ -735,12 +735,12 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.sorted = (int32_t *)(base + pw.sorted);
             p.tiles = (PfTile *)(base + pw.tiles);
             p.max_tiles = pw.max_tiles;
-            p.xh = (_Float16 *)(base + pw.xh);
+            p.xq = (int8_t *)(base + pw.xq);
             p.xd = (float *)(base + pw.xd);
             p.xm = (_Float16 *)(base + pw.xm);
             p.ygu = (float *)(base + pw.ygu);
-            p.ah = (_Float16 *)(base + pw.ah);
-            p.al = (_Float16 *)(base + pw.al);
+            p.aq = (int8_t *)(base + pw.aq);
+            p.as = (_Float16 *)(base + pw.as);
             p.ae = (float *)(base + pw.ae);
             p.ydn = (float *)(base + pw.ydn);
             hipEvent_t ev[4] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};

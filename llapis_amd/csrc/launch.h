@@ -102,7 +102,7 @@ hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 // ------------------------------------------------------------ prefill path
 
 constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)
-constexpr int PF_TOK = 32;            // routed pairs per tile
+constexpr int PF_TOK = 64;            // routed pairs per tile (two 32-column MFMA tiles per wave)
 constexpr int PF_MAX_PAIRS = 4096;    // routed pairs per prefill launch (T * top_k)
 constexpr int PF_MAX_FF = 4096;       // longest n_ff the down activation kernel stages
 
@@ -128,12 +128,12 @@ struct PfParams {
     int32_t * sorted;                    // [P] pair indices grouped by expert, ascending within
     PfTile * tiles;                      // [max_tiles]
     int max_tiles;
-    _Float16 * xh;                       // [T][d_model] q8_K values (exact fp16)
+    int8_t * xq;                         // [T][d_model] q8_K values
     float * xd;                          // [T][d_model / 256] q8_K scales
     _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
     float * ygu;                         // [P][2 n_ff]
-    _Float16 * ah;                       // [P][n_ff] down activations d8 q 2^e, fp16 high part
-    _Float16 * al;                       // [P][n_ff] and the exact low part
+    int8_t * aq;                         // [P][n_ff] q8_0 values of the down activations
+    _Float16 * as;                       // [P][n_ff / 32] q8_0 scale d8 times 2^e (exact fp16)
     float * ae;                          // [P] 2^-e
     float * ydn;                         // [P][d_model]
 };

@@ -46,10 +46,10 @@ __constant__ uint16_t c_iq2s_codes_pf[1024] = {
 };
 
 constexpr int PF_XS = 256 + 8;            // halfs per staged activation row of gate_up (padded)
-constexpr int PF_DCB = 8;                 // 32-blocks per down K chunk
+constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
 constexpr int PF_DXS = PF_DCB * 32 + 8;   // halfs per staged activation row of down (padded)
 constexpr int PF_WROW_GU = 144;           // LDS bytes per weight row and super-block (Q4_K 144, IQ2_S <= 96)
-constexpr int PF_WROW_DN = 192;           // LDS bytes per weight row and down chunk (<= 8 * 22 + 14)
+constexpr int PF_WROW_DN = 112;           // LDS bytes per weight row and down chunk (<= 4 * 22 + 14)
 
 __device__ __forceinline__ uint32_t hbits(h2 v) {
     uint32_t u;
@@ -121,31 +121,53 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         s_off[e] = run;                         // count for now
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0, nt = 0;
-        for (int e = 0; e < E; ++e) {
-            const int n = s_off[e];
-            s_off[e] = acc;
-            int tier = 1, idx = e;
-            if (p.k_slots > 0) {
-                const int s = p.exp_slot[e];
-                if (s >= 0 && s < p.k_slots && p.slot_state[s] == 2 && p.slot_exp[s] == e) {
-                    tier = 0;
-                    idx = s;
-                }
+    // per expert (one thread each): tier, pair offset and tile offset by
+    // exclusive scans over the experts
+    __shared__ int s_nt[257];
+    const int e0 = threadIdx.x;
+    int n_e = 0, tier = 1, idx = e0;
+    if (e0 < E) {
+        n_e = s_off[e0];
+        if (p.k_slots > 0) {
+            const int sl = p.exp_slot[e0];
+            if (sl >= 0 && sl < p.k_slots && p.slot_state[sl] == 2 && p.slot_exp[sl] == e0) {
+                tier = 0;
+                idx = sl;
             }
-            for (int b = 0; b < n && nt < p.max_tiles; b += PF_TOK) {
-                PfTile t;
-                t.tier = tier;
-                t.idx = idx;
-                t.begin = acc + b;
-                t.n = min(PF_TOK, n - b);
-                p.tiles[nt++] = t;
-            }
-            acc += n;
         }
-        s_off[256] = acc;                       // invalid ids are placed after every expert's pairs
-        *p.n_tiles = nt;
+    }
+    const int nt_e = (n_e + PF_TOK - 1) / PF_TOK;
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        s_off[threadIdx.x] = n_e;
+        s_nt[threadIdx.x] = nt_e;
+    }
+    __syncthreads();
+    // inclusive scans (Hillis-Steele over 256 entries)
+    for (int o = 1; o < 256; o <<= 1) {
+        const int a = threadIdx.x >= o ? s_off[threadIdx.x - o] : 0;
+        const int b = threadIdx.x >= o ? s_nt[threadIdx.x - o] : 0;
+        __syncthreads();
+        s_off[threadIdx.x] += a;
+        s_nt[threadIdx.x] += b;
+        __syncthreads();
+    }
+    const int pair0 = s_off[threadIdx.x] - n_e, tile0 = s_nt[threadIdx.x] - nt_e;
+    const int total = s_off[255], tiles = min(s_nt[255], p.max_tiles);
+    __syncthreads();
+    s_off[threadIdx.x] = pair0;                 // exclusive offsets for pass 2
+    if (threadIdx.x == 0) {
+        s_off[256] = total;                     // invalid ids are placed after every expert's pairs
+        *p.n_tiles = tiles;
+    }
+    for (int b = 0; b < nt_e; ++b) {
+        if (tile0 + b >= p.max_tiles) break;
+        PfTile t;
+        t.tier = tier;
+        t.idx = idx;
+        t.begin = pair0 + b * PF_TOK;
+        t.n = min(PF_TOK, n_e - b * PF_TOK);
+        p.tiles[tile0 + b] = t;
     }
     __syncthreads();
     // pass 2: positions
@@ -170,9 +192,9 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
 
 // ------------------------------------------------------------ token quant
 
-// One wave per (token, 256-block): q8_K exactly as the CPU path, then the
-// values as fp16 (exact), the scale, and the 8 per-32 sums as
-// {hi_0..hi_7, lo_0..lo_7} with sum = 32 hi + lo, 0 <= lo < 32.
+// One wave per (token, 256-block): q8_K exactly as the CPU path; the int8
+// values, the scale, and the 8 per-32 sums as {hi_0..hi_7, lo_0..lo_7} with
+// sum = 32 hi + lo, 0 <= lo < 32 (each part exact in fp16).
 __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     __shared__ __align__(16) uint8_t scratch[WG / 64][512];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -181,7 +203,7 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     const bool live = job < p.T * NSB;
     const int t = live ? job / NSB : 0, s = live ? job % NSB : 0;
     ActView L;
-    act_layout(256, 0, &L);                     // 256 + 16 + 16 + ... < 512 bytes
+    act_layout(256, 0, &L);                     // 416 bytes
     uint8_t * base = scratch[wave];
     if (live) {
         ActSrc src;
@@ -191,10 +213,9 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     }
     __syncthreads();
     if (!live) return;
-    const int8_t * q = reinterpret_cast<const int8_t *>(base + L.q);
-    _Float16 * xh = p.xh + (int64_t)t * p.d_model + 256 * s;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xh[lane + 64 * j] = (_Float16)(float)q[lane + 64 * j];
+    if (lane < 16)
+        reinterpret_cast<u32x4 *>(p.xq + (int64_t)t * p.d_model + 256 * s)[lane] =
+            reinterpret_cast<const u32x4 *>(base + L.q)[lane];
     if (lane == 0) p.xd[(int64_t)t * NSB + s] = reinterpret_cast<const float *>(base + L.dK)[0];
     if (lane < 8) {
         const int * bs = reinterpret_cast<const int *>(base + L.bsum);
@@ -203,6 +224,19 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
         _Float16 * xm = p.xm + ((int64_t)t * NSB + s) * 16;
         xm[lane] = (_Float16)(float)hi;
         xm[8 + lane] = (_Float16)(float)lo;
+    }
+}
+
+// 16 signed bytes -> 16 exact fp16 values (8 packed dwords)
+__device__ __forceinline__ void i8x16_to_h(const u32x4 & v, uint32_t (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const h2 off = splat((_Float16)(-1152.0f));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t a, b;
+        bytes_to_magic(w[i] ^ 0x80808080u, a, b);      // 1024 + (v + 128)
+        o[2 * i] = hbits(as_h2(a) + off);
+        o[2 * i + 1] = hbits(as_h2(b) + off);
     }
 }
 
@@ -267,15 +301,26 @@ __device__ __forceinline__ void build_iq2s_f16_tables(uint8_t * grid16, uint8_t 
     }
 }
 
-// copy the 16-byte chunks covering [ps, ps + len) of a slab into LDS at dst;
-// returns nothing -- the piece starts at dst + (ps & 15).  Chunks stay inside
-// the slab because slabs are whole 16-byte chunks.
+// 16-byte chunks covering [ps, ps + len) of a slab; they stay inside the
+// slab because slabs are whole 16-byte chunks
 __device__ __forceinline__ int chunk_count(uint64_t ps, int len) {
     return (int)(((ps + len + 15) >> 4) - (ps >> 4));
 }
 
+constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (Q4_K: 128 rows x 9)
+constexpr int GU_XREG = 4;     // activation chunks per thread per super-block (64 tokens x 16)
+
+// Registers of the next super-block in flight while the current one computes.
+struct GuStage {
+    u32x4 w[GU_WREG];
+    u32x4 x[GU_XREG];
+    u32x4 mb;
+    uint32_t dw;
+    float d8;
+};
+
 template <int HT, int CT>
-__global__ __launch_bounds__(WG) void k_pf_gate_up(const PfParams p) {
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
     __shared__ __align__(16) uint8_t s_w[PF_ROWS * PF_WROW_GU];
     __shared__ __align__(16) _Float16 s_x[PF_TOK * PF_XS];
     __shared__ __align__(16) _Float16 s_mb[PF_TOK * 16];
@@ -286,80 +331,102 @@ __global__ __launch_bounds__(WG) void k_pf_gate_up(const PfParams p) {
     __shared__ int s_tok[PF_TOK], s_pair[PF_TOK], s_poff[PF_ROWS];
     static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
     static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
+    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
 
     if ((int)blockIdx.y >= *p.n_tiles) return;
     const PfTile tile = p.tiles[blockIdx.y];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int wtype = tile.tier == 0 ? HT : CT;
+    const bool q4 = wtype == T_Q4_K;
     const int F2 = 2 * p.n_ff, NSB = p.d_model / 256, K = p.top_k;
     const int r0 = blockIdx.x * PF_ROWS;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, col = lane & 31;
-    const int bb = wtype == T_Q4_K ? 144 : 82;                 // bytes per super-block
-    const uint64_t rb = (uint64_t)NSB * bb;                     // bytes per row
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, col = lane & 31;
+    const int bb = q4 ? 144 : 82;                              // bytes per super-block
+    const int nwc = q4 ? 9 : 6;                                // staged 16-byte chunks per row
+    const uint64_t rb = (uint64_t)NSB * bb;                    // bytes per row
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
-    if (threadIdx.x < PF_TOK) {
-        const int j = threadIdx.x;
-        const int q = p.sorted[tile.begin + min(j, tile.n - 1)];
-        s_pair[j] = q;
-        s_tok[j] = q / K;
+    if (tid < PF_TOK) {
+        const int q = p.sorted[tile.begin + min(tid, tile.n - 1)];
+        s_pair[tid] = q;
+        s_tok[tid] = q / K;
     }
-    if (wtype == T_IQ2_S) build_iq2s_f16_tables(s_grid, s_sign);
+    if (!q4) build_iq2s_f16_tables(s_grid, s_sign);
     __syncthreads();
 
-    f16v y = {};
-    const int row_l = 32 * wave + col;                          // this lane's A row in the block
-    for (int s = 0; s < NSB; ++s) {
-        if (s) __syncthreads();
-        // ---- stage
-        if (wtype == T_Q4_K) {
-            for (int i = threadIdx.x; i < PF_ROWS * 9; i += WG) {
-                const int r = i / 9, c = i - 9 * (i / 9);
-                const uint64_t rr = (uint64_t)min(r0 + r, F2 - 1);
-                *reinterpret_cast<u32x4 *>(s_w + r * 144 + 16 * c) =
-                    *reinterpret_cast<const u32x4 *>(W + rr * rb + 144 * s + 16 * c);
-            }
-        } else {
-            for (int i = threadIdx.x; i < PF_ROWS * 6; i += WG) {
-                const int r = i / 6, c = i - 6 * (i / 6);
-                const uint64_t rr = (uint64_t)min(r0 + r, F2 - 1);
-                const uint64_t ps = rr * rb + 82 * s;
-                if (c < chunk_count(ps, 82))
-                    *reinterpret_cast<u32x4 *>(s_w + r * 96 + 16 * c) =
-                        *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
+    GuStage g;
+    auto fetch = [&](int s) {
+#pragma unroll
+        for (int k = 0; k < GU_WREG; ++k) {
+            const int i = tid + WG * k;
+            const int r = i / nwc, c = i - nwc * (i / nwc);
+            g.w[k] = u32x4{0, 0, 0, 0};
+            if (r < PF_ROWS) {
+                const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+                if (q4 || c < chunk_count(ps, 82))
+                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
             }
         }
-        for (int i = threadIdx.x; i < PF_TOK * 32; i += WG) {
-            const int j = i >> 5, c = i & 31;
-            *reinterpret_cast<u32x4 *>(s_x + j * PF_XS + 8 * c) =
-                *reinterpret_cast<const u32x4 *>(p.xh + (int64_t)s_tok[j] * p.d_model + 256 * s + 8 * c);
+#pragma unroll
+        for (int k = 0; k < GU_XREG; ++k) {
+            const int i = tid + WG * k, j = i >> 4, c = i & 15;
+            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + (int64_t)s_tok[j] * p.d_model + 256 * s + 16 * c);
         }
-        if (threadIdx.x < PF_TOK) s_d8[threadIdx.x] = p.xd[(int64_t)s_tok[threadIdx.x] * NSB + s];
-        if (threadIdx.x >= 64 && threadIdx.x < 64 + 2 * PF_TOK) {
-            const int i = threadIdx.x - 64, j = i >> 1, hh = i & 1;
-            *reinterpret_cast<u32x4 *>(s_mb + 16 * j + 8 * hh) =
-                *reinterpret_cast<const u32x4 *>(p.xm + ((int64_t)s_tok[j] * NSB + s) * 16 + 8 * hh);
+        if (tid < PF_TOK) g.d8 = p.xd[(int64_t)s_tok[tid] * NSB + s];
+        if (tid >= 64 && tid < 64 + 2 * PF_TOK) {
+            const int i = tid - 64;
+            g.mb = *reinterpret_cast<const u32x4 *>(p.xm + ((int64_t)s_tok[i >> 1] * NSB + s) * 16 + 8 * (i & 1));
         }
-        if (threadIdx.x >= 128) {
-            const int r = threadIdx.x - 128;
-            const uint64_t rr = (uint64_t)min(r0 + r, F2 - 1);
-            const uint64_t ps = rr * rb + (uint64_t)bb * s;
-            if (wtype == T_Q4_K) {
-                const uint32_t dd = *reinterpret_cast<const uint32_t *>(W + ps);
-                s_dw[r] = make_float2(h2f(dd & 0xFFFF), h2f(dd >> 16));
-                s_poff[r] = r * 144;
-            } else {
-                s_dw[r] = make_float2(h2f(*reinterpret_cast<const uint16_t *>(W + ps)), 0.0f);
-                s_poff[r] = r * 96 + (int)(ps & 15);
-            }
+        if (tid >= WG - PF_ROWS) {
+            const int r = tid - (WG - PF_ROWS);
+            const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+            g.dw = q4 ? *reinterpret_cast<const uint32_t *>(W + ps) : *reinterpret_cast<const uint16_t *>(W + ps);
         }
-        __syncthreads();
+    };
+    auto store = [&](int s) {
+#pragma unroll
+        for (int k = 0; k < GU_WREG; ++k) {
+            const int i = tid + WG * k;
+            const int r = i / nwc, c = i - nwc * (i / nwc);
+            if (r < PF_ROWS) *reinterpret_cast<u32x4 *>(s_w + r * (q4 ? 144 : 96) + 16 * c) = g.w[k];
+        }
+#pragma unroll
+        for (int k = 0; k < GU_XREG; ++k) {
+            const int i = tid + WG * k, j = i >> 4, c = i & 15;
+            uint32_t h[8];
+            i8x16_to_h(g.x[k], h);
+            u32x4 * d = reinterpret_cast<u32x4 *>(s_x + j * PF_XS + 16 * c);
+            d[0] = u32x4{h[0], h[1], h[2], h[3]};
+            d[1] = u32x4{h[4], h[5], h[6], h[7]};
+        }
+        if (tid < PF_TOK) s_d8[tid] = g.d8;
+        if (tid >= 64 && tid < 64 + 2 * PF_TOK) {
+            const int i = tid - 64;
+            *reinterpret_cast<u32x4 *>(s_mb + 16 * (i >> 1) + 8 * (i & 1)) = g.mb;
+        }
+        if (tid >= WG - PF_ROWS) {
+            const int r = tid - (WG - PF_ROWS);
+            const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+            s_dw[r] = make_float2(h2f(g.dw & 0xFFFF), q4 ? h2f(g.dw >> 16) : 0.0f);
+            s_poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
+        }
+    };
 
-        // ---- MFMA over the super-block
-        f16v acc = {};
+    f16v y0 = {}, y1 = {};
+    const int row_l = 32 * wave + col;                          // this lane's A row in the block
+    fetch(0);
+    for (int s = 0; s < NSB; ++s) {
+        if (s) __syncthreads();                                 // the previous super-block is consumed
+        store(s);
+        __syncthreads();
+        if (s + 1 < NSB) fetch(s + 1);
+
+        f16v a0 = {}, a1 = {};
         const uint8_t * wp = s_w + s_poff[row_l];
-        const _Float16 * xb = s_x + col * PF_XS + 8 * half;
-        if (wtype == T_Q4_K) {
+        const _Float16 * xb0 = s_x + col * PF_XS + 8 * half;
+        const _Float16 * xb1 = xb0 + 32 * PF_XS;
+        const float d80 = s_d8[col], d81 = s_d8[32 + col];
+        if (q4) {
             // 6-bit scales and mins of this row (get_scale_min_k4, ggml-quants.c:822)
             const uint32_t q0 = *reinterpret_cast<const uint32_t *>(wp + 4);
             const uint32_t q1 = *reinterpret_cast<const uint32_t *>(wp + 8);
@@ -374,57 +441,60 @@ __global__ __launch_bounds__(WG) void k_pf_gate_up(const PfParams p) {
             }
 #pragma unroll
             for (int step = 0; step < 16; ++step) {
-                const int j = step >> 1;
-                const int scj = j == 0 ? sc[0] : j == 1 ? sc[1] : j == 2 ? sc[2] : j == 3 ? sc[3]
-                              : j == 4 ? sc[4] : j == 5 ? sc[5] : j == 6 ? sc[6] : sc[7];
-                const h8 a = q4k_frag(wp, step, half, scj);
-                const h8 b = *reinterpret_cast<const h8 *>(xb + 16 * step);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+                const h8 a = q4k_frag(wp, step, half, sc[step >> 1]);
+                a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
             }
             // mins: sum_j m_j * (32 hi_j + lo_j), exact
             const _Float16 f = half ? (_Float16)1.0f : (_Float16)32.0f;
-            const h8 am = {(_Float16)(float)mn[0] * f, (_Float16)(float)mn[1] * f, (_Float16)(float)mn[2] * f,
-                           (_Float16)(float)mn[3] * f, (_Float16)(float)mn[4] * f, (_Float16)(float)mn[5] * f,
-                           (_Float16)(float)mn[6] * f, (_Float16)(float)mn[7] * f};
-            const h8 bm = *reinterpret_cast<const h8 *>(s_mb + 16 * col + 8 * half);
-            f16v mins = {};
-            mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, mins, 0, 0, 0);
-            const float d8 = s_d8[col];
+            h8 am;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) am[j] = (_Float16)(float)mn[j] * f;
+            f16v m0 = {}, m1 = {};
+            m0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * col + 8 * half), m0, 0, 0, 0);
+            m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * (32 + col) + 8 * half), m1, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
                     const float2 dm = s_dw[32 * wave + 8 * i + 4 * half + jj];
                     const int v = 4 * i + jj;
-                    y[v] += __fmul_rn(d8, dm.x) * acc[v] - __fmul_rn(d8, dm.y) * mins[v];
+                    y0[v] += __fmul_rn(d80, dm.x) * a0[v] - __fmul_rn(d80, dm.y) * m0[v];
+                    y1[v] += __fmul_rn(d81, dm.x) * a1[v] - __fmul_rn(d81, dm.y) * m1[v];
                 }
         } else {
 #pragma unroll
             for (int step = 0; step < 16; ++step) {
                 const h8 a = iq2s_frag(wp, step, half, s_grid, s_sign);
-                const h8 b = *reinterpret_cast<const h8 *>(xb + 16 * step);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+                a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
             }
-            const float d8 = s_d8[col];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
+                    const float dw = s_dw[32 * wave + 8 * i + 4 * half + jj].x;
                     const int v = 4 * i + jj;
-                    y[v] += __fmul_rn(s_dw[32 * wave + 8 * i + 4 * half + jj].x, d8) * acc[v];
+                    y0[v] += __fmul_rn(dw, d80) * a0[v];
+                    y1[v] += __fmul_rn(dw, d81) * a1[v];
                 }
         }
     }
-    // ---- store: rows 8i + 4 half + 0..3 of this wave's 32, token `col`
-    if (col < tile.n) {
-        float * out = p.ygu + (int64_t)s_pair[col] * F2;
-        const float f = wtype == T_IQ2_S ? 0.125f : 1.0f;
+    // ---- store: rows 8i + 4 half + 0..3 of this wave's 32, tokens col and 32 + col
+    const float f = q4 ? 1.0f : 0.125f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r0 + 32 * wave + 8 * i + 4 * half;
-            if (r + 3 < F2)
-                *reinterpret_cast<float4 *>(out + r) = make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2],
-                                                                   f * y[4 * i + 3]);
+    for (int tt = 0; tt < 2; ++tt) {
+        const int j = col + 32 * tt;
+        if (j < tile.n) {
+            const f16v & y = tt ? y1 : y0;
+            float * out = p.ygu + (int64_t)s_pair[j] * F2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = r0 + 32 * wave + 8 * i + 4 * half;
+                if (r + 3 < F2)
+                    *reinterpret_cast<float4 *>(out + r) =
+                        make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2], f * y[4 * i + 3]);
+            }
         }
     }
 }
@@ -432,9 +502,9 @@ __global__ __launch_bounds__(WG) void k_pf_gate_up(const PfParams p) {
 // ----------------------------------------------------- down activations
 
 // One workgroup per routed pair: GEGLU + q8_0 (the CPU path's activation
-// format for 32-blocks, bit-identical), then v = d8 * q * 2^e (exact in fp32)
-// with 2^e chosen per pair so the largest magnitude lands in [2^14, 2^15),
-// stored as hi = fp16(v) and lo = fp16(v - hi) (exact: v has <= 19 bits).
+// format for 32-blocks, bit-identical).  Stored: the int8 values, the block
+// scales times a per-pair power of two 2^e (exact in fp16; 2^e puts the
+// largest |d8 q| in [2^14, 2^15)), and 2^-e.
 template <int GSRC>
 __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     __shared__ __align__(16) uint8_t scratch[6400];     // act_layout(PF_MAX_FF) = 6240 bytes
@@ -458,7 +528,7 @@ __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     const int8_t * qv = reinterpret_cast<const int8_t *>(scratch + L.q);
     const float * d32 = reinterpret_cast<const float *>(scratch + L.d32);
     float amax = 0.0f;
-    for (int k = threadIdx.x; k < F; k += WG) amax = fmaxf(amax, fabsf(d32[k >> 5] * (float)qv[k]));
+    for (int b = threadIdx.x; b < F / 32; b += WG) amax = fmaxf(amax, d32[b] * 127.0f);
     amax = wave_max(amax);
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = amax;
     __syncthreads();
@@ -467,14 +537,9 @@ __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     if (amax > 0.0f) ex = 14 - ilogbf(amax);
     ex = max(-100, min(100, ex));
     const float sc = ldexpf(1.0f, ex);
-    _Float16 * hi = p.ah + (int64_t)q * F;
-    _Float16 * lo = p.al + (int64_t)q * F;
-    for (int k = threadIdx.x; k < F; k += WG) {
-        const float v = d32[k >> 5] * (float)qv[k] * sc;
-        const _Float16 h = (_Float16)v;
-        hi[k] = h;
-        lo[k] = (_Float16)(v - (float)h);
-    }
+    for (int i = threadIdx.x; i < F / 16; i += WG)
+        reinterpret_cast<u32x4 *>(p.aq + (int64_t)q * F)[i] = reinterpret_cast<const u32x4 *>(qv)[i];
+    for (int b = threadIdx.x; b < F / 32; b += WG) p.as[(int64_t)q * (F / 32) + b] = (_Float16)(d32[b] * sc);
     if (threadIdx.x == 0) p.ae[q] = ldexpf(1.0f, -ex);
 }
 
@@ -538,6 +603,15 @@ __device__ __forceinline__ void iq4nl_frag(const uint8_t * b, int o, h8 & hi, h8
     scale_split(v, d, hi, lo);
 }
 
+constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
+constexpr int DN_XREG = 2;     // activation chunks per thread per down chunk (64 tokens x 8)
+
+struct DnStage {
+    u32x4 w[DN_WREG];
+    u32x4 x[DN_XREG];
+    uint32_t s[DN_XREG];
+};
+
 template <int HT, int CT>
 __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
     __shared__ __align__(16) uint8_t s_w[PF_ROWS * PF_WROW_DN + 16];   // +16: funnel reads past a row's end
@@ -546,6 +620,7 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
     __shared__ int s_pair[PF_TOK], s_poff[PF_ROWS];
     static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
     static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
+    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 2 == DN_XREG * WG, "staging shape");
 
     if ((int)blockIdx.y >= *p.n_tiles) return;
     const PfTile tile = p.tiles[blockIdx.y];
@@ -553,62 +628,113 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
     const int wtype = tile.tier == 0 ? HT : CT;
     const int D = p.d_model, F = p.n_ff, NB = F / 32;
     const int r0 = blockIdx.x * PF_ROWS;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, col = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, col = lane & 31;
     const int bs = wtype == T_Q5_0 ? 22 : 18;
     const uint64_t rb = (uint64_t)NB * bs;
+    constexpr int WCH = PF_WROW_DN / 16;
     const uint8_t * W = tile.tier == 0 ? p.hot_dn + (uint64_t)tile.idx * p.hot_dn_stride
                                        : p.cold_dn + (uint64_t)tile.idx * p.cold_dn_stride;
-    if (threadIdx.x < PF_TOK) s_pair[threadIdx.x] = p.sorted[tile.begin + min((int)threadIdx.x, tile.n - 1)];
+    if (tid < PF_TOK) s_pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
     __syncthreads();
 
-    f16v y = {};
+    DnStage g;
+    auto fetch = [&](int c0) {
+        const int cb = min(PF_DCB, NB - c0);
+#pragma unroll
+        for (int k = 0; k < DN_WREG; ++k) {
+            const int i = tid + WG * k, r = i / WCH, c = i - WCH * (i / WCH);
+            g.w[k] = u32x4{0, 0, 0, 0};
+            if (r < PF_ROWS) {
+                const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rb + (uint64_t)c0 * bs;
+                if (c < chunk_count(ps, cb * bs))
+                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DN_XREG; ++k) {
+            const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;   // 16-value chunk c
+            g.x[k] = u32x4{0, 0, 0, 0};
+            g.s[k] = 0;
+            if (c < 2 * cb) {
+                const int64_t q = s_pair[j];
+                g.x[k] = *reinterpret_cast<const u32x4 *>(p.aq + q * F + 32 * c0 + 16 * c);
+                g.s[k] = *reinterpret_cast<const uint16_t *>(p.as + q * NB + c0 + (c >> 1));
+            }
+        }
+    };
+    auto store = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < DN_WREG; ++k) {
+            const int i = tid + WG * k, r = i / WCH, c = i - WCH * (i / WCH);
+            if (r < PF_ROWS) {
+                *reinterpret_cast<u32x4 *>(s_w + r * PF_WROW_DN + 16 * c) = g.w[k];
+                if (c == 0) {
+                    const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rb + (uint64_t)c0 * bs;
+                    s_poff[r] = r * PF_WROW_DN + (int)(ps & 15);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DN_XREG; ++k) {
+            const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;
+            uint32_t h[8];
+            i8x16_to_h(g.x[k], h);
+            const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)g.s[k]);
+            h8 hi0, lo0, hi1, lo1;
+            scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h), sv, hi0, lo0);
+            scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h + 4), sv, hi1, lo1);
+            h8 * dh = reinterpret_cast<h8 *>(s_x + j * PF_DXS + 16 * c);
+            h8 * dl = reinterpret_cast<h8 *>(s_xl + j * PF_DXS + 16 * c);
+            dh[0] = hi0;
+            dh[1] = hi1;
+            dl[0] = lo0;
+            dl[1] = lo1;
+        }
+    };
+
+    f16v y0 = {}, y1 = {};
     const int row_l = 32 * wave + col;
+    fetch(0);
     for (int c0 = 0; c0 < NB; c0 += PF_DCB) {
         const int cb = min(PF_DCB, NB - c0);           // blocks in this chunk
         if (c0) __syncthreads();
-        constexpr int WCH = PF_WROW_DN / 16;
-        for (int i = threadIdx.x; i < PF_ROWS * WCH; i += WG) {
-            const int r = i / WCH, c = i - WCH * (i / WCH);
-            const uint64_t rr = (uint64_t)min(r0 + r, D - 1);
-            const uint64_t ps = rr * rb + (uint64_t)c0 * bs;
-            if (c < chunk_count(ps, cb * bs))
-                *reinterpret_cast<u32x4 *>(s_w + r * PF_WROW_DN + 16 * c) =
-                    *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
-            if (c == 0) s_poff[r] = r * PF_WROW_DN + (int)(ps & 15);
-        }
-        const int xc = cb * 4;                          // 16-byte chunks per staged token row
-        for (int i = threadIdx.x; i < PF_TOK * xc; i += WG) {
-            const int j = i / xc, c = i - xc * (i / xc);
-            const int64_t g = (int64_t)s_pair[j] * F + 32 * c0 + 8 * c;
-            *reinterpret_cast<u32x4 *>(s_x + j * PF_DXS + 8 * c) = *reinterpret_cast<const u32x4 *>(p.ah + g);
-            *reinterpret_cast<u32x4 *>(s_xl + j * PF_DXS + 8 * c) = *reinterpret_cast<const u32x4 *>(p.al + g);
-        }
+        store(c0);
         __syncthreads();
+        if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
         const uint8_t * wp = s_w + s_poff[row_l];
-        const int xo = col * PF_DXS + 8 * half;
-        const int nsteps = 2 * cb;
-        for (int step = 0; step < nsteps; ++step) {
+        const int xo0 = col * PF_DXS + 8 * half, xo1 = xo0 + 32 * PF_DXS;
+        for (int step = 0; step < 2 * cb; ++step) {
             h8 ah, al;
             if (wtype == T_Q5_0) q5_0_frag(wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
             else iq4nl_frag(wp + 18 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
-            const h8 bh = *reinterpret_cast<const h8 *>(s_x + xo + 16 * step);
-            const h8 bl = *reinterpret_cast<const h8 *>(s_xl + xo + 16 * step);
-            y = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, y, 0, 0, 0);
-            y = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, y, 0, 0, 0);
-            y = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, y, 0, 0, 0);
+            const h8 b0h = *reinterpret_cast<const h8 *>(s_x + xo0 + 16 * step);
+            const h8 b0l = *reinterpret_cast<const h8 *>(s_xl + xo0 + 16 * step);
+            const h8 b1h = *reinterpret_cast<const h8 *>(s_x + xo1 + 16 * step);
+            const h8 b1l = *reinterpret_cast<const h8 *>(s_xl + xo1 + 16 * step);
+            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0h, y0, 0, 0, 0);
+            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0l, y0, 0, 0, 0);
+            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0h, y0, 0, 0, 0);
+            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1h, y1, 0, 0, 0);
+            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1l, y1, 0, 0, 0);
+            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1h, y1, 0, 0, 0);
         }
     }
-    if (col < tile.n) {
-        const int q = s_pair[col];
-        const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
-        const float f = p.ae[q] * sc;
-        float * out = p.ydn + (int64_t)q * D;
+    const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = r0 + 32 * wave + 8 * i + 4 * half;
-            if (r + 3 < D)
-                *reinterpret_cast<float4 *>(out + r) = make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2],
-                                                                   f * y[4 * i + 3]);
+    for (int tt = 0; tt < 2; ++tt) {
+        const int j = col + 32 * tt;
+        if (j < tile.n) {
+            const int q = s_pair[j];
+            const float f = p.ae[q] * sc;
+            const f16v & y = tt ? y1 : y0;
+            float * out = p.ydn + (int64_t)q * D;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = r0 + 32 * wave + 8 * i + 4 * half;
+                if (r + 3 < D)
+                    *reinterpret_cast<float4 *>(out + r) =
+                        make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2], f * y[4 * i + 3]);
+            }
         }
     }
 }
