@@ -148,8 +148,19 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
 
 /* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
- * (default 1), key 1 = down-slab prefetch during gate_up (default 0). */
+ * (default 1), key 1 = down-slab prefetch during gate_up (default 0),
+ * key 2 = MFMA prefill path for > 4 tokens (default 1), key 3 = the decode
+ * path as one kernel (default 0: three kernels, faster on MI355X today),
+ * key 4 = the bound of one wait of that kernel in microseconds (default
+ * 50000). */
 void llapis_set_tuning(int32_t key, int32_t value);
+
+/* Waits for `stream`, then reports whether a call on this workspace since
+ * the last status check had a wait of the single-kernel decode path time out
+ * (possible only if its workgroups could not all be resident at once, e.g.
+ * while other work occupies the GPU): 0 if not, else a negative code with
+ * llapis_last_error() set; the flag is cleared. */
+int32_t llapis_moe_ffn_status(void * workspace, uint64_t ws_bytes, void * stream);
 
 /* Stage timing of llapis_moe_ffn for measurement (not under stream capture):
  * while enabled, every call times its stages on the call's stream with HIP

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -528,7 +529,24 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefetch{0}, g_prefill{1};
+std::atomic<int> g_decode_path{1}, g_prefetch{0}, g_prefill{1}, g_fused{0};
+std::atomic<int64_t> g_spin_us{50000};        // bound of one wait in the single-kernel decode path
+
+// wall-clock ticks per microsecond of the current device (cached per device)
+int64_t wall_ticks_per_us() {
+    static std::mutex mu;
+    static std::map<int, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 100;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
+    const int64_t t = std::max<int64_t>(1, khz / 1000);
+    cache[dev] = t;
+    return t;
+}
 
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
@@ -626,6 +644,8 @@ void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
     if (key == 1) g_prefetch = value != 0;
     if (key == 2) g_prefill = value != 0;
+    if (key == 3) g_fused = value != 0;
+    if (key == 4) g_spin_us = std::max(0, value);
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
@@ -642,6 +662,21 @@ int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspa
     const uint64_t n = std::min<uint64_t>(ws_bytes, dw.ctl_bytes);
     LL_TRY(launch_zero_i32(static_cast<int *>(workspace), (int)(n / 4), (hipStream_t)stream));
     return 0;
+}
+
+int32_t llapis_moe_ffn_status(void * workspace, uint64_t ws_bytes, void * stream) {
+    if (!workspace || ws_bytes < sizeof(DecCtl)) return fail("llapis_moe_ffn_status: workspace too small");
+    hipStream_t s = (hipStream_t)stream;
+    DecCtl * ctl = static_cast<DecCtl *>(workspace);
+    int err = 0;
+    LL_TRY(hipMemcpyAsync(&err, &ctl->error, sizeof(int), hipMemcpyDeviceToHost, s));
+    LL_TRY(hipStreamSynchronize(s));
+    if (err == 0) return 0;
+    const int zero = 0;
+    LL_TRY(hipMemcpyAsync(&ctl->error, &zero, sizeof(int), hipMemcpyHostToDevice, s));
+    LL_TRY(hipStreamSynchronize(s));
+    return fail("llapis_moe_ffn: a wait of the single-kernel decode path timed out (its workgroups were not all "
+                "resident); that call's outputs are invalid");
 }
 
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
@@ -696,6 +731,16 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         if (dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) <= 65536 && dec_lds_down(p) <= 65536) {
             const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+            if (g_fused.load()) {
+                p.spin_limit = g_spin_us.load() * wall_ticks_per_us();
+                // the single kernel's time is reported as the gate_up stage
+                hipEvent_t evf[2] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1)};
+                const hipError_t e = launch_decode_fused(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type,
+                                                         L->cold_dn_type, L->act_mode, src, s, pc >= 0 ? evf : nullptr);
+                if (e == hipSuccess) return 0;
+                if (e != hipErrorNotSupported) return fail(std::string("launch_decode_fused: ") + hipGetErrorString(e));
+                if (pc >= 0) g_prof.used[pc][2] = false;
+            }
             hipEvent_t ev[6] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0),
                                 prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,

@@ -27,15 +27,17 @@
 // the call; B clears A's.
 #include <hip/hip_ext.h>
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "device.h"
 #include "launch.h"
 
 namespace llapis {
 namespace dev {
 
-__constant__ uint16_t c_iq2s_codes_dec[1024] = {
-#include "iq2s_grid.inc"
-};
+__constant__ Iq2sTables c_iq2s_tab_dec = make_iq2s_tables();
 
 template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
 static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
@@ -59,22 +61,6 @@ __device__ __forceinline__ bool arrive_last(int * counter, int n, int * s_flag) 
     return *s_flag != 0;
 }
 
-// wave64 reductions on DPP lane moves (quad perms, row mirrors, row
-// broadcasts); the result is read from lane 63 and is wave-uniform
-template <int CTRL, int ROWMASK = 0xF>
-__device__ __forceinline__ float dpp_mov(float old, float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWMASK, 0xF, false));
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v, v));          // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_mov<0x4E>(v, v));          // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_mov<0x141>(v, v));         // row_half_mirror
-    v = fmaxf(v, dpp_mov<0x140>(v, v));         // row_mirror
-    v = fmaxf(v, dpp_mov<0x142, 0xA>(v, v));    // row_bcast15
-    v = fmaxf(v, dpp_mov<0x143, 0xC>(v, v));    // row_bcast31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
 __device__ __forceinline__ int member(const GroupInfo & g, int i) {
     return i == 0 ? g.mem[0] : i == 1 ? g.mem[1] : i == 2 ? g.mem[2] : g.mem[3];
 }
@@ -90,7 +76,8 @@ __device__ __forceinline__ const uint8_t * group_slab(int tier, int idx, const u
 // in double, scaled by float(1/sum); argsort_top_k: descending, equal
 // probabilities in index order; weights p[ids] / max(sum, 6.103515625e-5)
 // with the sum accumulated in double in id order).  E <= 256.
-__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids) {
+__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
+                             float * s_w = nullptr) {
     const int lane = threadIdx.x & 63;
     float v[4];
 #pragma unroll
@@ -106,7 +93,7 @@ __device__ void select_token(const float * logits, int E, int K, int32_t * ids, 
         v[j] = e < E ? expf(v[j] - mx) : 0.0f;
         ls += (double)v[j];
     }
-    for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    ls = wave_sum_dpp(ls);
     const float inv = (float)(1.0 / ls);
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = lane + 64 * j < E ? __fmul_rn(v[j], inv) : -1.0f;
@@ -126,13 +113,100 @@ __device__ void select_token(const float * logits, int E, int K, int32_t * ids, 
         sum += (double)m;
         if (lane == k) sel = m;
         if (lane == 0) {
-            ids[k] = e;
+            if (ids) ids[k] = e;
             s_ids[k] = e;
         }
     }
     float sf = (float)sum;
     if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
-    if (lane < K) w[lane] = sel / sf;
+    if (lane < K) {
+        if (w) w[lane] = sel / sf;
+        if (s_w) s_w[lane] = sel / sf;
+    }
+}
+
+// Expert groups of the call from the routed ids in LDS (one wave): pairs that
+// share an expert form one group (at most one member per token), in the order
+// of their first pair; each group's tier by the residency predicate.
+__device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo * groups, int * n_groups) {
+    const int lane = threadIdx.x & 63;
+    const int T = p.T, E = p.n_expert, P = T * p.top_k;
+    const bool live = lane < P;
+    const int ex = live ? s_ids[lane] : -1;
+    int leader = lane, slot = 0, nmem = 0;
+    for (int q = 0; q < P; ++q) {
+        if (s_ids[q] == ex) {
+            if (q < lane) ++slot;
+            if (q < leader) leader = q;
+            ++nmem;
+        }
+    }
+    const bool is_leader = live && leader == lane;
+    const uint64_t lm = __ballot(is_leader);
+    const int gid = __popcll(lm & (leader == 0 ? 0ull : (~0ull >> (64 - leader))));
+    if (is_leader) {
+        int tier = 2, idx = 0;
+        if (ex >= 0 && ex < E) {
+            tier = 1;
+            idx = ex;
+            if (p.k_slots > 0) {
+                const int s = p.exp_slot[ex];
+                if (s >= 0 && s < p.k_slots && p.slot_state[s] == 2 && p.slot_exp[s] == ex) {
+                    tier = 0;
+                    idx = s;
+                }
+            }
+        }
+        groups[gid].tier = tier;
+        groups[gid].idx = idx;
+        groups[gid].n_mem = min(nmem, min(T, DEC_MAXT));     // one member per token at most
+    }
+    if (live && slot < DEC_MAXT) groups[gid].mem[slot] = lane;
+    if (lane == 0) *n_groups = __popcll(lm);
+}
+
+// Router logits of expert e for every token (one workgroup), written with
+// device-coherent stores.  Each lane issues all of its row loads (RU float4
+// per pass) before any arithmetic.
+__device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 64]) {
+    constexpr int RU = 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = p.d_model, E = p.n_expert, T = p.T, n4 = d / 4;
+    const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
+    const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
+    float acc[DEC_MAXT];
+#pragma unroll
+    for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
+    for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
+        // clamped indices (row end, last token): every load is unconditional
+        float4 w4[RU], xv[DEC_MAXT][RU];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+            for (int u = 0; u < RU; ++u) xv[t][u] = x4[(int64_t)min(t, T - 1) * n4 + min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+            for (int u = 0; u < RU; ++u)
+                if (t < T && k0 + u * WG < n4)
+                    acc[t] += w4[u].x * xv[t][u].x + w4[u].y * xv[t][u].y + w4[u].z * xv[t][u].z +
+                              w4[u].w * xv[t][u].w;
+    }
+#pragma unroll
+    for (int t = 0; t < DEC_MAXT; ++t) {
+        const float s = wave_sum_dpp(acc[t]);
+        if (lane == 0) s_part[t][wave] = s;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < T) {
+        const int t = threadIdx.x;
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
+        st_coh(p.logits + (int64_t)t * E + e, s + (p.router_b ? p.router_b[e] : 0.0f));
+    }
 }
 
 template <int AM>
@@ -140,51 +214,11 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     __shared__ int s_last;
     __shared__ int s_ids[DEC_PMAX];
     __shared__ float s_part[DEC_MAXT][WG / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6;
     const int gw = blockIdx.x * (WG / 64) + wave;          // wave id in the grid
     const int nw = gridDim.x * (WG / 64);
     const int d = p.d_model, E = p.n_expert, T = p.T, K = p.top_k;
-    // router: workgroup e computes expert e's logit for every token; each lane
-    // issues all of its row loads (RU float4 per pass) before any arithmetic
-    if ((int)blockIdx.x < E) {
-        constexpr int RU = 4;
-        const int e = blockIdx.x, n4 = d / 4;
-        const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
-        const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
-        float acc[DEC_MAXT];
-#pragma unroll
-        for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
-        for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
-            // clamped indices (row end, last token): every load is unconditional
-            float4 w4[RU], xv[DEC_MAXT][RU];
-#pragma unroll
-            for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
-#pragma unroll
-            for (int t = 0; t < DEC_MAXT; ++t)
-#pragma unroll
-                for (int u = 0; u < RU; ++u) xv[t][u] = x4[(int64_t)min(t, T - 1) * n4 + min(k0 + u * WG, n4 - 1)];
-#pragma unroll
-            for (int t = 0; t < DEC_MAXT; ++t)
-#pragma unroll
-                for (int u = 0; u < RU; ++u)
-                    if (t < T && k0 + u * WG < n4)
-                        acc[t] += w4[u].x * xv[t][u].x + w4[u].y * xv[t][u].y + w4[u].z * xv[t][u].z +
-                                  w4[u].w * xv[t][u].w;
-        }
-#pragma unroll
-        for (int t = 0; t < DEC_MAXT; ++t) {
-            const float s = wave_sum(acc[t]);
-            if (lane == 0) s_part[t][wave] = s;
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < T) {
-            const int t = threadIdx.x;
-            float s = 0.0f;
-#pragma unroll
-            for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
-            st_coh(p.logits + (int64_t)t * E + e, s + (p.router_b ? p.router_b[e] : 0.0f));
-        }
-    }
+    if ((int)blockIdx.x < E) router_expert(p, blockIdx.x, s_part);
     // the tokens' gate_up activations: one wave per 256-block (q8_K) or per
     // 64 values (q8_1)
     {
@@ -207,41 +241,7 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     if (wave < T) select_token(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
     for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
     __syncthreads();
-    if (wave == 0) {
-        const int P = T * K;
-        const bool live = lane < P;
-        const int ex = live ? s_ids[lane] : -1;
-        int leader = lane, slot = 0, nmem = 0;
-        for (int q = 0; q < P; ++q) {
-            if (s_ids[q] == ex) {
-                if (q < lane) ++slot;
-                if (q < leader) leader = q;
-                ++nmem;
-            }
-        }
-        const bool is_leader = live && leader == lane;
-        const uint64_t lm = __ballot(is_leader);
-        const int gid = __popcll(lm & (leader == 0 ? 0ull : (~0ull >> (64 - leader))));
-        if (is_leader) {
-            int tier = 2, idx = 0;
-            if (ex >= 0 && ex < E) {
-                tier = 1;
-                idx = ex;
-                if (p.k_slots > 0) {
-                    const int s = p.exp_slot[ex];
-                    if (s >= 0 && s < p.k_slots && p.slot_state[s] == 2 && p.slot_exp[s] == ex) {
-                        tier = 0;
-                        idx = s;
-                    }
-                }
-            }
-            p.ctl->groups[gid].tier = tier;
-            p.ctl->groups[gid].idx = idx;
-            p.ctl->groups[gid].n_mem = min(nmem, min(T, DEC_MAXT));     // one member per token at most
-        }
-        if (live && slot < DEC_MAXT) p.ctl->groups[gid].mem[slot] = lane;
-        if (lane == 0) p.ctl->n_groups = __popcll(lm);
-    }
+    if (wave == 0) build_groups(p, s_ids, p.ctl->groups, &p.ctl->n_groups);
 }
 
 // The group record g written by A, or an empty group when g is past the
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     for (int c = 0; c < DEC_MAXT; ++c)
         if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride, abytes);
     const int grid_off = align16i(a0 + min(p.T, DEC_MAXT) * abytes), sign_off = grid_off + 1024 * 8;
-    if (wtype == T_IQ2_S) build_iq2s_tables(smem, grid_off, sign_off, c_iq2s_codes_dec);
+    if (wtype == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();
 
@@ -358,11 +358,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int wb = (int)(start & 15) + rw * rb;
         const int U = d_in / Fmt<HT>::UNIT;
         if (gi.tier == 0) {
-            for (int u = lr; u < U; u += LPR)
-                unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            if (n_mem == 1) {           // one member: the single-column unit
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            } else {
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            }
         } else {
-            for (int u = lr; u < U; u += LPR)
-                unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            if (n_mem == 1) {           // one member: the single-column unit
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            } else {
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+            }
         }
     }
 #pragma unroll
@@ -426,9 +432,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int wb = (int)(start & 15) + rw * rb;
         const int U = d_in / Fmt<HT>::UNIT;
         if (gi.tier == 0) {
-            for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+            if (n_mem == 1) {           // one member: the single-column unit
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, 0, 0);
+            } else {
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+            }
         } else {
-            for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+            if (n_mem == 1) {           // one member: the single-column unit
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, 0, 0);
+            } else {
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+            }
         }
     }
 #pragma unroll
@@ -462,6 +476,290 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             float o = __fmul_rn(ld_coh(yt + r), wt[0]);
             for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(ld_coh(yt + (int64_t)k * D + r), wt[k]));
             p.out[(int64_t)t * D + r0 + r] = o;
+        }
+    }
+}
+
+// ------------------------------------------------------------ single kernel
+//
+// The layer in one launch.  Phases hand off through arrival counters in the
+// control block; a consumer waits (thread 0, bounded by p.spin_limit ticks of
+// the wall clock) until a counter reaches its target.  The grid is sized so
+// every workgroup is resident (occupancy x CUs); a wait that times out sets
+// ctl->error and the workgroup skips the rest of its work, so every wave
+// still exits.
+//   1  workgroup e < E: router logits of expert e (coherent stores, then one
+//      arrival); every workgroup: the tokens quantised into its own LDS and
+//      the IQ2_S tables
+//   2  wait for the router (its last arrival sets a flag); every workgroup
+//      selects the routing itself (DPP top-k per token) and builds the
+//      expert groups in LDS
+//   3  gate_up items (group, 16-row block) round-robin over the workgroups;
+//      outputs with coherent stores, then one arrival on the group's counter
+//      (the last one sets the group's flag)
+//   4  down items (group, 32-row block): wait for the group's flag, GEGLU +
+//      quantise its members (coherent loads), down, combine
+//   5  the last workgroup out resets every counter for the next call
+
+__device__ __forceinline__ int ld_coh_i(const int * q) {
+    return __hip_atomic_load(const_cast<int *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0 waits until the write-once flag is set (polling with a short
+// sleep; the counters themselves are only touched by their arrivals), or
+// until the wall-clock bound passes; the result is broadcast.
+__device__ bool wait_flag(const DecParams & p, const int * flag, int * s_flag) {
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        const long long t0 = wall_clock64();
+        while (ld_coh_i(flag) == 0) {
+            if (wall_clock64() - t0 > p.spin_limit) {
+                ok = 0;
+                __hip_atomic_store(&p.ctl->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        }
+        *s_flag = ok;
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
+// thread 0: one arrival on `ctr`; the arrival that completes `target` sets
+// the flag (after this workgroup's coherent stores have completed)
+__device__ __forceinline__ void arrive_flag(int * ctr, int target, int * flag) {
+    if (threadIdx.x == 0 && atomicAdd(ctr, 1) == target - 1)
+        __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HT, int CT, int HD, int CD, int AM, int GSRC>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_fused(const DecParams p) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float s_part[DEC_MAXT][WG / 64];
+    __shared__ int s_ids[DEC_PMAX];
+    __shared__ float s_wt[DEC_PMAX];
+    __shared__ GroupInfo s_grp[DEC_PMAX];
+    __shared__ int s_ng, s_flag, s_lastc[DEC_MAXT];
+    constexpr int LPR_G = Fmt<HT>::LPR, ROWS_G = WG / LPR_G;
+    constexpr int LPR_D = Fmt<HD>::LPR, ROWS_D = WG / LPR_D;
+    static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
+    static_assert(Fmt<HD>::LPR == Fmt<CD>::LPR && !k256<HD>() && !k256<CD>(), "down formats");
+    const int wave = threadIdx.x >> 6;
+    const int d = p.d_model, F = p.n_ff, E = p.n_expert, T = p.T, K = p.top_k;
+    const int F2 = 2 * F;
+    const int NRB_G = (F2 + ROWS_G - 1) / ROWS_G, NRB_D = (d + ROWS_D - 1) / ROWS_D;
+
+    // ---- phase 1
+    if ((int)blockIdx.x < E) {
+        router_expert(p, blockIdx.x, s_part);
+        wait_vm();
+        __syncthreads();
+        arrive_flag(&p.ctl->route_count, E, &p.ctl->route_ready);
+    }
+    ActView tmp;
+    const int abg = act_layout(d, 0, &tmp);
+    const int ag0 = p.w_lds_gu;
+    // token t's column: the layout at ag0 shifted by t * abg
+    ActView av0;
+    act_layout(d, ag0, &av0);
+    // each token is staged in LDS (the weight region, free until phase 3)
+    // with one round of 16-byte loads, then quantised from there
+    for (int t = 0; t < T; ++t) {
+        const u32x4 * xs = reinterpret_cast<const u32x4 *>(p.x + (int64_t)t * d);
+        for (int i = threadIdx.x; i < d / 4; i += WG) reinterpret_cast<u32x4 *>(smem)[i] = xs[i];
+        __syncthreads();
+        ActView v;
+        act_layout(d, ag0 + t * abg, &v);
+        ActSrc src;
+        src.p = reinterpret_cast<const float *>(smem);
+        src.n = d;
+        quantize_act<HT, AM, SRC_PLAIN>(smem, v, src, d);
+        __syncthreads();
+    }
+    const int grid_off = align16i(ag0 + min(T, DEC_MAXT) * abg), sign_off = grid_off + 1024 * 8;
+    if (HT == T_IQ2_S || CT == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
+
+    // ---- phase 2
+    bool ok = wait_flag(p, &p.ctl->route_ready, &s_flag);
+    if (ok && wave < T) select_token(p.logits + (int64_t)wave * E, E, K, nullptr, nullptr, s_ids + wave * K, s_wt + wave * K);
+    __syncthreads();
+    if (ok && wave == 0) build_groups(p, s_ids, s_grp, &s_ng);
+    __syncthreads();
+    if (ok && blockIdx.x == 0 && (int)threadIdx.x < T * K) {
+        p.ids[threadIdx.x] = s_ids[threadIdx.x];
+        p.w[threadIdx.x] = s_wt[threadIdx.x];
+    }
+    const int ng = ok ? min(s_ng, DEC_PMAX) : 0;
+
+    // ---- phase 3: gate_up
+    for (int it = blockIdx.x; it < ng * NRB_G; it += gridDim.x) {
+        const int g = it / NRB_G, rbi = it - g * NRB_G;
+        const GroupInfo gi = s_grp[g];
+        const bool valid = gi.tier < 2;
+        const int wtype = gi.tier == 0 ? HT : CT;
+        const int r0 = rbi * ROWS_G;
+        const int rows = min(ROWS_G, F2 - r0);
+        const int rb = (d / blk_elems(wtype)) * blk_bytes(wtype);
+        const uint64_t start = (uint64_t)r0 * rb;
+        const uint64_t c0 = start >> 4;
+        const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
+        const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_gu, p.hot_gu_stride, p.cold_gu, p.cold_gu_stride)
+                                  : nullptr;
+        const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+        Staged st;
+        stage_load(st, gW, nch);
+        stage_store(st, gW, nch, smem, 0);
+        __syncthreads();
+        const int rw = threadIdx.x / LPR_G, lr = threadIdx.x % LPR_G;
+        float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int n_mem = gi.n_mem;
+        if (valid && rw < rows) {
+            const int wb = (int)(start & 15) + rw * rb;
+            const int U = d / Fmt<HT>::UNIT;
+            // member c's activation column is its token's
+            ActView avm[DEC_MAXT];
+#pragma unroll
+            for (int c = 0; c < DEC_MAXT; ++c) {
+                const int sh = max(0, min(member(gi, c) / K, T - 1)) * abg;   // slots past n_mem are unused
+                avm[c] = ActView{av0.q + sh, av0.d32 + sh, av0.s32 + sh, av0.dK + sh, av0.bsum + sh};
+            }
+            if (gi.tier == 0) {
+                if (n_mem == 1) {           // one member: the single-column unit
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                } else {
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                }
+            } else {
+                if (n_mem == 1) {           // one member: the single-column unit
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                } else {
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c)
+#pragma unroll
+            for (int o = LPR_G / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR_G);
+        if (lr == 0 && rw < rows) {
+#pragma unroll
+            for (int c = 0; c < DEC_MAXT; ++c)
+                if (c < n_mem) st_coh(p.ygu + (int64_t)member(gi, c) * F2 + r0 + rw, acc[c]);
+        }
+        wait_vm();
+        __syncthreads();
+        arrive_flag(&p.ctl->group_count[g], NRB_G, &p.ctl->group_ready[g]);
+    }
+
+    // ---- phase 4: down (its LDS reuses the gate_up region)
+    ActView tmpd;
+    const int abd = act_layout(F, 0, &tmpd);
+    const int ad0 = p.w_lds_dn;
+    ActView avd[DEC_MAXT];
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) act_layout(F, ad0 + c * abd, &avd[c]);
+    constexpr int GCOH = GSRC == SRC_GEGLU_TANH ? SRC_GEGLU_TANH_COH : SRC_GEGLU_TABLE_COH;
+    for (int it = blockIdx.x; ok && it < ng * NRB_D; it += gridDim.x) {
+        const int g = it / NRB_D, rbi = it - g * NRB_D;
+        __syncthreads();                        // the previous item (or phase 3) is done with LDS
+        if (!wait_flag(p, &p.ctl->group_ready[g], &s_flag)) {
+            ok = false;
+            break;
+        }
+        const GroupInfo gi = s_grp[g];
+        const bool valid = gi.tier < 2;
+        const int wtype = gi.tier == 0 ? HD : CD;
+        const int r0 = rbi * ROWS_D;
+        const int rows = min(ROWS_D, d - r0);
+        const int rb = (F / blk_elems(wtype)) * blk_bytes(wtype);
+        const uint64_t start = (uint64_t)r0 * rb;
+        const uint64_t c0 = start >> 4;
+        const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
+        const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_dn, p.hot_dn_stride, p.cold_dn, p.cold_dn_stride)
+                                  : nullptr;
+        const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+        Staged st;
+        stage_load(st, gW, nch);
+        const int n_mem = gi.n_mem;
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c) {
+            if (c >= n_mem) break;
+            ActSrc src;
+            src.p = p.ygu + (int64_t)member(gi, c) * F2;
+            src.n = F;
+            quantize_act<T_Q5_0, AM, GCOH>(smem, avd[c], src, F);
+        }
+        stage_store(st, gW, nch, smem, 0);
+        __syncthreads();
+        const int rw = threadIdx.x / LPR_D, lr = threadIdx.x % LPR_D;
+        float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (valid && rw < rows) {
+            const int wb = (int)(start & 15) + rw * rb;
+            const int U = F / Fmt<HD>::UNIT;
+            if (gi.tier == 0) {
+                if (n_mem == 1) {           // one member: the single-column unit
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                } else {
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                }
+            } else {
+                if (n_mem == 1) {           // one member: the single-column unit
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                } else {
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c)
+#pragma unroll
+            for (int o = LPR_D / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR_D);
+        const float sc = !valid ? 0.0f
+                       : gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f) : (p.s_cold ? p.s_cold[gi.idx] : 1.0f);
+        if (lr == 0 && rw < rows) {
+#pragma unroll
+            for (int c = 0; c < DEC_MAXT; ++c)
+                if (c < n_mem) st_coh(p.ydn + (int64_t)member(gi, c) * d + r0 + rw, valid ? acc[c] * sc : 0.0f);
+        }
+        // combine: the last pair of a token to finish these rows sums them
+        wait_vm();
+        __syncthreads();
+        if ((int)threadIdx.x < n_mem) {
+            const int t = member(gi, threadIdx.x) / K;
+            s_lastc[threadIdx.x] = atomicAdd(&p.comb_count[t * p.n_rb_down + rbi], 1) == K - 1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < DEC_MAXT; ++c) {
+            if (c >= n_mem) break;
+            if (!s_lastc[c]) continue;
+            const int t = member(gi, c) / K;
+            const float * yt = p.ydn + (int64_t)t * K * d + r0;
+            const float * wt = s_wt + t * K;
+            for (int r = threadIdx.x; r < rows; r += WG) {
+                float o = __fmul_rn(ld_coh(yt + r), wt[0]);
+                for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(ld_coh(yt + (int64_t)k * d + r), wt[k]));
+                p.out[(int64_t)t * d + r0 + r] = o;
+            }
+        }
+    }
+
+    // ---- phase 5
+    wait_vm();
+    __syncthreads();
+    if (threadIdx.x == 0) s_flag = atomicAdd(&p.ctl->done_count, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (s_flag) {
+        for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
+        for (int i = threadIdx.x; i < DEC_PMAX; i += WG) {
+            p.ctl->group_count[i] = 0;
+            p.ctl->group_ready[i] = 0;
+        }
+        if (threadIdx.x == 0) {
+            p.ctl->route_count = 0;
+            p.ctl->route_ready = 0;
+            p.ctl->done_count = 0;
         }
     }
 }
@@ -544,6 +842,48 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
 #undef LL_DN
     }
     return hipGetLastError();
+}
+
+namespace {
+// resident workgroups of a kernel on the current device (cached per device
+// and instantiation; LDS bytes are part of the key)
+template <typename F>
+int resident_wgs(F k, int lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void *, int>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    const auto key = std::make_tuple(dev, reinterpret_cast<const void *>(k), lds);
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, WG, lds) != hipSuccess) per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+    const int n = per_cu * cus;
+    cache[key] = n;
+    return n;
+}
+}  // namespace
+
+hipError_t launch_decode_fused(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
+                               hipEvent_t * ev) {
+    if (!(hgu == T_Q4_K && cgu == T_IQ2_S && hdn == T_Q5_0 && cdn == T_IQ4_NL)) return hipErrorNotSupported;
+    const int lds = std::max(dec_lds_gate_up(p, hgu, cgu), dec_lds_down(p));
+    const int P = p.T * p.top_k;
+    const int items = P * std::max((2 * p.n_ff + 15) / 16, p.n_rb_down);
+    auto go = [&](auto k) -> hipError_t {
+        const int cap = resident_wgs(k, lds);
+        const int want = std::max(p.n_expert, items);
+        const int grid = std::min(cap, want);
+        if (cap < p.n_expert || grid < 1) return hipErrorNotSupported;   // the router needs E resident workgroups
+        launch_timed(k, dim3(grid), lds, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, p);
+        return hipGetLastError();
+    };
+    if (am == AM_CPU && gelu == SRC_GEGLU_TANH) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_CPU, SRC_GEGLU_TANH>);
+    if (am == AM_CPU) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_CPU, SRC_GEGLU_TABLE>);
+    if (gelu == SRC_GEGLU_TANH) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_Q8_1, SRC_GEGLU_TANH>);
+    return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_Q8_1, SRC_GEGLU_TABLE>);
 }
 
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s) {

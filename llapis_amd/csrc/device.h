@@ -15,9 +15,11 @@ constexpr int WG = 256;         // threads per workgroup (4 wave64)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // one 128-bit load/store
 constexpr int MAX_D_IN = 8192;  // longest activation column a workgroup quantises
 
-// Activation modes (llapis_moe.h LLAPIS_ACT_*) and activation sources.
+// Activation modes (llapis_moe.h LLAPIS_ACT_*) and activation sources.  The
+// _COH sources read their input with device-coherent loads (data written by
+// other workgroups of the same kernel).
 enum { AM_CPU = 0, AM_Q8_1 = 1 };
-enum { SRC_PLAIN = 0, SRC_GEGLU_TABLE = 1, SRC_GEGLU_TANH = 2 };
+enum { SRC_PLAIN = 0, SRC_GEGLU_TABLE = 1, SRC_GEGLU_TANH = 2, SRC_GEGLU_TABLE_COH = 3, SRC_GEGLU_TANH_COH = 4 };
 
 // --------------------------------------------------------------- LDS views
 
@@ -109,7 +111,7 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // fp16 lookup (vec.h:1414-1428): gelu evaluated at fp16(g), rounded to fp16.
 template <int SRC>
 __device__ __forceinline__ float geglu1(float g, float u) {
-    if (SRC == SRC_GEGLU_TANH) return __fmul_rn(gelu_tanh(g), u);
+    if (SRC == SRC_GEGLU_TANH || SRC == SRC_GEGLU_TANH_COH) return __fmul_rn(gelu_tanh(g), u);
     if (g <= -10.0f) return 0.0f;
     if (g >= 10.0f) return __fmul_rn(g, u);
     return __fmul_rn(round_to_half(gelu_tanh(round_to_half(g))), u);
@@ -119,6 +121,64 @@ __device__ __forceinline__ float geglu1(float g, float u) {
 
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// DPP lane moves (quad perms, row mirrors, row broadcasts): cross-lane data
+// without LDS round trips.  CTRL: 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm
+// [2,3,0,1], 0x141 row_half_mirror, 0x140 row_mirror, 0x142 row_bcast15
+// (row mask 0xA), 0x143 row_bcast31 (row mask 0xC).
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+    return __int_as_float(dpp_i<CTRL, ROWMASK>(__float_as_int(old), __float_as_int(v)));
+}
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ double dpp_d(double old, double v) {
+    const long long o = __double_as_longlong(old), x = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL, ROWMASK>((int)o, (int)x);
+    const int hi = dpp_i<CTRL, ROWMASK>((int)(o >> 32), (int)(x >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+// wave64 reductions; the result is read from lane 63 and is wave-uniform
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v, v));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1>(0.0f, v);
+    v += dpp_f<0x4E>(0.0f, v);
+    v += dpp_f<0x141>(0.0f, v);
+    v += dpp_f<0x140>(0.0f, v);
+    v += dpp_f<0x142, 0xA>(0.0f, v);
+    v += dpp_f<0x143, 0xC>(0.0f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+    v += dpp_d<0xB1>(0.0, v);
+    v += dpp_d<0x4E>(0.0, v);
+    v += dpp_d<0x141>(0.0, v);
+    v += dpp_d<0x140>(0.0, v);
+    v += dpp_d<0x142, 0xA>(0.0, v);
+    v += dpp_d<0x143, 0xC>(0.0, v);
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, 63), hi = __builtin_amdgcn_readlane((int)(b >> 32), 63);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+// sum over each row of 16 lanes, in every lane of the row
+__device__ __forceinline__ int row16_sum(int v) {
+    v += dpp_i<0xB1>(0, v);
+    v += dpp_i<0x4E>(0, v);
+    v += dpp_i<0x141>(0, v);
+    v += dpp_i<0x140>(0, v);
     return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
@@ -134,9 +194,15 @@ struct ActSrc {
     int n;             // d_in (GEGLU: n_ff; up half starts at p + n)
 };
 
+__device__ __forceinline__ float ld_coh_f(const float * p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int SRC>
 __device__ __forceinline__ float act_at(const ActSrc & s, int k) {
     if (SRC == SRC_PLAIN) return s.p[k];
+    if (SRC == SRC_GEGLU_TABLE_COH || SRC == SRC_GEGLU_TANH_COH)
+        return geglu1<SRC>(ld_coh_f(s.p + k), ld_coh_f(s.p + s.n + k));
     return geglu1<SRC>(s.p[k], s.p[s.n + k]);
 }
 
@@ -156,13 +222,13 @@ __device__ __forceinline__ void q8K_block(uint8_t * base, const ActView & L, con
         v[j] = act_at<SRC>(src, b * 256 + lane + 64 * j);
         amax = fmaxf(amax, fabsf(v[j]));
     }
-    amax = wave_max(amax);
+    amax = wave_max_dpp(amax);
     // first position holding |x| == amax: positions are lane + 64 j
     float max = 0.0f;
 #pragma unroll
     for (int j = 3; j >= 0; --j) {
         const uint64_t m = __ballot(fabsf(v[j]) == amax);
-        if (m) max = __shfl(v[j], __builtin_ctzll(m), 64);
+        if (m) max = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), (int)__builtin_ctzll(m)));
     }
     int qi[4];
     if (amax == 0.0f) {
@@ -181,8 +247,7 @@ __device__ __forceinline__ void q8K_block(uint8_t * base, const ActView & L, con
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         q[b * 256 + lane + 64 * j] = (int8_t)qi[j];
-        int s = qi[j];
-        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+        const int s = row16_sum(qi[j]);
         if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
     }
 }
@@ -242,33 +307,50 @@ __device__ __forceinline__ void quantize_act(uint8_t * base, const ActView & v, 
     else quantize_q8_32<SRC, AM>(base, v, src, n);
 }
 
-// IQ2_S tables in LDS: the codebook as bytes {0x08,0x19,0x2b} per level, and
-// for each sign byte s the negation masks {m_lo, m_hi, m_lo & 1s, m_hi & 1s}
-// with m = 0xFF in every byte whose sign bit is set.
-__device__ __forceinline__ void build_iq2s_tables(uint8_t * smem, int grid_off, int sign_off, const uint16_t * codes) {
-    uint2 * grid = reinterpret_cast<uint2 *>(smem + grid_off);
-    uint4 * sign = reinterpret_cast<uint4 *>(smem + sign_off);
-    for (int k = threadIdx.x; k < 1024; k += WG) {
-        const uint32_t c = codes[k];
+// IQ2_S tables: the codebook as bytes {0x08,0x19,0x2b} per level (from the
+// 2-bit codes), and for each sign byte s the negation masks {m_lo, m_hi,
+// m_lo & 1s, m_hi & 1s} with m = 0xFF in every byte whose sign bit is set.
+// Expanded at compile time; a workgroup copies them into LDS.
+struct Iq2sTables {
+    uint32_t grid[1024][2];
+    uint32_t sign[256][4];
+};
+constexpr uint16_t k_iq2s_codes[1024] = {
+#include "iq2s_grid.inc"
+};
+constexpr Iq2sTables make_iq2s_tables() {
+    Iq2sTables t{};
+    for (int k = 0; k < 1024; ++k) {
+        const uint32_t c = k_iq2s_codes[k];
         uint32_t lo = 0, hi = 0;
-#pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t l = (c >> (2 * i)) & 3;
             const uint32_t b = 8u + 17u * l + (l >> 1);     // 0x08, 0x19, 0x2b
             if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
         }
-        grid[k] = make_uint2(lo, hi);
+        t.grid[k][0] = lo;
+        t.grid[k][1] = hi;
     }
-    {
-        const uint32_t s = threadIdx.x;   // WG == 256 sign bytes
+    for (uint32_t s = 0; s < 256; ++s) {
         uint32_t m0 = 0, m1 = 0;
-#pragma unroll
         for (int i = 0; i < 4; ++i) {
             if ((s >> i) & 1) m0 |= 0xFFu << (8 * i);
             if ((s >> (i + 4)) & 1) m1 |= 0xFFu << (8 * i);
         }
-        sign[s] = make_uint4(m0, m1, m0 & 0x01010101u, m1 & 0x01010101u);
+        t.sign[s][0] = m0;
+        t.sign[s][1] = m1;
+        t.sign[s][2] = m0 & 0x01010101u;
+        t.sign[s][3] = m1 & 0x01010101u;
     }
+    return t;
+}
+static_assert(sizeof(Iq2sTables) == 1024 * 8 + 256 * 16, "table layout");
+
+// copy the tables (grid at grid_off, sign masks at sign_off = grid_off + 8 KB)
+__device__ __forceinline__ void copy_iq2s_tables(uint8_t * smem, int grid_off, const Iq2sTables * tab) {
+    const u32x4 * src = reinterpret_cast<const u32x4 *>(tab);
+    u32x4 * dst = reinterpret_cast<u32x4 *>(smem + grid_off);
+    for (int i = threadIdx.x; i < (int)(sizeof(Iq2sTables) / 16); i += WG) dst[i] = src[i];
 }
 
 // ------------------------------------------------------------ unit dots
@@ -342,8 +424,8 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
         if (AM == AM_CPU) {
             const float dK = reinterpret_cast<const float *>(smem + av[c].dK)[sb];
             const int * bs = reinterpret_cast<const int *>(smem + av[c].bsum) + sb * 16 + 4 * qq;
-            const int sumi = sc0 * dot1 + sc1 * dot2;
-            const int summ = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+            const int sumi = __mul24(sc0, dot1) + __mul24(sc1, dot2);
+            const int summ = __mul24(m0, bs[0] + bs[1]) + __mul24(m1, bs[2] + bs[3]);
             acc[c] += __fmul_rn(d * dK, (float)sumi) - __fmul_rn(dmin * dK, (float)summ);
         } else {
             int sq0 = 0, sq1 = 0;
@@ -353,8 +435,8 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
                 sq1 = dot4(0x01010101, (int)ahi[i], sq1);
             }
             const float * d32 = reinterpret_cast<const float *>(smem + av[c].d32) + (sb * 256 + 64 * qq) / 32;
-            const float sd = d32[0] * (float)(dot1 * sc0) + d32[1] * (float)(dot2 * sc1);
-            const float sm = d32[0] * (float)(sq0 * m0) + d32[1] * (float)(sq1 * m1);
+            const float sd = d32[0] * (float)__mul24(dot1, sc0) + d32[1] * (float)__mul24(dot2, sc1);
+            const float sm = d32[0] * (float)__mul24(sq0, m0) + d32[1] * (float)__mul24(sq1, m1);
             acc[c] += d * sd - dmin * sm;
         }
     }
@@ -406,9 +488,9 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
                 s[l >> 1] = dot4((int)g1[g], (int)a.y, s[l >> 1]);
             }
             if (AM == AM_CPU) {
-                bsum += (2 * (int)(scb & 15) + 1) * s[0] + (2 * (int)(scb >> 4) + 1) * s[1];
+                bsum += __mul24(2 * (int)(scb & 15) + 1, s[0]) + __mul24(2 * (int)(scb >> 4) + 1, s[1]);
             } else {
-                const int sumi = (s[0] * (int)(scb & 15) + s[1] * (int)(scb >> 4) + (s[0] + s[1]) / 2) / 4;
+                const int sumi = (__mul24(s[0], (int)(scb & 15)) + __mul24(s[1], (int)(scb >> 4)) + (s[0] + s[1]) / 2) / 4;
                 const float d8 = reinterpret_cast<const float *>(smem + av[c].d32)[(sb * 256 + 64 * qq + 32 * h) / 32];
                 accf += (d * d8) * (float)sumi;
             }

@@ -55,12 +55,18 @@ struct GroupInfo {
 };
 
 // control block at the start of the decode workspace (zero before first use):
-// kernel A's arrival counter and the expert groups it selected
+// arrival counters, the expert groups selected, and the error word a timed-out
+// wait of the single-kernel path sets (cleared by the host)
 struct DecCtl {
     int route_count;
     int n_groups;
-    int pad[2];
+    int done_count;
+    int error;
     GroupInfo groups[DEC_PMAX];
+    int group_count[DEC_PMAX];
+    int route_ready;            // single-kernel path: write-once flags set by the last arriver
+    int pad2[3];
+    int group_ready[DEC_PMAX];
 };
 
 struct DecParams {
@@ -88,6 +94,7 @@ struct DecParams {
     int n_rb_down;              // 32-row blocks of the down projection
     int prefetch;               // prefetch down slabs during gate_up
     int never;                  // always 0 (keeps prefetch loads from being dropped)
+    int64_t spin_limit;         // single-kernel path: wall-clock ticks a wait may take
 };
 
 int dec_act_bytes(int n);
@@ -97,6 +104,12 @@ int dec_lds_down(const DecParams & p);
 // timestamps of kernels A, B and C (ev[0..1], ev[2..3], ev[4..5])
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
                          hipStream_t s, hipEvent_t * ev);
+// The same layer in one kernel (phases hand off through arrival counters with
+// bounded waits).  Returns hipErrorNotSupported for format pairs it does not
+// instantiate or shapes it cannot keep co-resident; the caller then uses
+// launch_decode.  ev (optional): begin/end timestamps of the kernel.
+hipError_t launch_decode_fused(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
+                               hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 
 // ------------------------------------------------------------ prefill path

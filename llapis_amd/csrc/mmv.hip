@@ -22,9 +22,7 @@
 namespace llapis {
 namespace dev {
 
-__constant__ uint16_t c_iq2s_codes[1024] = {
-#include "iq2s_grid.inc"
-};
+__constant__ Iq2sTables c_iq2s_tab = make_iq2s_tables();
 
 constexpr int MAXPER = 8;   // 128-bit weight loads in flight per thread before the activation work
 
@@ -96,7 +94,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
 
     // ---- 3. activation into LDS (+ IQ2_S tables)
     const ActView av = {L.q, L.d32, L.s32, L.dK, L.bsum};
-    if (wtype == T_IQ2_S) build_iq2s_tables(smem, L.grid, L.sign, c_iq2s_codes);
+    if (wtype == T_IQ2_S) copy_iq2s_tables(smem, L.grid, &c_iq2s_tab);
     if (valid) {
         ActSrc src;
         src.p = p.act + (int64_t)col * p.act_ld;
