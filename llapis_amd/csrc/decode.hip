@@ -232,7 +232,11 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
             src.n = d;
             uint8_t * col = p.xq + (int64_t)t * p.xq_stride;
             if (AM == AM_CPU) q8K_block<SRC_PLAIN>(col, v, src, b);
-            else q8_32_step<SRC_PLAIN, AM_Q8_1>(col, v, src, d, 64 * b);
+            else {
+                const int pos = 64 * b + (threadIdx.x & 63);
+                const bool live = pos < d;
+                q8_32_put<AM_Q8_1>(col, v, live ? src.p[pos] : 0.0f, pos, live);
+            }
         }
     }
     if (!arrive_last(&p.ctl->route_count, gridDim.x, &s_last)) return;
@@ -347,7 +351,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c)
         if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride, abytes);
-    const int grid_off = align16i(a0 + min(p.T, DEC_MAXT) * abytes), sign_off = grid_off + 1024 * 8;
+    const int grid_off = align16i(a0 + min(p.T, DEC_MAXT) * abytes);
     if (wtype == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();
@@ -359,15 +363,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int U = d_in / Fmt<HT>::UNIT;
         if (gi.tier == 0) {
             if (n_mem == 1) {           // one member: the single-column unit
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off);
             }
         } else {
             if (n_mem == 1) {           // one member: the single-column unit
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off, sign_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, grid_off);
             }
         }
     }
@@ -381,6 +385,20 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             if (c < n_mem) p.ygu[(int64_t)member(gi, c) * F2 + r0 + rw] = acc[c];
     }
     if (p.never) p.ygu[threadIdx.x] = (float)sink;        // keeps the prefetch loads alive
+}
+
+// out = sum_k w_k y_k in k order (llama-graph.cpp:1812-1840), the K outputs
+// loaded together (one round trip) before the ordered sum
+constexpr int DEC_KMAX = 16;
+__device__ __forceinline__ float combine_row(const float * y, const float * w, int K, int D) {
+    float yv[DEC_KMAX];
+#pragma unroll
+    for (int k = 0; k < DEC_KMAX; ++k) yv[k] = k < K ? ld_coh(y + (int64_t)k * D) : 0.0f;
+    float o = __fmul_rn(yv[0], w[0]);
+#pragma unroll
+    for (int k = 1; k < DEC_KMAX; ++k)
+        if (k < K) o = __fadd_rn(o, __fmul_rn(yv[k], w[k]));
+    return o;
 }
 
 template <int HT, int CT, int AM, int GSRC>
@@ -433,15 +451,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int U = d_in / Fmt<HT>::UNIT;
         if (gi.tier == 0) {
             if (n_mem == 1) {           // one member: the single-column unit
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, 0, 0);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, 0);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0);
             }
         } else {
             if (n_mem == 1) {           // one member: the single-column unit
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, 0, 0);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, 0);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0, 0);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, av, n_mem, acc, 0);
             }
         }
     }
@@ -472,11 +490,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const int t = member(gi, c) / K;
         const float * yt = p.ydn + (int64_t)t * K * D + r0;
         const float * wt = p.w + t * K;
-        for (int r = threadIdx.x; r < rows; r += WG) {
-            float o = __fmul_rn(ld_coh(yt + r), wt[0]);
-            for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(ld_coh(yt + (int64_t)k * D + r), wt[k]));
-            p.out[(int64_t)t * D + r0 + r] = o;
-        }
+        for (int r = threadIdx.x; r < rows; r += WG) p.out[(int64_t)t * D + r0 + r] = combine_row(yt + r, wt, K, D);
     }
 }
 
@@ -577,7 +591,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         quantize_act<HT, AM, SRC_PLAIN>(smem, v, src, d);
         __syncthreads();
     }
-    const int grid_off = align16i(ag0 + min(T, DEC_MAXT) * abg), sign_off = grid_off + 1024 * 8;
+    const int grid_off = align16i(ag0 + min(T, DEC_MAXT) * abg);
     if (HT == T_IQ2_S || CT == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
 
     // ---- phase 2
@@ -626,15 +640,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             }
             if (gi.tier == 0) {
                 if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off);
                 } else {
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off);
                 }
             } else {
                 if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off);
                 } else {
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off, sign_off);
+                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off);
                 }
             }
         }
@@ -699,15 +713,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             const int U = F / Fmt<HD>::UNIT;
             if (gi.tier == 0) {
                 if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0);
                 } else {
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0);
                 }
             } else {
                 if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0);
                 } else {
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0, 0);
+                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0);
                 }
             }
         }
@@ -737,11 +751,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             const int t = member(gi, c) / K;
             const float * yt = p.ydn + (int64_t)t * K * d + r0;
             const float * wt = s_wt + t * K;
-            for (int r = threadIdx.x; r < rows; r += WG) {
-                float o = __fmul_rn(ld_coh(yt + r), wt[0]);
-                for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(ld_coh(yt + (int64_t)k * d + r), wt[k]));
-                p.out[(int64_t)t * d + r0 + r] = o;
-            }
+            for (int r = threadIdx.x; r < rows; r += WG) p.out[(int64_t)t * d + r0 + r] = combine_row(yt + r, wt, K, d);
         }
     }
 
@@ -783,7 +793,7 @@ int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
     ActView v;
     const int ab = act_layout(p.d_model, 0, &v);
     const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
-    return align16i(p.w_lds_gu + std::min(p.T, DEC_MAXT) * ab) + (iq2 ? 1024 * 8 + 256 * 16 : 0);
+    return align16i(p.w_lds_gu + std::min(p.T, DEC_MAXT) * ab) + (iq2 ? (int)sizeof(Iq2sTables) : 0);
 }
 
 int dec_lds_down(const DecParams & p) {

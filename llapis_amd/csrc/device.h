@@ -51,7 +51,6 @@ struct LdsLayout {
     int dK;       // float per 256 values (q8_K scale)
     int bsum;     // int per 16 values (q8_K block sums)
     int grid;     // IQ2_S codebook, 1024 x uint2
-    int sign;     // IQ2_S sign masks, 256 x uint4
     int total;
 };
 
@@ -66,8 +65,7 @@ LL_HD inline LdsLayout lds_layout(int w_bytes, int d_in, bool iq2_tables) {
     L.dK = align16(L.s32 + (d_in / 32) * 4);
     L.bsum = align16(L.dK + (d_in / 256 + 1) * 4);
     L.grid = align16(L.bsum + (d_in / 16) * 4);
-    L.sign = L.grid + (iq2_tables ? 1024 * 8 : 0);
-    L.total = L.sign + (iq2_tables ? 256 * 16 : 0);
+    L.total = L.grid + (iq2_tables ? 1024 * 8 : 0);   // the IQ2_S codebook
     return L;
 }
 
@@ -262,15 +260,12 @@ __device__ __forceinline__ void quantize_q8_K(uint8_t * base, const ActView & L,
 // q8_1 as ggml-cuda computes it (quantize.cu:5-50): d = amax/127,
 // q = roundf(x/d), s = butterfly sum of x; both stored as fp16.
 // One wave quantises the two 32-blocks starting at `at`.
-template <int SRC, int AM>
-__device__ __forceinline__ void q8_32_step(uint8_t * base, const ActView & L, const ActSrc & src, int d_in, int at) {
+template <int AM>
+__device__ __forceinline__ void q8_32_put(uint8_t * base, const ActView & L, float v, int pos, bool live) {
     const int lane = threadIdx.x & 63;
     int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
     float * d32 = reinterpret_cast<float *>(base + L.d32);
     float * s32 = reinterpret_cast<float *>(base + L.s32);
-    const int pos = at + lane;
-    const bool live = pos < d_in;          // d_in is a multiple of 32, not always of 64
-    const float v = live ? act_at<SRC>(src, pos) : 0.0f;
     float amax = fabsf(v);
     for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
     int qi;
@@ -295,9 +290,39 @@ __device__ __forceinline__ void q8_32_step(uint8_t * base, const ActView & L, co
     }
 }
 
+// One wave quantises the 64 values at at, at + WG, ... (up to Q8_BATCH
+// steps); every source load of the batch is issued before the first value is
+// used, so the batch costs one memory round trip.
+constexpr int Q8_BATCH = 4;
+
+template <int SRC>
+__device__ __forceinline__ float ld_src(const float * p) {
+    if (SRC == SRC_GEGLU_TABLE_COH || SRC == SRC_GEGLU_TANH_COH) return ld_coh_f(p);
+    return *p;
+}
+
 template <int SRC, int AM>
 __device__ __forceinline__ void quantize_q8_32(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
-    for (int at = (threadIdx.x >> 6) * 64; at < d_in; at += WG) q8_32_step<SRC, AM>(base, L, src, d_in, at);
+    const int lane = threadIdx.x & 63;
+    for (int at0 = (threadIdx.x >> 6) * 64; at0 < d_in; at0 += Q8_BATCH * WG) {
+        float g[Q8_BATCH], u[Q8_BATCH];
+#pragma unroll
+        for (int j = 0; j < Q8_BATCH; ++j) {
+            const int pos = at0 + j * WG + lane;
+            const bool live = pos < d_in;             // d_in is a multiple of 32, not always of 64
+            g[j] = live ? ld_src<SRC>(src.p + pos) : 0.0f;
+            u[j] = (SRC != SRC_PLAIN && live) ? ld_src<SRC>(src.p + src.n + pos) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < Q8_BATCH; ++j) {
+            const int at = at0 + j * WG;
+            if (at >= d_in) break;                    // wave-uniform
+            const int pos = at + lane;
+            const bool live = pos < d_in;
+            const float v = SRC == SRC_PLAIN ? g[j] : (live ? geglu1<SRC>(g[j], u[j]) : 0.0f);
+            q8_32_put<AM>(base, L, v, pos, live);
+        }
+    }
 }
 
 // Quantise an activation column into the format weight type T is dotted with.
@@ -307,13 +332,14 @@ __device__ __forceinline__ void quantize_act(uint8_t * base, const ActView & v, 
     else quantize_q8_32<SRC, AM>(base, v, src, n);
 }
 
-// IQ2_S tables: the codebook as bytes {0x08,0x19,0x2b} per level (from the
-// 2-bit codes), and for each sign byte s the negation masks {m_lo, m_hi,
-// m_lo & 1s, m_hi & 1s} with m = 0xFF in every byte whose sign bit is set.
-// Expanded at compile time; a workgroup copies them into LDS.
+// IQ2_S codebook in LDS: for each of the 1024 grid points its eight level
+// codes, one byte each (0, 1, 2 stand for the magnitudes 0x08, 0x19, 0x2b of
+// iq2s_grid, ggml-common.h:748).  Signs are applied in registers: a byte
+// selector code | 4*sign picks the signed magnitude out of the eight bytes
+// {8, 25, 43, 0, -8, -25, -43, 0} with one v_perm, so no sign table is read.
+// Expanded at compile time; a workgroup copies it into LDS.
 struct Iq2sTables {
     uint32_t grid[1024][2];
-    uint32_t sign[256][4];
 };
 constexpr uint16_t k_iq2s_codes[1024] = {
 #include "iq2s_grid.inc"
@@ -325,28 +351,28 @@ constexpr Iq2sTables make_iq2s_tables() {
         uint32_t lo = 0, hi = 0;
         for (int i = 0; i < 8; ++i) {
             const uint32_t l = (c >> (2 * i)) & 3;
-            const uint32_t b = 8u + 17u * l + (l >> 1);     // 0x08, 0x19, 0x2b
-            if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+            if (i < 4) lo |= l << (8 * i); else hi |= l << (8 * (i - 4));
         }
         t.grid[k][0] = lo;
         t.grid[k][1] = hi;
     }
-    for (uint32_t s = 0; s < 256; ++s) {
-        uint32_t m0 = 0, m1 = 0;
-        for (int i = 0; i < 4; ++i) {
-            if ((s >> i) & 1) m0 |= 0xFFu << (8 * i);
-            if ((s >> (i + 4)) & 1) m1 |= 0xFFu << (8 * i);
-        }
-        t.sign[s][0] = m0;
-        t.sign[s][1] = m1;
-        t.sign[s][2] = m0 & 0x01010101u;
-        t.sign[s][3] = m1 & 0x01010101u;
-    }
     return t;
 }
-static_assert(sizeof(Iq2sTables) == 1024 * 8 + 256 * 16, "table layout");
+static_assert(sizeof(Iq2sTables) == 1024 * 8, "table layout");
 
-// copy the tables (grid at grid_off, sign masks at sign_off = grid_off + 8 KB)
+constexpr uint32_t IQ2S_POS = 0x002B1908u, IQ2S_NEG = 0x00D5E7F8u;   // {8,25,43,0}, {-8,-25,-43,0}
+
+// four signed codebook bytes from four level codes (one per byte) and the
+// four matching sign bits (bit i of `nib` for byte i).  nib * 0x810204 (an
+// unsigned 24-bit multiply: bit 23 of the constant is set) puts
+// bit i at bits 8i+2 (and at 12 other bits, all distinct, so no carries);
+// the mask keeps bit 2 of every byte.
+__device__ __forceinline__ uint32_t iq2s_signed4(uint32_t codes, uint32_t nib) {
+    const uint32_t sel = (__umul24(nib, 0x810204u) & 0x04040404u) | codes;
+    return __builtin_amdgcn_perm(IQ2S_NEG, IQ2S_POS, sel);
+}
+
+// copy the codebook to smem + grid_off
 __device__ __forceinline__ void copy_iq2s_tables(uint8_t * smem, int grid_off, const Iq2sTables * tab) {
     const u32x4 * src = reinterpret_cast<const u32x4 *>(tab);
     u32x4 * dst = reinterpret_cast<u32x4 *>(smem + grid_off);
@@ -446,10 +472,10 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
 //   0.125 d_w dK sum_ib [(2 sc_lo + 1) s_1 + (2 sc_hi + 1) s_2]
 // IQ2_S . q8_1  (ggml-cuda/vecdotq.cuh:1061-1105): per 32-block
 //   d_w d8 ((s_1 sc_lo + s_2 sc_hi + (s_1 + s_2)/2) / 4)   (C integer division)
-// The codebook and sign masks are in LDS (tables at `grid`, `sign`).
+// The codebook is in LDS at `grid_off`; signs are applied with iq2s_signed4.
 template <int AM, int NC>
 __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
-                                          float * acc, int grid_off, int sign_off) {
+                                          float * acc, int grid_off) {
     const int sb = u >> 2, qq = u & 3;
     const int blk = wb + sb * 82;                         // 2-aligned
     const float d = h2f(lds32u(smem, blk));
@@ -458,7 +484,6 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
     const uint32_t qh2 = lds32u(smem, blk + 66 + 2 * qq);
     const uint32_t sc2 = lds32u(smem, blk + 74 + 2 * qq);
     const uint2 * grid = reinterpret_cast<const uint2 *>(smem + grid_off);
-    const uint4 * sign = reinterpret_cast<const uint4 *>(smem + sign_off);
     // signed codebook bytes of the unit's 8 groups of 8
     uint32_t g0[8], g1[8];
 #pragma unroll
@@ -466,9 +491,9 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
         const uint32_t qhb = (qh2 >> (8 * (g >> 2))) & 0xFF;
         const uint32_t idx = byte_of(qs0, qs1, g) | (((qhb >> (2 * (g & 3))) & 3) << 8);
         const uint2 gv = grid[idx];
-        const uint4 m = sign[byte_of(sg0, sg1, g)];
-        g0[g] = (gv.x ^ m.x) + m.z;
-        g1[g] = (gv.y ^ m.y) + m.w;
+        const uint32_t sw = (g < 4 ? sg0 : sg1) >> (8 * (g & 3));
+        g0[g] = iq2s_signed4(gv.x, sw & 15);
+        g1[g] = iq2s_signed4(gv.y, (sw >> 4) & 15);
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -593,9 +618,9 @@ __device__ __forceinline__ void iq4nl_unit(const uint8_t * smem, int wb, int u, 
 
 template <int T, int AM, int NC>
 __device__ __forceinline__ void unit_dot_n(const uint8_t * smem, int wb, int u, const ActView * av, int nc,
-                                           float * acc, int grid_off, int sign_off) {
+                                           float * acc, int grid_off) {
     if constexpr (T == T_Q4_K) q4k_unit<AM, NC>(smem, wb, u, av, nc, acc);
-    else if constexpr (T == T_IQ2_S) iq2s_unit<AM, NC>(smem, wb, u, av, nc, acc, grid_off, sign_off);
+    else if constexpr (T == T_IQ2_S) iq2s_unit<AM, NC>(smem, wb, u, av, nc, acc, grid_off);
     else if constexpr (T == T_Q5_0) q5_0_unit<AM, NC>(smem, wb, u, av, nc, acc);
     else iq4nl_unit<AM, NC>(smem, wb, u, av, nc, acc);
 }

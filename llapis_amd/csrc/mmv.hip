@@ -10,7 +10,7 @@
 //   3. while they are in flight, quantise the activation column into LDS in
 //      the format the reference's dot product uses (q8_K / q8_0 / q8_1),
 //      evaluating the GEGLU on the fly for the down projection, and build the
-//      IQ2_S codebook/sign tables in LDS when the tier is IQ2_S;
+//      IQ2_S codebook in LDS when the tier is IQ2_S;
 //   4. store the weight bytes to LDS, then lanes in groups of LPR dot whole
 //      units (quarter super-blocks or 32-blocks) with v_dot4_i32_i8 and
 //      reduce with cross-lane shuffles.
@@ -121,9 +121,9 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         constexpr int UNIT = Fmt<HT>::UNIT;
         const int U = p.d_in / UNIT;
         if (tier == 0) {
-            for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid, L.sign);
+            for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid);
         } else {
-            for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid, L.sign);
+            for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, &av, 1, &acc, L.grid);
         }
     }
 #pragma unroll
