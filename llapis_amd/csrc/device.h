@@ -33,9 +33,16 @@ struct ActView {
 LL_HD inline int align16i(int x) { return (x + 15) & ~15; }
 
 // layout of an n-value column placed at byte offset `at`; returns its size
+// Byte position of activation value x in the int8 region: 16 bytes of
+// padding after every 256 values.  A lane reading the 64-value unit u of a
+// 256-block starts at 64u + 16(u/4), so the 16 lanes of a row that read units
+// 0..15 hit 16 different bank groups (without the padding lanes 0, 4, 8, 12
+// would all start in bank 0).
+LL_HD constexpr int qpos(int x) { return x + ((x >> 8) << 4); }
+
 LL_HD inline int act_layout(int n, int at, ActView * v) {
     v->q = at;
-    v->d32 = align16i(at + n);
+    v->d32 = align16i(at + qpos(n));
     v->s32 = v->d32 + (n / 32) * 4;
     v->dK = align16i(v->s32 + (n / 32) * 4);
     v->bsum = align16i(v->dK + (n / 256 + 1) * 4);
@@ -60,7 +67,7 @@ LL_HD inline LdsLayout lds_layout(int w_bytes, int d_in, bool iq2_tables) {
     LdsLayout L;
     L.w = 0;
     L.q = align16(w_bytes + 16);            // +16: funnel reads may touch one dword past the end
-    L.d32 = align16(L.q + d_in + 16);
+    L.d32 = align16(L.q + qpos(d_in) + 16);
     L.s32 = align16(L.d32 + (d_in / 32) * 4);
     L.dK = align16(L.s32 + (d_in / 32) * 4);
     L.bsum = align16(L.dK + (d_in / 256 + 1) * 4);
@@ -244,7 +251,7 @@ __device__ __forceinline__ void q8K_block(uint8_t * base, const ActView & L, con
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        q[b * 256 + lane + 64 * j] = (int8_t)qi[j];
+        q[b * 272 + lane + 64 * j] = (int8_t)qi[j];        // qpos(b * 256 + lane + 64 j)
         const int s = row16_sum(qi[j]);
         if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
     }
@@ -285,7 +292,7 @@ __device__ __forceinline__ void q8_32_put(uint8_t * base, const ActView & L, flo
         if (live && (lane & 31) == 0) s32[pos >> 5] = round_to_half(s);
     }
     if (live) {
-        q[pos] = (int8_t)qi;
+        q[qpos(pos)] = (int8_t)qi;
         if ((lane & 31) == 0) d32[pos >> 5] = dstore;
     }
 }
@@ -436,7 +443,7 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (c >= nc) break;
-        const int ao = av[c].q + sb * 256 + 64 * qq;
+        const int ao = av[c].q + sb * 272 + 64 * qq;         // qpos(64 u)
         const u32x4 a0 = lds128(smem, ao), a1 = lds128(smem, ao + 16);
         const u32x4 a2 = lds128(smem, ao + 32), a3 = lds128(smem, ao + 48);
         const uint32_t alo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -498,7 +505,7 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (c >= nc) break;
-        const int ao = av[c].q + sb * 256 + 64 * qq;
+        const int ao = av[c].q + sb * 272 + 64 * qq;         // qpos(64 u)
         int bsum = 0;
         float accf = 0.0f;
 #pragma unroll
@@ -552,7 +559,8 @@ __device__ __forceinline__ void q5_0_unit(const uint8_t * smem, int wb, int u, c
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (c >= nc) break;
-        const u32x4 a0 = lds128(smem, av[c].q + u * 32), a1 = lds128(smem, av[c].q + u * 32 + 16);
+        const int ao = av[c].q + qpos(u * 32);
+        const u32x4 a0 = lds128(smem, ao), a1 = lds128(smem, ao + 16);
         const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
         int sumi = 0, suma = 0;
 #pragma unroll
@@ -602,7 +610,8 @@ __device__ __forceinline__ void iq4nl_unit(const uint8_t * smem, int wb, int u, 
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (c >= nc) break;
-        const u32x4 a0 = lds128(smem, av[c].q + u * 32), a1 = lds128(smem, av[c].q + u * 32 + 16);
+        const int ao = av[c].q + qpos(u * 32);
+        const u32x4 a0 = lds128(smem, ao), a1 = lds128(smem, ao + 16);
         const uint32_t alo[4] = {a0.x, a0.y, a0.z, a0.w}, ahi[4] = {a1.x, a1.y, a1.z, a1.w};
         int sumi = 0;
 #pragma unroll

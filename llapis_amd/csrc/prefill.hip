@@ -538,7 +538,7 @@ __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     ex = max(-100, min(100, ex));
     const float sc = ldexpf(1.0f, ex);
     for (int i = threadIdx.x; i < F / 16; i += WG)
-        reinterpret_cast<u32x4 *>(p.aq + (int64_t)q * F)[i] = reinterpret_cast<const u32x4 *>(qv)[i];
+        reinterpret_cast<u32x4 *>(p.aq + (int64_t)q * F)[i] = *reinterpret_cast<const u32x4 *>(qv + qpos(16 * i));
     for (int b = threadIdx.x; b < F / 32; b += WG) p.as[(int64_t)q * (F / 32) + b] = (_Float16)(d32[b] * sc);
     if (threadIdx.x == 0) p.ae[q] = ldexpf(1.0f, -ex);
 }
