@@ -158,6 +158,19 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// max over each half-wave (lanes 0-31, 32-63), in every lane of the half
+__device__ __forceinline__ float half_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));           // row (16-lane) max in every lane
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += dpp_f<0xB1>(0.0f, v);
     v += dpp_f<0x4E>(0.0f, v);
@@ -273,8 +286,7 @@ __device__ __forceinline__ void q8_32_put(uint8_t * base, const ActView & L, flo
     int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
     float * d32 = reinterpret_cast<float *>(base + L.d32);
     float * s32 = reinterpret_cast<float *>(base + L.s32);
-    float amax = fabsf(v);
-    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+    const float amax = half_max_dpp(fabsf(v));
     int qi;
     float dstore;
     if (AM == AM_CPU) {
