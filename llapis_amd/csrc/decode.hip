@@ -305,6 +305,33 @@ __device__ __forceinline__ void copy16(uint8_t * smem, int at, const uint8_t * s
         *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = reinterpret_cast<const u32x4 *>(src)[i];
 }
 
+// A small copy into LDS split in two: the first N chunks per thread are
+// loaded into registers (issue), stored later (land), and any rest is copied
+// in land.  Issued before the weight slab's loads, the copy's wait does not
+// wait for the slab (loads complete in issue order).
+template <int N>
+struct Early {
+    u32x4 r[N];
+    __device__ __forceinline__ void issue(const void * src, int n16) {
+        const u32x4 * g = reinterpret_cast<const u32x4 *>(src);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int i = threadIdx.x + k * WG;
+            if (i < n16) r[k] = g[i];
+        }
+    }
+    __device__ __forceinline__ void land(uint8_t * dst, const void * src, int n16) const {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const int i = threadIdx.x + k * WG;
+            if (i < n16) reinterpret_cast<u32x4 *>(dst)[i] = r[k];
+        }
+        const u32x4 * g = reinterpret_cast<const u32x4 *>(src);
+        for (int i = threadIdx.x + N * WG; i < n16; i += WG) reinterpret_cast<u32x4 *>(dst)[i] = g[i];
+    }
+};
+constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
+
 template <int HT, int CT, int AM>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -326,6 +353,21 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_gu, p.hot_gu_stride, p.cold_gu, p.cold_gu_stride)
                               : nullptr;
     const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+
+    // codebook and member columns first, then the slab
+    ActView tmp;
+    const int abytes = act_layout(d_in, 0, &tmp);
+    const int n_mem = gi.n_mem;
+    const bool iq2 = valid && wtype == T_IQ2_S;
+    Early<TAB_CHUNKS / WG> tab;
+    if (iq2) tab.issue(&c_iq2s_tab_dec, TAB_CHUNKS);
+    Early<2> col[DEC_MAXT];
+    const uint8_t * csrc[DEC_MAXT];
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) {
+        csrc[c] = p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride;
+        if (c < n_mem) col[c].issue(csrc[c], abytes / 16);
+    }
     Staged st;
     stage_load(st, gW, nch);
 
@@ -341,18 +383,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         for (int i = b0 + threadIdx.x; i < b1; i += WG) sink ^= D[i].x;
     }
 
-    ActView tmp;
-    const int abytes = act_layout(d_in, 0, &tmp);
     const int a0 = p.w_lds_gu;
     ActView av[DEC_MAXT];
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
-    const int n_mem = gi.n_mem;
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c)
-        if (c < n_mem) copy16(smem, a0 + c * abytes, p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride, abytes);
+        if (c < n_mem) col[c].land(smem + a0 + c * abytes, csrc[c], abytes / 16);
     const int grid_off = align16i(a0 + min(p.T, DEC_MAXT) * abytes);
-    if (wtype == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
+    if (iq2) tab.land(smem + grid_off, &c_iq2s_tab_dec, TAB_CHUNKS);
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();
 
@@ -422,6 +461,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_dn, p.hot_dn_stride, p.cold_dn, p.cold_dn_stride)
                               : nullptr;
     const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
+
+    // the members' gate_up rows (first batch) are loaded before the slab, so
+    // their GEGLU and quantisation overlap the slab's loads
+    const int n_mem = gi.n_mem;
+    const int at0 = (threadIdx.x >> 6) * 64;
+    ActSrc src[DEC_MAXT];
+    ActBatch ab[DEC_MAXT];
+#pragma unroll
+    for (int c = 0; c < DEC_MAXT; ++c) {
+        src[c].p = p.ygu + (int64_t)member(gi, c) * 2 * d_in;
+        src[c].n = d_in;
+        if (c < n_mem) act_batch_load<GSRC>(ab[c], src[c], d_in, at0);
+    }
     Staged st;
     stage_load(st, gW, nch);
 
@@ -432,14 +484,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     ActView av[DEC_MAXT];
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
-    const int n_mem = gi.n_mem;
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c) {
         if (c >= n_mem) break;
-        ActSrc src;
-        src.p = p.ygu + (int64_t)member(gi, c) * 2 * d_in;
-        src.n = d_in;
-        quantize_act<T_Q5_0, AM, GSRC>(smem, av[c], src, d_in);
+        if (at0 < d_in) act_batch_quant<GSRC, AM>(smem, av[c], ab[c], d_in, at0);
+        quantize_q8_32_rest<GSRC, AM>(smem, av[c], src[c], d_in);
     }
     stage_store(st, gW, nch, smem, 0);
     __syncthreads();

@@ -320,27 +320,55 @@ __device__ __forceinline__ float ld_src(const float * p) {
     return *p;
 }
 
+// One batch: the Q8_BATCH steps at0, at0 + WG, ... of one wave.  Loading is
+// separate from quantising so a caller can issue the loads early.
+struct ActBatch {
+    float g[Q8_BATCH], u[Q8_BATCH];
+};
+
+template <int SRC>
+__device__ __forceinline__ void act_batch_load(ActBatch & b, const ActSrc & src, int d_in, int at0) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < Q8_BATCH; ++j) {
+        const int pos = at0 + j * WG + lane;
+        const bool live = pos < d_in;             // d_in is a multiple of 32, not always of 64
+        b.g[j] = live ? ld_src<SRC>(src.p + pos) : 0.0f;
+        b.u[j] = (SRC != SRC_PLAIN && live) ? ld_src<SRC>(src.p + src.n + pos) : 0.0f;
+    }
+}
+
+template <int SRC, int AM>
+__device__ __forceinline__ void act_batch_quant(uint8_t * base, const ActView & L, const ActBatch & b, int d_in,
+                                                int at0) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < Q8_BATCH; ++j) {
+        const int at = at0 + j * WG;
+        if (at >= d_in) break;                    // wave-uniform
+        const int pos = at + lane;
+        const bool live = pos < d_in;
+        const float v = SRC == SRC_PLAIN ? b.g[j] : (live ? geglu1<SRC>(b.g[j], b.u[j]) : 0.0f);
+        q8_32_put<AM>(base, L, v, pos, live);
+    }
+}
+
+// the batches after the first (d_in > Q8_BATCH * WG)
+template <int SRC, int AM>
+__device__ __forceinline__ void quantize_q8_32_rest(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
+    for (int at0 = (threadIdx.x >> 6) * 64 + Q8_BATCH * WG; at0 < d_in; at0 += Q8_BATCH * WG) {
+        ActBatch b;
+        act_batch_load<SRC>(b, src, d_in, at0);
+        act_batch_quant<SRC, AM>(base, L, b, d_in, at0);
+    }
+}
+
 template <int SRC, int AM>
 __device__ __forceinline__ void quantize_q8_32(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
-    const int lane = threadIdx.x & 63;
     for (int at0 = (threadIdx.x >> 6) * 64; at0 < d_in; at0 += Q8_BATCH * WG) {
-        float g[Q8_BATCH], u[Q8_BATCH];
-#pragma unroll
-        for (int j = 0; j < Q8_BATCH; ++j) {
-            const int pos = at0 + j * WG + lane;
-            const bool live = pos < d_in;             // d_in is a multiple of 32, not always of 64
-            g[j] = live ? ld_src<SRC>(src.p + pos) : 0.0f;
-            u[j] = (SRC != SRC_PLAIN && live) ? ld_src<SRC>(src.p + src.n + pos) : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < Q8_BATCH; ++j) {
-            const int at = at0 + j * WG;
-            if (at >= d_in) break;                    // wave-uniform
-            const int pos = at + lane;
-            const bool live = pos < d_in;
-            const float v = SRC == SRC_PLAIN ? g[j] : (live ? geglu1<SRC>(g[j], u[j]) : 0.0f);
-            q8_32_put<AM>(base, L, v, pos, live);
-        }
+        ActBatch b;
+        act_batch_load<SRC>(b, src, d_in, at0);
+        act_batch_quant<SRC, AM>(base, L, b, d_in, at0);
     }
 }
 
