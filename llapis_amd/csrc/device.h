@@ -629,7 +629,8 @@ __device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx) {
     const uint32_t sel = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
     const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-    const uint32_t m = ((idx & 0x08080808u) >> 3) * 0xFFu;
+    // byte mask 0xFF where bit 3 is set: perm selector 12 gives 0x00, 13 gives 0xFF
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((idx >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
     return (hi & m) | (lo & ~m);
 }
 

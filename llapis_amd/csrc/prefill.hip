@@ -319,23 +319,36 @@ struct GuStage {
     float d8;
 };
 
-template <int HT, int CT>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
-    __shared__ __align__(16) uint8_t s_w[PF_ROWS * PF_WROW_GU];
-    __shared__ __align__(16) _Float16 s_x[PF_TOK * PF_XS];
-    __shared__ __align__(16) _Float16 s_mb[PF_TOK * 16];
-    __shared__ __align__(16) uint8_t s_grid[1024 * 16];
-    __shared__ __align__(16) uint8_t s_sign[256 * 16];
-    __shared__ float s_d8[PF_TOK];
-    __shared__ float2 s_dw[PF_ROWS];
-    __shared__ int s_tok[PF_TOK], s_pair[PF_TOK], s_poff[PF_ROWS];
+struct GuSmem {
+    uint8_t w[PF_ROWS * PF_WROW_GU];
+    _Float16 x[PF_TOK * PF_XS];
+    _Float16 mb[PF_TOK * 16];
+    uint8_t grid[1024 * 16];
+    uint8_t sign[256 * 16];
+    float d8[PF_TOK];
+    float2 dw[PF_ROWS];
+    int tok[PF_TOK], pair[PF_TOK], poff[PF_ROWS];
+};
+
+// One (tile, 128-row block) of the gate_up GEMM with NTT 32-token column
+// tiles (a tile of at most 32 pairs computes, stages and stores one).
+template <int HT, int CT, int NTT>
+__device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile & tile, GuSmem & sm) {
+    uint8_t * s_w = sm.w;
+    _Float16 * s_x = sm.x;
+    _Float16 * s_mb = sm.mb;
+    uint8_t * s_grid = sm.grid;
+    uint8_t * s_sign = sm.sign;
+    float * s_d8 = sm.d8;
+    float2 * s_dw = sm.dw;
+    int * s_tok = sm.tok;
+    int * s_pair = sm.pair;
+    int * s_poff = sm.poff;
+    constexpr int NTOK = 32 * NTT;
     static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
     static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
     static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
 
-    if ((int)blockIdx.y >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[blockIdx.y];
-    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int wtype = tile.tier == 0 ? HT : CT;
     const bool q4 = wtype == T_Q4_K;
     const int F2 = 2 * p.n_ff, NSB = p.d_model / 256, K = p.top_k;
@@ -368,12 +381,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             }
         }
 #pragma unroll
-        for (int k = 0; k < GU_XREG; ++k) {
+        for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
             const int i = tid + WG * k, j = i >> 4, c = i & 15;
             g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + (int64_t)s_tok[j] * p.d_model + 256 * s + 16 * c);
         }
-        if (tid < PF_TOK) g.d8 = p.xd[(int64_t)s_tok[tid] * NSB + s];
-        if (tid >= 64 && tid < 64 + 2 * PF_TOK) {
+        if (tid < NTOK) g.d8 = p.xd[(int64_t)s_tok[tid] * NSB + s];
+        if (tid >= 64 && tid < 64 + 2 * NTOK) {
             const int i = tid - 64;
             g.mb = *reinterpret_cast<const u32x4 *>(p.xm + ((int64_t)s_tok[i >> 1] * NSB + s) * 16 + 8 * (i & 1));
         }
@@ -391,7 +404,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             if (r < PF_ROWS) *reinterpret_cast<u32x4 *>(s_w + r * (q4 ? 144 : 96) + 16 * c) = g.w[k];
         }
 #pragma unroll
-        for (int k = 0; k < GU_XREG; ++k) {
+        for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
             const int i = tid + WG * k, j = i >> 4, c = i & 15;
             uint32_t h[8];
             i8x16_to_h(g.x[k], h);
@@ -399,8 +412,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             d[0] = u32x4{h[0], h[1], h[2], h[3]};
             d[1] = u32x4{h[4], h[5], h[6], h[7]};
         }
-        if (tid < PF_TOK) s_d8[tid] = g.d8;
-        if (tid >= 64 && tid < 64 + 2 * PF_TOK) {
+        if (tid < NTOK) s_d8[tid] = g.d8;
+        if (tid >= 64 && tid < 64 + 2 * NTOK) {
             const int i = tid - 64;
             *reinterpret_cast<u32x4 *>(s_mb + 16 * (i >> 1) + 8 * (i & 1)) = g.mb;
         }
@@ -425,7 +438,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const uint8_t * wp = s_w + s_poff[row_l];
         const _Float16 * xb0 = s_x + col * PF_XS + 8 * half;
         const _Float16 * xb1 = xb0 + 32 * PF_XS;
-        const float d80 = s_d8[col], d81 = s_d8[32 + col];
+        const float d80 = s_d8[col], d81 = NTT == 2 ? s_d8[32 + col] : 0.0f;
         if (q4) {
             // 6-bit scales and mins of this row (get_scale_min_k4, ggml-quants.c:822)
             const uint32_t q0 = *reinterpret_cast<const uint32_t *>(wp + 4);
@@ -443,7 +456,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             for (int step = 0; step < 16; ++step) {
                 const h8 a = q4k_frag(wp, step, half, sc[step >> 1]);
                 a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
+                if (NTT == 2) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
             }
             // mins: sum_j m_j * (32 hi_j + lo_j), exact
             const _Float16 f = half ? (_Float16)1.0f : (_Float16)32.0f;
@@ -452,7 +465,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             for (int j = 0; j < 8; ++j) am[j] = (_Float16)(float)mn[j] * f;
             f16v m0 = {}, m1 = {};
             m0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * col + 8 * half), m0, 0, 0, 0);
-            m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * (32 + col) + 8 * half), m1, 0, 0, 0);
+            if (NTT == 2) m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * (32 + col) + 8 * half), m1, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -460,14 +473,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                     const float2 dm = s_dw[32 * wave + 8 * i + 4 * half + jj];
                     const int v = 4 * i + jj;
                     y0[v] += __fmul_rn(d80, dm.x) * a0[v] - __fmul_rn(d80, dm.y) * m0[v];
-                    y1[v] += __fmul_rn(d81, dm.x) * a1[v] - __fmul_rn(d81, dm.y) * m1[v];
+                    if (NTT == 2) y1[v] += __fmul_rn(d81, dm.x) * a1[v] - __fmul_rn(d81, dm.y) * m1[v];
                 }
         } else {
 #pragma unroll
             for (int step = 0; step < 16; ++step) {
                 const h8 a = iq2s_frag(wp, step, half, s_grid, s_sign);
                 a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
-                a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
+                if (NTT == 2) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -476,14 +489,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                     const float dw = s_dw[32 * wave + 8 * i + 4 * half + jj].x;
                     const int v = 4 * i + jj;
                     y0[v] += __fmul_rn(dw, d80) * a0[v];
-                    y1[v] += __fmul_rn(dw, d81) * a1[v];
+                    if (NTT == 2) y1[v] += __fmul_rn(dw, d81) * a1[v];
                 }
         }
     }
     // ---- store: rows 8i + 4 half + 0..3 of this wave's 32, tokens col and 32 + col
     const float f = q4 ? 1.0f : 0.125f;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NTT; ++tt) {
         const int j = col + 32 * tt;
         if (j < tile.n) {
             const f16v & y = tt ? y1 : y0;
@@ -497,6 +510,16 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             }
         }
     }
+}
+
+template <int HT, int CT>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
+    __shared__ __align__(16) GuSmem sm;
+    if ((int)blockIdx.y >= *p.n_tiles) return;
+    const PfTile tile = p.tiles[blockIdx.y];
+    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
+    if (tile.n > 32) pf_gate_up_tile<HT, CT, 2>(p, tile, sm);
+    else pf_gate_up_tile<HT, CT, 1>(p, tile, sm);
 }
 
 // ----------------------------------------------------- down activations
@@ -563,11 +586,13 @@ __device__ __forceinline__ void scale_split(const uint32_t (&v)[4], _Float16 d, 
 
 // 8 values at offset o (0, 8, 16, 24) of a Q5_0 block at `b` (2-aligned):
 // q - 16 as exact fp16, then split-scaled by d
-__device__ __forceinline__ void q5_0_frag(const uint8_t * b, int o, h8 & hi, h8 & lo) {
-    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(b));
-    const uint32_t qh = lds32u(b, 2);
+// (the block starts at byte `b` of the 16-aligned staging buffer `sw`; dwords
+// are read at 4-aligned addresses and funnel-shifted)
+__device__ __forceinline__ void q5_0_frag(const uint8_t * sw, int b, int o, h8 & hi, h8 & lo) {
+    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(sw + b));
+    const uint32_t qh = lds32u(sw, b + 2);
     const int lw = o & 15;
-    const uint32_t w0 = lds32u(b, 6 + lw), w1 = lds32u(b, 10 + lw);
+    const uint32_t w0 = lds32u(sw, b + 6 + lw), w1 = lds32u(sw, b + 10 + lw);
     const bool hn = o >= 16;
     uint32_t x0 = (hn ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
     uint32_t x1 = (hn ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
@@ -585,10 +610,10 @@ __device__ __forceinline__ void q5_0_frag(const uint8_t * b, int o, h8 & hi, h8 
 }
 
 // IQ4_NL: kvalues[q] as exact fp16, split-scaled by d
-__device__ __forceinline__ void iq4nl_frag(const uint8_t * b, int o, h8 & hi, h8 & lo) {
-    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(b));
+__device__ __forceinline__ void iq4nl_frag(const uint8_t * sw, int b, int o, h8 & hi, h8 & lo) {
+    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(sw + b));
     const int lw = o & 15;
-    const uint32_t w0 = lds32u(b, 2 + lw), w1 = lds32u(b, 6 + lw);
+    const uint32_t w0 = lds32u(sw, b + 2 + lw), w1 = lds32u(sw, b + 6 + lw);
     const bool hn = o >= 16;
     // signed bytes + 128 -> unsigned, then (1024 + 128 + v) - 1152
     const uint32_t x0 = iq4nl_lookup((hn ? (w0 >> 4) : w0) & 0x0F0F0F0Fu) ^ 0x80808080u;
@@ -612,19 +637,25 @@ struct DnStage {
     uint32_t s[DN_XREG];
 };
 
-template <int HT, int CT>
-__global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
-    __shared__ __align__(16) uint8_t s_w[PF_ROWS * PF_WROW_DN + 16];   // +16: funnel reads past a row's end
-    __shared__ __align__(16) _Float16 s_x[PF_TOK * PF_DXS];
-    __shared__ __align__(16) _Float16 s_xl[PF_TOK * PF_DXS];
-    __shared__ int s_pair[PF_TOK], s_poff[PF_ROWS];
+struct DnSmem {
+    uint8_t w[PF_ROWS * PF_WROW_DN + 16];      // +16: funnel reads past a row's end
+    _Float16 x[PF_TOK * PF_DXS];
+    _Float16 xl[PF_TOK * PF_DXS];
+    int pair[PF_TOK], poff[PF_ROWS];
+};
+
+// One (tile, 128-row block) of the down GEMM with NTT 32-token column tiles.
+template <int HT, int CT, int NTT>
+__device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & tile, DnSmem & sm) {
+    uint8_t * s_w = sm.w;
+    _Float16 * s_x = sm.x;
+    _Float16 * s_xl = sm.xl;
+    int * s_pair = sm.pair;
+    int * s_poff = sm.poff;
     static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
     static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
     static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 2 == DN_XREG * WG, "staging shape");
 
-    if ((int)blockIdx.y >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[blockIdx.y];
-    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int wtype = tile.tier == 0 ? HT : CT;
     const int D = p.d_model, F = p.n_ff, NB = F / 32;
     const int r0 = blockIdx.x * PF_ROWS;
@@ -651,7 +682,7 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
             }
         }
 #pragma unroll
-        for (int k = 0; k < DN_XREG; ++k) {
+        for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
             const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;   // 16-value chunk c
             g.x[k] = u32x4{0, 0, 0, 0};
             g.s[k] = 0;
@@ -675,7 +706,7 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
             }
         }
 #pragma unroll
-        for (int k = 0; k < DN_XREG; ++k) {
+        for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
             const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;
             uint32_t h[8];
             i8x16_to_h(g.x[k], h);
@@ -701,27 +732,29 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
         store(c0);
         __syncthreads();
         if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
-        const uint8_t * wp = s_w + s_poff[row_l];
+        const int wp = s_poff[row_l];
         const int xo0 = col * PF_DXS + 8 * half, xo1 = xo0 + 32 * PF_DXS;
         for (int step = 0; step < 2 * cb; ++step) {
             h8 ah, al;
-            if (wtype == T_Q5_0) q5_0_frag(wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
-            else iq4nl_frag(wp + 18 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
+            if (wtype == T_Q5_0) q5_0_frag(s_w, wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
+            else iq4nl_frag(s_w, wp + 18 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
             const h8 b0h = *reinterpret_cast<const h8 *>(s_x + xo0 + 16 * step);
             const h8 b0l = *reinterpret_cast<const h8 *>(s_xl + xo0 + 16 * step);
-            const h8 b1h = *reinterpret_cast<const h8 *>(s_x + xo1 + 16 * step);
-            const h8 b1l = *reinterpret_cast<const h8 *>(s_xl + xo1 + 16 * step);
             y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0h, y0, 0, 0, 0);
             y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0l, y0, 0, 0, 0);
             y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0h, y0, 0, 0, 0);
-            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1h, y1, 0, 0, 0);
-            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1l, y1, 0, 0, 0);
-            y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1h, y1, 0, 0, 0);
+            if (NTT == 2) {
+                const h8 b1h = *reinterpret_cast<const h8 *>(s_x + xo1 + 16 * step);
+                const h8 b1l = *reinterpret_cast<const h8 *>(s_xl + xo1 + 16 * step);
+                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1h, y1, 0, 0, 0);
+                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1l, y1, 0, 0, 0);
+                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1h, y1, 0, 0, 0);
+            }
         }
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NTT; ++tt) {
         const int j = col + 32 * tt;
         if (j < tile.n) {
             const int q = s_pair[j];
@@ -737,6 +770,16 @@ __global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
             }
         }
     }
+}
+
+template <int HT, int CT>
+__global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
+    __shared__ __align__(16) DnSmem sm;
+    if ((int)blockIdx.y >= *p.n_tiles) return;
+    const PfTile tile = p.tiles[blockIdx.y];
+    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
+    if (tile.n > 32) pf_down_tile<HT, CT, 2>(p, tile, sm);
+    else pf_down_tile<HT, CT, 1>(p, tile, sm);
 }
 
 }  // namespace dev
