@@ -606,7 +606,7 @@ bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
 // prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
 // chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
 struct PfWs {
-    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, ygu, aq, as, ae, ydn, total;
+    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, ygu, ah, al, ae, ydn, parts, total;
     int Tc, max_tiles;
 };
 PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
@@ -622,14 +622,15 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     w.sorted = w.ntiles + 256;
     w.tiles = w.sorted + al256(P * 4);
     w.xq = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
-    w.xd = w.xq + al256((uint64_t)w.Tc * D);
+    w.xd = w.xq + al256((uint64_t)w.Tc * D * 2);
     w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
     w.ygu = w.xm + al256((uint64_t)w.Tc * NSB * 32);
-    w.aq = w.ygu + al256(P * 2 * F * 4);
-    w.as = w.aq + al256(P * F);
-    w.ae = w.as + al256(P * (F / 32) * 2);
+    w.ah = w.ygu + al256(P * 2 * F * 4);
+    w.al = w.ah + al256(P * F * 2);
+    w.ae = w.al + al256(P * F * 2);
     w.ydn = w.ae + al256(P * 4);
-    w.total = w.ydn + al256(P * D * 4);
+    w.parts = w.ydn + al256(P * D * 4);
+    w.total = w.parts + al256((uint64_t)router_parts_floats(w.Tc, L->n_expert) * 4);
     return w;
 }
 
@@ -760,11 +761,12 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             float * w = w_out ? w_out + (int64_t)t0 * K : (float *)(base + pw.w);
             const float * xc = x + (int64_t)t0 * L->d_model;
             const int pc = prof_slot();
+            float * parts = (float *)(base + pw.parts);
             LL_TRY(prof_record(pc, 0, 0, s));
-            LL_TRY(launch_router_logits(xc, Tc, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
+            LL_TRY(launch_router_mfma(xc, Tc, L->router_w, L->d_model, L->n_expert, parts, s));
             LL_TRY(prof_record(pc, 0, 1, s));
             LL_TRY(prof_record(pc, 1, 0, s));
-            LL_TRY(launch_topk(probs, Tc, L->n_expert, K, ids, w, s));
+            LL_TRY(launch_topk_parts(parts, L->router_b, Tc, L->n_expert, K, probs, ids, w, s));
             LL_TRY(prof_record(pc, 1, 1, s));
             PfParams p = {};
             p.d_model = L->d_model; p.n_ff = L->n_ff; p.n_expert = L->n_expert; p.top_k = K;
@@ -780,12 +782,12 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.sorted = (int32_t *)(base + pw.sorted);
             p.tiles = (PfTile *)(base + pw.tiles);
             p.max_tiles = pw.max_tiles;
-            p.xq = (int8_t *)(base + pw.xq);
+            p.xq = (_Float16 *)(base + pw.xq);
             p.xd = (float *)(base + pw.xd);
             p.xm = (_Float16 *)(base + pw.xm);
             p.ygu = (float *)(base + pw.ygu);
-            p.aq = (int8_t *)(base + pw.aq);
-            p.as = (_Float16 *)(base + pw.as);
+            p.ah = (_Float16 *)(base + pw.ah);
+            p.al = (_Float16 *)(base + pw.al);
             p.ae = (float *)(base + pw.ae);
             p.ydn = (float *)(base + pw.ydn);
             hipEvent_t ev[4] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};

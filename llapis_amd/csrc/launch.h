@@ -141,12 +141,12 @@ struct PfParams {
     int32_t * sorted;                    // [P] pair indices grouped by expert, ascending within
     PfTile * tiles;                      // [max_tiles]
     int max_tiles;
-    int8_t * xq;                         // [T][d_model] q8_K values
+    _Float16 * xq;                       // [T][d_model] q8_K values as exact fp16
     float * xd;                          // [T][d_model / 256] q8_K scales
     _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
     float * ygu;                         // [P][2 n_ff]
-    int8_t * aq;                         // [P][n_ff] q8_0 values of the down activations
-    _Float16 * as;                       // [P][n_ff / 32] q8_0 scale d8 times 2^e (exact fp16)
+    _Float16 * ah;                       // [P][n_ff] d8 q 2^e of the down activations: fp16 high part
+    _Float16 * al;                       // [P][n_ff]                                  and exact remainder
     float * ae;                          // [P] 2^-e
     float * ydn;                         // [P][d_model]
 };
@@ -159,6 +159,14 @@ hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn
 hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
                                 float * logits, hipStream_t s);
 hipError_t launch_topk(float * probs_inout, int T, int E, int K, int32_t * ids, float * w, hipStream_t s);
+// Router logits on the matrix cores (d a multiple of 256): the K-split
+// partial dot products go to `parts` (router_parts_floats(T, E) floats);
+// launch_topk_parts adds them in split order plus the bias, then selects as
+// launch_topk (probs, ids, w).
+int router_parts_floats(int T, int E);
+hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, int E, float * parts, hipStream_t s);
+hipError_t launch_topk_parts(const float * parts, const float * bias, int T, int E, int K, float * probs, int32_t * ids,
+                             float * w, hipStream_t s);
 hipError_t launch_combine(const float * y, const float * w, int T, int K, int D, float * out, hipStream_t s);
 hipError_t launch_geglu(const float * gu, int F, int n_cols, float * out, int mode, hipStream_t s);
 

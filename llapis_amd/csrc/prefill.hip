@@ -9,8 +9,9 @@
 //                  ffn_moe.cu:80-130 is the predicate).
 //   k_pf_quant_x   each token quantised once to q8_K (the CPU path's
 //                  activation format for 256-blocks) and stored as exact fp16
-//                  integers, with the per-256 scale and the per-32 sums split
-//                  into fp16-exact high and low parts.
+//                  integers (converted once, not per GEMM workgroup), with the
+//                  per-256 scale and the per-32 sums split into fp16-exact
+//                  high and low parts.
 //   k_pf_gate_up   grouped GEMM per (tile, 128-row block): weights staged raw
 //                  in LDS one super-block at a time and expanded in registers
 //                  to fp16 integers (Q4_K: q*sc <= 945; IQ2_S: grid*(2ls+1)
@@ -21,7 +22,7 @@
 //   k_pf_act       GEGLU and q8_0 quantisation of each pair's gate_up output
 //                  (bit-identical to the CPU path); d8*q (19 significant bits)
 //                  with a per-pair power-of-two range scale is stored as the
-//                  exact sum of two fp16 parts.
+//                  exact sum of two fp16 parts, ready for the MFMA operands.
 //   k_pf_down      grouped GEMM of the down projection.  Its scales are per
 //                  32-value block, so they are folded into the operands
 //                  instead of rescaling every output per block: d*q of the
@@ -73,6 +74,19 @@ __device__ __forceinline__ h2 splat(_Float16 x) { return h2{x, x}; }
 __device__ __forceinline__ void bytes_to_magic(uint32_t x, uint32_t & lo, uint32_t & hi) {
     lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
     hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+}
+
+// 16 signed bytes -> 16 exact fp16 values (8 packed dwords)
+__device__ __forceinline__ void i8x16_to_h(const u32x4 & v, uint32_t (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const h2 off = splat((_Float16)(-1152.0f));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t a, b;
+        bytes_to_magic(w[i] ^ 0x80808080u, a, b);      // 1024 + (v + 128)
+        o[2 * i] = hbits(as_h2(a) + off);
+        o[2 * i + 1] = hbits(as_h2(b) + off);
+    }
 }
 
 __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t) {
@@ -213,9 +227,13 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     }
     __syncthreads();
     if (!live) return;
-    if (lane < 16)
-        reinterpret_cast<u32x4 *>(p.xq + (int64_t)t * p.d_model + 256 * s)[lane] =
-            reinterpret_cast<const u32x4 *>(base + L.q)[lane];
+    if (lane < 16) {
+        uint32_t h[8];
+        i8x16_to_h(reinterpret_cast<const u32x4 *>(base + L.q)[lane], h);
+        u32x4 * d = reinterpret_cast<u32x4 *>(p.xq + (int64_t)t * p.d_model + 256 * s + 16 * lane);
+        d[0] = u32x4{h[0], h[1], h[2], h[3]};
+        d[1] = u32x4{h[4], h[5], h[6], h[7]};
+    }
     if (lane == 0) p.xd[(int64_t)t * NSB + s] = reinterpret_cast<const float *>(base + L.dK)[0];
     if (lane < 8) {
         const int * bs = reinterpret_cast<const int *>(base + L.bsum);
@@ -224,19 +242,6 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
         _Float16 * xm = p.xm + ((int64_t)t * NSB + s) * 16;
         xm[lane] = (_Float16)(float)hi;
         xm[8 + lane] = (_Float16)(float)lo;
-    }
-}
-
-// 16 signed bytes -> 16 exact fp16 values (8 packed dwords)
-__device__ __forceinline__ void i8x16_to_h(const u32x4 & v, uint32_t (&o)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    const h2 off = splat((_Float16)(-1152.0f));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t a, b;
-        bytes_to_magic(w[i] ^ 0x80808080u, a, b);      // 1024 + (v + 128)
-        o[2 * i] = hbits(as_h2(a) + off);
-        o[2 * i + 1] = hbits(as_h2(b) + off);
     }
 }
 
@@ -308,7 +313,7 @@ __device__ __forceinline__ int chunk_count(uint64_t ps, int len) {
 }
 
 constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (Q4_K: 128 rows x 9)
-constexpr int GU_XREG = 4;     // activation chunks per thread per super-block (64 tokens x 16)
+constexpr int GU_XREG = 8;     // fp16 activation chunks per thread per super-block (64 tokens x 32)
 
 // Registers of the next super-block in flight while the current one computes.
 struct GuStage {
@@ -347,7 +352,7 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
     constexpr int NTOK = 32 * NTT;
     static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
     static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
-    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
+    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 32 == GU_XREG * WG, "staging shape");
 
     const int wtype = tile.tier == 0 ? HT : CT;
     const bool q4 = wtype == T_Q4_K;
@@ -382,8 +387,8 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
         }
 #pragma unroll
         for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i >> 4, c = i & 15;
-            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + (int64_t)s_tok[j] * p.d_model + 256 * s + 16 * c);
+            const int i = tid + WG * k, j = i >> 5, c = i & 31;
+            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + (int64_t)s_tok[j] * p.d_model + 256 * s + 8 * c);
         }
         if (tid < NTOK) g.d8 = p.xd[(int64_t)s_tok[tid] * NSB + s];
         if (tid >= 64 && tid < 64 + 2 * NTOK) {
@@ -405,12 +410,8 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
         }
 #pragma unroll
         for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i >> 4, c = i & 15;
-            uint32_t h[8];
-            i8x16_to_h(g.x[k], h);
-            u32x4 * d = reinterpret_cast<u32x4 *>(s_x + j * PF_XS + 16 * c);
-            d[0] = u32x4{h[0], h[1], h[2], h[3]};
-            d[1] = u32x4{h[4], h[5], h[6], h[7]};
+            const int i = tid + WG * k, j = i >> 5, c = i & 31;
+            *reinterpret_cast<u32x4 *>(s_x + j * PF_XS + 8 * c) = g.x[k];
         }
         if (tid < NTOK) s_d8[tid] = g.d8;
         if (tid >= 64 && tid < 64 + 2 * NTOK) {
@@ -522,12 +523,28 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     else pf_gate_up_tile<HT, CT, 1>(p, tile, sm);
 }
 
+// exact ints (as fp16 pairs) times the block scale d: hi = fp16(d * v),
+// lo = fp16(d * v - hi) (exact: d * v has at most 11 + 8 significant bits)
+__device__ __forceinline__ void scale_split(const uint32_t (&v)[4], _Float16 d, h8 & hi, h8 & lo) {
+    const h2 m = splat(d);
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 x = as_h2(v[i]);
+        const h2 a = x * m;
+        h[i] = hbits(a);
+        l[i] = hbits(__builtin_elementwise_fma(x, m, -a));
+    }
+    hi = as_h8(h[0], h[1], h[2], h[3]);
+    lo = as_h8(l[0], l[1], l[2], l[3]);
+}
+
 // ----------------------------------------------------- down activations
 
 // One workgroup per routed pair: GEGLU + q8_0 (the CPU path's activation
-// format for 32-blocks, bit-identical).  Stored: the int8 values, the block
-// scales times a per-pair power of two 2^e (exact in fp16; 2^e puts the
-// largest |d8 q| in [2^14, 2^15)), and 2^-e.
+// format for 32-blocks, bit-identical).  Stored: d8 q times a per-pair power
+// of two 2^e (2^e puts the largest |d8 q| in [2^14, 2^15)) as the exact sum
+// of an fp16 high part and an fp16 remainder, and 2^-e.
 template <int GSRC>
 __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     __shared__ __align__(16) uint8_t scratch[6400];     // act_layout(PF_MAX_FF) = 6240 bytes
@@ -560,29 +577,26 @@ __global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
     if (amax > 0.0f) ex = 14 - ilogbf(amax);
     ex = max(-100, min(100, ex));
     const float sc = ldexpf(1.0f, ex);
-    for (int i = threadIdx.x; i < F / 16; i += WG)
-        reinterpret_cast<u32x4 *>(p.aq + (int64_t)q * F)[i] = *reinterpret_cast<const u32x4 *>(qv + qpos(16 * i));
-    for (int b = threadIdx.x; b < F / 32; b += WG) p.as[(int64_t)q * (F / 32) + b] = (_Float16)(d32[b] * sc);
+    // 16 values per thread step (within one 32-block: one scale)
+    for (int i = threadIdx.x; i < F / 16; i += WG) {
+        uint32_t h[8];
+        i8x16_to_h(*reinterpret_cast<const u32x4 *>(qv + qpos(16 * i)), h);
+        const _Float16 sv = (_Float16)(d32[i >> 1] * sc);
+        h8 hi0, lo0, hi1, lo1;
+        scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h), sv, hi0, lo0);
+        scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h + 4), sv, hi1, lo1);
+        h8 * dh = reinterpret_cast<h8 *>(p.ah + (int64_t)q * F + 16 * i);
+        h8 * dl = reinterpret_cast<h8 *>(p.al + (int64_t)q * F + 16 * i);
+        dh[0] = hi0;
+        dh[1] = hi1;
+        dl[0] = lo0;
+        dl[1] = lo1;
+    }
     if (threadIdx.x == 0) p.ae[q] = ldexpf(1.0f, -ex);
 }
 
 // ------------------------------------------------------------------ down
 
-// exact ints (as fp16 pairs) times the block scale d: hi = fp16(d * v),
-// lo = fp16(d * v - hi) (exact: d * v has at most 11 + 8 significant bits)
-__device__ __forceinline__ void scale_split(const uint32_t (&v)[4], _Float16 d, h8 & hi, h8 & lo) {
-    const h2 m = splat(d);
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const h2 x = as_h2(v[i]);
-        const h2 a = x * m;
-        h[i] = hbits(a);
-        l[i] = hbits(__builtin_elementwise_fma(x, m, -a));
-    }
-    hi = as_h8(h[0], h[1], h[2], h[3]);
-    lo = as_h8(l[0], l[1], l[2], l[3]);
-}
 
 // 8 values at offset o (0, 8, 16, 24) of a Q5_0 block at `b` (2-aligned):
 // q - 16 as exact fp16, then split-scaled by d
@@ -629,12 +643,11 @@ __device__ __forceinline__ void iq4nl_frag(const uint8_t * sw, int b, int o, h8 
 }
 
 constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
-constexpr int DN_XREG = 2;     // activation chunks per thread per down chunk (64 tokens x 8)
+constexpr int DN_XREG = 4;     // fp16 activation chunks per thread per down chunk and part (64 tokens x 16)
 
 struct DnStage {
     u32x4 w[DN_WREG];
-    u32x4 x[DN_XREG];
-    uint32_t s[DN_XREG];
+    u32x4 xh[DN_XREG], xl[DN_XREG];
 };
 
 struct DnSmem {
@@ -654,7 +667,7 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
     int * s_poff = sm.poff;
     static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
     static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
-    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 2 == DN_XREG * WG, "staging shape");
+    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 4 == DN_XREG * WG, "staging shape");
 
     const int wtype = tile.tier == 0 ? HT : CT;
     const int D = p.d_model, F = p.n_ff, NB = F / 32;
@@ -683,13 +696,13 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
         }
 #pragma unroll
         for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;   // 16-value chunk c
-            g.x[k] = u32x4{0, 0, 0, 0};
-            g.s[k] = 0;
-            if (c < 2 * cb) {
+            const int i = tid + WG * k, j = i / (4 * PF_DCB), c = i - (4 * PF_DCB) * j;   // 8-value chunk c
+            g.xh[k] = u32x4{0, 0, 0, 0};
+            g.xl[k] = u32x4{0, 0, 0, 0};
+            if (c < 4 * cb) {
                 const int64_t q = s_pair[j];
-                g.x[k] = *reinterpret_cast<const u32x4 *>(p.aq + q * F + 32 * c0 + 16 * c);
-                g.s[k] = *reinterpret_cast<const uint16_t *>(p.as + q * NB + c0 + (c >> 1));
+                g.xh[k] = *reinterpret_cast<const u32x4 *>(p.ah + q * F + 32 * c0 + 8 * c);
+                g.xl[k] = *reinterpret_cast<const u32x4 *>(p.al + q * F + 32 * c0 + 8 * c);
             }
         }
     };
@@ -707,19 +720,9 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
         }
 #pragma unroll
         for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i / (2 * PF_DCB), c = i - (2 * PF_DCB) * j;
-            uint32_t h[8];
-            i8x16_to_h(g.x[k], h);
-            const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)g.s[k]);
-            h8 hi0, lo0, hi1, lo1;
-            scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h), sv, hi0, lo0);
-            scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h + 4), sv, hi1, lo1);
-            h8 * dh = reinterpret_cast<h8 *>(s_x + j * PF_DXS + 16 * c);
-            h8 * dl = reinterpret_cast<h8 *>(s_xl + j * PF_DXS + 16 * c);
-            dh[0] = hi0;
-            dh[1] = hi1;
-            dl[0] = lo0;
-            dl[1] = lo1;
+            const int i = tid + WG * k, j = i / (4 * PF_DCB), c = i - (4 * PF_DCB) * j;
+            *reinterpret_cast<u32x4 *>(s_x + j * PF_DXS + 8 * c) = g.xh[k];
+            *reinterpret_cast<u32x4 *>(s_xl + j * PF_DXS + 8 * c) = g.xl[k];
         }
     };
 

@@ -52,20 +52,78 @@ __global__ __launch_bounds__(WG) void k_router_logits(const float * __restrict__
     }
 }
 
+// The same logits for long token batches on the matrix cores: one wave per
+// (32 tokens, 32 experts, K split); v_mfma_f32_32x32x2_f32 in fp32 (lane l
+// feeds x[row l%32][k + 8(l/32) + i] and W_r[expert l%32][same k] to the
+// i-th of eight MFMAs per 16 k).  The RSPLIT partial dot products per logit go
+// to parts[split][t][e]; k_topk adds them in split order (and the bias).
+constexpr int RSPLIT = 16;
+
+__global__ __launch_bounds__(64) void k_router_mfma(const float * __restrict__ x, int T,
+                                                    const float * __restrict__ w_r, int d, int E, int kc,
+                                                    float * __restrict__ parts) {
+    typedef float f16v __attribute__((ext_vector_type(16)));
+    const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
+    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32, sp = blockIdx.z;
+    const int k0 = sp * kc, k1 = min(d, k0 + kc);
+    const float * xr = x + (int64_t)min(t0 + r, T - 1) * d + 8 * h;
+    const float * wr = w_r + (int64_t)min(e0 + r, E - 1) * d + 8 * h;
+    f16v acc = {};
+    // 16 k per step: lane (r, h) reads 8 consecutive values (32 bytes) of its
+    // row at k + 8h, so each row's 64 bytes come in one pair of loads
+#pragma unroll 2
+    for (int k = k0; k < k1; k += 16) {
+        const float4 xa = *reinterpret_cast<const float4 *>(xr + k);
+        const float4 xb = *reinterpret_cast<const float4 *>(xr + k + 4);
+        const float4 wa = *reinterpret_cast<const float4 *>(wr + k);
+        const float4 wb = *reinterpret_cast<const float4 *>(wr + k + 4);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.w, wa.w, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.x, wb.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
+    }
+    const int e = e0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 8 * i + 4 * h + j;
+            if (t < T && e < E) parts[((int64_t)sp * T + t) * E + e] = acc[4 * i + j];
+        }
+}
+
 // In place: logits -> probabilities (ggml soft_max: exp(x - max), sum in
 // double, scaled by float(1/sum); ops.cpp:5344-5450), then top-K by
 // descending p with ties to the lower index (argsort_top_k), weights
 // p[ids] / max(sum, 6.103515625e-5) with the sum in double (sum_rows, clamp,
 // div: llama-graph.cpp:1636-1650).  One wave per token, E <= 256, K <= 16.
+// With `parts` the logits are first summed from the router's K splits.
 __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, int K,
-                                             int32_t * __restrict__ ids, float * __restrict__ w) {
+                                             int32_t * __restrict__ ids, float * __restrict__ w,
+                                             const float * __restrict__ parts, int T, const float * __restrict__ bias) {
     const int lane = threadIdx.x, t = blockIdx.x;
     float * row = probs + (int64_t)t * E;
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? row[e] : -INFINITY;
+        if (e >= E) {
+            v[j] = -INFINITY;
+        } else if (parts) {
+            float pv[RSPLIT];
+#pragma unroll
+            for (int q = 0; q < RSPLIT; ++q) pv[q] = parts[((int64_t)q * T + t) * E + e];
+            float a = pv[0];
+#pragma unroll
+            for (int q = 1; q < RSPLIT; ++q) a += pv[q];
+            v[j] = bias ? a + bias[e] : a;
+        } else {
+            v[j] = row[e];
+        }
     }
     const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     double ls = 0.0;
@@ -232,7 +290,23 @@ hipError_t launch_router_logits(const float * x, int T, const float * w_r, const
 }
 
 hipError_t launch_topk(float * probs, int T, int E, int K, int32_t * ids, float * w, hipStream_t s) {
-    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, s, probs, E, K, ids, w);
+    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, s, probs, E, K, ids, w, (const float *)nullptr, T,
+                       (const float *)nullptr);
+    return hipGetLastError();
+}
+
+int router_parts_floats(int T, int E) { return RSPLIT * T * E; }
+
+hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, int E, float * parts, hipStream_t s) {
+    if (d % (16 * RSPLIT) != 0 || T <= 0 || E <= 0) return hipErrorInvalidValue;
+    dim3 grid((T + 31) / 32, (E + 31) / 32, RSPLIT);
+    hipLaunchKernelGGL(k_router_mfma, grid, dim3(64), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
+    return hipGetLastError();
+}
+
+hipError_t launch_topk_parts(const float * parts, const float * bias, int T, int E, int K, float * probs, int32_t * ids,
+                             float * w, hipStream_t s) {
+    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, s, probs, E, K, ids, w, parts, T, bias);
     return hipGetLastError();
 }
 
