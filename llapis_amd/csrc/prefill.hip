@@ -1,9 +1,8 @@
 // prefill.hip -- the MoE layer for long token batches (prefill chunks) on
 // gfx950 matrix cores.
 //
-//   k_pf_bucket    routed pairs grouped by expert (a stable counting sort:
-//                  per-64-pair chunk ranks from wave ballots, chunk prefix
-//                  sums per expert) and cut into tiles of <= PF_TOK pairs,
+//   k_pf_bucket    routed pairs grouped by expert (a counting sort with LDS
+//                  atomics) and cut into tiles of <= PF_TOK pairs,
 //                  each tile tagged with its tier by the residency predicate
 //                  (ggml-cuda/mmid.cu:28-116 groups the same way; moert/cuda/
 //                  ffn_moe.cu:80-130 is the predicate).
@@ -95,53 +94,38 @@ __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t)
 
 // ----------------------------------------------------------------- bucket
 
-// One workgroup.  P = T * top_k <= PF_MAX_PAIRS, n_expert <= 256.
+// One workgroup.  P = T * top_k <= PF_MAX_PAIRS, n_expert <= 256.  A
+// counting sort by expert with LDS atomics: counts, an exclusive scan over
+// the experts (pair offsets and tile offsets), then each pair takes the next
+// slot of its expert.  The order of pairs inside an expert's range is not
+// fixed, and need not be: each pair's output column is computed on its own.
 __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
-    constexpr int MAXCH = PF_MAX_PAIRS / 64;
-    __shared__ uint16_t s_cc[MAXCH][257];      // per chunk, per expert (+1 column: invalid ids)
-    __shared__ int s_off[257];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int PER = PF_MAX_PAIRS / WG;
+    __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257];
     const int P = p.T * p.top_k, E = p.n_expert;
-    const int nch = (P + 63) / 64;
-    for (int i = threadIdx.x; i < nch * 257; i += WG) s_cc[i / 257][i % 257] = 0;
-    __syncthreads();
-    // pass 1: per chunk, per expert counts (leaders of equal-expert lane groups)
-    for (int c = wave; c < nch; c += WG / 64) {
-        const int q = 64 * c + lane;
-        int e = 256;                            // past-the-end lanes and invalid ids
-        if (q < P) {
-            const int v = p.ids[q];
-            e = (v >= 0 && v < E) ? v : 256;
-        }
-        uint64_t eq = ~0ull;
+    // the ids, read once with every load in flight together
+    int ev[PER];
 #pragma unroll
-        for (int b = 0; b < 9; ++b) {
-            const uint64_t m = __ballot((e >> b) & 1);
-            eq &= ((e >> b) & 1) ? m : ~m;
-        }
-        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-        const uint64_t live = __ballot(q < P);          // every lane votes (outside the branch)
-        if ((eq & below) == 0 && q < P) s_cc[c][e] = (uint16_t)__popcll(eq & live);
+    for (int k = 0; k < PER; ++k) {
+        const int q = threadIdx.x + WG * k;
+        const int v = q < P ? p.ids[q] : -1;
+        ev[k] = (v >= 0 && v < E) ? v : 256;     // 256: invalid id
+    }
+    for (int i = threadIdx.x; i < 257; i += WG) {
+        s_cnt[i] = 0;
+        s_fill[i] = 0;
     }
     __syncthreads();
-    // chunk prefix per expert; totals
-    for (int e = threadIdx.x; e < 257; e += WG) {
-        int run = 0;
-        for (int c = 0; c < nch; ++c) {
-            const int t = s_cc[c][e];
-            s_cc[c][e] = (uint16_t)run;
-            run += t;
-        }
-        s_off[e] = run;                         // count for now
-    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (threadIdx.x + WG * k < P) atomicAdd(&s_cnt[ev[k]], 1);
     __syncthreads();
     // per expert (one thread each): tier, pair offset and tile offset by
     // exclusive scans over the experts
-    __shared__ int s_nt[257];
     const int e0 = threadIdx.x;
     int n_e = 0, tier = 1, idx = e0;
     if (e0 < E) {
-        n_e = s_off[e0];
+        n_e = s_cnt[e0];
         if (p.k_slots > 0) {
             const int sl = p.exp_slot[e0];
             if (sl >= 0 && sl < p.k_slots && p.slot_state[sl] == 2 && p.slot_exp[sl] == e0) {
@@ -151,11 +135,8 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         }
     }
     const int nt_e = (n_e + PF_TOK - 1) / PF_TOK;
-    __syncthreads();
-    if (threadIdx.x < 256) {
-        s_off[threadIdx.x] = n_e;
-        s_nt[threadIdx.x] = nt_e;
-    }
+    s_off[threadIdx.x] = n_e;
+    s_nt[threadIdx.x] = nt_e;
     __syncthreads();
     // inclusive scans (Hillis-Steele over 256 entries)
     for (int o = 1; o < 256; o <<= 1) {
@@ -169,7 +150,7 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     const int pair0 = s_off[threadIdx.x] - n_e, tile0 = s_nt[threadIdx.x] - nt_e;
     const int total = s_off[255], tiles = min(s_nt[255], p.max_tiles);
     __syncthreads();
-    s_off[threadIdx.x] = pair0;                 // exclusive offsets for pass 2
+    s_off[threadIdx.x] = pair0;                 // exclusive offsets
     if (threadIdx.x == 0) {
         s_off[256] = total;                     // invalid ids are placed after every expert's pairs
         *p.n_tiles = tiles;
@@ -184,23 +165,10 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         p.tiles[tile0 + b] = t;
     }
     __syncthreads();
-    // pass 2: positions
-    for (int c = wave; c < nch; c += WG / 64) {
-        const int q = 64 * c + lane;
-        int e = 256;
-        if (q < P) {
-            const int v = p.ids[q];
-            e = (v >= 0 && v < E) ? v : 256;
-        }
-        uint64_t eq = ~0ull;
 #pragma unroll
-        for (int b = 0; b < 9; ++b) {
-            const uint64_t m = __ballot((e >> b) & 1);
-            eq &= ((e >> b) & 1) ? m : ~m;
-        }
-        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-        const int rank = __popcll(eq & below);
-        if (q < P) p.sorted[s_off[e] + s_cc[c][e] + rank] = q;
+    for (int k = 0; k < PER; ++k) {
+        const int q = threadIdx.x + WG * k;
+        if (q < P) p.sorted[s_off[ev[k]] + atomicAdd(&s_fill[ev[k]], 1)] = q;
     }
 }
 

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, 
             v[j] = row[e];
         }
     }
-    const float mx = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    const float mx = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     double ls = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -133,35 +133,27 @@ __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, 
         v[j] = e < E ? expf(v[j] - mx) : 0.0f;
         ls += (double)v[j];
     }
-    for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
+    ls = wave_sum_dpp(ls);
     const float inv = (float)(1.0 / ls);
-    bool taken[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int e = lane + 64 * j;
         v[j] = __fmul_rn(v[j], inv);
         if (e < E) row[e] = v[j];
-        taken[j] = e >= E;
+        if (e >= E) v[j] = -1.0f;            // probabilities are >= 0; a taken entry drops to -1
     }
     float sel = 0.0f;        // lane k (< K) keeps the k-th selected probability
     for (int k = 0; k < K; ++k) {
-        uint64_t key = 0;
+        const float m = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        int eb = -1;                          // the lowest index holding the maximum
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t e = lane + 64 * j;
-            const uint64_t kk = taken[j] ? 0 : (((uint64_t)__float_as_uint(v[j]) << 32) | (0xFFFFFFFFu - e)) + 1;
-            key = kk > key ? kk : key;
+            const uint64_t b = __ballot(v[j] == m);
+            if (eb < 0 && b) eb = 64 * j + __builtin_ctzll(b);
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const uint64_t other = __shfl_xor(key, o, 64);
-            key = other > key ? other : key;
-        }
-        key -= 1;
-        const uint32_t eb = 0xFFFFFFFFu - (uint32_t)key;
-        const float pb = __uint_as_float((uint32_t)(key >> 32));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) if ((uint32_t)(lane + 64 * j) == eb) taken[j] = true;
-        if (lane == k) sel = pb;
+        for (int j = 0; j < 4; ++j) if (lane + 64 * j == eb) v[j] = -1.0f;
+        if (lane == k) sel = m;
         if (lane == 0) ids[(int64_t)t * K + k] = (int32_t)eb;
     }
     double s = lane < K ? (double)sel : 0.0;
