@@ -175,11 +175,12 @@ def stage_times(wl, n):
 
 def stage_bytes(spec, n_hot, n_cold, T, pairs):
     """Algorithmic bytes per launch of the gate_up and down matvecs: the
-    distinct experts' slabs once, activations in, outputs out."""
+    distinct experts' slabs once, activations in, outputs out (the down
+    kernel also writes the combined layer output)."""
     gu_w = n_hot * spec.gu_bytes(spec.hot_gu_type) + n_cold * spec.gu_bytes(spec.cold_gu_type)
     dn_w = n_hot * spec.dn_bytes(spec.hot_dn_type) + n_cold * spec.dn_bytes(spec.cold_dn_type)
     gu = gu_w + T * spec.d_model * 4 + pairs * 2 * spec.n_ff * 4
-    dn = dn_w + pairs * 2 * spec.n_ff * 4 + pairs * spec.d_model * 4
+    dn = dn_w + pairs * 2 * spec.n_ff * 4 + pairs * spec.d_model * 4 + T * spec.d_model * 4
     return {"gate_up": gu, "down": dn}
 
 
