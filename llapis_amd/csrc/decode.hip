@@ -1,18 +1,22 @@
 // decode.hip -- the MoE layer for decode batches (1..4 tokens) in three
 // kernels on gfx950:
 //
-//   A  k_dec_route   router logits (one wave per expert, all tokens) and the
-//                    tokens' activation quantisation spread over the
-//                    workgroups; the last workgroup to finish selects the
-//                    routing (softmax, top-k with DPP wave reductions, ties to
-//                    the lower index), groups the routed pairs by expert
-//                    (decode once, dot N: the tokens that share an expert read
-//                    its slab once) and resolves each group's tier (the
-//                    residency predicate of moert/cuda/ffn_moe.cu:80-130).
-//   B  k_dec_gate_up per (expert group, 16-row block): one record read, then
-//                    the expert's gate_up rows stream through LDS with 128-bit
+//   A  k_dec_route   router logits (one workgroup per expert, all tokens) and
+//                    the tokens' activation quantisation spread over the
+//                    workgroups; for several tokens the last workgroup to
+//                    finish also selects the routing (below) and writes the
+//                    groups.
+//   B  k_dec_gate_up per (expert group, 16-row block): for one token every
+//                    workgroup selects the routing from the logits itself
+//                    (softmax, top-k with DPP wave reductions, ties to the
+//                    lower index), groups the routed pairs by expert (decode
+//                    once, dot N: the tokens that share an expert read its
+//                    slab once) and resolves each group's tier (the residency
+//                    predicate of moert/cuda/ffn_moe.cu:80-130); the first
+//                    workgroup publishes ids, weights and groups for C.  Then the
+//                    expert's gate_up rows stream through LDS with 128-bit
 //                    loads, dotted against every member token; a slice of the
-//                    same expert's down slab is prefetched into L2/MALL.
+//                    same expert's down slab can be prefetched into L2/MALL.
 //   C  k_dec_down    per (expert group, 32-row block): GEGLU and down
 //                    activation quantisation of the group's pairs in the
 //                    prologue (while the weight loads are in flight), the down
@@ -23,8 +27,8 @@
 // Hand-offs inside a kernel (A's logits, C's partial outputs) write with
 // device-scope coherent stores, wait for their completion, then count
 // arrivals with an atomic; the last arriver reads with device-scope coherent
-// loads -- no L2 writeback or invalidate.  Kernel A clears C's counters for
-// the call; B clears A's.
+// loads -- no L2 writeback or invalidate.  Whoever selects the routing (A's
+// last workgroup, or B's first) clears C's counters for the call.
 #include <hip/hip_ext.h>
 
 #include <map>
@@ -76,19 +80,28 @@ __device__ __forceinline__ const uint8_t * group_slab(int tier, int idx, const u
 // in double, scaled by float(1/sum); argsort_top_k: descending, equal
 // probabilities in index order; weights p[ids] / max(sum, 6.103515625e-5)
 // with the sum accumulated in double in id order).  E <= 256.
-__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
-                             float * s_w = nullptr) {
-    const int lane = threadIdx.x & 63;
-    float v[4];
+template <int NJ>
+__device__ __forceinline__ float vmax(const float (&v)[4]) {
+    float m = v[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 1; j < NJ; ++j) m = fmaxf(m, v[j]);
+    return m;
+}
+
+template <int NJ>
+__device__ void select_token_n(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
+                               float * s_w) {
+    const int lane = threadIdx.x & 63;
+    float v[4];                 // entries lane + 64 j, j < NJ (the rest are never read)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         v[j] = e < E ? ld_coh(logits + e) : -INFINITY;
     }
-    const float mx = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    const float mx = wave_max_dpp(vmax<NJ>(v));
     double ls = 0.0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         v[j] = e < E ? expf(v[j] - mx) : 0.0f;
         ls += (double)v[j];
@@ -96,20 +109,20 @@ __device__ void select_token(const float * logits, int E, int K, int32_t * ids, 
     ls = wave_sum_dpp(ls);
     const float inv = (float)(1.0 / ls);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = lane + 64 * j < E ? __fmul_rn(v[j], inv) : -1.0f;
+    for (int j = 0; j < NJ; ++j) v[j] = lane + 64 * j < E ? __fmul_rn(v[j], inv) : -1.0f;
     // probabilities are >= 0; a taken entry drops to -1
     float sel = 0.0f;
     double sum = 0.0;
     for (int k = 0; k < K; ++k) {
-        const float m = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        const float m = wave_max_dpp(vmax<NJ>(v));
         int e = -1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const uint64_t b = __ballot(v[j] == m);
             if (e < 0 && b) e = 64 * j + __builtin_ctzll(b);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) if (lane + 64 * j == e) v[j] = -1.0f;
+        for (int j = 0; j < NJ; ++j) if (lane + 64 * j == e) v[j] = -1.0f;
         sum += (double)m;
         if (lane == k) sel = m;
         if (lane == 0) {
@@ -123,6 +136,15 @@ __device__ void select_token(const float * logits, int E, int K, int32_t * ids, 
         if (w) w[lane] = sel / sf;
         if (s_w) s_w[lane] = sel / sf;
     }
+}
+
+// NJ = ceil(E / 64) entries per lane
+__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
+                             float * s_w = nullptr) {
+    if (E <= 64) select_token_n<1>(logits, E, K, ids, w, s_ids, s_w);
+    else if (E <= 128) select_token_n<2>(logits, E, K, ids, w, s_ids, s_w);
+    else if (E <= 192) select_token_n<3>(logits, E, K, ids, w, s_ids, s_w);
+    else select_token_n<4>(logits, E, K, ids, w, s_ids, s_w);
 }
 
 // Expert groups of the call from the routed ids in LDS (one wave): pairs that
@@ -209,11 +231,14 @@ __device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 6
     }
 }
 
-template <int AM>
+// SEL: the last workgroup to finish also selects the routing and writes the
+// groups (used for several tokens; for one token every gate_up workgroup
+// selects it itself, which takes the selection off the critical path).
+template <int AM, bool SEL>
 __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
+    __shared__ float s_part[DEC_MAXT][WG / 64];
     __shared__ int s_last;
     __shared__ int s_ids[DEC_PMAX];
-    __shared__ float s_part[DEC_MAXT][WG / 64];
     const int wave = threadIdx.x >> 6;
     const int gw = blockIdx.x * (WG / 64) + wave;          // wave id in the grid
     const int nw = gridDim.x * (WG / 64);
@@ -239,11 +264,12 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
             }
         }
     }
+    if (!SEL) return;
     if (!arrive_last(&p.ctl->route_count, gridDim.x, &s_last)) return;
-
     // ---- last workgroup: selection and groups
     if (wave < T) select_token(p.logits + (int64_t)wave * E, E, K, p.ids + wave * K, p.w + wave * K, s_ids + wave * K);
     for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
+    if (threadIdx.x == 0) p.ctl->route_count = 0;        // every workgroup has arrived
     __syncthreads();
     if (wave == 0) build_groups(p, s_ids, p.ctl->groups, &p.ctl->n_groups);
 }
@@ -254,9 +280,7 @@ __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
 // emptied; a tier other than 0/1 or an index outside its pool makes the group
 // invalid (tier 2: its members contribute zeros, their combine still counts).
 // The record and the count are read together (one round trip).
-__device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
-    GroupInfo gi = p.ctl->groups[g];
-    const int ng = p.ctl->n_groups;
+__device__ __forceinline__ GroupInfo validate_group(const DecParams & p, GroupInfo gi, int ng, int g) {
     const int P = p.T * p.top_k;
     bool ok = g < ng;
     gi.n_mem = max(0, min(gi.n_mem, min(p.T, DEC_MAXT)));
@@ -271,6 +295,9 @@ __device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
         gi.idx = 0;
     }
     return gi;
+}
+__device__ __forceinline__ GroupInfo load_group(const DecParams & p, int g) {
+    return validate_group(p, p.ctl->groups[g], p.ctl->n_groups, g);
 }
 
 // ---------------------------------------------------------------- B / C
@@ -332,14 +359,47 @@ struct Early {
 };
 constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
 
-template <int HT, int CT, int AM>
+template <int HT, int CT, int AM, bool SEL>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
     static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
+    __shared__ int s_ids[DEC_PMAX];
+    __shared__ GroupInfo s_grp[DEC_PMAX];
+    __shared__ int s_ng;
     const int g = blockIdx.y;
-    if (blockIdx.x == 0 && g == 0 && threadIdx.x == 0) p.ctl->route_count = 0;   // A is complete
-    const GroupInfo gi = load_group(p, g);
+    const int wave = threadIdx.x >> 6, T = p.T, K = p.top_k, E = p.n_expert;
+    // IQ2_S codebook loads first: they depend on nothing; with the routing
+    // selected here (one token) the member column is token 0's, so its loads
+    // go out before the selection too
+    Early<TAB_CHUNKS / WG> tab;
+    if (HT == T_IQ2_S || CT == T_IQ2_S) tab.issue(&c_iq2s_tab_dec, TAB_CHUNKS);
+    ActView tmp;
+    const int abytes = act_layout(p.d_model, 0, &tmp);
+    Early<2> col[DEC_MAXT];
+    if (SEL) col[0].issue(p.xq, abytes / 16);
+    GroupInfo gi;
+    if (SEL) {
+        // the routing: every workgroup selects it from the logits (identical
+        // results); the first one publishes ids, weights and groups for the
+        // down kernel and clears the combine counters
+        const bool first = blockIdx.x == 0 && g == 0;
+        if (wave < T)
+            select_token(p.logits + (int64_t)wave * E, E, K, first ? p.ids + wave * K : nullptr,
+                         first ? p.w + wave * K : nullptr, s_ids + wave * K);
+        __syncthreads();
+        if (wave == 0) build_groups(p, s_ids, s_grp, &s_ng);
+        __syncthreads();
+        const int ng = s_ng;
+        if (first) {
+            for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
+            for (int i = threadIdx.x; i < ng; i += WG) p.ctl->groups[i] = s_grp[i];
+            if (threadIdx.x == 0) p.ctl->n_groups = ng;
+        }
+        gi = validate_group(p, s_grp[min(g, DEC_PMAX - 1)], ng, g);
+    } else {
+        gi = load_group(p, g);              // written by A's last workgroup
+    }
     if (gi.n_mem == 0) return;
     const int F2 = 2 * p.n_ff, d_in = p.d_model;
     const bool valid = gi.tier < 2;
@@ -354,19 +414,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
                               : nullptr;
     const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
 
-    // codebook and member columns first, then the slab
-    ActView tmp;
-    const int abytes = act_layout(d_in, 0, &tmp);
+    // member columns first, then the slab
     const int n_mem = gi.n_mem;
     const bool iq2 = valid && wtype == T_IQ2_S;
-    Early<TAB_CHUNKS / WG> tab;
-    if (iq2) tab.issue(&c_iq2s_tab_dec, TAB_CHUNKS);
-    Early<2> col[DEC_MAXT];
     const uint8_t * csrc[DEC_MAXT];
 #pragma unroll
     for (int c = 0; c < DEC_MAXT; ++c) {
         csrc[c] = p.xq + (int64_t)(member(gi, c) / p.top_k) * p.xq_stride;
-        if (c < n_mem) col[c].issue(csrc[c], abytes / 16);
+        if (c < n_mem && !(SEL && c == 0)) col[c].issue(csrc[c], abytes / 16);
     }
     Staged st;
     stage_load(st, gW, nch);
@@ -870,8 +925,15 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     {
         const int per_tok = am == AM_CPU ? p.d_model / 256 : (p.d_model + 63) / 64;
         dim3 grid(std::max(p.n_expert, (p.T * per_tok + 3) / 4));
-        if (am == AM_CPU) launch_timed(k_dec_route<AM_CPU>, grid, 0, s, e[0], e[1], p);
-        else launch_timed(k_dec_route<AM_Q8_1>, grid, 0, s, e[0], e[1], p);
+        // one token: selection in every gate_up workgroup; more: in A
+        const bool sel_a = p.T > 1;
+        if (am == AM_CPU) {
+            if (sel_a) launch_timed(k_dec_route<AM_CPU, true>, grid, 0, s, e[0], e[1], p);
+            else launch_timed(k_dec_route<AM_CPU, false>, grid, 0, s, e[0], e[1], p);
+        } else {
+            if (sel_a) launch_timed(k_dec_route<AM_Q8_1, true>, grid, 0, s, e[0], e[1], p);
+            else launch_timed(k_dec_route<AM_Q8_1, false>, grid, 0, s, e[0], e[1], p);
+        }
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
@@ -879,7 +941,10 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         dim3 grid((2 * p.n_ff + 15) / 16, P);
         const int lds = dec_lds_gate_up(p, hgu, cgu);
 #define LL_GU(A, B, M) \
-        if (hgu == A && cgu == B && am == M) launch_timed(k_dec_gate_up<A, B, M>, grid, lds, s, e[2], e[3], p); else
+        if (hgu == A && cgu == B && am == M) { \
+            if (p.T > 1) launch_timed(k_dec_gate_up<A, B, M, false>, grid, lds, s, e[2], e[3], p); \
+            else launch_timed(k_dec_gate_up<A, B, M, true>, grid, lds, s, e[2], e[3], p); \
+        } else
 #define LL_GU2(A, B) LL_GU(A, B, AM_CPU) LL_GU(A, B, AM_Q8_1)
         LL_GU2(T_Q4_K, T_IQ2_S) LL_GU2(T_Q4_K, T_Q4_K) LL_GU2(T_IQ2_S, T_IQ2_S) LL_GU2(T_IQ2_S, T_Q4_K)
         return hipErrorInvalidValue;

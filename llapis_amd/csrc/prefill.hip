@@ -31,6 +31,8 @@
 // The combine is the generic k_combine.
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "device.h"
 #include "launch.h"
 
@@ -49,7 +51,9 @@ constexpr int PF_XS = 256 + 8;            // halfs per staged activation row of 
 constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
 constexpr int PF_DXS = PF_DCB * 32 + 8;   // halfs per staged activation row of down (padded)
 constexpr int PF_WROW_GU = 144;           // LDS bytes per weight row and super-block (Q4_K 144, IQ2_S <= 96)
-constexpr int PF_WROW_DN = 112;           // LDS bytes per weight row and down chunk (<= 4 * 22 + 14)
+constexpr int PF_WROW_DN = 112;           // staged bytes per weight row and down chunk (<= 4 * 22 + 14)
+constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows: 30 dwords, so the 32 rows a half-wave
+                                          // reads at one offset fall in 32 different bank pairs
 
 __device__ __forceinline__ uint32_t hbits(h2 v) {
     uint32_t u;
@@ -619,7 +623,7 @@ struct DnStage {
 };
 
 struct DnSmem {
-    uint8_t w[PF_ROWS * PF_WROW_DN + 16];      // +16: funnel reads past a row's end
+    uint8_t w[PF_ROWS * PF_WPITCH_DN + 16];    // +16: funnel reads past a row's end
     _Float16 x[PF_TOK * PF_DXS];
     _Float16 xl[PF_TOK * PF_DXS];
     int pair[PF_TOK], poff[PF_ROWS];
@@ -679,10 +683,12 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
         for (int k = 0; k < DN_WREG; ++k) {
             const int i = tid + WG * k, r = i / WCH, c = i - WCH * (i / WCH);
             if (r < PF_ROWS) {
-                *reinterpret_cast<u32x4 *>(s_w + r * PF_WROW_DN + 16 * c) = g.w[k];
+                uint2 * d = reinterpret_cast<uint2 *>(s_w + r * PF_WPITCH_DN + 16 * c);   // 8-aligned
+                d[0] = make_uint2(g.w[k].x, g.w[k].y);
+                d[1] = make_uint2(g.w[k].z, g.w[k].w);
                 if (c == 0) {
                     const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rb + (uint64_t)c0 * bs;
-                    s_poff[r] = r * PF_WROW_DN + (int)(ps & 15);
+                    s_poff[r] = r * PF_WPITCH_DN + (int)(ps & 15);
                 }
             }
         }
@@ -705,9 +711,10 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
         if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
         const int wp = s_poff[row_l];
         const int xo0 = col * PF_DXS + 8 * half, xo1 = xo0 + 32 * PF_DXS;
-        for (int step = 0; step < 2 * cb; ++step) {
+        // one 16-value step: weight fragment hi/lo, three MFMAs per token tile
+        auto step_fn = [&](auto wt, int step) {
             h8 ah, al;
-            if (wtype == T_Q5_0) q5_0_frag(s_w, wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
+            if constexpr (decltype(wt)::value == T_Q5_0) q5_0_frag(s_w, wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
             else iq4nl_frag(s_w, wp + 18 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
             const h8 b0h = *reinterpret_cast<const h8 *>(s_x + xo0 + 16 * step);
             const h8 b0l = *reinterpret_cast<const h8 *>(s_xl + xo0 + 16 * step);
@@ -721,7 +728,19 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
                 y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1l, y1, 0, 0, 0);
                 y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1h, y1, 0, 0, 0);
             }
-        }
+        };
+        // the weight format is uniform per tile: one branch per chunk, and
+        // whole chunks run fully unrolled
+        auto chunk = [&](auto wt) {
+            if (cb == PF_DCB) {
+#pragma unroll
+                for (int step = 0; step < 2 * PF_DCB; ++step) step_fn(wt, step);
+            } else {
+                for (int step = 0; step < 2 * cb; ++step) step_fn(wt, step);
+            }
+        };
+        if (wtype == T_Q5_0) chunk(std::integral_constant<int, T_Q5_0>{});
+        else chunk(std::integral_constant<int, T_IQ4_NL>{});
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
