@@ -344,42 +344,53 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
     if (!q4) build_iq2s_f16_tables(s_grid, s_sign);
     __syncthreads();
 
+    // per-thread staging geometry, fixed for the whole K loop (no divisions
+    // or token lookups per super-block)
+    uint32_t wrow[GU_WREG];      // byte offset of the chunk's row in the slab (row * rb); ~0u: no row
+    uint32_t wdst[GU_WREG];      // LDS offset of the chunk | chunk index << 16
+#pragma unroll
+    for (int k = 0; k < GU_WREG; ++k) {
+        const int i = tid + WG * k;
+        const int r = i / nwc, c = i - nwc * r;
+        wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)min(r0 + r, F2 - 1) * rb) : ~0u;
+        wdst[k] = (uint32_t)(r * (q4 ? 144 : 96) + 16 * c) | ((uint32_t)c << 16);
+    }
+    uint32_t xsrc[GU_XREG];      // element offset of the chunk's token row and column
+#pragma unroll
+    for (int k = 0; k < GU_XREG; ++k) {
+        const int i = tid + WG * k, j = i >> 5, c = i & 31;
+        xsrc[k] = (uint32_t)(s_tok[j] * p.d_model + 8 * c);
+    }
+    const int tok_s = tid < NTOK ? s_tok[tid] * NSB : 0;
+    const int tok_m = (tid >= 64 && tid < 64 + 2 * NTOK) ? (s_tok[(tid - 64) >> 1] * NSB) * 16 + 8 * ((tid - 64) & 1) : 0;
+    const uint32_t drow = tid >= WG - PF_ROWS ? (uint32_t)((uint64_t)min(r0 + tid - (WG - PF_ROWS), F2 - 1) * rb) : 0u;
+
     GuStage g;
     auto fetch = [&](int s) {
 #pragma unroll
         for (int k = 0; k < GU_WREG; ++k) {
-            const int i = tid + WG * k;
-            const int r = i / nwc, c = i - nwc * (i / nwc);
             g.w[k] = u32x4{0, 0, 0, 0};
-            if (r < PF_ROWS) {
-                const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+            if (wrow[k] != ~0u) {
+                const uint32_t ps = wrow[k] + (uint32_t)(bb * s);
+                const int c = (int)(wdst[k] >> 16);
                 if (q4 || c < chunk_count(ps, 82))
-                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
+                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~15u) + 16 * c);
             }
         }
 #pragma unroll
-        for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i >> 5, c = i & 31;
-            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + (int64_t)s_tok[j] * p.d_model + 256 * s + 8 * c);
-        }
-        if (tid < NTOK) g.d8 = p.xd[(int64_t)s_tok[tid] * NSB + s];
-        if (tid >= 64 && tid < 64 + 2 * NTOK) {
-            const int i = tid - 64;
-            g.mb = *reinterpret_cast<const u32x4 *>(p.xm + ((int64_t)s_tok[i >> 1] * NSB + s) * 16 + 8 * (i & 1));
-        }
+        for (int k = 0; k < GU_XREG * NTT / 2; ++k)
+            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + xsrc[k] + 256 * s);
+        if (tid < NTOK) g.d8 = p.xd[tok_s + s];
+        if (tid >= 64 && tid < 64 + 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
         if (tid >= WG - PF_ROWS) {
-            const int r = tid - (WG - PF_ROWS);
-            const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+            const uint32_t ps = drow + (uint32_t)(bb * s);
             g.dw = q4 ? *reinterpret_cast<const uint32_t *>(W + ps) : *reinterpret_cast<const uint16_t *>(W + ps);
         }
     };
     auto store = [&](int s) {
 #pragma unroll
-        for (int k = 0; k < GU_WREG; ++k) {
-            const int i = tid + WG * k;
-            const int r = i / nwc, c = i - nwc * (i / nwc);
-            if (r < PF_ROWS) *reinterpret_cast<u32x4 *>(s_w + r * (q4 ? 144 : 96) + 16 * c) = g.w[k];
-        }
+        for (int k = 0; k < GU_WREG; ++k)
+            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(s_w + (wdst[k] & 0xFFFF)) = g.w[k];
 #pragma unroll
         for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
             const int i = tid + WG * k, j = i >> 5, c = i & 31;
@@ -392,7 +403,7 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
         }
         if (tid >= WG - PF_ROWS) {
             const int r = tid - (WG - PF_ROWS);
-            const uint64_t ps = (uint64_t)min(r0 + r, F2 - 1) * rb + (uint64_t)bb * s;
+            const uint32_t ps = drow + (uint32_t)(bb * s);
             s_dw[r] = make_float2(h2f(g.dw & 0xFFFF), q4 ? h2f(g.dw >> 16) : 0.0f);
             s_poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
         }
