@@ -52,31 +52,49 @@ __global__ __launch_bounds__(WG) void k_router_logits(const float * __restrict__
     }
 }
 
-// The same logits for long token batches on the matrix cores: one wave per
-// (32 tokens, 32 experts, K split); v_mfma_f32_32x32x2_f32 in fp32 (lane l
-// feeds x[row l%32][k + 8(l/32) + i] and W_r[expert l%32][same k] to the
-// i-th of eight MFMAs per 16 k).  The RSPLIT partial dot products per logit go
-// to parts[split][t][e]; k_topk adds them in split order (and the bias).
+// The same logits for long token batches on the matrix cores: one 256-thread
+// workgroup per (64 tokens, 64 experts, K split), each wave a 32 x 32 tile on
+// v_mfma_f32_32x32x2_f32 in fp32.  16-k slices of x and W_r are loaded with
+// one coalesced 16-byte load per thread each (4 threads per 64-byte row
+// piece), staged in LDS (double-buffered, rows padded to 20 floats so the 16
+// rows a half-wave reads fall in different banks), and lane l feeds
+// x[row l%32][k + 8(l/32) + i] and W_r[expert l%32][same k] to the i-th of
+// eight MFMAs per slice.  The RSPLIT partial dot products per logit go to
+// parts[split][t][e]; k_topk adds them in split order (and the bias).
 constexpr int RSPLIT = 16;
+constexpr int RT = 64, RK = 16, RPAD = 20;
 
-__global__ __launch_bounds__(64) void k_router_mfma(const float * __restrict__ x, int T,
+__global__ __launch_bounds__(WG) void k_router_mfma(const float * __restrict__ x, int T,
                                                     const float * __restrict__ w_r, int d, int E, int kc,
                                                     float * __restrict__ parts) {
     typedef float f16v __attribute__((ext_vector_type(16)));
-    const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
-    const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32, sp = blockIdx.z;
+    __shared__ __align__(16) float s_x[2][RT * RPAD], s_w[2][RT * RPAD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 31, h = lane >> 5;
+    const int t0 = blockIdx.x * RT, e0 = blockIdx.y * RT, sp = blockIdx.z;
     const int k0 = sp * kc, k1 = min(d, k0 + kc);
-    const float * xr = x + (int64_t)min(t0 + r, T - 1) * d + 8 * h;
-    const float * wr = w_r + (int64_t)min(e0 + r, E - 1) * d + 8 * h;
+    // loader: thread -> (row tid / 4, 4 floats at 4 (tid % 4))
+    const int lr = tid >> 2, lc = 4 * (tid & 3);
+    const float * xs = x + (int64_t)min(t0 + lr, T - 1) * d + lc;
+    const float * ws = w_r + (int64_t)min(e0 + lr, E - 1) * d + lc;
+    // compute: wave -> tokens 32 (wave >> 1), experts 32 (wave & 1)
+    const int xo = (32 * (wave >> 1) + r) * RPAD + 8 * h, wo = (32 * (wave & 1) + r) * RPAD + 8 * h;
     f16v acc = {};
-    // 16 k per step: lane (r, h) reads 8 consecutive values (32 bytes) of its
-    // row at k + 8h, so each row's 64 bytes come in one pair of loads
-#pragma unroll 2
-    for (int k = k0; k < k1; k += 16) {
-        const float4 xa = *reinterpret_cast<const float4 *>(xr + k);
-        const float4 xb = *reinterpret_cast<const float4 *>(xr + k + 4);
-        const float4 wa = *reinterpret_cast<const float4 *>(wr + k);
-        const float4 wb = *reinterpret_cast<const float4 *>(wr + k + 4);
+    float4 gx = *reinterpret_cast<const float4 *>(xs + k0);
+    float4 gw = *reinterpret_cast<const float4 *>(ws + k0);
+    int buf = 0;
+    for (int k = k0; k < k1; k += RK) {
+        *reinterpret_cast<float4 *>(&s_x[buf][lr * RPAD + lc]) = gx;
+        *reinterpret_cast<float4 *>(&s_w[buf][lr * RPAD + lc]) = gw;
+        __syncthreads();
+        if (k + RK < k1) {
+            gx = *reinterpret_cast<const float4 *>(xs + k + RK);
+            gw = *reinterpret_cast<const float4 *>(ws + k + RK);
+        }
+        const float4 xa = *reinterpret_cast<const float4 *>(&s_x[buf][xo]);
+        const float4 xb = *reinterpret_cast<const float4 *>(&s_x[buf][xo + 4]);
+        const float4 wa = *reinterpret_cast<const float4 *>(&s_w[buf][wo]);
+        const float4 wb = *reinterpret_cast<const float4 *>(&s_w[buf][wo + 4]);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
@@ -85,13 +103,14 @@ __global__ __launch_bounds__(64) void k_router_mfma(const float * __restrict__ x
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
+        buf ^= 1;
     }
-    const int e = e0 + r;
+    const int e = e0 + 32 * (wave & 1) + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int t = t0 + 8 * i + 4 * h + j;
+            const int t = t0 + 32 * (wave >> 1) + 8 * i + 4 * h + j;
             if (t < T && e < E) parts[((int64_t)sp * T + t) * E + e] = acc[4 * i + j];
         }
 }
@@ -291,8 +310,8 @@ int router_parts_floats(int T, int E) { return RSPLIT * T * E; }
 
 hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, int E, float * parts, hipStream_t s) {
     if (d % (16 * RSPLIT) != 0 || T <= 0 || E <= 0) return hipErrorInvalidValue;
-    dim3 grid((T + 31) / 32, (E + 31) / 32, RSPLIT);
-    hipLaunchKernelGGL(k_router_mfma, grid, dim3(64), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
+    dim3 grid((T + RT - 1) / RT, (E + RT - 1) / RT, RSPLIT);
+    hipLaunchKernelGGL(k_router_mfma, grid, dim3(WG), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
     return hipGetLastError();
 }
 
