@@ -256,6 +256,128 @@ def measured_traffic(workload, kernel):
         return None
 
 
+class Stack:
+    """The 30-layer stack: per layer its own fp32 router (seeded per layer),
+    its own Zipf(1.1) hot set of 57 experts (a per-layer permutation) and a
+    router bias that puts ~85 % of the picks on them; the expert slabs are
+    per-layer device copies of the one quantised layer (distinct memory, the
+    same bytes).  Attention is omitted: each layer is h += moe(rms_norm(h)),
+    the MoE input normalised as the model's is (without the norm the
+    residual stream grows until q8 scales overflow fp16)."""
+
+    def __init__(self, la, torch, full, spec, n_layers, dev):
+        self.la, self.torch, self.spec = la, torch, spec
+        gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+        cold_gu = torch.from_numpy(full.cold_gu).to(dev)
+        cold_dn = torch.from_numpy(full.cold_dn).to(dev)
+        self.layers, self.descs, self.bytes_tok, self.hot_frac = [], [], 0.0, []
+        import copy
+        from llapis_amd.moe import seed_for
+        for il in range(n_layers):
+            prior, hot = la.zipf_hot_set(spec.n_expert, 57, 1000 + il)
+            lay = copy.copy(full)
+            lay.router_w = la.synth_normal(seed_for(2000 + il, 0, 0), spec.n_expert * spec.d_model,
+                                           0.0, 0.02).reshape(spec.n_expert, spec.d_model)
+            lay.hot_gu = np.concatenate([full.hot_gu[e * gb:(e + 1) * gb] for e in hot])
+            lay.hot_dn = np.concatenate([full.hot_dn[e * db:(e + 1) * db] for e in hot])
+            lay.residency = la.Residency.from_hot(spec.n_expert, hot)
+            bias, frac = la.tune_router_bias(lay.router_w, prior, hot, 0.85, 3000 + il)
+            lay.router_b = bias
+            self.hot_frac.append(frac)
+            lay.cold_gu = lay.cold_dn = None          # the shared cold pools are cloned on the device
+            d = la.DeviceLayer(lay, dev)
+            d.cold_gu, d.cold_dn = cold_gu.clone(), cold_dn.clone()
+            lay.hot_gu = lay.hot_dn = None            # host copies no longer needed
+            self.layers.append(d)
+            self.descs.append(d.desc())
+        self.fn = la.lib().llapis_moe_ffn
+
+    def run(self, h, xn, out, ws, stream, T, moe=True):
+        """h [T, d_model] (the residual stream) is updated in place through
+        every layer; xn and out are scratch.  moe=False runs only the glue
+        (norm and add) to time it on its own."""
+        torch = self.torch
+        sp = self.spec
+        ids = torch.empty(T, sp.top_k, dtype=torch.int32, device=h.device)
+        w = torch.empty(T, sp.top_k, device=h.device)
+        for d in self.descs:
+            xn.copy_(torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6))
+            if moe:
+                rc = self.fn(C.byref(d), xn.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                             ws.data_ptr(), ws.numel(), stream)
+                if rc != 0:
+                    raise RuntimeError(self.la.lib().llapis_last_error().decode())
+            h.add_(out)
+
+
+def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_tokens=11200):
+    t0 = time.time()
+    st = Stack(la, torch, full, spec, n_layers, dev)
+    log(f"[stack] {n_layers} layers ready in {time.time() - t0:.1f} s (hot share of picks "
+        f"{np.mean(st.hot_frac):.2f})")
+    s = torch.cuda.current_stream()
+    res = {"layers": n_layers}
+    for T, steps, name in ((1, decode_steps, "decode"), (prefill_tokens, 2, "prefill")):
+        need = int(la.lib().llapis_moe_ffn_workspace_size(C.byref(st.descs[0]), T))
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        h0 = torch.from_numpy(la.synth_normal(4000 + T, T * spec.d_model).reshape(T, spec.d_model)).to(dev)
+        h, xn, out = h0.clone(), torch.empty_like(h0), torch.zeros_like(h0)
+
+        def timed(moe):
+            # one pass (the reset of h included) captured as a HIP graph for
+            # the decode token; the long prefill pass is launched eagerly
+            cs = torch.cuda.Stream()
+            with torch.cuda.stream(cs):
+                h.copy_(h0)
+                st.run(h, xn, out, ws, cs.cuda_stream, T, moe)     # warm-up pass
+            torch.cuda.synchronize()
+            g = None
+            if T == 1:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=cs):
+                    h.copy_(h0)
+                    st.run(h, xn, out, ws, cs.cuda_stream, T, moe)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(steps):
+                if g is not None:
+                    g.replay()
+                else:
+                    h.copy_(h0)
+                    st.run(h, xn, out, ws, s.cuda_stream, T, moe)
+            e1.record(s)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / steps
+
+        ms = timed(True)
+        assert torch.isfinite(h).all().item(), "non-finite residual stream"
+        out.zero_()
+        glue = timed(False)
+        moe_ms = max(ms - glue, 1e-9)
+        ops = T * spec.top_k * OPS_PER_PAIR * n_layers
+        r = {"tokens": T, "ms_per_pass": ms, "glue_ms_per_pass": glue, "moe_ms_per_pass": moe_ms,
+             "tok_per_s": T * 1e3 / ms, "moe_tok_per_s": T * 1e3 / moe_ms,
+             "moe_us_per_layer": moe_ms * 1e3 / n_layers, "moe_int8_tops": ops / (moe_ms * 1e-3) / 1e12}
+        if T == 1:
+            # bytes: each layer's 8 routed experts (mixed tiers, ~85 % hot) once + router
+            per = spec.gu_bytes(spec.hot_gu_type) + spec.dn_bytes(spec.hot_dn_type)
+            per_c = spec.gu_bytes(spec.cold_gu_type) + spec.dn_bytes(spec.cold_dn_type)
+            b = n_layers * (8 * (0.85 * per + 0.15 * per_c) + spec.n_expert * spec.d_model * 4)
+            r["moe_hbm_gbs_est"] = b / (moe_ms * 1e-3) / 1e9
+            r["moe_hbm_frac_est"] = r["moe_hbm_gbs_est"] / HBM_PEAK_GBS
+        res[name] = r
+        log(f"[stack {name}] {T} token(s) x {n_layers} layers: {ms:.3f} ms per pass ({glue:.3f} ms of it the "
+            f"norm/add glue); MoE {r['moe_us_per_layer']:.1f} us per layer, {r['moe_tok_per_s']:.0f} tok/s"
+            + (f", ~{r['moe_hbm_gbs_est']:.0f} GB/s" if T == 1 else f", {r['moe_int8_tops']:.1f} int8 TOP/s"))
+        del ws, h, h0, xn, out
+    del st
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(host_layer, T, budget_s=12.0):
     """The reference's ggml CPU graph (oracle/_ref) on a bounded sample."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -292,7 +414,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill", help="comma list of iq2s,q4k,dual,prefill")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack",
+                    help="comma list of iq2s,q4k,dual,prefill,stack")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
@@ -328,7 +451,7 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = "q4k" in cfgs or "dual" in cfgs or "prefill" in cfgs
+    need_hot = "q4k" in cfgs or "dual" in cfgs or "prefill" in cfgs or "stack" in cfgs
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -356,7 +479,10 @@ def main():
             results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
 
-    head = results.get("iq2s") or next(iter(results.values()))
+    if "stack" in cfgs:
+        results["stack"] = run_stack(la, torch, full, spec, dev)
+
+    head = results.get("iq2s") or next(iter(v for v in results.values() if "tok_per_s" in v))
     workload = "decode_all_iq2s_1tok" if "iq2s" in results else None
     roof = {"bound": "hbm", "achieved": head["dominant_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": head["dominant_gbs"] / HBM_PEAK_GBS,
