@@ -148,11 +148,15 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
 
 /* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
- * (default 1), key 1 = down-slab prefetch during gate_up (default 0),
+ * (default 1), key 1 = gate_up kernel touches the down slabs ahead of the
+ * down kernel (default 0: no gain measured),
  * key 2 = MFMA prefill path for > 4 tokens (default 1), key 3 = the decode
  * path as one kernel (default 0: three kernels, faster on MI355X today),
- * key 4 = the bound of one wait of that kernel in microseconds (default
- * 50000). */
+ * key 4 = the bound of one wait of the kernels that wait (the one-kernel
+ * path and the fused gate_up+down kernel) in microseconds (default 50000),
+ * key 5 = gate_up and down as one kernel in the three-kernel path, for one
+ * token and the Q4_K/IQ2_S + Q5_0/IQ4_NL formats (default 0: measured
+ * slower than the two kernels on MI355X today). */
 void llapis_set_tuning(int32_t key, int32_t value);
 
 /* Waits for `stream`, then reports whether a call on this workspace since

@@ -529,7 +529,7 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefetch{0}, g_prefill{1}, g_fused{0};
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_fused{0}, g_fuse_bc{0}, g_prefetch_dn{0};
 std::atomic<int64_t> g_spin_us{50000};        // bound of one wait in the single-kernel decode path
 
 // wall-clock ticks per microsecond of the current device (cached per device)
@@ -551,8 +551,8 @@ int64_t wall_ticks_per_us() {
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
 uint64_t dec_ctl_bytes(const llapis_moe_layer * L) {
-    const int n_rb = (L->d_model + 31) / 32;
-    return al256(sizeof(DecCtl)) + al256((uint64_t)DEC_MAXT * n_rb * 4);
+    const int n_rb = (L->d_model + 31) / 32, n_rb_gu = (2 * L->n_ff + 15) / 16;
+    return al256(sizeof(DecCtl)) + al256((uint64_t)DEC_MAXT * n_rb * 4) + al256((uint64_t)DEC_PMAX * n_rb_gu * 4);
 }
 
 // generic path (any T): probs, ids, w, y_gu, y_dn -- after the decode path's
@@ -575,7 +575,7 @@ FfnWs ffn_ws(const llapis_moe_layer * L, int32_t T) {
 
 // decode path (T <= DEC_MAXT): control block first (zero before first use)
 struct DecWs {
-    uint64_t ctl, comb, logits, ids, w, xq, ygu, aq, ydn, total, ctl_bytes;
+    uint64_t ctl, comb, gu_done, logits, ids, w, xq, ygu, aq, ydn, total, ctl_bytes;
     int64_t xq_stride, aq_stride;
     int n_rb;
 };
@@ -587,6 +587,7 @@ DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
     w.aq_stride = dec_act_bytes(L->n_ff);
     w.ctl = 0;
     w.comb = al256(sizeof(DecCtl));
+    w.gu_done = w.comb + al256((uint64_t)DEC_MAXT * w.n_rb * 4);
     w.ctl_bytes = dec_ctl_bytes(L);
     w.logits = w.ctl_bytes;
     w.ids = w.logits + al256((uint64_t)T * L->n_expert * 4);
@@ -600,7 +601,8 @@ DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
 }
 
 bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
-    return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && (L->d_model % 4) == 0;
+    return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && L->k_slots <= 256 &&
+           (L->d_model % 4) == 0;
 }
 
 // prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
@@ -643,10 +645,11 @@ bool prefill_eligible(const llapis_moe_layer * L, int32_t T) {
 
 void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
-    if (key == 1) g_prefetch = value != 0;
+    if (key == 1) g_prefetch_dn = value != 0;
     if (key == 2) g_prefill = value != 0;
     if (key == 3) g_fused = value != 0;
     if (key == 4) g_spin_us = std::max(0, value);
+    if (key == 5) g_fuse_bc = value != 0;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
@@ -714,6 +717,11 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.s_hot = L->s_hot; p.s_cold = L->s_cold;
         p.ctl = reinterpret_cast<DecCtl *>(base + dw.ctl);
         p.comb_count = reinterpret_cast<int *>(base + dw.comb);
+        p.gu_done = reinterpret_cast<int *>(base + dw.gu_done);
+        p.hot_dn_type = L->hot_dn_type;
+        p.cold_dn_type = L->cold_dn_type;
+        p.prefetch_dn = g_prefetch_dn.load();
+        p.never = 0;
         p.logits = reinterpret_cast<float *>(base + dw.logits);
         p.ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + dw.ids);
         p.w = w_out ? w_out : reinterpret_cast<float *>(base + dw.w);
@@ -727,13 +735,11 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.w_lds_gu = dev::align16(16 * rbg + 32);
         p.w_lds_dn = dev::align16(32 * rbd + 32);
         p.n_rb_down = dw.n_rb;
-        p.prefetch = g_prefetch.load();
-        p.never = 0;
         if (dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) <= 65536 && dec_lds_down(p) <= 65536) {
             const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+            p.spin_limit = g_spin_us.load() * wall_ticks_per_us();
             if (g_fused.load()) {
-                p.spin_limit = g_spin_us.load() * wall_ticks_per_us();
                 // the single kernel's time is reported as the gate_up stage
                 hipEvent_t evf[2] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1)};
                 const hipError_t e = launch_decode_fused(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type,
@@ -745,7 +751,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             hipEvent_t ev[6] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0),
                                 prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
-                                 src, s, pc >= 0 ? ev : nullptr));
+                                 src, g_fuse_bc.load() != 0, s, pc >= 0 ? ev : nullptr));
             return 0;
         }
     }

@@ -82,6 +82,7 @@ struct DecParams {
     const float * s_hot; const float * s_cold;
     DecCtl * ctl;
     int * comb_count;           // [DEC_MAXT][n_rb_down]
+    int * gu_done;              // [DEC_PMAX][gate_up row blocks]: fused gate_up+down, item done flags
     float * logits;             // [T][n_expert]
     int32_t * ids;              // [T][top_k]
     float * w;                  // [T][top_k]
@@ -92,18 +93,22 @@ struct DecParams {
     float * out;                // [T][d_model]
     int w_lds_gu, w_lds_dn;     // LDS bytes for staged weights
     int n_rb_down;              // 32-row blocks of the down projection
-    int prefetch;               // prefetch down slabs during gate_up
-    int never;                  // always 0 (keeps prefetch loads from being dropped)
+    int hot_dn_type, cold_dn_type;   // the down pools' formats
+    int prefetch_dn;            // gate_up items touch their down item's slab (into L2/MALL) for the down kernel
+    int never;                  // always 0: keeps the touch loads from being dropped
     int64_t spin_limit;         // single-kernel path: wall-clock ticks a wait may take
 };
 
 int dec_act_bytes(int n);
 int dec_lds_gate_up(const DecParams & p, int ht, int ct);
 int dec_lds_down(const DecParams & p);
-// ev (optional, profiling): 6 events that receive the begin and end
-// timestamps of kernels A, B and C (ev[0..1], ev[2..3], ev[4..5])
+// fuse_bc: gate_up and down as one kernel where the formats are the standard
+// pair (Q4_K/IQ2_S gate_up, Q5_0/IQ4_NL down) and every workgroup can be
+// resident; otherwise (or false) as two.  ev (optional, profiling): 6 events
+// that receive the begin and end timestamps of the router kernel, gate_up
+// (or the fused kernel) and down (ev[0..1], ev[2..3], ev[4..5]).
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
-                         hipStream_t s, hipEvent_t * ev);
+                         bool fuse_bc, hipStream_t s, hipEvent_t * ev);
 // The same layer in one kernel (phases hand off through arrival counters with
 // bounded waits).  Returns hipErrorNotSupported for format pairs it does not
 // instantiate or shapes it cannot keep co-resident; the caller then uses

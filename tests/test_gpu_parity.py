@@ -219,10 +219,10 @@ def test_island_fires_match_layer(gpu, oracle):
 @pytest.mark.parametrize("T,n_hot", [(1, 0), (1, 16), (2, 7), (4, 9), (4, 0)])
 @pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
 def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode):
-    """The decode path -- as one kernel, and as three kernels with and without
-    the down-slab prefetch (expert groups, fused GEGLU quantisation,
-    last-arrival combine) -- against the generic per-pair path, over several
-    calls on one workspace."""
+    """The decode path -- as one kernel, as three kernels (expert groups,
+    fused GEGLU quantisation, last-arrival combine), and with gate_up and down
+    fused (one token) -- against the generic per-pair path, over several calls
+    on one workspace."""
     torch = torch_mod()
     say(f"decode vs generic T={T} hot={n_hot} act={act_mode}")
     spec = FULL16
@@ -231,11 +231,11 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode):
     lib = la.lib()
     outs = {}
     try:
-        for name, dec, fused, pf in (("generic", 0, 0, 0), ("fused", 1, 1, 0), ("three", 1, 0, 0),
-                                     ("three_pf", 1, 0, 1)):
+        for name, dec, fused, fbc in (("generic", 0, 0, 0), ("fused", 1, 1, 0), ("three", 1, 0, 0),
+                                      ("three_fused_bc", 1, 0, 1)):
             lib.llapis_set_tuning(0, dec)
             lib.llapis_set_tuning(3, fused)
-            lib.llapis_set_tuning(1, pf)
+            lib.llapis_set_tuning(5, fbc)
             res = []
             for rep in range(3):
                 x = tokens(300 + rep, T, spec.d_model)
@@ -246,8 +246,8 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode):
     finally:
         lib.llapis_set_tuning(0, 1)
         lib.llapis_set_tuning(3, 0)
-        lib.llapis_set_tuning(1, 0)
-    for name in ("fused", "three", "three_pf"):
+        lib.llapis_set_tuning(5, 0)
+    for name in ("fused", "three", "three_fused_bc"):
         for (o, i, w), (og, ig, wg) in zip(outs[name], outs["generic"]):
             assert np.array_equal(i, ig)
             assert np.allclose(w, wg, rtol=1e-6, atol=0)
@@ -328,19 +328,21 @@ def test_layer_vs_reference_golden(gpu, tag, sfx, path):
     assert err <= 1e-3
 
 
-@pytest.mark.parametrize("T,fused", [(1, 0), (4, 0), (1, 1), (4, 1), (6, 0)])
-def test_graph_replays_match_eager(gpu, T, fused):
+@pytest.mark.parametrize("T,fused,fused_bc", [(1, 0, 0), (4, 0, 0), (1, 1, 0), (4, 1, 0), (6, 0, 0), (1, 0, 1)])
+def test_graph_replays_match_eager(gpu, T, fused, fused_bc):
     """Three layer calls captured in one HIP graph: every replay, with eager
     calls on the same workspace between replays, reproduces the eager
-    results exactly (the workspace's counters are reset by the kernels
-    themselves, never by memset nodes)."""
+    results exactly (the workspace's counters and flags are reset by the
+    kernels themselves, never by memset nodes)."""
     torch = torch_mod()
-    say(f"graph replays T={T} fused={fused}")
+    say(f"graph replays T={T} fused={fused} fused_bc={fused_bc}")
     la.lib().llapis_set_tuning(3, fused)
+    la.lib().llapis_set_tuning(5, fused_bc)
     try:
         _graph_replays(gpu, T)
     finally:
         la.lib().llapis_set_tuning(3, 0)
+        la.lib().llapis_set_tuning(5, 0)
 
 
 def _graph_replays(gpu, T):
