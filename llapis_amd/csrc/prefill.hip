@@ -219,18 +219,26 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
 
 // -------------------------------------------------------------- gate_up
 
+// The (multiplier, offset) pair of Q4_K sub-block j with 6-bit scale sc, as
+// packed fp16 splats: sub-blocks come as the low nibbles (j even: (1024 + q)
+// sc - 1024 sc) or the high nibbles (j odd: (1024 + 16 q) sc/16 - 64 sc) of a
+// 32-byte run, both exact.  Computed once per super-block and row.
+__device__ __forceinline__ void q4k_scale(int sc, int j, h2 & m, h2 & o) {
+    const _Float16 scf = (_Float16)(float)sc;
+    const bool hi = (j & 1) != 0;
+    m = splat(hi ? scf * (_Float16)0.0625f : scf);
+    o = splat(hi ? scf * (_Float16)(-64.0f) : scf * (_Float16)(-1024.0f));
+}
+
 // A fragment of lane (row, half) for k-step `step` (16 values) of a Q4_K
-// super-block piece at `w`: 8 values q*sc as exact fp16.
-__device__ __forceinline__ h8 q4k_frag(const uint8_t * w, int step, int half, int sc) {
+// super-block piece at `w`: 8 values q*sc as exact fp16, (m, o) from
+// q4k_scale for sub-block step / 2.
+__device__ __forceinline__ h8 q4k_frag(const uint8_t * w, int step, int half, h2 m, h2 o) {
     const int off = 16 + 32 * (step >> 2) + 16 * (step & 1) + 8 * half;
     const uint2 v = *reinterpret_cast<const uint2 *>(w + off);
     const bool hi = (step & 2) != 0;
     const uint32_t x0 = hi ? (v.x & 0xF0F0F0F0u) : (v.x & 0x0F0F0F0Fu);
     const uint32_t x1 = hi ? (v.y & 0xF0F0F0F0u) : (v.y & 0x0F0F0F0Fu);
-    // lo: (1024 + q) sc - 1024 sc;  hi: (1024 + 16 q) sc/16 - 64 sc  (exact)
-    const _Float16 scf = (_Float16)(float)sc;
-    const h2 m = splat(hi ? scf * (_Float16)0.0625f : scf);
-    const h2 o = splat(hi ? scf * (_Float16)(-64.0f) : scf * (_Float16)(-1024.0f));
     uint32_t a, b, c, d;
     bytes_to_magic(x0, a, b);
     bytes_to_magic(x1, c, d);
@@ -436,9 +444,12 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
                 sc[j + 4] = ((q2 >> (8 * j)) & 15) | (((q0 >> (8 * j + 6)) & 3) << 4);
                 mn[j + 4] = ((q2 >> (8 * j + 4)) & 15) | (((q1 >> (8 * j + 6)) & 3) << 4);
             }
+            h2 qm[8], qo[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q4k_scale(sc[j], j, qm[j], qo[j]);
 #pragma unroll
             for (int step = 0; step < 16; ++step) {
-                const h8 a = q4k_frag(wp, step, half, sc[step >> 1]);
+                const h8 a = q4k_frag(wp, step, half, qm[step >> 1], qo[step >> 1]);
                 a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
                 if (NTT == 2) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
             }
