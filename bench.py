@@ -245,6 +245,31 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     return res
 
 
+def copy_ceiling(torch, dev, nbytes, reps=400):
+    """GB/s that a plain device-to-device copy moving `nbytes` per launch (half
+    read, half written) reaches, rotated over >= 512 MB of buffers so the MALL
+    does not hold them: what any kernel of this size can expect, launch and
+    ramp included."""
+    half = max(1 << 20, int(nbytes) // 2)
+    n = max(2, (512 << 20) // half + 1)
+    src = [torch.empty(half, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n)]
+    dst = [torch.empty(half, dtype=torch.uint8, device=dev) for _ in range(n)]
+    s = torch.cuda.current_stream()
+    for i in range(n):
+        dst[i].copy_(src[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(reps):
+        dst[i % n].copy_(src[i % n])
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * half / (ms * 1e-3) / 1e9
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes committed under profiles/ (scaled by a plain copy's
@@ -489,6 +514,11 @@ def main():
             "traffic": measured_traffic(workload, head["dominant_kernel"]),
             "kernel": head["dominant_kernel"], "algo_bytes_per_launch": head["dominant_bytes"],
             "avg_launch_ms": head["stage_ms"][head["dominant"]]}
+    ceil = copy_ceiling(torch, dev, head["dominant_bytes"])
+    roof["copy_ceiling_gbs_at_size"] = ceil
+    roof["frac_of_copy_ceiling"] = head["dominant_gbs"] / ceil
+    log(f"copy of the same {head['dominant_bytes'] / 1e6:.1f} MB per launch: {ceil:.0f} GB/s "
+        f"({100 * ceil / HBM_PEAK_GBS:.0f} % of peak); dominant kernel at {100 * head['dominant_gbs'] / ceil:.0f} % of it")
     cpu = None
     if not args.no_cpu_baseline and "iq2s" in cfgs:
         try:
