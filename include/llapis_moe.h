@@ -130,6 +130,14 @@ typedef struct llapis_moe_layer {
     const int32_t * slot_state;    /* [k_slots] */
     const float * s_hot;           /* [k_slots] down scale, or NULL */
     const float * s_cold;          /* [n_expert] down scale, or NULL */
+    /* Routing counters (replaces the island's, ffn_moe.cu:123-128, for this
+     * entry point), or NULL: every call adds, with device atomics, its routed
+     * pairs per expert to route_counts[n_expert] and its hot pairs and other
+     * pairs to route_hits[0] and [1] (route_hits may be NULL).  The caller
+     * owns, zeroes and reads them (e.g. a row of the moert_cuda_route_counts
+     * layout, fetched at refresh points into moert_policy_add_external_counts). */
+    int32_t * route_counts;
+    int32_t * route_hits;
 } llapis_moe_layer;
 
 /* Device scratch the layer needs for n_tokens (bytes). */
@@ -146,6 +154,63 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
 
 /* Zero the control block of a fused-layer workspace (a kernel on `stream`). */
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
+
+/* ------------------------------------------------------ promotion engine
+ *
+ * Replaces the transfer engine and the memmgr's promotion for a hot slab in
+ * HBM (src/moe_xfer.hpp:55-110 start/submit/flush/take_done/
+ * promotions_in_flight/wait_idle/stats; moert/memmgr.h:147-158
+ * moert_memmgr_promote): a promotion copies every page group of expert e of
+ * layer il from its promotion source into hot slot `slot`.  Mechanism only,
+ * as the reference's: the policy decides and marks the slot FILLING
+ * (moert/policy.h:95-104, stream_expert returning 2), the host submits, and
+ * applies each completion with moert_policy_complete_fill (ok) or
+ * moert_policy_abort_fill (failed), then publishes the layer's mirrors.
+ *
+ * Ordering contract (the reference's submit/flush split): submitted jobs stay
+ * pending until llapis_xfer_flush(after_stream), which starts their copies on
+ * the engine's own stream only after all work already queued on
+ * after_stream -- so publish the mirrors that mark the slots FILLING (and
+ * queue every fire that may still read the old experts) before flushing.
+ * Each job is one copy kernel of copy_wgs workgroups over its page groups
+ * (device sources; copy_wgs 0, or a pinned host source: hipMemcpyAsync). */
+#define LLAPIS_XFER_MAX_GROUPS 4
+typedef struct llapis_xfer llapis_xfer;
+typedef struct llapis_xfer_done {
+    int32_t il, e, slot;
+    int32_t ok;                    /* 1 copied, 0 a copy failed */
+} llapis_xfer_done;
+typedef struct llapis_xfer_stats {
+    long long submitted, completed, failed;
+    long long max_queue;           /* most jobs issued by one flush */
+    long long bytes;               /* bytes of the copies issued */
+    long long wait_idle_calls;
+    double    wait_idle_ms;
+} llapis_xfer_stats;
+/* NULL on bad geometry (llapis_xfer_last_error says why). */
+llapis_xfer * llapis_xfer_create(int32_t n_layers, int32_t n_expert, int32_t k_slots, int32_t copy_wgs);
+/* Waits for the copies in flight, then frees the engine. */
+void          llapis_xfer_free(llapis_xfer * x);
+const char *  llapis_xfer_last_error(void);
+/* Page group `group` (< LLAPIS_XFER_MAX_GROUPS) of layer il -- one group per
+ * (kind, weight|scale) as the memmgr's page groups (memmgr.h:120-135): expert
+ * e's bytes_per_expert bytes at src + e * src_stride go to
+ * slab + slot * bytes_per_expert.  slab: device memory; src: device memory or
+ * pinned host memory.  0 ok, -1 refused. */
+int32_t llapis_xfer_set_group(llapis_xfer * x, int32_t il, int32_t group, void * slab, const void * src,
+                              uint64_t src_stride, uint64_t bytes_per_expert);
+/* Queue a promotion (pending until flush).  0 ok, -1 out of range. */
+int32_t llapis_xfer_submit(llapis_xfer * x, int32_t il, int32_t e, int32_t slot);
+/* Issue every pending job, ordered after the work queued on after_stream. */
+int32_t llapis_xfer_flush(llapis_xfer * x, void * after_stream);
+/* Move up to max_out finished jobs, oldest first, into out; non-blocking.
+ * Returns how many were moved (-1 on a null argument). */
+int32_t llapis_xfer_take_done(llapis_xfer * x, llapis_xfer_done * out, int32_t max_out);
+/* Jobs pending or with copies in flight (not yet taken). */
+int64_t llapis_xfer_in_flight(llapis_xfer * x);
+/* Flush, then block until every copy issued has landed. */
+int32_t llapis_xfer_wait_idle(llapis_xfer * x, void * after_stream);
+void    llapis_xfer_get_stats(llapis_xfer * x, llapis_xfer_stats * out);
 
 /* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
  * (default 1), key 1 = gate_up kernel touches the down slabs ahead of the

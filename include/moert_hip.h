@@ -192,15 +192,26 @@ typedef struct moert_cuda_stats {
 } moert_cuda_stats;
 void moert_cuda_stats_get(moert_cuda_stats * out);
 
-/* Batch transport (cuda.h:255-262): init/async refuse (0), mark/poll return
- * -1; publish_h2d performs its n copies synchronously and returns 1. */
+/* Replaces the batch transport (cuda.h:246-262, ffn_moe.cu:521-690).
+ * init: a side stream of default priority; sm_blocks > 0 copies device
+ * sources with a copy kernel of that many workgroups (else hipMemcpyAsync),
+ * sm_ring_mib sizes the pinned ring for small pageable sources (>= 1 MiB),
+ * sm_stage_threads is ignored.  async: issue one copy now (device or pinned
+ * source in place; a pageable source <= 4 KiB staged; a larger pageable
+ * source refused: 0, the caller copies it itself).  mark: an event after the
+ * copies issued so far, returns its id (0, 1, ...); poll: the highest id
+ * whose copies landed (-1 before any; wait_all synchronises first).  mark and
+ * poll return -1 before init.  publish_h2d: n copies from pageable views,
+ * staged through pinned memory, landed before it returns.  Thread-safe. */
 int32_t moert_cuda_dir_init(int32_t sm_blocks, int32_t sm_ring_mib, int32_t sm_stage_threads);
 int32_t moert_cuda_dir_async(void * dst_dev, const void * src, uint64_t nbytes);
 int64_t moert_cuda_dir_mark(void);
 int64_t moert_cuda_dir_poll(int32_t wait_all);
 int32_t moert_cuda_publish_h2d(int32_t n, void * const * dsts, const void * const * srcs, const uint64_t * sizes);
 
-/* Replaces moert_cuda_dir_stats (cuda.h:263-270); all zero here. */
+/* Replaces moert_cuda_dir_stats (cuda.h:263-270): sm_copies counts the
+ * copy-kernel launches, sm_ring_* the staged pageable sources; the GPU-time
+ * fields stay 0. */
 typedef struct moert_cuda_dir_stats {
     long long async_copies, async_marks, bytes;
     long long pub_calls, pub_copies;
@@ -209,7 +220,14 @@ typedef struct moert_cuda_dir_stats {
     long long sm_ring_copies, sm_ring_waits; double sm_ring_wait_ms, sm_stage_ms;
 } moert_cuda_dir_stats;
 void    moert_cuda_dir_stats_get(moert_cuda_dir_stats * out);
-int64_t moert_cuda_dir_gate(int32_t op, int64_t arg);   /* refused: returns -1 */
+/* Replaces the early-decision gate (cuda.h:271-274, ffn_moe.cu:693-745):
+ * 0 enable (arg = last MoE layer | per_layer << 16), 1 arm -> target,
+ * 2 wait((layer << 40) | target) on the host (at most 2 s), then the copy
+ * stream waits on the layer's event on the device, 3 open (host),
+ * 4 stats (arg 0 waits, 1 timeouts, 2 wait us), 5 engine pacing (accepted,
+ * every copy is issued at once), 6 engine stats (0).  moert_ffn_moe's down
+ * fire of a gated layer records the event. */
+int64_t moert_cuda_dir_gate(int32_t op, int64_t arg);
 
 /* Replaces moert_cuda_set_hot_table (cuda.h:276): per (layer, kind) table of
  * n slot base pointers (device array) the hot matmul reads instead of the

@@ -73,7 +73,87 @@ class LlapisMoeLayer(C.Structure):
                 ("act_mode", i32), ("gelu_mode", i32),
                 ("router_w", vp), ("router_b", vp), ("hot_gu", vp), ("hot_dn", vp), ("cold_gu", vp),
                 ("cold_dn", vp), ("exp_slot", vp), ("slot_exp", vp), ("slot_state", vp), ("s_hot", vp),
-                ("s_cold", vp)]
+                ("s_cold", vp), ("route_counts", vp), ("route_hits", vp)]
+
+
+XFER_MAX_GROUPS = 4
+
+
+class LlapisXferDone(C.Structure):
+    _fields_ = [("il", i32), ("e", i32), ("slot", i32), ("ok", i32)]
+
+
+class LlapisXferStats(C.Structure):
+    _fields_ = [(n, C.c_longlong) for n in ("submitted", "completed", "failed", "max_queue", "bytes",
+                                            "wait_idle_calls")] + [("wait_idle_ms", C.c_double)]
+
+
+# moert_policy.h
+REFRESH_PROMPT_END, REFRESH_VISIBLE_INTERVAL, REFRESH_TURN_END, REFRESH_BOUNDARY = 0, 1, 2, 4
+f32 = C.c_float
+
+
+class MoertPolicyConfig(C.Structure):
+    _fields_ = [("n_layers", i32), ("n_expert", i32), ("k", i32), ("seed_prior", f32), ("session_decay", f32),
+                ("recent_decay", f32), ("blend_a", f32), ("blend_b", f32), ("blend_c", f32),
+                ("k_per_layer", vp), ("cost_horizon", i32), ("cost_reuse", f32), ("cost_rate_decay", f32),
+                ("cost_per_token", i32)]
+
+
+STREAM_EXPERT = C.CFUNCTYPE(i32, vp, i32, i32, i32)
+PUBLISH_LAYER = C.CFUNCTYPE(None, vp, i32)
+FETCH_EXTERNAL = C.CFUNCTYPE(None, vp)
+
+
+class MoertPolicyCallbacks(C.Structure):
+    _fields_ = [("stream_expert", STREAM_EXPERT), ("publish_layer", PUBLISH_LAYER),
+                ("fetch_external", FETCH_EXTERNAL), ("user", vp)]
+
+
+class MoertPolicyStats(C.Structure):
+    _fields_ = [(n, i64) for n in ("promotions", "demotions", "tokens", "visible_tokens", "hot_routes",
+                                   "cold_routes", "refresh_count", "refresh_promotions", "refresh_demotions")] + \
+               [("refresh_pause_ms_total", C.c_double), ("refresh_pause_ms_max", C.c_double),
+                ("last_refresh_tok", i64), ("last_refresh_promos", i64), ("last_refresh_pause_ms", C.c_double),
+                ("occupancy", C.c_double)] + \
+               [(n, i64) for n in ("fills_async", "fills_completed", "fills_stale", "fills_aborted")]
+
+
+class MoertPolicyWindow(C.Structure):
+    _fields_ = [("tokens", i32), ("span_ms", C.c_double), ("tok_per_s", C.c_double), ("ms_per_tok", C.c_double),
+                ("hit_rate", C.c_double), ("hot_routes", i64), ("cold_routes", i64)]
+
+
+_P = vp   # moert_policy *
+POLICY_SIGNATURES = {
+    "moert_policy_config_defaults": (None, [C.POINTER(MoertPolicyConfig)]),
+    "moert_policy_create": (_P, [C.POINTER(MoertPolicyConfig), C.POINTER(MoertPolicyCallbacks)]),
+    "moert_policy_free": (None, [_P]),
+    "moert_policy_set_external_observation": (None, [_P, i32]),
+    "moert_policy_observe": (None, [_P, i32, vp, i32, i64]),
+    "moert_policy_on_prompt_token": (None, [_P, i64]),
+    "moert_policy_on_token_end": (None, [_P]),
+    "moert_policy_refresh": (None, [_P, i32]),
+    "moert_policy_resize_k": (i32, [_P, i32]),
+    "moert_policy_set_active_k": (i32, [_P, i32]),
+    "moert_policy_can_seed": (i32, [_P, i32, i32]),
+    "moert_policy_commit_seed": (i32, [_P, i32, i32, i32]),
+    "moert_policy_complete_fill": (i32, [_P, i32, i32, i32]),
+    "moert_policy_abort_fill": (i32, [_P, i32, i32, i32]),
+    "moert_policy_boundary_layer": (i32, [_P, i32, vp, i64, f32, f32]),
+    "moert_policy_add_external_counts": (None, [_P, i32, vp, i64, i64]),
+    "moert_policy_reset_stats": (None, [_P]),
+    "moert_policy_layer_k": (i32, [_P, i32]),
+    "moert_policy_set_external_forecast": (None, [_P, vp, f32, i32]),
+    "moert_policy_hit_rate": (C.c_double, [_P]),
+    "moert_policy_get_stats": (None, [_P, C.POINTER(MoertPolicyStats)]),
+    "moert_policy_get_window": (None, [_P, i32, C.POINTER(MoertPolicyWindow)]),
+    "moert_policy_exp_slot_view": (C.POINTER(i32), [_P, i32]),
+    "moert_policy_slot_exp_view": (C.POINTER(i32), [_P, i32]),
+    "moert_policy_slot_state_view": (C.POINTER(i32), [_P, i32]),
+    "moert_policy_hotmap_view": (C.POINTER(i32), [_P, i32]),
+    "moert_policy_resid_view": (C.POINTER(f32), [_P, i32]),
+}
 
 
 # every symbol the two public headers declare, with its signature
@@ -114,6 +194,17 @@ SIGNATURES = {
     "llapis_set_tuning": (None, [i32, i32]),
     "llapis_profile_enable": (None, [i32]),
     "llapis_profile_read": (i32, [vp, i32]),
+    "llapis_xfer_create": (vp, [i32, i32, i32, i32]),
+    "llapis_xfer_free": (None, [vp]),
+    "llapis_xfer_last_error": (C.c_char_p, []),
+    "llapis_xfer_set_group": (i32, [vp, i32, i32, vp, vp, u64, u64]),
+    "llapis_xfer_submit": (i32, [vp, i32, i32, i32]),
+    "llapis_xfer_flush": (i32, [vp, vp]),
+    "llapis_xfer_take_done": (i32, [vp, C.POINTER(LlapisXferDone), i32]),
+    "llapis_xfer_in_flight": (i64, [vp]),
+    "llapis_xfer_wait_idle": (i32, [vp, vp]),
+    "llapis_xfer_get_stats": (None, [vp, C.POINTER(LlapisXferStats)]),
+    **POLICY_SIGNATURES,
 }
 
 STAGES = ("router", "topk", "gate_up", "down", "combine")

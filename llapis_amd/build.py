@@ -19,8 +19,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "libllapis_moe.so"
 ARCH = "gfx950"
 
-HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "api.hip"]
-HOST_SOURCES = ["quantize.cpp"]
+HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "transfer.hip", "api.hip"]
+HOST_SOURCES = ["quantize.cpp", "policy.cpp"]
 
 
 def _hipcc():
@@ -59,7 +59,7 @@ def build(verbose=False):
                 print(out)
     objs = [str(BUILD / (s + ".o")) for s in HIP_SOURCES + HOST_SOURCES]
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs, "-pthread"])
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", str(tmp), *objs, "-pthread"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -176,18 +176,7 @@ void moert_cuda_stats_get(moert_cuda_stats * out) {
     out->op_host_ns = g_op_ns.load();
 }
 
-int32_t moert_cuda_dir_init(int32_t, int32_t, int32_t) { return 0; }
-int32_t moert_cuda_dir_async(void *, const void *, uint64_t) { return 0; }
-int64_t moert_cuda_dir_mark(void) { return -1; }
-int64_t moert_cuda_dir_poll(int32_t) { return -1; }
-int32_t moert_cuda_publish_h2d(int32_t n, void * const * dsts, const void * const * srcs, const uint64_t * sizes) {
-    for (int32_t i = 0; i < n; ++i) MOERT_HIP_CHECK(hipMemcpy(dsts[i], srcs[i], sizes[i], hipMemcpyHostToDevice));
-    return 1;
-}
-void moert_cuda_dir_stats_get(moert_cuda_dir_stats * out) {
-    if (out) memset(out, 0, sizeof(*out));
-}
-int64_t moert_cuda_dir_gate(int32_t, int64_t) { return -1; }
+// the batch transport and the early-decision gate are in transfer.hip
 
 void moert_cuda_set_hot_table(int32_t il, int32_t kind, const void * const * dev_ptrs, int32_t n, int32_t type_tag) {
     if (il < 0 || il >= 128 || kind < 0 || kind > 1) return;
@@ -290,6 +279,7 @@ void moert_ffn_moe(const moert_ffn_moe_args * a, const moert_ffn_moe_host * h) {
     MOERT_HIP_CHECK(launch_scatter(y_hot, y_cold, D_out, kind, counts, ids_hot, hot_dst, ids_cold, cold_dst,
                                    (const float *)a->s_hot, (const float *)a->s_cold, (float *)a->dst, Pmax, stream));
     for (int i = n_scratch - 1; i >= 0; --i) h->pool_free(h->user, scratch[i]);
+    dir_gate_after_fire(a->il, kind, stream);
     g_op_ns += now_ns() - t0;
     ++g_fires;
 }
@@ -722,6 +712,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.cold_dn_type = L->cold_dn_type;
         p.prefetch_dn = g_prefetch_dn.load();
         p.never = 0;
+        p.rc_counts = L->route_counts;
+        p.rc_hits = L->route_counts ? L->route_hits : nullptr;
         p.logits = reinterpret_cast<float *>(base + dw.logits);
         p.ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + dw.ids);
         p.w = w_out ? w_out : reinterpret_cast<float *>(base + dw.w);
@@ -796,6 +788,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.al = (_Float16 *)(base + pw.al);
             p.ae = (float *)(base + pw.ae);
             p.ydn = (float *)(base + pw.ydn);
+            p.rc_counts = L->route_counts;
+            p.rc_hits = L->route_counts ? L->route_hits : nullptr;
             hipEvent_t ev[4] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
             LL_TRY(launch_prefill(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, src, s,
                                   pc >= 0 ? ev : nullptr));
@@ -821,6 +815,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     LL_TRY(prof_record(pc, 1, 0, s));
     LL_TRY(launch_topk(probs, T, L->n_expert, L->top_k, ids, w, s));
     LL_TRY(prof_record(pc, 1, 1, s));
+    LL_TRY(launch_route_count(ids, L->top_k, L->top_k, P, L->exp_slot, L->slot_exp, L->slot_state, L->n_expert,
+                              L->k_slots, L->route_counts, L->route_hits, s));
 
     MmvParams p = {};
     p.mode = MMV_ROUTED;

@@ -209,6 +209,25 @@ __device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo *
     if (lane == 0) *n_groups = __popcll(lm);
 }
 
+// Routing counters of the call (one workgroup, as the island's partition
+// kernel counts them, ffn_moe.cu:123-128): routed pairs per valid expert id,
+// then the hot pairs and the other pairs.
+__device__ void count_routes(const DecParams & p, const int * s_ids, const GroupInfo * groups, int ng) {
+    if (!p.rc_counts) return;
+    const int P = p.T * p.top_k;
+    if ((int)threadIdx.x < P) {
+        const int e = s_ids[threadIdx.x];
+        if (e >= 0 && e < p.n_expert) atomicAdd(p.rc_counts + e, 1);
+    }
+    if (threadIdx.x == 0 && p.rc_hits) {
+        int hot = 0;
+        for (int i = 0; i < ng; ++i)
+            if (groups[i].tier == 0) hot += groups[i].n_mem;
+        atomicAdd(p.rc_hits, hot);
+        atomicAdd(p.rc_hits + 1, P - hot);
+    }
+}
+
 // Router logits of expert e for every token (one workgroup), written with
 // device-coherent stores.  Each lane issues all of its row loads (RU float4
 // per pass) before any arithmetic.
@@ -847,6 +866,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         }
         for (int i = threadIdx.x; i < ng; i += WG) p.ctl->groups[i] = s_grp[i];
         if (threadIdx.x == 0) p.ctl->n_groups = ng;
+        count_routes(p, s_ids, s_grp, ng);
     }
     const int a0 = p.w_lds_gu;
 #pragma unroll
@@ -1048,6 +1068,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         p.w[threadIdx.x] = s_wt[threadIdx.x];
     }
     const int ng = ok ? min(s_ng, DEC_PMAX) : 0;
+    if (ok && blockIdx.x == 0) count_routes(p, s_ids, s_grp, ng);
 
     // ---- phase 3: gate_up
     for (int it = blockIdx.x; it < ng * NRB_G; it += gridDim.x) {

@@ -97,6 +97,8 @@ struct DecParams {
     int prefetch_dn;            // gate_up items touch their down item's slab (into L2/MALL) for the down kernel
     int never;                  // always 0: keeps the touch loads from being dropped
     int64_t spin_limit;         // single-kernel path: wall-clock ticks a wait may take
+    int32_t * rc_counts;        // [n_expert] routed pairs per expert, or NULL
+    int32_t * rc_hits;          // [2] hot pairs, other pairs (with rc_counts)
 };
 
 int dec_act_bytes(int n);
@@ -154,6 +156,8 @@ struct PfParams {
     _Float16 * al;                       // [P][n_ff]                                  and exact remainder
     float * ae;                          // [P] 2^-e
     float * ydn;                         // [P][d_model]
+    int32_t * rc_counts;                 // [n_expert] routed pairs per expert, or NULL
+    int32_t * rc_hits;                   // [2] hot pairs, other pairs (with rc_counts)
 };
 
 int pf_max_tiles(int P, int n_expert);
@@ -179,6 +183,14 @@ hipError_t launch_partition(const int32_t * ids, int n_used, int ids_s1, int n_p
                             const int32_t * slot_exp, const int32_t * slot_state, int n_expert, int K,
                             int32_t * ids_hot, int32_t * ids_cold, int32_t * hot_dst, int32_t * cold_dst,
                             int32_t * counts, int32_t * rc_counts, int32_t * rc_hits, hipStream_t s);
+// Routing counters for n_pairs routed ids (row stride ids_s1, n_used per
+// token): as the partition kernel counts them.  One workgroup.
+hipError_t launch_route_count(const int32_t * ids, int n_used, int ids_s1, int n_pairs, const int32_t * exp_slot,
+                              const int32_t * slot_exp, const int32_t * slot_state, int n_expert, int K,
+                              int32_t * rc_counts, int32_t * rc_hits, hipStream_t s);
+// Transport hook of moert_ffn_moe: the early-decision gate's event after a
+// gated layer's last fire.
+void dir_gate_after_fire(int il, int kind, hipStream_t stream);
 hipError_t launch_gather(const float * cur, int D_in, int kind, int n_used, const int32_t * counts,
                          const int32_t * hot_dst, const int32_t * cold_dst, float * x_hot, float * x_cold,
                          int Pmax, hipStream_t s);

@@ -105,7 +105,7 @@ __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t)
 // fixed, and need not be: each pair's output column is computed on its own.
 __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     constexpr int PER = PF_MAX_PAIRS / WG;
-    __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257];
+    __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_hot;
     const int P = p.T * p.top_k, E = p.n_expert;
     // the ids, read once with every load in flight together
     int ev[PER];
@@ -119,6 +119,7 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         s_cnt[i] = 0;
         s_fill[i] = 0;
     }
+    if (threadIdx.x == 0) s_hot = 0;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < PER; ++k)
@@ -139,6 +140,13 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         }
     }
     const int nt_e = (n_e + PF_TOK - 1) / PF_TOK;
+    if (p.rc_counts) {
+        // routing counters (ffn_moe.cu:123-128): pairs per expert, hot pairs,
+        // the other pairs (invalid ids included)
+        if (n_e) atomicAdd(p.rc_counts + e0, n_e);
+        const int hot = tier == 0 ? n_e : 0;
+        if (hot) atomicAdd(&s_hot, hot);
+    }
     s_off[threadIdx.x] = n_e;
     s_nt[threadIdx.x] = nt_e;
     __syncthreads();
@@ -153,6 +161,10 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     }
     const int pair0 = s_off[threadIdx.x] - n_e, tile0 = s_nt[threadIdx.x] - nt_e;
     const int total = s_off[255], tiles = min(s_nt[255], p.max_tiles);
+    if (p.rc_hits && threadIdx.x == 0) {
+        atomicAdd(p.rc_hits, s_hot);
+        atomicAdd(p.rc_hits + 1, P - s_hot);
+    }
     __syncthreads();
     s_off[threadIdx.x] = pair0;                 // exclusive offsets
     if (threadIdx.x == 0) {

@@ -250,6 +250,36 @@ __global__ __launch_bounds__(64) void k_partition(const int32_t * __restrict__ i
     }
 }
 
+// Routing counters without the partition (the fused layer's generic path):
+// the same counts k_partition adds, for any number of pairs.  One workgroup.
+__global__ __launch_bounds__(WG) void k_route_count(const int32_t * __restrict__ ids, int n_used, int ids_s1,
+                                                    int n_pairs, const int32_t * __restrict__ exp_slot,
+                                                    const int32_t * __restrict__ slot_exp,
+                                                    const int32_t * __restrict__ slot_state, int n_expert, int K,
+                                                    int32_t * __restrict__ rc_counts, int32_t * __restrict__ rc_hits) {
+    __shared__ int s_hot;
+    if (threadIdx.x == 0) s_hot = 0;
+    __syncthreads();
+    int hot = 0;
+    for (int q = threadIdx.x; q < n_pairs; q += WG) {
+        const int t = q / n_used;
+        const int e = ids[t * ids_s1 + (q - t * n_used)];
+        if (e >= 0 && e < n_expert) {
+            atomicAdd(&rc_counts[e], 1);
+            if (K > 0) {
+                const int sl = exp_slot[e];
+                if (sl >= 0 && sl < K && slot_state[sl] == 2 && slot_exp[sl] == e) ++hot;
+            }
+        }
+    }
+    if (hot) atomicAdd(&s_hot, hot);
+    __syncthreads();
+    if (threadIdx.x == 0 && rc_hits) {
+        atomicAdd(&rc_hits[0], s_hot);
+        atomicAdd(&rc_hits[1], n_pairs - s_hot);
+    }
+}
+
 // x_side[i] = activation column of compact pair i (ffn_moe.cu:135-153)
 __global__ __launch_bounds__(WG) void k_gather(const float * __restrict__ cur, int D_in, int kind, int n_used,
                                                const int32_t * __restrict__ counts, const int32_t * __restrict__ hot_dst,
@@ -339,6 +369,15 @@ hipError_t launch_partition(const int32_t * ids, int n_used, int ids_s1, int n_p
                             int32_t * counts, int32_t * rc_counts, int32_t * rc_hits, hipStream_t s) {
     hipLaunchKernelGGL(k_partition, dim3(1), dim3(64), 0, s, ids, n_used, ids_s1, n_pairs, exp_slot, slot_exp,
                        slot_state, n_expert, K, ids_hot, ids_cold, hot_dst, cold_dst, counts, rc_counts, rc_hits);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_count(const int32_t * ids, int n_used, int ids_s1, int n_pairs, const int32_t * exp_slot,
+                              const int32_t * slot_exp, const int32_t * slot_state, int n_expert, int K,
+                              int32_t * rc_counts, int32_t * rc_hits, hipStream_t s) {
+    if (!rc_counts || n_pairs <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_route_count, dim3(1), dim3(WG), 0, s, ids, n_used, ids_s1, n_pairs, exp_slot, slot_exp,
+                       slot_state, n_expert, K, rc_counts, rc_hits);
     return hipGetLastError();
 }
 

@@ -253,6 +253,7 @@ class DeviceLayer:
         self.exp_slot, self.slot_exp = up(layer.exp_slot), up(layer.slot_exp)
         self.slot_state = up(layer.slot_state)
         self.s_hot, self.s_cold = up(layer.s_hot), up(layer.s_cold)
+        self.route_counts = self.route_hits = None   # optional int32 device tensors [n_expert], [2]
         self._ws = None
 
     def desc(self):
@@ -262,7 +263,8 @@ class DeviceLayer:
                                 self.act_mode, self.gelu_mode,
                                 _ptr(self.router_w), _ptr(self.router_b), _ptr(self.hot_gu), _ptr(self.hot_dn),
                                 _ptr(self.cold_gu), _ptr(self.cold_dn), _ptr(self.exp_slot), _ptr(self.slot_exp),
-                                _ptr(self.slot_state), _ptr(self.s_hot), _ptr(self.s_cold))
+                                _ptr(self.slot_state), _ptr(self.s_hot), _ptr(self.s_cold),
+                                _ptr(self.route_counts), _ptr(self.route_hits))
 
     def workspace(self, n_tokens):
         torch = _torch()

@@ -50,7 +50,15 @@ MIRRORS = {
     "llapis_tensor": _lib.LlapisTensor,
     "llapis_moe_dual_op": _lib.LlapisMoeDualOp,
     "llapis_moe_layer": _lib.LlapisMoeLayer,
+    "llapis_xfer_done": _lib.LlapisXferDone,
+    "llapis_xfer_stats": _lib.LlapisXferStats,
+    "moert_policy_config": _lib.MoertPolicyConfig,
+    "moert_policy_callbacks": _lib.MoertPolicyCallbacks,
+    "moert_policy_stats": _lib.MoertPolicyStats,
+    "moert_policy_window": _lib.MoertPolicyWindow,
 }
+POLICY_STRUCTS = ("moert_policy_config", "moert_policy_callbacks", "moert_policy_stats", "moert_policy_window")
+REF_POLICY_HEADER = Path("/root/reference/moert/include/moert/policy.h")
 # structs of the reference header with no ctypes mirror (host callback payloads)
 CALLBACK_STRUCTS = {
     "moert_coldcpu_call": ["il", "kind", "n_cold", "cold_ids", "x", "x_per_pair", "w_host", "expert_bytes",
@@ -82,7 +90,8 @@ def compile_layouts(tmp_path, header, structs):
 
 
 def moert_structs():
-    out = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items() if k.startswith("moert_")}
+    out = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items()
+           if k.startswith("moert_") and k not in POLICY_STRUCTS}
     out.update(CALLBACK_STRUCTS)
     return out
 
@@ -90,7 +99,7 @@ def moert_structs():
 def test_ctypes_mirror_matches_headers(tmp_path):
     structs = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items()}
     prog_header = tmp_path / "both.h"
-    prog_header.write_text('#include "moert_hip.h"\n#include "llapis_moe.h"\n')
+    prog_header.write_text('#include "moert_hip.h"\n#include "llapis_moe.h"\n#include "moert_policy.h"\n')
     got = compile_layouts(tmp_path, str(prog_header), structs)
     for s, cls in MIRRORS.items():
         assert got[(s, "sizeof")] == C.sizeof(cls), s
@@ -107,6 +116,15 @@ def test_moert_structs_match_reference_header(tmp_path):
     assert ours[("moert_ffn_moe_args", "sizeof")] > 0
 
 
+@pytest.mark.skipif(not REF_POLICY_HEADER.exists(), reason="reference tree not present")
+def test_policy_structs_match_reference_header(tmp_path):
+    structs = {k: [f[0] for f in MIRRORS[k]._fields_] for k in POLICY_STRUCTS}
+    ours = compile_layouts(tmp_path, str(INCLUDE / "moert_policy.h"), structs)
+    (tmp_path / "r").mkdir()
+    theirs = compile_layouts(tmp_path / "r", str(REF_POLICY_HEADER), structs)
+    assert ours == theirs
+
+
 def test_config_defaults_match():
     """moert_cuda_config_defaults is header-inline in both; compare the values
     ours sets with the reference's documented defaults."""
@@ -120,15 +138,31 @@ def test_config_defaults_match():
                     "cold_guard_fn": "0", "cold_ffn": "0", "coldffn_submit_fn": "0", "coldffn_wait_fn": "0"}
 
 
-def test_refusing_services_without_a_device():
+def test_host_services_and_transport_before_init():
+    """Registration is refused (the cold tier is in HBM); the transport
+    answers as the reference's does before moert_cuda_dir_init (no device
+    call is made)."""
     lib = la.lib()
     assert lib.moert_cuda_host_register_pinned(None, 0) == 0
     assert lib.moert_cuda_host_register_mapped(None, 0) == 0
     assert lib.moert_cuda_host_map(None, 0) is None
-    assert lib.moert_cuda_dir_init(0, 0, 0) == 0
+    assert lib.moert_cuda_dir_async(None, None, 0) == 0
     assert lib.moert_cuda_dir_mark() == -1
     assert lib.moert_cuda_dir_poll(0) == -1
-    assert lib.moert_cuda_dir_gate(0, 0) == -1
+    assert lib.moert_cuda_dir_gate(4, 0) == 0            # no waits yet
+    assert lib.moert_cuda_dir_gate(2, 5) == 0            # gate not enabled: nothing to wait for
+    assert lib.moert_cuda_dir_gate(1, 0) == 1            # arm: target 1
+    assert lib.moert_cuda_dir_gate(3, 0) == 1
+    assert lib.moert_cuda_publish_h2d(0, None, None, None) == 1
     st = _lib.MoertCudaDirStats()
     lib.moert_cuda_dir_stats_get(C.byref(st))
     assert st.async_copies == 0 and st.pub_calls == 0
+
+
+def test_xfer_refuses_bad_arguments_without_a_device():
+    lib = la.lib()
+    assert lib.llapis_xfer_create(0, 128, 57, 8) is None
+    assert b"geometry" in lib.llapis_xfer_last_error()
+    assert lib.llapis_xfer_submit(None, 0, 0, 0) == -1
+    assert lib.llapis_xfer_take_done(None, None, 0) == -1
+    assert lib.llapis_xfer_in_flight(None) == 0

@@ -1,0 +1,361 @@
+"""GPU: the promotion path and the routing-counter loop.
+
+* The island's batch transport (moert_cuda_dir_*): device, pinned and small
+  pageable sources land byte for byte, large pageable ones are refused, marks
+  complete in order, the pinned ring is reused behind its events, the gate
+  orders a copy after the last MoE fire of a layer, publish_h2d lands.
+* The promotion engine (llapis_xfer_*): jobs stay pending until flush,
+  then every page group of the expert lands in its slot bit for bit (copy
+  kernel, and hipMemcpyAsync from pinned memory).
+* The loop a server runs: decode and prefill calls count their routing on the
+  device; the policy pulls the counts at each decision (they must equal the
+  counts of the ids the GPU returned), promotes asynchronously (FILLING), the
+  engine copies the expert from the promotion source in HBM, the completion
+  makes the slot READY and the mirrors are published.  Every call's output
+  is checked against the oracle under the page table it ran with: a FILLING
+  expert is served cold, a READY one hot from its new slot.
+"""
+import copy
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import llapis_amd as la
+from llapis_amd import _lib as L
+from llapis_amd.policy import Policy
+from helpers import FULL16, layer, rel_l2, tokens
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def torch_mod():
+    import torch
+    return torch
+
+
+def u8(torch, a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_batch_transport(gpu):
+    torch = torch_mod()
+    lib = la.lib()
+    say("transport: init, device / pinned / pageable sources")
+    assert lib.moert_cuda_dir_init(0, 1, 0) == 1
+    assert lib.moert_cuda_dir_init(0, 1, 0) == 1             # idempotent
+    st0 = L.MoertCudaDirStats()
+    lib.moert_cuda_dir_stats_get(C.byref(st0))
+    rng = np.random.default_rng(5)
+    n = 3_593_216
+    src_h = rng.integers(0, 256, n, dtype=np.uint8)
+    src_d = u8(torch, src_h, gpu)
+    dst = torch.zeros(3 * n + 8192, dtype=torch.uint8, device=gpu)
+    pin = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    pin.copy_(torch.from_numpy(src_h[::-1].copy()))
+    small = rng.integers(0, 256, 4096, dtype=np.uint8)
+    small_orig = small.copy()
+    big = rng.integers(0, 256, 8192, dtype=np.uint8)
+    base = dst.data_ptr()
+    assert lib.moert_cuda_dir_async(base, src_d.data_ptr(), n) == 1
+    assert lib.moert_cuda_dir_async(base + n, pin.data_ptr(), n) == 1
+    assert lib.moert_cuda_dir_async(base + 2 * n, small.ctypes.data, 4096) == 1
+    assert lib.moert_cuda_dir_async(base + 2 * n + 4096, big.ctypes.data, 8192) == 0    # pageable > 4 KiB
+    small[:] = 0                                              # staged: the caller may reuse it at once
+    m0 = lib.moert_cuda_dir_mark()
+    assert m0 >= 0
+    assert lib.moert_cuda_dir_poll(1) == m0
+    h = dst.cpu().numpy()
+    assert np.array_equal(h[:n], src_h)
+    assert np.array_equal(h[n:2 * n], src_h[::-1])
+    assert np.array_equal(h[2 * n:2 * n + 4096], small_orig)
+    assert not h[2 * n + 4096:].any()                         # the refused copy wrote nothing
+    say("transport: 600 small pageable copies through the pinned ring")
+    pages = rng.integers(0, 256, (600, 256), dtype=np.uint8)
+    out = torch.zeros(600 * 256, dtype=torch.uint8, device=gpu)
+    for i in range(600):
+        assert lib.moert_cuda_dir_async(out.data_ptr() + 256 * i, pages[i].ctypes.data, 256) == 1
+    m1 = lib.moert_cuda_dir_mark()
+    assert m1 == m0 + 1
+    while lib.moert_cuda_dir_poll(0) < m1:
+        pass
+    assert np.array_equal(out.cpu().numpy().reshape(600, 256), pages)
+    st = L.MoertCudaDirStats()
+    lib.moert_cuda_dir_stats_get(C.byref(st))
+    assert st.async_copies - st0.async_copies == 603
+    assert st.async_marks - st0.async_marks == 2
+    assert st.bytes - st0.bytes == 2 * n + 4096 + 600 * 256
+    assert st.sm_ring_copies - st0.sm_ring_copies == 601
+    say("transport: publish_h2d")
+    views = [np.arange(16, dtype=np.int32), np.full(4, 7, np.int32), np.array([2, 1, 0, 2], np.int32)]
+    dev = [torch.zeros(v.size, dtype=torch.int32, device=gpu) for v in views]
+    dsts = (C.c_void_p * 3)(*[d.data_ptr() for d in dev])
+    srcs = (C.c_void_p * 3)(*[v.ctypes.data for v in views])
+    sizes = (C.c_uint64 * 3)(*[v.nbytes for v in views])
+    assert lib.moert_cuda_publish_h2d(3, dsts, srcs, sizes) == 1
+    for d, v in zip(dev, views):
+        assert np.array_equal(d.cpu().numpy(), v)
+
+
+def test_transport_gate_orders_copy_after_last_fire(gpu):
+    """Gate ops of moert_cuda_dir_gate: a wait for a target no fire reached
+    times out on the host (2 s); after the layer's down fire the wait returns
+    at once and the copy stream waits for that fire on the device."""
+    torch = torch_mod()
+    lib = la.lib()
+    assert lib.moert_cuda_dir_init(0, 1, 0) == 1
+    spec = FULL16
+    lay = layer(spec, 61, [0, 3, 5], scales=True)
+    dl = la.DeviceLayer(lay, gpu)
+    assert lib.moert_cuda_dir_gate(0, 0) == 1                 # last MoE layer 0, one gate for the forward
+    w0, t0 = lib.moert_cuda_dir_gate(4, 0), lib.moert_cuda_dir_gate(4, 1)
+    target = lib.moert_cuda_dir_gate(1, 0)
+    assert target >= 1
+    say("gate: wait with no fire (times out)")
+    assert lib.moert_cuda_dir_gate(2, target) == 1
+    assert lib.moert_cuda_dir_gate(4, 1) == t0 + 1
+    say("gate: fires of layer 0, then the wait returns and orders the copy")
+    T = 2
+    x = torch.from_numpy(tokens(3, T, spec.d_model)).to(gpu)
+    ids, w, _ = dl.router(x)
+    gu = dl.moe_dual(0, x, ids, il=0)
+    act = la.geglu(gu.reshape(-1, 2 * spec.n_ff).contiguous(), spec.n_ff)
+    dn = dl.moe_dual(1, act, ids, il=0)
+    target = lib.moert_cuda_dir_gate(1, 0)
+    assert lib.moert_cuda_dir_gate(2, target - 1) == 1       # the fire above reached it
+    assert lib.moert_cuda_dir_gate(4, 1) == t0 + 1            # no new timeout
+    src = torch.arange(1 << 20, dtype=torch.int32, device=gpu)
+    dst = torch.zeros_like(src)
+    assert lib.moert_cuda_dir_async(dst.data_ptr(), src.data_ptr(), src.numel() * 4) == 1
+    m = lib.moert_cuda_dir_mark()
+    assert lib.moert_cuda_dir_poll(1) == m
+    assert torch.equal(dst, src)
+    assert lib.moert_cuda_dir_gate(3, 0) == 1                 # open: every layer reaches the armed target
+    assert lib.moert_cuda_dir_gate(4, 0) == w0 + 2
+    torch.cuda.synchronize()
+    assert dn.shape[-1] == spec.d_model
+
+
+@pytest.mark.parametrize("copy_wgs,pinned", [(8, False), (0, False), (0, True)])
+def test_xfer_copies_expert_pages(gpu, copy_wgs, pinned):
+    torch = torch_mod()
+    lib = la.lib()
+    say(f"xfer copy_wgs={copy_wgs} pinned={pinned}")
+    rng = np.random.default_rng(copy_wgs + 3 * pinned)
+    NL, E, K = 2, 6, 3
+    sizes = [2_230_272, 1_362_944, 4]          # Q4_K gate_up, Q5_0 down, a scale page
+    src_h = [[rng.integers(0, 256, E * b, dtype=np.uint8) for b in sizes] for _ in range(NL)]
+    if pinned:
+        src = [[torch.from_numpy(a).pin_memory() for a in row] for row in src_h]
+    else:
+        src = [[u8(torch, a, gpu) for a in row] for row in src_h]
+    slab = [[torch.zeros(K * b, dtype=torch.uint8, device=gpu) for b in sizes] for _ in range(NL)]
+    x = lib.llapis_xfer_create(NL, E, K, copy_wgs)
+    assert x
+    try:
+        for il in range(NL):
+            for g, b in enumerate(sizes):
+                assert lib.llapis_xfer_set_group(x, il, g, slab[il][g].data_ptr(), src[il][g].data_ptr(), b, b) == 0
+        assert lib.llapis_xfer_set_group(x, 0, 0, slab[0][0].data_ptr(), src_h[0][0].ctypes.data, sizes[0],
+                                         sizes[0]) == -1               # pageable source refused
+        assert lib.llapis_xfer_submit(x, 0, E, 0) == -1
+        jobs = [(0, 4, 1), (1, 2, 0), (0, 5, 2), (1, 0, 2), (0, 1, 0)]
+        for il, e, s in jobs:
+            assert lib.llapis_xfer_submit(x, il, e, s) == 0
+        assert lib.llapis_xfer_in_flight(x) == len(jobs)
+        torch.cuda.synchronize()
+        assert not any(t.any().item() for row in slab for t in row)    # pending: nothing issued
+        stream = torch.cuda.current_stream().cuda_stream
+        assert lib.llapis_xfer_flush(x, stream) == 0
+        assert lib.llapis_xfer_wait_idle(x, stream) == 0
+        done = (L.LlapisXferDone * 8)()
+        n = lib.llapis_xfer_take_done(x, done, 8)
+        assert n == len(jobs)
+        assert [(d.il, d.e, d.slot, d.ok) for d in done[:n]] == [j + (1,) for j in jobs]
+        assert lib.llapis_xfer_in_flight(x) == 0
+        expect = [[np.zeros(K * b, np.uint8) for b in sizes] for _ in range(NL)]
+        for il, e, s in jobs:
+            for g, b in enumerate(sizes):
+                expect[il][g][s * b:(s + 1) * b] = src_h[il][g][e * b:(e + 1) * b]
+        for il in range(NL):
+            for g in range(len(sizes)):
+                assert np.array_equal(slab[il][g].cpu().numpy(), expect[il][g]), (il, g)
+        st = L.LlapisXferStats()
+        lib.llapis_xfer_get_stats(x, C.byref(st))
+        assert (st.submitted, st.completed, st.failed) == (5, 5, 0)
+        assert st.bytes == 5 * sum(sizes)
+    finally:
+        lib.llapis_xfer_free(x)
+
+
+def _view_layer(lay_all, src_s, es, se, ss):
+    """The layer as the kernels see it under a page table: READY slots hold
+    their expert's promotion-source bytes, other slots are never read."""
+    sp = lay_all.spec
+    K = len(se)
+    gb, db = sp.gu_bytes(sp.hot_gu_type), sp.dn_bytes(sp.hot_dn_type)
+    v = copy.copy(lay_all)
+    v.residency = la.Residency(sp.n_expert, K, es.copy(), se.copy(), ss.copy())
+    v.hot_gu = np.zeros(K * gb, np.uint8)
+    v.hot_dn = np.zeros(K * db, np.uint8)
+    v.s_hot = np.ones(K, np.float32)
+    for s in range(K):
+        e = int(se[s])
+        if e >= 0 and ss[s] == la.SLOT_READY:
+            v.hot_gu[s * gb:(s + 1) * gb] = lay_all.hot_gu[e * gb:(e + 1) * gb]
+            v.hot_dn[s * db:(s + 1) * db] = lay_all.hot_dn[e * db:(e + 1) * db]
+            v.s_hot[s] = src_s[e]
+    return v
+
+
+def test_promotion_loop_with_device_counts(gpu, oracle):
+    torch = torch_mod()
+    lib = la.lib()
+    spec = FULL16
+    E, K, top_k = spec.n_expert, 4, spec.top_k
+    # the promotion source: every expert in the hot formats (slot e = expert e)
+    lay_all = layer(spec, 71, list(range(E)), scales=True)
+    src_s = lay_all.s_hot.copy()
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    src_gu, src_dn, src_sc = u8(torch, lay_all.hot_gu, gpu), u8(torch, lay_all.hot_dn, gpu), u8(torch, src_s, gpu)
+    # the live layer: K slots seeded with experts 0..3
+    live = copy.copy(lay_all)
+    live.residency = la.Residency.from_hot(E, list(range(K)))
+    live.hot_gu = lay_all.hot_gu[:K * gb].copy()
+    live.hot_dn = lay_all.hot_dn[:K * db].copy()
+    live.s_hot = src_s[:K].copy()
+    live.router_b = np.zeros(E, np.float32)
+    dl = la.DeviceLayer(live, gpu)
+    dl.route_counts = torch.zeros(E, dtype=torch.int32, device=gpu)
+    dl.route_hits = torch.zeros(2, dtype=torch.int32, device=gpu)
+    x_eng = lib.llapis_xfer_create(1, E, K, 8)
+    assert x_eng
+    for g, (slab, src, b) in enumerate(((dl.hot_gu, src_gu, gb), (dl.hot_dn, src_dn, db), (dl.s_hot, src_sc, 4))):
+        assert lib.llapis_xfer_set_group(x_eng, 0, g, slab.data_ptr(), src.data_ptr(), b, b) == 0
+
+    expect = {"counts": np.zeros(E, np.int64), "hot": 0, "cold": 0}
+    log = {"fetches": 0, "submitted": 0, "completed": 0, "filling_served_cold": 0, "promoted_used_hot": 0}
+    pol = None
+
+    def fetch():
+        c = dl.route_counts.cpu().numpy()
+        hc = dl.route_hits.cpu().numpy()
+        assert np.array_equal(c, expect["counts"]), (c, expect["counts"])
+        assert (int(hc[0]), int(hc[1])) == (expect["hot"], expect["cold"])
+        pol.add_counts(0, c, int(hc[0]), int(hc[1]))
+        dl.route_counts.zero_()
+        dl.route_hits.zero_()
+        expect["counts"][:] = 0
+        expect["hot"] = expect["cold"] = 0
+        log["fetches"] += 1
+
+    def stream_expert(il, e, slot):
+        assert lib.llapis_xfer_submit(x_eng, il, e, slot) == 0
+        log["submitted"] += 1
+        return 2
+
+    def publish(il):
+        v = pol.views(il)
+        dev = [dl.exp_slot, dl.slot_exp, dl.slot_state]
+        host = [v["exp_slot"], v["slot_exp"], v["slot_state"]]
+        dsts = (C.c_void_p * 3)(*[d.data_ptr() for d in dev])
+        srcs = (C.c_void_p * 3)(*[h.ctypes.data for h in host])
+        sizes = (C.c_uint64 * 3)(*[h.nbytes for h in host])
+        assert lib.moert_cuda_publish_h2d(3, dsts, srcs, sizes) == 1
+
+    pol = Policy(1, E, K, stream_expert=stream_expert, publish_layer=publish, fetch_external=fetch,
+                 cost_horizon=64, cost_reuse=2.0, cost_per_token=2)
+    pol.set_external(True)
+    for e in range(K):
+        assert pol.seed(0, e, e) == 1
+    publish(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    done = (L.LlapisXferDone * 64)()
+    try:
+        # phase A favours experts 8..15, phase B experts 0..7; T = 1 decode
+        # mostly, 4-token steps, a generic-path step and a prompt chunk on the
+        # prefill path (no decision: its counts are pulled at the turn end)
+        plan = [(1, "A")] * 8 + [(4, "A")] + [(1, "B"), (4, "B")] + [(1, "B")] * 14 + [(2, "Bg"), (40, "Bp")]
+        for step, (T, phase) in enumerate(plan):
+            if step % 2 == 0:
+                n = lib.llapis_xfer_take_done(x_eng, done, 64)
+                touched = False
+                for d in done[:n]:
+                    assert d.ok == 1
+                    if pol.complete(d.il, d.slot, d.e) == 1:
+                        touched = True
+                        log["completed"] += 1
+                if touched:
+                    publish(0)
+            bias = np.zeros(E, np.float32)
+            bias[8:] = 3.0 if phase == "A" else -3.0
+            dl.router_b.copy_(torch.from_numpy(bias))
+            live.router_b = bias
+            v = pol.views(0)
+            res = la.Residency(E, K, v["exp_slot"], v["slot_exp"], v["slot_state"])
+            say(f"step {step} T={T} phase {phase} slots {list(v['slot_exp'])} states {list(v['slot_state'])}")
+            x = tokens(500 + step, T, spec.d_model)
+            if phase == "Bg":
+                lib.llapis_set_tuning(0, 0)
+            try:
+                out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+                torch.cuda.synchronize()
+            finally:
+                lib.llapis_set_tuning(0, 1)
+            ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+            vl = _view_layer(lay_all, src_s, v["exp_slot"], v["slot_exp"], v["slot_state"])
+            vl.router_b = bias
+            ids_o, _, _ = oracle.router(x, vl.router_w, bias, top_k)
+            assert np.array_equal(ids_h, ids_o)
+            out_o, _ = oracle.moe_experts(vl, x, ids_h, w_h, la.ACT_CPU, la.GELU_TABLE)
+            err = rel_l2(out.cpu().numpy(), out_o)
+            assert err <= 1e-4, (step, err)
+            for e in ids_h.ravel():
+                s = int(v["exp_slot"][e])
+                if s >= 0 and v["slot_state"][s] == la.SLOT_FILLING:
+                    log["filling_served_cold"] += 1
+                if res.is_hot(int(e)) and s >= 0 and int(e) >= K:
+                    log["promoted_used_hot"] += 1
+            expect["counts"] += np.bincount(ids_h.ravel(), minlength=E)
+            hot = sum(res.is_hot(int(e)) for e in ids_h.ravel())
+            expect["hot"] += hot
+            expect["cold"] += ids_h.size - hot
+            if phase == "Bp":
+                pol.prompt_tokens(T)
+            else:
+                pol.token_end()                   # fetch -> decide -> submit / publish FILLING
+            assert lib.llapis_xfer_flush(x_eng, stream) == 0
+        pol.refresh(L.REFRESH_TURN_END)
+        assert lib.llapis_xfer_wait_idle(x_eng, stream) == 0
+        n = lib.llapis_xfer_take_done(x_eng, done, 64)
+        for d in done[:n]:
+            if pol.complete(d.il, d.slot, d.e) == 1:
+                log["completed"] += 1
+        publish(0)
+        torch.cuda.synchronize()
+        # every READY slot holds its expert's bytes, bit for bit
+        v = pol.views(0)
+        hg, hd, hs = dl.hot_gu.cpu().numpy(), dl.hot_dn.cpu().numpy(), dl.s_hot.cpu().numpy()
+        for s in range(K):
+            e = int(v["slot_exp"][s])
+            assert v["slot_state"][s] == la.SLOT_READY and e >= 0
+            assert np.array_equal(hg[s * gb:(s + 1) * gb], lay_all.hot_gu[e * gb:(e + 1) * gb])
+            assert np.array_equal(hd[s * db:(s + 1) * db], lay_all.hot_dn[e * db:(e + 1) * db])
+            assert hs[s] == src_s[e]
+        st = pol.stats()
+        say(f"loop: {log}; policy promotions {st['promotions']} demotions {st['demotions']} "
+            f"hit rate {pol.hit_rate():.3f}")
+        assert log["fetches"] == len(plan)
+        assert log["submitted"] >= 6 and log["completed"] == log["submitted"] == st["fills_completed"]
+        assert st["demotions"] >= 4
+        assert log["filling_served_cold"] > 0 and log["promoted_used_hot"] > 0
+        assert set(int(e) for e in v["slot_exp"]) <= set(range(8))      # phase B's experts hold the slots
+    finally:
+        lib.llapis_xfer_free(x_eng)
+        pol.close()
