@@ -332,6 +332,9 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
                 pol.token_end()                   # fetch -> decide -> submit / publish FILLING
             assert lib.llapis_xfer_flush(x_eng, stream) == 0
         pol.refresh(L.REFRESH_TURN_END)
+        # one pull per decision: each visible token and the turn end (the
+        # prompt chunk's counts wait for the turn end)
+        assert log["fetches"] == len(plan)
         assert lib.llapis_xfer_wait_idle(x_eng, stream) == 0
         n = lib.llapis_xfer_take_done(x_eng, done, 64)
         for d in done[:n]:
@@ -351,7 +354,6 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
         st = pol.stats()
         say(f"loop: {log}; policy promotions {st['promotions']} demotions {st['demotions']} "
             f"hit rate {pol.hit_rate():.3f}")
-        assert log["fetches"] == len(plan)
         assert log["submitted"] >= 6 and log["completed"] == log["submitted"] == st["fills_completed"]
         assert st["demotions"] >= 4
         assert log["filling_served_cold"] > 0 and log["promoted_used_hot"] > 0
