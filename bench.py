@@ -12,7 +12,8 @@ layer replica (and token) so the bytes touched per cycle exceed the 256 MB
 MALL: the HBM rate is HBM, not cache.
 
 Also reported (extra): all-Q4_K decode, the dual-precision K=57 4-token
-decode, and the dual-precision 512-token prefill (grouped MFMA GEMMs; int8
+decode, the promotion path (expert copies into hot slots, alone and beside
+the decode), and the dual-precision 512-token prefill (grouped MFMA GEMMs; int8
 TOP/s = 2 x 11 894 784 ops per routed pair, against the int8 peak and against
 the attainable min(peak, arithmetic intensity x HBM)), each with its own
 roofline; the dominant kernel's duration is timed live with HIP events on the
@@ -245,6 +246,114 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     return res
 
 
+def run_promote(la, torch, full, dual, spec, dev, jobs=256, steps=256):
+    """The promotion path: one promotion copies an expert's Q4_K gate_up and
+    Q5_0 down pages (3 593 216 B) from the promotion source in HBM (all 128
+    experts, 460 MB, rotated so the MALL does not hold them) into a slot of a
+    spare slab, through the promotion engine (llapis_xfer_*).  Measured alone
+    (back-to-back jobs per copy mode: hipMemcpyAsync, or the copy kernel with
+    8 / 32 / 128 workgroups) and overlapped with the K=57 4-token decode
+    (graph replays on the compute stream while 4 promotions per decode step
+    run on the engine's stream): the decode slowdown and the promotion rate."""
+    lib = la.lib()
+    E = spec.n_expert
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    per = gb + db
+    NS = 16
+    src_gu = torch.from_numpy(full.hot_gu).to(dev)
+    src_dn = torch.from_numpy(full.hot_dn).to(dev)
+    dst_gu = torch.zeros(NS * gb, dtype=torch.uint8, device=dev)
+    dst_dn = torch.zeros(NS * db, dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    done = (la._lib.LlapisXferDone * 1024)()
+
+    def engine(wgs):
+        x = lib.llapis_xfer_create(1, E, NS, wgs)
+        if not x:
+            raise RuntimeError(lib.llapis_xfer_last_error().decode())
+        for g, (d, src, b) in enumerate(((dst_gu, src_gu, gb), (dst_dn, src_dn, db))):
+            if lib.llapis_xfer_set_group(x, 0, g, d.data_ptr(), src.data_ptr(), b, b) != 0:
+                raise RuntimeError(lib.llapis_xfer_last_error().decode())
+        return x
+
+    def issue(x, n, k0):
+        for i in range(n):
+            lib.llapis_xfer_submit(x, 0, ((k0 + i) * 37) % E, (k0 + i) % NS)
+        lib.llapis_xfer_flush(x, s)
+
+    def drain(x):
+        lib.llapis_xfer_wait_idle(x, s)
+        while lib.llapis_xfer_take_done(x, done, 1024) > 0:
+            pass
+
+    alone = {}
+    for wgs in (0, 8, 32, 128):
+        x = engine(wgs)
+        issue(x, 16, 0)
+        drain(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        issue(x, jobs, 16)
+        drain(x)
+        us = (time.perf_counter() - t0) * 1e6 / jobs
+        alone[str(wgs)] = {"us_per_promotion": us, "gbs": 2 * per / (us * 1e-6) / 1e9}
+        lib.llapis_xfer_free(x)
+        log(f"[promote] copy mode {'hipMemcpyAsync' if wgs == 0 else f'kernel x{wgs} WGs'}: {us:.2f} us per "
+            f"promotion, {alone[str(wgs)]['gbs']:.0f} GB/s (read + write)")
+    # overlap with the dual 4-token decode, replayed as a graph
+    wl = Workload(la, torch, dual, 1, 4, 16, 1234, dev, 0, 0)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(8):
+            wl.step(i, stream.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(16):
+            wl.step(i, stream.cuda_stream)
+    reps = steps // 16
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def decode_ms():
+        e0.record(torch.cuda.current_stream())
+        for _ in range(reps):
+            g.replay()
+        e1.record(torch.cuda.current_stream())
+        return e0, e1
+
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    a, b = decode_ms()
+    torch.cuda.synchronize()
+    base_us = a.elapsed_time(b) * 1e3 / (reps * 16)
+    over = {}
+    for wgs in (0, 32, 128):
+        x = engine(wgs)
+        issue(x, 8, 0)
+        drain(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        issue(x, 4 * reps * 16, 0)          # queued first: the copies run beside the replays
+        a, b = decode_ms()
+        b.synchronize()
+        t_dec = time.perf_counter() - t0
+        drain(x)
+        t_all = time.perf_counter() - t0
+        us = a.elapsed_time(b) * 1e3 / (reps * 16)
+        over[str(wgs)] = {"decode_us_per_step": us, "slowdown": us / base_us,
+                          "promotions_per_s": 4 * reps * 16 / t_all,
+                          "copies_done_with_decode": t_all <= 1.05 * t_dec}
+        lib.llapis_xfer_free(x)
+        log(f"[promote] decode T=4 with 4 promotions per step ({'hipMemcpyAsync' if wgs == 0 else f'kernel x{wgs}'}): "
+            f"{us:.1f} us/step vs {base_us:.1f} alone (x{us / base_us:.2f}); {over[str(wgs)]['promotions_per_s']:.0f} "
+            "promotions/s")
+    del wl, src_gu, src_dn, dst_gu, dst_dn
+    torch.cuda.empty_cache()
+    return {"bytes_per_promotion": per, "alone": alone, "decode_alone_us_per_step": base_us,
+            "with_decode": over}
+
+
 def copy_ceiling(torch, dev, nbytes, reps=400):
     """GB/s that a plain device-to-device copy moving `nbytes` per launch (half
     read, half written) reaches, rotated over >= 512 MB of buffers so the MALL
@@ -439,8 +548,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack",
-                    help="comma list of iq2s,q4k,dual,prefill,stack")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack,promote",
+                    help="comma list of iq2s,q4k,dual,prefill,stack,promote")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
@@ -476,7 +585,7 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = "q4k" in cfgs or "dual" in cfgs or "prefill" in cfgs or "stack" in cfgs
+    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "stack", "promote"))
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -489,7 +598,7 @@ def main():
         results["iq2s"] = run_config(la, torch, "decode all-IQ2_S T=1", cold_only, 1, args.steps, args.warmup, dev)
     if "q4k" in cfgs:
         results["q4k"] = run_config(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev)
-    if "dual" in cfgs or "prefill" in cfgs:
+    if "dual" in cfgs or "prefill" in cfgs or "promote" in cfgs:
         dual = copy.copy(full)
         gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
         dual.hot_gu = np.concatenate([full.hot_gu[e * gb:(e + 1) * gb] for e in hot57])
@@ -503,11 +612,16 @@ def main():
         if "prefill" in cfgs:
             results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
+        if "promote" in cfgs:
+            results["promote"] = run_promote(la, torch, full, dual, spec, dev)
 
     if "stack" in cfgs:
         results["stack"] = run_stack(la, torch, full, spec, dev)
 
-    head = results.get("iq2s") or next(iter(v for v in results.values() if "tok_per_s" in v))
+    head = results.get("iq2s") or next(iter(v for v in results.values() if "tok_per_s" in v), None)
+    if head is None:
+        print(json.dumps({"extra": results}))
+        return
     workload = "decode_all_iq2s_1tok" if "iq2s" in results else None
     roof = {"bound": "hbm", "achieved": head["dominant_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": head["dominant_gbs"] / HBM_PEAK_GBS,

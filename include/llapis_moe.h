@@ -172,8 +172,10 @@ int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspa
  * the engine's own stream only after all work already queued on
  * after_stream -- so publish the mirrors that mark the slots FILLING (and
  * queue every fire that may still read the old experts) before flushing.
- * Each job is one copy kernel of copy_wgs workgroups over its page groups
- * (device sources; copy_wgs 0, or a pinned host source: hipMemcpyAsync). */
+ * The pages of device sources move in copy kernels of at most copy_wgs
+ * workgroups (one launch per 96 pages of a flush), so the copies leave the
+ * other CUs to the decode; copy_wgs 0, or a pinned host source:
+ * hipMemcpyAsync.  The jobs of one flush complete together. */
 #define LLAPIS_XFER_MAX_GROUPS 4
 typedef struct llapis_xfer llapis_xfer;
 typedef struct llapis_xfer_done {

@@ -15,11 +15,12 @@
 //    the copy stream waits on that event on the device.
 //  * The promotion engine (llapis_xfer_*): the job of moe_xfer plus the
 //    memmgr's promote (src/moe_xfer.hpp:55-110, memmgr.h:147-158) when both
-//    tiers live in HBM.  A promotion is one copy kernel per job (all of the
-//    expert's page groups) on a side stream.  flush() orders the copies after
-//    everything already queued on the compute stream with an event (this is
-//    what the reference's worker thread, read staging and host gate provide);
-//    completion is an event per job, polled by take_done().
+//    tiers live in HBM.  flush() issues every pending job's page copies on a
+//    side stream as copy kernels of a bounded number of workgroups (one launch
+//    per 96 page runs), ordered after everything already queued on the
+//    compute stream by an event (this is what the reference's worker thread,
+//    read staging and host gate provide); completion is an event per flush,
+//    polled by take_done().
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -53,40 +54,51 @@ namespace {
 
 constexpr int COPY_WG = 256;
 constexpr int MAX_RUNS = LLAPIS_XFER_MAX_GROUPS;
+constexpr int BATCH_RUNS = 96;             // byte runs per launch (kernel arguments < 4 KiB)
+constexpr uint64_t CHUNK = 65536;          // bytes one workgroup copies at a time
 
 struct CopyRun {
     const uint8_t * src;
     uint8_t * dst;
     uint64_t n;
 };
-struct CopyJob {
-    CopyRun run[MAX_RUNS];
+// Up to BATCH_RUNS runs cut into CHUNK-byte chunks; first[r] is the index of
+// run r's first chunk, first[n_runs] the number of chunks.
+struct CopyBatch {
+    CopyRun run[BATCH_RUNS];
+    uint32_t first[BATCH_RUNS + 1];
     int n_runs;
 };
 
-// Grid-stride copy of up to MAX_RUNS byte runs.  16-byte aligned runs whose
-// length is a multiple of 16 move as 128-bit loads, four in flight per lane;
+// Workgroup w copies chunks w, w + gridDim.x, ... (the grid is the number of
+// workgroups the copies may occupy).  A chunk of a 16-byte aligned run whose
+// length is a multiple of 16 moves as 128-bit loads, four in flight per lane;
 // anything else (a 4-byte scale page) byte by byte.
-__global__ __launch_bounds__(COPY_WG) void k_page_copy(const CopyJob j) {
-    const uint64_t tid = (uint64_t)blockIdx.x * COPY_WG + threadIdx.x;
-    const uint64_t step = (uint64_t)gridDim.x * COPY_WG;
-    for (int r = 0; r < j.n_runs; ++r) {
-        const CopyRun c = j.run[r];
-        if ((((uintptr_t)c.src | (uintptr_t)c.dst | c.n) & 15) == 0) {
-            const dev::u32x4 * s = (const dev::u32x4 *)c.src;
-            dev::u32x4 * d = (dev::u32x4 *)c.dst;
-            const uint64_t n16 = c.n >> 4;
-            uint64_t i = tid;
-            for (; i + 3 * step < n16; i += 4 * step) {
-                const dev::u32x4 a0 = s[i], a1 = s[i + step], a2 = s[i + 2 * step], a3 = s[i + 3 * step];
+__global__ __launch_bounds__(COPY_WG) void k_page_copy(const CopyBatch b) {
+    const uint32_t total = b.first[b.n_runs];
+    for (uint32_t c = blockIdx.x; c < total; c += gridDim.x) {
+        int r = 0;
+        while (r + 1 < b.n_runs && b.first[r + 1] <= c) ++r;
+        const CopyRun run = b.run[r];
+        const uint64_t off = (uint64_t)(c - b.first[r]) * CHUNK;
+        const uint64_t n = min(CHUNK, run.n - off);
+        const uint8_t * src = run.src + off;
+        uint8_t * dst = run.dst + off;
+        if ((((uintptr_t)src | (uintptr_t)dst | n) & 15) == 0) {
+            const dev::u32x4 * s = (const dev::u32x4 *)src;
+            dev::u32x4 * d = (dev::u32x4 *)dst;
+            const int n16 = (int)(n >> 4);
+            int i = threadIdx.x;
+            for (; i + 3 * COPY_WG < n16; i += 4 * COPY_WG) {
+                const dev::u32x4 a0 = s[i], a1 = s[i + COPY_WG], a2 = s[i + 2 * COPY_WG], a3 = s[i + 3 * COPY_WG];
                 d[i] = a0;
-                d[i + step] = a1;
-                d[i + 2 * step] = a2;
-                d[i + 3 * step] = a3;
+                d[i + COPY_WG] = a1;
+                d[i + 2 * COPY_WG] = a2;
+                d[i + 3 * COPY_WG] = a3;
             }
-            for (; i < n16; i += step) d[i] = s[i];
+            for (; i < n16; i += COPY_WG) d[i] = s[i];
         } else {
-            for (uint64_t i = tid; i < c.n; i += step) c.dst[i] = c.src[i];
+            for (int i = threadIdx.x; i < (int)n; i += COPY_WG) dst[i] = src[i];
         }
     }
 }
@@ -104,15 +116,31 @@ SrcKind src_kind(const void * p) {
     return SRC_PAGEABLE;
 }
 
-hipError_t launch_copy(const CopyJob & j, int wgs, hipStream_t s) {
-    if (j.n_runs <= 0) return hipSuccess;
-    uint64_t most = 0;
-    for (int r = 0; r < j.n_runs; ++r) most = std::max(most, j.run[r].n);
-    const uint64_t need = (most / 16 + COPY_WG - 1) / COPY_WG;
-    const int grid = (int)std::max<uint64_t>(1, std::min<uint64_t>((uint64_t)wgs, need));
-    hipLaunchKernelGGL(k_page_copy, dim3(grid), dim3(COPY_WG), 0, s, j);
-    return hipGetLastError();
-}
+// Collects runs and launches one copy kernel per BATCH_RUNS of them.
+struct Batcher {
+    CopyBatch b = {};
+    int wgs;
+    hipStream_t s;
+    hipError_t err = hipSuccess;
+    Batcher(int wgs_, hipStream_t s_) : wgs(wgs_), s(s_) {}
+    void add(const uint8_t * src, uint8_t * dst, uint64_t n) {
+        if (!n) return;
+        if (b.n_runs == BATCH_RUNS) launch();
+        b.first[b.n_runs + 1] = b.first[b.n_runs] + (uint32_t)((n + CHUNK - 1) / CHUNK);
+        b.run[b.n_runs++] = {src, dst, n};
+    }
+    hipError_t launch() {
+        if (b.n_runs > 0 && err == hipSuccess) {
+            const uint32_t chunks = b.first[b.n_runs];
+            const int grid = (int)std::max<uint32_t>(1, std::min<uint32_t>((uint32_t)wgs, chunks));
+            hipLaunchKernelGGL(k_page_copy, dim3(grid), dim3(COPY_WG), 0, s, b);
+            err = hipGetLastError();
+        }
+        b.n_runs = 0;
+        b.first[0] = 0;
+        return err;
+    }
+};
 
 // ------------------------------------------------------- batch transport
 
@@ -247,10 +275,9 @@ int32_t moert_cuda_dir_async(void * dst_dev, const void * src, uint64_t nbytes) 
         d.span_used[d.last_span] = true;
         ++d.ring_copies;
     } else if (k == SRC_DEVICE && d.wgs > 0) {
-        CopyJob j = {};
-        j.run[0] = {(const uint8_t *)src, (uint8_t *)dst_dev, nbytes};
-        j.n_runs = 1;
-        MOERT_HIP_CHECK(launch_copy(j, d.wgs, d.st));
+        Batcher bt(d.wgs, d.st);
+        bt.add((const uint8_t *)src, (uint8_t *)dst_dev, nbytes);
+        MOERT_HIP_CHECK(bt.launch());
         ++d.kernel_copies;
     } else {
         MOERT_HIP_CHECK(hipMemcpyAsync(dst_dev, src, (size_t)nbytes, hipMemcpyDefault, d.st));
@@ -410,12 +437,16 @@ struct llapis_xfer {
     hipStream_t st = nullptr;
     hipEvent_t after = nullptr;
     std::mutex mu;
-    struct Job {
-        llapis_xfer_done d;
+    // the jobs of one flush, finished when ev has completed (next = the
+    // first job not yet handed out by take_done)
+    struct Batch {
+        std::vector<llapis_xfer_done> jobs;
+        size_t next;
         hipEvent_t ev;
     };
     std::vector<llapis_xfer_done> pending;
-    std::deque<Job> live;
+    std::deque<Batch> live;
+    long long n_live = 0;              // jobs in live not yet handed out
     std::vector<hipEvent_t> ev_pool;
     llapis_xfer_stats s = {};
     Group & g(int il, int gi) { return groups[(size_t)il * MAX_RUNS + gi]; }
@@ -442,7 +473,7 @@ llapis_xfer * llapis_xfer_create(int32_t n_layers, int32_t n_expert, int32_t k_s
     x->n_layers = n_layers;
     x->n_expert = n_expert;
     x->k_slots = k_slots;
-    x->wgs = copy_wgs;
+    x->wgs = std::min<int32_t>(copy_wgs, 4096);
     x->groups.resize((size_t)n_layers * MAX_RUNS);
     if (hipStreamCreateWithFlags(&x->st, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&x->after, hipEventDisableTiming) != hipSuccess) {
@@ -457,7 +488,7 @@ llapis_xfer * llapis_xfer_create(int32_t n_layers, int32_t n_expert, int32_t k_s
 void llapis_xfer_free(llapis_xfer * x) {
     if (!x) return;
     (void)hipStreamSynchronize(x->st);
-    for (auto & j : x->live) (void)hipEventDestroy(j.ev);
+    for (auto & b : x->live) (void)hipEventDestroy(b.ev);
     for (auto e : x->ev_pool) (void)hipEventDestroy(e);
     (void)hipEventDestroy(x->after);
     (void)hipStreamDestroy(x->st);
@@ -504,42 +535,47 @@ int32_t llapis_xfer_flush(llapis_xfer * x, void * after_stream) {
         return xfail("llapis_xfer_flush: could not order the copies after the compute stream");
     }
     x->s.max_queue = std::max<long long>(x->s.max_queue, (long long)x->pending.size());
+    // device sources: one copy kernel per BATCH_RUNS page runs; pinned
+    // sources (or no copy workgroups): the runtime's asynchronous copies
+    Batcher bt(x->wgs, x->st);
+    bool ok = true;
     for (const llapis_xfer_done & d : x->pending) {
-        llapis_xfer::Job j = {d, nullptr};
-        CopyJob cj = {};
-        bool engine_ok = true;
         for (int gi = 0; gi < MAX_RUNS; ++gi) {
             const llapis_xfer::Group & g = x->g(d.il, gi);
             if (!g.slab) continue;
             const uint8_t * src = g.src + (uint64_t)d.e * g.stride;
             uint8_t * dst = g.slab + (uint64_t)d.slot * g.bytes;
             if (g.kind == SRC_DEVICE && x->wgs > 0) {
-                cj.run[cj.n_runs++] = {src, dst, g.bytes};
+                bt.add(src, dst, g.bytes);
             } else if (hipMemcpyAsync(dst, src, g.bytes, hipMemcpyDefault, x->st) != hipSuccess) {
                 (void)hipGetLastError();
-                engine_ok = false;
+                ok = false;
             }
             x->s.bytes += (long long)g.bytes;
         }
-        const bool ok = engine_ok && launch_copy(cj, x->wgs, x->st) == hipSuccess;
-        if (!ok) (void)hipGetLastError();
-        j.d.ok = ok ? 1 : 0;
-        if (x->ev_pool.empty()) {
-            if (hipEventCreateWithFlags(&j.ev, hipEventDisableTiming) != hipSuccess) {
-                (void)hipGetLastError();
-                return xfail("llapis_xfer_flush: event creation failed");
-            }
-        } else {
-            j.ev = x->ev_pool.back();
-            x->ev_pool.pop_back();
-        }
-        if (hipEventRecord(j.ev, x->st) != hipSuccess) {
-            (void)hipGetLastError();
-            return xfail("llapis_xfer_flush: event record failed");
-        }
-        x->live.push_back(j);
     }
+    if (bt.launch() != hipSuccess) {
+        (void)hipGetLastError();
+        ok = false;
+    }
+    llapis_xfer::Batch b = {std::move(x->pending), 0, nullptr};
     x->pending.clear();
+    for (auto & d : b.jobs) d.ok = ok ? 1 : 0;
+    if (x->ev_pool.empty()) {
+        if (hipEventCreateWithFlags(&b.ev, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return xfail("llapis_xfer_flush: event creation failed");
+        }
+    } else {
+        b.ev = x->ev_pool.back();
+        x->ev_pool.pop_back();
+    }
+    if (hipEventRecord(b.ev, x->st) != hipSuccess) {
+        (void)hipGetLastError();
+        return xfail("llapis_xfer_flush: event record failed");
+    }
+    x->n_live += (long long)b.jobs.size();
+    x->live.push_back(std::move(b));
     return 0;
 }
 
@@ -548,21 +584,28 @@ int32_t llapis_xfer_take_done(llapis_xfer * x, llapis_xfer_done * out, int32_t m
     std::lock_guard<std::mutex> lk(x->mu);
     int32_t n = 0;
     while (n < max_out && !x->live.empty()) {
-        const hipError_t e = hipEventQuery(x->live.front().ev);
-        if (e == hipErrorNotReady) {
-            (void)hipGetLastError();
-            break;
+        llapis_xfer::Batch & b = x->live.front();
+        if (b.next == 0) {   // not yet known to be finished
+            const hipError_t e = hipEventQuery(b.ev);
+            if (e == hipErrorNotReady) {
+                (void)hipGetLastError();
+                break;
+            }
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                for (auto & d : b.jobs) d.ok = 0;
+            }
         }
-        llapis_xfer::Job j = x->live.front();
+        while (n < max_out && b.next < b.jobs.size()) {
+            const llapis_xfer_done & d = b.jobs[b.next++];
+            out[n++] = d;
+            --x->n_live;
+            if (d.ok) ++x->s.completed;
+            else ++x->s.failed;
+        }
+        if (b.next < b.jobs.size()) break;
+        x->ev_pool.push_back(b.ev);
         x->live.pop_front();
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            j.d.ok = 0;
-        }
-        out[n++] = j.d;
-        x->ev_pool.push_back(j.ev);
-        if (j.d.ok) ++x->s.completed;
-        else ++x->s.failed;
     }
     return n;
 }
@@ -570,7 +613,7 @@ int32_t llapis_xfer_take_done(llapis_xfer * x, llapis_xfer_done * out, int32_t m
 int64_t llapis_xfer_in_flight(llapis_xfer * x) {
     if (!x) return 0;
     std::lock_guard<std::mutex> lk(x->mu);
-    return (int64_t)(x->pending.size() + x->live.size());
+    return (int64_t)x->pending.size() + x->n_live;
 }
 
 int32_t llapis_xfer_wait_idle(llapis_xfer * x, void * after_stream) {

@@ -361,3 +361,42 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
     finally:
         lib.llapis_xfer_free(x_eng)
         pol.close()
+
+
+def test_xfer_large_flush_split_into_launches(gpu):
+    """A flush of 40 jobs x 3 pages (two copy launches), pages that are not
+    a multiple of the copy chunk or of 16 bytes, and completions handed out a
+    few at a time."""
+    torch = torch_mod()
+    lib = la.lib()
+    rng = np.random.default_rng(11)
+    E, K = 50, 40
+    sizes = [200_000, 1000, 4]
+    src_h = [rng.integers(0, 256, E * b, dtype=np.uint8) for b in sizes]
+    src = [u8(torch, a, gpu) for a in src_h]
+    slab = [torch.zeros(K * b, dtype=torch.uint8, device=gpu) for b in sizes]
+    x = lib.llapis_xfer_create(1, E, K, 16)
+    assert x
+    try:
+        for g, b in enumerate(sizes):
+            assert lib.llapis_xfer_set_group(x, 0, g, slab[g].data_ptr(), src[g].data_ptr(), b, b) == 0
+        jobs = [(0, int(e), s) for s, e in enumerate(rng.permutation(E)[:K])]
+        for j in jobs:
+            assert lib.llapis_xfer_submit(x, *j) == 0
+        stream = torch.cuda.current_stream().cuda_stream
+        assert lib.llapis_xfer_wait_idle(x, stream) == 0
+        got = []
+        done = (L.LlapisXferDone * 3)()
+        while True:
+            n = lib.llapis_xfer_take_done(x, done, 3)
+            if n == 0:
+                break
+            got += [(d.il, d.e, d.slot, d.ok) for d in done[:n]]
+        assert got == [j + (1,) for j in jobs]
+        assert lib.llapis_xfer_in_flight(x) == 0
+        for g, b in enumerate(sizes):
+            h = slab[g].cpu().numpy()
+            for il, e, s in jobs:
+                assert np.array_equal(h[s * b:(s + 1) * b], src_h[g][e * b:(e + 1) * b]), (g, e, s)
+    finally:
+        lib.llapis_xfer_free(x)
