@@ -214,6 +214,37 @@ int64_t llapis_xfer_in_flight(llapis_xfer * x);
 int32_t llapis_xfer_wait_idle(llapis_xfer * x, void * after_stream);
 void    llapis_xfer_get_stats(llapis_xfer * x, llapis_xfer_stats * out);
 
+/* ------------------------------------------------------------ K re-fit
+ *
+ * Replaces kfit::fit (src/kfit_policy.hpp:38-94), the decision of how many
+ * hot slots per layer fit in device memory, with its four rules unchanged:
+ * pool = slab_now + free (bounded by slab_now + headroom when headroom >= 0);
+ * k = (pool - keep_free) / per_k, lifted to k_min, capped at n_expert, and
+ * capped at pool / per_k (floor_capped); no rebuild within one slot of k_cur
+ * unless the slab is evicted.  Host code.  On one MI355X there is no WDDM
+ * budget (headroom -1) and 288 GB holds every expert, so the usual answer is
+ * k = n_expert; the host then re-lays the slab (moert_policy_resize_k, the
+ * survivors re-streamed into their new slots with llapis_xfer_*) as
+ * slab_rebuild_at_k does (moe_dual_init.cpp:684-790). */
+typedef struct llapis_kfit_inputs {
+    long long free_mib;        /* device-free memory now */
+    long long slab_mib_now;    /* the slab's bytes now; 0 when evicted */
+    long long headroom_mib;    /* per-process budget; < 0: none */
+    long long per_k_mib;       /* one slot across all layers */
+    long long keep_free_mib;   /* margin left unallocated */
+    int32_t   k_cur, k_min, n_expert;
+    int32_t   evicted;
+} llapis_kfit_inputs;
+typedef struct llapis_kfit_decision {
+    int32_t   k;
+    int32_t   rebuild, wddm_bound, floor_capped;
+    long long pool_mib;
+} llapis_kfit_decision;
+void    llapis_kfit(const llapis_kfit_inputs * in, llapis_kfit_decision * out);
+/* Free and total memory of the current device in MiB (hipMemGetInfo):
+ * free_mib for llapis_kfit_inputs.  0 ok, -1 on a HIP error. */
+int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
+
 /* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
  * (default 1), key 1 = gate_up kernel touches the down slabs ahead of the
  * down kernel (default 0: no gain measured),

@@ -79,6 +79,16 @@ class LlapisMoeLayer(C.Structure):
 XFER_MAX_GROUPS = 4
 
 
+class LlapisKfitInputs(C.Structure):
+    _fields_ = [("free_mib", C.c_longlong), ("slab_mib_now", C.c_longlong), ("headroom_mib", C.c_longlong),
+                ("per_k_mib", C.c_longlong), ("keep_free_mib", C.c_longlong), ("k_cur", i32), ("k_min", i32),
+                ("n_expert", i32), ("evicted", i32)]
+
+
+class LlapisKfitDecision(C.Structure):
+    _fields_ = [("k", i32), ("rebuild", i32), ("wddm_bound", i32), ("floor_capped", i32), ("pool_mib", C.c_longlong)]
+
+
 class LlapisXferDone(C.Structure):
     _fields_ = [("il", i32), ("e", i32), ("slot", i32), ("ok", i32)]
 
@@ -204,6 +214,8 @@ SIGNATURES = {
     "llapis_xfer_in_flight": (i64, [vp]),
     "llapis_xfer_wait_idle": (i32, [vp, vp]),
     "llapis_xfer_get_stats": (None, [vp, C.POINTER(LlapisXferStats)]),
+    "llapis_kfit": (None, [C.POINTER(LlapisKfitInputs), C.POINTER(LlapisKfitDecision)]),
+    "llapis_device_memory_mib": (i32, [C.POINTER(C.c_longlong), C.POINTER(C.c_longlong)]),
     **POLICY_SIGNATURES,
 }
 

@@ -14,6 +14,7 @@
 // candidate lists and their orders (:262-300) and the application order of
 // the pairs (:303-315, std::sort on the net saving, as the reference).
 #include "../../include/moert_policy.h"
+#include "../../include/llapis_moe.h"
 
 #include <algorithm>
 #include <chrono>
@@ -540,6 +541,34 @@ const int32_t * moert_policy_hotmap_view(const moert_policy * p, int32_t il) {
 }
 const float * moert_policy_resid_view(const moert_policy * p, int32_t il) {
     return layer_ok(p, il) ? p->resid.data() + p->at(il, 0) : nullptr;
+}
+
+// K re-fit (kfit_policy.hpp:61-94): the slot count the device can hold now.
+void llapis_kfit(const llapis_kfit_inputs * in, llapis_kfit_decision * out) {
+    if (!in || !out) return;
+    llapis_kfit_decision d = {};
+    // one pool for both regimes (a resident slab's bytes are inside free),
+    // bounded by the per-process budget when there is one
+    d.pool_mib = in->slab_mib_now + in->free_mib;
+    if (in->headroom_mib >= 0 && in->slab_mib_now + in->headroom_mib < d.pool_mib) {
+        d.pool_mib = in->slab_mib_now + in->headroom_mib;
+        d.wddm_bound = 1;
+    }
+    const long long per_k = in->per_k_mib > 0 ? in->per_k_mib : 1;
+    const long long affordable = d.pool_mib / per_k;      // physics, before the preference
+    long long k = (d.pool_mib - in->keep_free_mib) / per_k;
+    k = std::max<long long>(k, in->k_min);
+    k = std::min<long long>(k, in->n_expert);
+    if (k > affordable) {
+        k = std::max<long long>(affordable, 1);
+        d.floor_capped = 1;
+    }
+    d.k = (int32_t)k;
+    // hysteresis: a one-slot change is not worth a rebuild, unless the
+    // rebuild is the restore of an evicted slab
+    d.rebuild = in->evicted || d.k <= in->k_cur - 2 || d.k >= in->k_cur + 2;
+    if (!d.rebuild) d.k = in->k_cur;
+    *out = d;
 }
 
 }  // extern "C"

@@ -464,6 +464,17 @@ extern "C" {
 
 const char * llapis_xfer_last_error(void) { return g_xerr; }
 
+int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib) {
+    size_t f = 0, t = 0;
+    if (hipMemGetInfo(&f, &t) != hipSuccess) {
+        (void)hipGetLastError();
+        return xfail("llapis_device_memory_mib: hipMemGetInfo failed");
+    }
+    if (free_mib) *free_mib = (long long)(f >> 20);
+    if (total_mib) *total_mib = (long long)(t >> 20);
+    return 0;
+}
+
 llapis_xfer * llapis_xfer_create(int32_t n_layers, int32_t n_expert, int32_t k_slots, int32_t copy_wgs) {
     if (n_layers <= 0 || n_expert <= 0 || k_slots <= 0 || copy_wgs < 0) {
         xfail("llapis_xfer_create: bad geometry");

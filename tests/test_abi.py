@@ -52,6 +52,8 @@ MIRRORS = {
     "llapis_moe_layer": _lib.LlapisMoeLayer,
     "llapis_xfer_done": _lib.LlapisXferDone,
     "llapis_xfer_stats": _lib.LlapisXferStats,
+    "llapis_kfit_inputs": _lib.LlapisKfitInputs,
+    "llapis_kfit_decision": _lib.LlapisKfitDecision,
     "moert_policy_config": _lib.MoertPolicyConfig,
     "moert_policy_callbacks": _lib.MoertPolicyCallbacks,
     "moert_policy_stats": _lib.MoertPolicyStats,

@@ -400,3 +400,104 @@ def test_xfer_large_flush_split_into_launches(gpu):
                 assert np.array_equal(h[s * b:(s + 1) * b], src_h[g][e * b:(e + 1) * b]), (g, e, s)
     finally:
         lib.llapis_xfer_free(x)
+
+
+def _rebuild_at_k(torch, lib, gpu, pol, lay_all, src, K_new):
+    """slab_rebuild_at_k for one layer: resize the page table, a slab of the
+    new size, every survivor re-streamed into its new slot by the engine,
+    the mirrors published with the new layer."""
+    spec = lay_all.spec
+    E = spec.n_expert
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    assert pol.resize(K_new) == 1
+    v = pol.views(0)
+    live = copy.copy(lay_all)
+    live.residency = la.Residency(E, K_new, v["exp_slot"].copy(), v["slot_exp"].copy(), v["slot_state"].copy())
+    live.hot_gu = np.zeros(K_new * gb, np.uint8)          # the new slab: nothing in it yet
+    live.hot_dn = np.zeros(K_new * db, np.uint8)
+    live.s_hot = np.zeros(K_new, np.float32)
+    dl = la.DeviceLayer(live, gpu)
+    x = lib.llapis_xfer_create(1, E, K_new, 32)
+    assert x
+    try:
+        for g, (slab, s, b) in enumerate(((dl.hot_gu, src[0], gb), (dl.hot_dn, src[1], db), (dl.s_hot, src[2], 4))):
+            assert lib.llapis_xfer_set_group(x, 0, g, slab.data_ptr(), s.data_ptr(), b, b) == 0
+        n = 0
+        for s_, e in enumerate(v["slot_exp"]):
+            if e >= 0:
+                assert lib.llapis_xfer_submit(x, 0, int(e), s_) == 0
+                n += 1
+        assert lib.llapis_xfer_wait_idle(x, torch.cuda.current_stream().cuda_stream) == 0
+        done = (L.LlapisXferDone * 256)()
+        assert lib.llapis_xfer_take_done(x, done, 256) == n
+        assert all(d.ok for d in done[:n])
+    finally:
+        lib.llapis_xfer_free(x)
+    return dl, v
+
+
+def test_refit_k_restreams_survivors(gpu, oracle):
+    """The K re-fit (moe_dual_init.cpp:565-630, 684-790) on one layer: the
+    measured device memory decides K (on 288 GB: every expert); under set
+    budgets the layer shrinks and grows again.  The policy keeps its best
+    residents compacted into slots 0..K-1, the engine re-streams them into a
+    slab of the new size, and the layer's output equals the oracle's under
+    the new page table."""
+    torch = torch_mod()
+    lib = la.lib()
+    spec = FULL16
+    E, K0, top_k = spec.n_expert, 8, spec.top_k
+    lay_all = layer(spec, 81, list(range(E)), scales=True)
+    src_s = lay_all.s_hot.copy()
+    src = (u8(torch, lay_all.hot_gu, gpu), u8(torch, lay_all.hot_dn, gpu), u8(torch, src_s, gpu))
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    pol = Policy(1, E, K0, stream_expert=lambda il, e, s: 1, publish_layer=lambda il: None, cost_reuse=1000.0)
+    for e in range(K0):
+        assert pol.seed(0, e, e) == 1
+    # a routing history that ranks the residents 5 > 2 > 7 > 0 > the rest
+    ids = [5] * 6 + [2] * 5 + [7] * 4 + [0] * 3 + [11] * 9
+    pol.observe(0, np.array(ids, np.int32), len(ids), 1)
+    pol.token_end()
+    free, total = C.c_longlong(), C.c_longlong()
+    assert lib.llapis_device_memory_mib(C.byref(free), C.byref(total)) == 0
+    say(f"refit: device memory free {free.value} MiB of {total.value} MiB")
+    per_k = max(1, (gb + db + 4) >> 20)
+    plan = [("measured", dict(free_mib=free.value, slab_mib_now=K0 * per_k)),
+            ("shrink", dict(free_mib=per_k, slab_mib_now=2 * per_k)),     # pool 3 slots, 0 kept free
+            ("grow", dict(free_mib=6 * per_k, slab_mib_now=3 * per_k))]
+    k_cur = K0
+    rank = [5, 2, 7, 0]
+    for name, kw in plan:
+        inp = L.LlapisKfitInputs(kw["free_mib"], kw["slab_mib_now"], -1, per_k, 0 if name != "measured" else 1024,
+                                 k_cur, 1, E, 0)
+        d = L.LlapisKfitDecision()
+        lib.llapis_kfit(C.byref(inp), C.byref(d))
+        say(f"refit {name}: K {k_cur} -> {d.k} (rebuild {d.rebuild}, pool {d.pool_mib} MiB)")
+        if name == "measured":
+            assert d.k == E and d.rebuild                 # 288 GB: every expert fits
+        elif name == "shrink":
+            assert d.k == 3 and d.rebuild and not d.floor_capped
+        else:
+            assert d.k == 9 and d.rebuild
+        dl, v = _rebuild_at_k(torch, lib, gpu, pol, lay_all, src, d.k)
+        resid = [int(e) for e in v["slot_exp"] if e >= 0]
+        if name == "shrink":
+            assert resid == rank[:3]                       # the best three, compacted in rank order
+        if name == "grow":
+            assert resid == rank[:3] and list(v["slot_state"][:3]) == [la.SLOT_READY] * 3
+        x = tokens(900 + d.k, 4, spec.d_model)
+        out, ids_d, w = dl.forward(torch.from_numpy(x).to(gpu))
+        torch.cuda.synchronize()
+        ids_h, w_h = ids_d.cpu().numpy(), w.cpu().numpy()
+        vl = _view_layer(lay_all, src_s, v["exp_slot"], v["slot_exp"], v["slot_state"])
+        out_o, _ = oracle.moe_experts(vl, x, ids_h, w_h, la.ACT_CPU, la.GELU_TABLE)
+        err = rel_l2(out.cpu().numpy(), out_o)
+        say(f"  K={d.k} residents {resid}: rel_l2 vs oracle {err:.2e}")
+        assert err <= 1e-4
+        # the slab holds each survivor's bytes in its new slot
+        hg = dl.hot_gu.cpu().numpy()
+        for s_, e in enumerate(v["slot_exp"]):
+            if e >= 0:
+                assert np.array_equal(hg[s_ * gb:(s_ + 1) * gb], lay_all.hot_gu[e * gb:(e + 1) * gb])
+        k_cur = d.k
+    pol.close()
