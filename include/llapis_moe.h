@@ -214,6 +214,58 @@ int64_t llapis_xfer_in_flight(llapis_xfer * x);
 int32_t llapis_xfer_wait_idle(llapis_xfer * x, void * after_stream);
 void    llapis_xfer_get_stats(llapis_xfer * x, llapis_xfer_stats * out);
 
+/* ------------------------------------------------------------ model files
+ *
+ * The on-disk sources of expert pages, read into device memory.  GGUF model
+ * files (versions 2 and 3 of the format ggml's gguf.cpp reads): the tensor
+ * table with absolute file offsets, and the stacked expert tensors
+ * blk.L.ffn_{gate_up,down}_exps.{weight,scale} as the page groups the
+ * memmgr registers from them (moe_dual_init.cpp:230-263: the expert axis is
+ * the highest dimension equal to n_expert, bytes per expert its stride).
+ * The expert store is in moert_store.h.  Uploads read the file with pread
+ * into two pinned staging buffers in turn, each copied to the device with
+ * hipMemcpyAsync on `stream` while the next read runs, and return when the
+ * copies have landed.  Errors: -1 / NULL with llapis_files_last_error(). */
+typedef struct llapis_gguf llapis_gguf;
+typedef struct llapis_gguf_tensor_info {
+    char     name[64];
+    int32_t  type;             /* ggml_type value */
+    int32_t  n_dims;
+    int64_t  ne[4];
+    uint64_t nb[4];            /* 0 for a type this build cannot size */
+    uint64_t offset;           /* absolute file offset of the data */
+    uint64_t nbytes;
+} llapis_gguf_tensor_info;
+typedef struct llapis_page_group {
+    int32_t  type;
+    int32_t  expert_axis;
+    int32_t  n_expert;
+    int32_t  reserved;
+    int64_t  ne[4];
+    uint64_t offset;           /* absolute file offset of expert 0 */
+    uint64_t bytes_per_expert;
+} llapis_page_group;
+const char *  llapis_files_last_error(void);
+llapis_gguf * llapis_gguf_open(const char * path);
+void          llapis_gguf_close(llapis_gguf * g);
+int64_t       llapis_gguf_n_tensors(const llapis_gguf * g);
+uint64_t      llapis_gguf_data_offset(const llapis_gguf * g);
+uint64_t      llapis_gguf_alignment(const llapis_gguf * g);
+int32_t       llapis_gguf_tensor(const llapis_gguf * g, int64_t i, llapis_gguf_tensor_info * out);
+int64_t       llapis_gguf_find(const llapis_gguf * g, const char * name);
+/* kind 0 gate_up, 1 down; is_scale 1 = the .scale tensor.  0 ok. */
+int32_t       llapis_gguf_expert_group(const llapis_gguf * g, int32_t layer, int32_t kind, int32_t is_scale,
+                                       int32_t n_expert, llapis_page_group * out);
+/* experts [e0, e0 + n) of the group into dst (n * bytes_per_expert bytes). */
+int32_t       llapis_gguf_upload(const llapis_gguf * g, const llapis_page_group * grp, int32_t e0, int32_t n,
+                                 void * dst, void * stream);
+/* Pages (layer, kind, is_scale, experts[i]) of an expert store into
+ * dst + i * dst_stride (verify: checksums checked as the bytes stream).  0 ok. */
+struct moert_store_reader;
+int32_t       llapis_store_upload(struct moert_store_reader * r, int32_t layer, int32_t kind, int32_t is_scale,
+                                  const int32_t * experts, int32_t n, void * dst, uint64_t dst_stride,
+                                  int32_t verify, void * stream);
+
 /* ------------------------------------------------------------ K re-fit
  *
  * Replaces kfit::fit (src/kfit_policy.hpp:38-94), the decision of how many

@@ -98,6 +98,50 @@ class LlapisXferStats(C.Structure):
                                             "wait_idle_calls")] + [("wait_idle_ms", C.c_double)]
 
 
+class LlapisGgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("type", i32), ("n_dims", i32), ("ne", i64 * 4), ("nb", u64 * 4),
+                ("offset", u64), ("nbytes", u64)]
+
+
+class LlapisPageGroup(C.Structure):
+    _fields_ = [("type", i32), ("expert_axis", i32), ("n_expert", i32), ("reserved", i32), ("ne", i64 * 4),
+                ("offset", u64), ("bytes_per_expert", u64)]
+
+
+# moert_store.h
+class MoertStoreInfo(C.Structure):
+    _fields_ = [("format_version", C.c_uint32), ("source_uuid", u64), ("arch", C.c_char * 16), ("n_layers", i32),
+                ("n_expert", i32), ("n_embd", u64), ("n_ff_exp", u64), ("pack_uuid", u64), ("record_count", u64)]
+
+
+PAGE_SCALE = 1 << 3
+FNV_SEED = 14695981039346656037
+STORE_SIGNATURES = {
+    "moert_store_probe": (i32, [C.c_char_p, C.POINTER(MoertStoreInfo)]),
+    "moert_store_verify": (i64, [C.c_char_p]),
+    "moert_store_writer_open": (vp, [C.c_char_p, C.c_char_p, C.POINTER(MoertStoreInfo)]),
+    "moert_store_writer_add_page": (i32, [vp, i32, i32, i32, i32, i32, i32, C.c_uint32, vp, i32, vp, u64]),
+    "moert_store_writer_close": (i32, [vp]),
+    "moert_store_fnv1a64": (u64, [vp, u64, u64]),
+    "moert_store_reader_open": (vp, [C.c_char_p, u64]),
+    "moert_store_reader_free": (None, [vp]),
+    "moert_store_reader_geometry": (i32, [vp, vp, vp]),
+    "moert_store_reader_page_nbytes": (u64, [vp, i32, i32, i32, i32]),
+    "moert_store_reader_page_info": (i32, [vp, i32, i32, i32, i32, vp, vp, vp]),
+    "moert_store_reader_read": (u64, [vp, i32, i32, i32, i32, vp, u64, i32]),
+}
+
+
+def bind(cdll, table):
+    """Set a signature table on a loaded library (this one, or a checker
+    exporting the same ABI); returns it."""
+    for name, (res, args) in table.items():
+        fn = getattr(cdll, name)
+        fn.restype = res
+        fn.argtypes = args
+    return cdll
+
+
 # moert_policy.h
 REFRESH_PROMPT_END, REFRESH_VISIBLE_INTERVAL, REFRESH_TURN_END, REFRESH_BOUNDARY = 0, 1, 2, 4
 f32 = C.c_float
@@ -216,7 +260,19 @@ SIGNATURES = {
     "llapis_xfer_get_stats": (None, [vp, C.POINTER(LlapisXferStats)]),
     "llapis_kfit": (None, [C.POINTER(LlapisKfitInputs), C.POINTER(LlapisKfitDecision)]),
     "llapis_device_memory_mib": (i32, [C.POINTER(C.c_longlong), C.POINTER(C.c_longlong)]),
+    "llapis_files_last_error": (C.c_char_p, []),
+    "llapis_gguf_open": (vp, [C.c_char_p]),
+    "llapis_gguf_close": (None, [vp]),
+    "llapis_gguf_n_tensors": (i64, [vp]),
+    "llapis_gguf_data_offset": (u64, [vp]),
+    "llapis_gguf_alignment": (u64, [vp]),
+    "llapis_gguf_tensor": (i32, [vp, i64, C.POINTER(LlapisGgufTensorInfo)]),
+    "llapis_gguf_find": (i64, [vp, C.c_char_p]),
+    "llapis_gguf_expert_group": (i32, [vp, i32, i32, i32, i32, C.POINTER(LlapisPageGroup)]),
+    "llapis_gguf_upload": (i32, [vp, C.POINTER(LlapisPageGroup), i32, i32, vp, vp]),
+    "llapis_store_upload": (i32, [vp, i32, i32, i32, vp, i32, vp, u64, i32, vp]),
     **POLICY_SIGNATURES,
+    **STORE_SIGNATURES,
 }
 
 STAGES = ("router", "topk", "gate_up", "down", "combine")

@@ -19,7 +19,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "libllapis_moe.so"
 ARCH = "gfx950"
 
-HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "transfer.hip", "api.hip"]
+HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "transfer.hip", "model_files.hip",
+               "api.hip"]
 HOST_SOURCES = ["quantize.cpp", "policy.cpp"]
 
 

@@ -125,7 +125,7 @@ struct Batcher {
     Batcher(int wgs_, hipStream_t s_) : wgs(wgs_), s(s_) {}
     void add(const uint8_t * src, uint8_t * dst, uint64_t n) {
         if (!n) return;
-        if (b.n_runs == BATCH_RUNS) launch();
+        if (b.n_runs == BATCH_RUNS) (void)launch();
         b.first[b.n_runs + 1] = b.first[b.n_runs] + (uint32_t)((n + CHUNK - 1) / CHUNK);
         b.run[b.n_runs++] = {src, dst, n};
     }

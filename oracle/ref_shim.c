@@ -183,3 +183,49 @@ void ref_layer_free(void * h) {
     ggml_free(L->ctx);
     free(L);
 }
+
+/* ---- GGUF through ggml's own gguf.cpp (the checker of the GGUF reader) ---- */
+#include "gguf.h"
+
+/* Writes n tensors (name, type, rank, ne, data) and two keys with ggml's
+ * writer; alignment 0 keeps the default.  Returns 1 on success. */
+int ref_gguf_write(const char * path, int n, const char * const * names, const int * types, const int * n_dims,
+                   const int64_t * ne, const void * const * data, uint32_t alignment) {
+    struct ggml_init_params ip = {(size_t)(n + 1) * ggml_tensor_overhead(), NULL, true};
+    struct ggml_context * ctx = ggml_init(ip);
+    struct gguf_context * g = gguf_init_empty();
+    gguf_set_val_str(g, "general.architecture", "gemma4");
+    if (alignment) gguf_set_val_u32(g, "general.alignment", alignment);
+    for (int i = 0; i < n; ++i) {
+        struct ggml_tensor * t = ggml_new_tensor(ctx, (enum ggml_type)types[i], n_dims[i], ne + 4 * i);
+        ggml_set_name(t, names[i]);
+        gguf_add_tensor(g, t);
+        gguf_set_tensor_data(g, names[i], data[i]);
+    }
+    const int ok = gguf_write_to_file(g, path, false) ? 1 : 0;
+    gguf_free(g);
+    ggml_free(ctx);
+    return ok;
+}
+
+/* Reads the tensor table with ggml's reader: per tensor its name (64 bytes
+ * each), type, offset relative to the data section and size.  Returns the
+ * tensor count (at most max are written), -1 on failure. */
+int64_t ref_gguf_read(const char * path, uint64_t * data_offset, uint64_t * alignment, int64_t max, char * names,
+                      int * types, uint64_t * offsets, uint64_t * sizes) {
+    struct gguf_init_params p = {true, NULL};
+    struct gguf_context * g = gguf_init_from_file(path, p);
+    if (!g) return -1;
+    *data_offset = gguf_get_data_offset(g);
+    *alignment = gguf_get_alignment(g);
+    const int64_t n = gguf_get_n_tensors(g);
+    for (int64_t i = 0; i < n && i < max; ++i) {
+        strncpy(names + 64 * i, gguf_get_tensor_name(g, i), 63);
+        names[64 * i + 63] = 0;
+        types[i] = (int)gguf_get_tensor_type(g, i);
+        offsets[i] = gguf_get_tensor_offset(g, i);
+        sizes[i] = gguf_get_tensor_size(g, i);
+    }
+    gguf_free(g);
+    return n;
+}

@@ -53,6 +53,9 @@ MIRRORS = {
     "llapis_xfer_done": _lib.LlapisXferDone,
     "llapis_xfer_stats": _lib.LlapisXferStats,
     "llapis_kfit_inputs": _lib.LlapisKfitInputs,
+    "llapis_gguf_tensor_info": _lib.LlapisGgufTensorInfo,
+    "llapis_page_group": _lib.LlapisPageGroup,
+    "moert_store_info": _lib.MoertStoreInfo,
     "llapis_kfit_decision": _lib.LlapisKfitDecision,
     "moert_policy_config": _lib.MoertPolicyConfig,
     "moert_policy_callbacks": _lib.MoertPolicyCallbacks,
@@ -60,6 +63,7 @@ MIRRORS = {
     "moert_policy_window": _lib.MoertPolicyWindow,
 }
 POLICY_STRUCTS = ("moert_policy_config", "moert_policy_callbacks", "moert_policy_stats", "moert_policy_window")
+REF_STORE_HEADER = Path("/root/reference/moert/include/moert/store.h")
 REF_POLICY_HEADER = Path("/root/reference/moert/include/moert/policy.h")
 # structs of the reference header with no ctypes mirror (host callback payloads)
 CALLBACK_STRUCTS = {
@@ -93,7 +97,7 @@ def compile_layouts(tmp_path, header, structs):
 
 def moert_structs():
     out = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items()
-           if k.startswith("moert_") and k not in POLICY_STRUCTS}
+           if k.startswith("moert_") and k not in POLICY_STRUCTS and k != "moert_store_info"}
     out.update(CALLBACK_STRUCTS)
     return out
 
@@ -101,7 +105,8 @@ def moert_structs():
 def test_ctypes_mirror_matches_headers(tmp_path):
     structs = {k: [f[0] for f in v._fields_] for k, v in MIRRORS.items()}
     prog_header = tmp_path / "both.h"
-    prog_header.write_text('#include "moert_hip.h"\n#include "llapis_moe.h"\n#include "moert_policy.h"\n')
+    prog_header.write_text('#include "moert_hip.h"\n#include "llapis_moe.h"\n#include "moert_policy.h"\n'
+                           '#include "moert_store.h"\n')
     got = compile_layouts(tmp_path, str(prog_header), structs)
     for s, cls in MIRRORS.items():
         assert got[(s, "sizeof")] == C.sizeof(cls), s
@@ -124,6 +129,15 @@ def test_policy_structs_match_reference_header(tmp_path):
     ours = compile_layouts(tmp_path, str(INCLUDE / "moert_policy.h"), structs)
     (tmp_path / "r").mkdir()
     theirs = compile_layouts(tmp_path / "r", str(REF_POLICY_HEADER), structs)
+    assert ours == theirs
+
+
+@pytest.mark.skipif(not REF_STORE_HEADER.exists(), reason="reference tree not present")
+def test_store_info_matches_reference_header(tmp_path):
+    structs = {"moert_store_info": [f[0] for f in _lib.MoertStoreInfo._fields_]}
+    ours = compile_layouts(tmp_path, str(INCLUDE / "moert_store.h"), structs)
+    (tmp_path / "r").mkdir()
+    theirs = compile_layouts(tmp_path / "r", str(REF_STORE_HEADER), structs)
     assert ours == theirs
 
 
