@@ -56,10 +56,13 @@ def layer_bytes(spec, n_hot, n_cold, T):
 class Workload:
     """R device replicas of one layer, prebuilt descriptors and buffers."""
 
-    def __init__(self, la, torch, host_layer, R, T, n_tok, seed, dev, act_mode, gelu_mode):
+    def __init__(self, la, torch, host_layer, R, T, n_tok, seed, dev, act_mode, gelu_mode, counts=False):
         self.la, self.torch, self.T, self.R = la, torch, T, R
         self.spec = host_layer.spec
         base = la.DeviceLayer(host_layer, dev, act_mode, gelu_mode)
+        if counts:   # device routing counters on every call (the policy's observation)
+            base.route_counts = torch.zeros(host_layer.spec.n_expert, dtype=torch.int32, device=dev)
+            base.route_hits = torch.zeros(2, dtype=torch.int32, device=dev)
         self.layers = [base]
         for _ in range(R - 1):
             d = la.DeviceLayer.__new__(la.DeviceLayer)
@@ -203,6 +206,12 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     ms_graph, timed = time_graph(wl, steps, warmup)
     ms_eager = time_eager(wl, min(steps, 200), min(warmup, 20))
     st = stage_times(wl, max(2 * R, 64))
+    ms_counts = None
+    if T <= 4:
+        # the same decode with the device routing counters on
+        wlc = Workload(la, torch, host_layer, R, T, 16, seed, dev, act, gelu, counts=True)
+        ms_counts, _ = time_graph(wlc, steps, warmup)
+        del wlc
     sb = stage_bytes(sp, n_hot, n_cold, T, pairs)
     dom = max(("gate_up", "down"), key=lambda k: st[k])
     kernel = ({"gate_up": "k_dec_gate_up", "down": "k_dec_down"} if T <= 4 else
@@ -210,6 +219,7 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     res = {
         "tok_per_s": T * 1e3 / ms_graph,
         "ms_per_step": ms_graph,
+        "ms_per_step_route_counts": ms_counts,
         "ms_per_step_eager": ms_eager,
         "steps_timed": timed,
         "hbm_gbs_step": bytes_step / (ms_graph * 1e-3) / 1e9,
@@ -241,6 +251,8 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
     log(f"[{name}] {res['tok_per_s']:.0f} tok/s, {ms_graph * 1e3:.1f} us/step (eager {ms_eager * 1e3:.1f} us), "
         f"step {res['hbm_gbs_step']:.0f} GB/s, {dom} {res['dominant_gbs']:.0f} GB/s, stages "
         + ", ".join(f"{k} {v * 1e3:.1f}us" for k, v in st.items()))
+    if ms_counts is not None:
+        log(f"[{name}] with device routing counters: {ms_counts * 1e3:.1f} us/step")
     del wl
     torch.cuda.empty_cache()
     return res
