@@ -524,6 +524,135 @@ def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_
     return res
 
 
+def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift_every=64):
+    """The 30-layer decode with the residency loop a server runs: every call
+    counts its routing on the device; after each token the policy pulls the
+    counts (one D2H copy for all layers), decides (cost rule, at most 4
+    promotions per token), publishes the FILLING mirrors and the promotion
+    engine copies the experts from the promotion source in HBM (every expert
+    in the hot formats) on its own stream while the next token runs; finished
+    copies become READY before the next token.  Every `drift_every` tokens
+    each layer's router bias is permuted, so the routing moves away from the
+    resident experts and the policy has to follow.  Token passes are graph
+    replays; the host work between them (fetch, decision, publication) is
+    part of the time."""
+    from llapis_amd.policy import Policy
+    lib = la.lib()
+    t0 = time.time()
+    st = Stack(la, torch, full, spec, n_layers, dev)
+    E, K = spec.n_expert, 57
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    rc = torch.zeros(n_layers * E + 2 * n_layers, dtype=torch.int32, device=dev)
+    for il, d in enumerate(st.layers):
+        d.route_counts = rc[il * E:(il + 1) * E]
+        d.route_hits = rc[n_layers * E + 2 * il:n_layers * E + 2 * il + 2]
+        st.descs[il] = d.desc()
+    src_gu = torch.from_numpy(full.hot_gu).to(dev)       # the promotion source: all experts, hot formats
+    src_dn = torch.from_numpy(full.hot_dn).to(dev)
+    x = lib.llapis_xfer_create(n_layers, E, K, 0)
+    for il, d in enumerate(st.layers):
+        for g, (slab, src, b) in enumerate(((d.hot_gu, src_gu, gb), (d.hot_dn, src_dn, db))):
+            if lib.llapis_xfer_set_group(x, il, g, slab.data_ptr(), src.data_ptr(), b, b) != 0:
+                raise RuntimeError(lib.llapis_xfer_last_error().decode())
+    stream = torch.cuda.Stream()
+    pol = None
+    stats = {"fetch_ms": 0.0, "publish_ms": 0.0, "submitted": 0, "completed": 0, "publishes": 0}
+    hits = []                                   # per pull: (hot pairs, other pairs) over all layers
+
+    def fetch():
+        a = time.perf_counter()
+        h = rc.cpu().numpy()                    # waits for the token's pass
+        rc.zero_()
+        hot = h[n_layers * E::2].sum()
+        hits.append((int(hot), int(h[n_layers * E + 1::2].sum())))
+        for il in range(n_layers):
+            pol.add_counts(il, h[il * E:(il + 1) * E], int(h[n_layers * E + 2 * il]), int(h[n_layers * E + 2 * il + 1]))
+        stats["fetch_ms"] += (time.perf_counter() - a) * 1e3
+
+    def publish(il):
+        a = time.perf_counter()
+        v = pol.views(il)
+        d = st.layers[il]
+        dev_t = [d.exp_slot, d.slot_exp, d.slot_state]
+        host = [v["exp_slot"], v["slot_exp"], v["slot_state"]]
+        dsts = (C.c_void_p * 3)(*[t.data_ptr() for t in dev_t])
+        srcs = (C.c_void_p * 3)(*[h.ctypes.data for h in host])
+        sizes = (C.c_uint64 * 3)(*[h.nbytes for h in host])
+        lib.moert_cuda_publish_h2d(3, dsts, srcs, sizes)
+        stats["publishes"] += 1
+        stats["publish_ms"] += (time.perf_counter() - a) * 1e3
+
+    def stream_expert(il, e, slot):
+        stats["submitted"] += 1
+        return 2 if lib.llapis_xfer_submit(x, il, e, slot) == 0 else 0
+
+    pol = Policy(n_layers, E, K, stream_expert=stream_expert, publish_layer=publish, fetch_external=fetch)
+    pol.set_external(True)
+    for il, d in enumerate(st.layers):
+        se = d.slot_exp.cpu().numpy()
+        for s_, e in enumerate(se):
+            pol.seed(il, int(e), s_)
+    biases = [d.router_b.clone() for d in st.layers]
+    rng = np.random.default_rng(5)
+    T = 1
+    need = int(lib.llapis_moe_ffn_workspace_size(C.byref(st.descs[0]), T))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    h0 = torch.from_numpy(la.synth_normal(4001, spec.d_model).reshape(1, spec.d_model)).to(dev)
+    h, xn, out = h0.clone(), torch.empty_like(h0), torch.zeros_like(h0)
+    with torch.cuda.stream(stream):
+        h.copy_(h0)
+        st.run(h, xn, out, ws, stream.cuda_stream, T)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        h.copy_(h0)
+        st.run(h, xn, out, ws, stream.cuda_stream, T)
+    torch.cuda.synchronize()
+    rc.zero_()
+    done = (la._lib.LlapisXferDone * 4096)()
+    log(f"[stack dynamic] {n_layers} layers, policy + promotion engine ready in {time.time() - t0:.1f} s")
+    t_start = time.perf_counter()
+    for tok in range(tokens):
+        if tok and tok % drift_every == 0:
+            for il, d in enumerate(st.layers):
+                d.router_b.copy_(biases[il][torch.from_numpy(rng.permutation(E)).to(dev)])
+        n = lib.llapis_xfer_take_done(x, done, 4096)
+        touched = set()
+        for j in range(n):
+            if pol.complete(done[j].il, done[j].slot, done[j].e) == 1:
+                stats["completed"] += 1
+                touched.add(done[j].il)
+        for il in sorted(touched):
+            publish(il)
+        g.replay()
+        pol.token_end()                         # fetch (waits for the token), decide, publish FILLING
+        lib.llapis_xfer_flush(x, stream.cuda_stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    lib.llapis_xfer_wait_idle(x, stream.cuda_stream)
+    xs = la._lib.LlapisXferStats()
+    lib.llapis_xfer_get_stats(x, C.byref(xs))
+    pst = pol.stats()
+    lib.llapis_xfer_free(x)
+    pol.close()
+    hw = np.array([hh / max(1, hh + cc) for hh, cc in hits[:tokens]])
+    segs = [float(hw[i:i + drift_every].mean()) for i in range(0, tokens, drift_every)]
+    first = [float(hw[i:i + 8].mean()) for i in range(0, tokens, drift_every)]
+    res = {"layers": n_layers, "tokens": tokens, "ms_per_token": wall * 1e3 / tokens, "tok_per_s": tokens / wall,
+           "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
+           "copies_bytes": int(xs.bytes), "hit_rate_per_phase": segs, "hit_rate_first_8_tokens_per_phase": first,
+           "host_fetch_ms_per_token": stats["fetch_ms"] / tokens, "host_publish_ms_per_token": stats["publish_ms"] / tokens}
+    log(f"[stack dynamic] {tokens} tokens x {n_layers} layers: {res['ms_per_token']:.3f} ms per token "
+        f"({res['tok_per_s']:.0f} tok/s) with the residency loop; {res['promotions']} promotions "
+        f"({xs.bytes / 1e9:.2f} GB copied), hit rate per {drift_every}-token phase "
+        + ", ".join(f"{v:.2f}" for v in segs) + " (first 8 tokens of each: " + ", ".join(f"{v:.2f}" for v in first)
+        + f"); waiting for the token + fetch {res['host_fetch_ms_per_token']:.3f} ms, publish "
+        f"{res['host_publish_ms_per_token']:.3f} ms per token")
+    del st, src_gu, src_dn, ws, rc
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(host_layer, T, budget_s=12.0):
     """The reference's ggml CPU graph (oracle/_ref) on a bounded sample."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -560,8 +689,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack,promote",
-                    help="comma list of iq2s,q4k,dual,prefill,stack,promote")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack,promote,stackdyn",
+                    help="comma list of iq2s,q4k,dual,prefill,stack,promote,stackdyn")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
@@ -597,7 +726,7 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "stack", "promote"))
+    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "stack", "promote", "stackdyn"))
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -629,8 +758,10 @@ def main():
 
     if "stack" in cfgs:
         results["stack"] = run_stack(la, torch, full, spec, dev)
+    if "stackdyn" in cfgs:
+        results["stack_dynamic"] = run_stack_dynamic(la, torch, full, spec, dev)
 
-    head = results.get("iq2s") or next(iter(v for v in results.values() if "tok_per_s" in v), None)
+    head = results.get("iq2s") or next(iter(v for v in results.values() if "dominant_gbs" in v), None)
     if head is None:
         print(json.dumps({"extra": results}))
         return
