@@ -525,73 +525,39 @@ def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_
 
 
 def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift_every=64):
-    """The 30-layer decode with the residency loop a server runs: every call
-    counts its routing on the device; after each token the policy pulls the
-    counts (one D2H copy for all layers), decides (cost rule, at most 4
-    promotions per token), publishes the FILLING mirrors and the promotion
-    engine copies the experts from the promotion source in HBM (every expert
-    in the hot formats) on its own stream while the next token runs; finished
-    copies become READY before the next token.  Every `drift_every` tokens
-    each layer's router bias is permuted, so the routing moves away from the
-    resident experts and the policy has to follow.  Token passes are graph
-    replays; the host work between them (fetch, decision, publication) is
-    part of the time."""
-    from llapis_amd.policy import Policy
+    """The 30-layer decode with the residency loop a server runs, in native
+    code (llapis_residency_*): every call counts its routing on the device;
+    after each token the runtime pulls the counts (one D2H copy for all
+    layers), the policy decides (cost rule, at most 4 promotions per token),
+    the FILLING mirrors are published with copies on the stream and the
+    promotion engine copies the experts from the promotion source in HBM
+    (every expert in the hot formats) on its own stream while the next token
+    runs; finished copies become READY at the next token end.  Every
+    `drift_every` tokens each layer's router bias is permuted, so the routing
+    moves away from the resident experts and the policy has to follow.  Token
+    passes are graph replays; the host work between them is part of the
+    time."""
+    from llapis_amd.policy import ResidencyLoop
     lib = la.lib()
     t0 = time.time()
     st = Stack(la, torch, full, spec, n_layers, dev)
     E, K = spec.n_expert, 57
     gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
-    rc = torch.zeros(n_layers * E + 2 * n_layers, dtype=torch.int32, device=dev)
-    for il, d in enumerate(st.layers):
-        d.route_counts = rc[il * E:(il + 1) * E]
-        d.route_hits = rc[n_layers * E + 2 * il:n_layers * E + 2 * il + 2]
-        st.descs[il] = d.desc()
+    rl = ResidencyLoop(n_layers, E, K, copy_wgs=0)
+    pol = rl.policy
     src_gu = torch.from_numpy(full.hot_gu).to(dev)       # the promotion source: all experts, hot formats
     src_dn = torch.from_numpy(full.hot_dn).to(dev)
-    x = lib.llapis_xfer_create(n_layers, E, K, 0)
     for il, d in enumerate(st.layers):
+        d.route_counts, d.route_hits = rl.counters(il)
+        st.descs[il] = d.desc()
         for g, (slab, src, b) in enumerate(((d.hot_gu, src_gu, gb), (d.hot_dn, src_dn, db))):
-            if lib.llapis_xfer_set_group(x, il, g, slab.data_ptr(), src.data_ptr(), b, b) != 0:
+            if lib.llapis_xfer_set_group(rl.xfer, il, g, slab.data_ptr(), src.data_ptr(), b, b) != 0:
                 raise RuntimeError(lib.llapis_xfer_last_error().decode())
-    stream = torch.cuda.Stream()
-    pol = None
-    stats = {"fetch_ms": 0.0, "publish_ms": 0.0, "submitted": 0, "completed": 0, "publishes": 0}
-    hits = []                                   # per pull: (hot pairs, other pairs) over all layers
-
-    def fetch():
-        a = time.perf_counter()
-        h = rc.cpu().numpy()                    # waits for the token's pass
-        rc.zero_()
-        hot = h[n_layers * E::2].sum()
-        hits.append((int(hot), int(h[n_layers * E + 1::2].sum())))
-        for il in range(n_layers):
-            pol.add_counts(il, h[il * E:(il + 1) * E], int(h[n_layers * E + 2 * il]), int(h[n_layers * E + 2 * il + 1]))
-        stats["fetch_ms"] += (time.perf_counter() - a) * 1e3
-
-    def publish(il):
-        a = time.perf_counter()
-        v = pol.views(il)
-        d = st.layers[il]
-        dev_t = [d.exp_slot, d.slot_exp, d.slot_state]
-        host = [v["exp_slot"], v["slot_exp"], v["slot_state"]]
-        dsts = (C.c_void_p * 3)(*[t.data_ptr() for t in dev_t])
-        srcs = (C.c_void_p * 3)(*[h.ctypes.data for h in host])
-        sizes = (C.c_uint64 * 3)(*[h.nbytes for h in host])
-        lib.moert_cuda_publish_h2d(3, dsts, srcs, sizes)
-        stats["publishes"] += 1
-        stats["publish_ms"] += (time.perf_counter() - a) * 1e3
-
-    def stream_expert(il, e, slot):
-        stats["submitted"] += 1
-        return 2 if lib.llapis_xfer_submit(x, il, e, slot) == 0 else 0
-
-    pol = Policy(n_layers, E, K, stream_expert=stream_expert, publish_layer=publish, fetch_external=fetch)
-    pol.set_external(True)
-    for il, d in enumerate(st.layers):
-        se = d.slot_exp.cpu().numpy()
-        for s_, e in enumerate(se):
+        rl.set_mirrors(il, d.exp_slot.data_ptr(), d.slot_exp.data_ptr(), d.slot_state.data_ptr())
+        for s_, e in enumerate(d.slot_exp.cpu().numpy()):
             pol.seed(il, int(e), s_)
+    stream = torch.cuda.Stream()
+    rl.publish_all(stream.cuda_stream)
     biases = [d.router_b.clone() for d in st.layers]
     rng = np.random.default_rng(5)
     T = 1
@@ -608,47 +574,56 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
         h.copy_(h0)
         st.run(h, xn, out, ws, stream.cuda_stream, T)
     torch.cuda.synchronize()
-    rc.zero_()
-    done = (la._lib.LlapisXferDone * 4096)()
-    log(f"[stack dynamic] {n_layers} layers, policy + promotion engine ready in {time.time() - t0:.1f} s")
+    rl.token_end(stream.cuda_stream)                     # drains the warm-up passes' counts
+    r0 = rl.stats()
+    hits = []                                            # per token: (hot pairs, other pairs) over all layers
+    host_s = 0.0
+    log(f"[stack dynamic] {n_layers} layers, native residency loop ready in {time.time() - t0:.1f} s")
     t_start = time.perf_counter()
-    for tok in range(tokens):
-        if tok and tok % drift_every == 0:
-            for il, d in enumerate(st.layers):
-                d.router_b.copy_(biases[il][torch.from_numpy(rng.permutation(E)).to(dev)])
-        n = lib.llapis_xfer_take_done(x, done, 4096)
-        touched = set()
-        for j in range(n):
-            if pol.complete(done[j].il, done[j].slot, done[j].e) == 1:
-                stats["completed"] += 1
-                touched.add(done[j].il)
-        for il in sorted(touched):
-            publish(il)
-        g.replay()
-        pol.token_end()                         # fetch (waits for the token), decide, publish FILLING
-        lib.llapis_xfer_flush(x, stream.cuda_stream)
+    prev = r0
+    with torch.cuda.stream(stream):
+        for tok in range(tokens):
+            if tok and tok % drift_every == 0:
+                for il, d in enumerate(st.layers):
+                    d.router_b.copy_(biases[il][torch.from_numpy(rng.permutation(E)).to(dev)])
+            g.replay()
+            a = time.perf_counter()
+            rl.token_end(stream.cuda_stream)            # waits for the token, decides, publishes, flushes
+            host_s += time.perf_counter() - a
+            cur = rl.stats()
+            hits.append((cur["hot_pairs"] - prev["hot_pairs"], cur["cold_pairs"] - prev["cold_pairs"]))
+            prev = cur
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    lib.llapis_xfer_wait_idle(x, stream.cuda_stream)
+    lib.llapis_xfer_wait_idle(rl.xfer, stream.cuda_stream)
+    # the same token passes with a wait after each and no residency loop:
+    # what a server's synchronous decode costs without the loop
+    t_sync = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for tok in range(tokens):
+            g.replay()
+            stream.synchronize()
+    sync_ms = (time.perf_counter() - t_sync) * 1e3 / tokens
     xs = la._lib.LlapisXferStats()
-    lib.llapis_xfer_get_stats(x, C.byref(xs))
+    lib.llapis_xfer_get_stats(rl.xfer, C.byref(xs))
     pst = pol.stats()
-    lib.llapis_xfer_free(x)
-    pol.close()
-    hw = np.array([hh / max(1, hh + cc) for hh, cc in hits[:tokens]])
+    rst = rl.stats()
+    rl.close()
+    hw = np.array([hh / max(1, hh + cc) for hh, cc in hits])
     segs = [float(hw[i:i + drift_every].mean()) for i in range(0, tokens, drift_every)]
     first = [float(hw[i:i + 8].mean()) for i in range(0, tokens, drift_every)]
     res = {"layers": n_layers, "tokens": tokens, "ms_per_token": wall * 1e3 / tokens, "tok_per_s": tokens / wall,
-           "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
-           "copies_bytes": int(xs.bytes), "hit_rate_per_phase": segs, "hit_rate_first_8_tokens_per_phase": first,
-           "host_fetch_ms_per_token": stats["fetch_ms"] / tokens, "host_publish_ms_per_token": stats["publish_ms"] / tokens}
+           "loop": "native", "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
+           "publications": int(rst["publications"] - r0["publications"]), "copies_bytes": int(xs.bytes),
+           "hit_rate_per_phase": segs, "hit_rate_first_8_tokens_per_phase": first,
+           "token_end_ms_per_token": host_s * 1e3 / tokens, "sync_no_loop_ms_per_token": sync_ms}
     log(f"[stack dynamic] {tokens} tokens x {n_layers} layers: {res['ms_per_token']:.3f} ms per token "
-        f"({res['tok_per_s']:.0f} tok/s) with the residency loop; {res['promotions']} promotions "
+        f"({res['tok_per_s']:.0f} tok/s) with the native residency loop; {res['promotions']} promotions "
         f"({xs.bytes / 1e9:.2f} GB copied), hit rate per {drift_every}-token phase "
         + ", ".join(f"{v:.2f}" for v in segs) + " (first 8 tokens of each: " + ", ".join(f"{v:.2f}" for v in first)
-        + f"); waiting for the token + fetch {res['host_fetch_ms_per_token']:.3f} ms, publish "
-        f"{res['host_publish_ms_per_token']:.3f} ms per token")
-    del st, src_gu, src_dn, ws, rc
+        + f"); token end (waits for the token's pass) {res['token_end_ms_per_token']:.3f} ms per token; the same "
+        f"passes with a wait after each and no loop: {sync_ms:.3f} ms per token")
+    del st, src_gu, src_dn, ws
     torch.cuda.empty_cache()
     return res
 

@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "moert_hip.h"
+#include "moert_policy.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -213,6 +214,49 @@ int64_t llapis_xfer_in_flight(llapis_xfer * x);
 /* Flush, then block until every copy issued has landed. */
 int32_t llapis_xfer_wait_idle(llapis_xfer * x, void * after_stream);
 void    llapis_xfer_get_stats(llapis_xfer * x, llapis_xfer_stats * out);
+
+/* ------------------------------------------------------ residency loop
+ *
+ * The per-token host loop around the fused op in native code: a policy
+ * (moert_policy.h, external observation), a promotion engine and the
+ * device routing counters of every layer, as moe_dual.cpp drives them
+ * (publish_fence / push_residency moe_dual.cpp:640-705, the batch transport
+ * :862-880, the policy callbacks policy.h:82-104).  Give each layer's
+ * llapis_moe_layer the counters of llapis_residency_counters, register its
+ * mirrors and its engine page groups, seed the policy, publish once; then
+ * after each visible token's layers are queued on `stream` call
+ * llapis_residency_token_end, which (1) hands finished copies to the policy
+ * (READY), (2) runs the per-token decision -- it pulls every layer's counters
+ * with one copy on `stream`, the loop's only wait (for the token), and
+ * submits promotions as FILLING -- (3) publishes the changed layers' mirrors
+ * with copies on `stream` (the next token sees them in stream order) and (4)
+ * flushes the engine, whose copies overlap the next token.  Counts reach the
+ * policy only there (stats reads in between do not pull them). */
+typedef struct llapis_residency llapis_residency;
+typedef struct llapis_residency_stats {
+    long long tokens, fetches, submitted, completed, publications;
+    long long hot_pairs, cold_pairs;     /* routed pairs the counters saw */
+} llapis_residency_stats;
+/* cfg as moert_policy_create's (callbacks are the runtime's own); copy_wgs
+ * as llapis_xfer_create's.  Allocates the counters (device), their pinned
+ * read-back and the publication staging.  NULL on failure. */
+llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int32_t copy_wgs);
+void               llapis_residency_free(llapis_residency * r);
+const char *       llapis_residency_last_error(void);
+/* The policy (seed it, read views and stats) and the engine (set its page
+ * groups) the runtime drives. */
+moert_policy *     llapis_residency_policy(llapis_residency * r);
+llapis_xfer *      llapis_residency_xfer(llapis_residency * r);
+/* Layer il's device mirrors: exp_slot [n_expert], slot_exp and slot_state
+ * [the policy's capacity]. */
+int32_t llapis_residency_set_mirrors(llapis_residency * r, int32_t il, int32_t * exp_slot, int32_t * slot_exp,
+                                     int32_t * slot_state);
+/* Layer il's counters for llapis_moe_layer.route_counts / route_hits. */
+int32_t llapis_residency_counters(llapis_residency * r, int32_t il, int32_t ** counts, int32_t ** hits);
+/* Every layer's mirrors, copied on stream (after seeding). */
+int32_t llapis_residency_publish_all(llapis_residency * r, void * stream);
+int32_t llapis_residency_token_end(llapis_residency * r, void * stream);
+void    llapis_residency_get_stats(llapis_residency * r, llapis_residency_stats * out);
 
 /* ------------------------------------------------------------ model files
  *

@@ -108,6 +108,11 @@ class LlapisPageGroup(C.Structure):
                 ("offset", u64), ("bytes_per_expert", u64)]
 
 
+class LlapisResidencyStats(C.Structure):
+    _fields_ = [(n, C.c_longlong) for n in ("tokens", "fetches", "submitted", "completed", "publications",
+                                            "hot_pairs", "cold_pairs")]
+
+
 # moert_store.h
 class MoertStoreInfo(C.Structure):
     _fields_ = [("format_version", C.c_uint32), ("source_uuid", u64), ("arch", C.c_char * 16), ("n_layers", i32),
@@ -271,6 +276,16 @@ SIGNATURES = {
     "llapis_gguf_expert_group": (i32, [vp, i32, i32, i32, i32, C.POINTER(LlapisPageGroup)]),
     "llapis_gguf_upload": (i32, [vp, C.POINTER(LlapisPageGroup), i32, i32, vp, vp]),
     "llapis_store_upload": (i32, [vp, i32, i32, i32, vp, i32, vp, u64, i32, vp]),
+    "llapis_residency_create": (vp, [vp, i32]),
+    "llapis_residency_free": (None, [vp]),
+    "llapis_residency_last_error": (C.c_char_p, []),
+    "llapis_residency_policy": (vp, [vp]),
+    "llapis_residency_xfer": (vp, [vp]),
+    "llapis_residency_set_mirrors": (i32, [vp, i32, vp, vp, vp]),
+    "llapis_residency_counters": (i32, [vp, i32, C.POINTER(vp), C.POINTER(vp)]),
+    "llapis_residency_publish_all": (i32, [vp, vp]),
+    "llapis_residency_token_end": (i32, [vp, vp]),
+    "llapis_residency_get_stats": (None, [vp, C.POINTER(LlapisResidencyStats)]),
     **POLICY_SIGNATURES,
     **STORE_SIGNATURES,
 }

@@ -20,7 +20,7 @@ LIB = PKG / "libllapis_moe.so"
 ARCH = "gfx950"
 
 HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "transfer.hip", "model_files.hip",
-               "api.hip"]
+               "residency.hip", "api.hip"]
 HOST_SOURCES = ["quantize.cpp", "policy.cpp"]
 
 

@@ -1,0 +1,248 @@
+// residency.hip -- the per-token residency loop in native code: device
+// routing counters, the policy's decision, asynchronous promotions and the
+// publication of the mirrors, the host side moe_dual.cpp runs around the
+// fused op (moe_dual.cpp:640-705 publish, 862-880 batch transport, the
+// policy callbacks of policy.h:82-104).
+//
+// After a visible token's layers are queued on the compute stream,
+// llapis_residency_token_end:
+//   1. hands the promotion engine's finished jobs to the policy
+//      (complete_fill / abort_fill; a READY slot marks its layer dirty);
+//   2. runs the policy's per-token decision (on_token_end): its
+//      fetch_external pulls every layer's counters with one D2H copy on the
+//      stream (the only wait of the loop: the token's kernels), zeroes them
+//      with a kernel, and pours them in; stream_expert submits a job and
+//      answers FILLING; publish_layer marks the layer dirty;
+//   3. publishes the dirty layers' mirrors with H2D copies on the compute
+//      stream from pinned staging, so the next token's kernels see them in
+//      stream order;
+//   4. flushes the engine: the copies start after all of that, on the
+//      engine's own stream, and overlap the next token.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/llapis_moe.h"
+#include "../../include/moert_policy.h"
+#include "launch.h"
+
+struct llapis_residency {
+    int L = 0, E = 0, K = 0;
+    moert_policy * pol = nullptr;
+    llapis_xfer * x = nullptr;
+    int32_t * counts_dev = nullptr;     // [L][E] routed pairs, then [L][2] hot / other
+    int32_t * counts_host = nullptr;    // pinned
+    hipStream_t cur = nullptr;          // the stream of the token_end in progress (0 is the null stream)
+    bool in_token_end = false;
+    struct Mirrors {
+        int32_t * es = nullptr;
+        int32_t * se = nullptr;
+        int32_t * ss = nullptr;
+    };
+    std::vector<Mirrors> mirrors;
+    std::vector<char> dirty;
+    int32_t * staging = nullptr;        // pinned: every layer's mirrors, [L][E + 2 K]
+    hipEvent_t staged = nullptr;        // after the last publication's copies
+    bool staged_used = false;
+    hipError_t err = hipSuccess;
+    llapis_residency_stats st = {};
+};
+
+namespace {
+
+thread_local char g_rerr[256];
+int32_t rfail(const char * msg) {
+    snprintf(g_rerr, sizeof g_rerr, "%s", msg);
+    return -1;
+}
+
+int32_t cb_stream_expert(void * user, int32_t il, int32_t e, int32_t slot) {
+    llapis_residency * r = static_cast<llapis_residency *>(user);
+    if (llapis_xfer_submit(r->x, il, e, slot) != 0) return 0;
+    ++r->st.submitted;
+    return 2;   // accepted asynchronously: FILLING until the copy lands
+}
+
+void cb_publish_layer(void * user, int32_t il) {
+    llapis_residency * r = static_cast<llapis_residency *>(user);
+    if (il >= 0 && il < r->L) r->dirty[il] = 1;
+}
+
+// every layer's counters in one copy; waits for the token on the stream
+void cb_fetch_external(void * user) {
+    llapis_residency * r = static_cast<llapis_residency *>(user);
+    if (!r->in_token_end || r->err != hipSuccess) return;
+    const size_t n = (size_t)r->L * r->E + 2 * (size_t)r->L;
+    hipError_t e = hipMemcpyAsync(r->counts_host, r->counts_dev, n * 4, hipMemcpyDeviceToHost, r->cur);
+    if (e == hipSuccess) e = hipStreamSynchronize(r->cur);
+    if (e == hipSuccess) e = llapis::launch_zero_i32(r->counts_dev, (int)n, r->cur);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        r->err = e;
+        return;
+    }
+    const int32_t * hits = r->counts_host + (size_t)r->L * r->E;
+    for (int il = 0; il < r->L; ++il) {
+        moert_policy_add_external_counts(r->pol, il, r->counts_host + (size_t)il * r->E, hits[2 * il], hits[2 * il + 1]);
+        r->st.hot_pairs += hits[2 * il];
+        r->st.cold_pairs += hits[2 * il + 1];
+    }
+    ++r->st.fetches;
+}
+
+// the dirty layers' mirrors, staged and copied in stream order
+int32_t publish(llapis_residency * r, hipStream_t s, bool all) {
+    if (r->staged_used && hipEventSynchronize(r->staged) != hipSuccess) {
+        (void)hipGetLastError();
+        return rfail("llapis_residency: staging wait failed");
+    }
+    const size_t per = (size_t)r->E + 2 * (size_t)r->K;
+    bool any = false;
+    for (int il = 0; il < r->L; ++il) {
+        if (!all && !r->dirty[il]) continue;
+        r->dirty[il] = 0;
+        const llapis_residency::Mirrors & m = r->mirrors[il];
+        if (!m.es || !m.se || !m.ss) continue;
+        const int k = moert_policy_layer_k(r->pol, il);
+        if (k < 0 || k > r->K) return rfail("llapis_residency: layer capacity above the mirrors' size");
+        int32_t * b = r->staging + (size_t)il * per;
+        memcpy(b, moert_policy_exp_slot_view(r->pol, il), (size_t)r->E * 4);
+        memcpy(b + r->E, moert_policy_slot_exp_view(r->pol, il), (size_t)k * 4);
+        memcpy(b + r->E + r->K, moert_policy_slot_state_view(r->pol, il), (size_t)k * 4);
+        if (hipMemcpyAsync(m.es, b, (size_t)r->E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(m.se, b + r->E, (size_t)k * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(m.ss, b + r->E + r->K, (size_t)k * 4, hipMemcpyHostToDevice, s) != hipSuccess) {
+            (void)hipGetLastError();
+            return rfail("llapis_residency: mirror copy failed");
+        }
+        ++r->st.publications;
+        any = true;
+    }
+    if (any) {
+        if (hipEventRecord(r->staged, s) != hipSuccess) {
+            (void)hipGetLastError();
+            return rfail("llapis_residency: event record failed");
+        }
+        r->staged_used = true;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char * llapis_residency_last_error(void) { return g_rerr; }
+
+llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int32_t copy_wgs) {
+    if (!cfg || cfg->n_layers <= 0 || cfg->n_expert <= 0 || cfg->k <= 0) {
+        rfail("llapis_residency_create: bad geometry");
+        return nullptr;
+    }
+    int kmax = cfg->k;
+    if (cfg->k_per_layer)
+        for (int il = 0; il < cfg->n_layers; ++il) kmax = std::max(kmax, cfg->k_per_layer[il]);
+    llapis_residency * r = new llapis_residency();
+    r->L = cfg->n_layers;
+    r->E = cfg->n_expert;
+    r->K = kmax;
+    moert_policy_callbacks cb = {cb_stream_expert, cb_publish_layer, cb_fetch_external, r};
+    r->pol = moert_policy_create(cfg, &cb);
+    r->x = r->pol ? llapis_xfer_create(r->L, r->E, r->K, copy_wgs) : nullptr;
+    const size_t n = (size_t)r->L * r->E + 2 * (size_t)r->L;
+    bool ok = r->pol && r->x && hipMalloc((void **)&r->counts_dev, n * 4) == hipSuccess &&
+              hipMemset(r->counts_dev, 0, n * 4) == hipSuccess &&
+              hipHostMalloc((void **)&r->counts_host, n * 4, hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc((void **)&r->staging, (size_t)r->L * (r->E + 2 * (size_t)r->K) * 4,
+                            hipHostMallocDefault) == hipSuccess &&
+              hipEventCreateWithFlags(&r->staged, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        rfail("llapis_residency_create: policy, engine or device buffers could not be created");
+        llapis_residency_free(r);
+        return nullptr;
+    }
+    moert_policy_set_external_observation(r->pol, 1);
+    r->mirrors.resize(r->L);
+    r->dirty.assign(r->L, 0);
+    return r;
+}
+
+void llapis_residency_free(llapis_residency * r) {
+    if (!r) return;
+    if (r->x) llapis_xfer_free(r->x);           // waits for its copies
+    if (r->staged) {
+        (void)hipEventSynchronize(r->staged);
+        (void)hipEventDestroy(r->staged);
+    }
+    if (r->counts_dev) (void)hipFree(r->counts_dev);
+    if (r->counts_host) (void)hipHostFree(r->counts_host);
+    if (r->staging) (void)hipHostFree(r->staging);
+    if (r->pol) moert_policy_free(r->pol);
+    delete r;
+}
+
+moert_policy * llapis_residency_policy(llapis_residency * r) { return r ? r->pol : nullptr; }
+llapis_xfer * llapis_residency_xfer(llapis_residency * r) { return r ? r->x : nullptr; }
+
+int32_t llapis_residency_set_mirrors(llapis_residency * r, int32_t il, int32_t * exp_slot, int32_t * slot_exp,
+                                     int32_t * slot_state) {
+    if (!r || il < 0 || il >= r->L || !exp_slot || !slot_exp || !slot_state)
+        return rfail("llapis_residency_set_mirrors: bad arguments");
+    r->mirrors[il] = {exp_slot, slot_exp, slot_state};
+    return 0;
+}
+
+int32_t llapis_residency_counters(llapis_residency * r, int32_t il, int32_t ** counts, int32_t ** hits) {
+    if (!r || il < 0 || il >= r->L || !counts || !hits) return rfail("llapis_residency_counters: bad arguments");
+    *counts = r->counts_dev + (size_t)il * r->E;
+    *hits = r->counts_dev + (size_t)r->L * r->E + 2 * (size_t)il;
+    return 0;
+}
+
+int32_t llapis_residency_publish_all(llapis_residency * r, void * stream) {
+    if (!r) return rfail("llapis_residency_publish_all: null runtime");
+    return publish(r, (hipStream_t)stream, true);
+}
+
+int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
+    if (!r) return rfail("llapis_residency_token_end: null runtime");
+    hipStream_t s = (hipStream_t)stream;
+    // 1. finished promotions
+    llapis_xfer_done done[256];
+    for (int32_t n; (n = llapis_xfer_take_done(r->x, done, 256)) > 0;) {
+        for (int32_t i = 0; i < n; ++i) {
+            const llapis_xfer_done & d = done[i];
+            if (d.ok ? moert_policy_complete_fill(r->pol, d.il, d.slot, d.e)
+                     : moert_policy_abort_fill(r->pol, d.il, d.slot, d.e)) {
+                r->dirty[d.il] = 1;
+                if (d.ok) ++r->st.completed;
+            }
+        }
+    }
+    // 2. the decision (pulls the counters through fetch_external)
+    r->cur = s;
+    r->in_token_end = true;
+    moert_policy_on_token_end(r->pol);
+    r->in_token_end = false;
+    if (r->err != hipSuccess) {
+        r->err = hipSuccess;
+        return rfail("llapis_residency_token_end: counter copy failed");
+    }
+    ++r->st.tokens;
+    // 3. publication, 4. the copies
+    if (publish(r, s, false) != 0) return -1;
+    if (llapis_xfer_flush(r->x, stream) != 0) return rfail(llapis_xfer_last_error());
+    return 0;
+}
+
+void llapis_residency_get_stats(llapis_residency * r, llapis_residency_stats * out) {
+    if (!out) return;
+    memset(out, 0, sizeof(*out));
+    if (r) *out = r->st;
+}
+
+}  // extern "C"

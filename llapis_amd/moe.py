@@ -235,7 +235,8 @@ def _torch():
 
 
 def _ptr(t):
-    return None if t is None else t.data_ptr()
+    """A device address: None, a raw address (int) or a tensor's."""
+    return None if t is None else t if isinstance(t, int) else t.data_ptr()
 
 
 class DeviceLayer:
@@ -253,7 +254,7 @@ class DeviceLayer:
         self.exp_slot, self.slot_exp = up(layer.exp_slot), up(layer.slot_exp)
         self.slot_state = up(layer.slot_state)
         self.s_hot, self.s_cold = up(layer.s_hot), up(layer.s_cold)
-        self.route_counts = self.route_hits = None   # optional int32 device tensors [n_expert], [2]
+        self.route_counts = self.route_hits = None   # optional int32 [n_expert], [2]: tensors or addresses
         self._ws = None
 
     def desc(self):

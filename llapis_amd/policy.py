@@ -24,6 +24,21 @@ def bind(cdll):
 TIMING_FIELDS = ("refresh_pause_ms_total", "refresh_pause_ms_max", "last_refresh_pause_ms")
 
 
+def _config(lib, n_layers, n_expert, k, k_per_layer, cfg):
+    c = L.MoertPolicyConfig()
+    lib.moert_policy_config_defaults(C.byref(c))
+    c.n_layers, c.n_expert, c.k = n_layers, n_expert, k
+    for name, v in cfg.items():
+        if not hasattr(c, name):
+            raise TypeError(f"no config field {name}")
+        setattr(c, name, v)
+    kpl = None
+    if k_per_layer is not None:
+        kpl = (L.i32 * n_layers)(*k_per_layer)
+        c.k_per_layer = C.cast(kpl, C.c_void_p)
+    return c, kpl
+
+
 class Policy:
     """moert_policy with Python callbacks.
 
@@ -35,17 +50,8 @@ class Policy:
     def __init__(self, n_layers, n_expert, k, lib=None, k_per_layer=None, stream_expert=None, publish_layer=None,
                  fetch_external=None, **cfg):
         self.lib = lib if lib is not None else L.lib()
-        c = L.MoertPolicyConfig()
-        self.lib.moert_policy_config_defaults(C.byref(c))
-        c.n_layers, c.n_expert, c.k = n_layers, n_expert, k
-        for name, v in cfg.items():
-            if not hasattr(c, name):
-                raise TypeError(f"no config field {name}")
-            setattr(c, name, v)
-        self._kpl = None
-        if k_per_layer is not None:
-            self._kpl = (L.i32 * n_layers)(*k_per_layer)
-            c.k_per_layer = C.cast(self._kpl, C.c_void_p)
+        c, self._kpl = _config(self.lib, n_layers, n_expert, k, k_per_layer, cfg)
+        self._owned = True
         cb = L.MoertPolicyCallbacks()
         self._cbs = []
         if stream_expert is not None:
@@ -66,10 +72,20 @@ class Policy:
             raise ValueError("moert_policy_create refused the configuration")
         self._forecast = None
 
+    @classmethod
+    def wrap(cls, p, n_layers, n_expert, lib=None):
+        """A view of a policy that something else owns and frees (the
+        residency runtime's)."""
+        self = cls.__new__(cls)
+        self.lib = lib if lib is not None else L.lib()
+        self.p, self.n_layers, self.n_expert = p, n_layers, n_expert
+        self._kpl, self._cbs, self._forecast, self._owned = None, [], None, False
+        return self
+
     def close(self):
-        if self.p:
+        if self.p and self._owned:
             self.lib.moert_policy_free(self.p)
-            self.p = None
+        self.p = None
 
     def __del__(self):
         try:
@@ -157,3 +173,56 @@ class Policy:
         w = L.MoertPolicyWindow()
         self.lib.moert_policy_get_window(self.p, n, C.byref(w))
         return {f: getattr(w, f) for f, _ in w._fields_}
+
+
+class ResidencyLoop:
+    """The native per-token residency loop (llapis_residency_*): a policy on
+    external observation, a promotion engine and every layer's device routing
+    counters.  `policy` views the runtime's policy (seed, views, stats);
+    `xfer` is its engine handle (set its page groups with
+    llapis_xfer_set_group).  Config keywords as Policy's."""
+
+    def __init__(self, n_layers, n_expert, k, copy_wgs=0, lib=None, k_per_layer=None, **cfg):
+        self.lib = lib if lib is not None else L.lib()
+        c, self._kpl = _config(self.lib, n_layers, n_expert, k, k_per_layer, cfg)
+        self.r = self.lib.llapis_residency_create(C.byref(c), copy_wgs)
+        if not self.r:
+            raise RuntimeError(self.lib.llapis_residency_last_error().decode())
+        self.policy = Policy.wrap(self.lib.llapis_residency_policy(self.r), n_layers, n_expert, self.lib)
+        self.xfer = self.lib.llapis_residency_xfer(self.r)
+
+    def _check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.lib.llapis_residency_last_error().decode())
+
+    def counters(self, il):
+        """Device addresses of layer il's counters: (counts [n_expert], hits [2])."""
+        cp, hp = C.c_void_p(), C.c_void_p()
+        self._check(self.lib.llapis_residency_counters(self.r, il, C.byref(cp), C.byref(hp)))
+        return cp.value, hp.value
+
+    def set_mirrors(self, il, exp_slot, slot_exp, slot_state):
+        self._check(self.lib.llapis_residency_set_mirrors(self.r, il, exp_slot, slot_exp, slot_state))
+
+    def publish_all(self, stream):
+        self._check(self.lib.llapis_residency_publish_all(self.r, stream))
+
+    def token_end(self, stream):
+        self._check(self.lib.llapis_residency_token_end(self.r, stream))
+
+    def stats(self):
+        s = L.LlapisResidencyStats()
+        self.lib.llapis_residency_get_stats(self.r, C.byref(s))
+        return {f: getattr(s, f) for f, _ in s._fields_}
+
+    def close(self):
+        if self.r:
+            self.policy.p = None
+            self.lib.llapis_residency_free(self.r)
+            self.r = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

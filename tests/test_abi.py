@@ -55,6 +55,7 @@ MIRRORS = {
     "llapis_kfit_inputs": _lib.LlapisKfitInputs,
     "llapis_gguf_tensor_info": _lib.LlapisGgufTensorInfo,
     "llapis_page_group": _lib.LlapisPageGroup,
+    "llapis_residency_stats": _lib.LlapisResidencyStats,
     "moert_store_info": _lib.MoertStoreInfo,
     "llapis_kfit_decision": _lib.LlapisKfitDecision,
     "moert_policy_config": _lib.MoertPolicyConfig,

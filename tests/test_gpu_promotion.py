@@ -30,6 +30,14 @@ from helpers import FULL16, layer, rel_l2, tokens
 pytestmark = pytest.mark.gpu
 
 
+# Per call, the required relative L2 bar of a whole layer.  A one-token call
+# sits near 1e-7 unless a last-bit difference in a gate_up output flips a
+# q8_0 rounding of the down activation (then up to a few 1e-4 on that token,
+# deterministic); an expert served in the wrong tier or with stale bytes costs
+# 1e-2 or more.  The loops also bound the median call at 1e-6.
+FLIP_BAR = 1e-3
+
+
 def say(*a):
     print(*a, flush=True)
     sys.stdout.flush()
@@ -240,6 +248,7 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
         assert lib.llapis_xfer_set_group(x_eng, 0, g, slab.data_ptr(), src.data_ptr(), b, b) == 0
 
     expect = {"counts": np.zeros(E, np.int64), "hot": 0, "cold": 0}
+    errs = []
     log = {"fetches": 0, "submitted": 0, "completed": 0, "filling_served_cold": 0, "promoted_used_hot": 0}
     pol = None
 
@@ -315,7 +324,8 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
             assert np.array_equal(ids_h, ids_o)
             out_o, _ = oracle.moe_experts(vl, x, ids_h, w_h, la.ACT_CPU, la.GELU_TABLE)
             err = rel_l2(out.cpu().numpy(), out_o)
-            assert err <= 1e-4, (step, err)
+            errs.append(float(err))
+            assert err <= FLIP_BAR, (step, err)
             for e in ids_h.ravel():
                 s = int(v["exp_slot"][e])
                 if s >= 0 and v["slot_state"][s] == la.SLOT_FILLING:
@@ -331,6 +341,7 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
             else:
                 pol.token_end()                   # fetch -> decide -> submit / publish FILLING
             assert lib.llapis_xfer_flush(x_eng, stream) == 0
+        assert np.median(errs) <= 1e-6, errs
         pol.refresh(L.REFRESH_TURN_END)
         # one pull per decision: each visible token and the turn end (the
         # prompt chunk's counts wait for the turn end)
@@ -361,6 +372,104 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
     finally:
         lib.llapis_xfer_free(x_eng)
         pol.close()
+
+
+def test_native_residency_loop_two_layers(gpu, oracle):
+    """The same loop run by the native runtime (llapis_residency_*) over two
+    layers whose routing drifts in opposite directions: every call's output
+    matches the oracle under the page table published at the previous token
+    end, the device mirrors equal the policy's after each token end, the
+    counters the runtime pulled add up to the pairs the GPU routed, and each
+    layer ends holding its own phase's experts, byte for byte."""
+    from llapis_amd.policy import ResidencyLoop
+    torch = torch_mod()
+    lib = la.lib()
+    spec = FULL16
+    E, K, top_k, NL = spec.n_expert, 4, spec.top_k, 2
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    rl = ResidencyLoop(NL, E, K, copy_wgs=8, cost_horizon=64, cost_reuse=2.0, cost_per_token=2)
+    pol = rl.policy
+    layers = []
+    try:
+        for il in range(NL):
+            lay_all = layer(spec, 81 + il, list(range(E)), scales=True)
+            src_s = lay_all.s_hot.copy()
+            srcs = [u8(torch, lay_all.hot_gu, gpu), u8(torch, lay_all.hot_dn, gpu), u8(torch, src_s, gpu)]
+            live = copy.copy(lay_all)
+            live.residency = la.Residency.from_hot(E, list(range(K)))
+            live.hot_gu = lay_all.hot_gu[:K * gb].copy()
+            live.hot_dn = lay_all.hot_dn[:K * db].copy()
+            live.s_hot = src_s[:K].copy()
+            live.router_b = np.zeros(E, np.float32)
+            dl = la.DeviceLayer(live, gpu)
+            dl.route_counts, dl.route_hits = rl.counters(il)
+            for g, (slab, src, b) in enumerate(((dl.hot_gu, srcs[0], gb), (dl.hot_dn, srcs[1], db),
+                                                (dl.s_hot, srcs[2], 4))):
+                assert lib.llapis_xfer_set_group(rl.xfer, il, g, slab.data_ptr(), src.data_ptr(), b, b) == 0
+            rl.set_mirrors(il, dl.exp_slot.data_ptr(), dl.slot_exp.data_ptr(), dl.slot_state.data_ptr())
+            for e in range(K):
+                assert pol.seed(il, e, e) == 1
+            layers.append((lay_all, src_s, srcs, dl))
+        stream = torch.cuda.current_stream().cuda_stream
+        rl.publish_all(stream)
+        routed = {"hot": 0, "cold": 0}
+        errs = []
+        plan = [(1, "A")] * 10 + [(4, "A")] + [(1, "B")] * 16 + [(4, "B")] + [(1, "B")] * 4
+        for step, (T, phase) in enumerate(plan):
+            for il, (lay_all, src_s, _, dl) in enumerate(layers):
+                v = pol.views(il)
+                assert np.array_equal(dl.exp_slot.cpu().numpy(), v["exp_slot"])
+                assert np.array_equal(dl.slot_exp.cpu().numpy(), v["slot_exp"])
+                assert np.array_equal(dl.slot_state.cpu().numpy(), v["slot_state"])
+                bias = np.zeros(E, np.float32)
+                up = (phase == "A") == (il == 0)
+                bias[8:] = 3.0 if up else -3.0
+                dl.router_b.copy_(torch.from_numpy(bias))
+                x = tokens(900 + 10 * step + il, T, spec.d_model)
+                out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+                ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+                vl = _view_layer(lay_all, src_s, v["exp_slot"], v["slot_exp"], v["slot_state"])
+                vl.router_b = bias
+                ids_o, _, _ = oracle.router(x, vl.router_w, bias, top_k)
+                assert np.array_equal(ids_h, ids_o)
+                out_o, _ = oracle.moe_experts(vl, x, ids_h, w_h, la.ACT_CPU, la.GELU_TABLE)
+                err = rel_l2(out.cpu().numpy(), out_o)
+                errs.append(float(err))
+                assert err <= FLIP_BAR, (step, il, err)
+                hot = sum(vl.residency.is_hot(int(e)) for e in ids_h.ravel())
+                routed["hot"] += hot
+                routed["cold"] += ids_h.size - hot
+            rl.token_end(stream)
+            say(f"step {step} T={T} {phase}: " + "; ".join(
+                f"L{il} slots {list(pol.views(il)['slot_exp'])} states {list(pol.views(il)['slot_state'])}"
+                for il in range(NL)))
+        torch.cuda.synchronize()
+        assert np.median(errs) <= 1e-6, errs
+        st = rl.stats()
+        say(f"runtime {st}; policy {pol.stats()}")
+        assert st["tokens"] == st["fetches"] == len(plan)
+        assert (st["hot_pairs"], st["cold_pairs"]) == (routed["hot"], routed["cold"])
+        assert st["submitted"] >= 8 and st["completed"] >= 4
+        # drain: the last copies land, one more token end makes them READY
+        assert lib.llapis_xfer_wait_idle(rl.xfer, stream) == 0
+        rl.token_end(stream)
+        assert lib.llapis_xfer_wait_idle(rl.xfer, stream) == 0
+        torch.cuda.synchronize()
+        for il, (lay_all, src_s, _, dl) in enumerate(layers):
+            v = pol.views(il)
+            assert np.array_equal(dl.slot_state.cpu().numpy(), v["slot_state"])
+            hg, hd, hs = dl.hot_gu.cpu().numpy(), dl.hot_dn.cpu().numpy(), dl.s_hot.cpu().numpy()
+            ready = [s for s in range(K) if v["slot_state"][s] == la.SLOT_READY]
+            assert len(ready) >= 2
+            for s in ready:
+                e = int(v["slot_exp"][s])
+                assert np.array_equal(hg[s * gb:(s + 1) * gb], lay_all.hot_gu[e * gb:(e + 1) * gb])
+                assert np.array_equal(hd[s * db:(s + 1) * db], lay_all.hot_dn[e * db:(e + 1) * db])
+                assert hs[s] == src_s[e]
+            held = {int(v["slot_exp"][s]) for s in ready}
+            assert held <= (set(range(8)) if il == 0 else set(range(8, 16))), (il, held)
+    finally:
+        rl.close()
 
 
 def test_xfer_large_flush_split_into_launches(gpu):
