@@ -440,16 +440,17 @@ class Stack:
 
     def run(self, h, xn, out, ws, stream, T, moe=True):
         """h [T, d_model] (the residual stream) is updated in place through
-        every layer; xn and out are scratch.  moe=False runs only the glue
+        every layer; out is scratch (xn is unused: the norm's output is the
+        layer's input).  moe=False runs only the glue
         (norm and add) to time it on its own."""
         torch = self.torch
         sp = self.spec
         ids = torch.empty(T, sp.top_k, dtype=torch.int32, device=h.device)
         w = torch.empty(T, sp.top_k, device=h.device)
         for d in self.descs:
-            xn.copy_(torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6))
+            xl = torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6)   # the layer's input, no extra copy
             if moe:
-                rc = self.fn(C.byref(d), xn.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                rc = self.fn(C.byref(d), xl.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
                              ws.data_ptr(), ws.numel(), stream)
                 if rc != 0:
                     raise RuntimeError(self.la.lib().llapis_last_error().decode())
@@ -558,8 +559,17 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
             pol.seed(il, int(e), s_)
     stream = torch.cuda.Stream()
     rl.publish_all(stream.cuda_stream)
-    biases = [d.router_b.clone() for d in st.layers]
     rng = np.random.default_rng(5)
+    # the drift phases' router biases, permuted ahead (device tensors)
+    n_drift = (tokens - 1) // drift_every
+    drifted = []
+    for il, d in enumerate(st.layers):
+        b = d.router_b.clone()
+        row = []
+        for _ in range(n_drift):
+            b = b[torch.from_numpy(rng.permutation(E)).to(dev)]
+            row.append(b.clone())
+        drifted.append(row)
     T = 1
     need = int(lib.llapis_moe_ffn_workspace_size(C.byref(st.descs[0]), T))
     ws = torch.zeros(need, dtype=torch.uint8, device=dev)
@@ -585,7 +595,7 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
         for tok in range(tokens):
             if tok and tok % drift_every == 0:
                 for il, d in enumerate(st.layers):
-                    d.router_b.copy_(biases[il][torch.from_numpy(rng.permutation(E)).to(dev)])
+                    d.router_b.copy_(drifted[il][tok // drift_every - 1])
             g.replay()
             a = time.perf_counter()
             rl.token_end(stream.cuda_stream)            # waits for the token, decides, publishes, flushes
@@ -616,13 +626,16 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
            "loop": "native", "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
            "publications": int(rst["publications"] - r0["publications"]), "copies_bytes": int(xs.bytes),
            "hit_rate_per_phase": segs, "hit_rate_first_8_tokens_per_phase": first,
-           "token_end_ms_per_token": host_s * 1e3 / tokens, "sync_no_loop_ms_per_token": sync_ms}
+           "token_end_ms_per_token": host_s * 1e3 / tokens, "sync_no_loop_ms_per_token": sync_ms,
+           "loop_host_ms_per_token": (rst["host_ms"] - r0["host_ms"]) / tokens,
+           "decision_ms_per_token": float(pst["refresh_pause_ms_total"]) / max(1, int(pst["refresh_count"]))}
     log(f"[stack dynamic] {tokens} tokens x {n_layers} layers: {res['ms_per_token']:.3f} ms per token "
         f"({res['tok_per_s']:.0f} tok/s) with the native residency loop; {res['promotions']} promotions "
         f"({xs.bytes / 1e9:.2f} GB copied), hit rate per {drift_every}-token phase "
         + ", ".join(f"{v:.2f}" for v in segs) + " (first 8 tokens of each: " + ", ".join(f"{v:.2f}" for v in first)
         + f"); token end (waits for the token's pass) {res['token_end_ms_per_token']:.3f} ms per token; the same "
-        f"passes with a wait after each and no loop: {sync_ms:.3f} ms per token")
+        f"passes with a wait after each and no loop: {sync_ms:.3f} ms per token; the loop's own host time "
+        f"{res['loop_host_ms_per_token']:.3f} ms per token (decision {res['decision_ms_per_token']:.3f})")
     del st, src_gu, src_dn, ws
     torch.cuda.empty_cache()
     return res

@@ -236,6 +236,8 @@ typedef struct llapis_residency llapis_residency;
 typedef struct llapis_residency_stats {
     long long tokens, fetches, submitted, completed, publications;
     long long hot_pairs, cold_pairs;     /* routed pairs the counters saw */
+    double wait_ms;                      /* in token_end, waiting for the token's kernels */
+    double host_ms;                      /* in token_end, everything else (the loop's own cost) */
 } llapis_residency_stats;
 /* cfg as moert_policy_create's (callbacks are the runtime's own); copy_wgs
  * as llapis_xfer_create's.  Allocates the counters (device), their pinned

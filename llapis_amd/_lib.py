@@ -110,7 +110,8 @@ class LlapisPageGroup(C.Structure):
 
 class LlapisResidencyStats(C.Structure):
     _fields_ = [(n, C.c_longlong) for n in ("tokens", "fetches", "submitted", "completed", "publications",
-                                            "hot_pairs", "cold_pairs")]
+                                            "hot_pairs", "cold_pairs")] + [("wait_ms", C.c_double),
+                                                                           ("host_ms", C.c_double)]
 
 
 # moert_store.h

@@ -283,33 +283,56 @@ void moert_policy_refresh(moert_policy * p, int32_t reason) {
                                  ? (long long)(ext && g.ext_cap > 0 ? g.ext_cap : g.cfg.cost_per_token)
                                  : (long long)1 << 40;
     std::vector<int> outside, free_slots, held;
+    std::vector<float> fc((size_t)g.E);
     for (int il = 0; il < g.L; ++il) {
         if (g.only_layer >= 0 && il != g.only_layer) continue;
         const float r = g.price_override >= 0.0f ? g.price_override : (ext ? g.ext_price : g.cfg.cost_reuse);
         outside.clear();
         free_slots.clear();
         held.clear();
+        // the layer's forecasts, once (nothing changes them during the pairing)
+        bool finite = true;
+        for (int e = 0; e < g.E; ++e) {
+            fc[e] = forecast(g, il, e);
+            finite = finite && std::isfinite(fc[e]);
+        }
+        float f_max = -INFINITY, f_min = INFINITY;
         for (int e = 0; e < g.E; ++e)
-            if (g.exp_slot[g.at(il, e)] < 0) outside.push_back(e);
-        for (int s = 0; s < g.cap[il]; ++s) (g.slot_exp[il][s] < 0 ? free_slots : held).push_back(s);
+            if (g.exp_slot[g.at(il, e)] < 0) {
+                outside.push_back(e);
+                f_max = std::max(f_max, fc[e]);
+            }
+        for (int s = 0; s < g.cap[il]; ++s) {
+            const int e = g.slot_exp[il][s];
+            if (e < 0) {
+                free_slots.push_back(s);
+            } else {
+                held.push_back(s);
+                f_min = std::min(f_min, fc[e]);
+            }
+        }
+        if (outside.empty()) continue;
+        // both pairings below stop at their first candidate unless the best
+        // non-resident beats the price (free slot) or the weakest resident by
+        // more than the price (swap): then the layer adds no pair
+        if (finite && (free_slots.empty() || f_max <= r) && (held.empty() || f_max - f_min <= r)) continue;
         // non-residents by forecast, highest first (ties: lower id first)
-        std::stable_sort(outside.begin(), outside.end(),
-                         [&](int a, int b) { return forecast(g, il, a) > forecast(g, il, b); });
+        std::stable_sort(outside.begin(), outside.end(), [&](int a, int b) { return fc[a] > fc[b]; });
         // occupied slots by their expert's forecast, lowest first (ties: lower id)
         std::sort(held.begin(), held.end(), [&](int a, int b) {
             const int ea = g.slot_exp[il][a], eb = g.slot_exp[il][b];
-            const float fa = forecast(g, il, ea), fb = forecast(g, il, eb);
+            const float fa = fc[ea], fb = fc[eb];
             return fa != fb ? fa < fb : ea < eb;
         });
         size_t next = 0;
         for (size_t i = 0; i < free_slots.size() && next < outside.size(); ++i, ++next) {
-            const float f_in = forecast(g, il, outside[next]);
+            const float f_in = fc[outside[next]];
             if (f_in <= r) break;
             pairs.push_back({il, outside[next], free_slots[i], -1, false, f_in - r});
         }
         for (size_t i = 0; i < held.size() && next < outside.size(); ++i, ++next) {
             const int victim = g.slot_exp[il][held[i]];
-            const float f_in = forecast(g, il, outside[next]), f_out = forecast(g, il, victim);
+            const float f_in = fc[outside[next]], f_out = fc[victim];
             if (f_in - f_out <= r) break;
             pairs.push_back({il, outside[next], held[i], victim, true, f_in - f_out - r});
         }

@@ -9,18 +9,20 @@
 //   1. hands the promotion engine's finished jobs to the policy
 //      (complete_fill / abort_fill; a READY slot marks its layer dirty);
 //   2. runs the policy's per-token decision (on_token_end): its
-//      fetch_external pulls every layer's counters with one D2H copy on the
-//      stream (the only wait of the loop: the token's kernels), zeroes them
-//      with a kernel, and pours them in; stream_expert submits a job and
-//      answers FILLING; publish_layer marks the layer dirty;
-//   3. publishes the dirty layers' mirrors with H2D copies on the compute
-//      stream from pinned staging, so the next token's kernels see them in
-//      stream order;
+//      fetch_external drains every layer's counters with one kernel on the
+//      stream (it writes them to mapped pinned memory and zeroes them), waits
+//      for the stream (the only wait of the loop: the token's kernels) and
+//      pours them in; stream_expert submits a job and answers FILLING;
+//      publish_layer marks the layer dirty;
+//   3. publishes the dirty layers' mirrors with one kernel on the compute
+//      stream that reads them from mapped pinned staging, so the next token's
+//      kernels see them in stream order;
 //   4. flushes the engine: the copies start after all of that, on the
 //      engine's own stream, and overlap the next token.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -34,7 +36,8 @@ struct llapis_residency {
     moert_policy * pol = nullptr;
     llapis_xfer * x = nullptr;
     int32_t * counts_dev = nullptr;     // [L][E] routed pairs, then [L][2] hot / other
-    int32_t * counts_host = nullptr;    // pinned
+    int32_t * counts_host = nullptr;    // pinned, mapped
+    int32_t * counts_host_dev = nullptr;  // its device address
     hipStream_t cur = nullptr;          // the stream of the token_end in progress (0 is the null stream)
     bool in_token_end = false;
     struct Mirrors {
@@ -44,7 +47,8 @@ struct llapis_residency {
     };
     std::vector<Mirrors> mirrors;
     std::vector<char> dirty;
-    int32_t * staging = nullptr;        // pinned: every layer's mirrors, [L][E + 2 K]
+    int32_t * staging = nullptr;        // pinned, mapped: every layer's mirrors, [L][E + 2 K]
+    const int32_t * staging_dev = nullptr;
     hipEvent_t staged = nullptr;        // after the last publication's copies
     bool staged_used = false;
     hipError_t err = hipSuccess;
@@ -52,6 +56,46 @@ struct llapis_residency {
 };
 
 namespace {
+
+// one launch publishes up to PUB_MAX layers: block b copies entry b's
+// exp_slot [E], slot_exp [k] and slot_state [k] from the staging rows
+constexpr int PUB_MAX = 64;
+struct PubEntry {
+    int32_t * es;
+    int32_t * se;
+    int32_t * ss;
+    int64_t off;    // first element of the layer's staging row
+    int32_t k;
+    int32_t pad;
+};
+struct PubBatch {
+    PubEntry e[PUB_MAX];
+    const int32_t * staging;
+    int32_t E, K;
+};
+
+__global__ __launch_bounds__(256) void k_publish_mirrors(const PubBatch b) {
+    const PubEntry & m = b.e[blockIdx.x];
+    const int32_t * row = b.staging + m.off;
+    for (int i = threadIdx.x; i < b.E; i += blockDim.x) m.es[i] = row[i];
+    for (int i = threadIdx.x; i < m.k; i += blockDim.x) {
+        m.se[i] = row[b.E + i];
+        m.ss[i] = row[b.E + b.K + i];
+    }
+}
+
+// counters -> mapped pinned memory, then zero
+__global__ __launch_bounds__(256) void k_drain_counts(int32_t * __restrict__ counts, int32_t * __restrict__ host,
+                                                      int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        host[i] = counts[i];
+        counts[i] = 0;
+    }
+}
+
+double ms_now() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
 
 thread_local char g_rerr[256];
 int32_t rfail(const char * msg) {
@@ -75,10 +119,12 @@ void cb_publish_layer(void * user, int32_t il) {
 void cb_fetch_external(void * user) {
     llapis_residency * r = static_cast<llapis_residency *>(user);
     if (!r->in_token_end || r->err != hipSuccess) return;
-    const size_t n = (size_t)r->L * r->E + 2 * (size_t)r->L;
-    hipError_t e = hipMemcpyAsync(r->counts_host, r->counts_dev, n * 4, hipMemcpyDeviceToHost, r->cur);
+    const int n = r->L * r->E + 2 * r->L;
+    k_drain_counts<<<std::min(16, (n + 255) / 256), 256, 0, r->cur>>>(r->counts_dev, r->counts_host_dev, n);
+    hipError_t e = hipGetLastError();
+    const double t0 = ms_now();
     if (e == hipSuccess) e = hipStreamSynchronize(r->cur);
-    if (e == hipSuccess) e = llapis::launch_zero_i32(r->counts_dev, (int)n, r->cur);
+    r->st.wait_ms += ms_now() - t0;
     if (e != hipSuccess) {
         (void)hipGetLastError();
         r->err = e;
@@ -101,6 +147,17 @@ int32_t publish(llapis_residency * r, hipStream_t s, bool all) {
     }
     const size_t per = (size_t)r->E + 2 * (size_t)r->K;
     bool any = false;
+    PubBatch pb;
+    pb.staging = r->staging_dev;
+    pb.E = r->E;
+    pb.K = r->K;
+    int nb = 0;
+    auto launch = [&]() {
+        if (nb == 0) return true;
+        k_publish_mirrors<<<nb, 256, 0, s>>>(pb);
+        nb = 0;
+        return hipGetLastError() == hipSuccess;
+    };
     for (int il = 0; il < r->L; ++il) {
         if (!all && !r->dirty[il]) continue;
         r->dirty[il] = 0;
@@ -112,15 +169,12 @@ int32_t publish(llapis_residency * r, hipStream_t s, bool all) {
         memcpy(b, moert_policy_exp_slot_view(r->pol, il), (size_t)r->E * 4);
         memcpy(b + r->E, moert_policy_slot_exp_view(r->pol, il), (size_t)k * 4);
         memcpy(b + r->E + r->K, moert_policy_slot_state_view(r->pol, il), (size_t)k * 4);
-        if (hipMemcpyAsync(m.es, b, (size_t)r->E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipMemcpyAsync(m.se, b + r->E, (size_t)k * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipMemcpyAsync(m.ss, b + r->E + r->K, (size_t)k * 4, hipMemcpyHostToDevice, s) != hipSuccess) {
-            (void)hipGetLastError();
-            return rfail("llapis_residency: mirror copy failed");
-        }
+        pb.e[nb++] = PubEntry{m.es, m.se, m.ss, (int64_t)il * (int64_t)per, k, 0};
+        if (nb == PUB_MAX && !launch()) return rfail("llapis_residency: publication launch failed");
         ++r->st.publications;
         any = true;
     }
+    if (!launch()) return rfail("llapis_residency: publication launch failed");
     if (any) {
         if (hipEventRecord(r->staged, s) != hipSuccess) {
             (void)hipGetLastError();
@@ -155,9 +209,11 @@ llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int3
     const size_t n = (size_t)r->L * r->E + 2 * (size_t)r->L;
     bool ok = r->pol && r->x && hipMalloc((void **)&r->counts_dev, n * 4) == hipSuccess &&
               hipMemset(r->counts_dev, 0, n * 4) == hipSuccess &&
-              hipHostMalloc((void **)&r->counts_host, n * 4, hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc((void **)&r->counts_host, n * 4, hipHostMallocMapped) == hipSuccess &&
+              hipHostGetDevicePointer((void **)&r->counts_host_dev, r->counts_host, 0) == hipSuccess &&
               hipHostMalloc((void **)&r->staging, (size_t)r->L * (r->E + 2 * (size_t)r->K) * 4,
-                            hipHostMallocDefault) == hipSuccess &&
+                            hipHostMallocMapped) == hipSuccess &&
+              hipHostGetDevicePointer((void **)&r->staging_dev, r->staging, 0) == hipSuccess &&
               hipEventCreateWithFlags(&r->staged, hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         (void)hipGetLastError();
@@ -210,6 +266,7 @@ int32_t llapis_residency_publish_all(llapis_residency * r, void * stream) {
 
 int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
     if (!r) return rfail("llapis_residency_token_end: null runtime");
+    const double t_in = ms_now(), w_in = r->st.wait_ms;
     hipStream_t s = (hipStream_t)stream;
     // 1. finished promotions
     llapis_xfer_done done[256];
@@ -236,6 +293,7 @@ int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
     // 3. publication, 4. the copies
     if (publish(r, s, false) != 0) return -1;
     if (llapis_xfer_flush(r->x, stream) != 0) return rfail(llapis_xfer_last_error());
+    r->st.host_ms += (ms_now() - t_in) - (r->st.wait_ms - w_in);
     return 0;
 }
 
