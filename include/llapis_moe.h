@@ -241,7 +241,11 @@ typedef struct llapis_residency_stats {
 } llapis_residency_stats;
 /* cfg as moert_policy_create's (callbacks are the runtime's own); copy_wgs
  * as llapis_xfer_create's.  Allocates the counters (device), their pinned
- * read-back and the publication staging.  NULL on failure. */
+ * read-back and the publication staging, sized for the largest capacity in
+ * cfg: a K re-fit (moert_policy_resize_k) above it needs a new runtime, and
+ * publication fails with an error rather than write past the staging.  All
+ * calls on one runtime must come from one thread.  NULL on failure (the
+ * geometry is checked before any device call). */
 llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int32_t copy_wgs);
 void               llapis_residency_free(llapis_residency * r);
 const char *       llapis_residency_last_error(void);

@@ -334,3 +334,24 @@ def test_matches_reference_policy(seed):
     assert sides[0][1].calls >= 3, sides[0][1].calls
     for p, _ in sides:
         p.close()
+
+
+def test_residency_runtime_refuses_bad_geometry():
+    """llapis_residency_create checks the geometry before any device call,
+    so the refusal is testable without a GPU."""
+    lib = L.lib()
+    for n_layers, n_expert, k in ((0, 16, 4), (2, 0, 4), (2, 16, 0)):
+        c = L.MoertPolicyConfig()
+        lib.moert_policy_config_defaults(C.byref(c))
+        c.n_layers, c.n_expert, c.k = n_layers, n_expert, k
+        assert not lib.llapis_residency_create(C.byref(c), 0)
+        assert b"bad geometry" in lib.llapis_residency_last_error()
+    assert not lib.llapis_residency_create(None, 0)
+    # the handle-taking calls refuse a null runtime
+    assert lib.llapis_residency_token_end(None, None) == -1
+    assert lib.llapis_residency_publish_all(None, None) == -1
+    assert lib.llapis_residency_set_mirrors(None, 0, None, None, None) == -1
+    assert not lib.llapis_residency_policy(None)
+    s = L.LlapisResidencyStats()
+    lib.llapis_residency_get_stats(None, C.byref(s))
+    assert s.tokens == 0
