@@ -18,6 +18,7 @@ underneath (torch is used only for device memory and the current stream):
 """
 from dataclasses import dataclass, field
 
+import copy
 import ctypes as C
 import numpy as np
 
@@ -266,6 +267,35 @@ class DeviceLayer:
                                 _ptr(self.cold_gu), _ptr(self.cold_dn), _ptr(self.exp_slot), _ptr(self.slot_exp),
                                 _ptr(self.slot_state), _ptr(self.s_hot), _ptr(self.s_cold),
                                 _ptr(self.route_counts), _ptr(self.route_hits))
+
+    def q4stream(self, src_gu, src_dn, src_scales=None):
+        """The reference's q4stream prefill (moe_dual_q4stream.cpp:723, 1123;
+        the hook's n_tokens > 1 branch, moe_dual.cpp:205-227): every expert of
+        a chunk at the hot tier's precision.  The reference stages each
+        layer's experts into a full-layer tensor at its top-k callback; here
+        the promotion source (every expert in the hot formats, resident in
+        HBM: src_gu / src_dn uint8 [n_expert * bytes per expert], src_scales
+        f32 [n_expert] when the layer has .scale factors) is that tensor
+        already, so nothing is copied.  The returned view shares this layer's
+        router, cold pools and counters and reads its hot pool from the source
+        with n_expert slots and the identity page table."""
+        torch = _torch()
+        sp = self.layer.spec
+        E = sp.n_expert
+        nbytes = lambda t: t.numel() * t.element_size()
+        if nbytes(src_gu) < E * sp.gu_bytes(sp.hot_gu_type) or nbytes(src_dn) < E * sp.dn_bytes(sp.hot_dn_type):
+            raise ValueError("q4stream: the source must hold every expert in the hot formats")
+        if (self.s_hot is None) != (src_scales is None) or (src_scales is not None and src_scales.numel() < E):
+            raise ValueError("q4stream: scales for every expert exactly when the layer has scales")
+        v = copy.copy(self)
+        v.layer = copy.copy(self.layer)
+        v.layer.residency = Residency.from_hot(E, list(range(E)))
+        v.hot_gu, v.hot_dn, v.s_hot = src_gu, src_dn, src_scales
+        v.exp_slot = torch.arange(E, dtype=torch.int32, device=self.device)
+        v.slot_exp = v.exp_slot.clone()
+        v.slot_state = torch.full((E,), SLOT_READY, dtype=torch.int32, device=self.device)
+        v._ws = None
+        return v
 
     def workspace(self, n_tokens):
         torch = _torch()

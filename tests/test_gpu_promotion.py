@@ -472,6 +472,41 @@ def test_native_residency_loop_two_layers(gpu, oracle):
         rl.close()
 
 
+def test_q4stream_prefill_reads_the_promotion_source(gpu, oracle):
+    """q4stream (every expert of a prefill chunk at the hot precision) on a
+    view of a dual layer whose hot pool is the promotion source: the outputs
+    equal the oracle's all-hot layer, the view reads the source in place, and
+    the dual layer itself still serves its non-resident experts cold."""
+    torch = torch_mod()
+    spec = FULL16
+    E, K = spec.n_expert, 4
+    gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
+    lay_all = layer(spec, 91, list(range(E)), scales=True)       # every expert in the hot formats
+    src_s = lay_all.s_hot.copy()
+    src_gu, src_dn = u8(torch, lay_all.hot_gu, gpu), u8(torch, lay_all.hot_dn, gpu)
+    src_sc = torch.from_numpy(src_s).to(gpu)
+    live = copy.copy(lay_all)
+    live.residency = la.Residency.from_hot(E, list(range(K)))
+    live.hot_gu, live.hot_dn, live.s_hot = lay_all.hot_gu[:K * gb].copy(), lay_all.hot_dn[:K * db].copy(), src_s[:K].copy()
+    dl = la.DeviceLayer(live, gpu)
+    q = dl.q4stream(src_gu, src_dn, src_sc)
+    assert q.hot_gu.data_ptr() == src_gu.data_ptr() and q.router_w.data_ptr() == dl.router_w.data_ptr()
+    with pytest.raises(ValueError):
+        dl.q4stream(src_gu[:gb], src_dn, src_sc)
+    for T in (40, 130):
+        say(f"q4stream prefill T={T}")
+        x = tokens(1200 + T, T, spec.d_model)
+        out, ids, w = q.forward(torch.from_numpy(x).to(gpu))
+        ids_h, w_h = ids.cpu().numpy(), w.cpu().numpy()
+        ids_o, _, _ = oracle.router(x, lay_all.router_w, lay_all.router_b, spec.top_k)
+        assert np.array_equal(ids_h, ids_o)
+        out_o, _ = oracle.moe_experts(lay_all, x, ids_h, w_h, la.ACT_CPU, la.GELU_TABLE)
+        err = rel_l2(out.cpu().numpy(), out_o)
+        assert err <= 5e-4, (T, err)
+        out_d = dl.forward(torch.from_numpy(x).to(gpu))[0].cpu().numpy()
+        assert rel_l2(out_d, out_o) > 1e-2          # the dual layer serves experts >= K cold
+
+
 def test_xfer_large_flush_split_into_launches(gpu):
     """A flush of 40 jobs x 3 pages (two copy launches), pages that are not
     a multiple of the copy chunk or of 16 bytes, and completions handed out a
