@@ -677,8 +677,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,stack,promote,stackdyn",
-                    help="comma list of iq2s,q4k,dual,prefill,stack,promote,stackdyn")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn",
+                    help="comma list of iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
@@ -714,7 +714,7 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "stack", "promote", "stackdyn"))
+    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "q4stream", "stack", "promote", "stackdyn"))
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -727,7 +727,7 @@ def main():
         results["iq2s"] = run_config(la, torch, "decode all-IQ2_S T=1", cold_only, 1, args.steps, args.warmup, dev)
     if "q4k" in cfgs:
         results["q4k"] = run_config(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev)
-    if "dual" in cfgs or "prefill" in cfgs or "promote" in cfgs:
+    if any(c in cfgs for c in ("dual", "prefill", "q4stream", "promote")):
         dual = copy.copy(full)
         gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
         dual.hot_gu = np.concatenate([full.hot_gu[e * gb:(e + 1) * gb] for e in hot57])
@@ -741,6 +741,13 @@ def main():
         if "prefill" in cfgs:
             results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
+        if "q4stream" in cfgs:
+            # q4stream: the same chunk with every expert at the hot precision,
+            # read from the all-expert hot source (identity page table)
+            q4s = copy.copy(full)
+            q4s.router_b = dual.router_b
+            results["q4stream"] = run_config(la, torch, "prefill q4stream (every expert Q4_K) T=512", q4s, 512,
+                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
         if "promote" in cfgs:
             results["promote"] = run_promote(la, torch, full, dual, spec, dev)
 
