@@ -158,13 +158,18 @@ int32_t publish(llapis_residency * r, hipStream_t s, bool all) {
         nb = 0;
         return hipGetLastError() == hipSuccess;
     };
+    // every capacity first: a refusal leaves all dirty marks in place
+    for (int il = 0; il < r->L; ++il) {
+        if (!all && !r->dirty[il]) continue;
+        const int k = moert_policy_layer_k(r->pol, il);
+        if (k < 0 || k > r->K) return rfail("llapis_residency: layer capacity above the runtime's staging");
+    }
     for (int il = 0; il < r->L; ++il) {
         if (!all && !r->dirty[il]) continue;
         r->dirty[il] = 0;
         const llapis_residency::Mirrors & m = r->mirrors[il];
         if (!m.es || !m.se || !m.ss) continue;
         const int k = moert_policy_layer_k(r->pol, il);
-        if (k < 0 || k > r->K) return rfail("llapis_residency: layer capacity above the mirrors' size");
         int32_t * b = r->staging + (size_t)il * per;
         memcpy(b, moert_policy_exp_slot_view(r->pol, il), (size_t)r->E * 4);
         memcpy(b + r->E, moert_policy_slot_exp_view(r->pol, il), (size_t)k * 4);
