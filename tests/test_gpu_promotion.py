@@ -374,24 +374,29 @@ def test_promotion_loop_with_device_counts(gpu, oracle):
         pol.close()
 
 
-def test_native_residency_loop_two_layers(gpu, oracle):
+@pytest.mark.parametrize("kpl", [None, (4, 2)])
+def test_native_residency_loop_two_layers(gpu, oracle, kpl):
     """The same loop run by the native runtime (llapis_residency_*) over two
     layers whose routing drifts in opposite directions: every call's output
     matches the oracle under the page table published at the previous token
     end, the device mirrors equal the policy's after each token end, the
     counters the runtime pulled add up to the pairs the GPU routed, and each
-    layer ends holding its own phase's experts, byte for byte."""
+    layer ends holding its own phase's experts, byte for byte.  With
+    per-layer capacities each layer's mirrors are published at its own K
+    from the runtime's staging (sized for the largest)."""
     from llapis_amd.policy import ResidencyLoop
     torch = torch_mod()
     lib = la.lib()
     spec = FULL16
     E, K, top_k, NL = spec.n_expert, 4, spec.top_k, 2
     gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
-    rl = ResidencyLoop(NL, E, K, copy_wgs=8, cost_horizon=64, cost_reuse=2.0, cost_per_token=2)
+    rl = ResidencyLoop(NL, E, K, copy_wgs=8, k_per_layer=kpl, cost_horizon=64, cost_reuse=2.0, cost_per_token=2)
     pol = rl.policy
     layers = []
     try:
         for il in range(NL):
+            K = kpl[il] if kpl else 4
+            assert pol.layer_k(il) == K
             lay_all = layer(spec, 81 + il, list(range(E)), scales=True)
             src_s = lay_all.s_hot.copy()
             srcs = [u8(torch, lay_all.hot_gu, gpu), u8(torch, lay_all.hot_dn, gpu), u8(torch, src_s, gpu)]
@@ -459,7 +464,7 @@ def test_native_residency_loop_two_layers(gpu, oracle):
             v = pol.views(il)
             assert np.array_equal(dl.slot_state.cpu().numpy(), v["slot_state"])
             hg, hd, hs = dl.hot_gu.cpu().numpy(), dl.hot_dn.cpu().numpy(), dl.s_hot.cpu().numpy()
-            ready = [s for s in range(K) if v["slot_state"][s] == la.SLOT_READY]
+            ready = [s for s in range(pol.layer_k(il)) if v["slot_state"][s] == la.SLOT_READY]
             assert len(ready) >= 2
             for s in ready:
                 e = int(v["slot_exp"][s])
