@@ -231,7 +231,8 @@ void    llapis_xfer_get_stats(llapis_xfer * x, llapis_xfer_stats * out);
  * submits promotions as FILLING -- (3) publishes the changed layers' mirrors
  * with copies on `stream` (the next token sees them in stream order) and (4)
  * flushes the engine, whose copies overlap the next token.  Counts reach the
- * policy only there (stats reads in between do not pull them). */
+ * policy only there and in llapis_residency_refresh (stats reads and
+ * refreshes called on the policy directly do not pull them). */
 typedef struct llapis_residency llapis_residency;
 typedef struct llapis_residency_stats {
     long long tokens, fetches, submitted, completed, publications;
@@ -262,6 +263,12 @@ int32_t llapis_residency_counters(llapis_residency * r, int32_t il, int32_t ** c
 /* Every layer's mirrors, copied on stream (after seeding). */
 int32_t llapis_residency_publish_all(llapis_residency * r, void * stream);
 int32_t llapis_residency_token_end(llapis_residency * r, void * stream);
+/* The same steps around moert_policy_refresh(reason) (a MOERT_REFRESH_*
+ * value): the prompt-end and turn-end decisions (moe_dual.cpp calls them at
+ * those points).  Prompt tokens are counted with moert_policy_on_prompt_token
+ * on llapis_residency_policy(r); their routing stays in the counters until
+ * the next token_end or refresh drains them. */
+int32_t llapis_residency_refresh(llapis_residency * r, int32_t reason, void * stream);
 void    llapis_residency_get_stats(llapis_residency * r, llapis_residency_stats * out);
 
 /* ------------------------------------------------------------ model files

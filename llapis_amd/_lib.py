@@ -286,6 +286,7 @@ SIGNATURES = {
     "llapis_residency_counters": (i32, [vp, i32, C.POINTER(vp), C.POINTER(vp)]),
     "llapis_residency_publish_all": (i32, [vp, vp]),
     "llapis_residency_token_end": (i32, [vp, vp]),
+    "llapis_residency_refresh": (i32, [vp, i32, vp]),
     "llapis_residency_get_stats": (None, [vp, C.POINTER(LlapisResidencyStats)]),
     **POLICY_SIGNATURES,
     **STORE_SIGNATURES,

@@ -39,7 +39,7 @@ struct llapis_residency {
     int32_t * counts_host = nullptr;    // pinned, mapped
     int32_t * counts_host_dev = nullptr;  // its device address
     hipStream_t cur = nullptr;          // the stream of the token_end in progress (0 is the null stream)
-    bool in_token_end = false;
+    bool in_call = false;               // inside token_end / refresh: the counters may be drained
     struct Mirrors {
         int32_t * es = nullptr;
         int32_t * se = nullptr;
@@ -118,7 +118,7 @@ void cb_publish_layer(void * user, int32_t il) {
 // every layer's counters in one copy; waits for the token on the stream
 void cb_fetch_external(void * user) {
     llapis_residency * r = static_cast<llapis_residency *>(user);
-    if (!r->in_token_end || r->err != hipSuccess) return;
+    if (!r->in_call || r->err != hipSuccess) return;
     const int n = r->L * r->E + 2 * r->L;
     k_drain_counts<<<std::min(16, (n + 255) / 256), 256, 0, r->cur>>>(r->counts_dev, r->counts_host_dev, n);
     hipError_t e = hipGetLastError();
@@ -269,8 +269,12 @@ int32_t llapis_residency_publish_all(llapis_residency * r, void * stream) {
     return publish(r, (hipStream_t)stream, true);
 }
 
-int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
-    if (!r) return rfail("llapis_residency_token_end: null runtime");
+}  // extern "C"
+
+namespace {
+
+// steps 1-4 around one decision: on_token_end (reason < 0) or refresh(reason)
+int32_t decide(llapis_residency * r, void * stream, int32_t reason) {
     const double t_in = ms_now(), w_in = r->st.wait_ms;
     hipStream_t s = (hipStream_t)stream;
     // 1. finished promotions
@@ -287,19 +291,35 @@ int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
     }
     // 2. the decision (pulls the counters through fetch_external)
     r->cur = s;
-    r->in_token_end = true;
-    moert_policy_on_token_end(r->pol);
-    r->in_token_end = false;
+    r->in_call = true;
+    if (reason < 0) moert_policy_on_token_end(r->pol);
+    else moert_policy_refresh(r->pol, reason);
+    r->in_call = false;
     if (r->err != hipSuccess) {
         r->err = hipSuccess;
-        return rfail("llapis_residency_token_end: counter copy failed");
+        return rfail("llapis_residency: counter drain failed");
     }
-    ++r->st.tokens;
+    if (reason < 0) ++r->st.tokens;
     // 3. publication, 4. the copies
     if (publish(r, s, false) != 0) return -1;
     if (llapis_xfer_flush(r->x, stream) != 0) return rfail(llapis_xfer_last_error());
     r->st.host_ms += (ms_now() - t_in) - (r->st.wait_ms - w_in);
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t llapis_residency_token_end(llapis_residency * r, void * stream) {
+    if (!r) return rfail("llapis_residency_token_end: null runtime");
+    return decide(r, stream, -1);
+}
+
+int32_t llapis_residency_refresh(llapis_residency * r, int32_t reason, void * stream) {
+    if (!r) return rfail("llapis_residency_refresh: null runtime");
+    if (reason < 0) return rfail("llapis_residency_refresh: bad reason");
+    return decide(r, stream, reason);
 }
 
 void llapis_residency_get_stats(llapis_residency * r, llapis_residency_stats * out) {

@@ -210,6 +210,10 @@ class ResidencyLoop:
     def token_end(self, stream):
         self._check(self.lib.llapis_residency_token_end(self.r, stream))
 
+    def refresh(self, reason, stream):
+        """A prompt-end / turn-end decision (L.REFRESH_*) with the counters drained."""
+        self._check(self.lib.llapis_residency_refresh(self.r, reason, stream))
+
     def stats(self):
         s = L.LlapisResidencyStats()
         self.lib.llapis_residency_get_stats(self.r, C.byref(s))

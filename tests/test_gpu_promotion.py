@@ -419,7 +419,9 @@ def test_native_residency_loop_two_layers(gpu, oracle, kpl):
         rl.publish_all(stream)
         routed = {"hot": 0, "cold": 0}
         errs = []
-        plan = [(1, "A")] * 10 + [(4, "A")] + [(1, "B")] * 16 + [(4, "B")] + [(1, "B")] * 4
+        # a 40-token prompt chunk (prefill path) near the end: no decision, its
+        # routing waits in the counters for the next token end
+        plan = [(1, "A")] * 10 + [(4, "A")] + [(1, "B")] * 16 + [(4, "B")] + [(40, "Bp")] + [(1, "B")] * 4
         for step, (T, phase) in enumerate(plan):
             for il, (lay_all, src_s, _, dl) in enumerate(layers):
                 v = pol.views(il)
@@ -444,15 +446,20 @@ def test_native_residency_loop_two_layers(gpu, oracle, kpl):
                 hot = sum(vl.residency.is_hot(int(e)) for e in ids_h.ravel())
                 routed["hot"] += hot
                 routed["cold"] += ids_h.size - hot
-            rl.token_end(stream)
+            if phase == "Bp":
+                pol.prompt_tokens(T)
+            else:
+                rl.token_end(stream)
             say(f"step {step} T={T} {phase}: " + "; ".join(
                 f"L{il} slots {list(pol.views(il)['slot_exp'])} states {list(pol.views(il)['slot_state'])}"
                 for il in range(NL)))
+        rl.refresh(L.REFRESH_TURN_END, stream)             # drains the counters too
         torch.cuda.synchronize()
         assert np.median(errs) <= 1e-6, errs
         st = rl.stats()
         say(f"runtime {st}; policy {pol.stats()}")
-        assert st["tokens"] == st["fetches"] == len(plan)
+        n_visible = sum(ph != "Bp" for _, ph in plan)
+        assert st["tokens"] == n_visible and st["fetches"] == n_visible + 1
         assert (st["hot_pairs"], st["cold_pairs"]) == (routed["hot"], routed["cold"])
         assert st["submitted"] >= 8 and st["completed"] >= 4
         # drain: the last copies land, one more token end makes them READY

@@ -350,6 +350,7 @@ def test_residency_runtime_refuses_bad_geometry():
     # the handle-taking calls refuse a null runtime
     assert lib.llapis_residency_token_end(None, None) == -1
     assert lib.llapis_residency_publish_all(None, None) == -1
+    assert lib.llapis_residency_refresh(None, 0, None) == -1
     assert lib.llapis_residency_set_mirrors(None, 0, None, None, None) == -1
     assert not lib.llapis_residency_policy(None)
     s = L.LlapisResidencyStats()
