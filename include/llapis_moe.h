@@ -243,8 +243,10 @@ typedef struct llapis_residency_stats {
 /* cfg as moert_policy_create's (callbacks are the runtime's own); copy_wgs
  * as llapis_xfer_create's.  Allocates the counters (device), their pinned
  * read-back and the publication staging, sized for the largest capacity in
- * cfg: a K re-fit (moert_policy_resize_k) above it needs a new runtime, and
- * publication fails with an error rather than write past the staging.  All
+ * cfg.  After a K re-fit (moert_policy_resize_k) publish every layer with
+ * llapis_residency_publish_all; a capacity above the one at creation needs a
+ * new runtime, and publication fails with an error rather than write past
+ * the staging.  All
  * calls on one runtime must come from one thread.  NULL on failure (the
  * geometry is checked before any device call). */
 llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int32_t copy_wgs);

@@ -484,6 +484,32 @@ def test_native_residency_loop_two_layers(gpu, oracle, kpl):
         rl.close()
 
 
+def test_native_residency_refuses_growth_past_its_staging(gpu):
+    """A re-fit that grows a layer above the capacity the runtime was created
+    for: the publication that follows a resize fails with an error (nothing
+    is written past the staging), and shrinking back makes it work again."""
+    from llapis_amd.policy import ResidencyLoop
+    torch = torch_mod()
+    E, K = 16, 2
+    rl = ResidencyLoop(1, E, K)
+    try:
+        mir = [torch.full((n,), -1, dtype=torch.int32, device=gpu) for n in (E, 2 * K, 2 * K)]
+        rl.set_mirrors(0, *[m.data_ptr() for m in mir])
+        stream = torch.cuda.current_stream().cuda_stream
+        rl.token_end(stream)
+        assert rl.policy.resize(K + 1) == 1 and rl.policy.layer_k(0) == K + 1
+        with pytest.raises(RuntimeError, match="capacity above"):
+            rl.publish_all(stream)
+        assert rl.policy.resize(K) == 1
+        rl.publish_all(stream)
+        rl.token_end(stream)
+        torch.cuda.synchronize()
+        assert rl.stats()["fetches"] == 2
+        assert torch.equal(mir[0].cpu(), torch.full((E,), -1, dtype=torch.int32))   # nothing resident
+    finally:
+        rl.close()
+
+
 def test_q4stream_prefill_reads_the_promotion_source(gpu, oracle):
     """q4stream (every expert of a prefill chunk at the hot precision) on a
     view of a dual layer whose hot pool is the promotion source: the outputs
