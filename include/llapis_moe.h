@@ -250,6 +250,9 @@ typedef struct llapis_residency_stats {
  * calls on one runtime must come from one thread.  NULL on failure (the
  * geometry is checked before any device call). */
 llapis_residency * llapis_residency_create(const moert_policy_config * cfg, int32_t copy_wgs);
+/* Waits for the engine's copies and the last publication; the calls that
+ * count into the runtime's counters must have completed before it is freed
+ * (synchronise their stream first). */
 void               llapis_residency_free(llapis_residency * r);
 const char *       llapis_residency_last_error(void);
 /* The policy (seed it, read views and stats) and the engine (set its page
