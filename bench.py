@@ -525,7 +525,7 @@ def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_
     return res
 
 
-def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift_every=64):
+def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift_every=64, copy_wgs=0):
     """The 30-layer decode with the residency loop a server runs, in native
     code (llapis_residency_*): every call counts its routing on the device;
     after each token the runtime pulls the counts (one D2H copy for all
@@ -544,7 +544,7 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
     st = Stack(la, torch, full, spec, n_layers, dev)
     E, K = spec.n_expert, 57
     gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
-    rl = ResidencyLoop(n_layers, E, K, copy_wgs=0)
+    rl = ResidencyLoop(n_layers, E, K, copy_wgs=copy_wgs)
     pol = rl.policy
     src_gu = torch.from_numpy(full.hot_gu).to(dev)       # the promotion source: all experts, hot formats
     src_dn = torch.from_numpy(full.hot_dn).to(dev)
@@ -623,7 +623,7 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
     segs = [float(hw[i:i + drift_every].mean()) for i in range(0, tokens, drift_every)]
     first = [float(hw[i:i + 8].mean()) for i in range(0, tokens, drift_every)]
     res = {"layers": n_layers, "tokens": tokens, "ms_per_token": wall * 1e3 / tokens, "tok_per_s": tokens / wall,
-           "loop": "native", "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
+           "loop": "native", "engine_copy_wgs": copy_wgs, "promotions": int(pst["promotions"]), "fills_completed": int(pst["fills_completed"]),
            "publications": int(rst["publications"] - r0["publications"]), "copies_bytes": int(xs.bytes),
            "hit_rate_per_phase": segs, "hit_rate_first_8_tokens_per_phase": first,
            "token_end_ms_per_token": host_s * 1e3 / tokens, "sync_no_loop_ms_per_token": sync_ms,
@@ -680,6 +680,8 @@ def main():
     ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn",
                     help="comma list of iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--engine-wgs", type=int, default=0,
+                    help="stackdyn: the promotion engine's copy mode (0 hipMemcpyAsync, else copy-kernel workgroups)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -754,7 +756,7 @@ def main():
     if "stack" in cfgs:
         results["stack"] = run_stack(la, torch, full, spec, dev)
     if "stackdyn" in cfgs:
-        results["stack_dynamic"] = run_stack_dynamic(la, torch, full, spec, dev)
+        results["stack_dynamic"] = run_stack_dynamic(la, torch, full, spec, dev, copy_wgs=args.engine_wgs)
 
     head = results.get("iq2s") or next(iter(v for v in results.values() if "dominant_gbs" in v), None)
     if head is None:
