@@ -183,3 +183,39 @@ def test_xfer_refuses_bad_arguments_without_a_device():
     assert lib.llapis_xfer_submit(None, 0, 0, 0) == -1
     assert lib.llapis_xfer_take_done(None, None, 0) == -1
     assert lib.llapis_xfer_in_flight(None) == 0
+
+
+RESIDENCY_BINDING_C = r"""
+#include "llapis_moe.h"
+void bind(llapis_moe_layer * layer, int32_t n_layers, int32_t n_expert, int32_t k, void * compute_stream,
+          int32_t ** es, int32_t ** se, int32_t ** ss, int64_t n_prompt) {
+    moert_policy_config cfg;
+    moert_policy_config_defaults(&cfg);
+    cfg.n_layers = n_layers; cfg.n_expert = n_expert; cfg.k = k;
+    llapis_residency * R = llapis_residency_create(&cfg, 0);
+    moert_policy * P = llapis_residency_policy(R);
+    llapis_xfer * X = llapis_residency_xfer(R);
+    (void)X;
+    for (int il = 0; il < n_layers; ++il) {
+        llapis_residency_counters(R, il, &layer[il].route_counts, &layer[il].route_hits);
+        llapis_residency_set_mirrors(R, il, es[il], se[il], ss[il]);
+        moert_policy_commit_seed(P, il, 0, 0);
+    }
+    llapis_residency_publish_all(R, compute_stream);
+    moert_policy_on_prompt_token(P, n_prompt);
+    llapis_residency_refresh(R, MOERT_REFRESH_PROMPT_END, compute_stream);
+    llapis_residency_token_end(R, compute_stream);
+    llapis_residency_refresh(R, MOERT_REFRESH_TURN_END, compute_stream);
+    llapis_residency_stats st;
+    llapis_residency_get_stats(R, &st);
+    llapis_residency_free(R);
+}
+"""
+
+
+def test_residency_binding_compiles_as_c(tmp_path):
+    """The residency loop's binding, as an integrator writes it in C against
+    the shipped headers, compiles (C11, warnings as errors)."""
+    src = tmp_path / "bind.c"
+    src.write_text(RESIDENCY_BINDING_C)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", "-I", str(INCLUDE), str(src)], check=True)
