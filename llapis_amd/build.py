@@ -39,13 +39,27 @@ def _run(cmd):
     return out
 
 
+def gelu_table():
+    """Generate the fp16 GELU table of the CPU path's GEGLU (gen_gelu_table.c:
+    host float arithmetic and glibc tanhf, as the CPU path fills its own)."""
+    gen = BUILD / "gen_gelu_table"
+    _run(["gcc", "-O2", "-ffp-contract=off", "-mf16c", str(CSRC / "gen_gelu_table.c"), "-o", str(gen), "-lm"])
+    out = subprocess.run([str(gen)], stdout=subprocess.PIPE, check=True, text=True).stdout
+    inc = BUILD / "gelu_table.inc"
+    if not inc.exists() or inc.read_text() != out:
+        inc.write_text(out)
+    return inc
+
+
 def build(verbose=False):
     BUILD.mkdir(exist_ok=True)
     hipcc = _hipcc()
+    gelu_table()
     hip_flags = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+                 "-Wno-unused-variable",
                  # packed fp32 VALU ops are kept out of every kernel
                  "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-                 f"-I{CSRC}", f"-I{PKG.parent / 'include'}"]
+                 f"-I{CSRC}", f"-I{BUILD}", f"-I{PKG.parent / 'include'}"]
     jobs = []
     for src in HIP_SOURCES:
         obj = BUILD / (src + ".o")

@@ -112,14 +112,22 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(SQRT_2_OVER_PI * x * (1.0f + GELU_COEF_A * x * x)));
 }
 
-// GEGLU of one element in a given mode.  Table mode reproduces the CPU's
-// fp16 lookup (vec.h:1414-1428): gelu evaluated at fp16(g), rounded to fp16.
+// The CPU path's fp16 GELU table, generated at build time by
+// gen_gelu_table.c with the host's float arithmetic and tanhf.
+#include "gelu_table.inc"
+
+// GEGLU of one element in a given mode.  Table mode is the CPU's fp16
+// lookup (vec.h:1414-1428): the table entry at fp16(g) (round to nearest
+// even), clamped to 0 below -10 and to the identity above 10.
 template <int SRC>
 __device__ __forceinline__ float geglu1(float g, float u) {
     if (SRC == SRC_GEGLU_TANH || SRC == SRC_GEGLU_TANH_COH) return __fmul_rn(gelu_tanh(g), u);
     if (g <= -10.0f) return 0.0f;
     if (g >= 10.0f) return __fmul_rn(g, u);
-    return __fmul_rn(round_to_half(gelu_tanh(round_to_half(g))), u);
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)g);
+    const uint32_t mag = min(h & 0x7FFFu, (uint32_t)LLAPIS_GELU_TAB_SPAN - 1u);    // |g| < 10: mag <= 0x4900
+    const uint16_t y = gelu_f16_table[mag + (h >> 15) * LLAPIS_GELU_TAB_SPAN];
+    return __fmul_rn((float)__builtin_bit_cast(_Float16, y), u);
 }
 
 // ----------------------------------------------- wave reductions (wave64)

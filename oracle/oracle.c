@@ -484,8 +484,12 @@ void orc_geglu(const float * g, const float * u, float * out, int64_t n, int gel
 void orc_router(const float * x, int64_t T, const float * w_r, const float * bias,
                 int64_t d, int64_t n_expert, int64_t top_k,
                 int32_t * ids, float * w, float * probs) {
+    /* tokens are independent: a parallel loop gives the serial loop's bits */
+    #pragma omp parallel
+    {
     float * p = malloc(sizeof(float) * n_expert);
     int32_t * order = malloc(sizeof(int32_t) * n_expert);
+    #pragma omp for schedule(static)
     for (int64_t t = 0; t < T; ++t) {
         const float * xt = x + t * d;
         float mx = -INFINITY;
@@ -525,6 +529,7 @@ void orc_router(const float * x, int64_t T, const float * w_r, const float * bia
     }
     free(p);
     free(order);
+    }
 }
 
 /* ---------------------------------------------------------------- layer */
@@ -540,9 +545,14 @@ void orc_moe_experts(const orc_layer * L, const float * x, int64_t T,
                      const int32_t * ids, const float * w, int act_mode, int gelu_mode,
                      float * out, float * y_pairs) {
     const int64_t D = L->d_model, F = L->n_ff, K = L->top_k;
+    /* tokens are independent (each token's pairs, then its combine): a
+     * parallel loop over tokens gives the serial loop's bits */
+    #pragma omp parallel
+    {
     float * gu = malloc(sizeof(float) * 2 * F);
     float * a = malloc(sizeof(float) * F);
     float * y = malloc(sizeof(float) * D * K);
+    #pragma omp for schedule(dynamic, 1)
     for (int64_t t = 0; t < T; ++t) {
         for (int64_t k = 0; k < K; ++k) {
             const int32_t e = ids[t * K + k];
@@ -573,4 +583,5 @@ void orc_moe_experts(const orc_layer * L, const float * x, int64_t T,
     free(gu);
     free(a);
     free(y);
+    }
 }

@@ -137,11 +137,36 @@ def test_geglu_vs_oracle(gpu, oracle, mode):
     torch.cuda.synchronize()
     og = out.cpu().numpy()
     oo = np.stack([oracle.geglu(gu[c, :F], gu[c, F:], mode) for c in range(n)])
-    # the device's tanhf may differ from glibc's by an ulp; in table mode that
-    # can move one fp16 rounding: allow it on a handful of elements
-    close = np.isclose(og, oo, rtol=2e-6 if mode == la.GELU_TANH else 0, atol=1e-7)
-    assert (~close).sum() <= max(2, og.size // 2000), (~close).sum()
-    assert rel_l2(og, oo) <= 1e-5
+    if mode == la.GELU_TABLE:
+        # the device reads the host-built fp16 table: bit-exact
+        assert np.array_equal(og.view(np.uint32), oo.view(np.uint32))
+    else:
+        # the device's tanhf may differ from glibc's by an ulp or two
+        close = np.isclose(og, oo, rtol=2e-6, atol=1e-7)
+        assert (~close).sum() <= max(2, og.size // 2000), (~close).sum()
+        assert rel_l2(og, oo) <= 1e-5
+
+
+def test_geglu_table_exhaustive(gpu, oracle):
+    """Table mode depends on g only through fp16(g): every fp16 value of
+    magnitude below 10 (and inputs just inside +-10, which round to fp16
+    +-10.0), against the oracle, bit for bit, with u = 1 and with a random u."""
+    torch = torch_mod()
+    say("geglu table exhaustive")
+    F = 1024
+    mags = np.arange(0, 0x4900, dtype=np.uint16)
+    g = np.concatenate([mags.view(np.float16).astype(np.float32), (mags | 0x8000).view(np.float16).astype(np.float32),
+                        np.array([9.9999990, -9.9999990, 9.99, -9.99, 10.0, -10.0, 12.0, -12.0], np.float32)])
+    g = np.concatenate([g, np.zeros((-g.size) % F, np.float32)])
+    n = g.size // F
+    for u in (np.ones_like(g), la.synth_normal(33, g.size)):
+        gu = np.concatenate([g.reshape(n, F), u.reshape(n, F)], axis=1)
+        out = la.geglu(torch.from_numpy(np.ascontiguousarray(gu)).to(gpu), F, la.GELU_TABLE)
+        torch.cuda.synchronize()
+        og = out.cpu().numpy().ravel()
+        oo = oracle.geglu(g, u, la.GELU_TABLE)
+        bad = np.nonzero(og.view(np.uint32) != oo.view(np.uint32))[0]
+        assert bad.size == 0, [(float(g[i]), float(og[i]), float(oo[i])) for i in bad[:5]]
 
 
 def _layer_case(spec, seed, n_hot, scales):
