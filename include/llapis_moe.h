@@ -153,6 +153,22 @@ uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tok
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
                        int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
 
+/* llapis_moe_ffn without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * call's scratch is a fixed device array of LLAPIS_NOALLOC_SCRATCH_BYTES in
+ * the library, one per GPU, held until the process ends; nothing is
+ * allocated.  A call whose llapis_moe_ffn_workspace_size exceeds it is
+ * refused (-1, llapis_last_error() says how much it needs): at the
+ * benchmark's shapes (d_model 2816, n_ff 704, 128 experts, top-8) that
+ * admits batches of up to 48 tokens.  The first call on a device clears the array with a kernel on
+ * its stream.  Every call on one GPU shares that GPU's array and leaves its
+ * contents behind: calls that overlap on one GPU (other streams, other
+ * threads) race, so order them as one stream would. */
+#define LLAPIS_NOALLOC_SCRATCH_BYTES (8u << 20)
+int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
+                               int32_t * ids, float * weights, void * stream);
+
 /* Zero the control block of a fused-layer workspace (a kernel on `stream`). */
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
 

@@ -77,6 +77,7 @@ class LlapisMoeLayer(C.Structure):
 
 
 XFER_MAX_GROUPS = 4
+NOALLOC_SCRATCH_BYTES = 8 << 20          # LLAPIS_NOALLOC_SCRATCH_BYTES
 
 
 class LlapisKfitInputs(C.Structure):
@@ -250,6 +251,7 @@ SIGNATURES = {
     "llapis_moe_ffn_workspace_size": (u64, [C.POINTER(LlapisMoeLayer), i32]),
     "llapis_moe_ffn": (i32, [C.POINTER(LlapisMoeLayer), vp, i32, vp, vp, vp, vp, u64, vp]),
     "llapis_moe_ffn_workspace_init": (i32, [C.POINTER(LlapisMoeLayer), vp, u64, vp]),
+    "llapis_moe_ffn_noalloc": (i32, [C.POINTER(LlapisMoeLayer), vp, i32, vp, vp, vp, vp]),
     "llapis_moe_ffn_status": (i32, [vp, u64, vp]),
     "llapis_set_tuning": (None, [i32, i32]),
     "llapis_profile_enable": (None, [i32]),

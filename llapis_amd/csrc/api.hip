@@ -867,4 +867,57 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
     return 0;
 }
 
+// ------------------------------------------------- entry point without allocation
+
+}  // extern "C"
+
+namespace {
+// The scratch of llapis_moe_ffn_noalloc: one fixed array per GPU, held until
+// the process ends.  Host code never uses this name as an address (on the
+// host it is only a stand-in for the symbol); it uses the device address
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[LLAPIS_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_na_mu;
+std::map<int, uint8_t *> g_na_ptr;     // device -> address of that device's scratch
+
+// The current device's scratch address: looked up (and the array zeroed on
+// `s`) at the first call on each device.
+int32_t noalloc_scratch(uint8_t ** out, hipStream_t s) {
+    int dev = 0;
+    LL_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    auto it = g_na_ptr.find(dev);
+    if (it != g_na_ptr.end()) {
+        *out = it->second;
+        return 0;
+    }
+    void * p = nullptr;
+    LL_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail("llapis_moe_ffn_noalloc: no device address for the scratch array");
+    // the decode path's control block must start at zero: clear the whole
+    // array once, with a kernel (no memset node if the caller is capturing)
+    LL_TRY(launch_zero_i32(static_cast<int *>(p), (int)(LLAPIS_NOALLOC_SCRATCH_BYTES / 4), s));
+    g_na_ptr[dev] = static_cast<uint8_t *>(p);
+    *out = static_cast<uint8_t *>(p);
+    return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
+                               float * w_out, void * stream) {
+    if (!L) return fail("llapis_moe_ffn_noalloc: null layer");
+    if (T <= 0) return 0;
+    const uint64_t need = llapis_moe_ffn_workspace_size(L, T);
+    if (need > LLAPIS_NOALLOC_SCRATCH_BYTES)
+        return fail("llapis_moe_ffn_noalloc: this call needs " + std::to_string(need) +
+                    " bytes of scratch, more than the fixed " + std::to_string(LLAPIS_NOALLOC_SCRATCH_BYTES) +
+                    " bytes; use llapis_moe_ffn with a workspace");
+    uint8_t * ptr = nullptr;
+    if (const int32_t rc = noalloc_scratch(&ptr, (hipStream_t)stream)) return rc;
+    return llapis_moe_ffn(L, x, T, out, ids_out, w_out, ptr, LLAPIS_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 }  // extern "C"

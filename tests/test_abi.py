@@ -219,3 +219,19 @@ def test_residency_binding_compiles_as_c(tmp_path):
     src = tmp_path / "bind.c"
     src.write_text(RESIDENCY_BINDING_C)
     subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-fsyntax-only", "-I", str(INCLUDE), str(src)], check=True)
+
+
+def test_noalloc_scratch_size_matches_header():
+    text = (INCLUDE / "llapis_moe.h").read_text()
+    m = re.search(r"#define LLAPIS_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_refuses_before_any_device_call():
+    """A null layer and a call larger than the fixed array are refused on the
+    host, with no GPU in the process."""
+    lib = _lib.lib()
+    assert lib.llapis_moe_ffn_noalloc(None, None, 1, None, None, None, None) != 0
+    d = _lib.LlapisMoeLayer(2816, 704, 128, 8, 57, 12, 6, 22, 20, 0, 0, *([None] * 12))
+    assert lib.llapis_moe_ffn_noalloc(C.byref(d), None, 512, None, None, None, None) != 0
+    assert b"bytes of scratch" in lib.llapis_last_error()
