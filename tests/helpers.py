@@ -89,7 +89,7 @@ def per_token_rel_l2(got, want):
     return np.array([rel_l2(got[t], want[t]) for t in range(got.shape[0])])
 
 
-def check_layer_bars(got, want, say=print):
+def check_layer_bars(got, want, say=print, frac_above=0.01):
     """The layer bar against the oracle: the whole output within relative L2
     5e-4 (the requirement is 1e-3), no token above 3e-3, at most 1 % of the
     tokens above 1e-3 and, with more than 16 tokens, the median token at most
@@ -98,14 +98,17 @@ def check_layer_bars(got, want, say=print):
     re-quantise one down activation to the neighbouring q8 integer, which
     moves that pair by ~1e-3 and its token by ~3e-4 (two such flips in one
     token reach ~1e-3).  Measured at 512 tokens: about one token in ten has a
-    flip, the median token is ~1e-7."""
+    flip, the median token is ~1e-7.  frac_above: the share of tokens allowed
+    above 1e-3 (1 %; q8_1 mode scales every 32-block in fp32 on both
+    matvecs, so its fp32 orders differ in more places and it flips about 1.5
+    times as often: 2 %)."""
     err = rel_l2(got, want)
     per = per_token_rel_l2(got, want)
     say(f"  rel_l2 = {err:.3e}; tokens: median {np.median(per):.1e} max {per.max():.1e} "
         f"({int((per > 1e-5).sum())} of {per.size} above 1e-5, {int((per > 1e-3).sum())} above 1e-3)")
     assert err <= 5e-4, err
     assert per.max() <= 3e-3, (int(per.argmax()), float(per.max()))
-    assert (per > 1e-3).sum() <= per.size // 100, int((per > 1e-3).sum())
+    assert (per > 1e-3).sum() <= int(frac_above * per.size), int((per > 1e-3).sum())
     if per.size > 16:
         assert np.median(per) <= 1e-5
     return per
