@@ -122,11 +122,11 @@ hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 // ------------------------------------------------------------ prefill path
 
 constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)
-constexpr int PF_TOK = 64;            // routed pairs per tile (two 32-column MFMA tiles per wave)
+constexpr int PF_TOK = 64;            // routed pairs per group (four 16-token MFMA tiles)
 constexpr int PF_MAX_PAIRS = 4096;    // routed pairs per prefill launch (T * top_k)
 constexpr int PF_MAX_FF = 4096;       // longest n_ff the down activation kernel stages
 
-// a run of up to PF_TOK pairs routed to one expert
+// a group: a run of up to PF_TOK pairs routed to one expert
 struct PfTile {
     int tier;                   // 0 hot (idx = slot), 1 cold (idx = expert)
     int idx;
@@ -148,13 +148,11 @@ struct PfParams {
     int32_t * sorted;                    // [P] pair indices grouped by expert, ascending within
     PfTile * tiles;                      // [max_tiles]
     int max_tiles;
-    _Float16 * xq;                       // [T][d_model] q8_K values as exact fp16
+    int8_t * xq;                         // [T][d_model] q8_K values
     float * xd;                          // [T][d_model / 256] q8_K scales
     _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
-    float * ygu;                         // [P][2 n_ff]
-    _Float16 * ah;                       // [P][n_ff] d8 q 2^e of the down activations: fp16 high part
-    _Float16 * al;                       // [P][n_ff]                                  and exact remainder
-    float * ae;                          // [P] 2^-e
+    int8_t * aq;                         // [P][n_ff] q8_0 values of the down activations
+    float * ad;                          // [P][n_ff / 32] their scales
     float * ydn;                         // [P][d_model]
     int32_t * rc_counts;                 // [n_expert] routed pairs per expert, or NULL
     int32_t * rc_hits;                   // [2] hot pairs, other pairs (with rc_counts)

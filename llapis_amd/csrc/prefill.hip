@@ -1,33 +1,32 @@
 // prefill.hip -- the MoE layer for long token batches (prefill chunks) on
-// gfx950 matrix cores.
+// gfx950 int8 matrix cores (v_mfma_i32_16x16x64_i8).
 //
 //   k_pf_bucket    routed pairs grouped by expert (a counting sort with LDS
-//                  atomics) and cut into tiles of <= PF_TOK pairs,
-//                  each tile tagged with its tier by the residency predicate
-//                  (ggml-cuda/mmid.cu:28-116 groups the same way; moert/cuda/
-//                  ffn_moe.cu:80-130 is the predicate).
+//                  atomics) and cut into groups of <= PF_TOK pairs, each tagged
+//                  with its tier by the residency predicate (ggml-cuda/mmid.cu:
+//                  28-116 groups the same way; moert/cuda/ffn_moe.cu:80-130 is
+//                  the predicate).
 //   k_pf_quant_x   each token quantised once to q8_K (the CPU path's
-//                  activation format for 256-blocks) and stored as exact fp16
-//                  integers (converted once, not per GEMM workgroup), with the
-//                  per-256 scale and the per-32 sums split into fp16-exact
-//                  high and low parts.
-//   k_pf_gate_up   grouped GEMM per (tile, 128-row block): weights staged raw
-//                  in LDS one super-block at a time and expanded in registers
-//                  to fp16 integers (Q4_K: q*sc <= 945; IQ2_S: grid*(2ls+1)
-//                  <= 1333, both exact in fp16), activations exact, so one
-//                  v_mfma_f32_32x32x16_f16 chain per super-block gives the
-//                  integer dot exactly; the Q4_K mins term is one more exact
-//                  MFMA.  Scales are applied once per super-block in fp32.
-//   k_pf_act       GEGLU and q8_0 quantisation of each pair's gate_up output
-//                  (bit-identical to the CPU path); d8*q (19 significant bits)
-//                  with a per-pair power-of-two range scale is stored as the
-//                  exact sum of two fp16 parts, ready for the MFMA operands.
-//   k_pf_down      grouped GEMM of the down projection.  Its scales are per
-//                  32-value block, so they are folded into the operands
-//                  instead of rescaling every output per block: d*q of the
-//                  weights also splits exactly into fp16 hi + lo, and three
-//                  MFMAs per step (hi*hi, hi*lo, lo*hi) give the dot to about
-//                  2^-21 relative.
+//                  activation format for 256-blocks): int8 values, the
+//                  per-256 scale, and the per-32 sums split as 32 hi + lo
+//                  (both exact in fp16) for the Q4_K mins term.
+//   k_pf_gate_up   grouped GEMM per (group, 64 gate rows + the 64 matching up
+//                  rows).  Each super-block of weights is expanded once into
+//                  int8 MFMA operands and used for every token of the group.
+//                  The sub-block scales are folded into the weights: Q4_K's
+//                  6-bit scale splits as 8 sh + sl, so q sh and q sl (<= 105)
+//                  are int8 and two accumulators give sum_j sc_j dot_j
+//                  exactly; IQ2_S's grid * (2 ls + 1) (<= 1333) splits as
+//                  64 h + l.  The Q4_K mins term is one exact fp16 MFMA against
+//                  the split per-32 sums.  Scales d_w * d8 are applied once per
+//                  super-block in fp32.  The epilogue pairs gate row i with up
+//                  row n_ff + i: GEGLU and the q8_0 quantisation of the down
+//                  activations happen here, so the gate_up outputs never go to
+//                  memory.
+//   k_pf_down      grouped GEMM of the down projection: one int8 MFMA per
+//                  32-block (the K = 64 instruction with the other block's
+//                  half of the activations zeroed), the per-block scale
+//                  d_w * d8 applied to each int32 partial in fp32.
 // The combine is the generic k_combine.
 #include <hip/hip_ext.h>
 
@@ -39,75 +38,100 @@
 namespace llapis {
 namespace dev {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-__constant__ uint16_t c_iq2s_codes_pf[1024] = {
-#include "iq2s_grid.inc"
-};
+__constant__ Iq2sTables c_iq2s_tab_pf = make_iq2s_tables();
 
-constexpr int PF_XS = 256 + 8;            // halfs per staged activation row of gate_up (padded)
+constexpr int PF_XP = 272;                // LDS pitch of a staged token row of one super-block (256 + 16)
+constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged weight row (Q4_K 144, IQ2_S <= 96)
 constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
-constexpr int PF_DXS = PF_DCB * 32 + 8;   // halfs per staged activation row of down (padded)
-constexpr int PF_WROW_GU = 144;           // LDS bytes per weight row and super-block (Q4_K 144, IQ2_S <= 96)
+constexpr int PF_DXP = PF_DCB * 32 + 16;  // LDS pitch of a staged down activation row
 constexpr int PF_WROW_DN = 112;           // staged bytes per weight row and down chunk (<= 4 * 22 + 14)
-constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows: 30 dwords, so the 32 rows a half-wave
-                                          // reads at one offset fall in 32 different bank pairs
+constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows
+constexpr int PF_NTS = PF_TOK / 16;       // 16-token MFMA tiles per group
 
-__device__ __forceinline__ uint32_t hbits(h2 v) {
-    uint32_t u;
-    __builtin_memcpy(&u, &v, 4);
-    return u;
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ h2 as_h2(uint32_t u) {
-    h2 v;
-    __builtin_memcpy(&v, &u, 4);
-    return v;
+__device__ __forceinline__ f4 mfma_f16(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ h8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const u32x4 u = {a, b, c, d};
-    h8 v;
+__device__ __forceinline__ v4i as_v4i(const u32x4 & u) {
+    v4i v;
     __builtin_memcpy(&v, &u, 16);
     return v;
 }
-__device__ __forceinline__ h2 splat(_Float16 x) { return h2{x, x}; }
-
-// four unsigned bytes -> two packed fp16 pairs of (1024 + byte)
-__device__ __forceinline__ void bytes_to_magic(uint32_t x, uint32_t & lo, uint32_t & hi) {
-    lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
-    hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+// four bytes (each < 16) times s (< 8) in one packed 16-bit multiply: every
+// product stays below 256, so no byte carries into its neighbour
+__device__ __forceinline__ uint32_t bytes_mul(uint32_t x, uint32_t s2) {
+    u16x2 a, b;
+    __builtin_memcpy(&a, &x, 4);
+    __builtin_memcpy(&b, &s2, 4);
+    const u16x2 c = a * b;
+    uint32_t r;
+    __builtin_memcpy(&r, &c, 4);
+    return r;
 }
-
-// 16 signed bytes -> 16 exact fp16 values (8 packed dwords)
-__device__ __forceinline__ void i8x16_to_h(const u32x4 & v, uint32_t (&o)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    const h2 off = splat((_Float16)(-1152.0f));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t a, b;
-        bytes_to_magic(w[i] ^ 0x80808080u, a, b);      // 1024 + (v + 128)
-        o[2 * i] = hbits(as_h2(a) + off);
-        o[2 * i + 1] = hbits(as_h2(b) + off);
-    }
+__device__ __forceinline__ uint32_t lds16(const uint8_t * smem, int off) {   // off even
+    return *reinterpret_cast<const uint16_t *>(smem + off);
 }
 
 __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t) {
     return (t.tier == 0 && t.idx >= 0 && t.idx < p.k_slots) || (t.tier == 1 && t.idx >= 0 && t.idx < p.n_expert);
 }
 
+// 16-byte chunks covering [ps, ps + len) of a slab; they stay inside the
+// slab because slabs are whole 16-byte chunks
+__device__ __forceinline__ int chunk_count(uint64_t ps, int len) {
+    return (int)(((ps + len + 15) >> 4) - (ps >> 4));
+}
+
+// ------------------------------------------------------------ IQ2_S tables
+
+// For a 4-bit IQ2_S scale ls: the three grid magnitudes {8, 25, 43} times
+// (2 ls + 1), each split as 64 h + l (h <= 20, l < 64), as the byte tables a
+// v_perm selector code | 4 sign picks from: {h+, h-, l+, l-}, bytes 0..2 for
+// codes 0..2 and byte 3 zero.
+struct Iq2sSplit {
+    uint32_t t[16][4];
+};
+constexpr Iq2sSplit make_iq2s_split() {
+    Iq2sSplit s{};
+    const int lev[3] = {8, 25, 43};
+    for (int ls = 0; ls < 16; ++ls) {
+        uint32_t hp = 0, hn = 0, lp = 0, ln = 0;
+        for (int c = 0; c < 3; ++c) {
+            const int w = lev[c] * (2 * ls + 1);
+            const int h = w >> 6, l = w & 63;
+            hp |= (uint32_t)(h & 0xFF) << (8 * c);
+            hn |= (uint32_t)((-h) & 0xFF) << (8 * c);
+            lp |= (uint32_t)(l & 0xFF) << (8 * c);
+            ln |= (uint32_t)((-l) & 0xFF) << (8 * c);
+        }
+        s.t[ls][0] = hp;
+        s.t[ls][1] = hn;
+        s.t[ls][2] = lp;
+        s.t[ls][3] = ln;
+    }
+    return s;
+}
+__constant__ Iq2sSplit c_iq2s_split = make_iq2s_split();
+
 // ----------------------------------------------------------------- bucket
 
 // One workgroup.  P = T * top_k <= PF_MAX_PAIRS, n_expert <= 256.  A
 // counting sort by expert with LDS atomics: counts, an exclusive scan over
-// the experts (pair offsets and tile offsets), then each pair takes the next
-// slot of its expert.  The order of pairs inside an expert's range is not
-// fixed, and need not be: each pair's output column is computed on its own.
+// the experts (pair offsets and group offsets), then each pair takes the
+// next slot of its expert.  The order of pairs inside an expert's range is
+// not fixed, and need not be: each pair's output column is computed on its
+// own.
 __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     constexpr int PER = PF_MAX_PAIRS / WG;
     __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_hot;
     const int P = p.T * p.top_k, E = p.n_expert;
-    // the ids, read once with every load in flight together
     int ev[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -125,8 +149,6 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     for (int k = 0; k < PER; ++k)
         if (threadIdx.x + WG * k < P) atomicAdd(&s_cnt[ev[k]], 1);
     __syncthreads();
-    // per expert (one thread each): tier, pair offset and tile offset by
-    // exclusive scans over the experts
     const int e0 = threadIdx.x;
     int n_e = 0, tier = 1, idx = e0;
     if (e0 < E) {
@@ -150,8 +172,7 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     s_off[threadIdx.x] = n_e;
     s_nt[threadIdx.x] = nt_e;
     __syncthreads();
-    // inclusive scans (Hillis-Steele over 256 entries)
-    for (int o = 1; o < 256; o <<= 1) {
+    for (int o = 1; o < 256; o <<= 1) {          // inclusive scans over the experts
         const int a = threadIdx.x >= o ? s_off[threadIdx.x - o] : 0;
         const int b = threadIdx.x >= o ? s_nt[threadIdx.x - o] : 0;
         __syncthreads();
@@ -166,7 +187,7 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         atomicAdd(p.rc_hits + 1, P - s_hot);
     }
     __syncthreads();
-    s_off[threadIdx.x] = pair0;                 // exclusive offsets
+    s_off[threadIdx.x] = pair0;
     if (threadIdx.x == 0) {
         s_off[256] = total;                     // invalid ids are placed after every expert's pairs
         *p.n_tiles = tiles;
@@ -185,6 +206,13 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     for (int k = 0; k < PER; ++k) {
         const int q = threadIdx.x + WG * k;
         if (q < P) p.sorted[s_off[ev[k]] + atomicAdd(&s_fill[ev[k]], 1)] = q;
+    }
+    // a pair with an invalid id is in no group: it contributes zeros to the combine
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int q = threadIdx.x + WG * k;
+        if (q < P && ev[k] == 256)
+            for (int r = 0; r < p.d_model; ++r) p.ydn[(int64_t)q * p.d_model + r] = 0.0f;
     }
 }
 
@@ -211,13 +239,9 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     }
     __syncthreads();
     if (!live) return;
-    if (lane < 16) {
-        uint32_t h[8];
-        i8x16_to_h(reinterpret_cast<const u32x4 *>(base + L.q)[lane], h);
-        u32x4 * d = reinterpret_cast<u32x4 *>(p.xq + (int64_t)t * p.d_model + 256 * s + 16 * lane);
-        d[0] = u32x4{h[0], h[1], h[2], h[3]};
-        d[1] = u32x4{h[4], h[5], h[6], h[7]};
-    }
+    if (lane < 16)
+        *reinterpret_cast<u32x4 *>(p.xq + (int64_t)t * p.d_model + 256 * s + 16 * lane) =
+            reinterpret_cast<const u32x4 *>(base + L.q)[lane];
     if (lane == 0) p.xd[(int64_t)t * NSB + s] = reinterpret_cast<const float *>(base + L.dK)[0];
     if (lane < 8) {
         const int * bs = reinterpret_cast<const int *>(base + L.bsum);
@@ -231,159 +255,128 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
 
 // -------------------------------------------------------------- gate_up
 
-// The (multiplier, offset) pair of Q4_K sub-block j with 6-bit scale sc, as
-// packed fp16 splats: sub-blocks come as the low nibbles (j even: (1024 + q)
-// sc - 1024 sc) or the high nibbles (j odd: (1024 + 16 q) sc/16 - 64 sc) of a
-// 32-byte run, both exact.  Computed once per super-block and row.
-__device__ __forceinline__ void q4k_scale(int sc, int j, h2 & m, h2 & o) {
-    const _Float16 scf = (_Float16)(float)sc;
-    const bool hi = (j & 1) != 0;
-    m = splat(hi ? scf * (_Float16)0.0625f : scf);
-    o = splat(hi ? scf * (_Float16)(-64.0f) : scf * (_Float16)(-1024.0f));
-}
+constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (128 rows x 9)
+constexpr int GU_XREG = 4;     // activation chunks per thread per super-block (64 tokens x 16)
 
-// A fragment of lane (row, half) for k-step `step` (16 values) of a Q4_K
-// super-block piece at `w`: 8 values q*sc as exact fp16, (m, o) from
-// q4k_scale for sub-block step / 2.
-__device__ __forceinline__ h8 q4k_frag(const uint8_t * w, int step, int half, h2 m, h2 o) {
-    const int off = 16 + 32 * (step >> 2) + 16 * (step & 1) + 8 * half;
-    const uint2 v = *reinterpret_cast<const uint2 *>(w + off);
-    const bool hi = (step & 2) != 0;
-    const uint32_t x0 = hi ? (v.x & 0xF0F0F0F0u) : (v.x & 0x0F0F0F0Fu);
-    const uint32_t x1 = hi ? (v.y & 0xF0F0F0F0u) : (v.y & 0x0F0F0F0Fu);
-    uint32_t a, b, c, d;
-    bytes_to_magic(x0, a, b);
-    bytes_to_magic(x1, c, d);
-    return as_h8(hbits(__builtin_elementwise_fma(as_h2(a), m, o)), hbits(__builtin_elementwise_fma(as_h2(b), m, o)),
-                 hbits(__builtin_elementwise_fma(as_h2(c), m, o)), hbits(__builtin_elementwise_fma(as_h2(d), m, o)));
-}
-
-// A fragment for IQ2_S: 8-group g8 = 2 step + half of the piece at `w`
-// (2-aligned): grid * sign * (2 ls + 1) as exact fp16.
-__device__ __forceinline__ h8 iq2s_frag(const uint8_t * w, int step, int half, const uint8_t * grid16,
-                                        const uint8_t * sign16) {
-    const int g8 = 2 * step + half;
-    const uint32_t qs = w[2 + g8], sg = w[34 + g8], qh = w[66 + (g8 >> 2)], scb = w[74 + (g8 >> 2)];
-    const uint32_t idx = qs | (((qh >> (2 * (g8 & 3))) & 3u) << 8);
-    const uint32_t ls = (g8 & 2) ? (scb >> 4) : (scb & 15u);
-    const u32x4 g = *reinterpret_cast<const u32x4 *>(grid16 + 16 * idx);
-    const u32x4 s = *reinterpret_cast<const u32x4 *>(sign16 + 16 * sg);
-    const h2 m = splat((_Float16)(float)(2 * ls + 1));
-    return as_h8(hbits(as_h2(g.x ^ s.x) * m), hbits(as_h2(g.y ^ s.y) * m), hbits(as_h2(g.z ^ s.z) * m),
-                 hbits(as_h2(g.w ^ s.w) * m));
-}
-
-// fp16 IQ2_S codebook [1024][8] and sign masks [256][8] (0x8000 per set bit)
-__device__ __forceinline__ void build_iq2s_f16_tables(uint8_t * grid16, uint8_t * sign16) {
-    const uint16_t lv[3] = {0x4800, 0x4E40, 0x5160};    // 8.0, 25.0, 43.0
-    for (int k = threadIdx.x; k < 1024; k += WG) {
-        const uint32_t c = c_iq2s_codes_pf[k];
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t l0 = (c >> (4 * i)) & 3, l1 = (c >> (4 * i + 2)) & 3;
-            const uint32_t v0 = l0 == 0 ? lv[0] : l0 == 1 ? lv[1] : lv[2];
-            const uint32_t v1 = l1 == 0 ? lv[0] : l1 == 1 ? lv[1] : lv[2];
-            w[i] = v0 | (v1 << 16);
-        }
-        *reinterpret_cast<u32x4 *>(grid16 + 16 * k) = u32x4{w[0], w[1], w[2], w[3]};
-    }
-    {
-        const uint32_t s = threadIdx.x;                  // WG == 256 sign bytes
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = (((s >> (2 * i)) & 1) ? 0x8000u : 0u) | (((s >> (2 * i + 1)) & 1) ? 0x80000000u : 0u);
-        *reinterpret_cast<u32x4 *>(sign16 + 16 * s) = u32x4{w[0], w[1], w[2], w[3]};
-    }
-}
-
-// 16-byte chunks covering [ps, ps + len) of a slab; they stay inside the
-// slab because slabs are whole 16-byte chunks
-__device__ __forceinline__ int chunk_count(uint64_t ps, int len) {
-    return (int)(((ps + len + 15) >> 4) - (ps >> 4));
-}
-
-constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (Q4_K: 128 rows x 9)
-constexpr int GU_XREG = 8;     // fp16 activation chunks per thread per super-block (64 tokens x 32)
+struct GuSmem {
+    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows: Q4_K at 144 r, IQ2_S at 96 r + offset
+    int8_t x[PF_TOK * PF_XP];             // the group's tokens' q8_K values of this super-block
+    _Float16 mb[PF_TOK * 16];             // their per-32 sums (32 hi + lo)
+    float d8[PF_TOK];                     // their q8_K scales
+    uint2 codes[1024];                    // IQ2_S grid: a level code per value
+    uint2 sgn[256];                       // IQ2_S sign byte: 4 per set bit, per value
+    u32x4 split[16];                      // Iq2sSplit
+    int poff[PF_ROWS];
+    int tok[PF_TOK], pair[PF_TOK];
+};
+// the epilogue's staging of one 16-token tile, over sm.x: [128 rows][17]
+constexpr int GU_STP = 17;
+static_assert(PF_ROWS * GU_STP * 4 <= PF_TOK * PF_XP, "epilogue staging fits the activation buffer");
 
 // Registers of the next super-block in flight while the current one computes.
 struct GuStage {
     u32x4 w[GU_WREG];
     u32x4 x[GU_XREG];
     u32x4 mb;
-    uint32_t dw;
     float d8;
 };
 
-struct GuSmem {
-    uint8_t w[PF_ROWS * PF_WROW_GU];
-    _Float16 x[PF_TOK * PF_XS];
-    _Float16 mb[PF_TOK * 16];
-    uint8_t grid[1024 * 16];
-    uint8_t sign[256 * 16];
-    float d8[PF_TOK];
-    float2 dw[PF_ROWS];
-    int tok[PF_TOK], pair[PF_TOK], poff[PF_ROWS];
-};
+// q8_0 (x86 CPU build, arch/x86/quants.c:302-360) or q8_1 (ggml-cuda
+// quantize.cu:5-50) of one 32-block held one value per lane of a half-wave;
+// q, d (and s for q8_1) stored to the pair's down activations.
+template <int AM>
+__device__ __forceinline__ void q8_store32(float v, int8_t * q, float * d, float * s, bool live) {
+    const float amax = half_max_dpp(fabsf(v));
+    int qi;
+    float dstore, sstore = 0.0f;
+    if (AM == AM_CPU) {
+        const float dd = amax / 127.f;
+        const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+        qi = (int)rintf(__fmul_rn(v, id));
+        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+        dstore = round_to_half(dd);
+    } else {
+        float sm = v;
+        for (int o = 16; o >= 1; o >>= 1) sm = __fadd_rn(sm, __shfl_xor(sm, o, 32));
+        const float dd = amax / 127.0f;
+        qi = amax == 0.0f ? 0 : (int)roundf(v / dd);
+        dstore = round_to_half(dd);
+        sstore = round_to_half(sm);
+    }
+    if (live) {
+        *q = (int8_t)qi;
+        if ((threadIdx.x & 31) == 0) {
+            *d = dstore;
+            if (AM != AM_CPU) *s = sstore;
+        }
+    }
+}
 
-// One (tile, 128-row block) of the gate_up GEMM with NTT 32-token column
-// tiles (a tile of at most 32 pairs computes, stages and stores one).
-template <int HT, int CT, int NTT>
-__device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile & tile, GuSmem & sm) {
-    uint8_t * s_w = sm.w;
-    _Float16 * s_x = sm.x;
-    _Float16 * s_mb = sm.mb;
-    uint8_t * s_grid = sm.grid;
-    uint8_t * s_sign = sm.sign;
-    float * s_d8 = sm.d8;
-    float2 * s_dw = sm.dw;
-    int * s_tok = sm.tok;
-    int * s_pair = sm.pair;
-    int * s_poff = sm.poff;
-    constexpr int NTOK = 32 * NTT;
+// One (group, row block) of the gate_up GEMM with NT 16-token tiles.  Wave w
+// owns local rows 32 w .. 32 w + 31 (waves 0, 1: gate rows; 2, 3: the up rows
+// of the same indices) as two 16-row MFMA tiles.
+template <int HT, int CT, int GSRC, int NT>
+__device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTile & tile, GuSmem & sm) {
     static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
     static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
-    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 32 == GU_XREG * WG, "staging shape");
+    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
+    constexpr int NTOK = 16 * NT;
 
     const int wtype = tile.tier == 0 ? HT : CT;
     const bool q4 = wtype == T_Q4_K;
-    const int F2 = 2 * p.n_ff, NSB = p.d_model / 256, K = p.top_k;
-    const int r0 = blockIdx.x * PF_ROWS;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, col = lane & 31;
-    const int bb = q4 ? 144 : 82;                              // bytes per super-block
-    const int nwc = q4 ? 9 : 6;                                // staged 16-byte chunks per row
-    const uint64_t rb = (uint64_t)NSB * bb;                    // bytes per row
+    const int F = p.n_ff, NSB = p.d_model / 256, K = p.top_k;
+    const int rb = blockIdx.x;                                  // gate rows 64 rb .. 64 rb + 63
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
+    const int bb = q4 ? 144 : 82;                               // bytes per super-block
+    const int nwc = q4 ? 9 : 6;                                 // staged 16-byte chunks per row
+    const uint64_t rbytes = (uint64_t)NSB * bb;
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
     if (tid < PF_TOK) {
-        const int q = p.sorted[tile.begin + min(tid, tile.n - 1)];
-        s_pair[tid] = q;
-        s_tok[tid] = q / K;
+        const int qp = p.sorted[tile.begin + min(tid, tile.n - 1)];
+        sm.pair[tid] = qp;
+        sm.tok[tid] = qp / K;
     }
-    if (!q4) build_iq2s_f16_tables(s_grid, s_sign);
+    if (!q4) {
+        const u32x4 * src = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_pf);
+        u32x4 * dst = reinterpret_cast<u32x4 *>(sm.codes);
+        for (int i = tid; i < 1024 * 8 / 16; i += WG) dst[i] = src[i];
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= ((tid >> i) & 1u) << (8 * i + 2);
+            hi |= ((tid >> (i + 4)) & 1u) << (8 * i + 2);
+        }
+        sm.sgn[tid] = make_uint2(lo, hi);                       // WG == 256 sign bytes
+        if (tid < 16) {
+            const uint32_t * t = c_iq2s_split.t[tid];
+            sm.split[tid] = u32x4{t[0], t[1], t[2], t[3]};
+        }
+    }
     __syncthreads();
 
-    // per-thread staging geometry, fixed for the whole K loop (no divisions
-    // or token lookups per super-block)
-    uint32_t wrow[GU_WREG];      // byte offset of the chunk's row in the slab (row * rb); ~0u: no row
+    // staging geometry, fixed for the K loop
+    uint32_t wrow[GU_WREG];      // byte offset of the chunk's row in the slab; ~0u: no chunk
     uint32_t wdst[GU_WREG];      // LDS offset of the chunk | chunk index << 16
 #pragma unroll
     for (int k = 0; k < GU_WREG; ++k) {
         const int i = tid + WG * k;
         const int r = i / nwc, c = i - nwc * r;
-        wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)min(r0 + r, F2 - 1) * rb) : ~0u;
+        // local row r: gate row 64 rb + r (r < 64) or up row F + 64 rb + r - 64,
+        // clamped into the slab (rows past n_ff are computed and discarded)
+        const int gi = min(64 * rb + (r & 63), F - 1);
+        const int row = r < 64 ? gi : F + gi;
+        wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)row * rbytes) : ~0u;
         wdst[k] = (uint32_t)(r * (q4 ? 144 : 96) + 16 * c) | ((uint32_t)c << 16);
     }
-    uint32_t xsrc[GU_XREG];      // element offset of the chunk's token row and column
+    uint32_t xsrc[GU_XREG];
 #pragma unroll
     for (int k = 0; k < GU_XREG; ++k) {
-        const int i = tid + WG * k, j = i >> 5, c = i & 31;
-        xsrc[k] = (uint32_t)(s_tok[j] * p.d_model + 8 * c);
+        const int i = tid + WG * k, j = i >> 4, c = i & 15;
+        xsrc[k] = (uint32_t)(sm.tok[j] * p.d_model + 16 * c);
     }
-    const int tok_s = tid < NTOK ? s_tok[tid] * NSB : 0;
-    const int tok_m = (tid >= 64 && tid < 64 + 2 * NTOK) ? (s_tok[(tid - 64) >> 1] * NSB) * 16 + 8 * ((tid - 64) & 1) : 0;
-    const uint32_t drow = tid >= WG - PF_ROWS ? (uint32_t)((uint64_t)min(r0 + tid - (WG - PF_ROWS), F2 - 1) * rb) : 0u;
+    const int tok_s = tid < NTOK ? sm.tok[tid] * NSB : 0;
+    const int tok_m = (tid >= 64 && tid < 64 + 2 * NTOK) ? sm.tok[(tid - 64) >> 1] * NSB * 16 + 8 * ((tid - 64) & 1) : 0;
 
     GuStage g;
     auto fetch = [&](int s) {
@@ -398,39 +391,39 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
             }
         }
 #pragma unroll
-        for (int k = 0; k < GU_XREG * NTT / 2; ++k)
+        for (int k = 0; k < GU_XREG * NT / PF_NTS; ++k)
             g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + xsrc[k] + 256 * s);
         if (tid < NTOK) g.d8 = p.xd[tok_s + s];
-        if (tid >= 64 && tid < 64 + 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
-        if (tid >= WG - PF_ROWS) {
-            const uint32_t ps = drow + (uint32_t)(bb * s);
-            g.dw = q4 ? *reinterpret_cast<const uint32_t *>(W + ps) : *reinterpret_cast<const uint16_t *>(W + ps);
-        }
+        if (q4 && tid >= 64 && tid < 64 + 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
     };
     auto store = [&](int s) {
 #pragma unroll
         for (int k = 0; k < GU_WREG; ++k)
-            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(s_w + (wdst[k] & 0xFFFF)) = g.w[k];
+            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(sm.w + (wdst[k] & 0xFFFF)) = g.w[k];
 #pragma unroll
-        for (int k = 0; k < GU_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i >> 5, c = i & 31;
-            *reinterpret_cast<u32x4 *>(s_x + j * PF_XS + 8 * c) = g.x[k];
+        for (int k = 0; k < GU_XREG * NT / PF_NTS; ++k) {
+            const int i = tid + WG * k, j = i >> 4, c = i & 15;
+            *reinterpret_cast<u32x4 *>(sm.x + j * PF_XP + 16 * c) = g.x[k];
         }
-        if (tid < NTOK) s_d8[tid] = g.d8;
-        if (tid >= 64 && tid < 64 + 2 * NTOK) {
+        if (tid < NTOK) sm.d8[tid] = g.d8;
+        if (q4 && tid >= 64 && tid < 64 + 2 * NTOK) {
             const int i = tid - 64;
-            *reinterpret_cast<u32x4 *>(s_mb + 16 * (i >> 1) + 8 * (i & 1)) = g.mb;
+            *reinterpret_cast<u32x4 *>(sm.mb + 16 * (i >> 1) + 8 * (i & 1)) = g.mb;
         }
-        if (tid >= WG - PF_ROWS) {
-            const int r = tid - (WG - PF_ROWS);
-            const uint32_t ps = drow + (uint32_t)(bb * s);
-            s_dw[r] = make_float2(h2f(g.dw & 0xFFFF), q4 ? h2f(g.dw >> 16) : 0.0f);
-            s_poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
+        if (tid < PF_ROWS) {
+            const int r = tid;
+            const int gi = min(64 * rb + (r & 63), F - 1);
+            const uint64_t ps = (uint64_t)(r < 64 ? gi : F + gi) * rbytes + (uint64_t)bb * s;
+            sm.poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
         }
     };
 
-    f16v y0 = {}, y1 = {};
-    const int row_l = 32 * wave + col;                          // this lane's A row in the block
+    f4 y[2][NT];
+#pragma unroll
+    for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
     fetch(0);
     for (int s = 0; s < NSB; ++s) {
         if (s) __syncthreads();                                 // the previous super-block is consumed
@@ -438,253 +431,220 @@ __device__ __forceinline__ void pf_gate_up_tile(const PfParams & p, const PfTile
         __syncthreads();
         if (s + 1 < NSB) fetch(s + 1);
 
-        f16v a0 = {}, a1 = {};
-        const uint8_t * wp = s_w + s_poff[row_l];
-        const _Float16 * xb0 = s_x + col * PF_XS + 8 * half;
-        const _Float16 * xb1 = xb0 + 32 * PF_XS;
-        const float d80 = s_d8[col], d81 = NTT == 2 ? s_d8[32 + col] : 0.0f;
-        if (q4) {
-            // 6-bit scales and mins of this row (get_scale_min_k4, ggml-quants.c:822)
-            const uint32_t q0 = *reinterpret_cast<const uint32_t *>(wp + 4);
-            const uint32_t q1 = *reinterpret_cast<const uint32_t *>(wp + 8);
-            const uint32_t q2 = *reinterpret_cast<const uint32_t *>(wp + 12);
-            int sc[8], mn[8];
+        // ---- the B operands of this wave's two 16-row tiles: 4 K-steps of 64,
+        // lane (row l16, quarter q) holds values 64 st + 16 q .. + 15
+        v4i bh[2][4], bl[2][4];
+        h8 bm[2];
+        float dr[2], mr[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sc[j] = (q0 >> (8 * j)) & 63;
-                mn[j] = (q1 >> (8 * j)) & 63;
-                sc[j + 4] = ((q2 >> (8 * j)) & 15) | (((q0 >> (8 * j + 6)) & 3) << 4);
-                mn[j + 4] = ((q2 >> (8 * j + 4)) & 15) | (((q1 >> (8 * j + 6)) & 3) << 4);
+        for (int rs = 0; rs < 2; ++rs) {
+            const uint8_t * wp = sm.w + sm.poff[32 * wave + 16 * rs + l16];
+            if (q4) {
+                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(wp);
+                dr[rs] = h2f(hdr.x & 0xFFFF);
+                mr[rs] = h2f(hdr.x >> 16);
+                // 6-bit scales and mins (get_scale_min_k4, ggml-quants.c:822)
+                int sc[8], mn[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sc[j] = (hdr.y >> (8 * j)) & 63;
+                    mn[j] = (hdr.z >> (8 * j)) & 63;
+                    sc[j + 4] = ((hdr.w >> (8 * j)) & 15) | (((hdr.y >> (8 * j + 6)) & 3) << 4);
+                    mn[j + 4] = ((hdr.w >> (8 * j + 4)) & 15) | (((hdr.z >> (8 * j + 6)) & 3) << 4);
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wp + 16 + 32 * st + 16 * (q & 1));
+                    const bool hn = (q >> 1) != 0;                   // sub-block 2 st + 1: high nibbles
+                    const uint32_t sc_q = hn ? sc[2 * st + 1] : sc[2 * st];
+                    const uint32_t sh = (sc_q >> 3) * 0x10001u, sl = (sc_q & 7) * 0x10001u;
+                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t nb = (hn ? (w4[i] >> 4) : w4[i]) & 0x0F0F0F0Fu;
+                        bh[rs][st][i] = (int)bytes_mul(nb, sh);
+                        bl[rs][st][i] = (int)bytes_mul(nb, sl);
+                    }
+                }
+                // mins B operand (16x16x32 f16): k 0..7 = 32 m_j, k 8..15 = m_j
+                const _Float16 f = q == 0 ? (_Float16)32.0f : (_Float16)1.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bm[rs][j] = q < 2 ? (_Float16)(float)mn[j] * f : (_Float16)0.0f;
+            } else {
+                const int wo = sm.poff[32 * wave + 16 * rs + l16];   // 2-aligned
+                dr[rs] = h2f(lds16(sm.w, wo));
+                mr[rs] = 0.0f;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const int g16 = 4 * st + q;                      // 16-value group: grid entries 2 g16, 2 g16 + 1
+                    const uint32_t qs2 = lds32u(sm.w, wo + 2 + 2 * g16);
+                    const uint32_t sg2 = lds32u(sm.w, wo + 34 + 2 * g16);
+                    const uint32_t qhb = (lds32u(sm.w, wo + 66 + 2 * st) >> (8 * (q >> 1))) >> (4 * (q & 1));
+                    const uint32_t ls = ((lds32u(sm.w, wo + 74 + 2 * st) >> (8 * (q >> 1))) >> (4 * (q & 1))) & 15;
+                    const uint32_t i0 = (qs2 & 0xFF) | ((qhb & 3) << 8);
+                    const uint32_t i1 = ((qs2 >> 8) & 0xFF) | (((qhb >> 2) & 3) << 8);
+                    const uint2 c0 = sm.codes[i0], c1 = sm.codes[i1];
+                    const uint2 s0 = sm.sgn[sg2 & 0xFF], s1 = sm.sgn[(sg2 >> 8) & 0xFF];
+                    const u32x4 t = sm.split[ls];
+                    const uint32_t sel[4] = {c0.x | s0.x, c0.y | s0.y, c1.x | s1.x, c1.y | s1.y};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        bh[rs][st][i] = (int)__builtin_amdgcn_perm(t.y, t.x, sel[i]);
+                        bl[rs][st][i] = (int)__builtin_amdgcn_perm(t.w, t.z, sel[i]);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bm[rs][j] = (_Float16)0.0f;
             }
-            h2 qm[8], qo[8];
+        }
+
+        // ---- every 16-token tile of the group against both row tiles
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q4k_scale(sc[j], j, qm[j], qo[j]);
+        for (int ts = 0; ts < NT; ++ts) {
+            const int8_t * xr = sm.x + (16 * ts + l16) * PF_XP + 16 * q;
+            v4i a[4];
 #pragma unroll
-            for (int step = 0; step < 16; ++step) {
-                const h8 a = q4k_frag(wp, step, half, qm[step >> 1], qo[step >> 1]);
-                a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
-                if (NTT == 2) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
-            }
-            // mins: sum_j m_j * (32 hi_j + lo_j), exact
-            const _Float16 f = half ? (_Float16)1.0f : (_Float16)32.0f;
+            for (int st = 0; st < 4; ++st) a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + 64 * st));
+            const f4 d8 = *reinterpret_cast<const f4 *>(sm.d8 + 16 * ts + 4 * q);
             h8 am;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) am[j] = (_Float16)(float)mn[j] * f;
-            f16v m0 = {}, m1 = {};
-            m0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * col + 8 * half), m0, 0, 0, 0);
-            if (NTT == 2) m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, *reinterpret_cast<const h8 *>(s_mb + 16 * (32 + col) + 8 * half), m1, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float2 dm = s_dw[32 * wave + 8 * i + 4 * half + jj];
-                    const int v = 4 * i + jj;
-                    y0[v] += __fmul_rn(d80, dm.x) * a0[v] - __fmul_rn(d80, dm.y) * m0[v];
-                    if (NTT == 2) y1[v] += __fmul_rn(d81, dm.x) * a1[v] - __fmul_rn(d81, dm.y) * m1[v];
-                }
-        } else {
-#pragma unroll
-            for (int step = 0; step < 16; ++step) {
-                const h8 a = iq2s_frag(wp, step, half, s_grid, s_sign);
-                a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb0 + 16 * step), a0, 0, 0, 0);
-                if (NTT == 2) a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, *reinterpret_cast<const h8 *>(xb1 + 16 * step), a1, 0, 0, 0);
+            if (q4) {
+                const u32x4 mv = q < 2 ? *reinterpret_cast<const u32x4 *>(sm.mb + 16 * (16 * ts + l16) + 8 * q)
+                                       : u32x4{0, 0, 0, 0};
+                __builtin_memcpy(&am, &mv, 16);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int rs = 0; rs < 2; ++rs) {
+                v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const float dw = s_dw[32 * wave + 8 * i + 4 * half + jj].x;
-                    const int v = 4 * i + jj;
-                    y0[v] += __fmul_rn(dw, d80) * a0[v];
-                    if (NTT == 2) y1[v] += __fmul_rn(dw, d81) * a1[v];
+                for (int st = 0; st < 4; ++st) {
+                    ah = mfma_i8(a[st], bh[rs][st], ah);
+                    al = mfma_i8(a[st], bl[rs][st], al);
                 }
+                if (q4) {
+                    const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float sf = (float)(8 * ah[r] + al[r]);
+                        y[rs][ts][r] += d8[r] * (dr[rs] * sf - mr[rs] * m[r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float sf = (float)(64 * ah[r] + al[r]);
+                        y[rs][ts][r] += d8[r] * (dr[rs] * sf);
+                    }
+                }
+            }
         }
     }
-    // ---- store: rows 8i + 4 half + 0..3 of this wave's 32, tokens col and 32 + col
+
+    // ---- epilogue: GEGLU of gate row i and up row i, q8_0 of each 32-block
+    // of the result into the pair's down activations
     const float f = q4 ? 1.0f : 0.125f;
+    float * stg = reinterpret_cast<float *>(sm.x);
 #pragma unroll
-    for (int tt = 0; tt < NTT; ++tt) {
-        const int j = col + 32 * tt;
-        if (j < tile.n) {
-            const f16v & y = tt ? y1 : y0;
-            float * out = p.ygu + (int64_t)s_pair[j] * F2;
+    for (int ts = 0; ts < NT; ++ts) {
+        __syncthreads();                                        // the K loop / previous tile's readers are done
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = r0 + 32 * wave + 8 * i + 4 * half;
-                if (r + 3 < F2)
-                    *reinterpret_cast<float4 *>(out + r) =
-                        make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2], f * y[4 * i + 3]);
-            }
+        for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) stg[(32 * wave + 16 * rs + l16) * GU_STP + 4 * q + r] = f * y[rs][ts][r];
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int u = 8 * pass + 2 * wave + (lane >> 5);    // (token, 32-block) unit, 0..31
+            const int tk = u >> 1, blk = u & 1, i = lane & 31;
+            const int j = 16 * ts + tk;
+            const int fi = 64 * rb + 32 * blk;                  // first gate index of the block
+            const bool live = j < tile.n && fi < F;
+            const float gv = stg[(32 * blk + i) * GU_STP + tk];
+            const float uv = stg[(64 + 32 * blk + i) * GU_STP + tk];
+            const float v = geglu1<GSRC>(gv, uv);
+            const int64_t qp = sm.pair[min(j, PF_TOK - 1)];
+            q8_store32<AM_CPU>(v, p.aq + qp * F + fi + i, p.ad + qp * (F / 32) + fi / 32, nullptr, live);
         }
     }
 }
 
-template <int HT, int CT>
+template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
     __shared__ __align__(16) GuSmem sm;
     if ((int)blockIdx.y >= *p.n_tiles) return;
     const PfTile tile = p.tiles[blockIdx.y];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
-    if (tile.n > 32) pf_gate_up_tile<HT, CT, 2>(p, tile, sm);
-    else pf_gate_up_tile<HT, CT, 1>(p, tile, sm);
-}
-
-// exact ints (as fp16 pairs) times the block scale d: hi = fp16(d * v),
-// lo = fp16(d * v - hi) (exact: d * v has at most 11 + 8 significant bits)
-__device__ __forceinline__ void scale_split(const uint32_t (&v)[4], _Float16 d, h8 & hi, h8 & lo) {
-    const h2 m = splat(d);
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const h2 x = as_h2(v[i]);
-        const h2 a = x * m;
-        h[i] = hbits(a);
-        l[i] = hbits(__builtin_elementwise_fma(x, m, -a));
-    }
-    hi = as_h8(h[0], h[1], h[2], h[3]);
-    lo = as_h8(l[0], l[1], l[2], l[3]);
-}
-
-// ----------------------------------------------------- down activations
-
-// One workgroup per routed pair: GEGLU + q8_0 (the CPU path's activation
-// format for 32-blocks, bit-identical).  Stored: d8 q times a per-pair power
-// of two 2^e (2^e puts the largest |d8 q| in [2^14, 2^15)) as the exact sum
-// of an fp16 high part and an fp16 remainder, and 2^-e.
-template <int GSRC>
-__global__ __launch_bounds__(WG) void k_pf_act(const PfParams p) {
-    __shared__ __align__(16) uint8_t scratch[6400];     // act_layout(PF_MAX_FF) = 6240 bytes
-    __shared__ float s_red[WG / 64];
-    const int q = blockIdx.x;
-    const int F = p.n_ff;
-    const int e = p.ids[q];
-    if (e < 0 || e >= p.n_expert) {
-        // an invalid id contributes zeros (its pair is in no tile)
-        for (int r = threadIdx.x; r < p.d_model; r += WG) p.ydn[(int64_t)q * p.d_model + r] = 0.0f;
-        if (threadIdx.x == 0) p.ae[q] = 0.0f;
-        return;
-    }
-    ActView L;
-    act_layout(F, 0, &L);
-    ActSrc src;
-    src.p = p.ygu + (int64_t)q * 2 * F;
-    src.n = F;
-    quantize_q8_32<GSRC, AM_CPU>(scratch, L, src, F);
-    __syncthreads();
-    const int8_t * qv = reinterpret_cast<const int8_t *>(scratch + L.q);
-    const float * d32 = reinterpret_cast<const float *>(scratch + L.d32);
-    float amax = 0.0f;
-    for (int b = threadIdx.x; b < F / 32; b += WG) amax = fmaxf(amax, d32[b] * 127.0f);
-    amax = wave_max(amax);
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    int ex = 0;
-    if (amax > 0.0f) ex = 14 - ilogbf(amax);
-    ex = max(-100, min(100, ex));
-    const float sc = ldexpf(1.0f, ex);
-    // 16 values per thread step (within one 32-block: one scale)
-    for (int i = threadIdx.x; i < F / 16; i += WG) {
-        uint32_t h[8];
-        i8x16_to_h(*reinterpret_cast<const u32x4 *>(qv + qpos(16 * i)), h);
-        const _Float16 sv = (_Float16)(d32[i >> 1] * sc);
-        h8 hi0, lo0, hi1, lo1;
-        scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h), sv, hi0, lo0);
-        scale_split(*reinterpret_cast<const uint32_t (*)[4]>(h + 4), sv, hi1, lo1);
-        h8 * dh = reinterpret_cast<h8 *>(p.ah + (int64_t)q * F + 16 * i);
-        h8 * dl = reinterpret_cast<h8 *>(p.al + (int64_t)q * F + 16 * i);
-        dh[0] = hi0;
-        dh[1] = hi1;
-        dl[0] = lo0;
-        dl[1] = lo1;
-    }
-    if (threadIdx.x == 0) p.ae[q] = ldexpf(1.0f, -ex);
+    if (64 * (int)blockIdx.x >= p.n_ff) return;
+    const int nt = (tile.n + 15) >> 4;
+    if (nt == 1) pf_gate_up_group<HT, CT, GSRC, 1>(p, tile, sm);
+    else if (nt == 2) pf_gate_up_group<HT, CT, GSRC, 2>(p, tile, sm);
+    else if (nt == 3) pf_gate_up_group<HT, CT, GSRC, 3>(p, tile, sm);
+    else pf_gate_up_group<HT, CT, GSRC, 4>(p, tile, sm);
 }
 
 // ------------------------------------------------------------------ down
 
-
-// 8 values at offset o (0, 8, 16, 24) of a Q5_0 block at `b` (2-aligned):
-// q - 16 as exact fp16, then split-scaled by d
-// (the block starts at byte `b` of the 16-aligned staging buffer `sw`; dwords
-// are read at 4-aligned addresses and funnel-shifted)
-__device__ __forceinline__ void q5_0_frag(const uint8_t * sw, int b, int o, h8 & hi, h8 & lo) {
-    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(sw + b));
-    const uint32_t qh = lds32u(sw, b + 2);
-    const int lw = o & 15;
-    const uint32_t w0 = lds32u(sw, b + 6 + lw), w1 = lds32u(sw, b + 10 + lw);
-    const bool hn = o >= 16;
-    uint32_t x0 = (hn ? (w0 >> 4) : w0) & 0x0F0F0F0Fu;
-    uint32_t x1 = (hn ? (w1 >> 4) : w1) & 0x0F0F0F0Fu;
-    const uint32_t hb = (qh >> o) & 0xFFu;
-    x0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
-    x1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
-    uint32_t m[4];
-    bytes_to_magic(x0, m[0], m[1]);
-    bytes_to_magic(x1, m[2], m[3]);
-    const h2 off = splat((_Float16)(-1040.0f));
-    uint32_t v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = hbits(as_h2(m[i]) + off);
-    scale_split(v, d, hi, lo);
-}
-
-// IQ4_NL: kvalues[q] as exact fp16, split-scaled by d
-__device__ __forceinline__ void iq4nl_frag(const uint8_t * sw, int b, int o, h8 & hi, h8 & lo) {
-    const _Float16 d = __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(sw + b));
-    const int lw = o & 15;
-    const uint32_t w0 = lds32u(sw, b + 2 + lw), w1 = lds32u(sw, b + 6 + lw);
-    const bool hn = o >= 16;
-    // signed bytes + 128 -> unsigned, then (1024 + 128 + v) - 1152
-    const uint32_t x0 = iq4nl_lookup((hn ? (w0 >> 4) : w0) & 0x0F0F0F0Fu) ^ 0x80808080u;
-    const uint32_t x1 = iq4nl_lookup((hn ? (w1 >> 4) : w1) & 0x0F0F0F0Fu) ^ 0x80808080u;
-    uint32_t m[4];
-    bytes_to_magic(x0, m[0], m[1]);
-    bytes_to_magic(x1, m[2], m[3]);
-    const h2 off = splat((_Float16)(-1152.0f));
-    uint32_t v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = hbits(as_h2(m[i]) + off);
-    scale_split(v, d, hi, lo);
-}
-
 constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
-constexpr int DN_XREG = 4;     // fp16 activation chunks per thread per down chunk and part (64 tokens x 16)
+constexpr int DN_XREG = 2;     // activation chunks per thread per down chunk (64 pairs x 8)
 
 struct DnStage {
     u32x4 w[DN_WREG];
-    u32x4 xh[DN_XREG], xl[DN_XREG];
+    u32x4 x[DN_XREG];
+    float d8;
 };
 
 struct DnSmem {
     uint8_t w[PF_ROWS * PF_WPITCH_DN + 16];    // +16: funnel reads past a row's end
-    _Float16 x[PF_TOK * PF_DXS];
-    _Float16 xl[PF_TOK * PF_DXS];
+    int8_t x[PF_TOK * PF_DXP];
+    float d8[PF_DCB][PF_TOK];
     int pair[PF_TOK], poff[PF_ROWS];
 };
 
-// One (tile, 128-row block) of the down GEMM with NTT 32-token column tiles.
-template <int HT, int CT, int NTT>
-__device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & tile, DnSmem & sm) {
-    uint8_t * s_w = sm.w;
-    _Float16 * s_x = sm.x;
-    _Float16 * s_xl = sm.xl;
-    int * s_pair = sm.pair;
-    int * s_poff = sm.poff;
+// 16 values (half h of 32-block `blk` at LDS byte offset b, 2-aligned) as
+// int8: Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q] (:2653); d_w out
+template <int T>
+__device__ __forceinline__ v4i down_frag(const uint8_t * sw, int b, int h, float & d) {
+    d = h2f(lds16(sw, b));
+    v4i o;
+    if constexpr (T == T_Q5_0) {
+        const uint32_t qh = lds32u(sw, b + 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = lds32u(sw, b + 6 + 4 * i);
+            const uint32_t nib = (h ? (w >> 4) : w) & 0x0F0F0F0Fu;
+            const uint32_t hb = (qh >> (16 * h + 4 * i)) & 15u;
+            const uint32_t spread = (hb * 0x00204081u) & 0x01010101u;           // bit k -> byte k
+            // q - 16 = nibble when the high bit is set, else nibble - 16 = nibble | 0xF0
+            const uint32_t hi = __builtin_amdgcn_perm(0u, 0xF0F0F0F0u, spread << 2);
+            o[i] = (int)(nib | hi);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = lds32u(sw, b + 2 + 4 * i);
+            o[i] = (int)iq4nl_lookup((h ? (w >> 4) : w) & 0x0F0F0F0Fu);
+        }
+    }
+    return o;
+}
+
+// One (group, 128-row block) of the down GEMM with NT 16-token tiles.
+template <int HT, int CT, int NT>
+__device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile & tile, DnSmem & sm) {
     static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
     static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
-    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 4 == DN_XREG * WG, "staging shape");
+    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 2 == DN_XREG * WG, "staging");
+    constexpr int NTOK = 16 * NT;
+    constexpr int WCH = PF_WROW_DN / 16;
+    constexpr int XK = (NT + 1) / 2;               // activation chunk rounds: 32 pair slots x 8 chunks each
 
     const int wtype = tile.tier == 0 ? HT : CT;
     const int D = p.d_model, F = p.n_ff, NB = F / 32;
     const int r0 = blockIdx.x * PF_ROWS;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, col = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     const int bs = wtype == T_Q5_0 ? 22 : 18;
-    const uint64_t rb = (uint64_t)NB * bs;
-    constexpr int WCH = PF_WROW_DN / 16;
+    const uint64_t rbytes = (uint64_t)NB * bs;
     const uint8_t * W = tile.tier == 0 ? p.hot_dn + (uint64_t)tile.idx * p.hot_dn_stride
                                        : p.cold_dn + (uint64_t)tile.idx * p.cold_dn_stride;
-    if (tid < PF_TOK) s_pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
+    if (tid < PF_TOK) sm.pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
     __syncthreads();
 
     DnStage g;
@@ -692,118 +652,131 @@ __device__ __forceinline__ void pf_down_tile(const PfParams & p, const PfTile & 
         const int cb = min(PF_DCB, NB - c0);
 #pragma unroll
         for (int k = 0; k < DN_WREG; ++k) {
-            const int i = tid + WG * k, r = i / WCH, c = i - WCH * (i / WCH);
+            const int i = tid + WG * k, r = i / WCH, c = i - WCH * r;
             g.w[k] = u32x4{0, 0, 0, 0};
             if (r < PF_ROWS) {
-                const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rb + (uint64_t)c0 * bs;
+                const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rbytes + (uint64_t)c0 * bs;
                 if (c < chunk_count(ps, cb * bs))
                     g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
             }
         }
 #pragma unroll
-        for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i / (4 * PF_DCB), c = i - (4 * PF_DCB) * j;   // 8-value chunk c
-            g.xh[k] = u32x4{0, 0, 0, 0};
-            g.xl[k] = u32x4{0, 0, 0, 0};
-            if (c < 4 * cb) {
-                const int64_t q = s_pair[j];
-                g.xh[k] = *reinterpret_cast<const u32x4 *>(p.ah + q * F + 32 * c0 + 8 * c);
-                g.xl[k] = *reinterpret_cast<const u32x4 *>(p.al + q * F + 32 * c0 + 8 * c);
-            }
+        for (int k = 0; k < XK; ++k) {
+            const int i = tid + WG * k, j = i >> 3, c = i & 7;   // 16-value chunk c of pair slot j
+            g.x[k] = u32x4{0, 0, 0, 0};
+            if (j < NTOK && c < 2 * cb)
+                g.x[k] = *reinterpret_cast<const u32x4 *>(p.aq + (int64_t)sm.pair[j] * F + 32 * c0 + 16 * c);
+        }
+        if (tid < PF_DCB * NTOK) {
+            const int j = tid % NTOK, b = tid / NTOK;
+            g.d8 = b < cb ? p.ad[(int64_t)sm.pair[j] * NB + c0 + b] : 0.0f;
         }
     };
     auto store = [&](int c0) {
 #pragma unroll
         for (int k = 0; k < DN_WREG; ++k) {
-            const int i = tid + WG * k, r = i / WCH, c = i - WCH * (i / WCH);
+            const int i = tid + WG * k, r = i / WCH, c = i - WCH * r;
             if (r < PF_ROWS) {
-                uint2 * d = reinterpret_cast<uint2 *>(s_w + r * PF_WPITCH_DN + 16 * c);   // 8-aligned
+                uint2 * d = reinterpret_cast<uint2 *>(sm.w + r * PF_WPITCH_DN + 16 * c);   // 8-aligned
                 d[0] = make_uint2(g.w[k].x, g.w[k].y);
                 d[1] = make_uint2(g.w[k].z, g.w[k].w);
                 if (c == 0) {
-                    const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rb + (uint64_t)c0 * bs;
-                    s_poff[r] = r * PF_WPITCH_DN + (int)(ps & 15);
+                    const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rbytes + (uint64_t)c0 * bs;
+                    sm.poff[r] = r * PF_WPITCH_DN + (int)(ps & 15);
                 }
             }
         }
 #pragma unroll
-        for (int k = 0; k < DN_XREG * NTT / 2; ++k) {
-            const int i = tid + WG * k, j = i / (4 * PF_DCB), c = i - (4 * PF_DCB) * j;
-            *reinterpret_cast<u32x4 *>(s_x + j * PF_DXS + 8 * c) = g.xh[k];
-            *reinterpret_cast<u32x4 *>(s_xl + j * PF_DXS + 8 * c) = g.xl[k];
+        for (int k = 0; k < XK; ++k) {
+            const int i = tid + WG * k, j = i >> 3, c = i & 7;
+            if (j < NTOK) *reinterpret_cast<u32x4 *>(sm.x + j * PF_DXP + 16 * c) = g.x[k];
+        }
+        if (tid < PF_DCB * NTOK) sm.d8[tid / NTOK][tid % NTOK] = g.d8;
+    };
+
+    f4 y[2][NT];
+#pragma unroll
+    for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto steps = [&](auto wt, int cb) {
+        constexpr int T = decltype(wt)::value;
+        for (int st = 0; 2 * st < cb; ++st) {
+            const int b0 = 2 * st, b1 = 2 * st + 1;              // 32-blocks of this K-step (b1 may be past cb)
+            const bool has1 = b1 < cb;
+            const int mb = (q >> 1) ? b1 : b0;                   // the block this lane's quarter covers
+            v4i bw[2];
+            float dw0[2], dw1[2];
+#pragma unroll
+            for (int rs = 0; rs < 2; ++rs) {
+                const int wp = sm.poff[32 * wave + 16 * rs + l16];
+                float dq;
+                bw[rs] = (mb < cb) ? down_frag<T>(sm.w, wp + bs * mb, q & 1, dq) : v4i{0, 0, 0, 0};
+                dw0[rs] = h2f(lds16(sm.w, wp + bs * b0));
+                dw1[rs] = has1 ? h2f(lds16(sm.w, wp + bs * b1)) : 0.0f;
+            }
+#pragma unroll
+            for (int ts = 0; ts < NT; ++ts) {
+                const u32x4 av = *reinterpret_cast<const u32x4 *>(sm.x + (16 * ts + l16) * PF_DXP + 64 * st + 16 * q);
+                const v4i a = as_v4i(av);
+                const v4i a0 = (q >> 1) ? v4i{0, 0, 0, 0} : a;  // K 0..31: block b0
+                const v4i a1 = (q >> 1) ? a : v4i{0, 0, 0, 0};  // K 32..63: block b1
+                const f4 d80 = *reinterpret_cast<const f4 *>(&sm.d8[b0][16 * ts + 4 * q]);
+                const f4 d81 = has1 ? *reinterpret_cast<const f4 *>(&sm.d8[b1][16 * ts + 4 * q])
+                                    : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs) {
+                    const v4i s0 = mfma_i8(a0, bw[rs], v4i{0, 0, 0, 0});
+                    const v4i s1 = has1 ? mfma_i8(a1, bw[rs], v4i{0, 0, 0, 0}) : v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        y[rs][ts][r] += (dw0[rs] * d80[r]) * (float)s0[r];
+                        y[rs][ts][r] += (dw1[rs] * d81[r]) * (float)s1[r];
+                    }
+                }
+            }
         }
     };
 
-    f16v y0 = {}, y1 = {};
-    const int row_l = 32 * wave + col;
     fetch(0);
     for (int c0 = 0; c0 < NB; c0 += PF_DCB) {
-        const int cb = min(PF_DCB, NB - c0);           // blocks in this chunk
+        const int cb = min(PF_DCB, NB - c0);
         if (c0) __syncthreads();
         store(c0);
         __syncthreads();
         if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
-        const int wp = s_poff[row_l];
-        const int xo0 = col * PF_DXS + 8 * half, xo1 = xo0 + 32 * PF_DXS;
-        // one 16-value step: weight fragment hi/lo, three MFMAs per token tile
-        auto step_fn = [&](auto wt, int step) {
-            h8 ah, al;
-            if constexpr (decltype(wt)::value == T_Q5_0) q5_0_frag(s_w, wp + 22 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
-            else iq4nl_frag(s_w, wp + 18 * (step >> 1), 16 * (step & 1) + 8 * half, ah, al);
-            const h8 b0h = *reinterpret_cast<const h8 *>(s_x + xo0 + 16 * step);
-            const h8 b0l = *reinterpret_cast<const h8 *>(s_xl + xo0 + 16 * step);
-            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0h, y0, 0, 0, 0);
-            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0l, y0, 0, 0, 0);
-            y0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0h, y0, 0, 0, 0);
-            if (NTT == 2) {
-                const h8 b1h = *reinterpret_cast<const h8 *>(s_x + xo1 + 16 * step);
-                const h8 b1l = *reinterpret_cast<const h8 *>(s_xl + xo1 + 16 * step);
-                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1h, y1, 0, 0, 0);
-                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1l, y1, 0, 0, 0);
-                y1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1h, y1, 0, 0, 0);
-            }
-        };
-        // the weight format is uniform per tile: one branch per chunk, and
-        // whole chunks run fully unrolled
-        auto chunk = [&](auto wt) {
-            if (cb == PF_DCB) {
-#pragma unroll
-                for (int step = 0; step < 2 * PF_DCB; ++step) step_fn(wt, step);
-            } else {
-                for (int step = 0; step < 2 * cb; ++step) step_fn(wt, step);
-            }
-        };
-        if (wtype == T_Q5_0) chunk(std::integral_constant<int, T_Q5_0>{});
-        else chunk(std::integral_constant<int, T_IQ4_NL>{});
+        if (wtype == T_Q5_0) steps(std::integral_constant<int, T_Q5_0>{}, cb);
+        else steps(std::integral_constant<int, T_IQ4_NL>{}, cb);
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
-    for (int tt = 0; tt < NTT; ++tt) {
-        const int j = col + 32 * tt;
-        if (j < tile.n) {
-            const int q = s_pair[j];
-            const float f = p.ae[q] * sc;
-            const f16v & y = tt ? y1 : y0;
-            float * out = p.ydn + (int64_t)q * D;
+    for (int ts = 0; ts < NT; ++ts) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = r0 + 32 * wave + 8 * i + 4 * half;
-                if (r + 3 < D)
-                    *reinterpret_cast<float4 *>(out + r) =
-                        make_float4(f * y[4 * i], f * y[4 * i + 1], f * y[4 * i + 2], f * y[4 * i + 3]);
+        for (int r = 0; r < 4; ++r) {
+            const int j = 16 * ts + 4 * q + r;
+            if (j >= tile.n) continue;
+            float * out = p.ydn + (int64_t)sm.pair[j] * D;
+#pragma unroll
+            for (int rs = 0; rs < 2; ++rs) {
+                const int row = r0 + 32 * wave + 16 * rs + l16;
+                if (row < D) out[row] = sc * y[rs][ts][r];
             }
         }
     }
 }
 
 template <int HT, int CT>
-__global__ __launch_bounds__(WG) void k_pf_down(const PfParams p) {
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_down(const PfParams p) {
     __shared__ __align__(16) DnSmem sm;
     if ((int)blockIdx.y >= *p.n_tiles) return;
     const PfTile tile = p.tiles[blockIdx.y];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
-    if (tile.n > 32) pf_down_tile<HT, CT, 2>(p, tile, sm);
-    else pf_down_tile<HT, CT, 1>(p, tile, sm);
+    const int nt = (tile.n + 15) >> 4;
+    if (nt == 1) pf_down_group<HT, CT, 1>(p, tile, sm);
+    else if (nt == 2) pf_down_group<HT, CT, 2>(p, tile, sm);
+    else if (nt == 3) pf_down_group<HT, CT, 3>(p, tile, sm);
+    else pf_down_group<HT, CT, 4>(p, tile, sm);
 }
 
 }  // namespace dev
@@ -818,6 +791,11 @@ void launch_pf(F k, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, cons
     if (e0) hipExtLaunchKernelGGL(k, grid, dim3(WG), 0u, s, e0, e1, 0u, p);
     else hipLaunchKernelGGL(k, grid, dim3(WG), 0, s, p);
 }
+template <int HT, int CT>
+void launch_gu(int gelu, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const PfParams & p) {
+    if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
+    else launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
+}
 }  // namespace
 
 hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn, int gelu, hipStream_t s,
@@ -825,26 +803,21 @@ hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn
     hipEvent_t e[4] = {};
     if (ev)
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
-    const int P = p.T * p.top_k;
     const int NSB = p.d_model / 256;
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(WG), 0, s, p);
     hipLaunchKernelGGL(k_pf_quant_x, dim3((p.T * NSB + 3) / 4), dim3(WG), 0, s, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     {
-        dim3 grid((2 * p.n_ff + PF_ROWS - 1) / PF_ROWS, p.max_tiles);
-        if (hgu == T_Q4_K && cgu == T_IQ2_S) launch_pf(k_pf_gate_up<T_Q4_K, T_IQ2_S>, grid, s, e[0], e[1], p);
-        else if (hgu == T_Q4_K && cgu == T_Q4_K) launch_pf(k_pf_gate_up<T_Q4_K, T_Q4_K>, grid, s, e[0], e[1], p);
-        else if (hgu == T_IQ2_S && cgu == T_IQ2_S) launch_pf(k_pf_gate_up<T_IQ2_S, T_IQ2_S>, grid, s, e[0], e[1], p);
-        else if (hgu == T_IQ2_S && cgu == T_Q4_K) launch_pf(k_pf_gate_up<T_IQ2_S, T_Q4_K>, grid, s, e[0], e[1], p);
+        dim3 grid((p.n_ff + 63) / 64, p.max_tiles);
+        if (hgu == T_Q4_K && cgu == T_IQ2_S) launch_gu<T_Q4_K, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);
+        else if (hgu == T_Q4_K && cgu == T_Q4_K) launch_gu<T_Q4_K, T_Q4_K>(gelu, grid, s, e[0], e[1], p);
+        else if (hgu == T_IQ2_S && cgu == T_IQ2_S) launch_gu<T_IQ2_S, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);
+        else if (hgu == T_IQ2_S && cgu == T_Q4_K) launch_gu<T_IQ2_S, T_Q4_K>(gelu, grid, s, e[0], e[1], p);
         else return hipErrorInvalidValue;
         err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    if (gelu == SRC_GEGLU_TANH) hipLaunchKernelGGL(k_pf_act<SRC_GEGLU_TANH>, dim3(P), dim3(WG), 0, s, p);
-    else hipLaunchKernelGGL(k_pf_act<SRC_GEGLU_TABLE>, dim3(P), dim3(WG), 0, s, p);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
     {
         dim3 grid((p.d_model + PF_ROWS - 1) / PF_ROWS, p.max_tiles);
         if (hdn == T_Q5_0 && cdn == T_IQ4_NL) launch_pf(k_pf_down<T_Q5_0, T_IQ4_NL>, grid, s, e[2], e[3], p);
