@@ -598,7 +598,7 @@ bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
 // prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
 // chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
 struct PfWs {
-    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, aq, ad, ydn, parts, total;
+    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, ah, al, ydn, parts, total;
     int Tc, max_tiles;
 };
 PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
@@ -616,9 +616,9 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     w.xq = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
     w.xd = w.xq + al256((uint64_t)w.Tc * D);
     w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
-    w.aq = w.xm + al256((uint64_t)w.Tc * NSB * 32);
-    w.ad = w.aq + al256(P * F);
-    w.ydn = w.ad + al256(P * (F / 32) * 4);
+    w.ah = w.xm + al256((uint64_t)w.Tc * NSB * 32);
+    w.al = w.ah + al256(P * F * 2);
+    w.ydn = w.al + al256(P * F * 2);
     w.parts = w.ydn + al256(P * D * 4);
     w.total = w.parts + al256((uint64_t)router_parts_floats(w.Tc, L->n_expert) * 4);
     return w;
@@ -781,8 +781,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.xq = (int8_t *)(base + pw.xq);
             p.xd = (float *)(base + pw.xd);
             p.xm = (_Float16 *)(base + pw.xm);
-            p.aq = (int8_t *)(base + pw.aq);
-            p.ad = (float *)(base + pw.ad);
+            p.ah = (_Float16 *)(base + pw.ah);
+            p.al = (_Float16 *)(base + pw.al);
             p.ydn = (float *)(base + pw.ydn);
             p.rc_counts = L->route_counts;
             p.rc_hits = L->route_counts ? L->route_hits : nullptr;

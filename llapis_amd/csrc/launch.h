@@ -151,8 +151,8 @@ struct PfParams {
     int8_t * xq;                         // [T][d_model] q8_K values
     float * xd;                          // [T][d_model / 256] q8_K scales
     _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
-    int8_t * aq;                         // [P][n_ff] q8_0 values of the down activations
-    float * ad;                          // [P][n_ff / 32] their scales
+    _Float16 * ah;                       // [P][n_ff] down activations d8 q: fp16 high part
+    _Float16 * al;                       // [P][n_ff]                        exact remainder
     float * ydn;                         // [P][d_model]
     int32_t * rc_counts;                 // [n_expert] routed pairs per expert, or NULL
     int32_t * rc_hits;                   // [2] hot pairs, other pairs (with rc_counts)

@@ -22,11 +22,19 @@
 //                  super-block in fp32.  The epilogue pairs gate row i with up
 //                  row n_ff + i: GEGLU and the q8_0 quantisation of the down
 //                  activations happen here, so the gate_up outputs never go to
-//                  memory.
-//   k_pf_down      grouped GEMM of the down projection: one int8 MFMA per
-//                  32-block (the K = 64 instruction with the other block's
-//                  half of the activations zeroed), the per-block scale
-//                  d_w * d8 applied to each int32 partial in fp32.
+//                  memory; each down activation d8 q is stored exactly as two
+//                  fp16 parts.
+//   k_pf_down      grouped GEMM of the down projection on fp16 MFMA
+//                  (v_mfma_f32_16x16x32_f16, K = one 32-block): the weights as
+//                  exact small integers (Q5_0 q - 16, IQ4_NL kvalues), the
+//                  activations as the exact hi + lo parts of d8 q (two MFMAs
+//                  into one fp32 accumulator), so the block's integer dot
+//                  times d8 comes out of the matrix core and one fma per
+//                  output applies the weight scale d_w.  Both operands carry a
+//                  scale per 32-block here; on int8 MFMA every output would
+//                  need a per-block fp32 rescale by d_w d8 (three VALU
+//                  operations per output and block), which made that variant
+//                  VALU-bound at several times this one's time.
 // The combine is the generic k_combine.
 #include <hip/hip_ext.h>
 
@@ -48,7 +56,7 @@ __constant__ Iq2sTables c_iq2s_tab_pf = make_iq2s_tables();
 constexpr int PF_XP = 272;                // LDS pitch of a staged token row of one super-block (256 + 16)
 constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged weight row (Q4_K 144, IQ2_S <= 96)
 constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
-constexpr int PF_DXP = PF_DCB * 32 + 16;  // LDS pitch of a staged down activation row
+constexpr int PF_DXP = PF_DCB * 32 + 8;   // LDS pitch (halfs) of a staged down activation row
 constexpr int PF_WROW_DN = 112;           // staged bytes per weight row and down chunk (<= 4 * 22 + 14)
 constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows
 constexpr int PF_NTS = PF_TOK / 16;       // 16-token MFMA tiles per group
@@ -78,6 +86,29 @@ __device__ __forceinline__ uint32_t bytes_mul(uint32_t x, uint32_t s2) {
 __device__ __forceinline__ uint32_t lds16(const uint8_t * smem, int off) {   // off even
     return *reinterpret_cast<const uint16_t *>(smem + off);
 }
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 as_h2(uint32_t u) {
+    h2 v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+}
+__device__ __forceinline__ uint32_t h2bits(h2 v) {
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    return u;
+}
+// 8 bytes at a 2-aligned LDS offset (two dwords)
+__device__ __forceinline__ uint2 lds64u(const uint8_t * smem, int off) {
+    const int a = off & ~3, sh = (off & 3) * 8;
+    const uint32_t w0 = *reinterpret_cast<const uint32_t *>(smem + a);
+    const uint32_t w1 = *reinterpret_cast<const uint32_t *>(smem + a + 4);
+    const uint32_t w2 = *reinterpret_cast<const uint32_t *>(smem + a + 8);
+    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
+}
+// four small unsigned bytes -> two packed fp16 pairs of (1024 + byte):
+// bytes {0, 1} and {2, 3}
+__device__ __forceinline__ uint32_t magic_lo(uint32_t x) { return __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u); }
+__device__ __forceinline__ uint32_t magic_hi(uint32_t x) { return __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u); }
 
 __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t) {
     return (t.tier == 0 && t.idx >= 0 && t.idx < p.k_slots) || (t.tier == 1 && t.idx >= 0 && t.idx < p.n_expert);
@@ -282,10 +313,13 @@ struct GuStage {
 };
 
 // q8_0 (x86 CPU build, arch/x86/quants.c:302-360) or q8_1 (ggml-cuda
-// quantize.cu:5-50) of one 32-block held one value per lane of a half-wave;
-// q, d (and s for q8_1) stored to the pair's down activations.
+// quantize.cu:5-50) of one 32-block held one value per lane of a half-wave,
+// stored as the value d8 q, exactly, in two fp16 parts: d8 (fp16) times q
+// (8 bits) has at most 19 significant bits and is a multiple of 2^-24, so
+// hi = fp16(d8 q) and lo = fp16(d8 q - hi) are exact and hi + lo = d8 q.
+// (q8_1 also stores its per-block sum s.)
 template <int AM>
-__device__ __forceinline__ void q8_store32(float v, int8_t * q, float * d, float * s, bool live) {
+__device__ __forceinline__ void q8_store32(float v, _Float16 * hi, _Float16 * lo, float * s, bool live) {
     const float amax = half_max_dpp(fabsf(v));
     int qi;
     float dstore, sstore = 0.0f;
@@ -303,12 +337,13 @@ __device__ __forceinline__ void q8_store32(float v, int8_t * q, float * d, float
         dstore = round_to_half(dd);
         sstore = round_to_half(sm);
     }
+    const float x = dstore * (float)qi;                 // exact
+    const _Float16 h = (_Float16)x;
+    const _Float16 l = (_Float16)(x - (float)h);       // exact
     if (live) {
-        *q = (int8_t)qi;
-        if ((threadIdx.x & 31) == 0) {
-            *d = dstore;
-            if (AM != AM_CPU) *s = sstore;
-        }
+        *hi = h;
+        *lo = l;
+        if (AM != AM_CPU && (threadIdx.x & 31) == 0) *s = sstore;
     }
 }
 
@@ -316,7 +351,7 @@ __device__ __forceinline__ void q8_store32(float v, int8_t * q, float * d, float
 // owns local rows 32 w .. 32 w + 31 (waves 0, 1: gate rows; 2, 3: the up rows
 // of the same indices) as two 16-row MFMA tiles.
 template <int HT, int CT, int GSRC, int NT>
-__device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTile & tile, GuSmem & sm) {
+__device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTile & tile, GuSmem & sm, const int rb) {
     static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
     static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
     static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
@@ -325,7 +360,7 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
     const int wtype = tile.tier == 0 ? HT : CT;
     const bool q4 = wtype == T_Q4_K;
     const int F = p.n_ff, NSB = p.d_model / 256, K = p.top_k;
-    const int rb = blockIdx.x;                                  // gate rows 64 rb .. 64 rb + 63
+    // gate rows 64 rb .. 64 rb + 63
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     const int bb = q4 ? 144 : 82;                               // bytes per super-block
     const int nwc = q4 ? 9 : 6;                                 // staged 16-byte chunks per row
@@ -423,6 +458,17 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
     for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // per-lane constants of the Q4_K expansion: the byte of this lane's
+    // sub-block scale in both 16-bit halves (sub-block 2 st + q / 2: byte
+    // q / 2 for even st, 2 + q / 2 for odd), the nibble, and the mins
+    // operand's (1024 + m) * mult + off (32 m, m or 0 by quarter)
+    const uint32_t jb_e = (uint32_t)(q >> 1), jb_o = 2u + (uint32_t)(q >> 1);
+    const uint32_t sel_even = jb_e | 0x0C00u | (jb_e << 16) | 0x0C000000u;
+    const uint32_t sel_odd = jb_o | 0x0C00u | (jb_o << 16) | 0x0C000000u;
+    const uint32_t nib_shift = 4u * (uint32_t)(q >> 1);
+    const _Float16 mm = q == 0 ? (_Float16)32.0f : q == 1 ? (_Float16)1.0f : (_Float16)0.0f;
+    const _Float16 mo = q == 0 ? (_Float16)(-32768.0f) : q == 1 ? (_Float16)(-1024.0f) : (_Float16)0.0f;
+    const h2 mn_mul = h2{mm, mm}, mn_off = h2{mo, mo};
 
     fetch(0);
     for (int s = 0; s < NSB; ++s) {
@@ -432,60 +478,73 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
         if (s + 1 < NSB) fetch(s + 1);
 
         // ---- the B operands of this wave's two 16-row tiles: 4 K-steps of 64,
-        // lane (row l16, quarter q) holds values 64 st + 16 q .. + 15
+        // lane (row l16, quarter q) holds 16 values of each step.  Q4_K: step st,
+        // quarter q = values 64 st + 16 q (sub-block 2 st + q / 2); IQ2_S: the
+        // 16-value group 4 q + st (its bytes are contiguous per lane).  The
+        // activations are read in the same order.
         v4i bh[2][4], bl[2][4];
         h8 bm[2];
         float dr[2], mr[2];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const uint8_t * wp = sm.w + sm.poff[32 * wave + 16 * rs + l16];
+            const int wo = sm.poff[32 * wave + 16 * rs + l16];
             if (q4) {
-                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(wp);
+                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(sm.w + wo);
                 dr[rs] = h2f(hdr.x & 0xFFFF);
                 mr[rs] = h2f(hdr.x >> 16);
-                // 6-bit scales and mins (get_scale_min_k4, ggml-quants.c:822)
-                int sc[8], mn[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    sc[j] = (hdr.y >> (8 * j)) & 63;
-                    mn[j] = (hdr.z >> (8 * j)) & 63;
-                    sc[j + 4] = ((hdr.w >> (8 * j)) & 15) | (((hdr.y >> (8 * j + 6)) & 3) << 4);
-                    mn[j + 4] = ((hdr.w >> (8 * j + 4)) & 15) | (((hdr.z >> (8 * j + 6)) & 3) << 4);
-                }
+                // 6-bit scales and mins, four per dword (get_scale_min_k4,
+                // ggml-quants.c:822): bytes j of sc03 / mn03 for j < 4, of
+                // sc47 / mn47 for j - 4
+                const uint32_t sc03 = hdr.y & 0x3F3F3F3Fu;
+                const uint32_t mn03 = hdr.z & 0x3F3F3F3Fu;
+                const uint32_t sc47 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+                const uint32_t mn47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+                // sc = 8 sh + sl
+                const uint32_t sh03 = (sc03 >> 3) & 0x07070707u, sl03 = sc03 & 0x07070707u;
+                const uint32_t sh47 = (sc47 >> 3) & 0x07070707u, sl47 = sc47 & 0x07070707u;
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wp + 16 + 32 * st + 16 * (q & 1));
-                    const bool hn = (q >> 1) != 0;                   // sub-block 2 st + 1: high nibbles
-                    const uint32_t sc_q = hn ? sc[2 * st + 1] : sc[2 * st];
-                    const uint32_t sh = (sc_q >> 3) * 0x10001u, sl = (sc_q & 7) * 0x10001u;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(sm.w + wo + 16 + 32 * st + 16 * (q & 1));
+                    // this lane's sub-block scale halves, each byte in both
+                    // 16-bit halves
+                    const uint32_t sel = (st & 1) ? sel_odd : sel_even;
+                    const uint32_t sh2 = __builtin_amdgcn_perm(0u, st < 2 ? sh03 : sh47, sel);
+                    const uint32_t sl2 = __builtin_amdgcn_perm(0u, st < 2 ? sl03 : sl47, sel);
                     const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const uint32_t nb = (hn ? (w4[i] >> 4) : w4[i]) & 0x0F0F0F0Fu;
-                        bh[rs][st][i] = (int)bytes_mul(nb, sh);
-                        bl[rs][st][i] = (int)bytes_mul(nb, sl);
+                        const uint32_t nb = (w4[i] >> nib_shift) & 0x0F0F0F0Fu;
+                        bh[rs][st][i] = (int)bytes_mul(nb, sh2);
+                        bl[rs][st][i] = (int)bytes_mul(nb, sl2);
                     }
                 }
-                // mins B operand (16x16x32 f16): k 0..7 = 32 m_j, k 8..15 = m_j
-                const _Float16 f = q == 0 ? (_Float16)32.0f : (_Float16)1.0f;
+                // mins B operand (16x16x32 f16): k 0..7 = 32 m_j, 8..15 = m_j,
+                // 16..31 = 0; (1024 + m) * mult + off per lane quarter
+                const uint32_t mb4[4] = {magic_lo(mn03), magic_hi(mn03), magic_lo(mn47), magic_hi(mn47)};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) bm[rs][j] = q < 2 ? (_Float16)(float)mn[j] * f : (_Float16)0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    const h2 mv = __builtin_elementwise_fma(as_h2(mb4[i]), mn_mul, mn_off);
+                    bm[rs][2 * i] = mv.x;
+                    bm[rs][2 * i + 1] = mv.y;
+                }
             } else {
-                const int wo = sm.poff[32 * wave + 16 * rs + l16];   // 2-aligned
                 dr[rs] = h2f(lds16(sm.w, wo));
                 mr[rs] = 0.0f;
+                // this lane's groups 4q .. 4q + 3: grid entries 8q .. 8q + 7
+                const uint2 qs8 = lds64u(sm.w, wo + 2 + 8 * q);
+                const uint2 sg8 = lds64u(sm.w, wo + 34 + 8 * q);
+                const uint32_t qh2 = lds16(sm.w, wo + 66 + 2 * q);          // 2 bits per entry
+                const uint32_t sc2 = lds16(sm.w, wo + 74 + 2 * q);          // 4 bits per group
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const int g16 = 4 * st + q;                      // 16-value group: grid entries 2 g16, 2 g16 + 1
-                    const uint32_t qs2 = lds32u(sm.w, wo + 2 + 2 * g16);
-                    const uint32_t sg2 = lds32u(sm.w, wo + 34 + 2 * g16);
-                    const uint32_t qhb = (lds32u(sm.w, wo + 66 + 2 * st) >> (8 * (q >> 1))) >> (4 * (q & 1));
-                    const uint32_t ls = ((lds32u(sm.w, wo + 74 + 2 * st) >> (8 * (q >> 1))) >> (4 * (q & 1))) & 15;
-                    const uint32_t i0 = (qs2 & 0xFF) | ((qhb & 3) << 8);
-                    const uint32_t i1 = ((qs2 >> 8) & 0xFF) | (((qhb >> 2) & 3) << 8);
+                    const uint32_t qsw = st < 2 ? qs8.x : qs8.y, sgw = st < 2 ? sg8.x : sg8.y;
+                    const int b0 = 16 * (st & 1);                            // bit of entry 2 st in its dword
+                    const uint32_t i0 = __builtin_amdgcn_ubfe(qsw, b0, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st, 2) << 8);
+                    const uint32_t i1 = __builtin_amdgcn_ubfe(qsw, b0 + 8, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st + 2, 2) << 8);
                     const uint2 c0 = sm.codes[i0], c1 = sm.codes[i1];
-                    const uint2 s0 = sm.sgn[sg2 & 0xFF], s1 = sm.sgn[(sg2 >> 8) & 0xFF];
-                    const u32x4 t = sm.split[ls];
+                    const uint2 s0 = sm.sgn[__builtin_amdgcn_ubfe(sgw, b0, 8)];
+                    const uint2 s1 = sm.sgn[__builtin_amdgcn_ubfe(sgw, b0 + 8, 8)];
+                    const u32x4 t = sm.split[__builtin_amdgcn_ubfe(sc2, 4 * st, 4)];
                     const uint32_t sel[4] = {c0.x | s0.x, c0.y | s0.y, c1.x | s1.x, c1.y | s1.y};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -499,12 +558,13 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
         }
 
         // ---- every 16-token tile of the group against both row tiles
+        const int xo_st = q4 ? 64 : 16, xo_q = q4 ? 16 : 64;
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) {
-            const int8_t * xr = sm.x + (16 * ts + l16) * PF_XP + 16 * q;
+            const int8_t * xr = sm.x + (16 * ts + l16) * PF_XP + xo_q * q;
             v4i a[4];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + 64 * st));
+            for (int st = 0; st < 4; ++st) a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + xo_st * st));
             const f4 d8 = *reinterpret_cast<const f4 *>(sm.d8 + 16 * ts + 4 * q);
             h8 am;
             if (q4) {
@@ -561,7 +621,7 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
             const float uv = stg[(64 + 32 * blk + i) * GU_STP + tk];
             const float v = geglu1<GSRC>(gv, uv);
             const int64_t qp = sm.pair[min(j, PF_TOK - 1)];
-            q8_store32<AM_CPU>(v, p.aq + qp * F + fi + i, p.ad + qp * (F / 32) + fi / 32, nullptr, live);
+            q8_store32<AM_CPU>(v, p.ah + qp * F + fi + i, p.al + qp * F + fi + i, nullptr, live);
         }
     }
 }
@@ -569,76 +629,90 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
 template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
     __shared__ __align__(16) GuSmem sm;
-    if ((int)blockIdx.y >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[blockIdx.y];
+    const int g = blockIdx.y, rb = blockIdx.x;
+    if (g >= *p.n_tiles) return;
+    const PfTile tile = p.tiles[g];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
-    if (64 * (int)blockIdx.x >= p.n_ff) return;
     const int nt = (tile.n + 15) >> 4;
-    if (nt == 1) pf_gate_up_group<HT, CT, GSRC, 1>(p, tile, sm);
-    else if (nt == 2) pf_gate_up_group<HT, CT, GSRC, 2>(p, tile, sm);
-    else if (nt == 3) pf_gate_up_group<HT, CT, GSRC, 3>(p, tile, sm);
-    else pf_gate_up_group<HT, CT, GSRC, 4>(p, tile, sm);
+    if (nt == 1) pf_gate_up_group<HT, CT, GSRC, 1>(p, tile, sm, rb);
+    else if (nt == 2) pf_gate_up_group<HT, CT, GSRC, 2>(p, tile, sm, rb);
+    else if (nt == 3) pf_gate_up_group<HT, CT, GSRC, 3>(p, tile, sm, rb);
+    else pf_gate_up_group<HT, CT, GSRC, 4>(p, tile, sm, rb);
 }
 
 // ------------------------------------------------------------------ down
 
 constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
-constexpr int DN_XREG = 2;     // activation chunks per thread per down chunk (64 pairs x 8)
+constexpr int DN_XREG = 8;     // activation chunks per thread per down chunk (64 pair slots x (16 hi + 16 lo))
 
 struct DnStage {
     u32x4 w[DN_WREG];
     u32x4 x[DN_XREG];
-    float d8;
 };
 
 struct DnSmem {
-    uint8_t w[PF_ROWS * PF_WPITCH_DN + 16];    // +16: funnel reads past a row's end
-    int8_t x[PF_TOK * PF_DXP];
-    float d8[PF_DCB][PF_TOK];
+    uint8_t w[PF_ROWS * PF_WPITCH_DN + 16];    // +16: reads past a row's end
+    _Float16 xh[PF_TOK * PF_DXP];              // d8 q, fp16 high part, [pair slot][128 values + pad]
+    _Float16 xl[PF_TOK * PF_DXP];              // and the exact remainder
     int pair[PF_TOK], poff[PF_ROWS];
 };
 
-// 16 values (half h of 32-block `blk` at LDS byte offset b, 2-aligned) as
-// int8: Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q] (:2653); d_w out
+// 8 values (8 u .. 8 u + 7 of 32-block `blk` at LDS byte offset b, 2-aligned)
+// as exact fp16 integers: Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q]
+// (:2653); the block scale d_w out
 template <int T>
-__device__ __forceinline__ v4i down_frag(const uint8_t * sw, int b, int h, float & d) {
+__device__ __forceinline__ h8 down_frag(const uint8_t * sw, int b, int u, float & d) {
     d = h2f(lds16(sw, b));
-    v4i o;
+    uint32_t h[4];
     if constexpr (T == T_Q5_0) {
-        const uint32_t qh = lds32u(sw, b + 2);
+        // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
+        const uint2 qs = lds64u(sw, b + 6 + 8 * (u & 1));
+        const uint32_t qh = __builtin_amdgcn_ubfe(lds32u(sw, b + 2), 8 * u, 8);
+        const int sh = 4 * (u >> 1);
+        uint32_t x[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w = lds32u(sw, b + 6 + 4 * i);
-            const uint32_t nib = (h ? (w >> 4) : w) & 0x0F0F0F0Fu;
-            const uint32_t hb = (qh >> (16 * h + 4 * i)) & 15u;
-            const uint32_t spread = (hb * 0x00204081u) & 0x01010101u;           // bit k -> byte k
-            // q - 16 = nibble when the high bit is set, else nibble - 16 = nibble | 0xF0
-            const uint32_t hi = __builtin_amdgcn_perm(0u, 0xF0F0F0F0u, spread << 2);
-            o[i] = (int)(nib | hi);
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t nib = ((i ? qs.y : qs.x) >> sh) & 0x0F0F0F0Fu;
+            const uint32_t hb = (qh >> (4 * i)) & 15u;
+            x[i] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);   // bit k -> bit 4 of byte k
         }
+        const h2 off = h2{(_Float16)(-1040.0f), (_Float16)(-1040.0f)};
+        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
+        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
+        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
+        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
     } else {
+        // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
+        const uint2 qs = lds64u(sw, b + 2 + 8 * (u & 1));
+        const int sh = 4 * (u >> 1);
+        const h2 off = h2{(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
+        uint32_t x[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w = lds32u(sw, b + 2 + 4 * i);
-            o[i] = (int)iq4nl_lookup((h ? (w >> 4) : w) & 0x0F0F0F0Fu);
-        }
+        for (int i = 0; i < 2; ++i) x[i] = iq4nl_lookup(((i ? qs.y : qs.x) >> sh) & 0x0F0F0F0Fu) ^ 0x80808080u;
+        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
+        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
+        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
+        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
     }
+    h8 o;
+    __builtin_memcpy(&o, h, 16);
     return o;
 }
 
-// One (group, 128-row block) of the down GEMM with NT 16-token tiles.
+// One (group, 128-row block) of the down GEMM with NT 16-token tiles.  Wave
+// w owns rows 32 w .. 32 w + 31 as two 16-row MFMA tiles.
 template <int HT, int CT, int NT>
-__device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile & tile, DnSmem & sm) {
+__device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile & tile, DnSmem & sm, const int rb) {
     static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
     static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
-    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * PF_DCB * 2 == DN_XREG * WG, "staging");
+    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * 32 == DN_XREG * WG, "staging");
     constexpr int NTOK = 16 * NT;
     constexpr int WCH = PF_WROW_DN / 16;
-    constexpr int XK = (NT + 1) / 2;               // activation chunk rounds: 32 pair slots x 8 chunks each
+    constexpr int XK = 2 * NT;                     // activation rounds of 8 pair slots
 
     const int wtype = tile.tier == 0 ? HT : CT;
     const int D = p.d_model, F = p.n_ff, NB = F / 32;
-    const int r0 = blockIdx.x * PF_ROWS;
+    const int r0 = rb * PF_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     const int bs = wtype == T_Q5_0 ? 22 : 18;
     const uint64_t rbytes = (uint64_t)NB * bs;
@@ -662,14 +736,14 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
         }
 #pragma unroll
         for (int k = 0; k < XK; ++k) {
-            const int i = tid + WG * k, j = i >> 3, c = i & 7;   // 16-value chunk c of pair slot j
+            // round k: pair slots 8 k .. 8 k + 7, 32 chunks of 8 values each:
+            // chunks 0..15 the high parts of the 128 values, 16..31 the low
+            const int i = tid + WG * k, j = i >> 5, c = i & 31, v8 = c & 15;
             g.x[k] = u32x4{0, 0, 0, 0};
-            if (j < NTOK && c < 2 * cb)
-                g.x[k] = *reinterpret_cast<const u32x4 *>(p.aq + (int64_t)sm.pair[j] * F + 32 * c0 + 16 * c);
-        }
-        if (tid < PF_DCB * NTOK) {
-            const int j = tid % NTOK, b = tid / NTOK;
-            g.d8 = b < cb ? p.ad[(int64_t)sm.pair[j] * NB + c0 + b] : 0.0f;
+            if (v8 < 4 * cb) {
+                const _Float16 * src = ((c >> 4) ? p.al : p.ah) + (int64_t)sm.pair[j] * F + 32 * c0 + 8 * v8;
+                g.x[k] = *reinterpret_cast<const u32x4 *>(src);
+            }
         }
     };
     auto store = [&](int c0) {
@@ -688,10 +762,10 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
         }
 #pragma unroll
         for (int k = 0; k < XK; ++k) {
-            const int i = tid + WG * k, j = i >> 3, c = i & 7;
-            if (j < NTOK) *reinterpret_cast<u32x4 *>(sm.x + j * PF_DXP + 16 * c) = g.x[k];
+            const int i = tid + WG * k, j = i >> 5, c = i & 31;
+            _Float16 * dst = ((c >> 4) ? sm.xl : sm.xh) + j * PF_DXP + 8 * (c & 15);
+            *reinterpret_cast<u32x4 *>(dst) = g.x[k];
         }
-        if (tid < PF_DCB * NTOK) sm.d8[tid / NTOK][tid % NTOK] = g.d8;
     };
 
     f4 y[2][NT];
@@ -700,40 +774,26 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto steps = [&](auto wt, int cb) {
+    auto blocks = [&](auto wt, int cb) {
         constexpr int T = decltype(wt)::value;
-        for (int st = 0; 2 * st < cb; ++st) {
-            const int b0 = 2 * st, b1 = 2 * st + 1;              // 32-blocks of this K-step (b1 may be past cb)
-            const bool has1 = b1 < cb;
-            const int mb = (q >> 1) ? b1 : b0;                   // the block this lane's quarter covers
-            v4i bw[2];
-            float dw0[2], dw1[2];
+        for (int b = 0; b < cb; ++b) {
+            // B: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block b
+            h8 bw[2];
+            float dw[2];
 #pragma unroll
-            for (int rs = 0; rs < 2; ++rs) {
-                const int wp = sm.poff[32 * wave + 16 * rs + l16];
-                float dq;
-                bw[rs] = (mb < cb) ? down_frag<T>(sm.w, wp + bs * mb, q & 1, dq) : v4i{0, 0, 0, 0};
-                dw0[rs] = h2f(lds16(sm.w, wp + bs * b0));
-                dw1[rs] = has1 ? h2f(lds16(sm.w, wp + bs * b1)) : 0.0f;
-            }
+            for (int rs = 0; rs < 2; ++rs)
+                bw[rs] = down_frag<T>(sm.w, sm.poff[32 * wave + 16 * rs + l16] + bs * b, q, dw[rs]);
 #pragma unroll
             for (int ts = 0; ts < NT; ++ts) {
-                const u32x4 av = *reinterpret_cast<const u32x4 *>(sm.x + (16 * ts + l16) * PF_DXP + 64 * st + 16 * q);
-                const v4i a = as_v4i(av);
-                const v4i a0 = (q >> 1) ? v4i{0, 0, 0, 0} : a;  // K 0..31: block b0
-                const v4i a1 = (q >> 1) ? a : v4i{0, 0, 0, 0};  // K 32..63: block b1
-                const f4 d80 = *reinterpret_cast<const f4 *>(&sm.d8[b0][16 * ts + 4 * q]);
-                const f4 d81 = has1 ? *reinterpret_cast<const f4 *>(&sm.d8[b1][16 * ts + 4 * q])
-                                    : f4{0.0f, 0.0f, 0.0f, 0.0f};
+                const int xo = (16 * ts + l16) * PF_DXP + 32 * b + 8 * q;
+                h8 ah, al;
+                __builtin_memcpy(&ah, sm.xh + xo, 16);
+                __builtin_memcpy(&al, sm.xl + xo, 16);
 #pragma unroll
                 for (int rs = 0; rs < 2; ++rs) {
-                    const v4i s0 = mfma_i8(a0, bw[rs], v4i{0, 0, 0, 0});
-                    const v4i s1 = has1 ? mfma_i8(a1, bw[rs], v4i{0, 0, 0, 0}) : v4i{0, 0, 0, 0};
+                    const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        y[rs][ts][r] += (dw0[rs] * d80[r]) * (float)s0[r];
-                        y[rs][ts][r] += (dw1[rs] * d81[r]) * (float)s1[r];
-                    }
+                    for (int r = 0; r < 4; ++r) y[rs][ts][r] += dw[rs] * sb[r];
                 }
             }
         }
@@ -746,8 +806,8 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
         store(c0);
         __syncthreads();
         if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
-        if (wtype == T_Q5_0) steps(std::integral_constant<int, T_Q5_0>{}, cb);
-        else steps(std::integral_constant<int, T_IQ4_NL>{}, cb);
+        if (wtype == T_Q5_0) blocks(std::integral_constant<int, T_Q5_0>{}, cb);
+        else blocks(std::integral_constant<int, T_IQ4_NL>{}, cb);
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
@@ -769,14 +829,15 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
 template <int HT, int CT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_down(const PfParams p) {
     __shared__ __align__(16) DnSmem sm;
-    if ((int)blockIdx.y >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[blockIdx.y];
+    const int g = blockIdx.y, rb = blockIdx.x;
+    if (g >= *p.n_tiles) return;
+    const PfTile tile = p.tiles[g];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int nt = (tile.n + 15) >> 4;
-    if (nt == 1) pf_down_group<HT, CT, 1>(p, tile, sm);
-    else if (nt == 2) pf_down_group<HT, CT, 2>(p, tile, sm);
-    else if (nt == 3) pf_down_group<HT, CT, 3>(p, tile, sm);
-    else pf_down_group<HT, CT, 4>(p, tile, sm);
+    if (nt == 1) pf_down_group<HT, CT, 1>(p, tile, sm, rb);
+    else if (nt == 2) pf_down_group<HT, CT, 2>(p, tile, sm, rb);
+    else if (nt == 3) pf_down_group<HT, CT, 3>(p, tile, sm, rb);
+    else pf_down_group<HT, CT, 4>(p, tile, sm, rb);
 }
 
 }  // namespace dev

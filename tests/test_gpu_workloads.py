@@ -120,7 +120,8 @@ def test_stack_slice_three_layers(gpu, oracle, T, act_mode, gelu_mode):
     layer against the oracle on the GPU's own input to it (ids identical,
     within the layer bars), then the oracle's own chain (numpy RMSNorm and
     add) against the GPU's final residual stream: tokens routed alike in every
-    layer within relative L2 1e-3 together, 1e-2 each (median 1e-5), and at most 1 % of the tokens routed differently (a
+    layer within relative L2 1e-3 together (3e-3 in q8_1 mode), 1e-2 each
+    (median 1e-5), and at most 1 % of the tokens routed differently (a
     top-8 boundary moved by the two chains' last-bit differences).  A token
     that re-rounded one q8 value in layer l enters layer l + 1 with a different
     input, whose own quantisation then differs in more places: the chain's
@@ -160,5 +161,7 @@ def test_stack_slice_three_layers(gpu, oracle, T, act_mode, gelu_mode):
     say(f"  chain: {int((~same).sum())} of {T} tokens routed differently; routed alike: max rel_l2 "
         f"{per[same].max():.1e}")
     assert (~same).sum() <= max(0, T // 100)
-    assert rel_l2(h_gpu[same], ho[same]) <= 1e-3
+    # q8_1 re-quantises each input in 32-blocks, so a perturbed input flips
+    # more of its own activations: its chain drifts about twice as far
+    assert rel_l2(h_gpu[same], ho[same]) <= (3e-3 if act_mode == la.ACT_Q8_1 else 1e-3)
     assert per[same].max() <= 1e-2 and np.median(per[same]) <= 1e-5
