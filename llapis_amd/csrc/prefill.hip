@@ -580,18 +580,23 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
                     ah = mfma_i8(a[st], bh[rs][st], ah);
                     al = mfma_i8(a[st], bl[rs][st], al);
                 }
+                // explicit fmas: every token column rounds alike.  A pair's
+                // column in its group depends on the bucketing order, and left
+                // to itself the compiler contracts some unrolled columns into
+                // an fma and not others.
                 if (q4) {
                     const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float sf = (float)(8 * ah[r] + al[r]);
-                        y[rs][ts][r] += d8[r] * (dr[rs] * sf - mr[rs] * m[r]);
+                        const float t = __builtin_fmaf(dr[rs], sf, -(mr[rs] * m[r]));
+                        y[rs][ts][r] = __builtin_fmaf(d8[r], t, y[rs][ts][r]);
                     }
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float sf = (float)(64 * ah[r] + al[r]);
-                        y[rs][ts][r] += d8[r] * (dr[rs] * sf);
+                        y[rs][ts][r] = __builtin_fmaf(d8[r], dr[rs] * sf, y[rs][ts][r]);
                     }
                 }
             }
@@ -793,7 +798,7 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
                 for (int rs = 0; rs < 2; ++rs) {
                     const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) y[rs][ts][r] += dw[rs] * sb[r];
+                    for (int r = 0; r < 4; ++r) y[rs][ts][r] = __builtin_fmaf(dw[rs], sb[r], y[rs][ts][r]);
                 }
             }
         }

@@ -426,6 +426,27 @@ def test_prefill_vs_oracle(gpu, oracle, T, n_hot, scales):
     check_flip_tolerant(out.cpu().numpy(), out_o)
 
 
+@pytest.mark.parametrize("T,n_hot,gelu_mode", [(200, 9, la.GELU_TABLE), (96, 5, la.GELU_TANH)])
+def test_prefill_is_independent_of_token_order(gpu, T, n_hot, gelu_mode):
+    """Each token's output is a function of that token alone: the same tokens
+    in another order give bit-identical rows.  A token's pairs land in other
+    group columns (the bucketing's order inside an expert is not fixed either),
+    so this fails if any column rounds differently from another."""
+    torch = torch_mod()
+    say(f"prefill token order T={T} hot={n_hot} gelu={gelu_mode}")
+    spec = FULL16
+    lay = _layer_case(spec, 70 + n_hot, n_hot, True)
+    dl = la.DeviceLayer(lay, gpu, gelu_mode=gelu_mode)
+    x = torch.from_numpy(tokens(700 + T, T, spec.d_model)).to(gpu)
+    perm = torch.from_numpy(np.random.default_rng(T).permutation(T)).to(gpu)
+    out, ids, w = (t.clone() for t in dl.forward(x))
+    out_p, ids_p, w_p = (t.clone() for t in dl.forward(x[perm].contiguous()))
+    torch.cuda.synchronize()
+    assert torch.equal(ids_p, ids[perm]) and torch.equal(w_p, w[perm])
+    diff = (out_p != out[perm]).any(dim=1)
+    assert not bool(diff.any()), f"tokens whose rows changed with their position: {diff.nonzero().flatten().tolist()}"
+
+
 def check_flip_tolerant(got, want):
     """Layer outputs whose gate_up values differ from the reference's in the
     last bits (another fp32 summation order) can re-quantise a down
