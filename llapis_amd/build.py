@@ -21,7 +21,7 @@ ARCH = "gfx950"
 
 HIP_SOURCES = ["mmv.hip", "decode.hip", "prefill.hip", "small_kernels.hip", "transfer.hip", "model_files.hip",
                "residency.hip", "api.hip"]
-HOST_SOURCES = ["quantize.cpp", "policy.cpp"]
+HOST_SOURCES = ["quantize.cpp", "policy.cpp", "kfit.cpp"]
 
 
 def _hipcc():

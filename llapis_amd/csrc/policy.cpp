@@ -1,20 +1,32 @@
-// policy.cpp -- the expert residency policy (moert_policy.h).  Host code,
+// policy.cpp -- the expert residency policy behind moert_policy.h.  Host code,
 // standard library only.
 //
-// State per layer: the page table (exp_slot, slot_exp, slot_state), the
-// blend-path mirrors (hotmap, resid) and four score rows (routes since the
-// last fold, the session and recent EMAs that rank survivors at resize, the
-// per-visible-token use rate the decision forecasts from).  Expert-indexed
-// rows live in flat [n_layers][n_expert] arrays; slot-indexed rows per layer
-// (their length changes with resize_k).
+// The pieces:
+//   Ema        one exponential-average step over n observation steps, with the
+//              weight of counts spread evenly over those steps;
+//   Book       one layer: its page table (slot -> expert, expert -> slot, slot
+//              states) with the blend-path mirrors derived from it (a mirror
+//              entry is set exactly while its expert's slot is READY), and the
+//              layer's score rows (routes since the last fold, session and
+//              recent EMAs ranking survivors at resize, per-visible-token use
+//              rate that the decision forecasts from);
+//   Ranking    lazy best-first extraction from a binary heap: the decision
+//              needs the head of each order only as far as its pairing goes;
+//   Decision   one refresh: every layer proposes moves (a non-resident into a
+//              free slot, or in place of a weaker resident), the moves are
+//              taken highest saving first up to the token's cap, re-checked
+//              against the page table as they go;
+//   Timeline   one sample per visible token for the windowed rates.
 //
-// The arithmetic follows moert/policy/policy.cpp step for step so that the
-// same calls leave the same page table: the float EMAs and their
-// chunk-corrected weights (policy.cpp:85-125), the forecast (:131-135), the
-// candidate lists and their orders (:262-300) and the application order of
-// the pairs (:303-315, std::sort on the net saving, as the reference).
+// Decisions equal the reference's call for call (moert/policy/policy.cpp):
+// the float EMA arithmetic (its :85-125), the forecast H min(1, rate (1 - d))
+// (:131-135), the two pairing orders -- non-residents by forecast, highest
+// first, ties by id; residents by forecast, lowest first, ties by id -- and
+// the pairing rule (:262-300), and the order the moves are taken in: the
+// whole list of moves, built layer by layer (free-slot moves, then swaps),
+// passed through std::sort on the saving (:303-315), which fixes the order of
+// equal savings as well.
 #include "../../include/moert_policy.h"
-#include "../../include/llapis_moe.h"
 
 #include <algorithm>
 #include <chrono>
@@ -22,141 +34,278 @@
 #include <cstring>
 #include <vector>
 
-struct moert_policy {
-    moert_policy_config cfg{};
-    moert_policy_callbacks cbs{};
-    int L = 0, E = 0;
-    std::vector<int32_t> cap;               // [L] active capacity of each layer
-
-    bool external = false;                  // counts arrive through add_external_counts
-    long long pending_steps = 0;            // steps the unfolded external counts cover
-    long long pending_visible = 0;          // ... of which visible decode steps
-
-    std::vector<float> routes;              // [L][E] since the last fold
-    std::vector<float> session, recent;     // [L][E] slow / fast EMA
-    std::vector<float> rate;                // [L][E] per-visible-token use rate
-
-    std::vector<int32_t> exp_slot, hotmap;  // [L][E]
-    std::vector<float> resid;               // [L][E]
-    std::vector<std::vector<int32_t>> slot_exp, slot_state;   // [L][cap]
-
-    int only_layer = -1;                    // boundary pass: the one layer decided
-    float price_override = -1.0f;           // boundary pass: its price
-    const float * ext_forecast = nullptr;   // [L][E] or NULL
-    float ext_price = 0.0f;
-    int32_t ext_cap = 0;
-
-    moert_policy_stats st{};                // occupancy is computed on read
-    static constexpr int RING = 128;        // one sample per visible token
-    struct Sample {
-        double t_ms;
-        long long hot, cold;
-    } ring[RING] = {};
-    long long n_samples = 0;
-
-    size_t at(int il, int e) const { return (size_t)il * E + e; }
-};
-
 namespace {
 
-constexpr int32_t FREE = MOERT_SLOT_FREE, FILLING = MOERT_SLOT_FILLING, READY = MOERT_SLOT_READY;
+constexpr int32_t kFree = MOERT_SLOT_FREE, kFilling = MOERT_SLOT_FILLING, kReady = MOERT_SLOT_READY;
 
-bool layer_ok(const moert_policy * p, int32_t il) { return p && il >= 0 && il < p->L; }
-
-// EMA step for counts spread uniformly over n steps (n = 1: s = d s + c):
-// s = d^n s + c (1 - d^n) / ((1 - d) n).  Returns {d^n, weight of c}.
-void chunk_coef(float d, long long n_steps, float * dn, float * w) {
-    if (n_steps > 1) {
-        const double n = (double)n_steps;
-        *dn = (float)std::pow((double)d, n);
-        *w = (float)((1.0 - *dn) / ((1.0 - (double)d) * n));
-    } else {
-        *dn = d;
-        *w = 1.0f;
+struct Ema {
+    float keep, take;     // s <- keep s + take c
+    // n <= 1: one plain step; n > 1: keep = d^n, take = (1 - d^n) / ((1 - d) n),
+    // the exact result of n single steps of c / n each
+    static Ema over(float d, long long n) {
+        if (n <= 1) return {d, 1.0f};
+        const float keep = (float)std::pow((double)d, (double)n);
+        return {keep, (float)((1.0 - keep) / ((1.0 - (double)d) * (double)n))};
     }
-}
+    float step(float s, float c) const { return keep * s + take * c; }
+};
 
-// routes -> session / recent EMAs, then clear the routes
-void fold_scores(moert_policy & g, long long n_steps) {
-    float ds, ws, dr, wr;
-    chunk_coef(g.cfg.session_decay, n_steps, &ds, &ws);
-    chunk_coef(g.cfg.recent_decay, n_steps, &dr, &wr);
-    for (size_t i = 0; i < g.routes.size(); ++i) {
-        const float c = g.routes[i];
-        g.session[i] = ds * g.session[i] + ws * c;
-        g.recent[i] = dr * g.recent[i] + wr * c;
-        g.routes[i] = 0.0f;
+struct Book {
+    int n_expert = 0;
+    int active = 0;                          // slots the decision may use
+    std::vector<int32_t> slot_of;            // [E] slot | -1
+    std::vector<int32_t> hotmap;             // [E] slot while READY, else 0
+    std::vector<float> resid;                // [E] 1 while READY, else 0
+    std::vector<int32_t> held_by;            // [slots] expert | -1
+    std::vector<int32_t> state;              // [slots] FREE / FILLING / READY
+    std::vector<float> routes, session, recent, rate;   // [E]
+
+    void init(int E, int slots) {
+        n_expert = E;
+        active = slots;
+        slot_of.assign(E, -1);
+        hotmap.assign(E, 0);
+        resid.assign(E, 0.0f);
+        routes.assign(E, 0.0f);
+        session.assign(E, 0.0f);
+        recent.assign(E, 0.0f);
+        rate.assign(E, 0.0f);
+        held_by.assign(slots, -1);
+        state.assign(slots, kFree);
     }
-}
-
-// routes -> use-rate EMA over n visible steps (before fold_scores clears them);
-// prompt-only folds (n = 0) leave the rate alone
-void fold_rate(moert_policy & g, long long n_visible) {
-    if (n_visible <= 0) return;
-    const double d = (double)g.cfg.cost_rate_decay;
-    const float dn = (float)std::pow(d, (double)n_visible);
-    const float w = n_visible > 1 ? (float)((1.0 - dn) / ((1.0 - d) * (double)n_visible)) : 1.0f;
-    for (size_t i = 0; i < g.routes.size(); ++i) g.rate[i] = dn * g.rate[i] + w * g.routes[i];
-}
-
-// expected uses over the next H visible tokens (at most one per token)
-float forecast(const moert_policy & g, int il, int e) {
-    if (g.ext_forecast && g.only_layer < 0) return g.ext_forecast[g.at(il, e)];
-    const float H = (float)g.cfg.cost_horizon;
-    return H * std::min(1.0f, g.rate[g.at(il, e)] * (1.0f - g.cfg.cost_rate_decay));
-}
-
-float blended(const moert_policy & g, int il, int e) {
-    float v = g.cfg.blend_a * g.recent[g.at(il, e)] + g.cfg.blend_b * g.session[g.at(il, e)];
-    if (g.cfg.blend_c != 0.0f && g.resid[g.at(il, e)] > 0.0f) v += g.cfg.blend_c * g.cfg.seed_prior;
-    return v;
-}
-
-void set_hot(moert_policy & g, int il, int e, int slot) {
-    g.hotmap[g.at(il, e)] = slot;
-    g.resid[g.at(il, e)] = 1.0f;
-}
-void set_cold(moert_policy & g, int il, int e) {
-    g.hotmap[g.at(il, e)] = 0;
-    g.resid[g.at(il, e)] = 0.0f;
-}
-
-void evict(moert_policy & g, int il, int slot) {
-    const int e = g.slot_exp[il][slot];
-    if (e < 0) return;
-    g.exp_slot[g.at(il, e)] = -1;
-    g.slot_exp[il][slot] = -1;
-    g.slot_state[il][slot] = FREE;
-    set_cold(g, il, e);
-    ++g.st.demotions;
-}
-
-// ask the host for the bytes; 1 -> READY now, 2 -> FILLING until complete_fill
-bool fill(moert_policy & g, int il, int e, int slot) {
-    const int32_t r = g.cbs.stream_expert ? g.cbs.stream_expert(g.cbs.user, il, e, slot) : 0;
-    if (!r) return false;
-    g.slot_exp[il][slot] = e;
-    g.exp_slot[g.at(il, e)] = slot;
-    if (r == 2) {
-        g.slot_state[il][slot] = FILLING;
-        ++g.st.fills_async;
-    } else {
-        g.slot_state[il][slot] = READY;
-        set_hot(g, il, e, slot);
+    bool valid_slot(int s) const { return s >= 0 && s < active; }
+    // the partition's predicate: resident in an active slot that is READY
+    bool serves_hot(int e) const {
+        const int s = slot_of[e];
+        return s >= 0 && s < active && state[s] == kReady;
     }
-    ++g.st.promotions;
-    return true;
-}
+    void show(int e, int s) {                // mirrors of a READY resident
+        hotmap[e] = s;
+        resid[e] = 1.0f;
+    }
+    void hide(int e) {
+        hotmap[e] = 0;
+        resid[e] = 0.0f;
+    }
+    void seat(int e, int s, int st) {
+        slot_of[e] = s;
+        held_by[s] = e;
+        state[s] = st;
+        if (st == kReady) show(e, s);
+    }
+    // empties slot s; returns its expert (-1 if it held none)
+    int vacate(int s) {
+        const int e = held_by[s];
+        if (e < 0) return -1;
+        slot_of[e] = -1;
+        held_by[s] = -1;
+        state[s] = kFree;
+        hide(e);
+        return e;
+    }
+    float blended(const moert_policy_config & c, int e) const {
+        float v = c.blend_a * recent[e] + c.blend_b * session[e];
+        if (c.blend_c != 0.0f && resid[e] > 0.0f) v += c.blend_c * c.seed_prior;
+        return v;
+    }
+};
 
-void pull_external(moert_policy * p) {
-    if (p->external && p->cbs.fetch_external) p->cbs.fetch_external(p->cbs.user);
-}
+// Best-first extraction under a strict weak order `first(a, b)` (a comes before b).
+template <typename First>
+class Ranking {
+public:
+    Ranking(std::vector<int> & items, First first) : v_(items), first_(first) {
+        std::make_heap(v_.begin(), v_.end(), [this](int a, int b) { return first_(b, a); });
+    }
+    bool empty() const { return v_.empty(); }
+    int head() const { return v_.front(); }
+    void drop() {
+        std::pop_heap(v_.begin(), v_.end(), [this](int a, int b) { return first_(b, a); });
+        v_.pop_back();
+    }
 
-double now_ms() {
+private:
+    std::vector<int> & v_;
+    First first_;
+};
+
+struct Move {
+    float gain;          // forecast uses saved beyond the price
+    int layer, expert, slot;
+    int victim;          // the resident it replaces, -1 for a free slot
+};
+
+struct Timeline {
+    static constexpr int kCap = 128;
+    struct Point {
+        double t_ms;
+        long long hot, cold;
+    } pts[kCap] = {};
+    long long n = 0;
+    void push(double t, long long hot, long long cold) { pts[n++ % kCap] = {t, hot, cold}; }
+    const Point & back(long long i) const { return pts[(n - 1 - i) % kCap]; }   // i = 0: the latest
+};
+
+double clock_ms() {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
 
 }  // namespace
+
+struct moert_policy {
+    moert_policy_config cfg{};
+    moert_policy_callbacks cbs{};
+    std::vector<Book> books;
+
+    bool external = false;             // counts arrive through add_external_counts
+    long long unfolded_steps = 0;      // steps the external counts not yet folded cover
+    long long unfolded_visible = 0;    // ... of them visible decode tokens
+
+    int boundary_layer = -1;           // a boundary pass decides this layer alone
+    float boundary_price = -1.0f;
+    const float * ext_f = nullptr;     // [L][E] host forecast, or NULL
+    float ext_price = 0.0f;
+    int32_t ext_cap = 0;
+
+    moert_policy_stats ledger{};       // occupancy is computed when read
+    Timeline timeline;
+
+    int n_layers() const { return (int)books.size(); }
+    bool has(int il) const { return il >= 0 && il < n_layers(); }
+    void pull() {
+        if (external && cbs.fetch_external) cbs.fetch_external(cbs.user);
+    }
+
+    // routes -> use rate (visible steps only), then routes -> session / recent
+    void fold(long long steps, long long visible) {
+        const Ema es = Ema::over(cfg.session_decay, steps), er = Ema::over(cfg.recent_decay, steps);
+        const Ema eu = Ema::over(cfg.cost_rate_decay, visible);
+        for (Book & b : books)
+            for (int e = 0; e < b.n_expert; ++e) {
+                const float c = b.routes[e];
+                if (visible > 0) b.rate[e] = eu.step(b.rate[e], c);
+                b.session[e] = es.step(b.session[e], c);
+                b.recent[e] = er.step(b.recent[e], c);
+                b.routes[e] = 0.0f;
+            }
+    }
+
+    // expected uses of each expert of layer il over the next H visible tokens
+    void forecast(int il, std::vector<float> & f) const {
+        const Book & b = books[il];
+        f.resize(b.n_expert);
+        if (ext_f && boundary_layer < 0) {
+            std::copy(ext_f + (size_t)il * cfg.n_expert, ext_f + (size_t)(il + 1) * cfg.n_expert, f.begin());
+            return;
+        }
+        const float H = (float)cfg.cost_horizon, per_use = 1.0f - cfg.cost_rate_decay;
+        for (int e = 0; e < b.n_expert; ++e) f[e] = H * std::min(1.0f, b.rate[e] * per_use);
+    }
+
+    void propose(int il, float price, std::vector<Move> & moves) const;
+    bool promote(int il, int e, int slot);
+    void decide(int32_t reason);
+};
+
+// Layer il's moves in pairing order: the best non-residents go to the free
+// slots (ascending) while a promotion pays its price, then replace the weakest
+// residents while the saving over the resident pays it; the first move that
+// does not pay ends each of the two runs.
+void moert_policy::propose(int il, float price, std::vector<Move> & moves) const {
+    const Book & b = books[il];
+    std::vector<float> f;
+    forecast(il, f);
+    std::vector<int> outside, free_slots, residents;
+    for (int e = 0; e < b.n_expert; ++e)
+        if (b.slot_of[e] < 0) outside.push_back(e);
+    if (outside.empty()) return;
+    for (int s = 0; s < b.active; ++s) {
+        if (b.held_by[s] < 0) free_slots.push_back(s);
+        else residents.push_back(b.held_by[s]);
+    }
+    auto stronger = [&](int a, int c) { return f[a] > f[c] || (f[a] == f[c] && a < c); };
+    auto weaker = [&](int a, int c) { return f[a] < f[c] || (f[a] == f[c] && a < c); };
+    Ranking<decltype(stronger)> in(outside, stronger);
+    for (int s : free_slots) {
+        if (in.empty()) break;
+        const int e = in.head();
+        if (f[e] <= price) break;
+        moves.push_back({f[e] - price, il, e, s, -1});
+        in.drop();
+    }
+    if (in.empty() || residents.empty()) return;
+    Ranking<decltype(weaker)> out(residents, weaker);
+    while (!in.empty() && !out.empty()) {
+        const int e = in.head(), v = out.head();
+        const float saving = f[e] - f[v];
+        if (saving <= price) break;
+        moves.push_back({saving - price, il, e, b.slot_of[v], v});
+        in.drop();
+        out.drop();
+    }
+}
+
+// ask the host for expert e's hot bytes in (il, slot): 1 READY now, 2 FILLING
+// until complete_fill, 0 refused
+bool moert_policy::promote(int il, int e, int slot) {
+    const int32_t r = cbs.stream_expert ? cbs.stream_expert(cbs.user, il, e, slot) : 0;
+    if (r == 0) return false;
+    books[il].seat(e, slot, r == 2 ? kFilling : kReady);
+    if (r == 2) ++ledger.fills_async;
+    ++ledger.promotions;
+    return true;
+}
+
+void moert_policy::decide(int32_t reason) {
+    if (external) {
+        // the one place the scores must be current: pour in the counts and
+        // fold the whole span at once
+        if (cbs.fetch_external) cbs.fetch_external(cbs.user);
+        fold(std::max<long long>(1, unfolded_steps), unfolded_visible);
+        unfolded_steps = unfolded_visible = 0;
+    }
+    const double t0 = clock_ms();
+    const bool ext = ext_f && boundary_layer < 0;
+    long long cap = (long long)1 << 40;
+    if (reason == MOERT_REFRESH_VISIBLE_INTERVAL) cap = ext && ext_cap > 0 ? ext_cap : cfg.cost_per_token;
+    const float price = boundary_price >= 0.0f ? boundary_price : (ext ? ext_price : cfg.cost_reuse);
+
+    std::vector<Move> moves;
+    for (int il = 0; il < n_layers(); ++il)
+        if (boundary_layer < 0 || il == boundary_layer) propose(il, price, moves);
+    std::sort(moves.begin(), moves.end(), [](const Move & a, const Move & b) { return a.gain > b.gain; });
+
+    std::vector<char> touched((size_t)n_layers(), 0);
+    long long promoted = 0, demoted = 0;
+    for (const Move & m : moves) {
+        if (promoted >= cap) break;
+        Book & b = books[m.layer];
+        if (b.slot_of[m.expert] >= 0) continue;                 // an earlier move seated it
+        const int in_slot = b.held_by[m.slot];
+        if (in_slot != m.victim) continue;                      // the slot changed since the proposal
+        if (m.victim >= 0) {
+            b.vacate(m.slot);
+            ++ledger.demotions;
+            ++demoted;
+        }
+        if (!promote(m.layer, m.expert, m.slot)) continue;      // refused: the slot stays free
+        touched[m.layer] = 1;
+        ++promoted;
+    }
+    if (cbs.publish_layer)
+        for (int il = 0; il < n_layers(); ++il)
+            if (touched[il]) cbs.publish_layer(cbs.user, il);
+
+    const double ms = clock_ms() - t0;
+    ++ledger.refresh_count;
+    ledger.refresh_promotions += promoted;
+    ledger.refresh_demotions += demoted;
+    ledger.refresh_pause_ms_total += ms;
+    ledger.refresh_pause_ms_max = std::max(ledger.refresh_pause_ms_max, ms);
+    ledger.last_refresh_tok = ledger.visible_tokens;
+    ledger.last_refresh_promos = promoted;
+    ledger.last_refresh_pause_ms = ms;
+}
 
 extern "C" {
 
@@ -177,34 +326,17 @@ void moert_policy_config_defaults(moert_policy_config * cfg) {
 
 moert_policy * moert_policy_create(const moert_policy_config * cfg, const moert_policy_callbacks * cbs) {
     if (!cfg || cfg->n_layers <= 0 || cfg->n_expert <= 0 || cfg->k <= 0 || cfg->k > cfg->n_expert) return nullptr;
-    std::vector<int32_t> cap((size_t)cfg->n_layers, cfg->k);
+    const int L = cfg->n_layers, E = cfg->n_expert;
     if (cfg->k_per_layer)
-        for (int il = 0; il < cfg->n_layers; ++il) {
-            if (cfg->k_per_layer[il] < 1 || cfg->k_per_layer[il] > cfg->n_expert) return nullptr;
-            cap[il] = cfg->k_per_layer[il];
-        }
+        for (int il = 0; il < L; ++il)
+            if (cfg->k_per_layer[il] < 1 || cfg->k_per_layer[il] > E) return nullptr;
     moert_policy * p = new moert_policy();
     p->cfg = *cfg;
-    p->cfg.k_per_layer = nullptr;
+    p->cfg.k_per_layer = nullptr;          // the table is copied into the books
     p->cfg.cost_per_token = std::max(1, p->cfg.cost_per_token);
     if (cbs) p->cbs = *cbs;
-    p->L = cfg->n_layers;
-    p->E = cfg->n_expert;
-    p->cap = cap;
-    const size_t n = (size_t)p->L * p->E;
-    p->routes.assign(n, 0.0f);
-    p->session.assign(n, 0.0f);
-    p->recent.assign(n, 0.0f);
-    p->rate.assign(n, 0.0f);
-    p->exp_slot.assign(n, -1);
-    p->hotmap.assign(n, 0);
-    p->resid.assign(n, 0.0f);
-    p->slot_exp.resize(p->L);
-    p->slot_state.resize(p->L);
-    for (int il = 0; il < p->L; ++il) {
-        p->slot_exp[il].assign(cap[il], -1);
-        p->slot_state[il].assign(cap[il], FREE);
-    }
+    p->books.resize(L);
+    for (int il = 0; il < L; ++il) p->books[il].init(E, cfg->k_per_layer ? cfg->k_per_layer[il] : cfg->k);
     return p;
 }
 
@@ -215,21 +347,20 @@ void moert_policy_set_external_observation(moert_policy * p, int32_t on) {
 }
 
 void moert_policy_observe(moert_policy * p, int32_t il, const int32_t * ids, int32_t n_used, int64_t n_tok) {
-    if (!layer_ok(p, il) || !ids) return;
-    moert_policy & g = *p;
-    for (int64_t i = 0; i < n_tok * (int64_t)n_used; ++i) {
+    if (!p || !p->has(il) || !ids) return;
+    Book & b = p->books[il];
+    const int64_t n = n_tok * (int64_t)n_used;
+    for (int64_t i = 0; i < n; ++i) {
         const int e = ids[i];
-        if (e < 0 || e >= g.E) continue;
-        g.routes[g.at(il, e)] += 1.0f;
-        const int s = g.exp_slot[g.at(il, e)];
-        if (s >= 0 && s < g.cap[il] && g.slot_state[il][s] == READY) ++g.st.hot_routes;
-        else ++g.st.cold_routes;
+        if (e < 0 || e >= b.n_expert) continue;
+        b.routes[e] += 1.0f;
+        ++(b.serves_hot(e) ? p->ledger.hot_routes : p->ledger.cold_routes);
     }
 }
 
 void moert_policy_set_external_forecast(moert_policy * p, const float * f, float r, int32_t cap) {
     if (!p) return;
-    p->ext_forecast = f;
+    p->ext_f = f;
     p->ext_price = r;
     p->ext_cap = cap;
 }
@@ -237,361 +368,205 @@ void moert_policy_set_external_forecast(moert_policy * p, const float * f, float
 void moert_policy_on_prompt_token(moert_policy * p, int64_t n_tokens) {
     if (!p) return;
     const long long n = std::max<int64_t>(1, n_tokens);
-    p->st.tokens += n;
-    if (p->external) p->pending_steps += n;
-    else fold_scores(*p, n_tokens);
+    p->ledger.tokens += n;
+    if (p->external) p->unfolded_steps += n;
+    else p->fold(n_tokens, 0);            // prompt routing never moves the use rate
 }
 
 void moert_policy_on_token_end(moert_policy * p) {
     if (!p) return;
-    moert_policy & g = *p;
-    ++g.st.tokens;
-    ++g.st.visible_tokens;
-    moert_policy::Sample & s = g.ring[g.n_samples % moert_policy::RING];
-    s.t_ms = now_ms();
-    s.hot = g.st.hot_routes;
-    s.cold = g.st.cold_routes;
-    ++g.n_samples;
-    if (g.external) {
-        ++g.pending_steps;
-        ++g.pending_visible;
+    ++p->ledger.tokens;
+    ++p->ledger.visible_tokens;
+    p->timeline.push(clock_ms(), p->ledger.hot_routes, p->ledger.cold_routes);
+    if (p->external) {
+        ++p->unfolded_steps;
+        ++p->unfolded_visible;
     } else {
-        fold_rate(g, 1);
-        fold_scores(g, 1);
+        p->fold(1, 1);
     }
-    moert_policy_refresh(p, MOERT_REFRESH_VISIBLE_INTERVAL);
+    p->decide(MOERT_REFRESH_VISIBLE_INTERVAL);
 }
 
 void moert_policy_refresh(moert_policy * p, int32_t reason) {
-    if (!p) return;
-    moert_policy & g = *p;
-    if (g.external) {
-        if (g.cbs.fetch_external) g.cbs.fetch_external(g.cbs.user);
-        fold_rate(g, g.pending_visible);
-        fold_scores(g, std::max<long long>(1, g.pending_steps));
-        g.pending_steps = g.pending_visible = 0;
-    }
-    const double t0 = now_ms();
-    struct Pair {
-        int il, e, slot, victim;
-        bool swap;
-        float gain;
-    };
-    std::vector<Pair> pairs;
-    const bool ext = g.ext_forecast && g.only_layer < 0;
-    const long long budget = reason == MOERT_REFRESH_VISIBLE_INTERVAL
-                                 ? (long long)(ext && g.ext_cap > 0 ? g.ext_cap : g.cfg.cost_per_token)
-                                 : (long long)1 << 40;
-    std::vector<int> outside, free_slots, held;
-    std::vector<float> fc((size_t)g.E);
-    for (int il = 0; il < g.L; ++il) {
-        if (g.only_layer >= 0 && il != g.only_layer) continue;
-        const float r = g.price_override >= 0.0f ? g.price_override : (ext ? g.ext_price : g.cfg.cost_reuse);
-        outside.clear();
-        free_slots.clear();
-        held.clear();
-        // the layer's forecasts, once (nothing changes them during the pairing)
-        bool finite = true;
-        for (int e = 0; e < g.E; ++e) {
-            fc[e] = forecast(g, il, e);
-            finite = finite && std::isfinite(fc[e]);
-        }
-        float f_max = -INFINITY, f_min = INFINITY;
-        for (int e = 0; e < g.E; ++e)
-            if (g.exp_slot[g.at(il, e)] < 0) {
-                outside.push_back(e);
-                f_max = std::max(f_max, fc[e]);
-            }
-        for (int s = 0; s < g.cap[il]; ++s) {
-            const int e = g.slot_exp[il][s];
-            if (e < 0) {
-                free_slots.push_back(s);
-            } else {
-                held.push_back(s);
-                f_min = std::min(f_min, fc[e]);
-            }
-        }
-        if (outside.empty()) continue;
-        // both pairings below stop at their first candidate unless the best
-        // non-resident beats the price (free slot) or the weakest resident by
-        // more than the price (swap): then the layer adds no pair
-        if (finite && (free_slots.empty() || f_max <= r) && (held.empty() || f_max - f_min <= r)) continue;
-        // non-residents by forecast, highest first (ties: lower id first)
-        std::stable_sort(outside.begin(), outside.end(), [&](int a, int b) { return fc[a] > fc[b]; });
-        // occupied slots by their expert's forecast, lowest first (ties: lower id)
-        std::sort(held.begin(), held.end(), [&](int a, int b) {
-            const int ea = g.slot_exp[il][a], eb = g.slot_exp[il][b];
-            const float fa = fc[ea], fb = fc[eb];
-            return fa != fb ? fa < fb : ea < eb;
-        });
-        size_t next = 0;
-        for (size_t i = 0; i < free_slots.size() && next < outside.size(); ++i, ++next) {
-            const float f_in = fc[outside[next]];
-            if (f_in <= r) break;
-            pairs.push_back({il, outside[next], free_slots[i], -1, false, f_in - r});
-        }
-        for (size_t i = 0; i < held.size() && next < outside.size(); ++i, ++next) {
-            const int victim = g.slot_exp[il][held[i]];
-            const float f_in = fc[outside[next]], f_out = fc[victim];
-            if (f_in - f_out <= r) break;
-            pairs.push_back({il, outside[next], held[i], victim, true, f_in - f_out - r});
-        }
-    }
-    std::sort(pairs.begin(), pairs.end(), [](const Pair & a, const Pair & b) { return a.gain > b.gain; });
-    std::vector<char> touched((size_t)g.L, 0);
-    long long promoted = 0, demoted = 0;
-    for (const Pair & c : pairs) {
-        if (promoted >= budget) break;
-        if (g.exp_slot[g.at(c.il, c.e)] >= 0) continue;              // became resident meanwhile
-        if (c.swap) {
-            if (g.slot_exp[c.il][c.slot] != c.victim) continue;      // the victim moved
-            evict(g, c.il, c.slot);
-            ++demoted;
-        } else if (g.slot_exp[c.il][c.slot] >= 0) {
-            continue;                                                // the slot was taken
-        }
-        if (!fill(g, c.il, c.e, c.slot)) continue;
-        touched[c.il] = 1;
-        ++promoted;
-    }
-    if (g.cbs.publish_layer)
-        for (int il = 0; il < g.L; ++il)
-            if (touched[il]) g.cbs.publish_layer(g.cbs.user, il);
-    const double ms = now_ms() - t0;
-    ++g.st.refresh_count;
-    g.st.refresh_promotions += promoted;
-    g.st.refresh_demotions += demoted;
-    g.st.refresh_pause_ms_total += ms;
-    g.st.refresh_pause_ms_max = std::max(g.st.refresh_pause_ms_max, ms);
-    g.st.last_refresh_tok = g.st.visible_tokens;
-    g.st.last_refresh_promos = promoted;
-    g.st.last_refresh_pause_ms = ms;
+    if (p) p->decide(reason);
 }
 
 int32_t moert_policy_resize_k(moert_policy * p, int32_t k_new) {
-    if (!p || k_new < 1 || k_new > p->E) return 0;
-    moert_policy & g = *p;
-    for (int il = 0; il < g.L; ++il) {
-        std::vector<int> held;
-        for (int s = 0; s < g.cap[il]; ++s)
-            if (g.slot_exp[il][s] >= 0) held.push_back(s);
-        std::sort(held.begin(), held.end(), [&](int a, int b) {
-            const int ea = g.slot_exp[il][a], eb = g.slot_exp[il][b];
-            const float sa = blended(g, il, ea), sb = blended(g, il, eb);
-            return sa != sb ? sa > sb : ea < eb;
-        });
-        const int keep = std::min((int)held.size(), (int)k_new);
-        for (size_t i = keep; i < held.size(); ++i) {
-            const int e = g.slot_exp[il][held[i]];
-            g.exp_slot[g.at(il, e)] = -1;
-            set_cold(g, il, e);
-            ++g.st.demotions;
+    if (!p || k_new < 1 || k_new > p->cfg.n_expert) return 0;
+    for (Book & b : p->books) {
+        // survivors: the residents by blended score, highest first (ties by id)
+        std::vector<int> res;
+        for (int s = 0; s < b.active; ++s)
+            if (b.held_by[s] >= 0) res.push_back(b.held_by[s]);
+        std::vector<float> score(b.n_expert, 0.0f);
+        for (int e : res) score[e] = b.blended(p->cfg, e);
+        std::sort(res.begin(), res.end(),
+                  [&](int a, int c) { return score[a] != score[c] ? score[a] > score[c] : a < c; });
+        const int keep = std::min((int)res.size(), (int)k_new);
+        for (size_t i = keep; i < res.size(); ++i) {
+            b.slot_of[res[i]] = -1;
+            b.hide(res[i]);
+            ++p->ledger.demotions;
         }
-        // survivors compact into slots 0..keep-1 in rank order and stay READY
-        // (the host re-streams each into its new slot before the next fire)
-        std::vector<int32_t> se((size_t)k_new, -1), ss((size_t)k_new, FREE);
-        for (int i = 0; i < keep; ++i) {
-            const int e = g.slot_exp[il][held[i]];
-            se[i] = e;
-            ss[i] = READY;
-            g.exp_slot[g.at(il, e)] = i;
-            set_hot(g, il, e, i);
-        }
-        g.slot_exp[il].swap(se);
-        g.slot_state[il].swap(ss);
-        g.cap[il] = k_new;
+        // the new slot arrays: survivors packed into slots 0.. in rank order,
+        // READY (the host re-streams each into its new slot before the next
+        // fire)
+        b.held_by.assign(k_new, -1);
+        b.state.assign(k_new, kFree);
+        b.active = k_new;
+        for (int i = 0; i < keep; ++i) b.seat(res[i], i, kReady);
     }
-    g.cfg.k = k_new;
+    p->cfg.k = k_new;
     return 1;
 }
 
 int32_t moert_policy_set_active_k(moert_policy * p, int32_t k) {
     if (!p || k < 1) return 0;
-    moert_policy & g = *p;
-    for (int il = 0; il < g.L; ++il) {
-        const int alloc = (int)g.slot_exp[il].size();
-        const int active = std::min((int)k, alloc);
-        for (int s = active; s < alloc; ++s) {
-            const int e = g.slot_exp[il][s];
-            if (e < 0) continue;
-            if (g.slot_state[il][s] == READY) {
-                set_cold(g, il, e);
-                ++g.st.demotions;
-            }
-            g.exp_slot[g.at(il, e)] = -1;
-            g.slot_exp[il][s] = -1;
-            g.slot_state[il][s] = FREE;
+    for (Book & b : p->books) {
+        const int slots = (int)b.held_by.size();
+        const int keep = std::min((int)k, slots);
+        for (int s = keep; s < slots; ++s) {
+            const bool was_ready = b.state[s] == kReady;
+            if (b.vacate(s) >= 0 && was_ready) ++p->ledger.demotions;   // an unfinished fill is no demotion
         }
-        g.cap[il] = active;
+        b.active = keep;
     }
     return 1;
 }
 
+// a completion or an abort matches only the slot's FILLING resident
+static bool filling_match(moert_policy * p, int32_t il, int32_t slot, int32_t e) {
+    const Book & b = p->books[il];
+    if (b.held_by[slot] == e && b.state[slot] == kFilling) return true;
+    ++p->ledger.fills_stale;
+    return false;
+}
+
 int32_t moert_policy_complete_fill(moert_policy * p, int32_t il, int32_t slot, int32_t e) {
-    if (!layer_ok(p, il) || slot < 0 || slot >= p->cap[il]) return 0;
-    moert_policy & g = *p;
-    if (g.slot_exp[il][slot] != e || g.slot_state[il][slot] != FILLING) {
-        ++g.st.fills_stale;
-        return 0;
-    }
-    g.slot_state[il][slot] = READY;
-    set_hot(g, il, e, slot);
-    ++g.st.fills_completed;
+    if (!p || !p->has(il) || !p->books[il].valid_slot(slot) || !filling_match(p, il, slot, e)) return 0;
+    Book & b = p->books[il];
+    b.state[slot] = kReady;
+    b.show(e, slot);
+    ++p->ledger.fills_completed;
     return 1;
 }
 
 int32_t moert_policy_abort_fill(moert_policy * p, int32_t il, int32_t slot, int32_t e) {
-    if (!layer_ok(p, il) || slot < 0 || slot >= p->cap[il]) return 0;
-    moert_policy & g = *p;
-    if (g.slot_exp[il][slot] != e || g.slot_state[il][slot] != FILLING) {
-        ++g.st.fills_stale;
-        return 0;
-    }
-    g.exp_slot[g.at(il, e)] = -1;
-    g.slot_exp[il][slot] = -1;
-    g.slot_state[il][slot] = FREE;
-    ++g.st.fills_aborted;
+    if (!p || !p->has(il) || !p->books[il].valid_slot(slot) || !filling_match(p, il, slot, e)) return 0;
+    p->books[il].vacate(slot);
+    ++p->ledger.fills_aborted;
     return 1;
 }
 
 int32_t moert_policy_boundary_layer(moert_policy * p, int32_t il, const int32_t * counts, int64_t n_tok, float weight,
                                     float r) {
-    if (!layer_ok(p, il) || !counts || n_tok <= 0) return -1;
-    moert_policy & g = *p;
+    if (!p || !p->has(il) || !counts || n_tok <= 0) return -1;
+    Book & b = p->books[il];
     const float w = std::min(1.0f, std::max(0.0f, weight));
-    const float d = g.cfg.cost_rate_decay;
-    for (int e = 0; e < g.E; ++e) {
-        // the prompt's routes per token become the rate's steady state: rate (1 - d) = q
-        const float q = std::min(1.0f, (float)counts[e] / (float)n_tok);
-        float & rt = g.rate[g.at(il, e)];
-        rt = (1.0f - w) * rt + w * q / (1.0f - d);
+    const float d = p->cfg.cost_rate_decay;
+    // the prompt's routes per token move the rate toward the steady state
+    // whose per-token use rate (1 - d) equals them
+    for (int e = 0; e < b.n_expert; ++e) {
+        const float per_tok = std::min(1.0f, (float)counts[e] / (float)n_tok);
+        b.rate[e] = (1.0f - w) * b.rate[e] + w * per_tok / (1.0f - d);
     }
-    g.only_layer = il;
-    g.price_override = std::max(0.0f, r);
-    const long long before = g.st.refresh_promotions;
-    moert_policy_refresh(p, MOERT_REFRESH_BOUNDARY);
-    g.only_layer = -1;
-    g.price_override = -1.0f;
-    return (int32_t)(g.st.refresh_promotions - before);
+    const long long before = p->ledger.refresh_promotions;
+    p->boundary_layer = il;
+    p->boundary_price = std::max(0.0f, r);
+    p->decide(MOERT_REFRESH_BOUNDARY);
+    p->boundary_layer = -1;
+    p->boundary_price = -1.0f;
+    return (int32_t)(p->ledger.refresh_promotions - before);
 }
 
 int32_t moert_policy_can_seed(const moert_policy * p, int32_t il, int32_t e) {
-    if (!layer_ok(p, il)) return 0;
-    return e >= 0 && e < p->E && p->exp_slot[p->at(il, e)] < 0 ? 1 : 0;
+    if (!p || !p->has(il)) return 0;
+    const Book & b = p->books[il];
+    return e >= 0 && e < b.n_expert && b.slot_of[e] < 0 ? 1 : 0;
 }
 
 int32_t moert_policy_commit_seed(moert_policy * p, int32_t il, int32_t e, int32_t slot) {
-    if (!moert_policy_can_seed(p, il, e) || slot < 0 || slot >= p->cap[il]) return 0;
-    moert_policy & g = *p;
-    g.slot_exp[il][slot] = e;
-    g.exp_slot[g.at(il, e)] = slot;
-    g.slot_state[il][slot] = READY;
-    set_hot(g, il, e, slot);
-    g.session[g.at(il, e)] = g.recent[g.at(il, e)] = g.cfg.seed_prior;
+    if (!moert_policy_can_seed(p, il, e) || !p->books[il].valid_slot(slot)) return 0;
+    Book & b = p->books[il];
+    b.seat(e, slot, kReady);
+    b.session[e] = b.recent[e] = p->cfg.seed_prior;
     return 1;
 }
 
 void moert_policy_add_external_counts(moert_policy * p, int32_t il, const int32_t * counts, int64_t hot,
                                       int64_t cold) {
-    if (!layer_ok(p, il) || !counts) return;
-    moert_policy & g = *p;
-    for (int e = 0; e < g.E; ++e) g.routes[g.at(il, e)] += (float)counts[e];
-    g.st.hot_routes += hot;
-    g.st.cold_routes += cold;
+    if (!p || !p->has(il) || !counts) return;
+    Book & b = p->books[il];
+    for (int e = 0; e < b.n_expert; ++e) b.routes[e] += (float)counts[e];
+    p->ledger.hot_routes += hot;
+    p->ledger.cold_routes += cold;
 }
 
 void moert_policy_reset_stats(moert_policy * p) {
     if (!p) return;
-    p->st = moert_policy_stats{};   // residency and scores are kept
-    p->n_samples = 0;
+    p->ledger = moert_policy_stats{};      // the page table and the scores stay
+    p->timeline.n = 0;
 }
 
-int32_t moert_policy_layer_k(const moert_policy * p, int32_t il) { return layer_ok(p, il) ? p->cap[il] : -1; }
+int32_t moert_policy_layer_k(const moert_policy * p, int32_t il) {
+    return p && p->has(il) ? p->books[il].active : -1;
+}
 
 double moert_policy_hit_rate(moert_policy * p) {
     if (!p) return 0.0;
-    pull_external(p);
-    const long long tot = p->st.hot_routes + p->st.cold_routes;
-    return tot > 0 ? (double)p->st.hot_routes / (double)tot : 0.0;
+    p->pull();
+    const long long all = p->ledger.hot_routes + p->ledger.cold_routes;
+    return all > 0 ? (double)p->ledger.hot_routes / (double)all : 0.0;
 }
 
 void moert_policy_get_stats(moert_policy * p, moert_policy_stats * out) {
     if (!p || !out) return;
-    pull_external(p);
-    *out = p->st;
-    out->occupancy = 0.0;
+    p->pull();
+    *out = p->ledger;
     long long ready = 0, slots = 0;
-    for (int il = 0; il < p->L; ++il) {
-        slots += p->cap[il];
-        for (int s = 0; s < p->cap[il]; ++s) ready += p->slot_state[il][s] == READY;
+    for (const Book & b : p->books) {
+        slots += b.active;
+        ready += std::count(b.state.begin(), b.state.begin() + b.active, kReady);
     }
-    if (slots > 0) out->occupancy = (double)ready / (double)slots;
+    out->occupancy = slots > 0 ? (double)ready / (double)slots : 0.0;
 }
 
 void moert_policy_get_window(moert_policy * p, int32_t n_tokens, moert_policy_window * out) {
     if (!out) return;
     memset(out, 0, sizeof(*out));
     if (!p || n_tokens < 2) return;
-    pull_external(p);
-    const long long n = std::min<long long>(n_tokens, std::min<long long>(p->n_samples, moert_policy::RING));
+    p->pull();
+    const Timeline & tl = p->timeline;
+    const long long n = std::min<long long>(n_tokens, std::min<long long>(tl.n, Timeline::kCap));
     if (n < 2) return;
-    const moert_policy::Sample & a = p->ring[(p->n_samples - n) % moert_policy::RING];
-    const moert_policy::Sample & b = p->ring[(p->n_samples - 1) % moert_policy::RING];
+    const Timeline::Point & first = tl.back(n - 1), & last = tl.back(0);
     out->tokens = (int32_t)n;
-    out->span_ms = b.t_ms - a.t_ms;
+    out->span_ms = last.t_ms - first.t_ms;
     if (out->span_ms > 0.0) {
         out->tok_per_s = 1000.0 * (double)(n - 1) / out->span_ms;
         out->ms_per_tok = out->span_ms / (double)(n - 1);
     }
-    // routes from the window's first sample to now
-    out->hot_routes = p->st.hot_routes - a.hot;
-    out->cold_routes = p->st.cold_routes - a.cold;
-    const long long tot = out->hot_routes + out->cold_routes;
-    if (tot > 0) out->hit_rate = (double)out->hot_routes / (double)tot;
+    // the routes since the window's first sample, up to now
+    out->hot_routes = p->ledger.hot_routes - first.hot;
+    out->cold_routes = p->ledger.cold_routes - first.cold;
+    const long long all = out->hot_routes + out->cold_routes;
+    if (all > 0) out->hit_rate = (double)out->hot_routes / (double)all;
 }
 
 const int32_t * moert_policy_exp_slot_view(const moert_policy * p, int32_t il) {
-    return layer_ok(p, il) ? p->exp_slot.data() + p->at(il, 0) : nullptr;
+    return p && p->has(il) ? p->books[il].slot_of.data() : nullptr;
 }
 const int32_t * moert_policy_slot_exp_view(const moert_policy * p, int32_t il) {
-    return layer_ok(p, il) ? p->slot_exp[il].data() : nullptr;
+    return p && p->has(il) ? p->books[il].held_by.data() : nullptr;
 }
 const int32_t * moert_policy_slot_state_view(const moert_policy * p, int32_t il) {
-    return layer_ok(p, il) ? p->slot_state[il].data() : nullptr;
+    return p && p->has(il) ? p->books[il].state.data() : nullptr;
 }
 const int32_t * moert_policy_hotmap_view(const moert_policy * p, int32_t il) {
-    return layer_ok(p, il) ? p->hotmap.data() + p->at(il, 0) : nullptr;
+    return p && p->has(il) ? p->books[il].hotmap.data() : nullptr;
 }
 const float * moert_policy_resid_view(const moert_policy * p, int32_t il) {
-    return layer_ok(p, il) ? p->resid.data() + p->at(il, 0) : nullptr;
-}
-
-// K re-fit (kfit_policy.hpp:61-94): the slot count the device can hold now.
-void llapis_kfit(const llapis_kfit_inputs * in, llapis_kfit_decision * out) {
-    if (!in || !out) return;
-    llapis_kfit_decision d = {};
-    // one pool for both regimes (a resident slab's bytes are inside free),
-    // bounded by the per-process budget when there is one
-    d.pool_mib = in->slab_mib_now + in->free_mib;
-    if (in->headroom_mib >= 0 && in->slab_mib_now + in->headroom_mib < d.pool_mib) {
-        d.pool_mib = in->slab_mib_now + in->headroom_mib;
-        d.wddm_bound = 1;
-    }
-    const long long per_k = in->per_k_mib > 0 ? in->per_k_mib : 1;
-    const long long affordable = d.pool_mib / per_k;      // physics, before the preference
-    long long k = (d.pool_mib - in->keep_free_mib) / per_k;
-    k = std::max<long long>(k, in->k_min);
-    k = std::min<long long>(k, in->n_expert);
-    if (k > affordable) {
-        k = std::max<long long>(affordable, 1);
-        d.floor_capped = 1;
-    }
-    d.k = (int32_t)k;
-    // hysteresis: a one-slot change is not worth a rebuild, unless the
-    // rebuild is the restore of an evicted slab
-    d.rebuild = in->evicted || d.k <= in->k_cur - 2 || d.k >= in->k_cur + 2;
-    if (!d.rebuild) d.k = in->k_cur;
-    *out = d;
+    return p && p->has(il) ? p->books[il].resid.data() : nullptr;
 }
 
 }  // extern "C"
