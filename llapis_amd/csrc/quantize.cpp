@@ -1,15 +1,19 @@
 // quantize.cpp -- host-side expert-pool preparation: the weight quantisers of
 // the four formats on the path, and the seeded synthetic-data generator.
 //
-// The quantisers follow ggml's algorithms operation for operation, so a pool
-// prepared here is byte-identical to one written by ggml_quantize_chunk
-// (third_party/llama/ggml/src/ggml.c:7761-7800):
-//   Q4_K   quantize_row_q4_K_ref + make_qkx2_quants   (ggml-quants.c:741-820, 1399-1469)
-//   Q5_0   quantize_row_q5_0_ref                      (ggml-quants.c:149-190)
-//   IQ4_NL quantize_iq4_nl / quantize_row_iq4_nl_impl (ggml-quants.c:4894-5026)
-//   IQ2_S  quantize_iq2_s + iq2xs_init_impl           (ggml-quants.c:2781-3196, 5070-5249)
-// This file is built with -ffp-contract=off: every float expression rounds in
-// the order written, as ggml-base's own (no -march) build does.
+// A pool prepared here is byte-identical to one written by the reference's
+// ggml_quantize_chunk (third_party/llama/ggml/src/ggml.c:7761-7800), whose
+// quantisers are (ggml-quants.c):
+//   Q4_K   quantize_row_q4_K_ref, make_qkx2_quants          (:741-820, :1399-1469)
+//   Q5_0   quantize_row_q5_0_ref                            (:149-190)
+//   IQ4_NL quantize_iq4_nl, quantize_row_iq4_nl_impl        (:4894-5026)
+//   IQ2_S  quantize_iq2_s, quantize_row_iq2_s_impl          (:5070-5249)
+// Byte equality fixes each algorithm's float operations and their order:
+// every weight, sum, candidate scale and comparison below is formed with the
+// same operands in the same association as there (this file is built with
+// -ffp-contract=off, like ggml-base's own build).  Rounding to the nearest
+// integer, halves to even, is lrintf (exact for the magnitudes that occur,
+// all far below 2^22).
 #include "formats.h"
 
 #include <algorithm>
@@ -17,481 +21,443 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
-#include <mutex>
 #include <thread>
 #include <vector>
 
 namespace llapis {
 namespace {
 
-// round to nearest, ties to even, for |x| <= 2^22 (ggml-quants.c:563-568)
-inline int nearest_int(float fval) {
-    float val = fval + 12582912.f;
-    int i;
-    memcpy(&i, &val, sizeof(int));
-    return (i & 0x007fffff) - 0x00400000;
+inline int rne(float v) { return (int)lrintf(v); }
+inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// ----------------------------------------------------------------- Q4_K
+//
+// A super-block is 8 sub-blocks of 32.  Each sub-block gets an affine fit
+// x ~ s q + m (q in 0..15, m <= 0) by weighted least squares over candidate
+// level assignments; the 8 scales and 8 offsets are then stored as 6-bit
+// multiples of two fp16 super-block steps, and the levels re-derived from the
+// stored (rounded) scales.
+
+constexpr int kQ4Top = 15;
+
+struct SubBlockFit {
+    float scale = 0.0f;      // s
+    float neg_min = 0.0f;    // -m
+};
+
+// The weighted squared error of (s, m) with levels q.
+inline float affine_error(const float * x, const float * w, const uint8_t * q, float s, float m) {
+    float e = 0;
+    for (int i = 0; i < 32; ++i) {
+        float r = s * q[i] + m - x[i];
+        r = r * r;
+        e += w[i] * r;
+    }
+    return e;
 }
 
-// ---------------------------------------------------------------- Q4_K
+// levels of x at inverse step inv from origin lo
+inline void affine_levels(const float * x, float inv, float lo, uint8_t * q) {
+    for (int i = 0; i < 32; ++i) q[i] = (uint8_t)clampi(rne(inv * (x[i] - lo)), 0, kQ4Top);
+}
 
-float make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
-                       uint8_t * Laux, float rmin, float rdelta, int nstep) {
-    float min = x[0], max = x[0];
-    float sum_w = weights[0];
-    float sum_x = sum_w * x[0];
-    for (int i = 1; i < n; ++i) {
-        if (x[i] < min) min = x[i];
-        if (x[i] > max) max = x[i];
-        const float w = weights[i];
-        sum_w += w;
-        sum_x += w * x[i];
+// The fit of one sub-block: the range's own step first, then 21 steps around
+// it (inverse steps (15 - 1 + 0.1 t) / range, t = 0..20), each with the least-
+// squares (s, m) of its levels; the lowest error wins.  The range of a trial
+// runs from the offset of the best fit so far (the block's minimum until a
+// trial wins), and its levels are counted from that offset.
+SubBlockFit fit_sub_block(const float * x, const float * w, uint8_t * q) {
+    float lo = x[0], hi = x[0], sw = 0, swx = 0;
+    for (int i = 0; i < 32; ++i) {
+        lo = std::min(lo, x[i]);
+        hi = std::max(hi, x[i]);
+        sw += w[i];
+        swx += w[i] * x[i];
     }
-    if (min > 0) min = 0;
-    if (max == min) {
-        for (int i = 0; i < n; ++i) L[i] = 0;
-        *the_min = -min;
-        return 0.f;
+    lo = std::min(lo, 0.0f);
+    SubBlockFit fit;
+    if (hi == lo) {
+        std::fill(q, q + 32, 0);
+        fit.neg_min = -lo;
+        return fit;
     }
-    float iscale = nmax / (max - min);
-    float scale = 1 / iscale;
-    float best_error = 0;
-    for (int i = 0; i < n; ++i) {
-        const int l = nearest_int(iscale * (x[i] - min));
-        L[i] = (uint8_t)std::max(0, std::min(nmax, l));
-        float diff = scale * L[i] + min - x[i];
-        diff = diff * diff;
-        best_error += weights[i] * diff;
-    }
-    for (int is = 0; is <= nstep; ++is) {
-        iscale = (rmin + rdelta * is + nmax) / (max - min);
-        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
-        for (int i = 0; i < n; ++i) {
-            int l = nearest_int(iscale * (x[i] - min));
-            l = std::max(0, std::min(nmax, l));
-            Laux[i] = (uint8_t)l;
-            const float w = weights[i];
-            sum_l += w * l;
-            sum_l2 += w * l * l;
-            sum_xl += w * l * x[i];
+    float inv = kQ4Top / (hi - lo);
+    float s = 1 / inv, m = lo;
+    affine_levels(x, inv, lo, q);
+    float err = affine_error(x, w, q, s, m);
+    uint8_t trial[32];
+    for (int t = 0; t <= 20; ++t) {
+        inv = (-1.f + 0.1f * t + kQ4Top) / (hi - m);
+        affine_levels(x, inv, m, trial);
+        float sl = 0, sll = 0, sxl = 0;
+        for (int i = 0; i < 32; ++i) {
+            const int l = trial[i];
+            sl += w[i] * l;
+            sll += w[i] * l * l;
+            sxl += w[i] * l * x[i];
         }
-        const float D = sum_w * sum_l2 - sum_l * sum_l;
-        if (D > 0) {
-            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
-            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
-            if (this_min > 0) {
-                this_min = 0;
-                this_scale = sum_xl / sum_l2;
-            }
-            float cur_error = 0;
-            for (int i = 0; i < n; ++i) {
-                float diff = this_scale * Laux[i] + this_min - x[i];
-                diff = diff * diff;
-                cur_error += weights[i] * diff;
-            }
-            if (cur_error < best_error) {
-                for (int i = 0; i < n; ++i) L[i] = Laux[i];
-                best_error = cur_error;
-                scale = this_scale;
-                min = this_min;
-            }
+        const float det = sw * sll - sl * sl;
+        if (!(det > 0)) continue;
+        float ts = (sw * sxl - swx * sl) / det;
+        float tm = (sll * swx - sl * sxl) / det;
+        if (tm > 0) {
+            tm = 0;
+            ts = sxl / sll;
+        }
+        const float te = affine_error(x, w, trial, ts, tm);
+        if (te < err) {
+            std::copy(trial, trial + 32, q);
+            err = te;
+            s = ts;
+            m = tm;
         }
     }
-    *the_min = -min;
-    return scale;
+    fit.scale = s;
+    fit.neg_min = -m;
+    return fit;
 }
 
-inline void q4k_scale_min(int j, const uint8_t * q, uint8_t * d, uint8_t * m) {
-    if (j < 4) {
-        *d = q[j] & 63;
-        *m = q[j + 4] & 63;
-    } else {
-        *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-        *m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
-    }
-}
+// 6-bit code of v on a step of 1 / inv: the integer cast to a byte, then at most 63
+inline uint8_t six_bit(float inv, float v) { return std::min<uint8_t>(63, (uint8_t)rne(inv * v)); }
 
-void quantize_block_q4_K(const float * x, blk_q4_K * y) {
-    uint8_t L[QK_K], Laux[32];
-    float weights[32], mins[8], scales[8];
-    float max_scale = 0, max_min = 0;
+void q4k_super_block(const float * x, blk_q4_K * out) {
+    uint8_t lv[QK_K];
+    SubBlockFit fits[8];
+    float top_scale = 0, top_min = 0;
     for (int j = 0; j < 8; ++j) {
-        float sum_x2 = 0;
-        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
-        const float av_x = sqrtf(sum_x2 / 32);
-        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-        scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
-        if (scales[j] > max_scale) max_scale = scales[j];
-        if (mins[j] > max_min) max_min = mins[j];
+        const float * xs = x + 32 * j;
+        float energy = 0;
+        for (int i = 0; i < 32; ++i) energy += xs[i] * xs[i];
+        const float rms = sqrtf(energy / 32);
+        float w[32];
+        for (int i = 0; i < 32; ++i) w[i] = rms + fabsf(xs[i]);
+        fits[j] = fit_sub_block(xs, w, lv + 32 * j);
+        if (fits[j].scale > top_scale) top_scale = fits[j].scale;
+        if (fits[j].neg_min > top_min) top_min = fits[j].neg_min;
     }
-    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
-    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-    memset(y->scales, 0, 12);
+    const float inv_s = top_scale > 0 ? 63.f / top_scale : 0.f;
+    const float inv_m = top_min > 0 ? 63.f / top_min : 0.f;
+    uint8_t sc[8], mn[8];
     for (int j = 0; j < 8; ++j) {
-        uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
-        uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
-        ls = std::min<uint8_t>(63, ls);
-        lm = std::min<uint8_t>(63, lm);
-        if (j < 4) {
-            y->scales[j] = ls;
-            y->scales[j + 4] = lm;
-        } else {
-            y->scales[j + 4] = (ls & 0xF) | ((lm & 0xF) << 4);
-            y->scales[j - 4] |= ((ls >> 4) << 6);
-            y->scales[j - 0] |= ((lm >> 4) << 6);
-        }
+        sc[j] = six_bit(inv_s, fits[j].scale);
+        mn[j] = six_bit(inv_m, fits[j].neg_min);
     }
-    y->d = float_to_half(max_scale / 63.f);
-    y->dmin = float_to_half(max_min / 63.f);
+    // the 12-byte scale field: sub-blocks 0..3 in the low 6 bits of bytes
+    // 0..3 (scales) and 4..7 (mins); sub-blocks 4..7 as nibbles of bytes 8..11
+    // with their top two bits in the high bits of bytes 0..7
+    for (int j = 0; j < 4; ++j) {
+        out->scales[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        out->scales[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+        out->scales[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+    }
+    out->d = float_to_half(top_scale / 63.f);
+    out->dmin = float_to_half(top_min / 63.f);
+    // levels against the stored steps (a sub-block whose step rounds to zero
+    // keeps its fitted levels)
+    const float dd = half_to_float(out->d), dm = half_to_float(out->dmin);
     for (int j = 0; j < 8; ++j) {
-        uint8_t sc, m;
-        q4k_scale_min(j, y->scales, &sc, &m);
-        const float d = half_to_float(y->d) * sc;
-        if (!d) continue;
-        const float dm = half_to_float(y->dmin) * m;
-        for (int ii = 0; ii < 32; ++ii) {
-            int l = nearest_int((x[32 * j + ii] + dm) / d);
-            L[32 * j + ii] = (uint8_t)std::max(0, std::min(15, l));
+        const float step = dd * sc[j];
+        if (!step) continue;
+        const float off = dm * mn[j];
+        for (int i = 0; i < 32; ++i) lv[32 * j + i] = (uint8_t)clampi(rne((x[32 * j + i] + off) / step), 0, kQ4Top);
+    }
+    // 64 values per 32 bytes: value i in the low nibble, value i + 32 in the high
+    for (int c = 0; c < 4; ++c)
+        for (int i = 0; i < 32; ++i) out->qs[32 * c + i] = (uint8_t)(lv[64 * c + i] | (lv[64 * c + 32 + i] << 4));
+}
+
+// ----------------------------------------------------------------- Q5_0
+//
+// Symmetric 5-bit levels around 16 on the step of the signed extreme / -16.
+
+void q50_block(const float * x, blk_q5_0 * out) {
+    float peak = 0.0f, extreme = 0.0f;          // the first value of largest magnitude
+    for (int i = 0; i < 32; ++i)
+        if (fabsf(x[i]) > peak) {
+            peak = fabsf(x[i]);
+            extreme = x[i];
         }
+    const float step = extreme / -16;
+    const float inv = step ? 1.0f / step : 0.0f;
+    out->d = float_to_half(step);
+    uint32_t high = 0;
+    for (int i = 0; i < 16; ++i) {
+        // truncation of a value in [0.5, 32.5], at most 31
+        const int a = std::min(31, (int)(x[i] * inv + 16.5f));
+        const int b = std::min(31, (int)(x[16 + i] * inv + 16.5f));
+        out->qs[i] = (uint8_t)((a & 0xF) | ((b & 0xF) << 4));
+        high |= (uint32_t)(a >> 4) << i;
+        high |= (uint32_t)(b >> 4) << (16 + i);
     }
-    uint8_t * q = y->qs;
-    for (int j = 0; j < QK_K; j += 64) {
-        for (int l = 0; l < 32; ++l) q[l] = L[j + l] | (L[j + l + 32] << 4);
-        q += 32;
-    }
+    memcpy(out->qh, &high, 4);
 }
 
-// ---------------------------------------------------------------- Q5_0
+// ----------------------------------------------------------------- IQ4_NL
+//
+// Each 32-value block: 16 fixed non-linear levels times one fp16 step, the
+// step chosen among the least-squares steps of 16 level assignments.
 
-void quantize_block_q5_0(const float * x, blk_q5_0 * y) {
-    float amax = 0.0f, max = 0.0f;
-    for (int j = 0; j < 32; j++) {
-        const float v = x[j];
-        if (amax < fabsf(v)) {
-            amax = fabsf(v);
-            max = v;
-        }
-    }
-    const float d = max / -16;
-    const float id = d ? 1.0f / d : 0.0f;
-    y->d = float_to_half(d);
-    uint32_t qh = 0;
-    for (int j = 0; j < 16; ++j) {
-        const float x0 = x[0 + j] * id;
-        const float x1 = x[16 + j] * id;
-        const uint8_t xi0 = std::min<uint8_t>(31, (uint8_t)(int8_t)(x0 + 16.5f));
-        const uint8_t xi1 = std::min<uint8_t>(31, (uint8_t)(int8_t)(x1 + 16.5f));
-        y->qs[j] = (xi0 & 0x0F) | ((xi1 & 0x0F) << 4);
-        qh |= ((xi0 & 0x10u) >> 4) << (j + 0);
-        qh |= ((xi1 & 0x10u) >> 4) << (j + 16);
-    }
-    memcpy(y->qh, &qh, 4);
+const int8_t kNlLevels[16] = LLAPIS_IQ4NL_VALUES;
+
+// the level nearest to v (ties to the upper one)
+inline int nl_nearest(float v) {
+    if (v <= kNlLevels[0]) return 0;
+    if (v >= kNlLevels[15]) return 15;
+    int up = 1;
+    while (kNlLevels[up] <= v) ++up;
+    return v - kNlLevels[up - 1] < kNlLevels[up] - v ? up - 1 : up;
 }
 
-// ---------------------------------------------------------------- IQ4_NL
+struct SymSums {
+    float qx = 0, qq = 0;   // sum w q x, sum w q q
+};
 
-const int8_t kIq4nl[16] = LLAPIS_IQ4NL_VALUES;
-
-inline int best_index_int8(int n, const int8_t * val, float x) {
-    if (x <= val[0]) return 0;
-    if (x >= val[n - 1]) return n - 1;
-    int ml = 0, mu = n - 1;
-    while (mu - ml > 1) {
-        const int mav = (ml + mu) / 2;
-        if (x < val[mav]) mu = mav; else ml = mav;
+// levels of x at inverse step inv (into lv when given) and their sums
+inline SymSums nl_assign(const float * x, const float * w, float inv, uint8_t * lv) {
+    SymSums s;
+    for (int i = 0; i < 32; ++i) {
+        const int l = nl_nearest(inv * x[i]);
+        if (lv) lv[i] = (uint8_t)l;
+        const float q = kNlLevels[l];
+        s.qx += w[i] * q * x[i];
+        s.qq += w[i] * q * q;
     }
-    return x - val[mu - 1] < val[mu] - x ? mu - 1 : mu;
+    return s;
 }
 
-// one 32-value block (super-block size == block size == 32, ntry = 7)
-void quantize_block_iq4_nl(const float * x, blk_iq4_nl * y, const float * qw) {
-    const int ntry = 7;
-    uint8_t L[32];
-    float weight[32];
-    float sigma2 = 0;
-    for (int j = 0; j < 32; ++j) sigma2 += x[j] * x[j];
-    sigma2 *= 2.f / 32;
-    memset(y->qs, 0, 16);
-    y->d = float_to_half(0.f);
-    float scale0;
-    if (qw) {
-        for (int j = 0; j < 32; ++j) weight[j] = qw[j] * sqrtf(sigma2 + x[j] * x[j]);
+void iq4nl_block(const float * x, blk_iq4_nl * out, const float * imat) {
+    float w[32];
+    if (imat) {
+        float energy = 0;
+        for (int i = 0; i < 32; ++i) energy += x[i] * x[i];
+        energy *= 2.f / 32;
+        for (int i = 0; i < 32; ++i) w[i] = imat[i] * sqrtf(energy + x[i] * x[i]);
     } else {
-        for (int j = 0; j < 32; ++j) weight[j] = x[j] * x[j];
+        for (int i = 0; i < 32; ++i) w[i] = x[i] * x[i];
     }
-    float amax = 0, max = 0;
-    for (int j = 0; j < 32; ++j) {
-        const float ax = fabsf(x[j]);
-        if (ax > amax) {
-            amax = ax;
-            max = x[j];
+    float peak = 0, extreme = 0;
+    for (int i = 0; i < 32; ++i)
+        if (fabsf(x[i]) > peak) {
+            peak = fabsf(x[i]);
+            extreme = x[i];
         }
-    }
-    if (amax < 1e-15f) {
-        scale0 = 0;
-    } else {
-        float d = ntry > 0 ? -max / kIq4nl[0] : max / kIq4nl[0];
-        float id = 1 / d;
-        float sumqx = 0, sumq2 = 0;
-        for (int j = 0; j < 32; ++j) {
-            const float al = id * x[j];
-            const int l = best_index_int8(16, kIq4nl, al);
-            L[j] = (uint8_t)l;
-            const float q = kIq4nl[l];
-            const float w = weight[j];
-            sumqx += w * q * x[j];
-            sumq2 += w * q * q;
-        }
-        d = sumq2 > 0 ? sumqx / sumq2 : 0.f;
-        float best = d * sumqx;
-        for (int itry = -ntry; itry <= ntry; ++itry) {
-            id = (itry + kIq4nl[0]) / max;
-            sumqx = sumq2 = 0;
-            for (int j = 0; j < 32; ++j) {
-                const float al = id * x[j];
-                const int l = best_index_int8(16, kIq4nl, al);
-                const float q = kIq4nl[l];
-                const float w = weight[j];
-                sumqx += w * q * x[j];
-                sumq2 += w * q * q;
-            }
-            if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
-                d = sumqx / sumq2;
-                best = d * sumqx;
+    float step = 0;
+    if (peak >= 1e-15f) {
+        // the extreme on the lowest level, then 15 inverse steps around it
+        const SymSums s0 = nl_assign(x, w, 1 / (-extreme / kNlLevels[0]), nullptr);
+        step = s0.qq > 0 ? s0.qx / s0.qq : 0.f;
+        float gain = step * s0.qx;
+        for (int t = -7; t <= 7; ++t) {
+            const SymSums s = nl_assign(x, w, (t + kNlLevels[0]) / extreme, nullptr);
+            if (s.qq > 0 && s.qx * s.qx > gain * s.qq) {
+                step = s.qx / s.qq;
+                gain = step * s.qx;
             }
         }
-        scale0 = d;
     }
-    y->d = float_to_half(scale0);
-    const float id = scale0 ? 1 / scale0 : 0;
-    for (int j = 0; j < 32; ++j) L[j] = (uint8_t)best_index_int8(16, kIq4nl, id * x[j]);
-    for (int j = 0; j < 16; ++j) y->qs[j] = L[j] | (L[16 + j] << 4);
+    out->d = float_to_half(step);
+    const float inv = step ? 1 / step : 0;
+    uint8_t lv[32];
+    for (int i = 0; i < 32; ++i) lv[i] = (uint8_t)nl_nearest(inv * x[i]);
+    for (int i = 0; i < 16; ++i) out->qs[i] = (uint8_t)(lv[i] | (lv[16 + i] << 4));
 }
 
-// ---------------------------------------------------------------- IQ2_S
+// ----------------------------------------------------------------- IQ2_S
+//
+// A super-block is 16 blocks of 16 values; each block is two groups of 8,
+// each group one of 1024 codebook points of {1, 3, 5}^8 (magnitudes) with a
+// sign byte, and the block a 4-bit step multiple.
 
 const uint16_t kIq2sCodes[1024] = {
 #include "iq2s_grid.inc"
 };
 
-// The quantiser's view of the codebook: per grid point the 8 levels as bytes
-// 2l+1, the map from a 16-bit level code to its grid index (or -1), and for
-// every level code off the grid the grid points at minimum squared distance,
-// in ascending index order (ggml-quants.c:3036-3186 with nwant = 1).
-struct Iq2sTables {
-    int8_t grid[1024][8];
-    std::vector<int> map;                       // 43692 entries
-    std::vector<std::vector<uint16_t>> neigh;   // per off-grid code
-    Iq2sTables() : map(43692, -1), neigh(43692) {
+// The codebook as the quantiser uses it: per point the 8 magnitudes 2l + 1;
+// the index of each base-4 level code (2 bits per value, levels 0..2) that is
+// a point, -1 otherwise; and for each level code off the book the points at
+// minimum squared distance, in ascending index order.
+struct Codebook {
+    int8_t mag[1024][8];
+    std::vector<int> index_of;                 // 4^8 codes (the largest formable one is < 43692)
+    std::vector<std::vector<uint16_t>> near;   // per off-book code
+    Codebook() : index_of(43692, -1), near(43692) {
         for (int k = 0; k < 1024; ++k) {
-            uint16_t index = 0;
+            uint16_t code = 0;
             for (int i = 0; i < 8; ++i) {
                 const int l = (kIq2sCodes[k] >> (2 * i)) & 3;
-                grid[k][i] = (int8_t)(2 * l + 1);
-                index |= (uint16_t)(l << (2 * i));
+                mag[k][i] = (int8_t)(2 * l + 1);
+                code |= (uint16_t)(l << (2 * i));
             }
-            map[index] = k;
+            index_of[code] = k;
         }
-        for (int u = 0; u < 43692; ++u) {
-            if (map[u] >= 0) continue;
-            bool valid = true;                  // codes the quantiser can form: levels 0..2
-            int8_t pos[8];
+        for (int code = 0; code < 43692; ++code) {
+            if (index_of[code] >= 0) continue;
+            int8_t v[8];
+            bool formable = true;              // levels 0..2 only
             for (int i = 0; i < 8; ++i) {
-                const int l = (u >> (2 * i)) & 3;
-                if (l == 3) valid = false;
-                pos[i] = (int8_t)(2 * l + 1);
+                const int l = (code >> (2 * i)) & 3;
+                formable = formable && l < 3;
+                v[i] = (int8_t)(2 * l + 1);
             }
-            if (!valid) continue;
+            if (!formable) continue;
             int best = 1 << 30;
-            for (int j = 0; j < 1024; ++j) {
+            for (int k = 0; k < 1024; ++k) {
                 int d2 = 0;
-                for (int i = 0; i < 8; ++i) d2 += (grid[j][i] - pos[i]) * (grid[j][i] - pos[i]);
-                if (d2 < best) { best = d2; neigh[u].clear(); }
-                if (d2 == best) neigh[u].push_back((uint16_t)j);
+                for (int i = 0; i < 8; ++i) d2 += (mag[k][i] - v[i]) * (mag[k][i] - v[i]);
+                if (d2 < best) {
+                    best = d2;
+                    near[code].clear();
+                }
+                if (d2 == best) near[code].push_back((uint16_t)k);
             }
         }
     }
 };
 
-const Iq2sTables & iq2s_tables() {
-    static const Iq2sTables t;
-    return t;
+const Codebook & codebook() {
+    static const Codebook cb;
+    return cb;
 }
 
-int iq2_find_best_neighbour(const Iq2sTables & T, const std::vector<uint16_t> & nb, const float * xval,
-                            const float * weight, float scale, int8_t * L) {
-    float best_d2 = FLT_MAX;
-    int grid_index = -1;
-    for (const uint16_t j : nb) {
-        const int8_t * pg = T.grid[j];
+// One group of 8 magnitudes set to levels.  Off the book, the levels become
+// those of the nearest point (weighted distance at `step`, the first of equals).
+// Returns whether the plain levels were on the book.
+bool snap_group(const Codebook & cb, const float * v, const float * sw, float inv, float step, int8_t * lv) {
+    uint16_t code = 0;
+    for (int i = 0; i < 8; ++i) {
+        lv[i] = (int8_t)clampi(rne(0.5f * (inv * v[i] - 1)), 0, 2);
+        code |= (uint16_t)(lv[i] << (2 * i));
+    }
+    if (cb.index_of[code] >= 0) return true;
+    float best = FLT_MAX;
+    int pick = -1;
+    for (const uint16_t k : cb.near[code]) {
         float d2 = 0;
         for (int i = 0; i < 8; ++i) {
-            const float q = pg[i];
-            const float diff = scale * q - xval[i];
-            d2 += weight[i] * diff * diff;
+            const float q = cb.mag[k][i];
+            const float r = step * q - v[i];
+            d2 += sw[i] * r * r;
         }
-        if (d2 < best_d2) {
-            best_d2 = d2;
-            grid_index = j;
+        if (d2 < best) {
+            best = d2;
+            pick = k;
         }
     }
-    const int8_t * pg = T.grid[grid_index];
-    for (int i = 0; i < 8; ++i) L[i] = (int8_t)((pg[i] - 1) / 2);
-    return grid_index;
+    for (int i = 0; i < 8; ++i) lv[i] = (int8_t)((cb.mag[pick][i] - 1) / 2);
+    return false;
 }
 
-void quantize_superblock_iq2_s(const float * xbl, blk_iq2_s * y, const float * qw_row) {
-    const Iq2sTables & T = iq2s_tables();
-    const int kMaxQ = 3;
-    float scales[16], weight[16], xval[16], waux[16];
-    int8_t L[16], Laux[16];
-    bool is_on_grid[2], is_on_grid_aux[2];
-    uint8_t block_signs[2];
+// sum w v q and sum w q q of a block's 16 levels (q = 2 l + 1)
+inline SymSums iq2_sums(const float * v, const float * w, const int8_t * lv) {
+    SymSums s;
+    for (int i = 0; i < 16; ++i) {
+        const float q = 2 * lv[i] + 1;
+        s.qx += w[i] * v[i] * q;
+        s.qq += w[i] * q * q;
+    }
+    return s;
+}
 
-    memset(y, 0, sizeof(blk_iq2_s));
-    y->d = float_to_half(0.f);
-    float max_scale = 0;
-    float sumx2 = 0;
-    for (int i = 0; i < QK_K; ++i) sumx2 += xbl[i] * xbl[i];
-    const float sigma2 = 2 * sumx2 / QK_K;
+void iq2s_super_block(const float * x, blk_iq2_s * out, const float * imat) {
+    const Codebook & cb = codebook();
+    memset(out, 0, sizeof(*out));
+    float energy = 0;
+    for (int i = 0; i < QK_K; ++i) energy += x[i] * x[i];
+    const float sigma2 = 2 * energy / QK_K;
+    float steps[16];
+    float top = 0;
+    for (int b = 0; b < 16; ++b) {
+        const float * xb = x + 16 * b;
+        float w[16], sw[16], v[16];
+        for (int i = 0; i < 16; ++i) {
+            w[i] = imat ? imat[16 * b + i] * sqrtf(sigma2 + xb[i] * xb[i]) : 0.25f * sigma2 + xb[i] * xb[i];
+            sw[i] = sqrtf(w[i]);
+        }
+        uint8_t signs[2] = {0, 0};
+        for (int i = 0; i < 16; ++i) {
+            v[i] = xb[i] >= 0 ? xb[i] : -xb[i];
+            if (!(xb[i] >= 0)) signs[i >> 3] |= (uint8_t)(1 << (i & 7));
+        }
+        float peak = v[0];
+        for (int i = 1; i < 16; ++i) peak = std::max(peak, v[i]);
+        steps[b] = 0;
+        if (peak < 1e-8f) continue;                        // an empty block: all zero bytes
 
-    for (int ib = 0; ib < 16; ++ib) {
-        const float * xb = xbl + 16 * ib;
-        if (qw_row) {
-            const float * qw = qw_row + 16 * ib;
-            for (int i = 0; i < 16; ++i) weight[i] = qw[i] * sqrtf(sigma2 + xb[i] * xb[i]);
-        } else {
-            for (int i = 0; i < 16; ++i) weight[i] = 0.25f * sigma2 + xb[i] * xb[i];
-        }
-        for (int i = 0; i < 16; ++i) waux[i] = sqrtf(weight[i]);
-        for (int k = 0; k < 2; ++k) {
-            uint8_t s = 0;
-            for (int i = 0; i < 8; ++i) {
-                if (xb[8 * k + i] >= 0) {
-                    xval[8 * k + i] = xb[8 * k + i];
-                } else {
-                    xval[8 * k + i] = -xb[8 * k + i];
-                    s |= (uint8_t)(1 << i);
-                }
-            }
-            block_signs[k] = s;
-        }
-        float max = xval[0];
-        for (int i = 1; i < 16; ++i) max = std::max(max, xval[i]);
-        memset(L, 0, 16);
-        if (max < 1e-8f) {
-            scales[ib] = 0;
-            continue;
-        }
-        float best = 0;
-        float scale = max / (2 * kMaxQ - 1);
-        is_on_grid[0] = is_on_grid[1] = true;
-        for (int is = -9; is <= 9; ++is) {
-            const float id = (2 * kMaxQ - 1 + is * 0.1f) / max;
-            const float this_scale = 1 / id;
-            for (int k = 0; k < 2; ++k) {
-                for (int i = 0; i < 8; ++i) {
-                    const int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
-                    Laux[8 * k + i] = (int8_t)std::max(0, std::min(kMaxQ - 1, l));
-                }
-                uint16_t u = 0;
-                for (int i = 0; i < 8; ++i) u |= (uint16_t)(Laux[8 * k + i] << (2 * i));
-                is_on_grid_aux[k] = true;
-                if (T.map[u] < 0) {
-                    is_on_grid_aux[k] = false;
-                    iq2_find_best_neighbour(T, T.neigh[u], xval + 8 * k, waux + 8 * k, this_scale, Laux + 8 * k);
-                }
-            }
-            float sumqx = 0, sumq2 = 0;
-            for (int i = 0; i < 16; ++i) {
-                const float w = weight[i];
-                const float q = 2 * Laux[i] + 1;
-                sumqx += w * xval[i] * q;
-                sumq2 += w * q * q;
-            }
-            if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
-                scale = sumqx / sumq2;
-                best = scale * sumqx;
-                for (int i = 0; i < 16; ++i) L[i] = Laux[i];
-                for (int k = 0; k < 2; ++k) is_on_grid[k] = is_on_grid_aux[k];
+        // 19 inverse steps (5 + 0.1 t) / peak, t = -9..9; the least-squares
+        // step of each assignment, the best gain kept
+        int8_t lv[16] = {}, trial[16];
+        bool on_book[2] = {true, true};
+        float step = peak / 5, gain = 0;
+        for (int t = -9; t <= 9; ++t) {
+            const float inv = (5 + t * 0.1f) / peak;
+            const float at = 1 / inv;
+            bool trial_on[2];
+            for (int g = 0; g < 2; ++g) trial_on[g] = snap_group(cb, v + 8 * g, sw + 8 * g, inv, at, trial + 8 * g);
+            const SymSums s = iq2_sums(v, w, trial);
+            if (s.qq > 0 && s.qx * s.qx > gain * s.qq) {
+                step = s.qx / s.qq;
+                gain = step * s.qx;
+                std::copy(trial, trial + 16, lv);
+                on_book[0] = trial_on[0];
+                on_book[1] = trial_on[1];
             }
         }
-        int n_not_ongrid = 0;
-        for (int k = 0; k < 2; ++k) if (!is_on_grid[k]) ++n_not_ongrid;
-        if (n_not_ongrid > 0 && scale > 0) {
-            const float id = 1 / scale;
-            for (int k = 0; k < 2; ++k) {
-                if (is_on_grid[k]) continue;
-                uint16_t u = 0;
-                for (int i = 0; i < 8; ++i) {
-                    int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
-                    l = std::max(0, std::min(kMaxQ - 1, l));
-                    u |= (uint16_t)(l << (2 * i));
-                    L[8 * k + i] = (int8_t)l;
-                }
-                if (T.map[u] < 0)
-                    iq2_find_best_neighbour(T, T.neigh[u], xval + 8 * k, waux + 8 * k, scale, L + 8 * k);
-            }
-            float sumqx = 0, sumq2 = 0;
-            for (int i = 0; i < 16; ++i) {
-                const float w = weight[i];
-                const float q = 2 * L[i] + 1;
-                sumqx += w * xval[i] * q;
-                sumq2 += w * q * q;
-            }
-            if (sumq2 > 0) scale = sumqx / sumq2;
+        // a group the best assignment had to move onto the book is re-snapped
+        // at the final step, and the step refitted
+        if ((!on_book[0] || !on_book[1]) && step > 0) {
+            const float inv = 1 / step;
+            for (int g = 0; g < 2; ++g)
+                if (!on_book[g]) snap_group(cb, v + 8 * g, sw + 8 * g, inv, step, lv + 8 * g);
+            const SymSums s = iq2_sums(v, w, lv);
+            if (s.qq > 0) step = s.qx / s.qq;
         }
-        if (scale < 0) {
-            scale = -scale;
-            for (int k = 0; k < 2; ++k) block_signs[k] = (uint8_t)~block_signs[k];
+        if (step < 0) {
+            step = -step;
+            signs[0] = (uint8_t)~signs[0];
+            signs[1] = (uint8_t)~signs[1];
         }
-        for (int k = 0; k < 2; ++k) {
-            uint16_t u = 0;
-            for (int i = 0; i < 8; ++i) u |= (uint16_t)(L[8 * k + i] << (2 * i));
-            const int grid_index = T.map[u];
-            if (grid_index < 0) {
-                fprintf(stderr, "llapis: IQ2_S level code %u is not on the grid\n", u);
+        for (int g = 0; g < 2; ++g) {
+            uint16_t code = 0;
+            for (int i = 0; i < 8; ++i) code |= (uint16_t)(lv[8 * g + i] << (2 * i));
+            const int k = cb.index_of[code];
+            if (k < 0) {
+                fprintf(stderr, "llapis: IQ2_S level code %u is not in the codebook\n", code);
                 abort();
             }
-            const int i8 = 2 * ib + k;
-            y->qs[i8] = (uint8_t)(grid_index & 255);
-            y->qh[i8 / 4] |= (uint8_t)((grid_index >> 8) << (2 * (i8 % 4)));
-            y->qs[32 + i8] = block_signs[k];
+            const int slot = 2 * b + g;                // 10-bit index: 8 bits in qs, 2 in qh
+            out->qs[slot] = (uint8_t)(k & 255);
+            out->qh[slot / 4] |= (uint8_t)((k >> 8) << (2 * (slot % 4)));
+            out->qs[32 + slot] = signs[g];
         }
-        scales[ib] = scale;
-        max_scale = std::max(max_scale, scale);
+        steps[b] = step;
+        top = std::max(top, step);
     }
-    if (!max_scale) return;
-    const float d = max_scale / 31;
-    y->d = float_to_half(d * 0.9875f);
-    const float id = 1 / d;
-    for (int ib = 0; ib < 16; ++ib) {
-        int l = nearest_int(0.5f * (id * scales[ib] - 1));
-        l = std::max(0, std::min(15, l));
-        if (ib % 2 == 0) y->scales[ib / 2] = (uint8_t)l;
-        else y->scales[ib / 2] |= (uint8_t)(l << 4);
+    if (!top) return;
+    // block steps as 4-bit odd multiples (2 l + 1) of half the super-block step
+    const float unit = top / 31;
+    out->d = float_to_half(unit * 0.9875f);
+    const float inv = 1 / unit;
+    for (int b = 0; b < 16; ++b) {
+        const int l = clampi(rne(0.5f * (inv * steps[b] - 1)), 0, 15);
+        out->scales[b / 2] |= (uint8_t)(l << (4 * (b % 2)));
     }
 }
 
 // ------------------------------------------------------------- driver
 
 void quantize_row(int type, const float * x, uint8_t * dst, int64_t n, const float * imatrix) {
-    switch (type) {
-        case T_Q4_K:
-            for (int64_t b = 0; b < n / QK_K; ++b) quantize_block_q4_K(x + b * QK_K, (blk_q4_K *)dst + b);
-            break;
-        case T_Q5_0:
-            for (int64_t b = 0; b < n / 32; ++b) quantize_block_q5_0(x + b * 32, (blk_q5_0 *)dst + b);
-            break;
-        case T_IQ4_NL:
-            for (int64_t b = 0; b < n / 32; ++b)
-                quantize_block_iq4_nl(x + b * 32, (blk_iq4_nl *)dst + b, imatrix ? imatrix + b * 32 : nullptr);
-            break;
-        case T_IQ2_S:
-            for (int64_t b = 0; b < n / QK_K; ++b)
-                quantize_superblock_iq2_s(x + b * QK_K, (blk_iq2_s *)dst + b, imatrix ? imatrix + b * QK_K : nullptr);
-            break;
-        default:
-            abort();
+    const int per = blk_elems(type), bytes = blk_bytes(type);
+    for (int64_t b = 0; b < n / per; ++b) {
+        const float * xb = x + b * per;
+        uint8_t * yb = dst + b * bytes;
+        const float * im = imatrix ? imatrix + b * per : nullptr;
+        switch (type) {
+            case T_Q4_K: q4k_super_block(xb, (blk_q4_K *)yb); break;
+            case T_Q5_0: q50_block(xb, (blk_q5_0 *)yb); break;
+            case T_IQ4_NL: iq4nl_block(xb, (blk_iq4_nl *)yb, im); break;
+            case T_IQ2_S: iq2s_super_block(xb, (blk_iq2_s *)yb, im); break;
+            default: abort();
+        }
     }
 }
 
@@ -546,7 +512,7 @@ uint64_t llapis_quantize(int32_t type, const float * src, void * dst, int64_t nr
     // which this library does not restate: refuse rather than differ.
     if (imatrix && (type == T_Q4_K || type == T_Q5_0)) return 0;
     const uint64_t rb = row_bytes(type, n_per_row);
-    if (type == T_IQ2_S) (void)iq2s_tables();   // build once, before the workers start
+    if (type == T_IQ2_S) (void)codebook();   // build once, before the workers start
     parallel_rows(nrow, [&](int64_t r0, int64_t r1) {
         for (int64_t r = r0; r < r1; ++r)
             quantize_row(type, src + r * n_per_row, (uint8_t *)dst + r * rb, n_per_row, imatrix);
