@@ -146,10 +146,10 @@ uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tok
 
 /* out [T][d_model] = the layer applied to x [T][d_model].  ids/weights
  * ([T][top_k], optional) receive the routing.  Batches of up to 4 tokens
- * take the three-kernel decode path, whose control block lives at the start
- * of the workspace: zero the workspace before its first use (e.g. with
- * llapis_moe_ffn_workspace_init); the library keeps it consistent after
- * that.  Calls that share a workspace must not run concurrently. */
+ * take the three-kernel decode path.  Each call writes every workspace word
+ * before it reads it, so nothing is carried from one call to the next (and
+ * calls can be captured in HIP graphs); calls that share a workspace must not
+ * run concurrently. */
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
                        int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
 
@@ -169,7 +169,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
 int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
                                int32_t * ids, float * weights, void * stream);
 
-/* Zero the control block of a fused-layer workspace (a kernel on `stream`). */
+/* Zero the control block at the start of a workspace (a kernel on
+ * `stream`).  Optional: no call reads a workspace word it has not written. */
 int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspace, uint64_t ws_bytes, void * stream);
 
 /* ------------------------------------------------------ promotion engine
@@ -375,24 +376,15 @@ void    llapis_kfit(const llapis_kfit_inputs * in, llapis_kfit_decision * out);
  * free_mib for llapis_kfit_inputs.  0 ok, -1 on a HIP error. */
 int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
 
-/* Tuning switches for measurement: key 0 = decode path for <= 4 tokens
- * (default 1), key 1 = gate_up kernel touches the down slabs ahead of the
- * down kernel (default 0: no gain measured),
- * key 2 = MFMA prefill path for > 4 tokens (default 1), key 3 = the decode
- * path as one kernel (default 0: three kernels, faster on MI355X today),
- * key 4 = the bound of one wait of the kernels that wait (the one-kernel
- * path and the fused gate_up+down kernel) in microseconds (default 50000),
- * key 5 = gate_up and down as one kernel in the three-kernel path, for one
- * token and the Q4_K/IQ2_S + Q5_0/IQ4_NL formats (default 0: measured
- * slower than the two kernels on MI355X today). */
+/* Switches for measurement: key 0 = the decode path for <= 4 tokens
+ * (default 1; 0 sends those calls down the generic path), key 2 = the MFMA
+ * prefill path for > 4 tokens (default 1), key 3 = log2 of the output rows
+ * per workgroup of the decode path's down kernel over every group (0..5;
+ * -1, the default, picks it from d_model and the token count), key 4 = the
+ * decode path's down kernel: 1 by expert group with a combine kernel after
+ * it, 0 over every group with the combine in it, -1 (default) by group from
+ * two tokens on.  Other keys are ignored. */
 void llapis_set_tuning(int32_t key, int32_t value);
-
-/* Waits for `stream`, then reports whether a call on this workspace since
- * the last status check had a wait of the single-kernel decode path time out
- * (possible only if its workgroups could not all be resident at once, e.g.
- * while other work occupies the GPU): 0 if not, else a negative code with
- * llapis_last_error() set; the flag is cleared. */
-int32_t llapis_moe_ffn_status(void * workspace, uint64_t ws_bytes, void * stream);
 
 /* Stage timing of llapis_moe_ffn for measurement (not under stream capture):
  * while enabled, every call times its stages on the call's stream with HIP

@@ -252,7 +252,6 @@ SIGNATURES = {
     "llapis_moe_ffn": (i32, [C.POINTER(LlapisMoeLayer), vp, i32, vp, vp, vp, vp, u64, vp]),
     "llapis_moe_ffn_workspace_init": (i32, [C.POINTER(LlapisMoeLayer), vp, u64, vp]),
     "llapis_moe_ffn_noalloc": (i32, [C.POINTER(LlapisMoeLayer), vp, i32, vp, vp, vp, vp]),
-    "llapis_moe_ffn_status": (i32, [vp, u64, vp]),
     "llapis_set_tuning": (None, [i32, i32]),
     "llapis_profile_enable": (None, [i32]),
     "llapis_profile_read": (i32, [vp, i32]),

@@ -519,31 +519,26 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefill{1}, g_fused{0}, g_fuse_bc{0}, g_prefetch_dn{0};
-std::atomic<int64_t> g_spin_us{50000};        // bound of one wait in the single-kernel decode path
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1};
 
-// wall-clock ticks per microsecond of the current device (cached per device)
-int64_t wall_ticks_per_us() {
+// the largest LDS allocation of one workgroup on the current device (cached)
+int max_lds_per_wg() {
     static std::mutex mu;
-    static std::map<int, int64_t> cache;
+    static std::map<int, int> cache;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 100;
+    if (hipGetDevice(&dev) != hipSuccess) return 65536;
     std::lock_guard<std::mutex> lk(mu);
     auto it = cache.find(dev);
     if (it != cache.end()) return it->second;
-    int khz = 0;
-    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) khz = 100000;
-    const int64_t t = std::max<int64_t>(1, khz / 1000);
-    cache[dev] = t;
-    return t;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+    cache[dev] = v;
+    return v;
 }
 
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
-uint64_t dec_ctl_bytes(const llapis_moe_layer * L) {
-    const int n_rb = (L->d_model + 31) / 32, n_rb_gu = (2 * L->n_ff + 15) / 16;
-    return al256(sizeof(DecCtl)) + al256((uint64_t)DEC_MAXT * n_rb * 4) + al256((uint64_t)DEC_PMAX * n_rb_gu * 4);
-}
+uint64_t dec_ctl_bytes(const llapis_moe_layer *) { return al256(sizeof(DecCtl)); }
 
 // generic path (any T): probs, ids, w, y_gu, y_dn -- after the decode path's
 // control block, which every layout reserves so the two paths can share a
@@ -563,36 +558,32 @@ FfnWs ffn_ws(const llapis_moe_layer * L, int32_t T) {
     return w;
 }
 
-// decode path (T <= DEC_MAXT): control block first (zero before first use)
+// decode path (T <= DEC_MAXT): control block first
 struct DecWs {
-    uint64_t ctl, comb, gu_done, logits, ids, w, xq, ygu, aq, ydn, total, ctl_bytes;
-    int64_t xq_stride, aq_stride;
-    int n_rb;
+    uint64_t ctl, logits, ids, w, xq, ya, ydn, total, ctl_bytes;
+    int64_t xq_stride;
 };
 DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
     const uint64_t P = (uint64_t)T * L->top_k;
     DecWs w;
-    w.n_rb = (L->d_model + 31) / 32;
     w.xq_stride = dec_act_bytes(L->d_model);
-    w.aq_stride = dec_act_bytes(L->n_ff);
     w.ctl = 0;
-    w.comb = al256(sizeof(DecCtl));
-    w.gu_done = w.comb + al256((uint64_t)DEC_MAXT * w.n_rb * 4);
     w.ctl_bytes = dec_ctl_bytes(L);
     w.logits = w.ctl_bytes;
     w.ids = w.logits + al256((uint64_t)T * L->n_expert * 4);
     w.w = w.ids + al256(P * 4);
     w.xq = w.w + al256(P * 4);
-    w.ygu = w.xq + al256((uint64_t)T * w.xq_stride);
-    w.aq = w.ygu + al256(P * 2 * L->n_ff * 4);
-    w.ydn = w.aq + al256(P * w.aq_stride);
+    w.ya = w.xq + al256((uint64_t)T * w.xq_stride);
+    w.ydn = w.ya + al256(P * L->n_ff * 4);
     w.total = w.ydn + al256(P * L->d_model * 4);
     return w;
 }
 
 bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
+    // n_ff <= 1024: the down kernel quantises one 16-byte chunk of each pair's
+    // activation per lane, and 16 lanes hold a row as whole block pairs
     return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && L->k_slots <= 256 &&
-           (L->d_model % 4) == 0;
+           (L->d_model % 4) == 0 && L->n_ff <= 1024 && L->n_ff % 64 == 0;
 }
 
 // prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
@@ -633,11 +624,9 @@ bool prefill_eligible(const llapis_moe_layer * L, int32_t T) {
 
 void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
-    if (key == 1) g_prefetch_dn = value != 0;
     if (key == 2) g_prefill = value != 0;
-    if (key == 3) g_fused = value != 0;
-    if (key == 4) g_spin_us = std::max(0, value);
-    if (key == 5) g_fuse_bc = value != 0;
+    if (key == 3) g_dn_rows_log2 = value >= 0 && value <= 5 ? value : -1;
+    if (key == 4) g_dn_by_group = value == 0 || value == 1 ? value : -1;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
@@ -654,21 +643,6 @@ int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspa
     const uint64_t n = std::min<uint64_t>(ws_bytes, dw.ctl_bytes);
     LL_TRY(launch_zero_i32(static_cast<int *>(workspace), (int)(n / 4), (hipStream_t)stream));
     return 0;
-}
-
-int32_t llapis_moe_ffn_status(void * workspace, uint64_t ws_bytes, void * stream) {
-    if (!workspace || ws_bytes < sizeof(DecCtl)) return fail("llapis_moe_ffn_status: workspace too small");
-    hipStream_t s = (hipStream_t)stream;
-    DecCtl * ctl = static_cast<DecCtl *>(workspace);
-    int err = 0;
-    LL_TRY(hipMemcpyAsync(&err, &ctl->error, sizeof(int), hipMemcpyDeviceToHost, s));
-    LL_TRY(hipStreamSynchronize(s));
-    if (err == 0) return 0;
-    const int zero = 0;
-    LL_TRY(hipMemcpyAsync(&ctl->error, &zero, sizeof(int), hipMemcpyHostToDevice, s));
-    LL_TRY(hipStreamSynchronize(s));
-    return fail("llapis_moe_ffn: a wait of the single-kernel decode path timed out (its workgroups were not all "
-                "resident); that call's outputs are invalid");
 }
 
 int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
@@ -704,44 +678,38 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         p.exp_slot = L->exp_slot; p.slot_exp = L->slot_exp; p.slot_state = L->slot_state;
         p.s_hot = L->s_hot; p.s_cold = L->s_cold;
         p.ctl = reinterpret_cast<DecCtl *>(base + dw.ctl);
-        p.comb_count = reinterpret_cast<int *>(base + dw.comb);
-        p.gu_done = reinterpret_cast<int *>(base + dw.gu_done);
-        p.hot_dn_type = L->hot_dn_type;
-        p.cold_dn_type = L->cold_dn_type;
-        p.prefetch_dn = g_prefetch_dn.load();
-        p.never = 0;
         p.rc_counts = L->route_counts;
         p.rc_hits = L->route_counts ? L->route_hits : nullptr;
         p.logits = reinterpret_cast<float *>(base + dw.logits);
         p.ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + dw.ids);
         p.w = w_out ? w_out : reinterpret_cast<float *>(base + dw.w);
         p.xq = base + dw.xq; p.xq_stride = dw.xq_stride;
-        p.ygu = reinterpret_cast<float *>(base + dw.ygu);
-        p.aq = base + dw.aq; p.aq_stride = dw.aq_stride;
+        p.ya = reinterpret_cast<float *>(base + dw.ya);
         p.ydn = reinterpret_cast<float *>(base + dw.ydn);
+        // the down kernel by group from two tokens on (one token: 0.4 us
+        // faster over every group, without the combine kernel)
+        p.dn_by_group = g_dn_by_group.load() >= 0 ? g_dn_by_group.load() : (T > 1 ? 1 : 0);
         p.out = out;
         const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
-        const int rbd = (int)std::max(rbytes(L->hot_dn_type, L->n_ff), rbytes(L->cold_dn_type, L->n_ff));
-        p.w_lds_gu = dev::align16(16 * rbg + 32);
-        p.w_lds_dn = dev::align16(32 * rbd + 32);
-        p.n_rb_down = dw.n_rb;
-        if (dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) <= 65536 && dec_lds_down(p) <= 65536) {
+        p.w_lds_gu = dev::align16(8 * rbg + 32);
+        // the down rows: a power of two giving about three blocks per CU of
+        // the part (256 CUs on MI355X: 4 rows, 704 blocks at d_model 2816) for
+        // one token, four times that for more (each block re-reads every
+        // pair's activation)
+        int lg2r = 0;
+        while ((1 << lg2r) < DEC_DN_MAXR && (1 << lg2r) * 768 < L->d_model) ++lg2r;
+        if (T > 1) lg2r = std::min(lg2r + 2, 5);
+        if (g_dn_rows_log2.load() >= 0) lg2r = g_dn_rows_log2.load();
+        p.dn_rows_log2 = lg2r;
+        const int lds_max = max_lds_per_wg();
+        if (dec_lds_down(p) + 16 * 1024 <= lds_max && dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) + 16 * 1024 <= lds_max) {
             const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
-            p.spin_limit = g_spin_us.load() * wall_ticks_per_us();
-            if (g_fused.load()) {
-                // the single kernel's time is reported as the gate_up stage
-                hipEvent_t evf[2] = {prof_ev(pc, 2, 0), prof_ev(pc, 2, 1)};
-                const hipError_t e = launch_decode_fused(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type,
-                                                         L->cold_dn_type, L->act_mode, src, s, pc >= 0 ? evf : nullptr);
-                if (e == hipSuccess) return 0;
-                if (e != hipErrorNotSupported) return fail(std::string("launch_decode_fused: ") + hipGetErrorString(e));
-                if (pc >= 0) g_prof.used[pc][2] = false;
-            }
-            hipEvent_t ev[6] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0),
-                                prof_ev(pc, 2, 1), prof_ev(pc, 3, 0), prof_ev(pc, 3, 1)};
+            hipEvent_t ev[8] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0), prof_ev(pc, 2, 1),
+                                prof_ev(pc, 3, 0), prof_ev(pc, 3, 1),
+                                p.dn_by_group ? prof_ev(pc, 4, 0) : nullptr, p.dn_by_group ? prof_ev(pc, 4, 1) : nullptr};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
-                                 src, g_fuse_bc.load() != 0, s, pc >= 0 ? ev : nullptr));
+                                 src, s, pc >= 0 ? ev : nullptr));
             return 0;
         }
     }

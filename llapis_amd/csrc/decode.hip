@@ -5,31 +5,34 @@
 //                    in the workgroups after those, the tokens' activation
 //                    quantisation.
 //   B  k_dec_gate_up every workgroup selects the routing from the logits
-//                    (softmax, top-k with DPP wave reductions, ties to the
-//                    lower index), groups the routed pairs by expert (decode
-//                    once, dot N: the tokens that share an expert read its
-//                    slab once) and resolves each group's tier (the residency
-//                    predicate of moert/cuda/ffn_moe.cu:80-130); the first
-//                    workgroup publishes ids, weights and groups for C.  Then a
-//                    loop over the workgroup's (expert group, 16-row block)
-//                    items: the expert's rows stream through LDS with 128-bit
-//                    loads and are dotted against every member token, the next
-//                    item's loads in flight meanwhile.
-//   C  k_dec_down    a loop over (expert group, 32-row block) items: GEGLU and
-//                    down activation quantisation of each group's pairs (while
-//                    the first slab is in flight), the down projection with
-//                    the expert's .scale, and the combine: the last arrival of
-//                    a (token, row block) writes the weighted sum of the
-//                    token's top_k outputs for those rows.
+//                    (softmax, top-k by a bisection for the k-th largest
+//                    probability, ties to the lower index), groups the routed
+//                    pairs by expert (decode once, dot N: the tokens that
+//                    share an expert read its slab once) and resolves each
+//                    group's tier (the residency predicate of
+//                    moert/cuda/ffn_moe.cu:80-130); the first workgroup
+//                    publishes ids, weights and groups for C.  Then its items:
+//                    an item is one group's 32-row block of gate rows and the
+//                    32 up rows paired with them (rows i and n_ff + i), read as
+//                    four 16-row steps that all go out at once; the rows are
+//                    dotted against every member token, and the item ends with
+//                    GEGLU of each gate/up pair and the q8 quantisation of the
+//                    32 results -- one block of each member's down activation,
+//                    written once.
+//   C  k_dec_down    one workgroup per block of output rows, over every group:
+//                    the blocks' rows of each routed expert's down slab stream
+//                    through LDS in batches of groups (the next batch in flight
+//                    meanwhile), are dotted against the members' down
+//                    activations and scaled by the expert's .scale, and the
+//                    workgroup writes the weighted sum of each token's top_k
+//                    outputs for its rows (llama-graph.cpp:1812-1840 order).
 //
-// Every load a kernel issues before its first wait is unconditional (clamped
-// addresses instead of branches) and issued in the order its data are needed:
-// loads complete in issue order, so a wait then covers only the loads before
-// it -- the routing does not wait for the codebook, nor the GEGLU for the
-// weight slab.  B and C grids are sized to the resident workgroups; no
-// workgroup ever waits on another.  C's per-pair outputs are handed to the
-// combine with device-scope coherent stores and one arrival atomic each; the
-// last arriver reads them with device-scope coherent loads.
+// No workgroup waits on another: B hands over through its first workgroup's
+// records and the down activations, C reads them at the kernel boundary and
+// owns its output rows outright, so any grid is safe.  Every load a kernel
+// issues before its first wait is unconditional (clamped addresses instead of
+// branches) and issued in the order its data are needed: loads complete in
+// issue order, so a wait covers only the loads before it.
 #include <hip/hip_ext.h>
 
 #include <climits>
@@ -46,26 +49,7 @@ namespace dev {
 __constant__ Iq2sTables c_iq2s_tab_dec = make_iq2s_tables();
 
 template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
-static_assert(DEC_MAXT == 4, "accumulator initialisers below assume four columns");
-
-__device__ __forceinline__ void st_coh(float * p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coh(const float * p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// this thread's outstanding vector memory operations have completed
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// all threads' coherent stores are complete; thread 0 arrives on `counter`;
-// returns (to every thread) whether this workgroup arrived last of `n`
-__device__ __forceinline__ bool arrive_last(int * counter, int n, int * s_flag) {
-    wait_vm();
-    __syncthreads();
-    if (threadIdx.x == 0) *s_flag = atomicAdd(counter, 1) == n - 1;
-    __syncthreads();
-    return *s_flag != 0;
-}
+static_assert(DEC_MAXT == 4, "one member column per wave in the gate_up epilogue");
 
 __device__ __forceinline__ int member(const GroupInfo & g, int i) {
     return i == 0 ? g.mem[0] : i == 1 ? g.mem[1] : i == 2 ? g.mem[2] : g.mem[3];
@@ -76,77 +60,204 @@ __device__ __forceinline__ const uint8_t * group_slab(int tier, int idx, const u
     return tier == 0 ? hot + (uint64_t)idx * hs : cold + (uint64_t)idx * cs;
 }
 
-// ---------------------------------------------------------------- A
-
-// Softmax + top-K of one token in one wave (ggml soft_max: exp(x - max), sum
-// in double, scaled by float(1/sum); argsort_top_k: descending, equal
-// probabilities in index order; weights p[ids] / max(sum, 6.103515625e-5)
-// with the sum accumulated in double in id order).  E <= 256.
-template <int NJ>
-__device__ __forceinline__ float vmax(const float (&v)[4]) {
-    float m = v[0];
-#pragma unroll
-    for (int j = 1; j < NJ; ++j) m = fmaxf(m, v[j]);
-    return m;
+__device__ __forceinline__ uint64_t lanes_below() {
+    const int lane = threadIdx.x & 63;
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-template <int NJ>
-__device__ void select_token_n(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
-                               float * s_w) {
-    const int lane = threadIdx.x & 63;
-    float v[4];                 // entries lane + 64 j, j < NJ (the rest are never read)
+// ---------------------------------------------------------------- A
+
+// Router logits of expert e for every token (one workgroup).  Each lane
+// issues all of its row loads (RU float4 per pass) before any arithmetic.
+__device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 64]) {
+    constexpr int RU = 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = p.d_model, E = p.n_expert, T = p.T, n4 = d / 4;
+    const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
+    const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
+    float acc[DEC_MAXT];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? ld_coh(logits + e) : -INFINITY;
+    for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
+    for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
+        // clamped indices (row end, last token): every load is unconditional
+        float4 w4[RU], xv[DEC_MAXT][RU];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+            for (int u = 0; u < RU; ++u) xv[t][u] = x4[(int64_t)min(t, T - 1) * n4 + min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+        for (int t = 0; t < DEC_MAXT; ++t)
+#pragma unroll
+            for (int u = 0; u < RU; ++u)
+                if (t < T && k0 + u * WG < n4)
+                    acc[t] += w4[u].x * xv[t][u].x + w4[u].y * xv[t][u].y + w4[u].z * xv[t][u].z +
+                              w4[u].w * xv[t][u].w;
     }
-    const float mx = wave_max_dpp(vmax<NJ>(v));
+#pragma unroll
+    for (int t = 0; t < DEC_MAXT; ++t) {
+        const float s = wave_sum_dpp(acc[t]);
+        if (lane == 0) s_part[t][wave] = s;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < T) {
+        const int t = threadIdx.x;
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
+        p.logits[(int64_t)t * E + e] = s + (p.router_b ? p.router_b[e] : 0.0f);
+    }
+}
+
+// Router logits of every token (workgroups e < E, one expert each) and the
+// tokens' gate_up activation quantisation (the workgroups after them: one
+// wave per q8_K 256-block, or per 64 values of q8_1).
+template <int AM>
+__global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
+    __shared__ float s_part[DEC_MAXT][WG / 64];
+    const int E = p.n_expert;
+    if ((int)blockIdx.x < E) {
+        router_expert(p, blockIdx.x, s_part);
+        return;
+    }
+    const int d = p.d_model, T = p.T;
+    const int gw = ((int)blockIdx.x - E) * (WG / 64) + (int)(threadIdx.x >> 6);
+    const int nw = ((int)gridDim.x - E) * (WG / 64);
+    ActView v;
+    act_layout(d, 0, &v);
+    const int per_tok = AM == AM_CPU ? d / 256 : (d + 63) / 64;
+    for (int j = gw; j < T * per_tok; j += nw) {
+        const int t = j / per_tok, b = j - t * per_tok;
+        ActSrc src;
+        src.p = p.x + (int64_t)t * d;
+        src.n = d;
+        uint8_t * col = p.xq + (int64_t)t * p.xq_stride;
+        if (AM == AM_CPU) q8K_block<SRC_PLAIN>(col, v, src, b);
+        else {
+            const int pos = 64 * b + (threadIdx.x & 63);
+            const bool live = pos < d;
+            q8_32_put<AM_Q8_1>(col, v, live ? src.p[pos] : 0.0f, pos, live);
+        }
+    }
+}
+
+// ------------------------------------------------------------ routing
+
+// order-preserving map of floats to ints (larger float <=> larger signed int)
+__device__ __forceinline__ int f2o(float f) {
+    const int b = __float_as_int(f);
+    return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float o2f(int o) { return __int_as_float(o ^ ((o >> 31) & 0x7FFFFFFF)); }
+// wave64 integer maximum (one DPP step each), wave-uniform
+__device__ __forceinline__ int wave_max_i(int v) {
+    v = max(v, dpp_i<0xB1>(v, v));
+    v = max(v, dpp_i<0x4E>(v, v));
+    v = max(v, dpp_i<0x141>(v, v));
+    v = max(v, dpp_i<0x140>(v, v));
+    v = max(v, dpp_i<0x142, 0xA>(v, v));
+    v = max(v, dpp_i<0x143, 0xC>(v, v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+constexpr int DEC_KMAX = 16;    // top_k of a decode call, at most
+
+// LDS scratch of one wave's selection
+struct SelScratch {
+    int key[DEC_KMAX], idx[DEC_KMAX];
+    int out_idx[DEC_KMAX], out_key[DEC_KMAX];
+};
+
+// Softmax + top-K of one token in one wave, from its logits in registers
+// (v[j] = entry lane + 64 j; entries at or past E are ignored), as ggml's CPU
+// graph computes them (soft_max: exp(x - max), the sum in double,
+// probabilities scaled by float(1/sum); argsort_top_k: descending, equal
+// probabilities in index order; weights p / max(sum of the K in double, in
+// order, 6.103515625e-5)).  Probabilities are >= 0, so they are compared as
+// ints.  The K-th largest is found by bisection over its bits (the largest t
+// with at least K probabilities >= t, one ballot count per bit), the entries
+// above it and the lowest-indexed ones equal to it are compacted into LDS in
+// index order, and each of the K lanes ranks its entry against the others.
+// Nothing branches per lane.  ids and weights go to LDS when `wr`.
+template <int NJ>
+__device__ __forceinline__ void select_topk(const float (&v)[4], int E, int K, int * s_ids, float * s_w, bool wr,
+                                            SelScratch & sc) {
+    const int lane = threadIdx.x & 63;
+    int mo = INT_MIN;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mo = max(mo, lane + 64 * j < E ? f2o(v[j]) : INT_MIN);
+    const float mx = o2f(wave_max_i(mo));
+    float ev[NJ];
     double ls = 0.0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? expf(v[j] - mx) : 0.0f;
-        ls += (double)v[j];
+        ev[j] = lane + 64 * j < E ? expf(v[j] - mx) : 0.0f;
+        ls += (double)ev[j];
     }
     ls = wave_sum_dpp(ls);
     const float inv = (float)(1.0 / ls);
+    int q[NJ];                  // probabilities as ints; -1: absent
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) v[j] = lane + 64 * j < E ? __fmul_rn(v[j], inv) : -1.0f;
-    // probabilities are >= 0; a taken entry drops to -1
-    float sel = 0.0f;
-    double sum = 0.0;
-    for (int k = 0; k < K; ++k) {
-        const float m = wave_max_dpp(vmax<NJ>(v));
-        int e = -1;
+    for (int j = 0; j < NJ; ++j) q[j] = lane + 64 * j < E ? __float_as_int(__fmul_rn(ev[j], inv)) : -1;
+    // the K-th largest probability (they are at most 1.0f: bit 30 is clear)
+    int theta = 0;
+    for (int bit = 29; bit >= 0; --bit) {
+        const int c = theta | (1 << bit);
+        int n = 0;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const uint64_t b = __ballot(v[j] == m);
-            if (e < 0 && b) e = 64 * j + __builtin_ctzll(b);
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) if (lane + 64 * j == e) v[j] = -1.0f;
-        sum += (double)m;
-        if (lane == k) sel = m;
-        if (lane == 0) {
-            if (ids) ids[k] = e;
-            s_ids[k] = e;
-        }
+        for (int j = 0; j < NJ; ++j) n += __popcll(__ballot(q[j] >= c));
+        theta = n >= K ? c : theta;
     }
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) above += __popcll(__ballot(q[j] > theta));
+    const int need = K - above;         // entries equal to theta taken, lowest index first
+    const uint64_t below = lanes_below();
+    int eq_before = 0, taken = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const uint64_t eq = __ballot(q[j] == theta);
+        const bool sel = q[j] > theta || (q[j] == theta && eq_before + __popcll(eq & below) < need);
+        const uint64_t sm = __ballot(sel);
+        if (sel) {
+            const int pos = taken + __popcll(sm & below);
+            sc.key[pos] = q[j];
+            sc.idx[pos] = lane + 64 * j;
+        }
+        eq_before += __popcll(eq);
+        taken += __popcll(sm);
+    }
+    taken = min(taken, K);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the rank of entry `lane` among the taken ones: larger first, then the
+    // lower index (the entries are in index order)
+    const int mine = min(lane, DEC_KMAX - 1);
+    const int kk = lane < taken ? sc.key[mine] : -1, ki = lane < taken ? sc.idx[mine] : -1;
+    int rank = 0;
+    for (int m = 0; m < taken; ++m) {
+        const int km = sc.key[m];
+        rank += (km > kk || (km == kk && m < lane)) ? 1 : 0;
+    }
+    if (lane < taken) {
+        sc.out_idx[rank] = ki;
+        sc.out_key[rank] = kk;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int myid = lane < taken ? sc.out_idx[mine] : -1;
+    const int mysel = lane < taken ? sc.out_key[mine] : 0;
+    double sum = 0.0;
+    for (int k = 0; k < taken; ++k) sum += (double)__int_as_float(__builtin_amdgcn_readlane(mysel, k));
     float sf = (float)sum;
     if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
-    if (lane < K) {
-        if (w) w[lane] = sel / sf;
-        if (s_w) s_w[lane] = sel / sf;
+    if (wr && lane < K) {
+        s_ids[lane] = myid;
+        s_w[lane] = __int_as_float(mysel) / sf;
     }
-}
-
-// NJ = ceil(E / 64) entries per lane
-__device__ void select_token(const float * logits, int E, int K, int32_t * ids, float * w, int * s_ids,
-                             float * s_w = nullptr) {
-    if (E <= 64) select_token_n<1>(logits, E, K, ids, w, s_ids, s_w);
-    else if (E <= 128) select_token_n<2>(logits, E, K, ids, w, s_ids, s_w);
-    else if (E <= 192) select_token_n<3>(logits, E, K, ids, w, s_ids, s_w);
-    else select_token_n<4>(logits, E, K, ids, w, s_ids, s_w);
 }
 
 // Expert groups of the call from the routed ids in LDS (one wave): pairs that
@@ -228,167 +339,11 @@ __device__ void count_routes(const DecParams & p, const int * s_ids, const Group
     }
 }
 
-// Router logits of expert e for every token (one workgroup), written with
-// device-coherent stores.  Each lane issues all of its row loads (RU float4
-// per pass) before any arithmetic.
-__device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 64]) {
-    constexpr int RU = 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int d = p.d_model, E = p.n_expert, T = p.T, n4 = d / 4;
-    const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
-    const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
-    float acc[DEC_MAXT];
-#pragma unroll
-    for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
-    for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
-        // clamped indices (row end, last token): every load is unconditional
-        float4 w4[RU], xv[DEC_MAXT][RU];
-#pragma unroll
-        for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
-#pragma unroll
-        for (int t = 0; t < DEC_MAXT; ++t)
-#pragma unroll
-            for (int u = 0; u < RU; ++u) xv[t][u] = x4[(int64_t)min(t, T - 1) * n4 + min(k0 + u * WG, n4 - 1)];
-#pragma unroll
-        for (int t = 0; t < DEC_MAXT; ++t)
-#pragma unroll
-            for (int u = 0; u < RU; ++u)
-                if (t < T && k0 + u * WG < n4)
-                    acc[t] += w4[u].x * xv[t][u].x + w4[u].y * xv[t][u].y + w4[u].z * xv[t][u].z +
-                              w4[u].w * xv[t][u].w;
-    }
-#pragma unroll
-    for (int t = 0; t < DEC_MAXT; ++t) {
-        const float s = wave_sum_dpp(acc[t]);
-        if (lane == 0) s_part[t][wave] = s;
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < T) {
-        const int t = threadIdx.x;
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
-        st_coh(p.logits + (int64_t)t * E + e, s + (p.router_b ? p.router_b[e] : 0.0f));
-    }
-}
-
-// Router logits of every token (workgroups e < E, one expert each) and the
-// tokens' gate_up activation quantisation (the workgroups after them: one
-// wave per q8_K 256-block, or per 64 values of q8_1); the first of those also
-// zeroes the call's hand-off counters and flags.  Nothing waits on anything:
-// the kernel ends when the router rows have been read.
-template <int AM>
-__global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
-    __shared__ float s_part[DEC_MAXT][WG / 64];
-    const int E = p.n_expert;
-    if ((int)blockIdx.x < E) {
-        router_expert(p, blockIdx.x, s_part);
-        return;
-    }
-    const int d = p.d_model, T = p.T;
-    if ((int)blockIdx.x == E) {
-        // the call's hand-off counters start at zero (the down kernel's
-        // combine arrivals; the fused gate_up+down kernel's item done flags)
-        for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
-        const int n_done = p.T * p.top_k * ((2 * p.n_ff + 15) / 16);
-        for (int i = threadIdx.x; i < n_done; i += WG) p.gu_done[i] = 0;
-    }
-    const int gw = ((int)blockIdx.x - E) * (WG / 64) + (int)(threadIdx.x >> 6);
-    const int nw = ((int)gridDim.x - E) * (WG / 64);
-    ActView v;
-    act_layout(d, 0, &v);
-    const int per_tok = AM == AM_CPU ? d / 256 : (d + 63) / 64;
-    for (int j = gw; j < T * per_tok; j += nw) {
-        const int t = j / per_tok, b = j - t * per_tok;
-        ActSrc src;
-        src.p = p.x + (int64_t)t * d;
-        src.n = d;
-        uint8_t * col = p.xq + (int64_t)t * p.xq_stride;
-        if (AM == AM_CPU) q8K_block<SRC_PLAIN>(col, v, src, b);
-        else {
-            const int pos = 64 * b + (threadIdx.x & 63);
-            const bool live = pos < d;
-            q8_32_put<AM_Q8_1>(col, v, live ? src.p[pos] : 0.0f, pos, live);
-        }
-    }
-}
-
-// order-preserving map of floats to ints (larger float <=> larger signed int)
-__device__ __forceinline__ int f2o(float f) {
-    const int b = __float_as_int(f);
-    return b ^ ((b >> 31) & 0x7FFFFFFF);
-}
-__device__ __forceinline__ float o2f(int o) { return __int_as_float(o ^ ((o >> 31) & 0x7FFFFFFF)); }
-// wave64 integer maximum (one DPP step each), wave-uniform
-__device__ __forceinline__ int wave_max_i(int v) {
-    v = max(v, dpp_i<0xB1>(v, v));
-    v = max(v, dpp_i<0x4E>(v, v));
-    v = max(v, dpp_i<0x141>(v, v));
-    v = max(v, dpp_i<0x140>(v, v));
-    v = max(v, dpp_i<0x142, 0xA>(v, v));
-    v = max(v, dpp_i<0x143, 0xC>(v, v));
-    return __builtin_amdgcn_readlane(v, 63);
-}
-
-// Softmax + top-K of one token in one wave, from its logits already in
-// registers (v[j] = entry lane + 64 j; entries at or past E are ignored): the
-// arithmetic of select_token_n (exp(x - max), the sum in double, probabilities
-// scaled by float(1/sum); the K largest in descending order, equal
-// probabilities to the lower index; weights p / max(sum of the K in double,
-// 6.103515625e-5)).  Probabilities are >= 0, so they are compared as ints (one
-// DPP max per step, no NaN canonicalisation); nothing branches per lane; ids
-// and weights stay in lane k until the end, written to LDS when `wr`.
-template <int NJ>
-__device__ __forceinline__ void select_fast(const float (&v)[4], int E, int K, int * s_ids, float * s_w, bool wr) {
-    const int lane = threadIdx.x & 63;
-    int mo = INT_MIN;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) mo = max(mo, lane + 64 * j < E ? f2o(v[j]) : INT_MIN);
-    const float mx = o2f(wave_max_i(mo));
-    float ev[NJ];
-    double ls = 0.0;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        ev[j] = lane + 64 * j < E ? expf(v[j] - mx) : 0.0f;
-        ls += (double)ev[j];
-    }
-    ls = wave_sum_dpp(ls);
-    const float inv = (float)(1.0 / ls);
-    int q[NJ];                  // probabilities as ints; -1: absent or taken
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) q[j] = lane + 64 * j < E ? __float_as_int(__fmul_rn(ev[j], inv)) : -1;
-    int myid = 0, mysel = 0;
-    for (int k = 0; k < K; ++k) {
-        int m = q[0];
-#pragma unroll
-        for (int j = 1; j < NJ; ++j) m = max(m, q[j]);
-        m = wave_max_i(m);
-        int e = -1;             // the lowest index holding m
-#pragma unroll
-        for (int j = NJ - 1; j >= 0; --j) {
-            const uint64_t b = __ballot(q[j] == m);
-            e = b ? 64 * j + (int)__builtin_ctzll(b) : e;
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) q[j] = lane + 64 * j == e ? -1 : q[j];
-        myid = lane == k ? e : myid;
-        mysel = lane == k ? m : mysel;
-    }
-    double sum = 0.0;
-    for (int k = 0; k < K; ++k) sum += (double)__int_as_float(__builtin_amdgcn_readlane(mysel, k));
-    float sf = (float)sum;
-    if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
-    if (wr && lane < K) {
-        s_ids[lane] = myid;
-        s_w[lane] = __int_as_float(mysel) / sf;
-    }
-}
-
 // The group record g, or an empty group when g is past the call's groups.
 // Validated so that no field can send a load or store out of bounds: member
 // count <= min(T, DEC_MAXT) and members < P, else the group is emptied; a
 // tier other than 0/1 or an index outside its pool makes the group invalid
-// (tier 2: its members contribute zeros, their combine still counts).
+// (tier 2: its members contribute zeros).
 __device__ __forceinline__ GroupInfo validate_group(const DecParams & p, GroupInfo gi, int ng, int g) {
     const int P = p.T * p.top_k;
     bool ok = g < ng;
@@ -406,188 +361,87 @@ __device__ __forceinline__ GroupInfo validate_group(const DecParams & p, GroupIn
     return gi;
 }
 
-// ---------------------------------------------------------------- B / C
-
-__device__ __forceinline__ int ld_coh_i(const int * q) {
-    return __hip_atomic_load(const_cast<int *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Thread 0 waits until the write-once flag is set (polling with a short
-// sleep; the counters themselves are only touched by their arrivals), or
-// until the wall-clock bound passes; the result is broadcast.
-__device__ bool wait_flag(const DecParams & p, const int * flag, int * s_flag) {
-    if (threadIdx.x == 0) {
-        int ok = 1;
-        const long long t0 = wall_clock64();
-        while (ld_coh_i(flag) == 0) {
-            if (wall_clock64() - t0 > p.spin_limit) {
-                ok = 0;
-                __hip_atomic_store(&p.ctl->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(4);
-        }
-        *s_flag = ok;
-    }
-    __syncthreads();
-    return *s_flag != 0;
-}
-
-// Wave 0 waits until all n write-once flags are set (each lane polls its
-// share with coherent loads; a wave vote decides), or until the wall-clock
-// bound passes (the error word is set); the result is broadcast.  The flags
-// are distinct words written by distinct workgroups: no atomic, so no
-// contention on one address.
-__device__ bool wait_all(const DecParams & p, const int * flags, int n, int * s_flag) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        int ok = 1;
-        const long long t0 = wall_clock64();
-        while (true) {
-            bool mine = true;
-            for (int i = lane; i < n; i += 64) mine = mine && ld_coh_i(flags + i) != 0;
-            if (__all(mine)) break;
-            if (wall_clock64() - t0 > p.spin_limit) {
-                ok = 0;
-                if (lane == 0) __hip_atomic_store(&p.ctl->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (lane == 0) *s_flag = ok;
-    }
-    __syncthreads();
-    return *s_flag != 0;
-}
-
-// thread 0: one arrival on `ctr`; the arrival that completes `target` sets
-// the flag (after this workgroup's coherent stores have completed)
-__device__ __forceinline__ void arrive_flag(int * ctr, int target, int * flag) {
-    if (threadIdx.x == 0 && atomicAdd(ctr, 1) == target - 1)
-        __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-constexpr int MAXPER_DEC = 8;
-
-struct Staged {
-    u32x4 r[MAXPER_DEC];
-};
-
-// loads of `nch` 16-byte chunks (issued now, stored to LDS later); lanes
-// past the end re-read the last chunk so the loads carry no condition
-__device__ __forceinline__ void stage_load(Staged & s, const u32x4 * g, int nch) {
-    if (nch > 0) {
-#pragma unroll
-        for (int k = 0; k < MAXPER_DEC; ++k) s.r[k] = g[min((int)threadIdx.x + k * WG, nch - 1)];
-    }
-}
-__device__ __forceinline__ void stage_store(const Staged & s, const u32x4 * g, int nch, uint8_t * smem, int at) {
-    if (nch > 0) {
-#pragma unroll
-        for (int k = 0; k < MAXPER_DEC; ++k) {
-            const int i = threadIdx.x + k * WG;
-            if (i < nch) *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = s.r[k];
-        }
-    }
-    for (int i = threadIdx.x + MAXPER_DEC * WG; i < nch; i += WG) *reinterpret_cast<u32x4 *>(smem + at + 16 * i) = g[i];
-}
-
-constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
-static_assert(TAB_CHUNKS % WG == 0, "codebook chunks per thread");
-constexpr int GU_LOADS = 7;     // 16-byte loads per thread issued for one gate_up item (16 rows <= 1792 B)
-constexpr int DN_LOADS = 4;     // ... for one down item (32 rows <= 512 B)
-constexpr int COL_LOADS = 2;    // ... for one quantised token column, issued early (the rest later)
-constexpr int DEC_MAXI = 16;    // items one workgroup may take (the grid is sized for it)
-
-// One work item of the gate_up or down kernel: `rows` weight rows from r0 of
-// one expert group's slab.  Its bytes are `nch` 16-byte chunks from src (row
-// r0 at byte `off` of the first chunk).  An item without weights to read
-// (past the call's items, or an invalid group) reads one chunk of a valid
-// dummy address so that its loads, like every other, are unconditional.
-struct DecItem {
-    GroupInfo gi;
-    const u32x4 * src;
-    int nch, off, r0, rows, rb;
-    int valid;                  // tier 0/1 with members: weights to dot (an int: a struct copy then
-                                // moves no sub-dword padding through scratch)
-};
-
-__device__ __forceinline__ DecItem dec_item(const DecParams & p, const GroupInfo * grp, int ng, int it, int nrb,
-                                            int rows_per, int n_rows, int d_in, int ht, int ct, const uint8_t * hot,
-                                            uint64_t hs, const uint8_t * cold, uint64_t cs) {
-    DecItem r;
-    const int g = it / nrb, rbi = it - g * nrb;
-    r.gi = validate_group(p, grp[max(0, min(g, DEC_PMAX - 1))], ng, g);
-    r.valid = r.gi.tier < 2 && r.gi.n_mem > 0;
-    const int wtype = r.gi.tier == 0 ? ht : ct;
-    r.r0 = rbi * rows_per;
-    r.rows = min(rows_per, n_rows - r.r0);
-    r.rb = (d_in / blk_elems(wtype)) * blk_bytes(wtype);
-    const uint64_t start = (uint64_t)r.r0 * r.rb;
-    r.off = (int)(start & 15);
-    if (r.valid) {
-        const uint8_t * W = group_slab(r.gi.tier, r.gi.idx, hot, hs, cold, cs);
-        r.src = reinterpret_cast<const u32x4 *>(W) + (start >> 4);
-        r.nch = (int)(((start + (uint64_t)r.rows * r.rb + 15) >> 4) - (start >> 4));
-    } else {
-        r.src = reinterpret_cast<const u32x4 *>(p.logits);
-        r.nch = 1;
-    }
-    return r;
-}
+// ------------------------------------------------------------- staging
 
 template <int N>
 struct Regs {
     u32x4 r[N];
 };
-template <int N>
-__device__ __forceinline__ void item_load(Regs<N> & s, const DecItem & it) {
-#pragma unroll
-    for (int k = 0; k < N; ++k) s.r[k] = it.src[min((int)threadIdx.x + k * WG, it.nch - 1)];
+
+// `rows` rows of one expert's slab from row r0: `nch` 16-byte chunks from
+// `src` (row r0 at byte `off` of the first chunk).  Without weights to read
+// (an invalid group, or past the workgroup's items) one chunk of a valid
+// dummy address, so that its loads, like every other, are unconditional.
+struct Span {
+    const u32x4 * src;
+    int nch, off, rb;
+    int valid;                  // tier 0/1 with members
+};
+
+__device__ __forceinline__ Span make_span(const GroupInfo & gi, int r0, int rows, int d_in, int ht, int ct,
+                                          const uint8_t * hot, uint64_t hs, const uint8_t * cold, uint64_t cs,
+                                          const void * dummy) {
+    Span s;
+    s.valid = gi.tier < 2 && gi.n_mem > 0;
+    const int wt = gi.tier == 0 ? ht : ct;
+    s.rb = (d_in / blk_elems(wt)) * blk_bytes(wt);
+    const uint64_t start = (uint64_t)r0 * s.rb;
+    s.off = (int)(start & 15);
+    if (s.valid) {
+        s.src = reinterpret_cast<const u32x4 *>(group_slab(gi.tier, gi.idx, hot, hs, cold, cs)) + (start >> 4);
+        s.nch = (int)(((start + (uint64_t)rows * s.rb + 15) >> 4) - (start >> 4));
+    } else {
+        s.src = reinterpret_cast<const u32x4 *>(dummy);
+        s.nch = 1;
+    }
+    return s;
 }
-// the item's chunks into LDS from 0 (chunks past N per thread: loaded here)
+
 template <int N>
-__device__ __forceinline__ void item_store(const Regs<N> & s, const DecItem & it, uint8_t * smem) {
+__device__ __forceinline__ void span_load(Regs<N> & s, const Span & sp) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) s.r[k] = sp.src[min((int)threadIdx.x + k * WG, sp.nch - 1)];
+}
+// the span's chunks into LDS at `dst` (chunks past N per thread: loaded here)
+template <int N>
+__device__ __forceinline__ void span_store(const Regs<N> & s, const Span & sp, uint8_t * dst) {
 #pragma unroll
     for (int k = 0; k < N; ++k) {
         const int i = threadIdx.x + k * WG;
-        if (i < it.nch) *reinterpret_cast<u32x4 *>(smem + 16 * i) = s.r[k];
+        if (i < sp.nch) *reinterpret_cast<u32x4 *>(dst + 16 * i) = s.r[k];
     }
-    for (int i = threadIdx.x + N * WG; i < it.nch; i += WG) *reinterpret_cast<u32x4 *>(smem + 16 * i) = it.src[i];
+    for (int i = threadIdx.x + N * WG; i < sp.nch; i += WG) *reinterpret_cast<u32x4 *>(dst + 16 * i) = sp.src[i];
 }
 
-// the workgroup's items: a contiguous range, so that consecutive items of a
-// workgroup are neighbouring row blocks of one expert
+// the workgroup's items: a contiguous range
 __device__ __forceinline__ void item_range(int n_items, int * i0, int * i1) {
     *i0 = (int)((int64_t)blockIdx.x * n_items / gridDim.x);
     *i1 = (int)((int64_t)(blockIdx.x + 1) * n_items / gridDim.x);
 }
 
-// Dots of one item's rows (staged in LDS at 0) against its members' columns
-// av[c], c < n_mem <= MT; the per-row sums are complete in lane lr == 0 of
-// the row.
+// Dots of the rows of a span staged at `sm` (one row per LPR lanes) against
+// the members' columns av[c], c < n_mem <= MT; the row sums are complete in
+// lane lr == 0 of the row.  Tier decides the format.
 template <int HT, int CT, int AM, int MT>
-__device__ __forceinline__ void item_dot(const uint8_t * smem, const DecItem & it, int d_in, const ActView * av,
-                                         float * acc, int grid_off) {
+__device__ __forceinline__ void rows_dot(const uint8_t * sm, int wb, int tier, int n_mem, int d_in, bool live,
+                                         const ActView * av, float * acc, int grid_off) {
     constexpr int LPR = Fmt<HT>::LPR;
-    const int rw = threadIdx.x / LPR, lr = threadIdx.x % LPR;
+    const int lr = threadIdx.x % LPR;
 #pragma unroll
     for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
-    const int n_mem = it.gi.n_mem;
-    if (it.valid && rw < it.rows) {
-        const int wb = it.off + rw * it.rb;
+    if (live) {
         const int U = d_in / Fmt<HT>::UNIT;
-        if (it.gi.tier == 0) {
-            if (MT == 1 || n_mem == 1) {    // one member: the single-column unit
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off);
+        if (tier == 0) {
+            if (MT == 1 || n_mem == 1) {
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(sm, wb, u, av, n_mem, acc, grid_off);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, MT>(smem, wb, u, av, n_mem, acc, grid_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, MT>(sm, wb, u, av, n_mem, acc, grid_off);
             }
         } else {
             if (MT == 1 || n_mem == 1) {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(smem, wb, u, av, n_mem, acc, grid_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(sm, wb, u, av, n_mem, acc, grid_off);
             } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, MT>(smem, wb, u, av, n_mem, acc, grid_off);
+                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, MT>(sm, wb, u, av, n_mem, acc, grid_off);
             }
         }
     }
@@ -597,194 +451,41 @@ __device__ __forceinline__ void item_dot(const uint8_t * smem, const DecItem & i
         for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
 }
 
-// out = sum_k w_k y_k in k order (llama-graph.cpp:1812-1840), the K outputs
-// loaded together (one round trip) before the ordered sum
-constexpr int DEC_KMAX = 16;
-__device__ __forceinline__ float combine_row(const float * y, const float * w, int K, int D) {
-    float yv[DEC_KMAX];
-#pragma unroll
-    for (int k = 0; k < DEC_KMAX; ++k) yv[k] = k < K ? ld_coh(y + (int64_t)k * D) : 0.0f;
-    float o = __fmul_rn(yv[0], w[0]);
-#pragma unroll
-    for (int k = 1; k < DEC_KMAX; ++k)
-        if (k < K) o = __fadd_rn(o, __fmul_rn(yv[k], w[k]));
-    return o;
-}
+// ---------------------------------------------------------------- B
 
-// The members' gate_up rows of group gi (loads only, unconditional: members
-// past n_mem and positions past d_in re-read valid entries).  SRC _COH: the
-// rows were written by other workgroups of the same kernel.
-template <int SRC, int MT>
-__device__ __forceinline__ void members_load(ActBatch (&ab)[MT], const DecParams & p, const GroupInfo & gi, int d_in) {
-    const int P = p.T * p.top_k, lane = threadIdx.x & 63, at0 = (threadIdx.x >> 6) * 64;
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-        const int m = max(0, min(member(gi, min(c, max(gi.n_mem - 1, 0))), P - 1));
-        const float * g = p.ygu + (int64_t)m * 2 * d_in;
-#pragma unroll
-        for (int j = 0; j < Q8_BATCH; ++j) {
-            const int pos = min(at0 + j * WG + lane, d_in - 1);
-            ab[c].g[j] = ld_src<SRC>(g + pos);
-            ab[c].u[j] = ld_src<SRC>(g + d_in + pos);
-        }
-    }
-}
-// GEGLU + q8 quantisation of the members' down activations into LDS (the
-// batch loaded by members_load; values past Q8_BATCH * WG are loaded here)
-template <int SRC, int AM, int MT>
-__device__ __forceinline__ void members_quant(uint8_t * smem, const ActView * av, const ActBatch (&ab)[MT],
-                                              const DecParams & p, const GroupInfo & gi, int d_in) {
-    const int at0 = (threadIdx.x >> 6) * 64;
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-        if (c < gi.n_mem) {
-            if (at0 < d_in) act_batch_quant<SRC, AM>(smem, av[c], ab[c], d_in, at0);
-            ActSrc src;
-            src.p = p.ygu + (int64_t)member(gi, c) * 2 * d_in;
-            src.n = d_in;
-            quantize_q8_32_rest<SRC, AM>(smem, av[c], src, d_in);
-        }
-    }
-}
+constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
+static_assert(TAB_CHUNKS % WG == 0, "codebook chunks per thread");
+constexpr int GU_HALF = 8;              // gate rows of an item (and as many up rows)
+constexpr int GU_LOADS = 4;             // 16-byte loads per thread and half issued ahead (8 rows <= 2048 B)
+constexpr int COL_LOADS = 2;            // quantised token column chunks per thread issued early
 
-constexpr int DEC_NARR = DEC_MAXI * DEC_MAXT;     // down-item arrivals one workgroup can make
-static_assert(DEC_NARR <= 64, "one wave compacts the arrivals");
-
-// The down items [i0, i1) of the call (32-row blocks of the groups' experts):
-// per group its members' GEGLU and down activation quantisation; per item the
-// down projection with the expert's .scale, the next item's slab loaded into
-// registers meanwhile; outputs per pair with coherent stores.  Then the
-// combine: one arrival per (member, item); the last arrival of a (token, row
-// block) writes the weighted sum of that token's top_k outputs for those
-// rows.  The first item's slab loads were issued by the caller (st, cur).
-// WAIT: the gate_up outputs come from the same kernel -- the done flags of
-// all of a group's gate_up items are awaited (bounded) before its members are
-// read; a wait that times out ends the loop (the error word is set).  Without
-// WAIT the caller has loaded the first group's members (ab) before the slab.
-// w: the routing weights [T][top_k] (LDS or global, as the caller has them).
-template <int HD, int CD, int AM, int SRC, int MT, bool WAIT>
-__device__ __forceinline__ void down_items(const DecParams & p, uint8_t * smem, const GroupInfo * grp, int ng, int i0, int i1,
-                           Regs<DN_LOADS> & st, DecItem cur, ActBatch (&ab)[MT], const float * w, int * s_arr,
-                           int * s_done, int * s_nd, int * s_flag) {
-    constexpr int LPR = Fmt<HD>::LPR, ROWS = WG / LPR;
-    static_assert(Fmt<HD>::LPR == Fmt<CD>::LPR && !k256<HD>() && !k256<CD>(), "down formats");
-    const int D = p.d_model, d_in = p.n_ff, K = p.top_k, nrb = p.n_rb_down;
-    const int nrb_gu = (2 * d_in + 15) / 16;
-    bool ok = true;
-    if (WAIT) {
-        ok = wait_all(p, p.gu_done + (i0 / nrb) * nrb_gu, nrb_gu, s_flag);
-        members_load<SRC, MT>(ab, p, cur.gi, d_in);
-    }
-    ActView tmp;
-    const int abytes = act_layout(d_in, 0, &tmp);
-    const int a0 = p.w_lds_dn;
-    ActView av[MT];
-#pragma unroll
-    for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + c * abytes, &av[c]);
-    members_quant<SRC, AM, MT>(smem, av, ab, p, cur.gi, d_in);
-
-    int n_arr = 0;
-    for (int it = i0; it < i1 && ok; ++it) {
-        __syncthreads();
-        item_store(st, cur, smem);
-        __syncthreads();
-        DecItem nxt = cur;
-        if (it + 1 < i1) {
-            nxt = dec_item(p, grp, ng, it + 1, nrb, ROWS, D, d_in, HD, CD, p.hot_dn, p.hot_dn_stride, p.cold_dn,
-                           p.cold_dn_stride);
-            item_load(st, nxt);
-        }
-        float acc[MT];
-        item_dot<HD, CD, AM, MT>(smem, cur, d_in, av, acc, 0);
-        const float sc = !cur.valid ? 0.0f
-                       : cur.gi.tier == 0 ? (p.s_hot ? p.s_hot[cur.gi.idx] : 1.0f)
-                                          : (p.s_cold ? p.s_cold[cur.gi.idx] : 1.0f);
-        const int rw = threadIdx.x / LPR, lr = threadIdx.x % LPR;
-        const int n_mem = cur.gi.n_mem;
-        if (lr == 0 && rw < cur.rows) {
-#pragma unroll
-            for (int c = 0; c < MT; ++c)
-                if (c < n_mem) st_coh(p.ydn + (int64_t)member(cur.gi, c) * D + cur.r0 + rw, cur.valid ? acc[c] * sc : 0.0f);
-        }
-        if ((int)threadIdx.x < n_mem && n_arr + n_mem <= DEC_NARR)
-            s_arr[n_arr + threadIdx.x] = (member(cur.gi, threadIdx.x) / K) * nrb + cur.r0 / ROWS;
-        n_arr = min(n_arr + n_mem, DEC_NARR);
-        if (it + 1 < i1 && (it + 1) / nrb != it / nrb) {
-            // the next item is another group's: its members' activations
-            __syncthreads();                  // every wave is done with these
-            if (WAIT) ok = wait_all(p, p.gu_done + ((it + 1) / nrb) * nrb_gu, nrb_gu, s_flag);
-            if (ok) {
-                members_load<SRC, MT>(ab, p, nxt.gi, d_in);
-                members_quant<SRC, AM, MT>(smem, av, ab, p, nxt.gi, d_in);
-            }
-        }
-        cur = nxt;
-    }
-
-    // combine: the arrivals (one atomic each, all in flight together), the
-    // completed ones compacted by one wave, then every row of every completed
-    // (token, row block) spread over the workgroup's threads
-    wait_vm();
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int a = threadIdx.x;
-        const bool last = a < n_arr && atomicAdd(&p.comb_count[s_arr[a]], 1) == K - 1;
-        const uint64_t m = __ballot(last);
-        if (last) s_done[__popcll(m & ((1ull << a) - 1))] = s_arr[a];
-        if (a == 0) *s_nd = __popcll(m);
-    }
-    __syncthreads();
-    const int nd = *s_nd;
-    for (int i = threadIdx.x; i < nd * ROWS; i += WG) {
-        const int a = i / ROWS, r = i - a * ROWS;
-        const int t = s_done[a] / nrb, r0 = (s_done[a] - t * nrb) * ROWS;
-        if (r0 + r < D)
-            p.out[(int64_t)t * D + r0 + r] = combine_row(p.ydn + (int64_t)t * K * D + r0 + r, w + t * K, K, D);
-    }
-}
-
-template <int SRC> struct CohSrc;
-template <> struct CohSrc<SRC_GEGLU_TABLE> { static constexpr int v = SRC_GEGLU_TABLE_COH; };
-template <> struct CohSrc<SRC_GEGLU_TANH> { static constexpr int v = SRC_GEGLU_TANH_COH; };
-
-// B: the routing, selected by every workgroup from the logits (softmax, top-k
-// with DPP wave reductions, ties to the lower index), grouped by expert
-// (decode once, dot N: the tokens that share an expert read its slab once),
-// each group's tier by the residency predicate (moert/cuda/ffn_moe.cu:80-130);
-// the first workgroup publishes ids, weights and groups.  Then a loop over the
-// workgroup's (group, 16-row block) items: the next item's slab is loaded into
-// registers while the current one is dotted from LDS against every member
-// token.  MT: members a group can have (min(T, DEC_MAXT); 1 or DEC_MAXT),
-// which bounds the columns loaded and dotted.
-//
-// FUSE: the down projection follows in the same kernel (HD, CD its formats,
-// GSRC its GEGLU source).  Each workgroup issues its first down item's slab
-// loads right after its first gate_up slab's, so they land while gate_up is
-// computed; gate_up outputs are stored with coherent stores and counted per
-// group (the arrival that completes a group sets its write-once ready flag);
-// then the workgroup's down items (down_items, waiting on those flags).  The
-// grid must not exceed the resident workgroups: every workgroup finishes all
-// of its gate_up items before it waits on anything, so every wait ends.
-template <int HT, int CT, int AM, int MT, bool FUSE, int HD, int CD, int GSRC>
+// B: the routing, selected by every workgroup from the logits, grouped by
+// expert, each group's tier by the residency predicate; the first workgroup
+// publishes ids, weights and groups.  Then the workgroup's items (group,
+// block j: gate rows 8 j .. 8 j + 7 and the up rows n_ff + 8 j .. paired with
+// them), one row per 16 lanes, the next item's loads in flight while the
+// current one is dotted; each item ends with GEGLU of gate row i with up row
+// i for every member, stored as fp32 down activations.  MT: members a group
+// can have (1 or DEC_MAXT).
+template <int HT, int CT, int AM, int MT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int LPR = Fmt<HT>::LPR, ROWS = WG / LPR;
-    static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
+    static_assert(Fmt<HT>::LPR == 16 && Fmt<CT>::LPR == 16 && k256<HT>() && k256<CT>(), "gate_up formats");
     constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
-    constexpr int ROWS_D = WG / Fmt<HD>::LPR;
     __shared__ int s_ids[DEC_PMAX];
     __shared__ float s_w[DEC_PMAX];
     __shared__ GroupInfo s_grp[DEC_PMAX];
     __shared__ int32_t s_res[3][256];       // exp_slot, slot_exp, slot_state
     __shared__ int s_ng;
-    __shared__ int s_arr[FUSE ? DEC_NARR : 1], s_done[FUSE ? DEC_NARR : 1], s_nd, s_flag;
+    __shared__ SelScratch s_sel[WG / 64];
+    __shared__ float s_y[2 * GU_HALF][MT];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int T = p.T, K = p.top_k, E = p.n_expert, d_in = p.d_model, F2 = 2 * p.n_ff;
+    const int T = p.T, K = p.top_k, E = p.n_expert, d_in = p.d_model, F = p.n_ff;
 
     // 1. every load of the prologue, in the order the data are needed and none
-    //    under a condition, so each wait below waits for its own loads only:
-    //    this wave's token's logits, the residency mirrors, the IQ2_S codebook,
-    //    every token's quantised column
+    //    under a condition: this wave's token's logits, the residency mirrors,
+    //    the IQ2_S codebook, every token's quantised column (the columns are
+    //    contiguous: xq_stride == their size)
     float lg[4];
     {
         const float * lt = p.logits + (int64_t)min(wave, T - 1) * E;
@@ -812,24 +513,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     }
     ActView tmp;
     const int abytes = act_layout(d_in, 0, &tmp), a16 = abytes / 16;
-    u32x4 col[MT][COL_LOADS];
+    const int ncol = min(T, MT) * a16;
+    const u32x4 * xq4 = reinterpret_cast<const u32x4 *>(p.xq);
+    u32x4 col[COL_LOADS * MT];
 #pragma unroll
-    for (int c = 0; c < MT; ++c) {
-        const u32x4 * src = reinterpret_cast<const u32x4 *>(p.xq + (int64_t)min(c, T - 1) * p.xq_stride);
-#pragma unroll
-        for (int k = 0; k < COL_LOADS; ++k) col[c][k] = src[min((int)threadIdx.x + k * WG, a16 - 1)];
-    }
+    for (int k = 0; k < COL_LOADS * MT; ++k) col[k] = xq4[min((int)threadIdx.x + k * WG, ncol - 1)];
 
     // 2. the routing: wave t < T selects token t (a wave past T repeats the
-    //    last token and writes nothing); then the expert groups.  The asm
-    //    statement uses every logits load on every path, so the compiler
-    //    cannot sink the loads an E <= 128 call leaves unused behind the later
-    //    loads.
+    //    last token and writes nothing); then the expert groups
     {
         asm volatile("" ::"v"(lg[2]), "v"(lg[3]));
         const int o = min(wave, T - 1) * K;
-        if (E <= 128) select_fast<2>(lg, E, K, s_ids + o, s_w + o, wave < T);
-        else select_fast<4>(lg, E, K, s_ids + o, s_w + o, wave < T);
+        if (E <= 128) select_topk<2>(lg, E, K, s_ids + o, s_w + o, wave < T, s_sel[wave]);
+        else select_topk<4>(lg, E, K, s_ids + o, s_w + o, wave < T, s_sel[wave]);
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) s_res[i][threadIdx.x] = res[i];
@@ -837,28 +533,30 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     if (wave == 0) build_groups(p, s_ids, s_grp, &s_ng, s_res[0], s_res[1], s_res[2]);
     __syncthreads();
     const int ng = max(0, min(s_ng, DEC_PMAX));
-    const int NRB = (F2 + ROWS - 1) / ROWS;
+    const int NB = F / GU_HALF;
     int i0, i1;
-    item_range(ng * NRB, &i0, &i1);
+    item_range(ng * NB, &i0, &i1);
 
-    // 3. the first item's slab loads (a dummy one when there is none); fused:
-    //    the first down item (its loads go out once this slab has landed, so
-    //    they overlap the gate_up dots instead of sharing HBM with this slab)
-    DecItem cur = dec_item(p, s_grp, ng, i0, NRB, ROWS, F2, d_in, HT, CT, p.hot_gu, p.hot_gu_stride, p.cold_gu,
-                           p.cold_gu_stride);
-    Regs<GU_LOADS> st;
-    item_load(st, cur);
-    int d0 = 0, d1 = 0;
-    DecItem dcur;
-    Regs<DN_LOADS> dst;
-    if (FUSE) {
-        item_range(ng * p.n_rb_down, &d0, &d1);
-        dcur = dec_item(p, s_grp, ng, d0, p.n_rb_down, ROWS_D, p.d_model, p.n_ff, HD, CD, p.hot_dn,
-                        p.hot_dn_stride, p.cold_dn, p.cold_dn_stride);
+    // 3. the first item's loads (both halves)
+    auto item_group = [&](int it) {
+        const int g = it / NB;
+        return validate_group(p, s_grp[max(0, min(g, DEC_PMAX - 1))], ng, g);
+    };
+    auto half_span = [&](const GroupInfo & gi, int it, int h) {
+        return make_span(gi, h * F + GU_HALF * (it % NB), GU_HALF, d_in, HT, CT, p.hot_gu, p.hot_gu_stride,
+                         p.cold_gu, p.cold_gu_stride, p.logits);
+    };
+    GroupInfo gcur = item_group(i0);
+    Span sp[2];
+    Regs<GU_LOADS> st[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        sp[h] = half_span(gcur, i0, h);
+        span_load(st[h], sp[h]);
     }
 
     // 4. the first workgroup publishes the routing; the codebook and the
-    //    columns land in LDS
+    //    columns land in LDS (after the two halves: at a0)
     if (blockIdx.x == 0) {
         if ((int)threadIdx.x < T * K) {
             p.ids[threadIdx.x] = s_ids[threadIdx.x];
@@ -868,19 +566,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         if (threadIdx.x == 0) p.ctl->n_groups = ng;
         count_routes(p, s_ids, s_grp, ng);
     }
-    const int a0 = p.w_lds_gu;
+    const int a0 = 2 * p.w_lds_gu;
 #pragma unroll
-    for (int c = 0; c < MT; ++c) {
-        if (c >= T) break;
-        uint8_t * dst8 = smem + a0 + c * abytes;
-#pragma unroll
-        for (int k = 0; k < COL_LOADS; ++k) {
-            const int i = threadIdx.x + k * WG;
-            if (i < a16) reinterpret_cast<u32x4 *>(dst8)[i] = col[c][k];
-        }
-        const u32x4 * src = reinterpret_cast<const u32x4 *>(p.xq + (int64_t)c * p.xq_stride);
-        for (int i = threadIdx.x + COL_LOADS * WG; i < a16; i += WG) reinterpret_cast<u32x4 *>(dst8)[i] = src[i];
+    for (int k = 0; k < COL_LOADS * MT; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < ncol) reinterpret_cast<u32x4 *>(smem + a0)[i] = col[k];
     }
+    for (int i = threadIdx.x + COL_LOADS * MT * WG; i < ncol; i += WG) reinterpret_cast<u32x4 *>(smem + a0)[i] = xq4[i];
     const int grid_off = align16i(a0 + min(T, DEC_MAXT) * abytes);
     if (IQ2) {
 #pragma unroll
@@ -889,353 +581,474 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     }
 
     // 5. the items
-    ActView av[MT];
-    uint32_t sink = 0;
+    const int row = threadIdx.x >> 4, h = row >> 3;          // h 0: gate rows, 1: up rows
     for (int it = i0; it < i1; ++it) {
-        __syncthreads();                      // the previous item's dots are done with LDS
-        item_store(st, cur, smem);
+        const GroupInfo gi = gcur;
+        ActView av[MT];
+#pragma unroll
+        for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + max(0, min(member(gi, c) / K, T - 1)) * abytes, &av[c]);
+        __syncthreads();                      // the previous item is done with LDS
+        span_store(st[0], sp[0], smem);
+        span_store(st[1], sp[1], smem + p.w_lds_gu);
         __syncthreads();
-        if (FUSE && it == i0) item_load(dst, dcur);
-        DecItem nxt = cur;
+        // (no array indexed by a per-lane value: that would live in scratch)
+        const int wb = h ? p.w_lds_gu + sp[1].off + (row & 7) * sp[1].rb : sp[0].off + (row & 7) * sp[0].rb;
+        const bool live = sp[0].valid != 0;
         if (it + 1 < i1) {
-            nxt = dec_item(p, s_grp, ng, it + 1, NRB, ROWS, F2, d_in, HT, CT, p.hot_gu, p.hot_gu_stride, p.cold_gu,
-                           p.cold_gu_stride);
-            item_load(st, nxt);               // in flight during this item's dots
-        }
-        // down kernel only: touch this item's share of its expert's down slab
-        // (one 16-byte load per 128-byte line; unconditional, the index
-        // clamped) so the down kernel's loads find it in L2/MALL; issued
-        // after this item's slab has landed, it overlaps the dots below
-        if (!FUSE && p.prefetch_dn) {
-            const DecItem pf = dec_item(p, s_grp, ng, (int)((int64_t)it * p.n_rb_down / NRB), p.n_rb_down,
-                                        WG / Fmt<HD>::LPR, p.d_model, p.n_ff, p.hot_dn_type, p.cold_dn_type, p.hot_dn,
-                                        p.hot_dn_stride, p.cold_dn, p.cold_dn_stride);
-            sink ^= pf.src[min(8 * (int)threadIdx.x, pf.nch - 1)].x;
-        }
-        // member c's column is its token's
+            gcur = item_group(it + 1);
 #pragma unroll
-        for (int c = 0; c < MT; ++c)
-            act_layout(d_in, a0 + max(0, min(member(cur.gi, c) / K, T - 1)) * abytes, &av[c]);
+            for (int k = 0; k < 2; ++k) {
+                sp[k] = half_span(gcur, it + 1, k);
+                span_load(st[k], sp[k]);      // in flight during this item's dots
+            }
+        }
         float acc[MT];
-        item_dot<HT, CT, AM, MT>(smem, cur, d_in, av, acc, grid_off);
-        const int rw = threadIdx.x / LPR, lr = threadIdx.x % LPR;
-        if (lr == 0 && rw < cur.rows && cur.valid) {
+        rows_dot<HT, CT, AM, MT>(smem, wb, gi.tier, gi.n_mem, d_in, live, av, acc, grid_off);
+        if ((threadIdx.x & 15) == 0) {
 #pragma unroll
-            for (int c = 0; c < MT; ++c)
-                if (c < cur.gi.n_mem) {
-                    float * y = p.ygu + (int64_t)member(cur.gi, c) * F2 + cur.r0 + rw;
-                    if (FUSE) st_coh(y, acc[c]);
-                    else *y = acc[c];
-                }
+            for (int c = 0; c < MT; ++c) s_y[row][c] = acc[c];
         }
-        cur = nxt;
-    }
-    if (!FUSE) {
-        if (p.never) p.ygu[threadIdx.x] = (float)sink;      // keeps the touch loads alive
-        return;
-    }
-
-    // 6. fused: each gate_up item's done flag (item index = group * NRB +
-    //    row block), once this workgroup's coherent stores have completed
-    wait_vm();
-    __syncthreads();
-    if ((int)threadIdx.x < i1 - i0)
-        __hip_atomic_store(p.gu_done + i0 + threadIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (i0 >= i1) item_load(dst, dcur);       // no gate_up item: the first down slab was not loaded yet
-    // 7. the down items (the LDS of the gate_up items is free again)
-    if (d0 < d1) {
-        ActBatch ab[MT];
-        down_items<HD, CD, AM, CohSrc<GSRC>::v, MT, true>(p, smem, s_grp, ng, d0, d1, dst, dcur, ab, s_w, s_arr,
-                                                          s_done, &s_nd, &s_flag);
+        __syncthreads();
+        // GEGLU of gate row 8 j + i with up row n_ff + 8 j + i, member c
+        if (live && (int)threadIdx.x < GU_HALF * MT) {
+            const int i = threadIdx.x & (GU_HALF - 1), c = threadIdx.x / GU_HALF;
+            if (c < gi.n_mem) {
+                const int pair = max(0, min(member(gi, c), T * K - 1));
+                p.ya[(int64_t)pair * F + GU_HALF * (it % NB) + i] = geglu1<GSRC>(s_y[i][c], s_y[GU_HALF + i][c]);
+            }
+        }
     }
 }
 
-// C: the down items of the gate_up kernel's groups, as a kernel of its own.
-template <int HT, int CT, int AM, int GSRC, int MT>
+// ---------------------------------------------------------------- C
+
+constexpr int DN_LPR = 16;      // lanes per row: lane l holds the row's block pair l (blocks 2 l, 2 l + 1)
+constexpr int DN_RPP = WG / DN_LPR;   // rows per pass
+constexpr int DN_QP = 8;        // pairs quantised per pass (fp32 activations in)
+constexpr int DN_GRP_NPS = 2;   // passes of 16 rows of a down-by-group workgroup (4 measured slower)
+constexpr int DN_GRP_ROWS = DN_GRP_NPS * DN_RPP;
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+// per-group state of the down kernel, in LDS.  The slab is kept as a byte
+// offset into its pool, not as a pointer: a pointer read back from LDS is
+// generic, and loads through it would be flat loads, which also count on the
+// LDS counter (every LDS wait would then wait for them).
+struct DnGroup {
+    int tier, n_mem, pad0, pad1;
+    int mem[DEC_MAXT];
+    float scale;
+    int rb;                     // bytes per row
+    uint64_t row0;              // byte offset of this block's first row in the pool (tier 0 hot, else cold)
+};
+
+// one block pair of a down row (Q5_0: 44 bytes, IQ4_NL: 36), loaded as dwords
+// from a 4-aligned address
+struct DnPair {
+    uint32_t w[11];
+};
+
+template <int T>
+__device__ __forceinline__ void dn_pair_load(DnPair & q, const uint8_t * src) {
+    const u32x4a * s4 = reinterpret_cast<const u32x4a *>(src);
+    const u32x4a a = s4[0], b = s4[1];
+    q.w[0] = a.x; q.w[1] = a.y; q.w[2] = a.z; q.w[3] = a.w;
+    q.w[4] = b.x; q.w[5] = b.y; q.w[6] = b.z; q.w[7] = b.w;
+    const uint32_t * s1 = reinterpret_cast<const uint32_t *>(src + 32);
+    if constexpr (T == T_Q5_0) {
+        q.w[8] = s1[0]; q.w[9] = s1[1]; q.w[10] = s1[2];
+    } else {
+        q.w[8] = s1[0]; q.w[9] = 0u; q.w[10] = 0u;
+    }
+}
+
+// the member activation's 32-block b from LDS: 32 int8 values, its scale
+// (and q8_1 sum)
+struct Act32 {
+    u32x4 lo, hi;
+    float d, s;
+};
+template <int AM>
+__device__ __forceinline__ Act32 act32(const uint8_t * smem, const ActView & av, int b) {
+    Act32 a;
+    const int ao = av.q + qpos(32 * b);
+    a.lo = lds128(smem, ao);
+    a.hi = lds128(smem, ao + 16);
+    a.d = reinterpret_cast<const float *>(smem + av.d32)[b];
+    a.s = AM == AM_CPU ? 0.0f : reinterpret_cast<const float *>(smem + av.s32)[b];
+    return a;
+}
+
+// Q5_0 . q8_0 (ggml-cpu/quants.c:314-352):  d_w d8 sum (q - 16) a
+// Q5_0 . q8_1 (ggml-cuda/vecdotq.cuh:172-198): d_w (d8 sum q a - 16 s8)
+// block h (0, 1) of the pair
+template <int AM>
+__device__ __forceinline__ float q5_0_block(const DnPair & q, int h, const Act32 & a) {
+    uint32_t d16, qh, qs[4];
+    if (h == 0) {
+        d16 = q.w[0] & 0xFFFF;
+        qh = __builtin_amdgcn_alignbit(q.w[1], q.w[0], 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[2 + i], q.w[1 + i], 16);
+    } else {
+        d16 = q.w[5] >> 16;
+        qh = q.w[6];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = q.w[7 + i];
+    }
+    const uint32_t al[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w}, ah[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+    int sumi = 0, suma = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t vh0 = qh >> (4 * i), vh1 = qh >> (16 + 4 * i);
+        uint32_t v0 = qs[i] & 0x0F0F0F0Fu;
+        v0 |= (vh0 << 4) & 0x10u; v0 |= (vh0 << 11) & 0x1000u; v0 |= (vh0 << 18) & 0x100000u; v0 |= (vh0 << 25) & 0x10000000u;
+        uint32_t v1 = (qs[i] >> 4) & 0x0F0F0F0Fu;
+        v1 |= (vh1 << 4) & 0x10u; v1 |= (vh1 << 11) & 0x1000u; v1 |= (vh1 << 18) & 0x100000u; v1 |= (vh1 << 25) & 0x10000000u;
+        sumi = dot4((int)v0, (int)al[i], sumi);
+        sumi = dot4((int)v1, (int)ah[i], sumi);
+        if (AM == AM_CPU) {
+            suma = dot4(0x01010101, (int)al[i], suma);
+            suma = dot4(0x01010101, (int)ah[i], suma);
+        }
+    }
+    const float d = h2f(d16);
+    if (AM == AM_CPU) return __fmul_rn(d * a.d, (float)(sumi - 16 * suma));
+    return d * ((float)sumi * a.d - 16.0f * a.s);
+}
+
+// IQ4_NL . q8_0 (ggml-cpu/quants.c:1203-1228) and . q8_1 (vecdotq.cuh:1270-1289):
+//   d_w d8 sum kvalues[q] a
+template <int AM>
+__device__ __forceinline__ float iq4nl_block(const DnPair & q, int h, const Act32 & a) {
+    uint32_t d16, qs[4];
+    if (h == 0) {
+        d16 = q.w[0] & 0xFFFF;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[1 + i], q.w[i], 16);
+    } else {
+        d16 = q.w[4] >> 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = q.w[5 + i];
+    }
+    const uint32_t al[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w}, ah[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+    int sumi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sumi = dot4((int)iq4nl_lookup(qs[i] & 0x0F0F0F0Fu), (int)al[i], sumi);
+        sumi = dot4((int)iq4nl_lookup((qs[i] >> 4) & 0x0F0F0F0Fu), (int)ah[i], sumi);
+    }
+    const float d = h2f(d16);
+    if (AM == AM_CPU) return __fmul_rn(a.d * d, (float)sumi);
+    return (d * a.d) * (float)sumi;
+}
+
+// max over each group of 8 lanes (lanes 8 m .. 8 m + 7), in every lane of it
+__device__ __forceinline__ float oct_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));        // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v, v));        // quad_perm [2,3,0,1]
+    v = fmaxf(v, __shfl_xor(v, 4, 8));
+    return v;
+}
+
+// q8 of one 32-block held as 4 values per lane by 8 consecutive lanes, into
+// a column at `col` (layout L): q8_0 as the x86 CPU build computes it
+// (arch/x86/quants.c:302-360: d = amax / 127 stored as fp16, q =
+// round-to-nearest-even(x 127 / amax)) or q8_1 (ggml-cuda quantize.cu:5-50:
+// q = roundf(x / d), and the block sum, stored as fp16).  `c4` is the index
+// of the lane's 4 values in the column.
+template <int AM>
+__device__ __forceinline__ void q8_quad(uint8_t * col, const ActView & L, const float (&v)[4], int c4, bool live) {
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float amax = oct_max(m);
+    int q[4];
+    float dstore, sstore = 0.0f;
+    if (AM == AM_CPU) {
+        const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (int)rintf(__fmul_rn(v[j], id));
+            q[j] = r > 127 ? 127 : (r < -128 ? -128 : r);
+        }
+        dstore = round_to_half(amax / 127.f);
+    } else {
+        const float d = amax / 127.0f;
+        float s = __fadd_rn(__fadd_rn(v[0], v[1]), __fadd_rn(v[2], v[3]));
+        s = __fadd_rn(s, dpp_f<0xB1>(0.0f, s));
+        s = __fadd_rn(s, dpp_f<0x4E>(0.0f, s));
+        s = __fadd_rn(s, __shfl_xor(s, 4, 8));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = amax == 0.0f ? 0 : (int)roundf(v[j] / d);
+        dstore = round_to_half(d);
+        sstore = round_to_half(s);
+    }
+    if (live) {
+        const uint32_t w = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
+                           ((uint32_t)(q[3] & 0xFF) << 24);
+        *reinterpret_cast<uint32_t *>(col + L.q + qpos(4 * c4)) = w;
+        if ((c4 & 7) == 0) {
+            reinterpret_cast<float *>(col + L.d32)[c4 >> 3] = dstore;
+            if (AM != AM_CPU) reinterpret_cast<float *>(col + L.s32)[c4 >> 3] = sstore;
+        }
+    }
+}
+
+// C: output rows [r0, r0 + R) of every token, r0 = blockIdx.x R, R =
+// 2^dn_rows_log2.  First, with no dependence on anything, the loads of the
+// pairs' down activations (the pairs are 0 .. T top_k - 1 whatever the
+// grouping) and of the groups' records and routing weights (from B's first
+// workgroup); then a table of the groups (tier, members, .scale, where this
+// block's rows start in the pool).  The weights never pass through LDS: each
+// row's lanes load its block pairs straight into registers (lane l: blocks
+// 2 l, 2 l + 1, dword-aligned), the next pass's rows in flight while the
+// current ones are dotted against the members' activations, which are in
+// LDS, quantised here from B's fp32 GEGLU outputs (8 lanes a 32-block).  Each row is scaled by the expert's
+// .scale into s_y[pair][row]; then each (token, row) output is the sum of
+// w_k y_k in k order.  Invalid groups leave their pairs at zero.
+template <int HD, int CD, int AM, int MT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_down(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int ROWS = WG / Fmt<HT>::LPR;
-    __shared__ GroupInfo s_grp[DEC_PMAX];
-    __shared__ int s_arr[DEC_NARR], s_done[DEC_NARR];
-    __shared__ int s_ng, s_nd, s_flag;
-    const int nrb = p.n_rb_down;
-    // the call's groups, written by B's first workgroup
+    static_assert(!k256<HD>() && !k256<CD>(), "down formats");
+    __shared__ DnGroup s_gi[DEC_PMAX];
+    __shared__ float s_wt[DEC_PMAX];
+    __shared__ float s_y[DEC_PMAX][DEC_DN_MAXR];
+    __shared__ int s_ng;
+    const int D = p.d_model, F = p.n_ff, K = p.top_k, T = p.T, P = T * K;
+    const int lg2r = p.dn_rows_log2, R = 1 << lg2r, r0 = blockIdx.x << lg2r, nr = max(0, min(R, D - r0));
+    ActView L;
+    const int abytes = act_layout(F, 0, &L);
+    const int F4 = F / 4;                                     // 16-byte chunks of one pair's fp32 activation
+    const int NP = F / 64;                                    // block pairs per row
+
+    // 1. the activations' first loads, then the records
+    const u32x4 * ya4 = reinterpret_cast<const u32x4 *>(p.ya);
+    u32x4 act[DN_QP];
+#pragma unroll
+    for (int q = 0; q < DN_QP; ++q) act[q] = ya4[(int64_t)min(q, P - 1) * F4 + min((int)threadIdx.x, F4 - 1)];
     {
-        constexpr int GW = (int)(sizeof(GroupInfo) / 4) * DEC_PMAX;
-        static_assert(GW % WG == 0, "group words per thread");
-        const int * gsrc = reinterpret_cast<const int *>(p.ctl->groups);
-        int v[GW / WG];
-#pragma unroll
-        for (int k = 0; k < GW / WG; ++k) v[k] = gsrc[threadIdx.x + k * WG];
+        const GroupInfo gi_in = p.ctl->groups[min((int)threadIdx.x, DEC_PMAX - 1)];
         const int ngv = p.ctl->n_groups;
-#pragma unroll
-        for (int k = 0; k < GW / WG; ++k) reinterpret_cast<int *>(s_grp)[threadIdx.x + k * WG] = v[k];
+        const float wv = p.w[min((int)threadIdx.x, P - 1)];
         if (threadIdx.x == 0) s_ng = ngv;
+        if ((int)threadIdx.x < DEC_PMAX) s_wt[threadIdx.x] = (int)threadIdx.x < P ? wv : 0.0f;
+        for (int i = threadIdx.x; i < P * DEC_DN_MAXR; i += WG) (&s_y[0][0])[i] = 0.0f;
+        __syncthreads();
+        const int ng = max(0, min(s_ng, DEC_PMAX));
+        if ((int)threadIdx.x < ng) {
+            const GroupInfo gi = validate_group(p, gi_in, ng, threadIdx.x);
+            DnGroup d;
+            d.tier = gi.tier;
+            d.n_mem = gi.tier < 2 ? gi.n_mem : 0;
+            d.pad0 = d.pad1 = 0;
+#pragma unroll
+            for (int c = 0; c < DEC_MAXT; ++c) d.mem[c] = gi.mem[c];
+            d.scale = gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f)
+                                   : (gi.tier == 1 ? (p.s_cold ? p.s_cold[gi.idx] : 1.0f) : 0.0f);
+            const int wt = gi.tier == 0 ? HD : CD;
+            d.rb = (F / 32) * blk_bytes(wt);
+            d.row0 = d.n_mem > 0 ? (gi.tier == 0 ? (uint64_t)gi.idx * p.hot_dn_stride : (uint64_t)gi.idx * p.cold_dn_stride) +
+                                       (uint64_t)r0 * d.rb
+                                 : 0;
+            s_gi[threadIdx.x] = d;
+        }
     }
     __syncthreads();
     const int ng = max(0, min(s_ng, DEC_PMAX));
-    int i0, i1;
-    item_range(ng * nrb, &i0, &i1);
-    if (i0 >= i1) return;
-    // the first group's members, then the first item's slab: the members'
-    // GEGLU and quantisation run while the slab is in flight
-    DecItem cur = dec_item(p, s_grp, ng, i0, nrb, ROWS, p.d_model, p.n_ff, HT, CT, p.hot_dn, p.hot_dn_stride, p.cold_dn,
-                           p.cold_dn_stride);
-    ActBatch ab[MT];
-    members_load<GSRC, MT>(ab, p, cur.gi, p.n_ff);
-    Regs<DN_LOADS> st;
-    item_load(st, cur);
-    down_items<HT, CT, AM, GSRC, MT, false>(p, smem, s_grp, ng, i0, i1, st, cur, ab, p.w, s_arr, s_done, &s_nd,
-                                            &s_flag);
+    const int rows = ng << lg2r, passes = (rows + DN_RPP - 1) / DN_RPP;
+    const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
+    const int pl = min(lane16, NP - 1);
+
+    // the block pair of this lane in pass `ps` (a clamped, valid address when
+    // the lane has none)
+    auto pair_src = [&](int ps, int * kind) {
+        const int k = ps * DN_RPP + lrow, s = min(k >> lg2r, max(ng - 1, 0)), r = min(k & (R - 1), max(nr - 1, 0));
+        const DnGroup & d = s_gi[s];
+        *kind = d.tier == 0 ? 0 : 1;
+        const uint8_t * base = d.tier == 0 ? p.hot_dn : p.cold_dn;
+        return base + d.row0 + (uint64_t)r * d.rb + (uint64_t)pl * (blk_bytes(d.tier == 0 ? HD : CD) * 2);
+    };
+    DnPair cur, nxt;
+    int kc = 0, kn = 0;
+    auto load = [&](DnPair & q, int ps, int * kind) {
+        const uint8_t * src = pair_src(ps, kind);
+        if (*kind == 0) dn_pair_load<HD>(q, src);
+        else dn_pair_load<CD>(q, src);
+    };
+    if (ng > 0) load(cur, 0, &kc);
+
+    // 2. the activations into LDS
+    {
+        const bool qlane = (int)threadIdx.x < F4;             // F4 <= WG: one chunk of each pair per lane
+        for (int q0 = 0; q0 < P; q0 += DN_QP) {
+            if (q0 > 0) {
+#pragma unroll
+                for (int q = 0; q < DN_QP; ++q)
+                    act[q] = ya4[(int64_t)min(q0 + q, P - 1) * F4 + min((int)threadIdx.x, F4 - 1)];
+            }
+#pragma unroll
+            for (int q = 0; q < DN_QP; ++q) {
+                const float v[4] = {__uint_as_float(act[q].x), __uint_as_float(act[q].y), __uint_as_float(act[q].z),
+                                    __uint_as_float(act[q].w)};
+                q8_quad<AM>(smem + (q0 + q) * abytes, L, v, threadIdx.x, qlane && q0 + q < P);
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. the passes: DN_RPP rows each, one row per DN_LPR lanes
+    for (int ps = 0; ps < passes; ++ps) {
+        if (ps + 1 < passes) load(nxt, ps + 1, &kn);
+        const int k = ps * DN_RPP + lrow, s = min(k >> lg2r, ng - 1), r = k & (R - 1);
+        const DnGroup & d = s_gi[s];
+        const bool live = k < rows && r < nr && d.n_mem > 0 && lane16 < NP;
+        float acc[MT];
+#pragma unroll
+        for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
+        if (live) {
+#pragma unroll
+            for (int c = 0; c < MT; ++c) {
+                if (c >= d.n_mem) break;
+                ActView av;
+                act_layout(F, max(0, min(d.mem[c], P - 1)) * abytes, &av);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const Act32 a = act32<AM>(smem, av, 2 * lane16 + h);
+                    acc[c] += kc == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(cur, h, a) : iq4nl_block<AM>(cur, h, a))
+                                      : (CD == T_Q5_0 ? q5_0_block<AM>(cur, h, a) : iq4nl_block<AM>(cur, h, a));
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < MT; ++c)
+#pragma unroll
+            for (int o = DN_LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, DN_LPR);
+        if (live && lane16 == 0) {
+#pragma unroll
+            for (int c = 0; c < MT; ++c)
+                if (c < d.n_mem) s_y[d.mem[c]][r] = acc[c] * d.scale;
+        }
+        cur = nxt;
+        kc = kn;
+    }
+    __syncthreads();
+
+    // 4. the combine (llama-graph.cpp:1812-1840): out = sum_k w_k y_k in k order
+    for (int i = threadIdx.x; i < (T << lg2r); i += WG) {
+        const int t = i >> lg2r, r = i & (R - 1);
+        if (r >= nr) continue;
+        float o = __fmul_rn(s_y[t * K][r], s_wt[t * K]);
+        for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(s_y[t * K + k][r], s_wt[t * K + k]));
+        p.out[(int64_t)t * D + r0 + r] = o;
+    }
 }
 
-// ------------------------------------------------------------ single kernel
-//
-// The layer in one launch.  Phases hand off through arrival counters in the
-// control block; a consumer waits (thread 0, bounded by p.spin_limit ticks of
-// the wall clock) until a counter reaches its target.  The grid is sized so
-// every workgroup is resident (occupancy x CUs); a wait that times out sets
-// ctl->error and the workgroup skips the rest of its work, so every wave
-// still exits.
-//   1  workgroup e < E: router logits of expert e (coherent stores, then one
-//      arrival); every workgroup: the tokens quantised into its own LDS and
-//      the IQ2_S tables
-//   2  wait for the router (its last arrival sets a flag); every workgroup
-//      selects the routing itself (DPP top-k per token) and builds the
-//      expert groups in LDS
-//   3  gate_up items (group, 16-row block) round-robin over the workgroups;
-//      outputs with coherent stores, then one arrival on the group's counter
-//      (the last one sets the group's flag)
-//   4  down items (group, 32-row block): wait for the group's flag, GEGLU +
-//      quantise its members (coherent loads), down, combine
-//   5  the last workgroup out resets every counter for the next call
-
-template <int HT, int CT, int HD, int CD, int AM, int GSRC>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_fused(const DecParams p) {
+// C by group (more than one token): workgroup (b, g) computes output rows
+// [b R, b R + R) of group g's expert for the group's members only (R = 16
+// NPS rows, all of them in flight at once: lane l of a row's 16 holds its
+// block pair l), writing the scaled rows y_pair = .scale W a_pair to ydn;
+// workgroups of groups past the call's count return at once.  Only the
+// members' GEGLU outputs are quantised here (one to four columns, where the
+// kernel over every group quantises all T top_k of them in every workgroup).
+// k_dec_combine then sums each token's top_k rows.
+template <int HD, int CD, int AM, int MT, int NPS>
+__global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float s_part[DEC_MAXT][WG / 64];
-    __shared__ int s_ids[DEC_PMAX];
-    __shared__ float s_wt[DEC_PMAX];
-    __shared__ GroupInfo s_grp[DEC_PMAX];
-    __shared__ int s_ng, s_flag, s_lastc[DEC_MAXT];
-    constexpr int LPR_G = Fmt<HT>::LPR, ROWS_G = WG / LPR_G;
-    constexpr int LPR_D = Fmt<HD>::LPR, ROWS_D = WG / LPR_D;
-    static_assert(Fmt<HT>::LPR == Fmt<CT>::LPR && k256<HT>() && k256<CT>(), "gate_up formats");
-    static_assert(Fmt<HD>::LPR == Fmt<CD>::LPR && !k256<HD>() && !k256<CD>(), "down formats");
-    const int wave = threadIdx.x >> 6;
-    const int d = p.d_model, F = p.n_ff, E = p.n_expert, T = p.T, K = p.top_k;
-    const int F2 = 2 * F;
-    const int NRB_G = (F2 + ROWS_G - 1) / ROWS_G, NRB_D = (d + ROWS_D - 1) / ROWS_D;
+    static_assert(!k256<HD>() && !k256<CD>(), "down formats");
+    constexpr int R = NPS * DN_RPP;
+    const int D = p.d_model, F = p.n_ff, K = p.top_k, T = p.T, P = T * K;
+    const int b = blockIdx.x, r0 = b * R, nr = max(0, min(R, D - r0));
+    const int g = blockIdx.y;
+    const int ng = max(0, min(p.ctl->n_groups, P));
+    if (g >= ng) return;
+    const GroupInfo gi = validate_group(p, p.ctl->groups[g], ng, g);
+    const int nm = gi.tier < 2 ? gi.n_mem : 0;
+    const int F4 = F / 4, NP = F / 64;
+    ActView L;
+    const int abytes = act_layout(F, 0, &L);
 
-    // ---- phase 1
-    if ((int)blockIdx.x < E) {
-        router_expert(p, blockIdx.x, s_part);
-        wait_vm();
-        __syncthreads();
-        arrive_flag(&p.ctl->route_count, E, &p.ctl->route_ready);
-    }
-    ActView tmp;
-    const int abg = act_layout(d, 0, &tmp);
-    const int ag0 = p.w_lds_gu;
-    // token t's column: the layout at ag0 shifted by t * abg
-    ActView av0;
-    act_layout(d, ag0, &av0);
-    // each token is staged in LDS (the weight region, free until phase 3)
-    // with one round of 16-byte loads, then quantised from there
-    for (int t = 0; t < T; ++t) {
-        const u32x4 * xs = reinterpret_cast<const u32x4 *>(p.x + (int64_t)t * d);
-        for (int i = threadIdx.x; i < d / 4; i += WG) reinterpret_cast<u32x4 *>(smem)[i] = xs[i];
-        __syncthreads();
-        ActView v;
-        act_layout(d, ag0 + t * abg, &v);
-        ActSrc src;
-        src.p = reinterpret_cast<const float *>(smem);
-        src.n = d;
-        quantize_act<HT, AM, SRC_PLAIN>(smem, v, src, d);
-        __syncthreads();
-    }
-    const int grid_off = align16i(ag0 + min(T, DEC_MAXT) * abg);
-    if (HT == T_IQ2_S || CT == T_IQ2_S) copy_iq2s_tables(smem, grid_off, &c_iq2s_tab_dec);
-
-    // ---- phase 2
-    bool ok = wait_flag(p, &p.ctl->route_ready, &s_flag);
-    if (ok && wave < T) select_token(p.logits + (int64_t)wave * E, E, K, nullptr, nullptr, s_ids + wave * K, s_wt + wave * K);
-    __syncthreads();
-    if (ok && wave == 0) build_groups(p, s_ids, s_grp, &s_ng, p.exp_slot, p.slot_exp, p.slot_state);
-    __syncthreads();
-    if (ok && blockIdx.x == 0 && (int)threadIdx.x < T * K) {
-        p.ids[threadIdx.x] = s_ids[threadIdx.x];
-        p.w[threadIdx.x] = s_wt[threadIdx.x];
-    }
-    const int ng = ok ? min(s_ng, DEC_PMAX) : 0;
-    if (ok && blockIdx.x == 0) count_routes(p, s_ids, s_grp, ng);
-
-    // ---- phase 3: gate_up
-    for (int it = blockIdx.x; it < ng * NRB_G; it += gridDim.x) {
-        const int g = it / NRB_G, rbi = it - g * NRB_G;
-        const GroupInfo gi = s_grp[g];
-        const bool valid = gi.tier < 2;
-        const int wtype = gi.tier == 0 ? HT : CT;
-        const int r0 = rbi * ROWS_G;
-        const int rows = min(ROWS_G, F2 - r0);
-        const int rb = (d / blk_elems(wtype)) * blk_bytes(wtype);
-        const uint64_t start = (uint64_t)r0 * rb;
-        const uint64_t c0 = start >> 4;
-        const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
-        const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_gu, p.hot_gu_stride, p.cold_gu, p.cold_gu_stride)
-                                  : nullptr;
-        const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
-        Staged st;
-        stage_load(st, gW, nch);
-        stage_store(st, gW, nch, smem, 0);
-        __syncthreads();
-        const int rw = threadIdx.x / LPR_G, lr = threadIdx.x % LPR_G;
-        float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int n_mem = gi.n_mem;
-        if (valid && rw < rows) {
-            const int wb = (int)(start & 15) + rw * rb;
-            const int U = d / Fmt<HT>::UNIT;
-            // member c's activation column is its token's
-            ActView avm[DEC_MAXT];
+    // 1. the members' activations, then every row's block pairs
+    const u32x4 * ya4 = reinterpret_cast<const u32x4 *>(p.ya);
+    u32x4 act[MT];
 #pragma unroll
-            for (int c = 0; c < DEC_MAXT; ++c) {
-                const int sh = max(0, min(member(gi, c) / K, T - 1)) * abg;   // slots past n_mem are unused
-                avm[c] = ActView{av0.q + sh, av0.d32 + sh, av0.s32 + sh, av0.dK + sh, av0.bsum + sh};
-            }
-            if (gi.tier == 0) {
-                if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off);
-                } else {
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<HT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off);
-                }
-            } else {
-                if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, 1>(smem, wb, u, avm, n_mem, acc, grid_off);
-                } else {
-                    for (int u = lr; u < U; u += LPR_G) unit_dot_n<CT, AM, DEC_MAXT>(smem, wb, u, avm, n_mem, acc, grid_off);
+    for (int c = 0; c < MT; ++c)
+        act[c] = ya4[(int64_t)max(0, min(c < nm ? gi.mem[c] : gi.mem[0], P - 1)) * F4 + min((int)threadIdx.x, F4 - 1)];
+    const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
+    const int pl = min(lane16, NP - 1);
+    const int wt = gi.tier == 0 ? HD : CD;
+    const int rbytes = (F / 32) * blk_bytes(wt);
+    const uint8_t * slab = gi.tier == 0 ? p.hot_dn + (uint64_t)gi.idx * p.hot_dn_stride
+                                        : p.cold_dn + (uint64_t)gi.idx * p.cold_dn_stride;
+    DnPair w[NPS];
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+        const int r = min(ps * DN_RPP + lrow, max(nr - 1, 0));
+        const uint8_t * src = slab + (uint64_t)(r0 + r) * rbytes + (uint64_t)pl * (2 * blk_bytes(wt));
+        if (gi.tier == 0) dn_pair_load<HD>(w[ps], src);
+        else dn_pair_load<CD>(w[ps], src);
+    }
+
+    // 2. the members' q8 columns
+    {
+        const bool qlane = (int)threadIdx.x < F4;
+#pragma unroll
+        for (int c = 0; c < MT; ++c) {
+            if (c >= max(nm, 1)) break;
+            const float v[4] = {__uint_as_float(act[c].x), __uint_as_float(act[c].y), __uint_as_float(act[c].z),
+                                __uint_as_float(act[c].w)};
+            q8_quad<AM>(smem + c * abytes, L, v, threadIdx.x, qlane && c < nm);
+        }
+    }
+    __syncthreads();
+
+    // 3. the rows: dot, reduce over the row's 16 lanes, scale, store
+    const float scale = gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f)
+                                     : (gi.tier == 1 ? (p.s_cold ? p.s_cold[gi.idx] : 1.0f) : 0.0f);
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+        const int r = ps * DN_RPP + lrow;
+        float acc[MT];
+#pragma unroll
+        for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
+        if (lane16 < NP) {
+#pragma unroll
+            for (int c = 0; c < MT; ++c) {
+                if (c >= nm) break;
+                ActView av;
+                act_layout(F, c * abytes, &av);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const Act32 a = act32<AM>(smem, av, 2 * lane16 + h);
+                    acc[c] += gi.tier == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a))
+                                           : (CD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a));
                 }
             }
         }
 #pragma unroll
-        for (int c = 0; c < DEC_MAXT; ++c)
+        for (int c = 0; c < MT; ++c)
 #pragma unroll
-            for (int o = LPR_G / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR_G);
-        if (lr == 0 && rw < rows) {
+            for (int o = DN_LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, DN_LPR);
+        if (lane16 == 0 && r < nr) {
+            // an invalid id's members get zero rows
+            const int nw = gi.tier < 2 ? nm : max(0, min(gi.n_mem, MT));
 #pragma unroll
-            for (int c = 0; c < DEC_MAXT; ++c)
-                if (c < n_mem) st_coh(p.ygu + (int64_t)member(gi, c) * F2 + r0 + rw, acc[c]);
-        }
-        wait_vm();
-        __syncthreads();
-        arrive_flag(&p.ctl->group_count[g], NRB_G, &p.ctl->group_ready[g]);
-    }
-
-    // ---- phase 4: down (its LDS reuses the gate_up region)
-    ActView tmpd;
-    const int abd = act_layout(F, 0, &tmpd);
-    const int ad0 = p.w_lds_dn;
-    ActView avd[DEC_MAXT];
-#pragma unroll
-    for (int c = 0; c < DEC_MAXT; ++c) act_layout(F, ad0 + c * abd, &avd[c]);
-    constexpr int GCOH = GSRC == SRC_GEGLU_TANH ? SRC_GEGLU_TANH_COH : SRC_GEGLU_TABLE_COH;
-    for (int it = blockIdx.x; ok && it < ng * NRB_D; it += gridDim.x) {
-        const int g = it / NRB_D, rbi = it - g * NRB_D;
-        __syncthreads();                        // the previous item (or phase 3) is done with LDS
-        if (!wait_flag(p, &p.ctl->group_ready[g], &s_flag)) {
-            ok = false;
-            break;
-        }
-        const GroupInfo gi = s_grp[g];
-        const bool valid = gi.tier < 2;
-        const int wtype = gi.tier == 0 ? HD : CD;
-        const int r0 = rbi * ROWS_D;
-        const int rows = min(ROWS_D, d - r0);
-        const int rb = (F / blk_elems(wtype)) * blk_bytes(wtype);
-        const uint64_t start = (uint64_t)r0 * rb;
-        const uint64_t c0 = start >> 4;
-        const int nch = valid ? (int)(((start + (uint64_t)rows * rb + 15) >> 4) - c0) : 0;
-        const uint8_t * W = valid ? group_slab(gi.tier, gi.idx, p.hot_dn, p.hot_dn_stride, p.cold_dn, p.cold_dn_stride)
-                                  : nullptr;
-        const u32x4 * gW = reinterpret_cast<const u32x4 *>(W) + c0;
-        Staged st;
-        stage_load(st, gW, nch);
-        const int n_mem = gi.n_mem;
-#pragma unroll
-        for (int c = 0; c < DEC_MAXT; ++c) {
-            if (c >= n_mem) break;
-            ActSrc src;
-            src.p = p.ygu + (int64_t)member(gi, c) * F2;
-            src.n = F;
-            quantize_act<T_Q5_0, AM, GCOH>(smem, avd[c], src, F);
-        }
-        stage_store(st, gW, nch, smem, 0);
-        __syncthreads();
-        const int rw = threadIdx.x / LPR_D, lr = threadIdx.x % LPR_D;
-        float acc[DEC_MAXT] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (valid && rw < rows) {
-            const int wb = (int)(start & 15) + rw * rb;
-            const int U = F / Fmt<HD>::UNIT;
-            if (gi.tier == 0) {
-                if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0);
-                } else {
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<HD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0);
-                }
-            } else {
-                if (n_mem == 1) {           // one member: the single-column unit
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, 1>(smem, wb, u, avd, n_mem, acc, 0);
-                } else {
-                    for (int u = lr; u < U; u += LPR_D) unit_dot_n<CD, AM, DEC_MAXT>(smem, wb, u, avd, n_mem, acc, 0);
-                }
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < DEC_MAXT; ++c)
-#pragma unroll
-            for (int o = LPR_D / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR_D);
-        const float sc = !valid ? 0.0f
-                       : gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f) : (p.s_cold ? p.s_cold[gi.idx] : 1.0f);
-        if (lr == 0 && rw < rows) {
-#pragma unroll
-            for (int c = 0; c < DEC_MAXT; ++c)
-                if (c < n_mem) st_coh(p.ydn + (int64_t)member(gi, c) * d + r0 + rw, valid ? acc[c] * sc : 0.0f);
-        }
-        // combine: the last pair of a token to finish these rows sums them
-        wait_vm();
-        __syncthreads();
-        if ((int)threadIdx.x < n_mem) {
-            const int t = member(gi, threadIdx.x) / K;
-            s_lastc[threadIdx.x] = atomicAdd(&p.comb_count[t * p.n_rb_down + rbi], 1) == K - 1;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < DEC_MAXT; ++c) {
-            if (c >= n_mem) break;
-            if (!s_lastc[c]) continue;
-            const int t = member(gi, c) / K;
-            const float * yt = p.ydn + (int64_t)t * K * d + r0;
-            const float * wt = s_wt + t * K;
-            for (int r = threadIdx.x; r < rows; r += WG) p.out[(int64_t)t * d + r0 + r] = combine_row(yt + r, wt, K, d);
+            for (int c = 0; c < MT; ++c)
+                if (c < nw) p.ydn[(int64_t)max(0, min(gi.mem[c], P - 1)) * D + r0 + r] = acc[c] * scale;
         }
     }
 
-    // ---- phase 5
-    wait_vm();
-    __syncthreads();
-    if (threadIdx.x == 0) s_flag = atomicAdd(&p.ctl->done_count, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (s_flag) {
-        for (int i = threadIdx.x; i < DEC_MAXT * p.n_rb_down; i += WG) p.comb_count[i] = 0;
-        for (int i = threadIdx.x; i < DEC_PMAX; i += WG) {
-            p.ctl->group_count[i] = 0;
-            p.ctl->group_ready[i] = 0;
-        }
-        if (threadIdx.x == 0) {
-            p.ctl->route_count = 0;
-            p.ctl->route_ready = 0;
-            p.ctl->done_count = 0;
-        }
-    }
+}
+
+// the combine after the down kernel by group (llama-graph.cpp:1812-1840):
+// out[t][r] = sum_k w_k ydn[t K + k][r] in k order
+__global__ __launch_bounds__(WG) void k_dec_combine(const DecParams p) {
+    const int D = p.d_model, K = p.top_k;
+    const int i = blockIdx.x * WG + threadIdx.x;
+    if (i >= p.T * D) return;
+    const int t = i / D, r = i - t * D;
+    const float * y = p.ydn + (int64_t)t * K * D + r;
+    const float * wk = p.w + t * K;
+    float o = __fmul_rn(y[0], wk[0]);
+    for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(y[(int64_t)k * D], wk[k]));
+    p.out[i] = o;
 }
 
 __global__ void k_zero(int * p, int n) {
@@ -1251,68 +1064,56 @@ int dec_act_bytes(int n) {
     return act_layout(n, 0, &v);
 }
 
-// dynamic LDS: staged weights, one activation column per token of the call
-// (a group has at most one member per token), IQ2_S tables when used
+// dynamic LDS of B: the two halves of an item, one activation column per
+// token of the call (a group has at most one member per token), the IQ2_S
+// codebook when used
 int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
-    ActView v;
-    const int ab = act_layout(p.d_model, 0, &v);
     const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
-    return align16i(p.w_lds_gu + std::min(p.T, DEC_MAXT) * ab) + (iq2 ? (int)sizeof(Iq2sTables) : 0);
+    return align16i(2 * p.w_lds_gu + std::min(p.T, DEC_MAXT) * dec_act_bytes(p.d_model)) +
+           (iq2 ? (int)sizeof(Iq2sTables) : 0);
 }
 
+// dynamic LDS of C: every pair's down activation
 int dec_lds_down(const DecParams & p) {
-    ActView v;
-    const int ab = act_layout(p.n_ff, 0, &v);
-    return p.w_lds_dn + std::min(p.T, DEC_MAXT) * ab;
+    return p.T * p.top_k * dec_act_bytes(p.n_ff);
 }
 
 namespace {
 // launch with the dispatch's own begin/end timestamps recorded into e0/e1
 // when profiling (e0 != nullptr)
 template <typename F>
-void launch_timed(F k, dim3 grid, int lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const DecParams & p) {
-    if (e0) hipExtLaunchKernelGGL(k, grid, dim3(WG), (uint32_t)lds, s, e0, e1, 0u, p);
-    else hipLaunchKernelGGL(k, grid, dim3(WG), lds, s, p);
+void launch_timed(F k, dim3 grid, int lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const DecParams & p,
+                  int block = WG) {
+    if (e0) hipExtLaunchKernelGGL(k, grid, dim3(block), (uint32_t)lds, s, e0, e1, 0u, p);
+    else hipLaunchKernelGGL(k, grid, dim3(block), lds, s, p);
 }
 
 // resident workgroups of a kernel on the current device (cached per device
 // and instantiation; LDS bytes are part of the key)
 template <typename F>
-int resident_wgs(F k, int lds) {
+int resident_wgs(F k, int lds, int block) {
     static std::mutex mu;
     static std::map<std::tuple<int, const void *, int>, int> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    const auto key = std::make_tuple(dev, reinterpret_cast<const void *>(k), lds);
+    const auto key = std::make_tuple(dev, reinterpret_cast<const void *>(k), lds);   // block is fixed per kernel
     std::lock_guard<std::mutex> lk(mu);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, WG, lds) != hipSuccess) per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, block, lds) != hipSuccess) per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
     const int n = per_cu * cus;
     cache[key] = n;
     return n;
 }
-
-// grid of a persistent item loop: as many workgroups as can be resident (the
-// next item's loads then overlap the current item's dots), at most one per
-// item, and enough that no workgroup takes more than DEC_MAXI items.  No
-// workgroup waits on another, so any grid is safe.
-template <typename F>
-int item_grid(F k, int lds, int max_items) {
-    const int cap = resident_wgs(k, lds);
-    const int g = cap > 0 ? std::min(max_items, cap) : max_items;
-    return std::max(std::max(g, 1), (max_items + DEC_MAXI - 1) / DEC_MAXI);
-}
 }  // namespace
 
-hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, bool fuse_bc,
-                         hipStream_t s, hipEvent_t * ev) {
-    hipEvent_t e[6] = {};
+hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
+                         hipEvent_t * ev) {
+    hipEvent_t e[8] = {};
     if (ev)
-        for (int i = 0; i < 6; ++i) e[i] = ev[i];
-    const int P = p.T * p.top_k;
+        for (int i = 0; i < 8; ++i) e[i] = ev[i];
     {
         // E router workgroups, then the quantisation workgroups (4 waves each)
         const int per_tok = am == AM_CPU ? p.d_model / 256 : (p.d_model + 63) / 64;
@@ -1322,49 +1123,22 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
-    const int gu_items = P * ((2 * p.n_ff + 15) / 16), dn_items = P * p.n_rb_down;
-    if (fuse_bc && p.T == 1 && hgu == T_Q4_K && cgu == T_IQ2_S && hdn == T_Q5_0 && cdn == T_IQ4_NL) {
-        // gate_up and down in one kernel for one token (with more, the four
-        // member columns leave too few registers for the fused loop): only
-        // with every workgroup resident (its down items wait on gate_up items
-        // of other workgroups)
-        const int lds = std::max(dec_lds_gate_up(p, hgu, cgu), dec_lds_down(p));
-        auto go = [&](auto k) -> bool {
-            const int cap = resident_wgs(k, lds);
-            const int grid = std::min(std::max(gu_items, dn_items), cap);
-            if (grid < 1 || (gu_items + grid - 1) / grid > DEC_MAXI || (dn_items + grid - 1) / grid > DEC_MAXI)
-                return false;
-            launch_timed(k, dim3(grid), lds, s, e[2], e[3], p);
-            return true;
-        };
-        bool launched = false;
-#define LL_F(M, G) \
-        if (am == M && gelu == G) launched = go(k_dec_gate_up<T_Q4_K, T_IQ2_S, M, 1, true, T_Q5_0, T_IQ4_NL, G>);
-        LL_F(AM_CPU, SRC_GEGLU_TABLE) LL_F(AM_CPU, SRC_GEGLU_TANH) LL_F(AM_Q8_1, SRC_GEGLU_TABLE)
-        LL_F(AM_Q8_1, SRC_GEGLU_TANH)
-#undef LL_F
-        if (launched) {
-            const hipError_t err = hipGetLastError();
-            if (err != hipSuccess) return err;
-            // profiling: the fused kernel is timed as the gate_up stage; the
-            // down stage's events are recorded back to back (0 ms)
-            if (e[4]) {
-                const hipError_t e4 = hipEventRecord(e[4], s);
-                if (e4 != hipSuccess) return e4;
-                return hipEventRecord(e[5], s);
-            }
-            return hipSuccess;
-        }
-    }
     {
+        // one workgroup per item while they can all be resident; no
+        // workgroup waits on another, so any grid is safe
+        const int items = p.T * p.top_k * (p.n_ff / GU_HALF);   // at most; the groups decide
         const int lds = dec_lds_gate_up(p, hgu, cgu);
-        auto go = [&](auto k) { launch_timed(k, dim3(item_grid(k, lds, gu_items)), lds, s, e[2], e[3], p); };
-#define LL_GU(A, B, M) \
-        if (hgu == A && cgu == B && am == M) { \
-            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, false, T_Q5_0, T_IQ4_NL, SRC_GEGLU_TABLE>); \
-            else go(k_dec_gate_up<A, B, M, DEC_MAXT, false, T_Q5_0, T_IQ4_NL, SRC_GEGLU_TABLE>); \
+        auto go = [&](auto k) {
+            const int cap = resident_wgs(k, lds, WG);
+            const int grid = std::max(1, cap > 0 ? std::min(items, cap) : items);
+            launch_timed(k, dim3(grid), lds, s, e[2], e[3], p);
+        };
+#define LL_GU(A, B, M, G) \
+        if (hgu == A && cgu == B && am == M && gelu == G) { \
+            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, G>); else go(k_dec_gate_up<A, B, M, DEC_MAXT, G>); \
         } else
-#define LL_GU2(A, B) LL_GU(A, B, AM_CPU) LL_GU(A, B, AM_Q8_1)
+#define LL_GU2(A, B) LL_GU(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_GU(A, B, AM_CPU, SRC_GEGLU_TANH) \
+                     LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TANH)
         LL_GU2(T_Q4_K, T_IQ2_S) LL_GU2(T_Q4_K, T_Q4_K) LL_GU2(T_IQ2_S, T_IQ2_S) LL_GU2(T_IQ2_S, T_Q4_K)
         return hipErrorInvalidValue;
 #undef LL_GU2
@@ -1374,39 +1148,26 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     }
     {
         const int lds = dec_lds_down(p);
-        auto go = [&](auto k) { launch_timed(k, dim3(item_grid(k, lds, dn_items)), lds, s, e[4], e[5], p); };
-#define LL_DN(A, B, M, G) \
-        if (hdn == A && cdn == B && am == M && gelu == G) { \
-            if (p.T == 1) go(k_dec_down<A, B, M, G, 1>); else go(k_dec_down<A, B, M, G, DEC_MAXT>); \
+        const int rows = 1 << p.dn_rows_log2;
+        const dim3 grid((p.d_model + rows - 1) / rows);
+        const dim3 ggrid((p.d_model + DN_GRP_ROWS - 1) / DN_GRP_ROWS, p.T * p.top_k);
+        const int glds = std::min(p.T, DEC_MAXT) * dec_act_bytes(p.n_ff);
+#define LL_DN(A, B, M) \
+        if (hdn == A && cdn == B && am == M) { \
+            if (p.dn_by_group) { \
+                if (p.T == 1) launch_timed(k_dec_down_grp<A, B, M, 1, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
+                else launch_timed(k_dec_down_grp<A, B, M, DEC_MAXT, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
+            } else if (p.T == 1) launch_timed(k_dec_down<A, B, M, 1>, grid, lds, s, e[4], e[5], p); \
+            else launch_timed(k_dec_down<A, B, M, DEC_MAXT>, grid, lds, s, e[4], e[5], p); \
         } else
-#define LL_DN2(A, B) LL_DN(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_DN(A, B, AM_CPU, SRC_GEGLU_TANH) \
-                     LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_DN(A, B, AM_Q8_1, SRC_GEGLU_TANH)
+#define LL_DN2(A, B) LL_DN(A, B, AM_CPU) LL_DN(A, B, AM_Q8_1)
         LL_DN2(T_Q5_0, T_IQ4_NL) LL_DN2(T_Q5_0, T_Q5_0) LL_DN2(T_IQ4_NL, T_IQ4_NL) LL_DN2(T_IQ4_NL, T_Q5_0)
         return hipErrorInvalidValue;
 #undef LL_DN2
 #undef LL_DN
+        if (p.dn_by_group) launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
     }
     return hipGetLastError();
-}
-
-hipError_t launch_decode_fused(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
-                               hipEvent_t * ev) {
-    if (!(hgu == T_Q4_K && cgu == T_IQ2_S && hdn == T_Q5_0 && cdn == T_IQ4_NL)) return hipErrorNotSupported;
-    const int lds = std::max(dec_lds_gate_up(p, hgu, cgu), dec_lds_down(p));
-    const int P = p.T * p.top_k;
-    const int items = P * std::max((2 * p.n_ff + 15) / 16, p.n_rb_down);
-    auto go = [&](auto k) -> hipError_t {
-        const int cap = resident_wgs(k, lds);
-        const int want = std::max(p.n_expert, items);
-        const int grid = std::min(cap, want);
-        if (cap < p.n_expert || grid < 1) return hipErrorNotSupported;   // the router needs E resident workgroups
-        launch_timed(k, dim3(grid), lds, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, p);
-        return hipGetLastError();
-    };
-    if (am == AM_CPU && gelu == SRC_GEGLU_TANH) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_CPU, SRC_GEGLU_TANH>);
-    if (am == AM_CPU) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_CPU, SRC_GEGLU_TABLE>);
-    if (gelu == SRC_GEGLU_TANH) return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_Q8_1, SRC_GEGLU_TANH>);
-    return go(k_dec_fused<T_Q4_K, T_IQ2_S, T_Q5_0, T_IQ4_NL, AM_Q8_1, SRC_GEGLU_TABLE>);
 }
 
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s) {

@@ -54,19 +54,14 @@ struct GroupInfo {
     int mem[DEC_MAXT];          // routed-pair indices, one per member token
 };
 
-// control block at the start of the decode workspace (zero before first use):
-// arrival counters, the expert groups selected, and the error word a timed-out
-// wait of the single-kernel path sets (cleared by the host)
+constexpr int DEC_DN_MAXR = 32;  // output rows of one down workgroup, at most
+
+// control block at the start of the decode workspace: the expert groups the
+// gate_up kernel selected, for the down kernel
 struct DecCtl {
-    int route_count;
     int n_groups;
-    int done_count;
-    int error;
+    int pad[3];
     GroupInfo groups[DEC_PMAX];
-    int group_count[DEC_PMAX];
-    int route_ready;            // single-kernel path: write-once flags set by the last arriver
-    int pad2[3];
-    int group_ready[DEC_PMAX];
 };
 
 struct DecParams {
@@ -81,22 +76,16 @@ struct DecParams {
     const int32_t * exp_slot; const int32_t * slot_exp; const int32_t * slot_state;
     const float * s_hot; const float * s_cold;
     DecCtl * ctl;
-    int * comb_count;           // [DEC_MAXT][n_rb_down]
-    int * gu_done;              // [DEC_PMAX][gate_up row blocks]: fused gate_up+down, item done flags
     float * logits;             // [T][n_expert]
     int32_t * ids;              // [T][top_k]
     float * w;                  // [T][top_k]
     uint8_t * xq; int64_t xq_stride;     // quantised tokens
-    float * ygu;                // [P][2 n_ff]
-    uint8_t * aq; int64_t aq_stride;     // quantised down activations per pair
-    float * ydn;                // [P][d_model]
+    float * ya;                 // [P][n_ff] down activations (GEGLU outputs) per routed pair
+    float * ydn;                // [P][d_model] scaled down rows per routed pair (down by group)
+    int dn_by_group;            // 1: the down kernel by group + k_dec_combine, 0: the down kernel over every group
     float * out;                // [T][d_model]
-    int w_lds_gu, w_lds_dn;     // LDS bytes for staged weights
-    int n_rb_down;              // 32-row blocks of the down projection
-    int hot_dn_type, cold_dn_type;   // the down pools' formats
-    int prefetch_dn;            // gate_up items touch their down item's slab (into L2/MALL) for the down kernel
-    int never;                  // always 0: keeps the touch loads from being dropped
-    int64_t spin_limit;         // single-kernel path: wall-clock ticks a wait may take
+    int w_lds_gu;               // LDS bytes of one half of a gate_up item (8 rows)
+    int dn_rows_log2;           // log2 of the output rows per down workgroup (<= DEC_DN_MAXR)
     int32_t * rc_counts;        // [n_expert] routed pairs per expert, or NULL
     int32_t * rc_hits;          // [2] hot pairs, other pairs (with rc_counts)
 };
@@ -104,19 +93,12 @@ struct DecParams {
 int dec_act_bytes(int n);
 int dec_lds_gate_up(const DecParams & p, int ht, int ct);
 int dec_lds_down(const DecParams & p);
-// fuse_bc: gate_up and down as one kernel where the formats are the standard
-// pair (Q4_K/IQ2_S gate_up, Q5_0/IQ4_NL down) and every workgroup can be
-// resident; otherwise (or false) as two.  ev (optional, profiling): 6 events
-// that receive the begin and end timestamps of the router kernel, gate_up
-// (or the fused kernel) and down (ev[0..1], ev[2..3], ev[4..5]).
+// ev (optional, profiling): 8 events that receive the begin and end
+// timestamps of the router, gate_up, down and combine kernels (ev[0..1],
+// ev[2..3], ev[4..5], ev[6..7]; the last two stay unrecorded without a
+// combine kernel).
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
-                         bool fuse_bc, hipStream_t s, hipEvent_t * ev);
-// The same layer in one kernel (phases hand off through arrival counters with
-// bounded waits).  Returns hipErrorNotSupported for format pairs it does not
-// instantiate or shapes it cannot keep co-resident; the caller then uses
-// launch_decode.  ev (optional): begin/end timestamps of the kernel.
-hipError_t launch_decode_fused(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
-                               hipStream_t s, hipEvent_t * ev);
+                         hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 
 // ------------------------------------------------------------ prefill path
