@@ -67,7 +67,9 @@ class Workload:
         for _ in range(R - 1):
             d = la.DeviceLayer.__new__(la.DeviceLayer)
             d.__dict__.update(base.__dict__)
-            for k in ("hot_gu", "hot_dn", "cold_gu", "cold_dn"):
+            # every tensor a step reads is the replica's own (the router too:
+            # its 1.44 MB is counted in the step's bytes)
+            for k in ("hot_gu", "hot_dn", "cold_gu", "cold_dn", "router_w", "router_b"):
                 if getattr(base, k) is not None:
                     setattr(d, k, getattr(base, k).clone())
             d._ws = None
@@ -438,6 +440,31 @@ class Stack:
             self.descs.append(d.desc())
         self.fn = la.lib().llapis_moe_ffn
 
+    def routed_tiers(self, h0, ws, stream):
+        """Distinct hot and cold experts one pass of h0 routes to, over every
+        layer (each layer's ids read back after its call)."""
+        torch, sp = self.torch, self.spec
+        T = h0.shape[0]
+        h = h0.clone()
+        out = torch.zeros_like(h0)
+        ids = torch.empty(T, sp.top_k, dtype=torch.int32, device=h.device)
+        w = torch.empty(T, sp.top_k, device=h.device)
+        n_hot = n_cold = 0
+        for d, dl in zip(self.descs, self.layers):
+            xl = torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6)
+            rc = self.fn(C.byref(d), xl.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                         ws.data_ptr(), ws.numel(), stream)
+            if rc != 0:
+                raise RuntimeError(self.la.lib().llapis_last_error().decode())
+            torch.cuda.synchronize()
+            res = dl.layer.residency
+            ex = set(ids.cpu().numpy().ravel().tolist())
+            hot = sum(1 for e in ex if res.is_hot(int(e)))
+            n_hot += hot
+            n_cold += len(ex) - hot
+            h.add_(out)
+        return n_hot, n_cold
+
     def run(self, h, xn, out, ws, stream, T, moe=True):
         """h [T, d_model] (the residual stream) is updated in place through
         every layer; out is scratch (xn is unused: the norm's output is the
@@ -509,16 +536,20 @@ def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_
              "tok_per_s": T * 1e3 / ms, "moe_tok_per_s": T * 1e3 / moe_ms,
              "moe_us_per_layer": moe_ms * 1e3 / n_layers, "moe_int8_tops": ops / (moe_ms * 1e-3) / 1e12}
         if T == 1:
-            # bytes: each layer's 8 routed experts (mixed tiers, ~85 % hot) once + router
+            # bytes: each layer's routed experts of this token (hot and cold
+            # counted from the pass's own routing) once + its router
             per = spec.gu_bytes(spec.hot_gu_type) + spec.dn_bytes(spec.hot_dn_type)
             per_c = spec.gu_bytes(spec.cold_gu_type) + spec.dn_bytes(spec.cold_dn_type)
-            b = n_layers * (8 * (0.85 * per + 0.15 * per_c) + spec.n_expert * spec.d_model * 4)
-            r["moe_hbm_gbs_est"] = b / (moe_ms * 1e-3) / 1e9
-            r["moe_hbm_frac_est"] = r["moe_hbm_gbs_est"] / HBM_PEAK_GBS
+            n_hot, n_cold = st.routed_tiers(h0, ws, s.cuda_stream)
+            b = n_hot * per + n_cold * per_c + n_layers * spec.n_expert * spec.d_model * 4
+            r["distinct_hot_per_pass"], r["distinct_cold_per_pass"] = n_hot, n_cold
+            r["moe_hbm_gbs"] = b / (moe_ms * 1e-3) / 1e9
+            r["moe_hbm_frac"] = r["moe_hbm_gbs"] / HBM_PEAK_GBS
         res[name] = r
         log(f"[stack {name}] {T} token(s) x {n_layers} layers: {ms:.3f} ms per pass ({glue:.3f} ms of it the "
             f"norm/add glue); MoE {r['moe_us_per_layer']:.1f} us per layer, {r['moe_tok_per_s']:.0f} tok/s"
-            + (f", ~{r['moe_hbm_gbs_est']:.0f} GB/s" if T == 1 else f", {r['moe_int8_tops']:.1f} int8 TOP/s"))
+            + (f", {r['moe_hbm_gbs']:.0f} GB/s ({r['distinct_hot_per_pass']} hot + {r['distinct_cold_per_pass']} "
+               f"cold experts per pass)" if T == 1 else f", {r['moe_int8_tops']:.1f} int8 TOP/s"))
         del ws, h, h0, xn, out
     del st
     torch.cuda.empty_cache()

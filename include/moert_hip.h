@@ -13,8 +13,10 @@
  *    and 2 and the CPU sidecar callbacks are accepted in the config but
  *    moert_ffn_moe refuses a fire with planc_mode != 0 (prints and aborts,
  *    the island's error contract);
- *  - the host-memory registration and batch-transport services are stubs
- *    that refuse (return 0 / -1), except moert_cuda_publish_h2d, which copies.
+ *  - the host-memory registration services refuse (return 0 / NULL): the
+ *    cold tier lives in HBM, so nothing host-side is mapped for kernels.  The
+ *    batch transport (moert_cuda_dir_*, moert_cuda_publish_h2d and the
+ *    early-decision gate) is implemented: see its declarations below.
  */
 #ifndef MOERT_HIP_H
 #define MOERT_HIP_H

@@ -75,6 +75,7 @@ __device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 6
     const int d = p.d_model, E = p.n_expert, T = p.T, n4 = d / 4;
     const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
     const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
+    const float bias = p.router_b ? p.router_b[e] : 0.0f;     // issued with the row's loads
     float acc[DEC_MAXT];
 #pragma unroll
     for (int t = 0; t < DEC_MAXT; ++t) acc[t] = 0.0f;
@@ -106,7 +107,7 @@ __device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 6
         float s = 0.0f;
 #pragma unroll
         for (int q = 0; q < WG / 64; ++q) s += s_part[t][q];
-        p.logits[(int64_t)t * E + e] = s + (p.router_b ? p.router_b[e] : 0.0f);
+        p.logits[(int64_t)t * E + e] = s + bias;
     }
 }
 
@@ -1046,8 +1047,17 @@ __global__ __launch_bounds__(WG) void k_dec_combine(const DecParams p) {
     const int t = i / D, r = i - t * D;
     const float * y = p.ydn + (int64_t)t * K * D + r;
     const float * wk = p.w + t * K;
-    float o = __fmul_rn(y[0], wk[0]);
-    for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(y[(int64_t)k * D], wk[k]));
+    // every load issued before the first use (K <= DEC_KMAX)
+    float yv[DEC_KMAX], wv[DEC_KMAX];
+#pragma unroll
+    for (int k = 0; k < DEC_KMAX; ++k) {
+        yv[k] = k < K ? y[(int64_t)k * D] : 0.0f;
+        wv[k] = k < K ? wk[k] : 0.0f;
+    }
+    float o = __fmul_rn(yv[0], wv[0]);
+#pragma unroll
+    for (int k = 1; k < DEC_KMAX; ++k)
+        if (k < K) o = __fadd_rn(o, __fmul_rn(yv[k], wv[k]));
     p.out[i] = o;
 }
 

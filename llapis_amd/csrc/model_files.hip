@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <fcntl.h>
+#include <sys/stat.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -422,8 +423,15 @@ bool load_store(const char * index_path, IdxHeader & h, std::vector<IdxRecord> &
         ffail(std::string("moert-store: cannot open index ") + index_path);
         return false;
     }
-    bool ok = fread(&h, sizeof h, 1, f) == 1 && header_ok(h) && fseeko(f, (off_t)h.header_bytes, SEEK_SET) == 0 &&
-              h.record_count < (1ull << 32);
+    // the index's own size bounds the record count, and the page table the
+    // reader builds (n_layers x n_expert x 8 entries) stays below 64 MB
+    off_t idx_size = -1;
+    if (fseeko(f, 0, SEEK_END) == 0) idx_size = ftello(f);
+    bool ok = idx_size > 0 && fseeko(f, 0, SEEK_SET) == 0 && fread(&h, sizeof h, 1, f) == 1 && header_ok(h) &&
+              h.header_bytes <= (uint64_t)idx_size &&
+              h.record_count <= ((uint64_t)idx_size - h.header_bytes) / h.record_stride &&
+              h.n_layers >= 1 && h.n_expert >= 1 && (uint64_t)h.n_layers * h.n_expert <= (1ull << 20) &&
+              fseeko(f, (off_t)h.header_bytes, SEEK_SET) == 0;
     if (ok) {
         recs.resize(h.record_count);
         for (uint64_t i = 0; i < h.record_count && ok; ++i) {
@@ -445,6 +453,21 @@ bool load_store(const char * index_path, IdxHeader & h, std::vector<IdxRecord> &
         if (fd >= 0) close(fd);
         ffail("moert-store: " + pp + ": missing pack, bad pack header or index/pack uuid mismatch");
         return false;
+    }
+    // every record inside the pack
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+        close(fd);
+        ffail("moert-store: " + pp + ": cannot stat the pack");
+        return false;
+    }
+    const uint64_t pack_size = (uint64_t)st.st_size;
+    for (const IdxRecord & r : recs) {
+        if (r.offset > pack_size || r.nbytes > pack_size - r.offset) {
+            close(fd);
+            ffail("moert-store: " + std::string(index_path) + ": a record lies outside the pack");
+            return false;
+        }
     }
     *pack_fd = fd;
     return true;
@@ -516,13 +539,20 @@ int64_t moert_store_verify(const char * index_path) {
     std::vector<IdxRecord> recs;
     int fd;
     if (!index_path || !load_store(index_path, h, recs, &fd)) return -1;
-    std::vector<uint8_t> buf;
+    // each page hashed through a fixed buffer (FNV-1a continues from the
+    // running value)
+    std::vector<uint8_t> buf(1 << 20);
     int64_t bad = 0;
     for (const IdxRecord & r : recs) {
-        buf.resize(r.nbytes);
-        if (read_fully(fd, buf.data(), r.nbytes, r.offset) != 0 ||
-            moert_store_fnv1a64(buf.data(), r.nbytes, MOERT_STORE_FNV_SEED) != r.checksum)
-            ++bad;
+        uint64_t hsh = MOERT_STORE_FNV_SEED, done = 0;
+        bool ok = true;
+        while (ok && done < r.nbytes) {
+            const uint64_t n = std::min<uint64_t>(buf.size(), r.nbytes - done);
+            ok = read_fully(fd, buf.data(), n, r.offset + done) == 0;
+            if (ok) hsh = moert_store_fnv1a64(buf.data(), n, hsh);
+            done += n;
+        }
+        if (!ok || hsh != r.checksum) ++bad;
     }
     close(fd);
     return bad;

@@ -443,6 +443,7 @@ struct llapis_xfer {
         std::vector<llapis_xfer_done> jobs;
         size_t next;
         hipEvent_t ev;
+        bool settled;                  // finished (or failed) before it was queued: no event to query
     };
     std::vector<llapis_xfer_done> pending;
     std::deque<Batch> live;
@@ -545,6 +546,18 @@ int32_t llapis_xfer_flush(llapis_xfer * x, void * after_stream) {
         (void)hipGetLastError();
         return xfail("llapis_xfer_flush: could not order the copies after the compute stream");
     }
+    // the batch's completion event first: without one the jobs stay pending
+    // (nothing issued, nothing lost) and the next flush tries again
+    hipEvent_t ev = nullptr;
+    if (x->ev_pool.empty()) {
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return xfail("llapis_xfer_flush: event creation failed");
+        }
+    } else {
+        ev = x->ev_pool.back();
+        x->ev_pool.pop_back();
+    }
     x->s.max_queue = std::max<long long>(x->s.max_queue, (long long)x->pending.size());
     // device sources: one copy kernel per BATCH_RUNS page runs; pinned
     // sources (or no copy workgroups): the runtime's asynchronous copies
@@ -569,25 +582,22 @@ int32_t llapis_xfer_flush(llapis_xfer * x, void * after_stream) {
         (void)hipGetLastError();
         ok = false;
     }
-    llapis_xfer::Batch b = {std::move(x->pending), 0, nullptr};
+    llapis_xfer::Batch b = {std::move(x->pending), 0, ev, false};
     x->pending.clear();
     for (auto & d : b.jobs) d.ok = ok ? 1 : 0;
-    if (x->ev_pool.empty()) {
-        if (hipEventCreateWithFlags(&b.ev, hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            return xfail("llapis_xfer_flush: event creation failed");
-        }
-    } else {
-        b.ev = x->ev_pool.back();
-        x->ev_pool.pop_back();
-    }
+    int32_t rc = 0;
     if (hipEventRecord(b.ev, x->st) != hipSuccess) {
+        // the copies are issued but cannot be tracked: wait for the stream,
+        // then hand the jobs out as failed, so their slots are released
         (void)hipGetLastError();
-        return xfail("llapis_xfer_flush: event record failed");
+        if (hipStreamSynchronize(x->st) != hipSuccess) (void)hipGetLastError();
+        for (auto & d : b.jobs) d.ok = 0;
+        b.settled = true;
+        rc = xfail("llapis_xfer_flush: event record failed; the batch is reported as failed");
     }
     x->n_live += (long long)b.jobs.size();
     x->live.push_back(std::move(b));
-    return 0;
+    return rc;
 }
 
 int32_t llapis_xfer_take_done(llapis_xfer * x, llapis_xfer_done * out, int32_t max_out) {
@@ -596,7 +606,7 @@ int32_t llapis_xfer_take_done(llapis_xfer * x, llapis_xfer_done * out, int32_t m
     int32_t n = 0;
     while (n < max_out && !x->live.empty()) {
         llapis_xfer::Batch & b = x->live.front();
-        if (b.next == 0) {   // not yet known to be finished
+        if (b.next == 0 && !b.settled) {   // not yet known to be finished
             const hipError_t e = hipEventQuery(b.ev);
             if (e == hipErrorNotReady) {
                 (void)hipGetLastError();

@@ -229,6 +229,40 @@ def test_store_round_trip_with_reference(tmp_path, writer):
     assert not ours.moert_store_reader_open(str(idx).encode(), 0x123)
 
 
+def test_store_refuses_corrupt_index(tmp_path):
+    """A damaged index is refused with an error return (no allocation sized
+    from it): a record count beyond the index's own size, a truncated index,
+    a geometry whose page table would be huge, a record reaching past the
+    end of the pack."""
+    import struct
+    lib = la.lib()
+    pages = store_pages(np.random.default_rng(12))
+    idx, pack = tmp_path / "c.experts.index", tmp_path / "c.experts.pack"
+    write_store(lib, idx, pack, pages)
+    good = idx.read_bytes()
+
+    def patched(off, fmt, val):
+        raw = bytearray(good)
+        struct.pack_into(fmt, raw, off, val)
+        return bytes(raw)
+
+    header = 96                                   # records follow the 96-byte header, 72 bytes each
+    bad = [patched(72, "<Q", 1 << 31),            # record_count
+           good[:header + 72 * 3 + 10],           # truncated
+           patched(40, "<I", 1 << 20),            # n_layers (x 6 experts)
+           patched(header + 16, "<Q", 1 << 40),   # first record's nbytes
+           patched(header + 8, "<Q", 1 << 62)]    # first record's offset
+    for i, raw in enumerate(bad):
+        idx.write_bytes(raw)
+        assert not lib.moert_store_reader_open(str(idx).encode(), 0), i
+        assert lib.moert_store_verify(str(idx).encode()) == -1, i
+    idx.write_bytes(good)
+    assert lib.moert_store_verify(str(idx).encode()) == 0
+    r = lib.moert_store_reader_open(str(idx).encode(), 0)
+    assert r
+    lib.moert_store_reader_free(r)
+
+
 def test_store_fnv_matches(tmp_path):
     ref = ref_store()
     data = np.random.default_rng(2).integers(0, 256, 1000, dtype=np.uint8)
