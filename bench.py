@@ -109,6 +109,44 @@ class Workload:
         return acc / self.n_tok
 
 
+class IslandWorkload(Workload):
+    """The same replicas driven through the reference's operator boundary:
+    llapis_router_topk, the gate_up fire of the dual op (moert_ffn_moe:
+    partition, gather, hot and cold mul_mat_id, scatter), GEGLU, the down
+    fire, and the weighted sum over top_k (ggml's mul + adds, here one fp32
+    torch bmm) -- the per-fire island a relinked ggml graph runs."""
+
+    def step(self, i, stream):
+        torch = self.torch
+        dl = self.layers[i % self.R]
+        sp = self.spec
+        x = self.x[i % self.n_tok]
+        ids, w, _ = dl.router(x)
+        gu = dl.moe_dual(0, x, ids)
+        act = self.la.geglu(gu.reshape(-1, 2 * sp.n_ff), sp.n_ff, dl.gelu_mode)
+        dn = dl.moe_dual(1, act, ids)
+        torch.bmm(w.unsqueeze(1), dn, out=self.out.view(self.T, 1, sp.d_model))
+
+
+def run_island(la, torch, name, host_layer, T, steps, warmup, dev, layer_res):
+    """Tokens per second of the island path beside llapis_moe_ffn's on the
+    same workload (layer_res: run_config's result for it)."""
+    sp = host_layer.spec
+    R = layer_res["replicas"]
+    wl = IslandWorkload(la, torch, host_layer, R, T, 16, 1234, dev, 0, 0)
+    ms_graph, timed = time_graph(wl, steps, warmup)
+    ms_eager = time_eager(wl, min(steps, 200), min(warmup, 20))
+    res = {"tok_per_s": T * 1e3 / ms_graph, "ms_per_step": ms_graph, "ms_per_step_eager": ms_eager,
+           "steps_timed": timed, "replicas": R,
+           "hbm_gbs_step": layer_res["algo_bytes_step"] / (ms_graph * 1e-3) / 1e9,
+           "vs_moe_ffn": layer_res["ms_per_step"] / ms_graph}
+    log(f"[island {name}] {res['tok_per_s']:.0f} tok/s, {ms_graph * 1e3:.1f} us/step (eager {ms_eager * 1e3:.1f} us); "
+        f"llapis_moe_ffn {layer_res['ms_per_step'] * 1e3:.1f} us/step: island at {res['vs_moe_ffn']:.2f}x its rate")
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_graph(wl, steps, warmup):
     """Capture R consecutive steps (one pass over the replicas) in a HIP graph
     and K mod R steps in a second one; time exactly K steps of replays."""
@@ -708,8 +746,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn",
-                    help="comma list of iq2s,q4k,dual,prefill,q4stream,stack,promote,stackdyn")
+    ap.add_argument("--configs", default="iq2s,q4k,dual,island,prefill,q4stream,stack,promote,stackdyn",
+                    help="comma list of iq2s,q4k,dual,island,prefill,q4stream,stack,promote,stackdyn (island: "
+                         "the operator-boundary path beside each decode config run)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--engine-wgs", type=int, default=0,
                     help="stackdyn: the promotion engine's copy mode (0 hipMemcpyAsync, else copy-kernel workgroups)")
@@ -754,12 +793,19 @@ def main():
 
     import copy
     results = {}
+    island = {}
     if "iq2s" in cfgs:
         cold_only = copy.copy(full)
         cold_only.residency = la.Residency.from_hot(spec.n_expert, [])
         results["iq2s"] = run_config(la, torch, "decode all-IQ2_S T=1", cold_only, 1, args.steps, args.warmup, dev)
+        if "island" in cfgs:
+            island["iq2s"] = run_island(la, torch, "decode all-IQ2_S T=1", cold_only, 1, args.steps, args.warmup,
+                                        dev, results["iq2s"])
     if "q4k" in cfgs:
         results["q4k"] = run_config(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev)
+        if "island" in cfgs:
+            island["q4k"] = run_island(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev,
+                                       results["q4k"])
     if any(c in cfgs for c in ("dual", "prefill", "q4stream", "promote")):
         dual = copy.copy(full)
         gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
@@ -771,6 +817,9 @@ def main():
         log(f"dual: router bias puts {frac:.2f} of picks on the 57 hot experts")
         if "dual" in cfgs:
             results["dual"] = run_config(la, torch, "decode dual K=57 T=4", dual, 4, args.steps, args.warmup, dev)
+            if "island" in cfgs:
+                island["dual"] = run_island(la, torch, "decode dual K=57 T=4", dual, 4, args.steps, args.warmup, dev,
+                                            results["dual"])
         if "prefill" in cfgs:
             results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
@@ -784,6 +833,8 @@ def main():
         if "promote" in cfgs:
             results["promote"] = run_promote(la, torch, full, dual, spec, dev)
 
+    if island:
+        results["island"] = island
     if "stack" in cfgs:
         results["stack"] = run_stack(la, torch, full, spec, dev)
     if "stackdyn" in cfgs:

@@ -99,7 +99,9 @@ int32_t  llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace
  * to the lower index), w = p[ids] / max(sum p[ids], 6.103515625e-5).
  * x [T][d], W_r [n_expert][d] (ggml ne0 = d), bias [n_expert] or NULL,
  * ids/w [T][top_k], probs [T][n_expert] (required: it also holds the logits
- * between the two kernels).  n_expert <= 256, top_k <= 16. */
+ * between the two kernels).  n_expert <= 256, top_k <= 16, d a multiple of
+ * 4.  The logits are computed in the same order as llapis_moe_ffn's decode
+ * path, so both route a token alike. */
 int32_t llapis_router_topk(const float * x, int32_t n_tokens, const float * w_r, const float * bias,
                            int32_t d, int32_t n_expert, int32_t top_k,
                            int32_t * ids, float * weights, float * probs, void * stream);

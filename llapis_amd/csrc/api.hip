@@ -46,6 +46,23 @@ int32_t fail(const std::string & msg) {
         if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1}, g_fused_fire{1};
+
+// the largest LDS allocation of one workgroup on the current device (cached)
+int max_lds_per_wg() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 65536;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+    cache[dev] = v;
+    return v;
+}
+
 std::atomic<int> g_act_mode{LLAPIS_ACT_CPU};
 std::atomic<int> g_gelu_mode{LLAPIS_GELU_TABLE};
 
@@ -408,6 +425,45 @@ int32_t llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace,
     if (!supported_w(w_hot->type) || w_hot->type == T_F32 || !supported_w(w_cold->type))
         return fail("llapis_moe_dual_compute: unsupported pool type");
 
+    // one kernel per fire when the formats and sizes allow it (and no
+    // per-slot pointer table overrides the hot slab); otherwise the island
+    const bool k256 = a.kind == 0 && (w_hot->type == T_Q4_K || w_hot->type == T_IQ2_S) &&
+                      (w_cold->type == T_Q4_K || w_cold->type == T_IQ2_S) && a.d_in % 256 == 0 && a.d_in <= 3072;
+    const bool k32 = a.kind == 1 && (w_hot->type == T_Q5_0 || w_hot->type == T_IQ4_NL) &&
+                     (w_cold->type == T_Q5_0 || w_cold->type == T_IQ4_NL) && a.d_in % 64 == 0 && a.d_in <= 1024;
+    const bool table = a.il >= 0 && a.il < 128 && g_hot_tab[a.il][a.kind].ptrs && g_hot_tab[a.il][a.kind].n == a.k;
+    if (g_fused_fire.load() && (k256 || k32) && !table && a.n_expert <= 256 && a.k <= 256) {
+        const long long t0 = now_ns();
+        FireParams f = {};
+        f.kind = a.kind; f.d_in = a.d_in; f.d_out = a.d_out; f.n_used = a.n_used; f.n_tokens = a.n_tokens;
+        f.ids_s1 = a.ids_s1; f.n_expert = a.n_expert; f.k_slots = w_hot->data ? a.k : 0;
+        f.cur = static_cast<const float *>(a.cur);
+        f.ids = static_cast<const int32_t *>(a.ids);
+        f.exp_slot = static_cast<const int32_t *>(a.exp_slot);
+        f.slot_exp = static_cast<const int32_t *>(a.slot_exp);
+        f.slot_state = static_cast<const int32_t *>(a.slot_state);
+        f.hot = static_cast<const uint8_t *>(w_hot->data);
+        f.hot_stride = rbytes(w_hot->type, a.d_in) * (uint64_t)a.d_out;
+        f.cold = static_cast<const uint8_t *>(w_cold->data);
+        f.cold_stride = rbytes(w_cold->type, a.d_in) * (uint64_t)a.d_out;
+        f.s_hot = static_cast<const float *>(a.s_hot);
+        f.s_cold = static_cast<const float *>(a.s_cold);
+        f.dst = static_cast<float *>(a.dst);
+        if (g_rc.on && a.kind == 0 && a.il >= 0 && a.il < g_rc.nl) {
+            f.rc_counts = g_rc.dev + (size_t)a.il * g_rc.ne;
+            f.rc_hits = g_rc.dev + (size_t)g_rc.nl * g_rc.ne + (size_t)a.il * 2;
+        }
+        const int rb = (int)std::max(rbytes(w_hot->type, a.d_in), rbytes(w_cold->type, a.d_in));
+        f.w_lds = dev::align16(16 * rb + 32);
+        if (fire_lds(f, w_hot->type, w_cold->type) + 16 * 1024 <= max_lds_per_wg()) {
+            LL_TRY(launch_fire(f, w_hot->type, w_cold->type, g_act_mode.load(), (hipStream_t)stream));
+            dir_gate_after_fire(a.il, a.kind, (hipStream_t)stream);
+            g_op_ns += now_ns() - t0;
+            ++g_fires;
+            return 0;
+        }
+    }
+
     HostCtx hc;
     hc.base = static_cast<uint8_t *>(workspace);
     hc.cap = ws_bytes;
@@ -519,22 +575,6 @@ int32_t llapis_profile_read(float * ms, int32_t n) {
 // ------------------------------------------------------------- fused layer
 
 namespace {
-std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1};
-
-// the largest LDS allocation of one workgroup on the current device (cached)
-int max_lds_per_wg() {
-    static std::mutex mu;
-    static std::map<int, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 65536;
-    std::lock_guard<std::mutex> lk(mu);
-    auto it = cache.find(dev);
-    if (it != cache.end()) return it->second;
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
-    cache[dev] = v;
-    return v;
-}
 
 uint64_t al256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
@@ -627,6 +667,7 @@ void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 2) g_prefill = value != 0;
     if (key == 3) g_dn_rows_log2 = value >= 0 && value <= 5 ? value : -1;
     if (key == 4) g_dn_by_group = value == 0 || value == 1 ? value : -1;
+    if (key == 6) g_fused_fire = value != 0;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {

@@ -49,6 +49,7 @@ namespace dev {
 __constant__ Iq2sTables c_iq2s_tab_dec = make_iq2s_tables();
 
 template <int T> constexpr bool k256() { return T == T_Q4_K || T == T_IQ2_S; }
+inline bool k256_type(int t) { return t == T_Q4_K || t == T_IQ2_S; }
 static_assert(DEC_MAXT == 4, "one member column per wave in the gate_up epilogue");
 
 __device__ __forceinline__ int member(const GroupInfo & g, int i) {
@@ -1061,6 +1062,242 @@ __global__ __launch_bounds__(WG) void k_dec_combine(const DecParams p) {
     p.out[i] = o;
 }
 
+// ------------------------------------------------------------ fires
+
+// One fire of the dual op (the reference's moert_ffn_moe: partition, gather,
+// hot and cold mul_mat_id, scatter; ffn_moe.cu:892-1246) as one kernel:
+// workgroup (b, p) computes output rows of routed pair p (p = t n_used + j,
+// expert ids[t ids_s1 + j]) from the hot slab when the residency predicate
+// holds (ffn_moe.cu:80-130: exp_slot[e] = s, slot_state[s] READY,
+// slot_exp[s] = e) and from the cold pool otherwise, into dst[p]; the down
+// fire (kind 1) scales by the expert's .scale, as the island's scatter does.
+// A pair with an invalid id gets zeros.  Every workgroup reads its pair's id
+// and the whole residency mirrors in one round of loads (no chain of
+// dependent loads), then its rows' weights.
+
+struct FireRes {
+    int tier, idx;              // 0 hot (slot), 1 cold (expert), 2 invalid id
+};
+
+// the pair's id and tier from the mirrors, staged through LDS (s_m: 3 x 256)
+__device__ __forceinline__ FireRes fire_resolve(const FireParams & f, int p, int32_t (*s_m)[256], int * e_out) {
+    const int t = p / f.n_used, j = p - t * f.n_used;
+    const int e = f.ids[(int64_t)t * f.ids_s1 + j];
+    const int ks = f.k_slots, E = f.n_expert;
+    {
+        const int32_t * dummy = f.ids;
+        const int is = ks > 0 ? min((int)threadIdx.x, ks - 1) : 0;
+        const int32_t a = ks > 0 ? f.exp_slot[min((int)threadIdx.x, E - 1)] : dummy[0];
+        const int32_t b = ks > 0 ? f.slot_exp[is] : dummy[0];
+        const int32_t c = ks > 0 ? f.slot_state[is] : dummy[0];
+        s_m[0][threadIdx.x] = a;
+        s_m[1][threadIdx.x] = b;
+        s_m[2][threadIdx.x] = c;
+    }
+    __syncthreads();
+    FireRes r = {2, 0};
+    if (e >= 0 && e < E) {
+        r.tier = 1;
+        r.idx = e;
+        if (ks > 0) {
+            const int sl = s_m[0][e];
+            if (sl >= 0 && sl < ks && s_m[2][sl] == 2 && s_m[1][sl] == e) {
+                r.tier = 0;
+                r.idx = sl;
+            }
+        }
+    }
+    *e_out = e;
+    return r;
+}
+
+// the routing counters of a gate_up fire (k_partition's counts), once per pair
+__device__ __forceinline__ void fire_count(const FireParams & f, int e, const FireRes & r) {
+    if (f.rc_counts && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (e >= 0 && e < f.n_expert) atomicAdd(f.rc_counts + e, 1);
+        if (f.rc_hits) atomicAdd(f.rc_hits + (r.tier == 0 ? 0 : 1), 1);
+    }
+}
+
+constexpr int FIRE_GU_ROWS = 16;        // output rows per workgroup, 256-value block formats
+constexpr int FIRE_GU_LOADS = 7;        // 16-byte weight chunks per thread in flight (16 Q4_K rows of 2816)
+constexpr int FIRE_XV = 12;             // fp32 input values per lane (d_in <= 3072)
+
+// q8_K of 256-block b held as v[j] = x[256 b + lane + 64 j] by one wave
+// (ggml-quants.c:2696-2733, as q8K_block computes it from memory)
+__device__ __forceinline__ void q8K_block_v(uint8_t * base, const ActView & L, const float (&v)[4], int b) {
+    const int lane = threadIdx.x & 63;
+    int8_t * q = reinterpret_cast<int8_t *>(base + L.q);
+    float * dK = reinterpret_cast<float *>(base + L.dK);
+    int * bsum = reinterpret_cast<int *>(base + L.bsum);
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = wave_max_dpp(amax);
+    float max = 0.0f;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+        const uint64_t m = __ballot(fabsf(v[j]) == amax);
+        if (m) max = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), (int)__builtin_ctzll(m)));
+    }
+    int qi[4];
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qi[j] = 0;
+        if (lane == 0) dK[b] = 0.0f;
+    } else {
+        const float iscale = -127.f / max;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = (int)rintf(__fmul_rn(iscale, v[j]));
+            qi[j] = r < 127 ? r : 127;
+        }
+        if (lane == 0) dK[b] = 1.0f / iscale;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        q[b * 272 + lane + 64 * j] = (int8_t)qi[j];
+        const int s = row16_sum(qi[j]);
+        if ((lane & 15) == 0) bsum[b * 16 + (lane >> 4) + 4 * j] = s;
+    }
+}
+
+// gate_up fire (Q4_K / IQ2_S weights, d_in a multiple of 256, <= 3072):
+// 16 rows of one pair per workgroup, staged through LDS like the decode
+// path's gate_up items; the token's column quantised here (q8_K, or q8_1 in
+// the GPU activation mode).
+template <int HT, int CT, int AM>
+__global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
+    __shared__ int32_t s_m[3][256];
+    const int p = blockIdx.y, d_in = f.d_in, r0 = blockIdx.x * FIRE_GU_ROWS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = p / f.n_used;
+    // 1. the column's values and the codebook (no dependence on the routing)
+    const float * x = f.cur + (int64_t)t * d_in;
+    float xv[FIRE_XV];
+#pragma unroll
+    for (int i = 0; i < FIRE_XV; ++i) {
+        const int pos = AM == AM_CPU ? 256 * (wave + 4 * (i / 4)) + lane + 64 * (i % 4) : 64 * (wave + 4 * i) + lane;
+        xv[i] = x[min(pos, d_in - 1)];
+    }
+    u32x4 tab[TAB_CHUNKS / WG];
+    if (IQ2) {
+#pragma unroll
+        for (int k = 0; k < TAB_CHUNKS / WG; ++k)
+            tab[k] = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_dec)[threadIdx.x + k * WG];
+    }
+    // 2. the pair's tier, then its rows
+    int e;
+    const FireRes rs = fire_resolve(f, p, s_m, &e);
+    if (f.kind == 0) fire_count(f, e, rs);
+    GroupInfo gi = {};
+    gi.tier = rs.tier;
+    gi.idx = rs.idx;
+    gi.n_mem = 1;
+    const int nr = min(FIRE_GU_ROWS, f.d_out - r0);
+    const Span sp = make_span(gi, r0, nr, d_in, HT, CT, f.hot, f.hot_stride, f.cold, f.cold_stride, f.ids);
+    Regs<FIRE_GU_LOADS> st;
+    span_load(st, sp);
+    // 3. the column's q8 into LDS (after the rows), the codebook after it
+    const int a0 = f.w_lds;
+    ActView av[1], L0;                      // av: offsets from smem (the dots), L0: from the column
+    const int abytes = act_layout(d_in, a0, &av[0]);
+    act_layout(d_in, 0, &L0);
+    if (AM == AM_CPU) {
+#pragma unroll
+        for (int k = 0; k < FIRE_XV / 4; ++k) {
+            const int b = wave + 4 * k;
+            if (b < d_in / 256) {
+                const float v[4] = {xv[4 * k], xv[4 * k + 1], xv[4 * k + 2], xv[4 * k + 3]};
+                q8K_block_v(smem + a0, L0, v, b);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FIRE_XV; ++i) {
+            const int pos = 64 * (wave + 4 * i) + lane;
+            if (64 * (wave + 4 * i) < d_in) q8_32_put<AM_Q8_1>(smem + a0, L0, xv[i], pos, pos < d_in);
+        }
+    }
+    const int grid_off = align16i(a0 + abytes);
+    if (IQ2) {
+#pragma unroll
+        for (int k = 0; k < TAB_CHUNKS / WG; ++k)
+            reinterpret_cast<u32x4 *>(smem + grid_off)[threadIdx.x + k * WG] = tab[k];
+    }
+    span_store(st, sp, smem);
+    __syncthreads();
+    // 4. one row per 16 lanes
+    const int row = threadIdx.x >> 4;
+    const bool live = sp.valid != 0 && row < nr;
+    float acc[1];
+    rows_dot<HT, CT, AM, 1>(smem, sp.off + row * sp.rb, gi.tier, 1, d_in, live, av, acc, grid_off);
+    if ((threadIdx.x & 15) == 0 && row < nr) f.dst[(int64_t)p * f.d_out + r0 + row] = live ? acc[0] : 0.0f;
+}
+
+// down fire (Q5_0 / IQ4_NL weights, d_in a multiple of 64, <= 1024): 32 rows
+// of one pair per workgroup, each row's block pairs loaded straight into
+// registers (as the decode path's down kernels do), the pair's column
+// quantised here (q8_0, or q8_1), y = .scale W a.
+template <int HD, int CD, int AM>
+__global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int32_t s_m[3][256];
+    constexpr int NPS = 2, R = NPS * DN_RPP;
+    const int p = blockIdx.y, F = f.d_in, D = f.d_out, r0 = blockIdx.x * R, nr = max(0, min(R, D - r0));
+    const int F4 = F / 4, NP = F / 64;
+    // 1. the pair's column (fp32), then its tier
+    const u32x4 a4 = reinterpret_cast<const u32x4 *>(f.cur + (int64_t)p * F)[min((int)threadIdx.x, F4 - 1)];
+    int e;
+    const FireRes rs = fire_resolve(f, p, s_m, &e);
+    if (f.kind == 0) fire_count(f, e, rs);
+    // 2. the rows' block pairs
+    const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
+    const int pl = min(lane16, NP - 1);
+    const int tier = rs.tier < 2 ? rs.tier : 1, idx = rs.tier < 2 ? rs.idx : 0;
+    const int wt = tier == 0 ? HD : CD;
+    const int rbytes = (F / 32) * blk_bytes(wt);
+    const uint8_t * slab = tier == 0 ? f.hot + (uint64_t)idx * f.hot_stride : f.cold + (uint64_t)idx * f.cold_stride;
+    DnPair w[NPS];
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+        const int r = min(ps * DN_RPP + lrow, max(nr - 1, 0));
+        const uint8_t * src = slab + (uint64_t)(r0 + r) * rbytes + (uint64_t)pl * (2 * blk_bytes(wt));
+        if (tier == 0) dn_pair_load<HD>(w[ps], src);
+        else dn_pair_load<CD>(w[ps], src);
+    }
+    // 3. the column's q8 in LDS
+    ActView L;
+    act_layout(F, 0, &L);
+    {
+        const float v[4] = {__uint_as_float(a4.x), __uint_as_float(a4.y), __uint_as_float(a4.z), __uint_as_float(a4.w)};
+        q8_quad<AM>(smem, L, v, threadIdx.x, (int)threadIdx.x < F4);
+    }
+    __syncthreads();
+    const float scale = f.kind == 1 ? (rs.tier == 0 ? (f.s_hot ? f.s_hot[rs.idx] : 1.0f)
+                                                    : (rs.tier == 1 ? (f.s_cold ? f.s_cold[rs.idx] : 1.0f) : 0.0f))
+                                    : (rs.tier < 2 ? 1.0f : 0.0f);
+    // 4. the rows
+#pragma unroll
+    for (int ps = 0; ps < NPS; ++ps) {
+        const int r = ps * DN_RPP + lrow;
+        float acc = 0.0f;
+        if (lane16 < NP && rs.tier < 2) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const Act32 a = act32<AM>(smem, L, 2 * lane16 + h);
+                acc += tier == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a))
+                                 : (CD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a));
+            }
+        }
+#pragma unroll
+        for (int o = DN_LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, DN_LPR);
+        if (lane16 == 0 && r < nr) f.dst[(int64_t)p * D + r0 + r] = acc * scale;
+    }
+}
+
 __global__ void k_zero(int * p, int n) {
     for (int i = blockIdx.x * WG + threadIdx.x; i < n; i += gridDim.x * WG) p[i] = 0;
 }
@@ -1176,6 +1413,37 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
 #undef LL_DN2
 #undef LL_DN
         if (p.dn_by_group) launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
+    }
+    return hipGetLastError();
+}
+
+int fire_lds(const FireParams & f, int ht, int ct) {
+    if (k256_type(ht)) {
+        const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
+        return align16i(f.w_lds + dec_act_bytes(f.d_in)) + (iq2 ? (int)sizeof(Iq2sTables) : 0);
+    }
+    return dec_act_bytes(f.d_in);
+}
+
+hipError_t launch_fire(const FireParams & f, int ht, int ct, int am, hipStream_t s) {
+    const int P = f.n_used * f.n_tokens;
+    const int lds = fire_lds(f, ht, ct);
+    if (k256_type(ht)) {
+        const dim3 grid((f.d_out + FIRE_GU_ROWS - 1) / FIRE_GU_ROWS, P);
+#define LL_F(A, B, M) if (ht == A && ct == B && am == M) hipLaunchKernelGGL((k_fire_k256<A, B, M>), grid, dim3(WG), lds, s, f); else
+#define LL_F2(A, B) LL_F(A, B, AM_CPU) LL_F(A, B, AM_Q8_1)
+        LL_F2(T_Q4_K, T_IQ2_S) LL_F2(T_Q4_K, T_Q4_K) LL_F2(T_IQ2_S, T_IQ2_S) LL_F2(T_IQ2_S, T_Q4_K)
+        return hipErrorInvalidValue;
+#undef LL_F2
+#undef LL_F
+    } else {
+        const dim3 grid((f.d_out + 2 * DN_RPP - 1) / (2 * DN_RPP), P);
+#define LL_F(A, B, M) if (ht == A && ct == B && am == M) hipLaunchKernelGGL((k_fire_k32<A, B, M>), grid, dim3(WG), lds, s, f); else
+#define LL_F2(A, B) LL_F(A, B, AM_CPU) LL_F(A, B, AM_Q8_1)
+        LL_F2(T_Q5_0, T_IQ4_NL) LL_F2(T_Q5_0, T_Q5_0) LL_F2(T_IQ4_NL, T_IQ4_NL) LL_F2(T_IQ4_NL, T_Q5_0)
+        return hipErrorInvalidValue;
+#undef LL_F2
+#undef LL_F
     }
     return hipGetLastError();
 }

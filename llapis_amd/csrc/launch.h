@@ -101,6 +101,24 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
                          hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);
 
+// One fire of the dual op in one kernel (the island's partition, gather,
+// mul_mat_id and scatter fused): see k_fire_k256 / k_fire_k32.
+struct FireParams {
+    int kind, d_in, d_out, n_used, n_tokens, ids_s1, n_expert, k_slots;
+    const float * cur;          // kind 0: [n_tokens][d_in] token columns; kind 1: [n_tokens * n_used][d_in]
+    const int32_t * ids;        // [n_tokens] rows of stride ids_s1
+    const int32_t * exp_slot; const int32_t * slot_exp; const int32_t * slot_state;
+    const uint8_t * hot; uint64_t hot_stride;     // slab bytes per slot
+    const uint8_t * cold; uint64_t cold_stride;   // slab bytes per expert
+    const float * s_hot; const float * s_cold;
+    float * dst;                // [n_tokens * n_used][d_out]
+    int32_t * rc_counts;        // routing counters of a gate_up fire, or NULL
+    int32_t * rc_hits;
+    int w_lds;                  // LDS bytes of 16 staged rows (256-value block formats)
+};
+int fire_lds(const FireParams & f, int ht, int ct);
+hipError_t launch_fire(const FireParams & f, int ht, int ct, int act_mode, hipStream_t s);
+
 // ------------------------------------------------------------ prefill path
 
 constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)

@@ -9,46 +9,55 @@ namespace dev {
 
 // ------------------------------------------------------------- router
 
-constexpr int ROUTER_TOK = 8;    // tokens per wave (the expert row stays in registers)
+constexpr int ROUTER_TOK = 4;    // tokens per workgroup of k_router_logits
 
-// logits[t][e] = W_r[e] . x[t] (+ bias[e]); one wave per (expert, 8 tokens)
-// (build_lora_mm(gate_inp, cur), llama-graph.cpp:1541; ggml mul_mat f32).
+// logits[t][e] = W_r[e] . x[t] (+ bias[e]) (build_lora_mm(gate_inp, cur),
+// llama-graph.cpp:1541; ggml mul_mat f32): one workgroup per (expert, 4
+// tokens), every load of the row and the tokens issued before the first
+// product (one memory round trip for d <= 4096); per-thread partial sums
+// over its float4s in order, a wave sum, the four waves' sums in order --
+// the decode path's router arithmetic, so both give the same logits.
 __global__ __launch_bounds__(WG) void k_router_logits(const float * __restrict__ x, int T,
                                                       const float * __restrict__ w_r, const float * __restrict__ bias,
                                                       int d, int E, float * __restrict__ logits) {
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * (WG / 64) + (threadIdx.x >> 6);
-    if (e >= E) return;                         // whole wave leaves; no barriers below
-    const int t0 = blockIdx.y * ROUTER_TOK;
-    const int nt = min(ROUTER_TOK, T - t0);
-    const float * wrow = w_r + (int64_t)e * d;
+    constexpr int RU = 4;
+    __shared__ float s_part[ROUTER_TOK][WG / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x, t0 = blockIdx.y * ROUTER_TOK, nt = min(ROUTER_TOK, T - t0), n4 = d / 4;
+    const float4 * wrow = reinterpret_cast<const float4 *>(w_r + (int64_t)e * d);
+    const float4 * x4 = reinterpret_cast<const float4 *>(x);
+    const float b = bias ? bias[e] : 0.0f;
     float acc[ROUTER_TOK];
 #pragma unroll
     for (int j = 0; j < ROUTER_TOK; ++j) acc[j] = 0.0f;
-    if ((d & 3) == 0) {
-        for (int k = 4 * lane; k < d; k += 256) {
-            const float4 w4 = *reinterpret_cast<const float4 *>(wrow + k);
+    for (int k0 = threadIdx.x; k0 < n4; k0 += RU * WG) {
+        float4 w4[RU], xv[ROUTER_TOK][RU];
 #pragma unroll
-            for (int j = 0; j < ROUTER_TOK; ++j) {
-                if (j < nt) {
-                    const float4 x4 = *reinterpret_cast<const float4 *>(x + (int64_t)(t0 + j) * d + k);
-                    acc[j] += w4.x * x4.x + w4.y * x4.y + w4.z * x4.z + w4.w * x4.w;
-                }
-            }
-        }
-    } else {
-        for (int k = lane; k < d; k += 64) {
-            const float w = wrow[k];
+        for (int u = 0; u < RU; ++u) w4[u] = wrow[min(k0 + u * WG, n4 - 1)];
 #pragma unroll
-            for (int j = 0; j < ROUTER_TOK; ++j)
-                if (j < nt) acc[j] += w * x[(int64_t)(t0 + j) * d + k];
-        }
+        for (int j = 0; j < ROUTER_TOK; ++j)
+#pragma unroll
+            for (int u = 0; u < RU; ++u) xv[j][u] = x4[(int64_t)(t0 + min(j, nt - 1)) * n4 + min(k0 + u * WG, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < ROUTER_TOK; ++j)
+#pragma unroll
+            for (int u = 0; u < RU; ++u)
+                if (j < nt && k0 + u * WG < n4)
+                    acc[j] += w4[u].x * xv[j][u].x + w4[u].y * xv[j][u].y + w4[u].z * xv[j][u].z +
+                              w4[u].w * xv[j][u].w;
     }
-    const float b = bias ? bias[e] : 0.0f;
 #pragma unroll
     for (int j = 0; j < ROUTER_TOK; ++j) {
-        const float s = wave_sum(acc[j]);
-        if (lane == 0 && j < nt) logits[(int64_t)(t0 + j) * E + e] = s + b;
+        const float sj = wave_sum_dpp(acc[j]);
+        if (lane == 0) s_part[j][wave] = sj;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nt) {
+        const int j = threadIdx.x;
+        float sj = 0.0f;
+#pragma unroll
+        for (int q = 0; q < WG / 64; ++q) sj += s_part[j][q];
+        logits[(int64_t)(t0 + j) * E + e] = sj + b;
     }
 }
 
@@ -325,7 +334,8 @@ using namespace dev;
 
 hipError_t launch_router_logits(const float * x, int T, const float * w_r, const float * bias, int d, int E,
                                 float * logits, hipStream_t s) {
-    dim3 grid((E + 3) / 4, (T + ROUTER_TOK - 1) / ROUTER_TOK);
+    if (d % 4) return hipErrorInvalidValue;
+    dim3 grid(E, (T + ROUTER_TOK - 1) / ROUTER_TOK);
     hipLaunchKernelGGL(k_router_logits, grid, dim3(WG), 0, s, x, T, w_r, bias, d, E, logits);
     return hipGetLastError();
 }

@@ -197,25 +197,34 @@ def test_layer_vs_oracle(gpu, oracle, spec_name, n_hot, T, scales, act_mode, gel
     assert err <= 1e-4
 
 
-def test_island_fires_match_layer(gpu, oracle):
-    """gate_up and down through moert_ffn_moe (the reference's operator
-    boundary) give the oracle's per-pair matvecs."""
+@pytest.mark.parametrize("fused", [1, 0])
+@pytest.mark.parametrize("act_mode", [la.ACT_CPU, la.ACT_Q8_1])
+@pytest.mark.parametrize("T", [1, 4])
+def test_island_fires_match_layer(gpu, oracle, fused, act_mode, T):
+    """gate_up and down through the dual op (the reference's operator
+    boundary) give the oracle's per-pair matvecs: as one kernel per fire
+    (fused 1) and through moert_ffn_moe's partition, gather, mul_mat_id and
+    scatter (fused 0, tuning key 6)."""
     torch = torch_mod()
-    say("island fires")
+    say(f"island fires fused={fused} act={act_mode} T={T}")
     spec = FULL16
     lay = _layer_case(spec, 55, 5, True)
-    dl = la.DeviceLayer(lay, gpu)
-    T = 4
+    dl = la.DeviceLayer(lay, gpu, act_mode, la.GELU_TABLE)
     x = tokens(90, T, spec.d_model)
     xd = torch.from_numpy(x).to(gpu)
     ids, w, _ = dl.router(xd)
     # a strided ids view, as argsort_top_k hands the op (row stride n_expert)
     ids_full = torch.full((T, spec.n_expert), -7, dtype=torch.int32, device=gpu)
     ids_full[:, : spec.top_k] = ids
-    gu = dl.moe_dual(0, xd, ids_full, il=0, ids_row_stride=spec.n_expert)
-    act = la.geglu(gu.reshape(-1, 2 * spec.n_ff).contiguous(), spec.n_ff)
-    dn = dl.moe_dual(1, act, ids_full, il=0, ids_row_stride=spec.n_expert)
-    torch.cuda.synchronize()
+    lib = la.lib()
+    lib.llapis_set_tuning(6, fused)
+    try:
+        gu = dl.moe_dual(0, xd, ids_full, il=0, ids_row_stride=spec.n_expert)
+        act = la.geglu(gu.reshape(-1, 2 * spec.n_ff).contiguous(), spec.n_ff)
+        dn = dl.moe_dual(1, act, ids_full, il=0, ids_row_stride=spec.n_expert)
+        torch.cuda.synchronize()
+    finally:
+        lib.llapis_set_tuning(6, 1)
     ids_h = ids.cpu().numpy()
     gu_h, act_h, dn_h = gu.cpu().numpy(), act.cpu().numpy(), dn.cpu().numpy()
     res = lay.residency
@@ -230,9 +239,9 @@ def test_island_fires_match_layer(gpu, oracle):
             gpool = lay.hot_gu if hot else lay.cold_gu
             dpool = lay.hot_dn if hot else lay.cold_dn
             gb, db = spec.gu_bytes(gut), spec.dn_bytes(dnt)
-            yo = oracle.matvec(gut, la.ACT_CPU, gpool[idx * gb:(idx + 1) * gb], 2 * spec.n_ff, spec.d_model, x[t])
+            yo = oracle.matvec(gut, act_mode, gpool[idx * gb:(idx + 1) * gb], 2 * spec.n_ff, spec.d_model, x[t])
             assert rel_l2(gu_h[t, k], yo) <= 2e-6
-            do = oracle.matvec(dnt, la.ACT_CPU, dpool[idx * db:(idx + 1) * db], spec.d_model, spec.n_ff,
+            do = oracle.matvec(dnt, act_mode, dpool[idx * db:(idx + 1) * db], spec.d_model, spec.n_ff,
                                act_h[t * spec.top_k + k])
             sc = (lay.s_hot[s] if hot else lay.s_cold[e])
             assert rel_l2(dn_h[t, k], do * sc) <= 2e-6
