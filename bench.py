@@ -746,8 +746,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--configs", default="iq2s,q4k,dual,island,prefill,q4stream,stack,promote,stackdyn",
-                    help="comma list of iq2s,q4k,dual,island,prefill,q4stream,stack,promote,stackdyn (island: "
+    ap.add_argument("--configs", default="iq2s,q4k,dual,island,prefill,prefill_q81,q4stream,stack,promote,stackdyn",
+                    help="comma list of iq2s,q4k,dual,island,prefill,prefill_q81,q4stream,stack,promote,stackdyn (island: "
                          "the operator-boundary path beside each decode config run)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--engine-wgs", type=int, default=0,
@@ -786,7 +786,8 @@ def main():
     t0 = time.time()
     # all fp32 expert weights are generated once per expert; each tier is
     # quantised from the same floats (seed 1)
-    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "q4stream", "stack", "promote", "stackdyn"))
+    need_hot = any(c in cfgs for c in ("q4k", "dual", "prefill", "prefill_q81", "q4stream", "stack", "promote",
+                                       "stackdyn"))
     prior, hot57 = la.zipf_hot_set(spec.n_expert, 57, 7)
     full = la.make_layer(spec, 1, list(range(spec.n_expert)) if need_hot else [], cold=True)
     log(f"quantised {spec.n_expert} experts x {'4' if need_hot else '2'} formats in {time.time() - t0:.1f} s")
@@ -806,7 +807,7 @@ def main():
         if "island" in cfgs:
             island["q4k"] = run_island(la, torch, "decode all-Q4_K T=1", full, 1, args.steps, args.warmup, dev,
                                        results["q4k"])
-    if any(c in cfgs for c in ("dual", "prefill", "q4stream", "promote")):
+    if any(c in cfgs for c in ("dual", "prefill", "prefill_q81", "q4stream", "promote")):
         dual = copy.copy(full)
         gb, db = spec.gu_bytes(spec.hot_gu_type), spec.dn_bytes(spec.hot_dn_type)
         dual.hot_gu = np.concatenate([full.hot_gu[e * gb:(e + 1) * gb] for e in hot57])
@@ -823,6 +824,11 @@ def main():
         if "prefill" in cfgs:
             results["prefill"] = run_config(la, torch, "prefill dual K=57 T=512", dual, 512,
                                             max(10, args.steps // 40), max(2, args.warmup // 20), dev)
+        if "prefill_q81" in cfgs:
+            # the same chunk in the reference GPU path's activation mode (q8_1, GELU tanh)
+            results["prefill_q81"] = run_config(la, torch, "prefill dual K=57 T=512 q8_1", dual, 512,
+                                                max(10, args.steps // 40), max(2, args.warmup // 20), dev,
+                                                act=1, gelu=1)
         if "q4stream" in cfgs:
             # q4stream: the same chunk with every expert at the hot precision,
             # read from the all-expert hot source (identity page table)

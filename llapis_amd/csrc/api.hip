@@ -626,10 +626,10 @@ bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
            (L->d_model % 4) == 0 && L->n_ff <= 1024 && L->n_ff % 64 == 0;
 }
 
-// prefill path (T > DEC_MAXT, CPU activation mode): tokens are processed in
+// prefill path (T > DEC_MAXT, either activation mode): tokens are processed in
 // chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
 struct PfWs {
-    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, ah, al, ydn, parts, total;
+    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, xh, ah, al, ydn, parts, total;
     int Tc, max_tiles;
 };
 PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
@@ -647,7 +647,8 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     w.xq = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
     w.xd = w.xq + al256((uint64_t)w.Tc * D);
     w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
-    w.ah = w.xm + al256((uint64_t)w.Tc * NSB * 32);
+    w.xh = w.xm + al256((uint64_t)w.Tc * NSB * 32);
+    w.ah = w.xh + al256((uint64_t)w.Tc * D * 4);
     w.al = w.ah + al256(P * F * 2);
     w.ydn = w.al + al256(P * F * 2);
     w.parts = w.ydn + al256(P * D * 4);
@@ -656,7 +657,7 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
 }
 
 bool prefill_eligible(const llapis_moe_layer * L, int32_t T) {
-    return g_prefill.load() && T > DEC_MAXT && L->act_mode == LLAPIS_ACT_CPU && L->top_k >= 1 &&
+    return g_prefill.load() && T > DEC_MAXT && L->top_k >= 1 &&
            L->top_k <= PF_MAX_PAIRS && L->n_expert <= 256 && L->n_ff <= PF_MAX_FF && L->d_model % 256 == 0 &&
            L->n_ff % 32 == 0;
 }
@@ -790,6 +791,8 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.xq = (int8_t *)(base + pw.xq);
             p.xd = (float *)(base + pw.xd);
             p.xm = (_Float16 *)(base + pw.xm);
+            p.act_mode = L->act_mode == LLAPIS_ACT_Q8_1 ? dev::AM_Q8_1 : dev::AM_CPU;
+            p.xh = (_Float16 *)(base + pw.xh);
             p.ah = (_Float16 *)(base + pw.ah);
             p.al = (_Float16 *)(base + pw.al);
             p.ydn = (float *)(base + pw.ydn);

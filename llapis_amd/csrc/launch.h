@@ -150,7 +150,10 @@ struct PfParams {
     int max_tiles;
     int8_t * xq;                         // [T][d_model] q8_K values
     float * xd;                          // [T][d_model / 256] q8_K scales
-    _Float16 * xm;                       // [T][d_model / 256][16] per-32 sums as 32 hi + lo
+    _Float16 * xm;                       // [T][d_model / 256][16] q8_K: per-32 sums as 32 hi + lo;
+                                         //   q8_1: per-32 d sum(q) as hi, lo
+    int act_mode;                        // AM_CPU (q8_K / q8_0) or AM_Q8_1
+    _Float16 * xh;                       // [T][d_model / 256][512] q8_1 values d q as fp16 hi (256), lo (256)
     _Float16 * ah;                       // [P][n_ff] down activations d8 q: fp16 high part
     _Float16 * al;                       // [P][n_ff]                        exact remainder
     float * ydn;                         // [P][d_model]

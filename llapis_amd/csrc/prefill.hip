@@ -284,6 +284,44 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
     }
 }
 
+// One wave per (token, 64 values): q8_1 of two 32-blocks as ggml-cuda's
+// quantize_q8_1 computes it (quantize.cu:5-50: d = amax / 127, q =
+// roundf(x / d), d kept as fp16), stored for the fp16 matrix cores: each
+// value d q (at most 19 significant bits) as its exact fp16 hi + lo parts,
+// [token][256-block] {256 hi, 256 lo}; and per 32-block u = d sum(q) (the
+// Q4_K mins term of vecdotq.cuh's q4_K . q8_1) as exact hi + lo,
+// [token][256-block] {hi_0..hi_7, lo_0..lo_7}.
+__global__ __launch_bounds__(WG) void k_pf_quant_x1(const PfParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int D = p.d_model, per = D / 64;
+    const int job = blockIdx.x * (WG / 64) + wave;
+    if (job >= p.T * per) return;                        // whole waves leave
+    const int t = job / per, pos = 64 * (job - t * per) + lane;
+    const float v = p.x[(int64_t)t * D + pos];
+    const float amax = half_max_dpp(fabsf(v));
+    const float d = amax / 127.0f;
+    const int qi = amax == 0.0f ? 0 : (int)roundf(v / d);
+    const float dstore = (float)(_Float16)d;
+    const float xv = dstore * (float)qi;                // exact
+    const _Float16 xh = (_Float16)xv;
+    const _Float16 xl = (_Float16)(xv - (float)xh);     // exact
+    int sq = qi;
+    for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 32);
+    const int sb = pos >> 8, k = pos & 255;
+    _Float16 * row = p.xh + ((int64_t)t * (D / 256) + sb) * 512;
+    row[k] = xh;
+    row[256 + k] = xl;
+    if ((lane & 31) == 0) {
+        const int j = k >> 5;
+        const float u = dstore * (float)sq;             // exact: 11 x 13 bits
+        const _Float16 h = (_Float16)u;
+        const _Float16 l = (_Float16)(u - (float)h);
+        _Float16 * xm = p.xm + ((int64_t)t * (D / 256) + sb) * 16;
+        xm[j] = h;
+        xm[8 + j] = l;
+    }
+}
+
 // -------------------------------------------------------------- gate_up
 
 constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (128 rows x 9)
@@ -343,7 +381,7 @@ __device__ __forceinline__ void q8_store32(float v, _Float16 * hi, _Float16 * lo
     if (live) {
         *hi = h;
         *lo = l;
-        if (AM != AM_CPU && (threadIdx.x & 31) == 0) *s = sstore;
+        if (AM != AM_CPU && s && (threadIdx.x & 31) == 0) *s = sstore;
     }
 }
 
@@ -645,6 +683,335 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     else pf_gate_up_group<HT, CT, GSRC, 4>(p, tile, sm, rb);
 }
 
+// ---------------------------------------------------- gate_up, q8_1 mode
+
+// IQ2_S on fp16 operands: for each 4-bit scale ls, the fp16 bit patterns of
+// the three grid magnitudes {8, 25, 43} times (2 ls + 1) (<= 1333, exact),
+// low bytes in .x and high bytes in .y (byte 3 zero), for v_perm.
+struct Iq2sHalf {
+    uint32_t t[16][2];
+};
+constexpr uint32_t half_bits_of_int(int v) {      // v < 2048, v > 0: exact
+    int e = 0;
+    while ((v >> e) >= 2) ++e;                      // 2^e <= v < 2^(e + 1)
+    const uint32_t mant = (uint32_t)((v << (10 - e)) & 0x3FF);
+    return ((uint32_t)(e + 15) << 10) | mant;
+}
+constexpr Iq2sHalf make_iq2s_half() {
+    Iq2sHalf h{};
+    const int lev[3] = {8, 25, 43};
+    for (int ls = 0; ls < 16; ++ls) {
+        uint32_t lo = 0, hi = 0;
+        for (int c = 0; c < 3; ++c) {
+            const uint32_t b = half_bits_of_int(lev[c] * (2 * ls + 1));
+            lo |= (b & 0xFF) << (8 * c);
+            hi |= (b >> 8) << (8 * c);
+        }
+        h.t[ls][0] = lo;
+        h.t[ls][1] = hi;
+    }
+    return h;
+}
+__constant__ Iq2sHalf c_iq2s_half = make_iq2s_half();
+
+constexpr int PF_XH = 512 + 8;            // halfs per staged token row of one super-block: 256 hi, 256 lo, pad
+constexpr int PF_TOK1 = 32;               // tokens of one q8_1 workgroup (half a group)
+constexpr int GU1_XREG = 8;               // activation chunks per thread per super-block (32 tokens x 64)
+
+struct GuSmemQ1 {
+    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows, as in the q8_K kernel
+    _Float16 x[PF_TOK1 * PF_XH];          // the tokens' d q of this super-block, exact hi and lo parts
+    _Float16 mb[PF_TOK1 * 16];            // their per-32 mins terms u = d sum(q), {hi_0..7, lo_0..7}
+    u32x4 csel[1024];                     // IQ2_S grid: v_perm selectors (lo byte c, hi byte 4 + c) per value pair
+    u32x4 sgnh[256];                      // IQ2_S sign byte: 0x8000 per negative value, per value pair
+    uint2 lsT[16];                        // Iq2sHalf
+    int poff[PF_ROWS];
+    int tok[PF_TOK1], pair[PF_TOK1];
+};
+static_assert(sizeof(GuSmemQ1) <= 80 * 1024, "two workgroups per CU");
+static_assert(PF_ROWS * GU_STP * 4 <= (int)sizeof(GuSmemQ1::x), "epilogue staging fits the activation buffer");
+
+struct GuStageQ1 {
+    u32x4 w[GU_WREG];
+    u32x4 x[GU1_XREG];
+    u32x4 mb;
+};
+
+// One (group half, row block) of the gate_up GEMM in the q8_1 activation mode
+// (ggml-cuda's arithmetic, vecdotq.cuh:504-522 / 864-907): the activation
+// scale is per 32 values, so it is carried by the activation operand -- each
+// value d q as exact fp16 hi + lo parts, two v_mfma_f32_16x16x32_f16 per
+// 32-block -- and the weights are exact fp16 integers with the sub-block
+// scale folded in (Q4_K q sc <= 945, IQ2_S grid (2 ls + 1) <= 1333, both
+// exact).  Every product is exact and one fp32 accumulator chains through the
+// super-block; then d_w per super-block (Q4_K minus dmin times the mins MFMA,
+// IQ2_S d / 8 in the epilogue).  The epilogue is the q8_K kernel's with q8_1
+// down activations.  Workgroup z of a group takes its tokens 32 z ..
+template <int HT, int CT, int GSRC, int NT>
+__device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const PfTile & tile, GuSmemQ1 & sm,
+                                                    const int rb, const int t0, const int n) {
+    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK1 * 64 == GU1_XREG * WG, "staging shape");
+    constexpr int NTOK = 16 * NT;
+    const int wtype = tile.tier == 0 ? HT : CT;
+    const bool q4 = wtype == T_Q4_K;
+    const int F = p.n_ff, D = p.d_model, NSB = D / 256, K = p.top_k;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
+    const int bb = q4 ? 144 : 82;
+    const int nwc = q4 ? 9 : 6;
+    const uint64_t rbytes = (uint64_t)NSB * bb;
+    const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
+                                       : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
+    if (tid < PF_TOK1) {
+        const int qp = p.sorted[tile.begin + t0 + min(tid, n - 1)];
+        sm.pair[tid] = qp;
+        sm.tok[tid] = qp / K;
+    }
+    if (!q4) {
+        // selectors from the level codes (one byte 0..2 per value)
+        const uint2 * codes = reinterpret_cast<const uint2 *>(&c_iq2s_tab_pf);
+        for (int i = tid; i < 1024; i += WG) {
+            const uint2 c = codes[i];
+            u32x4 v;
+            v.x = __builtin_amdgcn_perm(0u, c.x, 0x01010000u) + 0x04000400u;
+            v.y = __builtin_amdgcn_perm(0u, c.x, 0x03030202u) + 0x04000400u;
+            v.z = __builtin_amdgcn_perm(0u, c.y, 0x01010000u) + 0x04000400u;
+            v.w = __builtin_amdgcn_perm(0u, c.y, 0x03030202u) + 0x04000400u;
+            sm.csel[i] = v;
+        }
+        u32x4 sg;
+        sg.x = ((tid & 1) ? 0x8000u : 0u) | ((tid & 2) ? 0x80000000u : 0u);
+        sg.y = ((tid & 4) ? 0x8000u : 0u) | ((tid & 8) ? 0x80000000u : 0u);
+        sg.z = ((tid & 16) ? 0x8000u : 0u) | ((tid & 32) ? 0x80000000u : 0u);
+        sg.w = ((tid & 64) ? 0x8000u : 0u) | ((tid & 128) ? 0x80000000u : 0u);
+        sm.sgnh[tid] = sg;                                      // WG == 256 sign bytes
+        if (tid < 16) sm.lsT[tid] = make_uint2(c_iq2s_half.t[tid][0], c_iq2s_half.t[tid][1]);
+    }
+    __syncthreads();
+
+    uint32_t wrow[GU_WREG], wdst[GU_WREG];
+#pragma unroll
+    for (int k = 0; k < GU_WREG; ++k) {
+        const int i = tid + WG * k;
+        const int r = i / nwc, c = i - nwc * r;
+        const int gi = min(64 * rb + (r & 63), F - 1);
+        const int row = r < 64 ? gi : F + gi;
+        wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)row * rbytes) : ~0u;
+        wdst[k] = (uint32_t)(r * (q4 ? 144 : 96) + 16 * c) | ((uint32_t)c << 16);
+    }
+    const int tok_m = tid < 2 * NTOK ? sm.tok[tid >> 1] * NSB * 16 + 8 * (tid & 1) : 0;
+
+    GuStageQ1 g;
+    auto fetch = [&](int s) {
+#pragma unroll
+        for (int k = 0; k < GU_WREG; ++k) {
+            g.w[k] = u32x4{0, 0, 0, 0};
+            if (wrow[k] != ~0u) {
+                const uint32_t ps = wrow[k] + (uint32_t)(bb * s);
+                const int c = (int)(wdst[k] >> 16);
+                if (q4 || c < chunk_count(ps, 82))
+                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~15u) + 16 * c);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NT * GU1_XREG / 2; ++k) {
+            const int i = tid + WG * k, j = i >> 6, c = i & 63;
+            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xh + ((int64_t)sm.tok[j] * NSB + s) * 512 + 8 * c);
+        }
+        if (q4 && tid < 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
+    };
+    auto store = [&](int s) {
+#pragma unroll
+        for (int k = 0; k < GU_WREG; ++k)
+            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(sm.w + (wdst[k] & 0xFFFF)) = g.w[k];
+#pragma unroll
+        for (int k = 0; k < NT * GU1_XREG / 2; ++k) {
+            const int i = tid + WG * k, j = i >> 6, c = i & 63;
+            *reinterpret_cast<u32x4 *>(sm.x + j * PF_XH + 8 * c) = g.x[k];
+        }
+        if (q4 && tid < 2 * NTOK) *reinterpret_cast<u32x4 *>(sm.mb + 16 * (tid >> 1) + 8 * (tid & 1)) = g.mb;
+        if (tid < PF_ROWS) {
+            const int r = tid;
+            const int gi = min(64 * rb + (r & 63), F - 1);
+            const uint64_t ps = (uint64_t)(r < 64 ? gi : F + gi) * rbytes + (uint64_t)bb * s;
+            sm.poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
+        }
+    };
+
+    f4 y[2][NT];
+#pragma unroll
+    for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+        for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const _Float16 mm = q < 2 ? (_Float16)1.0f : (_Float16)0.0f;
+    const _Float16 mo = q < 2 ? (_Float16)(-1024.0f) : (_Float16)0.0f;
+    const h2 mn_mul = h2{mm, mm}, mn_off = h2{mo, mo};
+    const h2 m1024 = h2{(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+
+    fetch(0);
+#pragma unroll 1
+    for (int s = 0; s < NSB; ++s) {
+        if (s) __syncthreads();
+        store(s);
+        __syncthreads();
+        if (s + 1 < NSB) fetch(s + 1);
+
+        // ---- per row tile: the super-block's header
+        int wo[2];
+        float dr[2], mr[2];
+        h2 scp[2][4];
+        uint2 qh8[2], sc8[2];
+        h8 bm[2];
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) {
+            wo[rs] = sm.poff[32 * wave + 16 * rs + l16];
+            if (q4) {
+                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(sm.w + wo[rs]);
+                dr[rs] = h2f(hdr.x & 0xFFFF);
+                mr[rs] = h2f(hdr.x >> 16);
+                const uint32_t sc03 = hdr.y & 0x3F3F3F3Fu;
+                const uint32_t mn03 = hdr.z & 0x3F3F3F3Fu;
+                const uint32_t sc47 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+                const uint32_t mn47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+                // the 8 scales as fp16 (1024 + sc) - 1024, pairs {sc_2i, sc_2i+1}
+                scp[rs][0] = as_h2(magic_lo(sc03)) + m1024;
+                scp[rs][1] = as_h2(magic_hi(sc03)) + m1024;
+                scp[rs][2] = as_h2(magic_lo(sc47)) + m1024;
+                scp[rs][3] = as_h2(magic_hi(sc47)) + m1024;
+                // mins B operand: k 0..7 and 8..15 = m_j, 16..31 = 0
+                const uint32_t mb4[4] = {magic_lo(mn03), magic_hi(mn03), magic_lo(mn47), magic_hi(mn47)};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const h2 mv = __builtin_elementwise_fma(as_h2(mb4[i]), mn_mul, mn_off);
+                    bm[rs][2 * i] = mv.x;
+                    bm[rs][2 * i + 1] = mv.y;
+                }
+            } else {
+                dr[rs] = h2f(lds16(sm.w, wo[rs]));
+                mr[rs] = 0.0f;
+                qh8[rs] = lds64u(sm.w, wo[rs] + 66);
+                sc8[rs] = lds64u(sm.w, wo[rs] + 74);
+            }
+        }
+
+        // ---- per 32-block j: B (lane (row l16, quarter q): values
+        // 8 q .. 8 q + 7 of block j, exact fp16 integers, scale folded in),
+        // then hi and lo of every token tile into the chained accumulators
+        f4 acc[2][NT];
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+            for (int ts = 0; ts < NT; ++ts) acc[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            h8 bw[2];
+#pragma unroll
+            for (int rs = 0; rs < 2; ++rs) {
+                uint32_t hv[4];
+                if (q4) {
+                    const h2 spair = scp[rs][j >> 1];
+                    const _Float16 scj = (j & 1) ? spair.y : spair.x;
+                    const h2 sc2 = h2{scj, scj};
+                    const h2 off = sc2 * m1024;                 // -1024 sc, exact
+                    // nibbles of qs bytes 32 (j / 2) + 8 q ..: low for even j, high for odd
+                    const uint2 wq = *reinterpret_cast<const uint2 *>(sm.w + wo[rs] + 16 + 32 * (j >> 1) + 8 * q);
+                    const uint32_t sh = 4u * (uint32_t)(j & 1);
+                    const uint32_t n0 = (wq.x >> sh) & 0x0F0F0F0Fu, n1 = (wq.y >> sh) & 0x0F0F0F0Fu;
+                    hv[0] = h2bits(__builtin_elementwise_fma(as_h2(magic_lo(n0)), sc2, off));
+                    hv[1] = h2bits(__builtin_elementwise_fma(as_h2(magic_hi(n0)), sc2, off));
+                    hv[2] = h2bits(__builtin_elementwise_fma(as_h2(magic_lo(n1)), sc2, off));
+                    hv[3] = h2bits(__builtin_elementwise_fma(as_h2(magic_hi(n1)), sc2, off));
+                } else {
+                    // group 4 j + q: codebook entry, signs, 4-bit scale of its 16
+                    const uint32_t qsw = lds32u(sm.w, wo[rs] + 2 + 4 * j);
+                    const uint32_t sgw = lds32u(sm.w, wo[rs] + 34 + 4 * j);
+                    const uint32_t qhj = __builtin_amdgcn_ubfe(j < 4 ? qh8[rs].x : qh8[rs].y, 8 * (j & 3) + 2 * q, 2);
+                    const uint32_t idx = __builtin_amdgcn_ubfe(qsw, 8 * q, 8) | (qhj << 8);
+                    const uint32_t ls =
+                        __builtin_amdgcn_ubfe(j < 4 ? sc8[rs].x : sc8[rs].y, 8 * (j & 3) + 4 * (q >> 1), 4);
+                    const u32x4 sel = sm.csel[idx];
+                    const u32x4 sg = sm.sgnh[__builtin_amdgcn_ubfe(sgw, 8 * q, 8)];
+                    const uint2 t = sm.lsT[ls];
+                    hv[0] = __builtin_amdgcn_perm(t.y, t.x, sel.x) | sg.x;
+                    hv[1] = __builtin_amdgcn_perm(t.y, t.x, sel.y) | sg.y;
+                    hv[2] = __builtin_amdgcn_perm(t.y, t.x, sel.z) | sg.z;
+                    hv[3] = __builtin_amdgcn_perm(t.y, t.x, sel.w) | sg.w;
+                }
+                __builtin_memcpy(&bw[rs], hv, 16);
+            }
+#pragma unroll
+            for (int ts = 0; ts < NT; ++ts) {
+                const _Float16 * xr = sm.x + (16 * ts + l16) * PF_XH + 32 * j + 8 * q;
+                h8 ah, al;
+                __builtin_memcpy(&ah, xr, 16);
+                __builtin_memcpy(&al, xr + 256, 16);
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs) acc[rs][ts] = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], acc[rs][ts]));
+            }
+        }
+        // ---- the super-block into y: d_w (Q4_K: minus dmin times the mins MFMA)
+#pragma unroll
+        for (int ts = 0; ts < NT; ++ts) {
+            if (q4) {
+                h8 am;
+                const u32x4 mv = q < 2 ? *reinterpret_cast<const u32x4 *>(sm.mb + 16 * (16 * ts + l16) + 8 * q)
+                                       : u32x4{0, 0, 0, 0};
+                __builtin_memcpy(&am, &mv, 16);
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs) {
+                    const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        y[rs][ts][r] = __fadd_rn(y[rs][ts][r], __builtin_fmaf(dr[rs], acc[rs][ts][r], -(mr[rs] * m[r])));
+                }
+            } else {
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) y[rs][ts][r] = __builtin_fmaf(dr[rs], acc[rs][ts][r], y[rs][ts][r]);
+            }
+        }
+    }
+
+    // ---- epilogue: GEGLU of gate row i and up row i, q8_1 of each 32-block
+    const float f = q4 ? 1.0f : 0.125f;
+    float * stg = reinterpret_cast<float *>(sm.x);
+#pragma unroll
+    for (int ts = 0; ts < NT; ++ts) {
+        __syncthreads();
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) stg[(32 * wave + 16 * rs + l16) * GU_STP + 4 * q + r] = f * y[rs][ts][r];
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int u = 8 * pass + 2 * wave + (lane >> 5);
+            const int tk = u >> 1, blk = u & 1, i = lane & 31;
+            const int j = 16 * ts + tk;
+            const int fi = 64 * rb + 32 * blk;
+            const bool live = j < n && fi < F;
+            const float gv = stg[(32 * blk + i) * GU_STP + tk];
+            const float uv = stg[(64 + 32 * blk + i) * GU_STP + tk];
+            const float v = geglu1<GSRC>(gv, uv);
+            const int64_t qp = sm.pair[min(j, PF_TOK1 - 1)];
+            q8_store32<AM_Q8_1>(v, p.ah + qp * F + fi + i, p.al + qp * F + fi + i, nullptr, live);
+        }
+    }
+}
+
+// grid (row blocks, groups, 2): z takes the group's tokens 32 z .. 32 z + 31
+template <int HT, int CT, int GSRC>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up_q1(const PfParams p) {
+    __shared__ __align__(16) GuSmemQ1 sm;
+    const int g = blockIdx.y, rb = blockIdx.x, t0 = PF_TOK1 * blockIdx.z;
+    if (g >= *p.n_tiles) return;
+    const PfTile tile = p.tiles[g];
+    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK || t0 >= tile.n) return;
+    const int n = min(PF_TOK1, tile.n - t0);
+    if (n > 16) pf_gate_up_group_q1<HT, CT, GSRC, 2>(p, tile, sm, rb, t0, n);
+    else pf_gate_up_group_q1<HT, CT, GSRC, 1>(p, tile, sm, rb, t0, n);
+}
+
 // ------------------------------------------------------------------ down
 
 constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
@@ -859,7 +1226,10 @@ void launch_pf(F k, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, cons
 }
 template <int HT, int CT>
 void launch_gu(int gelu, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const PfParams & p) {
-    if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
+    if (p.act_mode == AM_Q8_1) {
+        if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
+        else launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
+    } else if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
     else launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
 }
 }  // namespace
@@ -871,11 +1241,13 @@ hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
     const int NSB = p.d_model / 256;
     hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(WG), 0, s, p);
-    hipLaunchKernelGGL(k_pf_quant_x, dim3((p.T * NSB + 3) / 4), dim3(WG), 0, s, p);
+    if (p.act_mode == AM_Q8_1)
+        hipLaunchKernelGGL(k_pf_quant_x1, dim3((p.T * (p.d_model / 64) + 3) / 4), dim3(WG), 0, s, p);
+    else hipLaunchKernelGGL(k_pf_quant_x, dim3((p.T * NSB + 3) / 4), dim3(WG), 0, s, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     {
-        dim3 grid((p.n_ff + 63) / 64, p.max_tiles);
+        dim3 grid((p.n_ff + 63) / 64, p.max_tiles, p.act_mode == AM_Q8_1 ? PF_TOK / PF_TOK1 : 1);
         if (hgu == T_Q4_K && cgu == T_IQ2_S) launch_gu<T_Q4_K, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);
         else if (hgu == T_Q4_K && cgu == T_Q4_K) launch_gu<T_Q4_K, T_Q4_K>(gelu, grid, s, e[0], e[1], p);
         else if (hgu == T_IQ2_S && cgu == T_IQ2_S) launch_gu<T_IQ2_S, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);

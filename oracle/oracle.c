@@ -255,7 +255,7 @@ void orc_quantize_act(int act_type, const float * x, void * y, int64_t k) {
 }
 
 int orc_act_type(int wtype, int act_mode) {
-    if (act_mode == ORC_ACT_Q8_1) return ORC_Q8_1;
+    if (act_mode == ORC_ACT_Q8_1 || act_mode == ORC_ACT_Q8_1_MMA) return ORC_Q8_1;
     return (wtype == ORC_Q4_K || wtype == ORC_IQ2_S) ? ORC_Q8_K : ORC_Q8_0;
 }
 
@@ -425,8 +425,57 @@ static float dot_iq4_nl_q8_1(int64_t n, const blk_iq4_nl * x, const blk_q8_1 * y
     return (float)acc;
 }
 
+/* ORC_ACT_Q8_1_MMA's IQ2_S: each 16-value half of a 32-block scaled by
+ * (2 ls + 1) exactly (mmq.cuh:2881-2945 keeps d (2 ls + 1) / 8 as a float;
+ * the integer form here is the same value), the block's sum times d d8 / 8. */
+static float dot_iq2_s_q8_1_mma(int64_t n, const blk_iq2_s * x, const blk_q8_1 * y) {
+    double acc = 0;
+    for (int64_t i = 0; i < n / QK_K; ++i) {
+        for (int ib = 0; ib < 8; ++ib) {
+            const blk_q8_1 * b = &y[i * 8 + ib];
+            const int ls0 = x[i].scales[ib] & 0x0F, ls1 = x[i].scales[ib] >> 4;
+            int s[2] = {0, 0};
+            for (int l = 0; l < 4; ++l) {
+                const int g = x[i].qs[4 * ib + l] | (((x[i].qh[ib] >> (2 * l)) & 3) << 8);
+                const uint8_t sg = x[i].qs[32 + 4 * ib + l];
+                for (int j = 0; j < 8; ++j)
+                    s[l / 2] += b->qs[8 * l + j] * iq2s_grid_byte(g, j) * ((sg >> j) & 1 ? -1 : 1);
+            }
+            const int sum8 = s[0] * (2 * ls0 + 1) + s[1] * (2 * ls1 + 1);     /* 8 x the scaled sum, exact */
+            const float d = orc_fp16_to_fp32(x[i].d) * orc_fp16_to_fp32(b->d);
+            acc += (double)(d * (float)sum8) * 0.125;
+        }
+    }
+    return (float)acc;
+}
+
+/* ORC_ACT_Q8_1_MMA's Q5_0: the weights as q - 16 (mmq.cuh load_tiles_q5_0),
+ * d_w d8 sum (q - 16) a, without q8_1's stored sum s8. */
+static float dot_q5_0_q8_1_mma(int64_t n, const blk_q5_0 * x, const blk_q8_1 * y) {
+    double acc = 0;
+    for (int64_t i = 0; i < n / 32; ++i) {
+        uint32_t qh;
+        memcpy(&qh, x[i].qh, 4);
+        int sumi = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int x0 = ((x[i].qs[j] & 0x0F) | (((qh >> j) & 1) << 4)) - 16;
+            const int x1 = ((x[i].qs[j] >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+            sumi += x0 * y[i].qs[j] + x1 * y[i].qs[j + 16];
+        }
+        acc += (double)(orc_fp16_to_fp32(x[i].d) * orc_fp16_to_fp32(y[i].d) * (float)sumi);
+    }
+    return (float)acc;
+}
+
 float orc_vec_dot(int wtype, int act_mode, int64_t n, const void * w, const void * a) {
-    if (act_mode == ORC_ACT_Q8_1) {
+    if (act_mode == ORC_ACT_Q8_1_MMA) {
+        switch (wtype) {
+            case ORC_Q4_K:   return dot_q4_K_q8_1(n, w, a);
+            case ORC_IQ2_S:  return dot_iq2_s_q8_1_mma(n, w, a);
+            case ORC_Q5_0:   return dot_q5_0_q8_1_mma(n, w, a);
+            case ORC_IQ4_NL: return dot_iq4_nl_q8_1(n, w, a);
+        }
+    } else if (act_mode == ORC_ACT_Q8_1) {
         switch (wtype) {
             case ORC_Q4_K:   return dot_q4_K_q8_1(n, w, a);
             case ORC_IQ2_S:  return dot_iq2_s_q8_1(n, w, a);

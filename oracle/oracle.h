@@ -31,7 +31,12 @@ enum {
 
 /* activation formats: 0 = what the x86 ggml CPU path quantises to (q8_K for
  * 256-wide blocks, q8_0 for 32-wide blocks); 1 = q8_1 as ggml-cuda does. */
-enum { ORC_ACT_CPU = 0, ORC_ACT_Q8_1 = 1 };
+/* ORC_ACT_Q8_1_MMA: q8_1 activations with the sums ggml-cuda's matrix-core
+ * path (mmq.cuh) forms for IQ2_S and Q5_0 -- the per-16 scale d (2 ls + 1) / 8
+ * applied exactly (no integer truncation) and Q5_0 as d d8 sum (q - 16) a
+ * (no s8 term); Q4_K and IQ4_NL as in ORC_ACT_Q8_1.  The device's prefill
+ * path in its q8_1 mode computes these. */
+enum { ORC_ACT_CPU = 0, ORC_ACT_Q8_1 = 1, ORC_ACT_Q8_1_MMA = 2 };
 /* GEGLU: 0 = the CPU's fp16 GELU table (ggml-cpu/vec.h:1414-1428),
  *        1 = exact tanh GELU (ggml-cuda/unary.cuh:101-104). */
 enum { ORC_GELU_TABLE = 0, ORC_GELU_TANH = 1 };

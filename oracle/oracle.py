@@ -14,7 +14,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 
 F32, Q5_0, Q8_0, Q8_1, Q4_K, Q8_K, IQ4_NL, IQ2_S = 0, 6, 8, 9, 12, 15, 20, 22
-ACT_CPU, ACT_Q8_1 = 0, 1
+ACT_CPU, ACT_Q8_1, ACT_Q8_1_MMA = 0, 1, 2
 GELU_TABLE, GELU_TANH = 0, 1
 
 _BLOCK = {Q4_K: (256, 144), IQ2_S: (256, 82), Q5_0: (32, 22), IQ4_NL: (32, 18),

@@ -89,6 +89,17 @@ def per_token_rel_l2(got, want):
     return np.array([rel_l2(got[t], want[t]) for t in range(got.shape[0])])
 
 
+def oracle_mode(act_mode, T):
+    """The oracle mode a layer call of T tokens is checked in.  Past 4 tokens
+    the prefill path runs on the matrix cores, and in the q8_1 mode it forms
+    its sums as ggml-cuda's matrix-core path (mmq) does -- IQ2_S's per-16
+    scale exact instead of vecdotq's truncating integer formula, Q5_0 as
+    (q - 16) against d8 q instead of the stored sum s8 -- which the oracle's
+    ACT_Q8_1_MMA mode restates."""
+    from oracle import ACT_Q8_1, ACT_Q8_1_MMA
+    return ACT_Q8_1_MMA if act_mode == ACT_Q8_1 and T > 4 else act_mode
+
+
 def check_layer_bars(got, want, say=print, frac_above=0.01):
     """The layer bar against the oracle: the whole output within relative L2
     5e-4 (the requirement is 1e-3), no token above 3e-3, at most 1 % of the

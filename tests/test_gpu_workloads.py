@@ -25,7 +25,8 @@ import numpy as np
 import pytest
 
 import llapis_amd as la
-from helpers import FULL, check_layer_bars, dual_k57, full_layer, per_token_rel_l2, rel_l2, tokens, with_hot_set
+from helpers import (FULL, check_layer_bars, dual_k57, full_layer, oracle_mode, per_token_rel_l2, rel_l2, tokens,
+                     with_hot_set)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +48,7 @@ def run_layer(gpu, oracle, lay, x, act_mode, gelu_mode):
     ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, lay.spec.top_k)
     assert np.array_equal(ids_g, ids_o), "routing differs from the oracle"
     assert np.allclose(w_g, w_o, rtol=1e-5, atol=1e-7)
-    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, act_mode, gelu_mode)
+    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, oracle_mode(act_mode, x.shape[0]), gelu_mode)
     return out_g, out_o, ids_g
 
 
@@ -142,7 +143,7 @@ def test_stack_slice_three_layers(gpu, oracle, T, act_mode, gelu_mode):
         ids_g, w_g, out_g = ids.cpu().numpy(), w.cpu().numpy(), out.cpu().numpy()
         ids_o, _, _ = oracle.router(x, lay.router_w, lay.router_b, FULL.top_k)
         assert np.array_equal(ids_g, ids_o), f"layer {il}: routing differs"
-        out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, act_mode, gelu_mode)
+        out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, oracle_mode(act_mode, T), gelu_mode)
         say(f" layer {il}:")
         check_layer_bars(out_g, out_o, say, 0.02 if act_mode == la.ACT_Q8_1 else 0.01)
         ids_gpu.append(ids_g)
@@ -155,7 +156,7 @@ def test_stack_slice_three_layers(gpu, oracle, T, act_mode, gelu_mode):
         x = _rms_norm_np(ho)
         ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, FULL.top_k)
         same &= (ids_o == ids_gpu[il]).all(axis=1)
-        out_o, _ = oracle.moe_experts(lay, x, ids_o, w_o, act_mode, gelu_mode)
+        out_o, _ = oracle.moe_experts(lay, x, ids_o, w_o, oracle_mode(act_mode, T), gelu_mode)
         ho = ho + out_o
     per = per_token_rel_l2(h_gpu, ho)
     say(f"  chain: {int((~same).sum())} of {T} tokens routed differently; routed alike: max rel_l2 "

@@ -27,6 +27,10 @@ How each oracle function is pinned:
       the truncation bound of its integer formula (at most one unit of
       d*d8 per 32 values).  Parity with the reference's CUDA code itself is
       unpinned (no CUDA compiler here).
+  orc_vec_dot q8_1 matrix-core mode (ACT_Q8_1_MMA: the prefill's sums)
+      every format equal to the float64 dot of the dequantised operands: its
+      IQ2_S keeps the per-16 scale exact and its Q5_0 uses (q - 16) against
+      d8 q, so every sum is an exact integer times scales.
   orc_geglu
       table mode bit-exact against the reference's geglu_split (geglu.npz),
       including the +-10 clamps; tanh mode against the closed form in float64.
@@ -49,7 +53,7 @@ from types import SimpleNamespace
 import numpy as np
 import pytest
 
-from oracle import (ACT_CPU, ACT_Q8_1, GELU_TABLE, GELU_TANH, IQ2_S, IQ4_NL, Q4_K, Q5_0, Q8_0, Q8_1, Q8_K,
+from oracle import (ACT_CPU, ACT_Q8_1, ACT_Q8_1_MMA, GELU_TABLE, GELU_TANH, IQ2_S, IQ4_NL, Q4_K, Q5_0, Q8_0, Q8_1, Q8_K,
                     row_size)
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -228,7 +232,7 @@ def _deq_act(oracle, at, a, n):
 
 
 @pytest.mark.parametrize("name", list(WTYPES))
-@pytest.mark.parametrize("mode", [ACT_CPU, ACT_Q8_1])
+@pytest.mark.parametrize("mode", [ACT_CPU, ACT_Q8_1, ACT_Q8_1_MMA])
 def test_vec_dot_equals_dequantised_dot(oracle, name, mode):
     t = WTYPES[name]
     g = load("quant.npz")
