@@ -710,35 +710,96 @@ def run_stack_dynamic(la, torch, full, spec, dev, n_layers=30, tokens=192, drift
     return res
 
 
-def cpu_baseline(host_layer, T, budget_s=12.0):
-    """The reference's ggml CPU graph (oracle/_ref) on a bounded sample."""
-    sys.path.insert(0, str(ROOT / "oracle"))
-    from oracle import Ref
-    import llapis_amd as la
-    sp = host_layer.spec
+AVX512_FLAGS = ("avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd", "avx512_vnni", "avx512vbmi")
+
+
+def host_cpu():
+    """(model name, logical CPUs, ISA of the reference build to load, path)."""
+    model, flags, n = "unknown", set(), 0
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+            elif line.startswith("processor"):
+                n += 1
+    except OSError:
+        pass
+    lib512 = ROOT / "oracle" / "_ref" / "libggml_ref_avx512.so"
+    if all(f in flags for f in AVX512_FLAGS) and lib512.exists():
+        return model, n, "avx512", lib512
+    return model, n, "avx2", ROOT / "oracle" / "_ref" / "libggml_ref.so"
+
+
+def cpu_threads():
+    """The threads the CPU baseline runs on: every core this process may use,
+    up to the host CPU share a one-GPU job gets (OMP_NUM_THREADS, 16 when
+    unset) -- the reference's own sidecar pool also stops at 16 workers."""
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
-    ref = Ref()
-    rl = ref.layer(host_layer.router_w, host_layer.router_b, sp.top_k, sp.cold_gu_type, host_layer.cold_gu,
-                   sp.cold_dn_type, host_layer.cold_dn, sp.n_ff, T)
-    xs = la.synth_normal(99, 256 * T * sp.d_model).reshape(256, T, sp.d_model)
-    for i in range(3):
-        rl.run(xs[i], cores, False)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n < 100000:
-        rl.run(xs[n % 256], cores, False)
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": n * T / dt, "unit": "tok/s", "cores": cores, "kind": "reference",
-            "sample": f"{n} decode steps of {T} token(s) on the all-IQ2_S layer (ggml CPU mul_mat_id graph, "
-                      f"{n_threads_note(cores)}), {dt:.1f} s"}
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(cores, share, 16))
 
 
-def n_threads_note(c):
-    return f"{c} threads"
+def cpu_baseline(layers, budget_s=8.0):
+    """The reference's CPU path, built from its sources (oracle/_ref), timed on
+    the host cores on a bounded sample of each workload, with the same
+    quantised bytes as the GPU run and weights rotating over >= 512 MB of
+    layer replicas (DRAM, not the LLC):
+      iq2s, q4k   the ggml CPU graph of one layer (router, soft_max, top-k,
+                  mul_mat_id gate_up, geglu, mul_mat_id down, combine);
+      dual, prefill  that graph for the routing and the hot pairs, the
+                  reference's CPU cold executor (src/moe_sidecar.cpp) for the
+                  cold pairs.
+    layers: {name: (host layer, tokens per step, single tier: 'cold'/'hot'/None)}."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    from oracle import Ref
+    import llapis_amd as la
+    model, n_cpu, isa, lib = host_cpu()
+    threads = cpu_threads()
+    ref = Ref(str(lib))
+    res = {"cpu_model": model, "logical_cpus": n_cpu, "isa": isa, "threads": threads, "configs": {}}
+    for name, (lay, T, tier) in layers.items():
+        sp = lay.spec
+        if tier is not None:
+            gt, dt = (sp.cold_gu_type, sp.cold_dn_type) if tier == "cold" else (sp.hot_gu_type, sp.hot_dn_type)
+            gu, dn = (lay.cold_gu, lay.cold_dn) if tier == "cold" else (lay.hot_gu, lay.hot_dn)
+            per = len(gu) + len(dn) + lay.router_w.nbytes
+            R = max(2, int(np.ceil((512 << 20) / per)))
+            reps = [ref.layer(lay.router_w, lay.router_b, sp.top_k, gt, gu, dt, dn, sp.n_ff, T) for _ in range(R)]
+
+            def step(i, x, reps=reps):
+                reps[i % len(reps)].run(x, threads, False)
+        else:
+            import copy
+            per = len(lay.hot_gu) + len(lay.hot_dn) + len(lay.cold_gu) + len(lay.cold_dn) + lay.router_w.nbytes
+            R = max(2, int(np.ceil((512 << 20) / per)))
+            reps = []
+            for _ in range(R):
+                c = copy.copy(lay)
+                c.cold_gu, c.cold_dn = lay.cold_gu.copy(), lay.cold_dn.copy()
+                reps.append(ref.dual(c, T, threads))
+
+            def step(i, x, reps=reps):
+                reps[i % len(reps)].run(x)
+        xs = la.synth_normal(99, 8 * T * sp.d_model).reshape(8, T, sp.d_model)
+        for i in range(2):
+            step(i, xs[i])
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s and n < 100000:
+            step(n, xs[n % 8])
+            n += 1
+        dt_s = time.perf_counter() - t0
+        res["configs"][name] = {"tok_per_s": n * T / dt_s, "ms_per_step": dt_s * 1e3 / n, "steps": n,
+                                "seconds": dt_s, "replicas": R, "replica_mb": per / 1e6,
+                                "tokens_per_step": T}
+        log(f"[cpu {name}] {n * T / dt_s:.1f} tok/s ({dt_s * 1e3 / n:.2f} ms per step of {T} token(s), {n} steps, "
+            f"{R} replicas x {per / 1e6:.0f} MB) on {threads} threads ({isa}, {model})")
+        del reps
+    return res
 
 
 def main():
@@ -752,7 +813,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--engine-wgs", type=int, default=0,
                     help="stackdyn: the promotion engine's copy mode (0 hipMemcpyAsync, else copy-kernel workgroups)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU baseline seconds per workload")
     ap.add_argument("--tune", default="", help="key=value,... passed to llapis_set_tuning (measurement switches)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 20 device-to-device copies of MIB MiB (scales the HBM byte counters) and exit")
@@ -866,7 +927,26 @@ def main():
         try:
             cold_only = copy.copy(full)
             cold_only.residency = la.Residency.from_hot(spec.n_expert, [])
-            cpu = cpu_baseline(cold_only, 1, args.cpu_seconds)
+            layers = {"iq2s": (cold_only, 1, "cold")}
+            if "q4k" in results:
+                layers["q4k"] = (full, 1, "hot")
+            if "dual" in results:
+                layers["dual"] = (dual, 4, None)
+            if "prefill" in results:
+                layers["prefill"] = (dual, 512, None)
+            cb = cpu_baseline(layers, args.cpu_seconds)
+            for name, c in cb["configs"].items():
+                g = results.get(name)
+                if g:
+                    c["gpu_over_cpu"] = g["tok_per_s"] / c["tok_per_s"]
+                    c["effective_gbs"] = g["algo_bytes_step"] / (c["ms_per_step"] * 1e-3) / 1e9
+            h = cb["configs"]["iq2s"]
+            cpu = {"value": h["tok_per_s"], "unit": "tok/s", "cores": cb["threads"], "kind": "reference",
+                   "sample": f"{h['steps']} decode steps of 1 token on the all-IQ2_S layer, {h['seconds']:.1f} s, "
+                             f"weights rotated over {h['replicas']} replicas of {h['replica_mb']:.0f} MB; the "
+                             f"reference's ggml CPU graph built from its sources for {cb['isa']} "
+                             f"({cb['cpu_model']}, {cb['logical_cpus']} logical CPUs, {cb['threads']} threads)",
+                   "cpu_model": cb["cpu_model"], "isa": cb["isa"], "configs": cb["configs"]}
             log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
         except Exception as e:  # the checker library may be absent; say so
             cpu = {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference", "sample": f"unavailable: {e}"}

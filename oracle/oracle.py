@@ -152,6 +152,11 @@ class Ref:
         lib.ref_layer_create.restype = vp
         lib.ref_layer_run.argtypes = [vp, vp, vp, vp, vp, i32]
         lib.ref_layer_free.argtypes = [vp]
+        lib.ref_dual_create.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp, i64, i32, vp, i32, vp, i32, vp, i32, vp,
+                                        i32]
+        lib.ref_dual_create.restype = vp
+        lib.ref_dual_run.argtypes = [vp, vp, vp, vp, vp]
+        lib.ref_dual_free.argtypes = [vp]
         self.lib = lib
 
     def quantize(self, t, x, imatrix=None):
@@ -199,6 +204,13 @@ class Ref:
     def layer(self, w_r, bias, top_k, gu_type, w_gu, dn_type, w_dn, n_ff, T):
         return RefLayer(self, w_r, bias, top_k, gu_type, w_gu, dn_type, w_dn, n_ff, T)
 
+    def dual(self, L, T, n_threads=1):
+        """The reference's CPU path for a dual-precision layer: ggml graph for
+        the routing and the hot pairs, its CPU cold executor for the cold
+        pairs (ref_dual.cpp).  L: a LayerData-like object with numpy fields
+        and a residency (slot_of via exp_slot with every slot READY)."""
+        return RefDual(self, L, T, n_threads)
+
 
 class RefLayer:
     """A built single-tier ggml MoE layer graph (reference CPU path)."""
@@ -223,4 +235,40 @@ class RefLayer:
     def __del__(self):
         if getattr(self, "h", None):
             self.ref.lib.ref_layer_free(self.h)
+            self.h = None
+
+
+class RefDual:
+    """A built dual-precision layer over the reference's ggml graph and CPU
+    cold executor.  The cold pools stay the caller's arrays (kept alive here)."""
+
+    def __init__(self, ref, L, T, n_threads=1):
+        self.ref, self.T, self.k, self.d = ref, T, L.top_k, L.d_model
+        r = L.residency
+        slot_of = np.full(L.n_expert, -1, np.int32)
+        for e in range(L.n_expert):
+            if r.is_hot(e):
+                slot_of[e] = int(r.exp_slot[e])
+        self._keep = [np.ascontiguousarray(a) for a in (L.router_w, L.hot_gu, L.hot_dn, L.cold_gu, L.cold_dn)]
+        self._keep[0] = _f32(self._keep[0])
+        b = _f32(L.router_b) if L.router_b is not None else None
+        self._keep.append(b)
+        self._keep.append(slot_of)
+        k_slots = max(int(L.k_slots), 1)
+        self.h = ref.lib.ref_dual_create(_p(self._keep[0]), _p(b), L.d_model, L.n_expert, L.top_k, L.n_ff, T,
+                                         _p(slot_of), k_slots, L.hot_gu_type, _p(self._keep[1]), L.hot_dn_type,
+                                         _p(self._keep[2]), L.cold_gu_type, _p(self._keep[3]), L.cold_dn_type,
+                                         _p(self._keep[4]), n_threads)
+
+    def run(self, x):
+        x = _f32(x)
+        out = np.empty((self.T, self.d), np.float32)
+        ids = np.empty((self.T, self.k), np.int32)
+        n_hot = np.zeros(1, np.int32)
+        self.ref.lib.ref_dual_run(self.h, _p(x), _p(out), _p(ids), _p(n_hot))
+        return out, ids, int(n_hot[0])
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.ref.lib.ref_dual_free(self.h)
             self.h = None

@@ -433,3 +433,45 @@ def test_live_reference_random_rows(oracle, live_ref, name):
         assert np.array_equal(oracle.quantize_act(at, a), aq)
         want = live_ref.vec_dot(t, n, w, aq)
         assert abs(oracle.vec_dot(t, ACT_CPU, n, w, aq) - want) <= 2e-6 * max(1.0, abs(want))
+
+
+@pytest.mark.parametrize("T,n_hot", [(3, 6), (40, 10), (4, 0)])
+def test_reference_dual_layer_matches_oracle(oracle, live_ref, T, n_hot):
+    """The CPU baseline's dual-precision layer (the reference's ggml graph for
+    the routing and the hot pairs, its CPU cold executor for the cold pairs)
+    against the oracle's layer in the CPU activation mode: the same routing,
+    the same hot/cold split, the same outputs."""
+    import llapis_amd as la
+    from helpers import SMALL, layer, rel_l2, tokens
+    rng = np.random.default_rng(n_hot)
+    hot = sorted(rng.choice(SMALL.n_expert, n_hot, replace=False).tolist()) if n_hot else []
+    lay = layer(SMALL, 120 + n_hot, hot)
+    x = tokens(130 + T, T, SMALL.d_model)
+    rd = live_ref.dual(lay, T, n_threads=2)
+    out, ids, n_hot_pairs = rd.run(x)
+    ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, SMALL.top_k)
+    assert np.array_equal(ids, ids_o)
+    assert n_hot_pairs == sum(lay.residency.is_hot(int(e)) for e in ids.ravel())
+    out_o, _ = oracle.moe_experts(lay, x, ids_o, w_o)
+    assert rel_l2(out, out_o) <= 1e-6, rel_l2(out, out_o)
+
+
+def test_reference_avx512_build_matches_oracle(oracle):
+    """The AVX-512 build of the reference's ggml (the CPU baseline on hosts
+    that have it) computes the same layer as the oracle."""
+    import bench
+    from helpers import SMALL, layer, rel_l2, tokens
+    from oracle import Ref
+    _, _, isa, lib = bench.host_cpu()
+    if isa != "avx512":
+        pytest.skip("no AVX-512 build or host support")
+    ref = Ref(str(lib))
+    lay = layer(SMALL, 140, [])
+    x = tokens(141, 3, SMALL.d_model)
+    rl = ref.layer(lay.router_w, lay.router_b, SMALL.top_k, SMALL.cold_gu_type, lay.cold_gu, SMALL.cold_dn_type,
+                   lay.cold_dn, SMALL.n_ff, 3)
+    out, ids, w = rl.run(x, 2)
+    ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, SMALL.top_k)
+    assert np.array_equal(ids, ids_o)
+    out_o, _ = oracle.moe_experts(lay, x, ids_o, w_o)
+    assert rel_l2(out, out_o) <= 1e-5, rel_l2(out, out_o)
