@@ -163,7 +163,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
  * allocated.  A call whose llapis_moe_ffn_workspace_size exceeds it is
  * refused (-1, llapis_last_error() says how much it needs): at the
  * benchmark's shapes (d_model 2816, n_ff 704, 128 experts, top-8) that
- * admits batches of up to 48 tokens.  The first call on a device clears the array with a kernel on
+ * admits batches of up to 61 tokens.  The first call on a device clears the array with a kernel on
  * its stream.  Every call on one GPU shares that GPU's array and leaves its
  * contents behind: calls that overlap on one GPU (other streams, other
  * threads) race, so order them as one stream would. */
@@ -385,7 +385,9 @@ int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
  * -1, the default, picks it from d_model and the token count), key 4 = the
  * decode path's down kernel: 1 by expert group with a combine kernel after
  * it, 0 over every group with the combine in it, -1 (default) by group from
- * two tokens on.  Other keys are ignored. */
+ * two tokens on, key 6 = llapis_moe_dual_compute's one-kernel fires (default
+ * 1; 0 runs every fire through the island's generic pipeline).  Other keys
+ * are ignored. */
 void llapis_set_tuning(int32_t key, int32_t value);
 
 /* Stage timing of llapis_moe_ffn for measurement (not under stream capture):

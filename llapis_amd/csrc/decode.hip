@@ -1,38 +1,41 @@
-// decode.hip -- the MoE layer for decode batches (1..4 tokens) in three
-// kernels on gfx950:
+// decode.hip -- the MoE layer for decode batches (1..4 tokens) on gfx950,
+// and the one-kernel fires of the dual op.
 //
-//   A  k_dec_route   router logits (one workgroup per expert, all tokens) and,
-//                    in the workgroups after those, the tokens' activation
-//                    quantisation.
-//   B  k_dec_gate_up every workgroup selects the routing from the logits
-//                    (softmax, top-k by a bisection for the k-th largest
-//                    probability, ties to the lower index), groups the routed
-//                    pairs by expert (decode once, dot N: the tokens that
-//                    share an expert read its slab once) and resolves each
-//                    group's tier (the residency predicate of
-//                    moert/cuda/ffn_moe.cu:80-130); the first workgroup
-//                    publishes ids, weights and groups for C.  Then its items:
-//                    an item is one group's 32-row block of gate rows and the
-//                    32 up rows paired with them (rows i and n_ff + i), read as
-//                    four 16-row steps that all go out at once; the rows are
-//                    dotted against every member token, and the item ends with
-//                    GEGLU of each gate/up pair and the q8 quantisation of the
-//                    32 results -- one block of each member's down activation,
-//                    written once.
-//   C  k_dec_down    one workgroup per block of output rows, over every group:
-//                    the blocks' rows of each routed expert's down slab stream
-//                    through LDS in batches of groups (the next batch in flight
-//                    meanwhile), are dotted against the members' down
-//                    activations and scaled by the expert's .scale, and the
-//                    workgroup writes the weighted sum of each token's top_k
-//                    outputs for its rows (llama-graph.cpp:1812-1840 order).
+//   A  k_dec_route     router logits (one workgroup per expert, all tokens)
+//                      and, in the workgroups after those, the tokens'
+//                      activation quantisation.
+//   B  k_dec_gate_up   every workgroup selects the routing from the logits
+//                      (softmax, top-k by a bisection for the k-th largest
+//                      probability, ties to the lower index), groups the
+//                      routed pairs by expert (the tokens that share an expert
+//                      read its slab once) and resolves each group's tier (the
+//                      residency predicate of moert/cuda/ffn_moe.cu:80-130);
+//                      the first workgroup publishes ids, weights and groups.
+//                      Then its items: an item is one group's 8 gate rows and
+//                      the 8 up rows paired with them (rows i and n_ff + i),
+//                      one row per 16 lanes, the next item's loads in flight;
+//                      the rows are dotted against every member token and the
+//                      item ends with GEGLU of each gate/up pair, stored as
+//                      fp32 down activations.
+//   C  k_dec_down      one token: one workgroup per block of output rows over
+//                      every group; each row's lanes load its block pairs
+//                      straight into registers, dot them against the members'
+//                      down activations (quantised in LDS from B's fp32
+//                      outputs), scale by the expert's .scale and sum each
+//                      token's top_k outputs in k order (llama-graph.cpp:
+//                      1812-1840).
+//      k_dec_down_grp  2-4 tokens: one workgroup per (block of rows, group),
+//      k_dec_combine   the members' activations only, then a combine kernel
+//                      that sums each token's top_k rows in k order.
 //
-// No workgroup waits on another: B hands over through its first workgroup's
-// records and the down activations, C reads them at the kernel boundary and
-// owns its output rows outright, so any grid is safe.  Every load a kernel
-// issues before its first wait is unconditional (clamped addresses instead of
-// branches) and issued in the order its data are needed: loads complete in
-// issue order, so a wait covers only the loads before it.
+//   k_fire_k256 / k_fire_k32: one GGML_OP_MOE_DUAL fire (gate_up over the
+//   256-value block formats, down over the 32-value ones) as one kernel.
+//
+// No workgroup waits on another: every hand-over is a kernel boundary, so any
+// grid is safe.  Every load a kernel issues before its first wait is
+// unconditional (clamped addresses instead of branches) and issued in the
+// order its data are needed: loads complete in issue order, so a wait covers
+// only the loads before it.
 #include <hip/hip_ext.h>
 
 #include <climits>
