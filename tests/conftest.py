@@ -32,3 +32,18 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.fail("GPU test run without a visible GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _library_defaults(request):
+    """Every GPU test starts from the library's default switches: the
+    process-wide activation mode (set by the dual op's callers) and the
+    tuning keys a test may change are put back after it."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import llapis_amd as la
+    lib = la.lib()
+    lib.llapis_set_modes(la.ACT_CPU, la.GELU_TABLE)
+    for key, value in ((0, 1), (2, 1), (3, -1), (4, -1), (6, 1)):
+        lib.llapis_set_tuning(key, value)
