@@ -629,8 +629,8 @@ bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
 // prefill path (T > DEC_MAXT, either activation mode): tokens are processed in
 // chunks of Tc = PF_MAX_PAIRS / top_k; one chunk's scratch
 struct PfWs {
-    uint64_t probs, ids, w, ntiles, sorted, tiles, xq, xd, xm, xh, ah, al, ydn, parts, total;
-    int Tc, max_tiles;
+    uint64_t probs, ids, w, ntiles, sorted, tiles, gtiles, xq, xd, xm, xh, ah, al, ydn, parts, total;
+    int Tc, max_tiles, max_gtiles;
 };
 PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     PfWs w;
@@ -638,13 +638,15 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
     const uint64_t P = (uint64_t)w.Tc * L->top_k;
     const uint64_t D = L->d_model, F = L->n_ff, NSB = L->d_model / 256;
     w.max_tiles = pf_max_tiles((int)P, L->n_expert);
+    w.max_gtiles = pf_max_gtiles((int)P, L->n_expert);
     w.probs = dec_ctl_bytes(L);
     w.ids = w.probs + al256((uint64_t)w.Tc * L->n_expert * 4);
     w.w = w.ids + al256(P * 4);
     w.ntiles = w.w + al256(P * 4);
     w.sorted = w.ntiles + 256;
     w.tiles = w.sorted + al256(P * 4);
-    w.xq = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
+    w.gtiles = w.tiles + al256((uint64_t)w.max_tiles * sizeof(PfTile));
+    w.xq = w.gtiles + al256((uint64_t)w.max_gtiles * sizeof(PfTile));
     w.xd = w.xq + al256((uint64_t)w.Tc * D);
     w.xm = w.xd + al256((uint64_t)w.Tc * NSB * 4);
     w.xh = w.xm + al256((uint64_t)w.Tc * NSB * 32);
@@ -788,6 +790,9 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             p.sorted = (int32_t *)(base + pw.sorted);
             p.tiles = (PfTile *)(base + pw.tiles);
             p.max_tiles = pw.max_tiles;
+            p.gtiles = (PfTile *)(base + pw.gtiles);
+            p.max_gtiles = pw.max_gtiles;
+            p.n_gtiles = p.n_tiles + 1;
             p.xq = (int8_t *)(base + pw.xq);
             p.xd = (float *)(base + pw.xd);
             p.xm = (_Float16 *)(base + pw.xm);

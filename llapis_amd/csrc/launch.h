@@ -123,6 +123,7 @@ hipError_t launch_fire(const FireParams & f, int ht, int ct, int act_mode, hipSt
 
 constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)
 constexpr int PF_TOK = 64;            // routed pairs per group (four 16-token MFMA tiles)
+constexpr int PF_GTOK = 128;          // routed pairs per gate_up group, at most
 constexpr int PF_MAX_PAIRS = 4096;    // routed pairs per prefill launch (T * top_k)
 constexpr int PF_MAX_FF = 4096;       // longest n_ff the down activation kernel stages
 
@@ -148,6 +149,12 @@ struct PfParams {
     int32_t * sorted;                    // [P] pair indices grouped by expert, ascending within
     PfTile * tiles;                      // [max_tiles]
     int max_tiles;
+    // the gate_up kernel's groups: runs of up to gcap[tier] pairs of one
+    // expert, the full groups of every expert first, then the remainders
+    PfTile * gtiles;                     // [max_gtiles]
+    int * n_gtiles;                      // [1]
+    int max_gtiles;
+    int gcap[2];                         // hot, cold (a multiple of 16 in [16, PF_GTOK])
     int8_t * xq;                         // [T][d_model] q8_K values
     float * xd;                          // [T][d_model / 256] q8_K scales
     _Float16 * xm;                       // [T][d_model / 256][16] q8_K: per-32 sums as 32 hi + lo;
@@ -162,6 +169,7 @@ struct PfParams {
 };
 
 int pf_max_tiles(int P, int n_expert);
+int pf_max_gtiles(int P, int n_expert);
 // ev (optional, profiling): begin/end timestamps of the gate_up and down GEMMs
 hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn, int gelu_src, hipStream_t s,
                           hipEvent_t * ev);

@@ -11,19 +11,25 @@
 //                  per-256 scale, and the per-32 sums split as 32 hi + lo
 //                  (both exact in fp16) for the Q4_K mins term.
 //   k_pf_gate_up   grouped GEMM per (group, 64 gate rows + the 64 matching up
-//                  rows).  Each super-block of weights is expanded once into
-//                  int8 MFMA operands and used for every token of the group.
-//                  The sub-block scales are folded into the weights: Q4_K's
-//                  6-bit scale splits as 8 sh + sl, so q sh and q sl (<= 105)
-//                  are int8 and two accumulators give sum_j sc_j dot_j
-//                  exactly; IQ2_S's grid * (2 ls + 1) (<= 1333) splits as
-//                  64 h + l.  The Q4_K mins term is one exact fp16 MFMA against
-//                  the split per-32 sums.  Scales d_w * d8 are applied once per
-//                  super-block in fp32.  The epilogue pairs gate row i with up
-//                  row n_ff + i: GEGLU and the q8_0 quantisation of the down
-//                  activations happen here, so the gate_up outputs never go to
-//                  memory; each down activation d8 q is stored exactly as two
-//                  fp16 parts.
+//                  rows), on groups of its own (<= 48 pairs of a Q4_K expert,
+//                  <= 64 of an IQ2_S one), the full groups first, every row
+//                  block of a group on one XCD.  Each super-block of weights
+//                  is expanded once into int8 MFMA operands and used for
+//                  every token of the group.  The sub-block scales are folded
+//                  into the weights: Q4_K's 6-bit scale splits as 8 sh + sl,
+//                  so q sh and q sl (<= 105) are int8 and two accumulators
+//                  give sum_j sc_j dot_j exactly; IQ2_S's grid * (2 ls + 1)
+//                  (<= 1333) splits as 64 h + l.  The Q4_K mins term is one
+//                  exact fp16 MFMA against the split per-32 sums.  Scales
+//                  d_w * d8 are applied once per super-block in fp32.  The
+//                  load unit copies the next super-block's activations (and
+//                  Q4_K rows) into LDS while the current one is used; IQ2_S
+//                  rows go straight to registers.  The epilogue pairs gate
+//                  row i with up row n_ff + i: GEGLU and the q8_0
+//                  quantisation of the down activations happen here, so the
+//                  gate_up outputs never go to memory; each down activation
+//                  d8 q is stored exactly as two fp16 parts.
+//   k_pf_gate_up_q1  the same GEMM in the q8_1 activation mode (fp16 MFMA).
 //   k_pf_down      grouped GEMM of the down projection on fp16 MFMA
 //                  (v_mfma_f32_16x16x32_f16, K = one 32-block): the weights as
 //                  exact small integers (Q5_0 q - 16, IQ4_NL kvalues), the
@@ -50,16 +56,15 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 __constant__ Iq2sTables c_iq2s_tab_pf = make_iq2s_tables();
 
-constexpr int PF_XP = 272;                // LDS pitch of a staged token row of one super-block (256 + 16)
 constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged weight row (Q4_K 144, IQ2_S <= 96)
 constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
 constexpr int PF_DXP = PF_DCB * 32 + 8;   // LDS pitch (halfs) of a staged down activation row
 constexpr int PF_WROW_DN = 112;           // staged bytes per weight row and down chunk (<= 4 * 22 + 14)
 constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows
-constexpr int PF_NTS = PF_TOK / 16;       // 16-token MFMA tiles per group
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -161,7 +166,7 @@ __constant__ Iq2sSplit c_iq2s_split = make_iq2s_split();
 // own.
 __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     constexpr int PER = PF_MAX_PAIRS / WG;
-    __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_hot;
+    __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_gf[256], s_gr[256], s_hot;
     const int P = p.T * p.top_k, E = p.n_expert;
     int ev[PER];
 #pragma unroll
@@ -193,6 +198,9 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
         }
     }
     const int nt_e = (n_e + PF_TOK - 1) / PF_TOK;
+    // gate_up groups: full groups of gcap pairs, then one remainder group
+    const int gcap = max(16, min(PF_GTOK, p.gcap[tier]));
+    const int gf_e = n_e / gcap, gr_e = n_e - gf_e * gcap > 0 ? 1 : 0;
     if (p.rc_counts) {
         // routing counters (ffn_moe.cu:123-128): pairs per expert, hot pairs,
         // the other pairs (invalid ids included)
@@ -202,17 +210,34 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     }
     s_off[threadIdx.x] = n_e;
     s_nt[threadIdx.x] = nt_e;
+    s_gf[threadIdx.x] = gf_e;
+    s_gr[threadIdx.x] = gr_e;
     __syncthreads();
     for (int o = 1; o < 256; o <<= 1) {          // inclusive scans over the experts
         const int a = threadIdx.x >= o ? s_off[threadIdx.x - o] : 0;
         const int b = threadIdx.x >= o ? s_nt[threadIdx.x - o] : 0;
+        const int c = threadIdx.x >= o ? s_gf[threadIdx.x - o] : 0;
+        const int d = threadIdx.x >= o ? s_gr[threadIdx.x - o] : 0;
         __syncthreads();
         s_off[threadIdx.x] += a;
         s_nt[threadIdx.x] += b;
+        s_gf[threadIdx.x] += c;
+        s_gr[threadIdx.x] += d;
         __syncthreads();
     }
     const int pair0 = s_off[threadIdx.x] - n_e, tile0 = s_nt[threadIdx.x] - nt_e;
     const int total = s_off[255], tiles = min(s_nt[255], p.max_tiles);
+    const int nfull = s_gf[255], gf0 = s_gf[threadIdx.x] - gf_e, gr0 = nfull + s_gr[threadIdx.x] - gr_e;
+    for (int b = 0; b <= gf_e; ++b) {
+        const int gi = b < gf_e ? gf0 + b : gr0;
+        if ((b == gf_e && !gr_e) || gi >= p.max_gtiles) continue;
+        PfTile t;
+        t.tier = tier;
+        t.idx = idx;
+        t.begin = pair0 + b * gcap;
+        t.n = min(gcap, n_e - b * gcap);
+        p.gtiles[gi] = t;
+    }
     if (p.rc_hits && threadIdx.x == 0) {
         atomicAdd(p.rc_hits, s_hot);
         atomicAdd(p.rc_hits + 1, P - s_hot);
@@ -222,6 +247,7 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     if (threadIdx.x == 0) {
         s_off[256] = total;                     // invalid ids are placed after every expert's pairs
         *p.n_tiles = tiles;
+        *p.n_gtiles = min(nfull + s_gr[255], p.max_gtiles);
     }
     for (int b = 0; b < nt_e; ++b) {
         if (tile0 + b >= p.max_tiles) break;
@@ -324,31 +350,9 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x1(const PfParams p) {
 
 // -------------------------------------------------------------- gate_up
 
-constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (128 rows x 9)
-constexpr int GU_XREG = 4;     // activation chunks per thread per super-block (64 tokens x 16)
-
-struct GuSmem {
-    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows: Q4_K at 144 r, IQ2_S at 96 r + offset
-    int8_t x[PF_TOK * PF_XP];             // the group's tokens' q8_K values of this super-block
-    _Float16 mb[PF_TOK * 16];             // their per-32 sums (32 hi + lo)
-    float d8[PF_TOK];                     // their q8_K scales
-    uint2 codes[1024];                    // IQ2_S grid: a level code per value
-    uint2 sgn[256];                       // IQ2_S sign byte: 4 per set bit, per value
-    u32x4 split[16];                      // Iq2sSplit
-    int poff[PF_ROWS];
-    int tok[PF_TOK], pair[PF_TOK];
-};
-// the epilogue's staging of one 16-token tile, over sm.x: [128 rows][17]
+// the epilogue's staging of one 16-token tile: [128 rows][17]
 constexpr int GU_STP = 17;
-static_assert(PF_ROWS * GU_STP * 4 <= PF_TOK * PF_XP, "epilogue staging fits the activation buffer");
-
-// Registers of the next super-block in flight while the current one computes.
-struct GuStage {
-    u32x4 w[GU_WREG];
-    u32x4 x[GU_XREG];
-    u32x4 mb;
-    float d8;
-};
+constexpr int GU_WREG = 5;     // weight chunks per thread per super-block (q8_1 kernel; 128 rows x 9)
 
 // q8_0 (x86 CPU build, arch/x86/quants.c:302-360) or q8_1 (ggml-cuda
 // quantize.cu:5-50) of one 32-block held one value per lane of a half-wave,
@@ -385,109 +389,202 @@ __device__ __forceinline__ void q8_store32(float v, _Float16 * hi, _Float16 * lo
     }
 }
 
-// One (group, row block) of the gate_up GEMM with NT 16-token tiles.  Wave w
-// owns local rows 32 w .. 32 w + 31 (waves 0, 1: gate rows; 2, 3: the up rows
-// of the same indices) as two 16-row MFMA tiles.
-template <int HT, int CT, int GSRC, int NT>
-__device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTile & tile, GuSmem & sm, const int rb) {
-    static_assert(HT == T_Q4_K || HT == T_IQ2_S, "gate_up formats");
-    static_assert(CT == T_Q4_K || CT == T_IQ2_S, "gate_up formats");
-    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK * 16 == GU_XREG * WG, "staging shape");
-    constexpr int NTOK = 16 * NT;
+// ------------------------------------------------------ gate_up, q8_K
+//
+// One workgroup per (gate_up group, 64 gate rows + the 64 matching up rows).
+// Wave w owns local rows 32 w .. 32 w + 31 (waves 0, 1: gate rows; 2, 3: the
+// up rows of the same indices) as two 16-row MFMA tiles.  The load unit
+// copies the group's activations of the next super-block (and the Q4_K rows)
+// into LDS (global_load_lds) while the current one is expanded and used;
+// IQ2_S rows go straight to registers with buffer loads, as their 82-byte
+// super-blocks are not 16-byte aligned.  Two buffers of each kind, so one
+// barrier per super-block both publishes super-block s and retires s - 1.
+// A token's 16-byte chunk c of a super-block sits in slot c ^ (token & 15)
+// of its 256-byte LDS row: the 16 tokens of an MFMA fragment read 16
+// distinct slots, so the fragment loads meet no bank conflict.
 
-    const int wtype = tile.tier == 0 ? HT : CT;
-    const bool q4 = wtype == T_Q4_K;
-    const int F = p.n_ff, NSB = p.d_model / 256, K = p.top_k;
-    // gate rows 64 rb .. 64 rb + 63
+constexpr int G2_TOKQ4 = 48;            // pairs per group of a Q4_K expert (at 64 the kernel spills registers)
+constexpr int G2_TOKIQ2 = 64;           // of an IQ2_S expert (its tables share the LDS)
+static_assert(G2_TOKQ4 <= PF_GTOK && G2_TOKIQ2 <= PF_GTOK, "group caps");
+constexpr int G2_TOKMAX = G2_TOKQ4 > G2_TOKIQ2 ? G2_TOKQ4 : G2_TOKIQ2;
+constexpr int G2_MBT = (G2_TOKQ4 + 31) / 32 * 32;     // tokens of a mins buffer: 32 per moving wave
+
+// LDS of one workgroup.  Each of the two buffers of a kind is a separate
+// object: the compiler then knows that a copy into one does not write the
+// other, and it does not make reads of the current buffer wait for the copy
+// of the next.  The epilogue stages gate rows in x0 and up rows in x1
+// ([64 rows][NTOK + 1] floats each); the IQ2_S tables live in w0 / w1 (that
+// format's rows go straight to registers).
+constexpr int G2_XB = 64 * (G2_TOKMAX + 1) * 4;
+constexpr int G2_WB = PF_ROWS * 144;                      // one super-block of 128 Q4_K rows
+static_assert(G2_XB >= G2_TOKQ4 * 256 && G2_XB >= G2_TOKIQ2 * 256, "activation buffers");
+static_assert(G2_WB >= 1024 * 8 && G2_WB >= 16 * 16, "IQ2_S tables fit the weight buffers");
+struct Gu2Lds {
+    uint8_t * x0; uint8_t * x1;                   // the group's q8_K values of one super-block
+    uint8_t * w0; uint8_t * w1;                   // Q4_K: the 128 rows of one super-block, [row][144]
+    _Float16 * mb0; _Float16 * mb1;               // their per-32 sums (32 hi + lo), Q4_K
+    float * d80; float * d81;                     // their q8_K scales
+    uint2 * codes;                                // IQ2_S grid: a level code per value (in w0)
+    u32x4 * split;                                // Iq2sSplit (in w1)
+    int * tok; int * pair;
+};
+
+typedef const void __attribute__((address_space(1))) * gptr_t;
+typedef void __attribute__((address_space(3))) * lptr_t;
+
+// 16 (or 4) bytes per lane from global memory into LDS at dst + 16 lane
+// (4 lane): the load unit writes LDS itself, tracked by the vector memory
+// counter
+__device__ __forceinline__ void lds_dma16(const void * src, void * dst) {
+    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void * src, void * dst) {
+    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 4, 0, 0);
+}
+
+// one lane's bytes of one IQ2_S super-block of a 16-row tile
+struct Iq2Raw {
+    uint32_t d;                 // dword holding d
+    u32x3 qs;                   // three dwords holding qs[8 q .. 8 q + 7]
+    u32x3 sg;                   //          ... and the signs
+    uint32_t qh, sc;            // dwords holding qh[2 q, 2 q + 1], scales[2 q, 2 q + 1]
+    int sh_d, sh_q, sh_h;       // byte shifts of those fields in their dwords
+};
+
+// IQ2_S super-blocks are 82 bytes, so a field is 2-aligned: each is read
+// from the dword-aligned address at or below it and shifted into place.
+// Super-block s of a row starts at row_start + 82 s, which is
+// 2 (rowpar + s) mod 4 (rowpar: row_start mod 4, halved).
+__device__ __forceinline__ void iq2_raw_load(Iq2Raw & w, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t rowpar,
+                                             int s, int q) {
+    const uint32_t a = ((rowpar + (uint32_t)s) & 1u) * 2u;      // super-block start mod 4
+    const uint32_t aq = a ^ 2u;                                  // qs, signs: start + 2 + 8 q
+    const uint32_t ah = (a + 2u + 2u * (uint32_t)q) & 2u;       // qh, scales: start + 66 / 74 + 2 q
+    // every offset is taken in the lane's register (>= 0), none in soffset
+    const uint32_t v0 = voff + 82u * (uint32_t)s;
+    w.d = __builtin_amdgcn_raw_buffer_load_b32(r, v0 - a, 0, 0);
+    const uint32_t vq = v0 + 2 + 8 * (uint32_t)q - aq;
+    w.qs = __builtin_amdgcn_raw_buffer_load_b96(r, vq, 0, 0);
+    w.sg = __builtin_amdgcn_raw_buffer_load_b96(r, vq + 32, 0, 0);
+    const uint32_t vh = v0 + 66 + 2 * (uint32_t)q - ah;
+    w.qh = __builtin_amdgcn_raw_buffer_load_b32(r, vh, 0, 0);
+    w.sc = __builtin_amdgcn_raw_buffer_load_b32(r, vh + 8, 0, 0);
+    w.sh_d = 8 * (int)a;
+    w.sh_q = 8 * (int)aq;
+    w.sh_h = 8 * (int)ah;
+}
+
+// The v_perm sign picks of 8 IQ2_S values from their sign byte (bits b ..
+// b + 7 of w): bit 2 of byte k set when value k is negative.  A 4-bit
+// nibble times 0x810204 = 2^2 + 2^9 + 2^16 + 2^23 puts its bit k at bit
+// 8 k + 2 (the four shifted copies do not overlap, so nothing carries).
+__device__ __forceinline__ uint2 sign_sel(uint32_t w, int b) {
+    const uint32_t lo = __builtin_amdgcn_ubfe(w, b, 4), hi = __builtin_amdgcn_ubfe(w, b + 4, 4);
+    return make_uint2((lo * 0x810204u) & 0x04040404u, (hi * 0x810204u) & 0x04040404u);
+}
+
+// Table-mode GEGLU (geglu1) in two steps, so that a lane's table reads can
+// all be in flight at once: the entry at fp16(g) (index clamped, read
+// unconditionally), then the clamps at -10 and 10 and the product.
+__device__ __forceinline__ uint32_t gelu_entry(float g) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)g);
+    const uint32_t mag = min(h & 0x7FFFu, (uint32_t)LLAPIS_GELU_TAB_SPAN - 1u);
+    return gelu_f16_table[mag + (h >> 15) * LLAPIS_GELU_TAB_SPAN];
+}
+__device__ __forceinline__ float geglu_from_entry(float g, float u, uint32_t e) {
+    const float t = __fmul_rn((float)__builtin_bit_cast(_Float16, (uint16_t)e), u);
+    return g <= -10.0f ? 0.0f : (g >= 10.0f ? __fmul_rn(g, u) : t);
+}
+
+template <int WT, int GSRC, int NT>
+__device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & tile, const Gu2Lds & L, const int rb) {
+    constexpr bool Q4 = WT == T_Q4_K;
+    static_assert(Q4 || WT == T_IQ2_S, "gate_up formats");
+    constexpr int NTOK = 16 * NT;
+    static_assert(NTOK <= (Q4 ? G2_TOKQ4 : G2_TOKIQ2), "group fits the LDS");
+    constexpr int BB = Q4 ? 144 : 82;                           // bytes per super-block
+    const int F = p.n_ff, NSB = p.d_model / 256, K = p.top_k, D = p.d_model;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
-    const int bb = q4 ? 144 : 82;                               // bytes per super-block
-    const int nwc = q4 ? 9 : 6;                                 // staged 16-byte chunks per row
-    const uint64_t rbytes = (uint64_t)NSB * bb;
+    const uint32_t rbytes = (uint32_t)(NSB * BB);
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
-    if (tid < PF_TOK) {
+    const uint32_t slab = (uint32_t)(2u * (uint32_t)F * rbytes);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), 0, (int)slab,
+                                                                         0x00020000);
+    if (tid < NTOK) {
         const int qp = p.sorted[tile.begin + min(tid, tile.n - 1)];
-        sm.pair[tid] = qp;
-        sm.tok[tid] = qp / K;
+        L.pair[tid] = qp;
+        L.tok[tid] = qp / K;
     }
-    if (!q4) {
+    if (!Q4) {
         const u32x4 * src = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_pf);
-        u32x4 * dst = reinterpret_cast<u32x4 *>(sm.codes);
+        u32x4 * dst = reinterpret_cast<u32x4 *>(L.codes);
         for (int i = tid; i < 1024 * 8 / 16; i += WG) dst[i] = src[i];
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo |= ((tid >> i) & 1u) << (8 * i + 2);
-            hi |= ((tid >> (i + 4)) & 1u) << (8 * i + 2);
-        }
-        sm.sgn[tid] = make_uint2(lo, hi);                       // WG == 256 sign bytes
         if (tid < 16) {
             const uint32_t * t = c_iq2s_split.t[tid];
-            sm.split[tid] = u32x4{t[0], t[1], t[2], t[3]};
+            L.split[tid] = u32x4{t[0], t[1], t[2], t[3]};
         }
     }
     __syncthreads();
 
-    // staging geometry, fixed for the K loop
-    uint32_t wrow[GU_WREG];      // byte offset of the chunk's row in the slab; ~0u: no chunk
-    uint32_t wdst[GU_WREG];      // LDS offset of the chunk | chunk index << 16
-#pragma unroll
-    for (int k = 0; k < GU_WREG; ++k) {
-        const int i = tid + WG * k;
-        const int r = i / nwc, c = i - nwc * r;
-        // local row r: gate row 64 rb + r (r < 64) or up row F + 64 rb + r - 64,
-        // clamped into the slab (rows past n_ff are computed and discarded)
+    // ---- copies into LDS: wave w moves token blocks 4 (w NT + i) .. + 3 (16
+    // lanes a token, lane slot i ^ token), the mins sums of 32 tokens (wave <
+    // ceil(NT / 2), Q4_K) and the scales of 64 tokens (wave < ceil(NT / 4))
+    const bool mb_mover = Q4 && 32 * wave < NTOK, d8_mover = 64 * wave < NTOK;
+    // Q4_K rows: 128 rows x 9 chunks of one super-block, [row][144] in LDS;
+    // copy j (0..17, wave w takes j = w, w + 4, ...) moves chunks 64 j .. + 63
+    auto wrow_off = [&](int j) {
+        const int i = 64 * j + lane, r = i / 9, c = i - 9 * r;
         const int gi = min(64 * rb + (r & 63), F - 1);
-        const int row = r < 64 ? gi : F + gi;
-        wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)row * rbytes) : ~0u;
-        wdst[k] = (uint32_t)(r * (q4 ? 144 : 96) + 16 * c) | ((uint32_t)c << 16);
-    }
-    uint32_t xsrc[GU_XREG];
+        return (uint32_t)(r < 64 ? gi : F + gi) * rbytes + 16u * (uint32_t)c;
+    };
+    auto copy_in = [&](int s, uint8_t * xb, _Float16 * mbb, float * d8b, uint8_t * wb) {
+        if constexpr (Q4) {
+            const uint8_t * wsb = W + 144 * s;
+            asm volatile("" : "+s"(wsb));
 #pragma unroll
-    for (int k = 0; k < GU_XREG; ++k) {
-        const int i = tid + WG * k, j = i >> 4, c = i & 15;
-        xsrc[k] = (uint32_t)(sm.tok[j] * p.d_model + 16 * c);
-    }
-    const int tok_s = tid < NTOK ? sm.tok[tid] * NSB : 0;
-    const int tok_m = (tid >= 64 && tid < 64 + 2 * NTOK) ? sm.tok[(tid - 64) >> 1] * NSB * 16 + 8 * ((tid - 64) & 1) : 0;
-
-    GuStage g;
-    auto fetch = [&](int s) {
-#pragma unroll
-        for (int k = 0; k < GU_WREG; ++k) {
-            g.w[k] = u32x4{0, 0, 0, 0};
-            if (wrow[k] != ~0u) {
-                const uint32_t ps = wrow[k] + (uint32_t)(bb * s);
-                const int c = (int)(wdst[k] >> 16);
-                if (q4 || c < chunk_count(ps, 82))
-                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~15u) + 16 * c);
+            for (int k = 0; k < 5; ++k) {
+                const int j = wave + 4 * k;
+                if (j < 18) lds_dma16(wsb + wrow_off(j), wb + 1024 * j);
             }
         }
+        // the super-block's offsets are made opaque, so that the compiler
+        // keeps one uniform base per copy (an SGPR pair) and the lanes' 32-bit
+        // offsets (recomputed from the token list: no registers held)
+        const uint8_t * xs = reinterpret_cast<const uint8_t *>(p.xq) + 256 * s;
+        const uint8_t * ms = reinterpret_cast<const uint8_t *>(p.xm) + 32 * s;
+        const uint8_t * ds = reinterpret_cast<const uint8_t *>(p.xd) + 4 * s;
+        asm volatile("" : "+s"(xs), "+s"(ms), "+s"(ds));
 #pragma unroll
-        for (int k = 0; k < GU_XREG * NT / PF_NTS; ++k)
-            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xq + xsrc[k] + 256 * s);
-        if (tid < NTOK) g.d8 = p.xd[tok_s + s];
-        if (q4 && tid >= 64 && tid < 64 + 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
+        for (int i = 0; i < NT; ++i) {
+            const int t = 4 * (wave * NT + i) + (lane >> 4);
+            const int c = (lane & 15) ^ (t & 15);
+            lds_dma16(xs + (uint32_t)(L.tok[t] * D + 16 * c), xb + 1024 * (wave * NT + i));
+        }
+        if (mb_mover) {
+            const int t = min(32 * wave + (lane >> 1), NTOK - 1);
+            lds_dma16(ms + (uint32_t)(L.tok[t] * NSB * 32 + 16 * (lane & 1)), mbb + 16 * 32 * wave);
+        }
+        if (d8_mover) lds_dma4(ds + (uint32_t)(L.tok[min(64 * wave + lane, NTOK - 1)] * NSB * 4), d8b + 64 * wave);
     };
-    auto store = [&](int s) {
+
+    // ---- this lane's rows: local row 32 wave + 16 rs + l16 is gate row
+    // 64 rb + r (r < 64) or up row F + 64 rb + r - 64, clamped into the slab
+    // (rows past n_ff are computed and discarded)
+    uint32_t voff[2], rowpar[2];
 #pragma unroll
-        for (int k = 0; k < GU_WREG; ++k)
-            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(sm.w + (wdst[k] & 0xFFFF)) = g.w[k];
+    for (int rs = 0; rs < 2; ++rs) {
+        const int r = 32 * wave + 16 * rs + l16;
+        const int gi = min(64 * rb + (r & 63), F - 1);
+        const int row = r < 64 ? gi : F + gi;
+        voff[rs] = (uint32_t)row * rbytes;
+        rowpar[rs] = (voff[rs] >> 1) & 1u;                      // row start mod 4, halved (slabs are 16-aligned)
+    }
+    Iq2Raw wi[Q4 ? 1 : 2];
+    auto load_rows = [&](int s) {
+        if constexpr (!Q4) {
 #pragma unroll
-        for (int k = 0; k < GU_XREG * NT / PF_NTS; ++k) {
-            const int i = tid + WG * k, j = i >> 4, c = i & 15;
-            *reinterpret_cast<u32x4 *>(sm.x + j * PF_XP + 16 * c) = g.x[k];
-        }
-        if (tid < NTOK) sm.d8[tid] = g.d8;
-        if (q4 && tid >= 64 && tid < 64 + 2 * NTOK) {
-            const int i = tid - 64;
-            *reinterpret_cast<u32x4 *>(sm.mb + 16 * (i >> 1) + 8 * (i & 1)) = g.mb;
-        }
-        if (tid < PF_ROWS) {
-            const int r = tid;
-            const int gi = min(64 * rb + (r & 63), F - 1);
-            const uint64_t ps = (uint64_t)(r < 64 ? gi : F + gi) * rbytes + (uint64_t)bb * s;
-            sm.poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
+            for (int rs = 0; rs < 2; ++rs) iq2_raw_load(wi[rs], wr, voff[rs], rowpar[rs], s, q);
         }
     };
 
@@ -508,26 +605,29 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
     const _Float16 mo = q == 0 ? (_Float16)(-32768.0f) : q == 1 ? (_Float16)(-1024.0f) : (_Float16)0.0f;
     const h2 mn_mul = h2{mm, mm}, mn_off = h2{mo, mo};
 
-    fetch(0);
-    for (int s = 0; s < NSB; ++s) {
-        if (s) __syncthreads();                                 // the previous super-block is consumed
-        store(s);
+    // one super-block: expand this lane's rows, start the next super-block's
+    // copies and rows, then every 16-token tile against both row tiles
+    auto step = [&](int s, const uint8_t * xb, const _Float16 * mbb, const float * d8b, const uint8_t * wb,
+                    uint8_t * xn, _Float16 * mbn, float * d8n, uint8_t * wn) {
+        // this wave's copies and rows of super-block s have landed; after the
+        // barrier every wave's have, and every wave is done with s - 1
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (s + 1 < NSB) fetch(s + 1);
 
-        // ---- the B operands of this wave's two 16-row tiles: 4 K-steps of 64,
-        // lane (row l16, quarter q) holds 16 values of each step.  Q4_K: step st,
-        // quarter q = values 64 st + 16 q (sub-block 2 st + q / 2); IQ2_S: the
-        // 16-value group 4 q + st (its bytes are contiguous per lane).  The
-        // activations are read in the same order.
+        // ---- B operands of this wave's two 16-row tiles: 4 K-steps of 64,
+        // lane (row l16, quarter q) holds 16 values of each step.  Q4_K: step
+        // st, quarter q = values 64 st + 16 q (sub-block 2 st + q / 2); IQ2_S:
+        // the 16-value group 4 q + st.  The activations are read in the same
+        // order.  The sub-block scales are folded in: Q4_K's 6-bit scale as
+        // 8 sh + sl (q sh, q sl <= 105), IQ2_S's grid (2 ls + 1) as 64 h + l.
         v4i bh[2][4], bl[2][4];
         h8 bm[2];
         float dr[2], mr[2];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const int wo = sm.poff[32 * wave + 16 * rs + l16];
-            if (q4) {
-                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(sm.w + wo);
+            if constexpr (Q4) {
+                const uint8_t * wrw = wb + (32 * wave + 16 * rs + l16) * 144;
+                const u32x4 hdr = *reinterpret_cast<const u32x4 *>(wrw);
                 dr[rs] = h2f(hdr.x & 0xFFFF);
                 mr[rs] = h2f(hdr.x >> 16);
                 // 6-bit scales and mins, four per dword (get_scale_min_k4,
@@ -537,21 +637,18 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
                 const uint32_t mn03 = hdr.z & 0x3F3F3F3Fu;
                 const uint32_t sc47 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
                 const uint32_t mn47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-                // sc = 8 sh + sl
                 const uint32_t sh03 = (sc03 >> 3) & 0x07070707u, sl03 = sc03 & 0x07070707u;
                 const uint32_t sh47 = (sc47 >> 3) & 0x07070707u, sl47 = sc47 & 0x07070707u;
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(sm.w + wo + 16 + 32 * st + 16 * (q & 1));
-                    // this lane's sub-block scale halves, each byte in both
-                    // 16-bit halves
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wrw + 16 + 32 * st + 16 * (q & 1));
                     const uint32_t sel = (st & 1) ? sel_odd : sel_even;
                     const uint32_t sh2 = __builtin_amdgcn_perm(0u, st < 2 ? sh03 : sh47, sel);
                     const uint32_t sl2 = __builtin_amdgcn_perm(0u, st < 2 ? sl03 : sl47, sel);
-                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                    const uint32_t w4v[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const uint32_t nb = (w4[i] >> nib_shift) & 0x0F0F0F0Fu;
+                        const uint32_t nb = (w4v[i] >> nib_shift) & 0x0F0F0F0Fu;
                         bh[rs][st][i] = (int)bytes_mul(nb, sh2);
                         bl[rs][st][i] = (int)bytes_mul(nb, sl2);
                     }
@@ -566,23 +663,25 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
                     bm[rs][2 * i + 1] = mv.y;
                 }
             } else {
-                dr[rs] = h2f(lds16(sm.w, wo));
+                const Iq2Raw & w = wi[rs];
+                dr[rs] = h2f((w.d >> w.sh_d) & 0xFFFFu);
                 mr[rs] = 0.0f;
                 // this lane's groups 4q .. 4q + 3: grid entries 8q .. 8q + 7
-                const uint2 qs8 = lds64u(sm.w, wo + 2 + 8 * q);
-                const uint2 sg8 = lds64u(sm.w, wo + 34 + 8 * q);
-                const uint32_t qh2 = lds16(sm.w, wo + 66 + 2 * q);          // 2 bits per entry
-                const uint32_t sc2 = lds16(sm.w, wo + 74 + 2 * q);          // 4 bits per group
+                const uint2 qs8 = make_uint2(__builtin_amdgcn_alignbit(w.qs.y, w.qs.x, w.sh_q),
+                                             __builtin_amdgcn_alignbit(w.qs.z, w.qs.y, w.sh_q));
+                const uint2 sg8 = make_uint2(__builtin_amdgcn_alignbit(w.sg.y, w.sg.x, w.sh_q),
+                                             __builtin_amdgcn_alignbit(w.sg.z, w.sg.y, w.sh_q));
+                const uint32_t qh2 = (w.qh >> w.sh_h) & 0xFFFFu;        // 2 bits per entry
+                const uint32_t sc2 = (w.sc >> w.sh_h) & 0xFFFFu;        // 4 bits per group
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
                     const uint32_t qsw = st < 2 ? qs8.x : qs8.y, sgw = st < 2 ? sg8.x : sg8.y;
-                    const int b0 = 16 * (st & 1);                            // bit of entry 2 st in its dword
+                    const int b0 = 16 * (st & 1);                       // bit of entry 2 st in its dword
                     const uint32_t i0 = __builtin_amdgcn_ubfe(qsw, b0, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st, 2) << 8);
                     const uint32_t i1 = __builtin_amdgcn_ubfe(qsw, b0 + 8, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st + 2, 2) << 8);
-                    const uint2 c0 = sm.codes[i0], c1 = sm.codes[i1];
-                    const uint2 s0 = sm.sgn[__builtin_amdgcn_ubfe(sgw, b0, 8)];
-                    const uint2 s1 = sm.sgn[__builtin_amdgcn_ubfe(sgw, b0 + 8, 8)];
-                    const u32x4 t = sm.split[__builtin_amdgcn_ubfe(sc2, 4 * st, 4)];
+                    const uint2 c0 = L.codes[i0], c1 = L.codes[i1];
+                    const uint2 s0 = sign_sel(sgw, b0), s1 = sign_sel(sgw, b0 + 8);
+                    const u32x4 t = L.split[__builtin_amdgcn_ubfe(sc2, 4 * st, 4)];
                     const uint32_t sel[4] = {c0.x | s0.x, c0.y | s0.y, c1.x | s1.x, c1.y | s1.y};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -595,19 +694,29 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
             }
         }
 
+        // ---- the next super-block in flight during this one's MFMAs
+        if (s + 1 < NSB) {
+            copy_in(s + 1, xn, mbn, d8n, wn);
+            load_rows(s + 1);
+        }
+
         // ---- every 16-token tile of the group against both row tiles
-        const int xo_st = q4 ? 64 : 16, xo_q = q4 ? 16 : 64;
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) {
-            const int8_t * xr = sm.x + (16 * ts + l16) * PF_XP + xo_q * q;
+            const uint8_t * xr = xb + (16 * ts + l16) * 256;
             v4i a[4];
 #pragma unroll
-            for (int st = 0; st < 4; ++st) a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + xo_st * st));
-            const f4 d8 = *reinterpret_cast<const f4 *>(sm.d8 + 16 * ts + 4 * q);
+            for (int st = 0; st < 4; ++st) {
+                const int c = Q4 ? q + 4 * st : 4 * q + st;
+                a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + 16 * (c ^ l16)));
+            }
+            const f4 d8 = *reinterpret_cast<const f4 *>(d8b + 16 * ts + 4 * q);
             h8 am;
-            if (q4) {
-                const u32x4 mv = q < 2 ? *reinterpret_cast<const u32x4 *>(sm.mb + 16 * (16 * ts + l16) + 8 * q)
-                                       : u32x4{0, 0, 0, 0};
+            if constexpr (Q4) {
+                // every lane loads (no branch); quarters 2, 3 are zeroed
+                u32x4 mv = *reinterpret_cast<const u32x4 *>(mbb + 16 * (16 * ts + l16) + 8 * (q & 1));
+                const uint32_t keep = q < 2 ? ~0u : 0u;
+                mv.x &= keep; mv.y &= keep; mv.z &= keep; mv.w &= keep;
                 __builtin_memcpy(&am, &mv, 16);
             }
 #pragma unroll
@@ -622,7 +731,7 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
                 // column in its group depends on the bucketing order, and left
                 // to itself the compiler contracts some unrolled columns into
                 // an fma and not others.
-                if (q4) {
+                if constexpr (Q4) {
                     const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -639,48 +748,104 @@ __device__ __forceinline__ void pf_gate_up_group(const PfParams & p, const PfTil
                 }
             }
         }
+    };
+
+    copy_in(0, L.x0, L.mb0, L.d80, L.w0);
+    load_rows(0);
+    for (int s = 0; s < NSB; s += 2) {
+        step(s, L.x0, L.mb0, L.d80, L.w0, L.x1, L.mb1, L.d81, L.w1);
+        if (s + 1 < NSB) step(s + 1, L.x1, L.mb1, L.d81, L.w1, L.x0, L.mb0, L.d80, L.w0);
     }
 
-    // ---- epilogue: GEGLU of gate row i and up row i, q8_0 of each 32-block
-    // of the result into the pair's down activations
-    const float f = q4 ? 1.0f : 0.125f;
-    float * stg = reinterpret_cast<float *>(sm.x);
+    // ---- epilogue: every tile's outputs into LDS at once (gate rows in x0,
+    // up rows in x1: [64 rows][NTOK + 1]), then per (token, 32-block) unit --
+    // one per half-wave and pass -- GEGLU of gate row i and up row i and q8_0
+    // of the 32 results into the pair's down activations.  A lane reads all
+    // its units' values and GEGLU table entries before it uses the first.
+    constexpr int SP = NTOK + 1;
+    constexpr int NU = NTOK / 4;                                // units per half-wave
+    const float f = Q4 ? 1.0f : 0.125f;
+    float * sg = reinterpret_cast<float *>(L.x0);
+    float * su = reinterpret_cast<float *>(L.x1);
+    __syncthreads();                                            // the K loop's readers are done
+    {
+        float * dst = wave < 2 ? sg : su;
 #pragma unroll
-    for (int ts = 0; ts < NT; ++ts) {
-        __syncthreads();                                        // the K loop / previous tile's readers are done
+        for (int ts = 0; ts < NT; ++ts)
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs)
+            for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) stg[(32 * wave + 16 * rs + l16) * GU_STP + 4 * q + r] = f * y[rs][ts][r];
-        __syncthreads();
+                for (int r = 0; r < 4; ++r)
+                    dst[(32 * (wave & 1) + 16 * rs + l16) * SP + 16 * ts + 4 * q + r] = f * y[rs][ts][r];
+    }
+    __syncthreads();
+    const int hw = 2 * wave + (lane >> 5), i = lane & 31;
+    float gv[NU], uv[NU];
+    uint32_t te[NU];
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int u = 8 * pass + 2 * wave + (lane >> 5);    // (token, 32-block) unit, 0..31
-            const int tk = u >> 1, blk = u & 1, i = lane & 31;
-            const int j = 16 * ts + tk;
-            const int fi = 64 * rb + 32 * blk;                  // first gate index of the block
-            const bool live = j < tile.n && fi < F;
-            const float gv = stg[(32 * blk + i) * GU_STP + tk];
-            const float uv = stg[(64 + 32 * blk + i) * GU_STP + tk];
-            const float v = geglu1<GSRC>(gv, uv);
-            const int64_t qp = sm.pair[min(j, PF_TOK - 1)];
-            q8_store32<AM_CPU>(v, p.ah + qp * F + fi + i, p.al + qp * F + fi + i, nullptr, live);
-        }
+    for (int k = 0; k < NU; ++k) {
+        const int u = 8 * k + hw, j = u >> 1, blk = u & 1;
+        gv[k] = sg[(32 * blk + i) * SP + j];
+        uv[k] = su[(32 * blk + i) * SP + j];
+    }
+    if constexpr (GSRC == SRC_GEGLU_TABLE) {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) te[k] = gelu_entry(gv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const int u = 8 * k + hw, j = u >> 1, blk = u & 1;
+        const int fi = 64 * rb + 32 * blk;                      // first gate index of the block
+        const bool live = j < tile.n && fi < F;
+        const int64_t qp = L.pair[j];
+        const float v = GSRC == SRC_GEGLU_TABLE ? geglu_from_entry(gv[k], uv[k], te[k]) : geglu1<GSRC>(gv[k], uv[k]);
+        q8_store32<AM_CPU>(v, p.ah + qp * F + fi + i, p.al + qp * F + fi + i, nullptr, live);
     }
 }
 
+// Grid: 8 x ceil(max_tiles / 8) x RB workgroups in one dimension.  The
+// hardware deals workgroups to the 8 XCDs in turn (workgroup i to XCD
+// i mod 8), so workgroup i serves group 8 (k / RB) + i mod 8, row block
+// k mod RB (k = i / 8): all row blocks of a group run on one XCD and read
+// its activations through one L2, and every XCD takes the full groups first.
 template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up(const PfParams p) {
-    __shared__ __align__(16) GuSmem sm;
-    const int g = blockIdx.y, rb = blockIdx.x;
-    if (g >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[g];
-    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
+    __shared__ __align__(16) uint8_t x0[G2_XB];
+    __shared__ __align__(16) uint8_t x1[G2_XB];
+    __shared__ __align__(16) _Float16 mb0[G2_MBT * 16];
+    __shared__ __align__(16) _Float16 mb1[G2_MBT * 16];
+    __shared__ __align__(16) float d80[128];
+    __shared__ __align__(16) float d81[128];
+    __shared__ __align__(16) uint8_t w0[G2_WB];
+    __shared__ __align__(16) uint8_t w1[G2_WB];
+    __shared__ int tok[G2_TOKMAX], pair[G2_TOKMAX];
+    const Gu2Lds sm = {x0, x1, w0, w1, mb0, mb1, d80, d81, reinterpret_cast<uint2 *>(w0),
+                       reinterpret_cast<u32x4 *>(w1), tok, pair};
+    const int RB = (p.n_ff + 63) / 64;
+    const int i = blockIdx.x, k = i >> 3;
+    const int g = 8 * (k / RB) + (i & 7), rb = k - (k / RB) * RB;
+    if (g >= *p.n_gtiles) return;
+    const PfTile tile = p.gtiles[g];
+    if (!tile_valid(p, tile) || tile.n <= 0) return;
+    const int wt = tile.tier == 0 ? HT : CT;
     const int nt = (tile.n + 15) >> 4;
-    if (nt == 1) pf_gate_up_group<HT, CT, GSRC, 1>(p, tile, sm, rb);
-    else if (nt == 2) pf_gate_up_group<HT, CT, GSRC, 2>(p, tile, sm, rb);
-    else if (nt == 3) pf_gate_up_group<HT, CT, GSRC, 3>(p, tile, sm, rb);
-    else pf_gate_up_group<HT, CT, GSRC, 4>(p, tile, sm, rb);
+    if (wt == T_Q4_K) {
+        if (tile.n > G2_TOKQ4) return;
+        switch (nt) {
+        case 1: pf_gu2_group<T_Q4_K, GSRC, 1>(p, tile, sm, rb); break;
+        case 2: pf_gu2_group<T_Q4_K, GSRC, 2>(p, tile, sm, rb); break;
+        case 3: pf_gu2_group<T_Q4_K, GSRC, 3>(p, tile, sm, rb); break;
+        default: pf_gu2_group<T_Q4_K, GSRC, 3>(p, tile, sm, rb); break;
+        }
+    } else {
+        if (tile.n > G2_TOKIQ2) return;
+        switch (nt) {
+        case 1: pf_gu2_group<T_IQ2_S, GSRC, 1>(p, tile, sm, rb); break;
+        case 2: pf_gu2_group<T_IQ2_S, GSRC, 2>(p, tile, sm, rb); break;
+        case 3: pf_gu2_group<T_IQ2_S, GSRC, 3>(p, tile, sm, rb); break;
+        default: pf_gu2_group<T_IQ2_S, GSRC, 4>(p, tile, sm, rb); break;
+        }
+    }
 }
 
 // ---------------------------------------------------- gate_up, q8_1 mode
@@ -719,7 +884,7 @@ constexpr int PF_TOK1 = 32;               // tokens of one q8_1 workgroup (half 
 constexpr int GU1_XREG = 8;               // activation chunks per thread per super-block (32 tokens x 64)
 
 struct GuSmemQ1 {
-    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows, as in the q8_K kernel
+    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows: Q4_K at 144 r, IQ2_S at 96 r + offset
     _Float16 x[PF_TOK1 * PF_XH];          // the tokens' d q of this super-block, exact hi and lo parts
     _Float16 mb[PF_TOK1 * 16];            // their per-32 mins terms u = d sum(q), {hi_0..7, lo_0..7}
     u32x4 csel[1024];                     // IQ2_S grid: v_perm selectors (lo byte c, hi byte 4 + c) per value pair
@@ -1217,6 +1382,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 using namespace dev;
 
 int pf_max_tiles(int P, int n_expert) { return (P + PF_TOK - 1) / PF_TOK + std::min(n_expert, P); }
+int pf_max_gtiles(int P, int n_expert) { return (P + 15) / 16 + std::min(n_expert, P); }
 
 namespace {
 template <typename F>
@@ -1229,13 +1395,22 @@ void launch_gu(int gelu, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1,
     if (p.act_mode == AM_Q8_1) {
         if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
         else launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
-    } else if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
-    else launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
+    } else {
+        const dim3 g2(8 * ((p.max_gtiles + 7) / 8) * ((p.n_ff + 63) / 64));
+        if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, g2, s, e0, e1, p);
+        else launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TABLE>, g2, s, e0, e1, p);
+    }
 }
+// pairs per gate_up group of an expert in format t (the Q4_K kernel holds
+// 128 tokens' activations in LDS; IQ2_S's tables take the room of half)
+int gate_up_cap(int t) { return t == T_Q4_K ? G2_TOKQ4 : G2_TOKIQ2; }
 }  // namespace
 
-hipError_t launch_prefill(const PfParams & p, int hgu, int cgu, int hdn, int cdn, int gelu, hipStream_t s,
+hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cdn, int gelu, hipStream_t s,
                           hipEvent_t * ev) {
+    PfParams p = p0;
+    p.gcap[0] = p.act_mode == AM_Q8_1 ? PF_TOK : gate_up_cap(hgu);
+    p.gcap[1] = p.act_mode == AM_Q8_1 ? PF_TOK : gate_up_cap(cgu);
     hipEvent_t e[4] = {};
     if (ev)
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
