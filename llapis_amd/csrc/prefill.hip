@@ -40,7 +40,9 @@
 //                  scale per 32-block here; on int8 MFMA every output would
 //                  need a per-block fp32 rescale by d_w d8 (three VALU
 //                  operations per output and block), which made that variant
-//                  VALU-bound at several times this one's time.
+//                  VALU-bound at several times this one's time.  K runs in
+//                  chunks of two blocks, copied into LDS by the load unit one
+//                  chunk ahead; every row block of a group on one XCD.
 // The combine is the generic k_combine.
 #include <hip/hip_ext.h>
 
@@ -61,10 +63,6 @@ typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 __constant__ Iq2sTables c_iq2s_tab_pf = make_iq2s_tables();
 
 constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged weight row (Q4_K 144, IQ2_S <= 96)
-constexpr int PF_DCB = 4;                 // 32-blocks per down K chunk
-constexpr int PF_DXP = PF_DCB * 32 + 8;   // LDS pitch (halfs) of a staged down activation row
-constexpr int PF_WROW_DN = 112;           // staged bytes per weight row and down chunk (<= 4 * 22 + 14)
-constexpr int PF_WPITCH_DN = 120;         // LDS pitch of those rows
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -1179,21 +1177,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 // ------------------------------------------------------------------ down
 
-constexpr int DN_WREG = 4;     // weight chunks per thread per down chunk (128 rows x 7)
-constexpr int DN_XREG = 8;     // activation chunks per thread per down chunk (64 pair slots x (16 hi + 16 lo))
-
-struct DnStage {
-    u32x4 w[DN_WREG];
-    u32x4 x[DN_XREG];
-};
-
-struct DnSmem {
-    uint8_t w[PF_ROWS * PF_WPITCH_DN + 16];    // +16: reads past a row's end
-    _Float16 xh[PF_TOK * PF_DXP];              // d8 q, fp16 high part, [pair slot][128 values + pad]
-    _Float16 xl[PF_TOK * PF_DXP];              // and the exact remainder
-    int pair[PF_TOK], poff[PF_ROWS];
-};
-
 // 8 values (8 u .. 8 u + 7 of 32-block `blk` at LDS byte offset b, 2-aligned)
 // as exact fp16 integers: Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q]
 // (:2653); the block scale d_w out
@@ -1237,71 +1220,63 @@ __device__ __forceinline__ h8 down_frag(const uint8_t * sw, int b, int u, float 
 }
 
 // One (group, 128-row block) of the down GEMM with NT 16-token tiles.  Wave
-// w owns rows 32 w .. 32 w + 31 as two 16-row MFMA tiles.
-template <int HT, int CT, int NT>
-__device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile & tile, DnSmem & sm, const int rb) {
-    static_assert(HT == T_Q5_0 || HT == T_IQ4_NL, "down formats");
-    static_assert(CT == T_Q5_0 || CT == T_IQ4_NL, "down formats");
-    static_assert(PF_ROWS * (PF_WROW_DN / 16) <= DN_WREG * WG && PF_TOK * 32 == DN_XREG * WG, "staging");
-    constexpr int NTOK = 16 * NT;
-    constexpr int WCH = PF_WROW_DN / 16;
-    constexpr int XK = 2 * NT;                     // activation rounds of 8 pair slots
+// w owns rows 32 w .. 32 w + 31 as two 16-row MFMA tiles.  K (n_ff) runs in
+// chunks of two 32-blocks: the load unit copies the next chunk's activation
+// parts and weight rows into LDS while the current one is used (two buffers
+// of each, separately declared, one barrier per chunk).  A pair's chunk is
+// 16 slots of 16 bytes (slots 0..7 the high parts of its 64 values, 8..15
+// the low parts), slot s at s ^ (pair & 15): the 16 pairs of an MFMA
+// fragment read 16 distinct slots.  A row's chunk is the 16-byte aligned
+// window holding its two blocks (<= 59 bytes: four slots).
+constexpr int D2_WP = 64;                          // LDS bytes per weight row and chunk
+constexpr int D2_XB = PF_TOK * 256;                // activations of one chunk: [pair slot][16][16 bytes]
+constexpr int D2_WB = PF_ROWS * D2_WP;
 
-    const int wtype = tile.tier == 0 ? HT : CT;
-    const int D = p.d_model, F = p.n_ff, NB = F / 32;
+struct Dn2Lds {
+    uint8_t * x0; uint8_t * x1;
+    uint8_t * w0; uint8_t * w1;
+    int * pair;
+};
+
+template <int WT, int NT>
+__device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile & tile, const Dn2Lds & L,
+                                               const int rb) {
+    static_assert(WT == T_Q5_0 || WT == T_IQ4_NL, "down formats");
+    constexpr int NTOK = 16 * NT;
+    constexpr int BS = WT == T_Q5_0 ? 22 : 18;
+    static_assert(2 * BS + 15 <= D2_WP, "a chunk's window fits its LDS row");
+    const int D = p.d_model, F = p.n_ff, NB = F / 32, NC = (NB + 1) / 2;
     const int r0 = rb * PF_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
-    const int bs = wtype == T_Q5_0 ? 22 : 18;
-    const uint64_t rbytes = (uint64_t)NB * bs;
+    const uint32_t rbytes = (uint32_t)(NB * BS);
+    const uint32_t last16 = (uint32_t)D * rbytes - 16u;      // the slab's last 16-byte chunk
     const uint8_t * W = tile.tier == 0 ? p.hot_dn + (uint64_t)tile.idx * p.hot_dn_stride
                                        : p.cold_dn + (uint64_t)tile.idx * p.cold_dn_stride;
-    if (tid < PF_TOK) sm.pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
+    if (tid < NTOK) L.pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
     __syncthreads();
 
-    DnStage g;
-    auto fetch = [&](int c0) {
-        const int cb = min(PF_DCB, NB - c0);
+    auto copy_in = [&](int c, uint8_t * xb, uint8_t * wb) {
+        const _Float16 * ah = p.ah;
+        const _Float16 * al = p.al;
+        const uint8_t * w = W;
+        asm volatile("" : "+s"(ah), "+s"(al), "+s"(w));
+        // activations: wave w moves pair blocks w NT + k (four pair slots each);
+        // a last chunk of one block reads its second block's slots from inside
+        // the row (unused)
 #pragma unroll
-        for (int k = 0; k < DN_WREG; ++k) {
-            const int i = tid + WG * k, r = i / WCH, c = i - WCH * r;
-            g.w[k] = u32x4{0, 0, 0, 0};
-            if (r < PF_ROWS) {
-                const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rbytes + (uint64_t)c0 * bs;
-                if (c < chunk_count(ps, cb * bs))
-                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~(uint64_t)15) + 16 * c);
-            }
+        for (int k = 0; k < NT; ++k) {
+            const int j = 4 * (wave * NT + k) + (lane >> 4);
+            const int sg = (lane & 15) ^ (j & 15);
+            const uint32_t off = (uint32_t)(L.pair[j] * F + min(64 * c + 8 * (sg & 7), F - 8));
+            lds_dma16((sg < 8 ? ah : al) + off, xb + 1024 * (wave * NT + k));
         }
+        // weights: 128 rows x 4 slots; wave w moves slots 64 j .. + 63 for j = w, w + 4
 #pragma unroll
-        for (int k = 0; k < XK; ++k) {
-            // round k: pair slots 8 k .. 8 k + 7, 32 chunks of 8 values each:
-            // chunks 0..15 the high parts of the 128 values, 16..31 the low
-            const int i = tid + WG * k, j = i >> 5, c = i & 31, v8 = c & 15;
-            g.x[k] = u32x4{0, 0, 0, 0};
-            if (v8 < 4 * cb) {
-                const _Float16 * src = ((c >> 4) ? p.al : p.ah) + (int64_t)sm.pair[j] * F + 32 * c0 + 8 * v8;
-                g.x[k] = *reinterpret_cast<const u32x4 *>(src);
-            }
-        }
-    };
-    auto store = [&](int c0) {
-#pragma unroll
-        for (int k = 0; k < DN_WREG; ++k) {
-            const int i = tid + WG * k, r = i / WCH, c = i - WCH * r;
-            if (r < PF_ROWS) {
-                uint2 * d = reinterpret_cast<uint2 *>(sm.w + r * PF_WPITCH_DN + 16 * c);   // 8-aligned
-                d[0] = make_uint2(g.w[k].x, g.w[k].y);
-                d[1] = make_uint2(g.w[k].z, g.w[k].w);
-                if (c == 0) {
-                    const uint64_t ps = (uint64_t)min(r0 + r, D - 1) * rbytes + (uint64_t)c0 * bs;
-                    sm.poff[r] = r * PF_WPITCH_DN + (int)(ps & 15);
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < XK; ++k) {
-            const int i = tid + WG * k, j = i >> 5, c = i & 31;
-            _Float16 * dst = ((c >> 4) ? sm.xl : sm.xh) + j * PF_DXP + 8 * (c & 15);
-            *reinterpret_cast<u32x4 *>(dst) = g.x[k];
+        for (int k = 0; k < 2; ++k) {
+            const int jj = wave + 4 * k, i = 64 * jj + lane, r = i >> 2, cc = i & 3;
+            const uint32_t ps = (uint32_t)min(r0 + r, D - 1) * rbytes + (uint32_t)(2 * BS * c);
+            const uint32_t off = min((ps & ~15u) + 16u * (uint32_t)cc, last16);    // slots past the slab: unused
+            lds_dma16(w + off, wb + 1024 * jj);
         }
     };
 
@@ -1310,22 +1285,31 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
     for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int rowc[2];
+#pragma unroll
+    for (int rs = 0; rs < 2; ++rs) rowc[rs] = min(r0 + 32 * wave + 16 * rs + l16, D - 1);
 
-    auto blocks = [&](auto wt, int cb) {
-        constexpr int T = decltype(wt)::value;
+    auto step = [&](int c, const uint8_t * xb, const uint8_t * wb, uint8_t * xn, uint8_t * wn) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c + 1 < NC) copy_in(c + 1, xn, wn);
+        const int cb = min(2, NB - 2 * c);
+        int base[2];
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs)
+            base[rs] = (32 * wave + 16 * rs + l16) * D2_WP + (int)(((uint32_t)rowc[rs] * rbytes + 2u * BS * c) & 15u);
         for (int b = 0; b < cb; ++b) {
             // B: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block b
             h8 bw[2];
             float dw[2];
 #pragma unroll
-            for (int rs = 0; rs < 2; ++rs)
-                bw[rs] = down_frag<T>(sm.w, sm.poff[32 * wave + 16 * rs + l16] + bs * b, q, dw[rs]);
+            for (int rs = 0; rs < 2; ++rs) bw[rs] = down_frag<WT>(wb, base[rs] + BS * b, q, dw[rs]);
 #pragma unroll
             for (int ts = 0; ts < NT; ++ts) {
-                const int xo = (16 * ts + l16) * PF_DXP + 32 * b + 8 * q;
+                const uint8_t * xr = xb + (16 * ts + l16) * 256;
                 h8 ah, al;
-                __builtin_memcpy(&ah, sm.xh + xo, 16);
-                __builtin_memcpy(&al, sm.xl + xo, 16);
+                __builtin_memcpy(&ah, xr + 16 * ((4 * b + q) ^ l16), 16);
+                __builtin_memcpy(&al, xr + 16 * ((8 + 4 * b + q) ^ l16), 16);
 #pragma unroll
                 for (int rs = 0; rs < 2; ++rs) {
                     const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
@@ -1336,15 +1320,10 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
         }
     };
 
-    fetch(0);
-    for (int c0 = 0; c0 < NB; c0 += PF_DCB) {
-        const int cb = min(PF_DCB, NB - c0);
-        if (c0) __syncthreads();
-        store(c0);
-        __syncthreads();
-        if (c0 + PF_DCB < NB) fetch(c0 + PF_DCB);
-        if (wtype == T_Q5_0) blocks(std::integral_constant<int, T_Q5_0>{}, cb);
-        else blocks(std::integral_constant<int, T_IQ4_NL>{}, cb);
+    copy_in(0, L.x0, L.w0);
+    for (int c = 0; c < NC; c += 2) {
+        step(c, L.x0, L.w0, L.x1, L.w1);
+        if (c + 1 < NC) step(c + 1, L.x1, L.w1, L.x0, L.w0);
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
@@ -1353,7 +1332,7 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
         for (int r = 0; r < 4; ++r) {
             const int j = 16 * ts + 4 * q + r;
             if (j >= tile.n) continue;
-            float * out = p.ydn + (int64_t)sm.pair[j] * D;
+            float * out = p.ydn + (int64_t)L.pair[j] * D;
 #pragma unroll
             for (int rs = 0; rs < 2; ++rs) {
                 const int row = r0 + 32 * wave + 16 * rs + l16;
@@ -1363,18 +1342,34 @@ __device__ __forceinline__ void pf_down_group(const PfParams & p, const PfTile &
     }
 }
 
+// Grid: 8 x ceil(max_tiles / 8) x RB workgroups in one dimension, dealt to
+// the XCDs as the gate_up kernel's: all row blocks of a group on one XCD.
 template <int HT, int CT>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_down(const PfParams p) {
-    __shared__ __align__(16) DnSmem sm;
-    const int g = blockIdx.y, rb = blockIdx.x;
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_pf_down(const PfParams p) {
+    __shared__ __align__(16) uint8_t x0[D2_XB];
+    __shared__ __align__(16) uint8_t x1[D2_XB];
+    __shared__ __align__(16) uint8_t w0[D2_WB];
+    __shared__ __align__(16) uint8_t w1[D2_WB];
+    __shared__ int pair[PF_TOK];
+    const Dn2Lds sm = {x0, x1, w0, w1, pair};
+    const int RB = (p.d_model + PF_ROWS - 1) / PF_ROWS;
+    const int i = blockIdx.x, k = i >> 3;
+    const int g = 8 * (k / RB) + (i & 7), rb = k - (k / RB) * RB;
     if (g >= *p.n_tiles) return;
     const PfTile tile = p.tiles[g];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int nt = (tile.n + 15) >> 4;
-    if (nt == 1) pf_down_group<HT, CT, 1>(p, tile, sm, rb);
-    else if (nt == 2) pf_down_group<HT, CT, 2>(p, tile, sm, rb);
-    else if (nt == 3) pf_down_group<HT, CT, 3>(p, tile, sm, rb);
-    else pf_down_group<HT, CT, 4>(p, tile, sm, rb);
+    if ((tile.tier == 0 ? HT : CT) == T_Q5_0) {
+        if (nt == 1) pf_down2_group<T_Q5_0, 1>(p, tile, sm, rb);
+        else if (nt == 2) pf_down2_group<T_Q5_0, 2>(p, tile, sm, rb);
+        else if (nt == 3) pf_down2_group<T_Q5_0, 3>(p, tile, sm, rb);
+        else pf_down2_group<T_Q5_0, 4>(p, tile, sm, rb);
+    } else {
+        if (nt == 1) pf_down2_group<T_IQ4_NL, 1>(p, tile, sm, rb);
+        else if (nt == 2) pf_down2_group<T_IQ4_NL, 2>(p, tile, sm, rb);
+        else if (nt == 3) pf_down2_group<T_IQ4_NL, 3>(p, tile, sm, rb);
+        else pf_down2_group<T_IQ4_NL, 4>(p, tile, sm, rb);
+    }
 }
 
 }  // namespace dev
@@ -1432,7 +1427,7 @@ hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cd
         if (err != hipSuccess) return err;
     }
     {
-        dim3 grid((p.d_model + PF_ROWS - 1) / PF_ROWS, p.max_tiles);
+        dim3 grid(8 * ((p.max_tiles + 7) / 8) * ((p.d_model + PF_ROWS - 1) / PF_ROWS));
         if (hdn == T_Q5_0 && cdn == T_IQ4_NL) launch_pf(k_pf_down<T_Q5_0, T_IQ4_NL>, grid, s, e[2], e[3], p);
         else if (hdn == T_Q5_0 && cdn == T_Q5_0) launch_pf(k_pf_down<T_Q5_0, T_Q5_0>, grid, s, e[2], e[3], p);
         else if (hdn == T_IQ4_NL && cdn == T_IQ4_NL) launch_pf(k_pf_down<T_IQ4_NL, T_IQ4_NL>, grid, s, e[2], e[3], p);
