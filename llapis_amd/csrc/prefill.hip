@@ -878,7 +878,7 @@ constexpr Iq2sHalf make_iq2s_half() {
 __constant__ Iq2sHalf c_iq2s_half = make_iq2s_half();
 
 constexpr int PF_XH = 512 + 8;            // halfs per staged token row of one super-block: 256 hi, 256 lo, pad
-constexpr int PF_TOK1 = 32;               // tokens of one q8_1 workgroup (half a group)
+constexpr int PF_TOK1 = 32;               // pairs per gate_up group in the q8_1 mode
 constexpr int GU1_XREG = 8;               // activation chunks per thread per super-block (32 tokens x 64)
 
 struct GuSmemQ1 {
@@ -900,7 +900,7 @@ struct GuStageQ1 {
     u32x4 mb;
 };
 
-// One (group half, row block) of the gate_up GEMM in the q8_1 activation mode
+// One (group of <= 32 pairs, row block) of the gate_up GEMM in the q8_1 activation mode
 // (ggml-cuda's arithmetic, vecdotq.cuh:504-522 / 864-907): the activation
 // scale is per 32 values, so it is carried by the activation operand -- each
 // value d q as exact fp16 hi + lo parts, two v_mfma_f32_16x16x32_f16 per
@@ -908,11 +908,11 @@ struct GuStageQ1 {
 // scale folded in (Q4_K q sc <= 945, IQ2_S grid (2 ls + 1) <= 1333, both
 // exact).  Every product is exact and one fp32 accumulator chains through the
 // super-block; then d_w per super-block (Q4_K minus dmin times the mins MFMA,
-// IQ2_S d / 8 in the epilogue).  The epilogue is the q8_K kernel's with q8_1
-// down activations.  Workgroup z of a group takes its tokens 32 z ..
+// IQ2_S d / 8 in the epilogue).  The epilogue quantises the down activations
+// to q8_1.
 template <int HT, int CT, int GSRC, int NT>
 __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const PfTile & tile, GuSmemQ1 & sm,
-                                                    const int rb, const int t0, const int n) {
+                                                    const int rb, const int n) {
     static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK1 * 64 == GU1_XREG * WG, "staging shape");
     constexpr int NTOK = 16 * NT;
     const int wtype = tile.tier == 0 ? HT : CT;
@@ -925,7 +925,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
     if (tid < PF_TOK1) {
-        const int qp = p.sorted[tile.begin + t0 + min(tid, n - 1)];
+        const int qp = p.sorted[tile.begin + min(tid, n - 1)];
         sm.pair[tid] = qp;
         sm.tok[tid] = qp / K;
     }
@@ -1166,13 +1166,17 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
 template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up_q1(const PfParams p) {
     __shared__ __align__(16) GuSmemQ1 sm;
-    const int g = blockIdx.y, rb = blockIdx.x, t0 = PF_TOK1 * blockIdx.z;
-    if (g >= *p.n_tiles) return;
-    const PfTile tile = p.tiles[g];
-    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK || t0 >= tile.n) return;
-    const int n = min(PF_TOK1, tile.n - t0);
-    if (n > 16) pf_gate_up_group_q1<HT, CT, GSRC, 2>(p, tile, sm, rb, t0, n);
-    else pf_gate_up_group_q1<HT, CT, GSRC, 1>(p, tile, sm, rb, t0, n);
+    // the gate_up groups of this mode hold <= PF_TOK1 pairs; workgroups are
+    // dealt to the XCDs as k_pf_gate_up's (all row blocks of a group on one)
+    const int RB = (p.n_ff + 63) / 64;
+    const int i = blockIdx.x, k = i >> 3;
+    const int g = 8 * (k / RB) + (i & 7), rb = k - (k / RB) * RB;
+    if (g >= *p.n_gtiles) return;
+    const PfTile tile = p.gtiles[g];
+    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK1) return;
+    const int n = tile.n;
+    if (n > 16) pf_gate_up_group_q1<HT, CT, GSRC, 2>(p, tile, sm, rb, n);
+    else pf_gate_up_group_q1<HT, CT, GSRC, 1>(p, tile, sm, rb, n);
 }
 
 // ------------------------------------------------------------------ down
@@ -1386,12 +1390,12 @@ void launch_pf(F k, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, cons
     else hipLaunchKernelGGL(k, grid, dim3(WG), 0, s, p);
 }
 template <int HT, int CT>
-void launch_gu(int gelu, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const PfParams & p) {
+void launch_gu(int gelu, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const PfParams & p) {
+    const dim3 g2(8 * ((p.max_gtiles + 7) / 8) * ((p.n_ff + 63) / 64));
     if (p.act_mode == AM_Q8_1) {
-        if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TANH>, grid, s, e0, e1, p);
-        else launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TABLE>, grid, s, e0, e1, p);
+        if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TANH>, g2, s, e0, e1, p);
+        else launch_pf(k_pf_gate_up_q1<HT, CT, SRC_GEGLU_TABLE>, g2, s, e0, e1, p);
     } else {
-        const dim3 g2(8 * ((p.max_gtiles + 7) / 8) * ((p.n_ff + 63) / 64));
         if (gelu == SRC_GEGLU_TANH) launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TANH>, g2, s, e0, e1, p);
         else launch_pf(k_pf_gate_up<HT, CT, SRC_GEGLU_TABLE>, g2, s, e0, e1, p);
     }
@@ -1404,8 +1408,8 @@ int gate_up_cap(int t) { return t == T_Q4_K ? G2_TOKQ4 : G2_TOKIQ2; }
 hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cdn, int gelu, hipStream_t s,
                           hipEvent_t * ev) {
     PfParams p = p0;
-    p.gcap[0] = p.act_mode == AM_Q8_1 ? PF_TOK : gate_up_cap(hgu);
-    p.gcap[1] = p.act_mode == AM_Q8_1 ? PF_TOK : gate_up_cap(cgu);
+    p.gcap[0] = p.act_mode == AM_Q8_1 ? PF_TOK1 : gate_up_cap(hgu);
+    p.gcap[1] = p.act_mode == AM_Q8_1 ? PF_TOK1 : gate_up_cap(cgu);
     hipEvent_t e[4] = {};
     if (ev)
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
@@ -1417,11 +1421,10 @@ hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cd
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     {
-        dim3 grid((p.n_ff + 63) / 64, p.max_tiles, p.act_mode == AM_Q8_1 ? PF_TOK / PF_TOK1 : 1);
-        if (hgu == T_Q4_K && cgu == T_IQ2_S) launch_gu<T_Q4_K, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);
-        else if (hgu == T_Q4_K && cgu == T_Q4_K) launch_gu<T_Q4_K, T_Q4_K>(gelu, grid, s, e[0], e[1], p);
-        else if (hgu == T_IQ2_S && cgu == T_IQ2_S) launch_gu<T_IQ2_S, T_IQ2_S>(gelu, grid, s, e[0], e[1], p);
-        else if (hgu == T_IQ2_S && cgu == T_Q4_K) launch_gu<T_IQ2_S, T_Q4_K>(gelu, grid, s, e[0], e[1], p);
+        if (hgu == T_Q4_K && cgu == T_IQ2_S) launch_gu<T_Q4_K, T_IQ2_S>(gelu, s, e[0], e[1], p);
+        else if (hgu == T_Q4_K && cgu == T_Q4_K) launch_gu<T_Q4_K, T_Q4_K>(gelu, s, e[0], e[1], p);
+        else if (hgu == T_IQ2_S && cgu == T_IQ2_S) launch_gu<T_IQ2_S, T_IQ2_S>(gelu, s, e[0], e[1], p);
+        else if (hgu == T_IQ2_S && cgu == T_Q4_K) launch_gu<T_IQ2_S, T_Q4_K>(gelu, s, e[0], e[1], p);
         else return hipErrorInvalidValue;
         err = hipGetLastError();
         if (err != hipSuccess) return err;
