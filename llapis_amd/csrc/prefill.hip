@@ -910,17 +910,17 @@ struct GuStageQ1 {
 // super-block; then d_w per super-block (Q4_K minus dmin times the mins MFMA,
 // IQ2_S d / 8 in the epilogue).  The epilogue quantises the down activations
 // to q8_1.
-template <int HT, int CT, int GSRC, int NT>
+template <int WT, int GSRC, int NT>
 __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const PfTile & tile, GuSmemQ1 & sm,
                                                     const int rb, const int n) {
     static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK1 * 64 == GU1_XREG * WG, "staging shape");
     constexpr int NTOK = 16 * NT;
-    const int wtype = tile.tier == 0 ? HT : CT;
-    const bool q4 = wtype == T_Q4_K;
+    constexpr bool q4 = WT == T_Q4_K;
+    static_assert(q4 || WT == T_IQ2_S, "gate_up formats");
     const int F = p.n_ff, D = p.d_model, NSB = D / 256, K = p.top_k;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
-    const int bb = q4 ? 144 : 82;
-    const int nwc = q4 ? 9 : 6;
+    constexpr int bb = q4 ? 144 : 82;
+    constexpr int nwc = q4 ? 9 : 6;
     const uint64_t rbytes = (uint64_t)NSB * bb;
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
@@ -929,7 +929,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
         sm.pair[tid] = qp;
         sm.tok[tid] = qp / K;
     }
-    if (!q4) {
+    if constexpr (!q4) {
         // selectors from the level codes (one byte 0..2 per value)
         const uint2 * codes = reinterpret_cast<const uint2 *>(&c_iq2s_tab_pf);
         for (int i = tid; i < 1024; i += WG) {
@@ -1027,7 +1027,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
             wo[rs] = sm.poff[32 * wave + 16 * rs + l16];
-            if (q4) {
+            if constexpr (q4) {
                 const u32x4 hdr = *reinterpret_cast<const u32x4 *>(sm.w + wo[rs]);
                 dr[rs] = h2f(hdr.x & 0xFFFF);
                 mr[rs] = h2f(hdr.x >> 16);
@@ -1070,7 +1070,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
 #pragma unroll
             for (int rs = 0; rs < 2; ++rs) {
                 uint32_t hv[4];
-                if (q4) {
+                if constexpr (q4) {
                     const h2 spair = scp[rs][j >> 1];
                     const _Float16 scj = (j & 1) ? spair.y : spair.x;
                     const h2 sc2 = h2{scj, scj};
@@ -1114,7 +1114,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
         // ---- the super-block into y: d_w (Q4_K: minus dmin times the mins MFMA)
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) {
-            if (q4) {
+            if constexpr (q4) {
                 h8 am;
                 const u32x4 mv = q < 2 ? *reinterpret_cast<const u32x4 *>(sm.mb + 16 * (16 * ts + l16) + 8 * q)
                                        : u32x4{0, 0, 0, 0};
@@ -1162,7 +1162,6 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
     }
 }
 
-// grid (row blocks, groups, 2): z takes the group's tokens 32 z .. 32 z + 31
 template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up_q1(const PfParams p) {
     __shared__ __align__(16) GuSmemQ1 sm;
@@ -1175,8 +1174,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const PfTile tile = p.gtiles[g];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK1) return;
     const int n = tile.n;
-    if (n > 16) pf_gate_up_group_q1<HT, CT, GSRC, 2>(p, tile, sm, rb, n);
-    else pf_gate_up_group_q1<HT, CT, GSRC, 1>(p, tile, sm, rb, n);
+    if ((tile.tier == 0 ? HT : CT) == T_Q4_K) {
+        if (n > 16) pf_gate_up_group_q1<T_Q4_K, GSRC, 2>(p, tile, sm, rb, n);
+        else pf_gate_up_group_q1<T_Q4_K, GSRC, 1>(p, tile, sm, rb, n);
+    } else {
+        if (n > 16) pf_gate_up_group_q1<T_IQ2_S, GSRC, 2>(p, tile, sm, rb, n);
+        else pf_gate_up_group_q1<T_IQ2_S, GSRC, 1>(p, tile, sm, rb, n);
+    }
 }
 
 // ------------------------------------------------------------------ down
