@@ -111,10 +111,10 @@ class Workload:
 
 class IslandWorkload(Workload):
     """The same replicas driven through the reference's operator boundary:
-    llapis_router_topk, the gate_up fire of the dual op (moert_ffn_moe:
-    partition, gather, hot and cold mul_mat_id, scatter), GEGLU, the down
-    fire, and the weighted sum over top_k (ggml's mul + adds, here one fp32
-    torch bmm) -- the per-fire island a relinked ggml graph runs."""
+    llapis_router_topk, the gate_up fire of the dual op (one kernel, or
+    moert_ffn_moe's partition, gather, hot and cold mul_mat_id, scatter),
+    GEGLU, the down fire, and the weighted sum over top_k (ggml's mul + adds:
+    llapis_moe_combine) -- the per-fire island a relinked ggml graph runs."""
 
     def step(self, i, stream):
         torch = self.torch
@@ -125,7 +125,9 @@ class IslandWorkload(Workload):
         gu = dl.moe_dual(0, x, ids)
         act = self.la.geglu(gu.reshape(-1, 2 * sp.n_ff), sp.n_ff, dl.gelu_mode)
         dn = dl.moe_dual(1, act, ids)
-        torch.bmm(w.unsqueeze(1), dn, out=self.out.view(self.T, 1, sp.d_model))
+        if self.la.lib().llapis_moe_combine(dn.data_ptr(), w.data_ptr(), self.T, sp.top_k, sp.d_model,
+                                            self.out.data_ptr(), stream) != 0:
+            raise RuntimeError(self.la.lib().llapis_last_error())
 
 
 def run_island(la, torch, name, host_layer, T, steps, warmup, dev, layer_res):

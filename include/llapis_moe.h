@@ -111,6 +111,13 @@ int32_t llapis_router_topk(const float * x, int32_t n_tokens, const float * w_r,
 int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float * out, int32_t gelu_mode,
                      void * stream);
 
+/* The weighted sum of each token's expert outputs (llama-graph.cpp:1812-1840:
+ * ggml_mul by the routing weights, then the top_k views added in order):
+ * out[t][r] = ((w[t][0] y[t K][r] + w[t][1] y[t K + 1][r]) + ...) for
+ * y [n_tokens * top_k][d] (the down fire's output), w [n_tokens][top_k]. */
+int32_t llapis_moe_combine(const float * y, const float * weights, int32_t n_tokens, int32_t top_k, int32_t d,
+                           float * out, void * stream);
+
 /* One dual-precision MoE FFN layer: build_moe_ffn's merged gate_up path for
  * gemma4-style MoE (llama-graph.cpp:1507-1850) with each routed pair computed
  * at its tier.  Pools are device slabs (see the note at the top):

@@ -504,6 +504,15 @@ int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float 
     return 0;
 }
 
+int32_t llapis_moe_combine(const float * y, const float * weights, int32_t n_tokens, int32_t top_k, int32_t d,
+                           float * out, void * stream) {
+    if (n_tokens <= 0 || d <= 0) return 0;
+    if (!y || !weights || !out) return fail("llapis_moe_combine: null pointer");
+    if (top_k < 1 || top_k > 64) return fail("llapis_moe_combine: need 1 <= top_k <= 64");
+    LL_TRY(launch_combine(y, weights, n_tokens, top_k, d, out, (hipStream_t)stream));
+    return 0;
+}
+
 // ------------------------------------------------------------ profiling
 
 namespace {

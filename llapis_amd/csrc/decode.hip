@@ -936,12 +936,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     }
     __syncthreads();
 
-    // 4. the combine (llama-graph.cpp:1812-1840): out = sum_k w_k y_k in k order
+    // 4. the combine (llama-graph.cpp:1812-1840): out = sum_k w_k y_k in k order,
+    // every product and sum rounded on its own (ggml_mul, then ggml_add)
     for (int i = threadIdx.x; i < (T << lg2r); i += WG) {
+#pragma clang fp contract(off)
         const int t = i >> lg2r, r = i & (R - 1);
         if (r >= nr) continue;
-        float o = __fmul_rn(s_y[t * K][r], s_wt[t * K]);
-        for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(s_y[t * K + k][r], s_wt[t * K + k]));
+        float o = s_y[t * K][r] * s_wt[t * K];
+        for (int k = 1; k < K; ++k) o = o + s_y[t * K + k][r] * s_wt[t * K + k];
         p.out[(int64_t)t * D + r0 + r] = o;
     }
 }
@@ -1058,10 +1060,15 @@ __global__ __launch_bounds__(WG) void k_dec_combine(const DecParams p) {
         yv[k] = k < K ? y[(int64_t)k * D] : 0.0f;
         wv[k] = k < K ? wk[k] : 0.0f;
     }
-    float o = __fmul_rn(yv[0], wv[0]);
+    // every product and sum rounded on its own (ggml_mul, then ggml_add)
+    float o;
+    {
+#pragma clang fp contract(off)
+        o = yv[0] * wv[0];
 #pragma unroll
-    for (int k = 1; k < DEC_KMAX; ++k)
-        if (k < K) o = __fadd_rn(o, __fmul_rn(yv[k], wv[k]));
+        for (int k = 1; k < DEC_KMAX; ++k)
+            if (k < K) o = o + yv[k] * wv[k];
+    }
     p.out[i] = o;
 }
 

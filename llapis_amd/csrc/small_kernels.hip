@@ -195,12 +195,31 @@ __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, 
 // ggml_mul by the weights, then the views added in order)
 __global__ __launch_bounds__(WG) void k_combine(const float * __restrict__ y, const float * __restrict__ w, int K, int D,
                                                 float * __restrict__ out) {
+#pragma clang fp contract(off)
     const int r = blockIdx.x * WG + threadIdx.x, t = blockIdx.y;
     if (r >= D) return;
+    // every product and sum rounded on its own (ggml_mul, then ggml_add):
+    // plain operators under the pragma (__fmul_rn / __fadd_rn are header
+    // functions whose operations the compiler may still fuse)
     const float * yp = y + (int64_t)t * K * D + r;
     const float * wt = w + (int64_t)t * K;
-    float o = __fmul_rn(yp[0], wt[0]);
-    for (int k = 1; k < K; ++k) o = __fadd_rn(o, __fmul_rn(yp[(int64_t)k * D], wt[k]));
+    float o;
+    if (K <= 16) {
+        // every load issued before the first use
+        float yv[16], wv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            yv[k] = k < K ? yp[(int64_t)k * D] : 0.0f;
+            wv[k] = k < K ? wt[k] : 0.0f;
+        }
+        o = yv[0] * wv[0];
+#pragma unroll
+        for (int k = 1; k < 16; ++k)
+            if (k < K) o = o + yv[k] * wv[k];
+    } else {
+        o = yp[0] * wt[0];
+        for (int k = 1; k < K; ++k) o = o + yp[(int64_t)k * D] * wt[k];
+    }
     out[(int64_t)t * D + r] = o;
 }
 

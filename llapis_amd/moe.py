@@ -400,6 +400,18 @@ class DeviceLayer:
         return ids, w, probs
 
 
+def combine(y, weights):
+    """out[t] = sum_k weights[t][k] y[t top_k + k] in k order (the graph's
+    weighted sum of the down fire's outputs), y [T * top_k][d]."""
+    torch = _torch()
+    T, K = weights.shape
+    d = y.shape[-1]
+    out = torch.empty(T, d, dtype=torch.float32, device=y.device)
+    s = torch.cuda.current_stream().cuda_stream
+    check(lib().llapis_moe_combine(y.data_ptr(), weights.data_ptr(), T, K, d, out.data_ptr(), s), "llapis_moe_combine")
+    return out
+
+
 def geglu(gate_up, n_ff, gelu_mode=L.GELU_TABLE):
     torch = _torch()
     n_cols = gate_up.numel() // (2 * n_ff)

@@ -147,6 +147,27 @@ def test_geglu_vs_oracle(gpu, oracle, mode):
         assert rel_l2(og, oo) <= 1e-5
 
 
+@pytest.mark.parametrize("K", [1, 8, 20])
+def test_combine_is_the_k_order_sum(gpu, K):
+    """llapis_moe_combine: out[t] = ((w0 y0 + w1 y1) + ...) in k order, each
+    product and sum rounded in fp32 (ggml's mul then the views added in
+    order), bit for bit; top_k above 16 takes the kernel's loop."""
+    torch = torch_mod()
+    say(f"combine K={K}")
+    T, D = 3, 2816 + 5
+    rng = np.random.default_rng(60 + K)
+    y = rng.standard_normal((T * K, D)).astype(np.float32)
+    w = rng.random((T, K)).astype(np.float32)
+    got = la.combine(torch.from_numpy(y).to(gpu), torch.from_numpy(w).to(gpu)).cpu().numpy()
+    want = np.empty((T, D), np.float32)
+    for t in range(T):
+        o = y[t * K] * w[t, 0]
+        for k in range(1, K):
+            o = (o + y[t * K + k] * w[t, k]).astype(np.float32)
+        want[t] = o
+    assert np.array_equal(got, want)
+
+
 def test_geglu_table_exhaustive(gpu, oracle):
     """Table mode depends on g only through fp16(g): every fp16 value of
     magnitude below 10 (and inputs just inside +-10, which round to fp16
