@@ -123,6 +123,29 @@ int32_t llapis_mul_mat_id(const moert_mm_call * c, int32_t w_type, const void * 
     if (eb % 16) return fail("llapis_mul_mat_id: expert slab is not a multiple of 16 bytes");
     if (c->n_ids <= 0) return 0;
     if (c->b_ncols != 1 && c->b_ncols != c->n_ids) return fail("llapis_mul_mat_id: b_ncols must be 1 or n_ids");
+    // the fire kernels where the format and size allow (one workgroup per
+    // (rows, channel), the channel's column quantised in LDS, every load of a
+    // round issued together); a per-expert pointer table takes the generic one
+    const bool k256 = (w_type == T_Q4_K || w_type == T_IQ2_S) && d_in % 256 == 0 && d_in <= 3072;
+    const bool k32 = (w_type == T_Q5_0 || w_type == T_IQ4_NL) && d_in % 64 == 0 && d_in <= 1024;
+    if (g_fused_fire.load() && (k256 || k32) && !c->w_ptrs && w_n <= INT32_MAX && c->n_ids <= INT32_MAX) {
+        FireParams f = {};
+        f.kind = k256 ? 0 : 1;
+        f.d_in = d_in; f.d_out = d_out; f.n_used = 1; f.n_tokens = (int)c->n_ids; f.ids_s1 = 1;
+        f.n_expert = (int)w_n; f.k_slots = 0;
+        f.cur = static_cast<const float *>(c->b);
+        f.cur_shared = c->b_ncols == 1;
+        f.ids = static_cast<const int32_t *>(c->ids);
+        f.hot = f.cold = static_cast<const uint8_t *>(w_base);
+        f.hot_stride = f.cold_stride = eb;
+        f.dst = static_cast<float *>(c->y);
+        f.n_live = c->ne_live;
+        f.w_lds = dev::align16(16 * (int)rb + 32);
+        if (fire_lds(f, w_type, w_type) + 16 * 1024 <= max_lds_per_wg()) {
+            LL_TRY(launch_fire(f, w_type, w_type, g_act_mode.load(), (hipStream_t)stream));
+            return 0;
+        }
+    }
     MmvParams p = {};
     p.mode = MMV_COMPACT;
     p.d_in = d_in;

@@ -1182,10 +1182,11 @@ __global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
     constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
     __shared__ int32_t s_m[3][256];
     const int p = blockIdx.y, d_in = f.d_in, r0 = blockIdx.x * FIRE_GU_ROWS;
+    if (f.n_live && p >= *f.n_live) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = p / f.n_used;
     // 1. the column's values and the codebook (no dependence on the routing)
-    const float * x = f.cur + (int64_t)t * d_in;
+    const float * x = f.cur + (f.cur_shared ? 0 : (int64_t)t * d_in);
     float xv[FIRE_XV];
 #pragma unroll
     for (int i = 0; i < FIRE_XV; ++i) {
@@ -1257,9 +1258,10 @@ __global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
     __shared__ int32_t s_m[3][256];
     constexpr int NPS = 2, R = NPS * DN_RPP;
     const int p = blockIdx.y, F = f.d_in, D = f.d_out, r0 = blockIdx.x * R, nr = max(0, min(R, D - r0));
+    if (f.n_live && p >= *f.n_live) return;
     const int F4 = F / 4, NP = F / 64;
     // 1. the pair's column (fp32), then its tier
-    const u32x4 a4 = reinterpret_cast<const u32x4 *>(f.cur + (int64_t)p * F)[min((int)threadIdx.x, F4 - 1)];
+    const u32x4 a4 = reinterpret_cast<const u32x4 *>(f.cur + (f.cur_shared ? 0 : (int64_t)p * F))[min((int)threadIdx.x, F4 - 1)];
     int e;
     const FireRes rs = fire_resolve(f, p, s_m, &e);
     if (f.kind == 0) fire_count(f, e, rs);

@@ -115,6 +115,8 @@ struct FireParams {
     int32_t * rc_counts;        // routing counters of a gate_up fire, or NULL
     int32_t * rc_hits;
     int w_lds;                  // LDS bytes of 16 staged rows (256-value block formats)
+    int cur_shared;             // 1: every pair reads cur's first column (mul_mat_id with one shared column)
+    const int32_t * n_live;     // device count of the pairs to compute (the rest are left untouched), or NULL
 };
 int fire_lds(const FireParams & f, int ht, int ct);
 hipError_t launch_fire(const FireParams & f, int ht, int ct, int act_mode, hipStream_t s);

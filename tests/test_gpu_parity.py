@@ -43,11 +43,16 @@ MM_CASES = [(la.Q4_K, 2816, 40), (la.IQ2_S, 2816, 40), (la.Q5_0, 704, 72), (la.I
             (la.Q4_K, 512, 33), (la.IQ2_S, 768, 24), (la.Q5_0, 96, 40), (la.IQ4_NL, 96, 40)]
 
 
+@pytest.mark.parametrize("fused", [1, 0])
 @pytest.mark.parametrize("wtype,d_in,d_out", MM_CASES)
 @pytest.mark.parametrize("act_mode", [la.ACT_CPU, la.ACT_Q8_1])
-def test_mul_mat_id_vs_oracle(gpu, oracle, wtype, d_in, d_out, act_mode):
+def test_mul_mat_id_vs_oracle(gpu, oracle, wtype, d_in, d_out, act_mode, fused):
+    """llapis_mul_mat_id against the oracle's matvecs, channels past ne_live
+    untouched: through the fire kernels where the format and size allow
+    (fused 1) and through the generic matvec (fused 0, tuning key 6)."""
     torch = torch_mod()
-    say(f"mul_mat_id type={wtype} d_in={d_in} d_out={d_out} act={act_mode}")
+    say(f"mul_mat_id type={wtype} d_in={d_in} d_out={d_out} act={act_mode} fused={fused}")
+    la.lib().llapis_set_tuning(6, fused)
     n_pool, n_ids = 5, 6
     rs = la.row_size(wtype, d_in)
     w = np.concatenate([la.quantize(wtype, la.synth_normal(100 + e, d_out * d_in, 0, 0.02).reshape(d_out, d_in),
@@ -90,9 +95,11 @@ def test_mul_mat_id_refuses_unaligned_slab(gpu):
     assert rc != 0 and b"16 bytes" in la.lib().llapis_last_error()
 
 
-def test_mul_mat_id_shared_column(gpu, oracle):
+@pytest.mark.parametrize("fused", [1, 0])
+def test_mul_mat_id_shared_column(gpu, oracle, fused):
     torch = torch_mod()
-    say("mul_mat_id shared column")
+    say(f"mul_mat_id shared column fused={fused}")
+    la.lib().llapis_set_tuning(6, fused)
     d_in, d_out, n_pool = 2816, 48, 3
     w = np.concatenate([la.quantize(la.Q4_K, la.synth_normal(200 + e, d_out * d_in, 0, 0.02).reshape(d_out, d_in))
                         for e in range(n_pool)])
