@@ -1229,22 +1229,85 @@ __device__ __forceinline__ h8 down_frag(const uint8_t * sw, int b, int u, float 
 
 // One (group, 128-row block) of the down GEMM with NT 16-token tiles.  Wave
 // w owns rows 32 w .. 32 w + 31 as two 16-row MFMA tiles.  K (n_ff) runs in
-// chunks of two 32-blocks: the load unit copies the next chunk's activation
-// parts and weight rows into LDS while the current one is used (two buffers
-// of each, separately declared, one barrier per chunk).  A pair's chunk is
-// 16 slots of 16 bytes (slots 0..7 the high parts of its 64 values, 8..15
-// the low parts), slot s at s ^ (pair & 15): the 16 pairs of an MFMA
-// fragment read 16 distinct slots.  A row's chunk is the 16-byte aligned
-// window holding its two blocks (<= 59 bytes: four slots).
-constexpr int D2_WP = 64;                          // LDS bytes per weight row and chunk
+// chunks of two 32-blocks.  The load unit copies the next chunk's activation
+// parts into LDS while the current one is used (two buffers, separately
+// declared, one barrier per chunk): a pair's chunk is 16 slots of 16 bytes
+// (slots 0..7 the high parts of its 64 values, 8..15 the low parts), slot s
+// at s ^ (pair & 15), so the 16 pairs of an MFMA fragment read 16 distinct
+// slots.  Each lane loads its rows' chunk (44 bytes of Q5_0, 36 of IQ4_NL)
+// straight into registers, the next chunk in flight during the current
+// one's MFMAs.
 constexpr int D2_XB = PF_TOK * 256;                // activations of one chunk: [pair slot][16][16 bytes]
-constexpr int D2_WB = PF_ROWS * D2_WP;
 
 struct Dn2Lds {
     uint8_t * x0; uint8_t * x1;
-    uint8_t * w0; uint8_t * w1;
     int * pair;
 };
+
+// One lane's row window of a two-block chunk: 44 bytes (Q5_0) or 36
+// (IQ4_NL), from the chunk's first byte.
+struct DnWin {
+    u32x4 a, b;
+    u32x3 e;
+};
+template <int I>
+__device__ __forceinline__ uint32_t win_dword(const DnWin & w) {
+    if constexpr (I < 4) return w.a[I];
+    else if constexpr (I < 8) return w.b[I - 4];
+    else return w.e[I - 8];
+}
+// the dword holding bytes BYTE .. BYTE + 3 of the window (BYTE even)
+template <int BYTE>
+__device__ __forceinline__ uint32_t win_at(const DnWin & w) {
+    if constexpr (BYTE & 3) return __builtin_amdgcn_alignbit(win_dword<(BYTE >> 2) + 1>(w), win_dword<(BYTE >> 2)>(w), 16);
+    else return win_dword<(BYTE >> 2)>(w);
+}
+
+// 8 values (8 u .. 8 u + 7 of block B of the chunk) as exact fp16 integers:
+// Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q] (:2653); the block
+// scale d_w out.  Block 1 starts 2 bytes into a dword of the window.
+template <int T, int B>
+__device__ __forceinline__ h8 down_frag_r(const DnWin & w, int u, float & d) {
+    constexpr int BS = T == T_Q5_0 ? 22 : 18;
+    constexpr int o0 = BS * B;                          // the block's first byte
+    d = h2f((o0 & 3) ? (win_dword<(o0 >> 2)>(w) >> 16) : (win_dword<(o0 >> 2)>(w) & 0xFFFFu));
+    const bool hiq = (u & 1) != 0;                      // bytes 8..15 of the qs
+    uint32_t h[4];
+    if constexpr (T == T_Q5_0) {
+        // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
+        const uint32_t qs0 = hiq ? win_at<o0 + 14>(w) : win_at<o0 + 6>(w);
+        const uint32_t qs1 = hiq ? win_at<o0 + 18>(w) : win_at<o0 + 10>(w);
+        const uint32_t qh = __builtin_amdgcn_ubfe(win_at<o0 + 2>(w), 8 * u, 8);
+        const int sh = 4 * (u >> 1);
+        uint32_t x[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t nib = ((i ? qs1 : qs0) >> sh) & 0x0F0F0F0Fu;
+            const uint32_t hb = (qh >> (4 * i)) & 15u;
+            x[i] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);   // bit k -> bit 4 of byte k
+        }
+        const h2 off = h2{(_Float16)(-1040.0f), (_Float16)(-1040.0f)};
+        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
+        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
+        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
+        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
+    } else {
+        const uint32_t qs0 = hiq ? win_at<o0 + 10>(w) : win_at<o0 + 2>(w);
+        const uint32_t qs1 = hiq ? win_at<o0 + 14>(w) : win_at<o0 + 6>(w);
+        const int sh = 4 * (u >> 1);
+        const h2 off = h2{(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
+        uint32_t x[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) x[i] = iq4nl_lookup(((i ? qs1 : qs0) >> sh) & 0x0F0F0F0Fu) ^ 0x80808080u;
+        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
+        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
+        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
+        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
+    }
+    h8 o;
+    __builtin_memcpy(&o, h, 16);
+    return o;
+}
 
 template <int WT, int NT>
 __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile & tile, const Dn2Lds & L,
@@ -1252,25 +1315,25 @@ __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile 
     static_assert(WT == T_Q5_0 || WT == T_IQ4_NL, "down formats");
     constexpr int NTOK = 16 * NT;
     constexpr int BS = WT == T_Q5_0 ? 22 : 18;
-    static_assert(2 * BS + 15 <= D2_WP, "a chunk's window fits its LDS row");
     const int D = p.d_model, F = p.n_ff, NB = F / 32, NC = (NB + 1) / 2;
     const int r0 = rb * PF_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     const uint32_t rbytes = (uint32_t)(NB * BS);
-    const uint32_t last16 = (uint32_t)D * rbytes - 16u;      // the slab's last 16-byte chunk
     const uint8_t * W = tile.tier == 0 ? p.hot_dn + (uint64_t)tile.idx * p.hot_dn_stride
                                        : p.cold_dn + (uint64_t)tile.idx * p.cold_dn_stride;
+    // the slab as a buffer: a last chunk of one block reads past its row
+    // (unused bytes; past the slab they read as zero)
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), 0,
+                                                                         (int)((uint32_t)D * rbytes), 0x00020000);
     if (tid < NTOK) L.pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
     __syncthreads();
 
-    auto copy_in = [&](int c, uint8_t * xb, uint8_t * wb) {
+    auto copy_in = [&](int c, uint8_t * xb) {
         const _Float16 * ah = p.ah;
         const _Float16 * al = p.al;
-        const uint8_t * w = W;
-        asm volatile("" : "+s"(ah), "+s"(al), "+s"(w));
-        // activations: wave w moves pair blocks w NT + k (four pair slots each);
-        // a last chunk of one block reads its second block's slots from inside
-        // the row (unused)
+        asm volatile("" : "+s"(ah), "+s"(al));
+        // wave w moves pair blocks w NT + k (four pair slots each); a last
+        // chunk of one block reads its second block's slots from inside the row
 #pragma unroll
         for (int k = 0; k < NT; ++k) {
             const int j = 4 * (wave * NT + k) + (lane >> 4);
@@ -1278,13 +1341,23 @@ __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile 
             const uint32_t off = (uint32_t)(L.pair[j] * F + min(64 * c + 8 * (sg & 7), F - 8));
             lds_dma16((sg < 8 ? ah : al) + off, xb + 1024 * (wave * NT + k));
         }
-        // weights: 128 rows x 4 slots; wave w moves slots 64 j .. + 63 for j = w, w + 4
+    };
+    uint32_t voff[2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int jj = wave + 4 * k, i = 64 * jj + lane, r = i >> 2, cc = i & 3;
-            const uint32_t ps = (uint32_t)min(r0 + r, D - 1) * rbytes + (uint32_t)(2 * BS * c);
-            const uint32_t off = min((ps & ~15u) + 16u * (uint32_t)cc, last16);    // slots past the slab: unused
-            lds_dma16(w + off, wb + 1024 * jj);
+    for (int rs = 0; rs < 2; ++rs) voff[rs] = (uint32_t)min(r0 + 32 * wave + 16 * rs + l16, D - 1) * rbytes;
+    // raw windows: from the dword at or below the chunk's start (a row of an
+    // odd block count starts 2 bytes into a dword), 48 bytes
+    u32x4 wr0[2], wr1[2], wr2[2];
+    uint32_t wsh[2];
+    auto load_rows = [&](int c) {
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) {
+            const uint32_t st = voff[rs] + (uint32_t)(2 * BS * c);
+            const uint32_t v0 = st & ~3u;
+            wsh[rs] = 8u * (st & 3u);
+            wr0[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0, 0, 0);
+            wr1[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0 + 16, 0, 0);
+            wr2[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0 + 32, 0, 0);
         }
     };
 
@@ -1293,31 +1366,42 @@ __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile 
     for (int rs = 0; rs < 2; ++rs)
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    int rowc[2];
-#pragma unroll
-    for (int rs = 0; rs < 2; ++rs) rowc[rs] = min(r0 + 32 * wave + 16 * rs + l16, D - 1);
 
-    auto step = [&](int c, const uint8_t * xb, const uint8_t * wb, uint8_t * xn, uint8_t * wn) {
+    auto step = [&](int c, const uint8_t * xb, uint8_t * xn) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (c + 1 < NC) copy_in(c + 1, xn, wn);
-        const int cb = min(2, NB - 2 * c);
-        int base[2];
+        // this chunk's rows out of the registers the loads land in, the next
+        // chunk's copies and loads in flight during the MFMAs
+        DnWin wc[2];
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs)
-            base[rs] = (32 * wave + 16 * rs + l16) * D2_WP + (int)(((uint32_t)rowc[rs] * rbytes + 2u * BS * c) & 15u);
-        for (int b = 0; b < cb; ++b) {
-            // B: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block b
+        for (int rs = 0; rs < 2; ++rs) {
+            const uint32_t r[12] = {wr0[rs].x, wr0[rs].y, wr0[rs].z, wr0[rs].w, wr1[rs].x, wr1[rs].y,
+                                    wr1[rs].z, wr1[rs].w, wr2[rs].x, wr2[rs].y, wr2[rs].z, wr2[rs].w};
+            uint32_t t[11];
+#pragma unroll
+            for (int i = 0; i < 11; ++i) t[i] = __builtin_amdgcn_alignbit(r[i + 1], r[i], wsh[rs]);
+            wc[rs].a = u32x4{t[0], t[1], t[2], t[3]};
+            wc[rs].b = u32x4{t[4], t[5], t[6], t[7]};
+            wc[rs].e = u32x3{t[8], t[9], t[10]};
+        }
+        if (c + 1 < NC) {
+            copy_in(c + 1, xn);
+            load_rows(c + 1);
+        }
+        const int cb = min(2, NB - 2 * c);
+        auto block = [&](auto bc) {
+            constexpr int B = decltype(bc)::value;
+            // B operand: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block B
             h8 bw[2];
             float dw[2];
 #pragma unroll
-            for (int rs = 0; rs < 2; ++rs) bw[rs] = down_frag<WT>(wb, base[rs] + BS * b, q, dw[rs]);
+            for (int rs = 0; rs < 2; ++rs) bw[rs] = down_frag_r<WT, B>(wc[rs], q, dw[rs]);
 #pragma unroll
             for (int ts = 0; ts < NT; ++ts) {
                 const uint8_t * xr = xb + (16 * ts + l16) * 256;
                 h8 ah, al;
-                __builtin_memcpy(&ah, xr + 16 * ((4 * b + q) ^ l16), 16);
-                __builtin_memcpy(&al, xr + 16 * ((8 + 4 * b + q) ^ l16), 16);
+                __builtin_memcpy(&ah, xr + 16 * ((4 * B + q) ^ l16), 16);
+                __builtin_memcpy(&al, xr + 16 * ((8 + 4 * B + q) ^ l16), 16);
 #pragma unroll
                 for (int rs = 0; rs < 2; ++rs) {
                     const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
@@ -1325,13 +1409,16 @@ __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile 
                     for (int r = 0; r < 4; ++r) y[rs][ts][r] = __builtin_fmaf(dw[rs], sb[r], y[rs][ts][r]);
                 }
             }
-        }
+        };
+        block(std::integral_constant<int, 0>{});
+        if (cb > 1) block(std::integral_constant<int, 1>{});
     };
 
-    copy_in(0, L.x0, L.w0);
+    copy_in(0, L.x0);
+    load_rows(0);
     for (int c = 0; c < NC; c += 2) {
-        step(c, L.x0, L.w0, L.x1, L.w1);
-        if (c + 1 < NC) step(c + 1, L.x1, L.w1, L.x0, L.w0);
+        step(c, L.x0, L.x1);
+        if (c + 1 < NC) step(c + 1, L.x1, L.x0);
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
@@ -1356,10 +1443,8 @@ template <int HT, int CT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_pf_down(const PfParams p) {
     __shared__ __align__(16) uint8_t x0[D2_XB];
     __shared__ __align__(16) uint8_t x1[D2_XB];
-    __shared__ __align__(16) uint8_t w0[D2_WB];
-    __shared__ __align__(16) uint8_t w1[D2_WB];
     __shared__ int pair[PF_TOK];
-    const Dn2Lds sm = {x0, x1, w0, w1, pair};
+    const Dn2Lds sm = {x0, x1, pair};
     const int RB = (p.d_model + PF_ROWS - 1) / PF_ROWS;
     const int i = blockIdx.x, k = i >> 3;
     const int g = 8 * (k / RB) + (i & 7), rb = k - (k / RB) * RB;
