@@ -124,7 +124,7 @@ hipError_t launch_fire(const FireParams & f, int ht, int ct, int act_mode, hipSt
 // ------------------------------------------------------------ prefill path
 
 constexpr int PF_ROWS = 128;          // weight rows per workgroup (4 waves x 32)
-constexpr int PF_TOK = 64;            // routed pairs per group (four 16-token MFMA tiles)
+constexpr int PF_TOK = 96;            // routed pairs per down group (six 16-token MFMA tiles)
 constexpr int PF_GTOK = 128;          // routed pairs per gate_up group, at most
 constexpr int PF_MAX_PAIRS = 4096;    // routed pairs per prefill launch (T * top_k)
 constexpr int PF_MAX_FF = 4096;       // longest n_ff the down activation kernel stages

@@ -2,8 +2,10 @@
 // gfx950 int8 matrix cores (v_mfma_i32_16x16x64_i8).
 //
 //   k_pf_bucket    routed pairs grouped by expert (a counting sort with LDS
-//                  atomics) and cut into groups of <= PF_TOK pairs, each tagged
-//                  with its tier by the residency predicate (ggml-cuda/mmid.cu:
+//                  atomics) and cut into groups two ways over the same sorted
+//                  list: down groups of <= PF_TOK pairs and gate_up groups
+//                  (their sizes set per tier by the host), each tagged with
+//                  its tier by the residency predicate (ggml-cuda/mmid.cu:
 //                  28-116 groups the same way; moert/cuda/ffn_moe.cu:80-130 is
 //                  the predicate).
 //   k_pf_quant_x   each token quantised once to q8_K (the CPU path's
@@ -1452,16 +1454,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     const PfTile tile = p.tiles[g];
     if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK) return;
     const int nt = (tile.n + 15) >> 4;
+    static_assert(PF_TOK == 96, "six tile counts");
     if ((tile.tier == 0 ? HT : CT) == T_Q5_0) {
-        if (nt == 1) pf_down2_group<T_Q5_0, 1>(p, tile, sm, rb);
-        else if (nt == 2) pf_down2_group<T_Q5_0, 2>(p, tile, sm, rb);
-        else if (nt == 3) pf_down2_group<T_Q5_0, 3>(p, tile, sm, rb);
-        else pf_down2_group<T_Q5_0, 4>(p, tile, sm, rb);
+        switch (nt) {
+        case 1: pf_down2_group<T_Q5_0, 1>(p, tile, sm, rb); break;
+        case 2: pf_down2_group<T_Q5_0, 2>(p, tile, sm, rb); break;
+        case 3: pf_down2_group<T_Q5_0, 3>(p, tile, sm, rb); break;
+        case 4: pf_down2_group<T_Q5_0, 4>(p, tile, sm, rb); break;
+        case 5: pf_down2_group<T_Q5_0, 5>(p, tile, sm, rb); break;
+        default: pf_down2_group<T_Q5_0, 6>(p, tile, sm, rb); break;
+        }
     } else {
-        if (nt == 1) pf_down2_group<T_IQ4_NL, 1>(p, tile, sm, rb);
-        else if (nt == 2) pf_down2_group<T_IQ4_NL, 2>(p, tile, sm, rb);
-        else if (nt == 3) pf_down2_group<T_IQ4_NL, 3>(p, tile, sm, rb);
-        else pf_down2_group<T_IQ4_NL, 4>(p, tile, sm, rb);
+        switch (nt) {
+        case 1: pf_down2_group<T_IQ4_NL, 1>(p, tile, sm, rb); break;
+        case 2: pf_down2_group<T_IQ4_NL, 2>(p, tile, sm, rb); break;
+        case 3: pf_down2_group<T_IQ4_NL, 3>(p, tile, sm, rb); break;
+        case 4: pf_down2_group<T_IQ4_NL, 4>(p, tile, sm, rb); break;
+        case 5: pf_down2_group<T_IQ4_NL, 5>(p, tile, sm, rb); break;
+        default: pf_down2_group<T_IQ4_NL, 6>(p, tile, sm, rb); break;
+        }
     }
 }
 
