@@ -395,7 +395,9 @@ int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
  * two tokens on, key 6 = the one-kernel fires of llapis_moe_dual_compute
  * and of llapis_mul_mat_id (default 1; 0 runs every fire through the
  * island's generic pipeline and every mul_mat_id through the generic
- * matvec).  Other keys are ignored. */
+ * matvec), key 7 = the most workgroups of the decode path's gate_up kernel
+ * (> 0; 0 or -1, the default, as many as the device holds resident).
+ * Other keys are ignored. */
 void llapis_set_tuning(int32_t key, int32_t value);
 
 /* Stage timing of llapis_moe_ffn for measurement (not under stream capture):

@@ -46,7 +46,7 @@ int32_t fail(const std::string & msg) {
         if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1}, g_fused_fire{1};
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1}, g_fused_fire{1}, g_gu_wgs{-1};
 
 // the largest LDS allocation of one workgroup on the current device (cached)
 int max_lds_per_wg() {
@@ -703,6 +703,7 @@ void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 3) g_dn_rows_log2 = value >= 0 && value <= 5 ? value : -1;
     if (key == 4) g_dn_by_group = value == 0 || value == 1 ? value : -1;
     if (key == 6) g_fused_fire = value != 0;
+    if (key == 7) g_gu_wgs = value > 0 ? value : -1;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
@@ -765,6 +766,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         // the down kernel by group from two tokens on (one token: 0.4 us
         // faster over every group, without the combine kernel)
         p.dn_by_group = g_dn_by_group.load() >= 0 ? g_dn_by_group.load() : (T > 1 ? 1 : 0);
+        p.gu_wgs_max = g_gu_wgs.load();
         p.out = out;
         const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
         p.w_lds_gu = dev::align16(8 * rbg + 32);

@@ -1389,7 +1389,8 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         const int lds = dec_lds_gate_up(p, hgu, cgu);
         auto go = [&](auto k) {
             const int cap = resident_wgs(k, lds, WG);
-            const int grid = std::max(1, cap > 0 ? std::min(items, cap) : items);
+            int grid = std::max(1, cap > 0 ? std::min(items, cap) : items);
+            if (p.gu_wgs_max > 0) grid = std::min(grid, p.gu_wgs_max);
             launch_timed(k, dim3(grid), lds, s, e[2], e[3], p);
         };
 #define LL_GU(A, B, M, G) \

@@ -83,6 +83,7 @@ struct DecParams {
     float * ya;                 // [P][n_ff] down activations (GEGLU outputs) per routed pair
     float * ydn;                // [P][d_model] scaled down rows per routed pair (down by group)
     int dn_by_group;            // 1: the down kernel by group + k_dec_combine, 0: the down kernel over every group
+    int gu_wgs_max;             // > 0: at most this many gate_up workgroups (else as many as are resident)
     float * out;                // [T][d_model]
     int w_lds_gu;               // LDS bytes of one half of a gate_up item (8 rows)
     int dn_rows_log2;           // log2 of the output rows per down workgroup (<= DEC_DN_MAXR)
