@@ -88,7 +88,7 @@ class Workload:
 
     def step(self, i, stream):
         d = self.descs[i % self.R]
-        rc = self.fn(C.byref(d), self.x[i % self.n_tok].data_ptr(), self.T, self.out.data_ptr(), self.ids.data_ptr(),
+        rc = self.fn(C.byref(d), self.x[i % self.n_tok].data_ptr(), None, self.T, self.out.data_ptr(), self.ids.data_ptr(),
                      self.w.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream)
         if rc != 0:
             raise RuntimeError(self.la.lib().llapis_last_error().decode())
@@ -492,7 +492,7 @@ class Stack:
         n_hot = n_cold = 0
         for d, dl in zip(self.descs, self.layers):
             xl = torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6)
-            rc = self.fn(C.byref(d), xl.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+            rc = self.fn(C.byref(d), xl.data_ptr(), None, T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
                          ws.data_ptr(), ws.numel(), stream)
             if rc != 0:
                 raise RuntimeError(self.la.lib().llapis_last_error().decode())
@@ -517,7 +517,7 @@ class Stack:
         for d in self.descs:
             xl = torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6)   # the layer's input, no extra copy
             if moe:
-                rc = self.fn(C.byref(d), xl.data_ptr(), T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                rc = self.fn(C.byref(d), xl.data_ptr(), None, T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
                              ws.data_ptr(), ws.numel(), stream)
                 if rc != 0:
                     raise RuntimeError(self.la.lib().llapis_last_error().decode())

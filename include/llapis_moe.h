@@ -153,14 +153,20 @@ typedef struct llapis_moe_layer {
 /* Device scratch the layer needs for n_tokens (bytes). */
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens);
 
-/* out [T][d_model] = the layer applied to x [T][d_model].  ids/weights
- * ([T][top_k], optional) receive the routing.  Batches of up to 4 tokens
- * take the three-kernel decode path.  Each call writes every workspace word
- * before it reads it, so nothing is carried from one call to the next (and
- * calls can be captured in HIP graphs); calls that share a workspace must not
- * run concurrently. */
-int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
-                       int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
+/* out [T][d_model] = the layer applied to x [T][d_model] (the experts'
+ * input), routed on x_router [T][d_model]: logits = W_r x_router (+ b).
+ * x_router NULL routes on x.  Gemma4's MoE block routes on a tensor of its
+ * own (gemma4.cpp:393-403: the experts read ffn_pre_norm_2(attn_out), the
+ * router rms_norm(attn_out) / sqrt(n_embd) * ffn_gate_inp_s, handed to
+ * build_moe_ffn as probs_in, llama-graph.cpp:1537-1541); pass that tensor
+ * as x_router and ffn_gate_inp as router_w.  ids/weights ([T][top_k],
+ * optional) receive the routing.  Batches of up to 4 tokens take the
+ * three-kernel decode path.  Each call writes every workspace word before it
+ * reads it, so nothing is carried from one call to the next (and calls can
+ * be captured in HIP graphs); calls that share a workspace must not run
+ * concurrently. */
+int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, const float * x_router, int32_t n_tokens,
+                       float * out, int32_t * ids, float * weights, void * workspace, uint64_t ws_bytes, void * stream);
 
 /* llapis_moe_ffn without a workspace argument.  No counterpart in the
  * reference: for callers that cannot allocate device memory (code under HIP
@@ -170,13 +176,15 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t n_to
  * allocated.  A call whose llapis_moe_ffn_workspace_size exceeds it is
  * refused (-1, llapis_last_error() says how much it needs): at the
  * benchmark's shapes (d_model 2816, n_ff 704, 128 experts, top-8) that
- * admits batches of up to 61 tokens.  The first call on a device clears the array with a kernel on
- * its stream.  Every call on one GPU shares that GPU's array and leaves its
- * contents behind: calls that overlap on one GPU (other streams, other
- * threads) race, so order them as one stream would. */
+ * admits batches of up to 61 tokens.  Nothing is launched to prepare the
+ * array: every call writes each scratch word before it reads it, so the first
+ * call may itself be captured in a HIP graph.  Every call on one GPU shares
+ * that GPU's array and leaves its contents behind: calls that overlap on one
+ * GPU (other streams, other threads) race, so order them as one stream
+ * would. */
 #define LLAPIS_NOALLOC_SCRATCH_BYTES (8u << 20)
-int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int32_t n_tokens, float * out,
-                               int32_t * ids, float * weights, void * stream);
+int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, const float * x_router,
+                               int32_t n_tokens, float * out, int32_t * ids, float * weights, void * stream);
 
 /* Zero the control block at the start of a workspace (a kernel on
  * `stream`).  Optional: no call reads a workspace word it has not written. */

@@ -722,10 +722,11 @@ int32_t llapis_moe_ffn_workspace_init(const llapis_moe_layer * L, void * workspa
     return 0;
 }
 
-int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
-                       float * w_out, void * workspace, uint64_t ws_bytes, void * stream) {
+int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, const float * x_router, int32_t T, float * out,
+                       int32_t * ids_out, float * w_out, void * workspace, uint64_t ws_bytes, void * stream) {
     if (!L) return fail("llapis_moe_ffn: null layer");
     if (T <= 0) return 0;
+    const float * xr = x_router ? x_router : x;     // the router's input (gemma4.cpp:400-403)
     if (!is_gu_type(L->hot_gu_type) || !is_gu_type(L->cold_gu_type) || !is_dn_type(L->hot_dn_type) ||
         !is_dn_type(L->cold_dn_type))
         return fail("llapis_moe_ffn: gate_up pools must be Q4_K/IQ2_S and down pools Q5_0/IQ4_NL");
@@ -747,7 +748,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
         DecParams p = {};
         p.d_model = L->d_model; p.n_ff = L->n_ff; p.n_expert = L->n_expert; p.top_k = L->top_k;
         p.k_slots = L->k_slots; p.T = T;
-        p.x = x; p.router_w = L->router_w; p.router_b = L->router_b;
+        p.x = x; p.xr = xr; p.router_w = L->router_w; p.router_b = L->router_b;
         p.hot_gu = static_cast<const uint8_t *>(L->hot_gu); p.hot_gu_stride = gu_hot;
         p.cold_gu = static_cast<const uint8_t *>(L->cold_gu); p.cold_gu_stride = gu_cold;
         p.hot_dn = static_cast<const uint8_t *>(L->hot_dn); p.hot_dn_stride = dn_hot;
@@ -802,10 +803,11 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
             int32_t * ids = ids_out ? ids_out + (int64_t)t0 * K : (int32_t *)(base + pw.ids);
             float * w = w_out ? w_out + (int64_t)t0 * K : (float *)(base + pw.w);
             const float * xc = x + (int64_t)t0 * L->d_model;
+            const float * xrc = xr + (int64_t)t0 * L->d_model;
             const int pc = prof_slot();
             float * parts = (float *)(base + pw.parts);
             LL_TRY(prof_record(pc, 0, 0, s));
-            LL_TRY(launch_router_mfma(xc, Tc, L->router_w, L->d_model, L->n_expert, parts, s));
+            LL_TRY(launch_router_mfma(xrc, Tc, L->router_w, L->d_model, L->n_expert, parts, s));
             LL_TRY(prof_record(pc, 0, 1, s));
             LL_TRY(prof_record(pc, 1, 0, s));
             LL_TRY(launch_topk_parts(parts, L->router_b, Tc, L->n_expert, K, probs, ids, w, s));
@@ -857,7 +859,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, int32_t T, f
 
     const int pc = prof_slot();        // profiling slot of this call
     LL_TRY(prof_record(pc, 0, 0, s));
-    LL_TRY(launch_router_logits(x, T, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
+    LL_TRY(launch_router_logits(xr, T, L->router_w, L->router_b, L->d_model, L->n_expert, probs, s));
     LL_TRY(prof_record(pc, 0, 1, s));
     LL_TRY(prof_record(pc, 1, 0, s));
     LL_TRY(launch_topk(probs, T, L->n_expert, L->top_k, ids, w, s));
@@ -928,9 +930,11 @@ static __device__ __align__(256) uint8_t scratch[LLAPIS_NOALLOC_SCRATCH_BYTES];
 std::mutex g_na_mu;
 std::map<int, uint8_t *> g_na_ptr;     // device -> address of that device's scratch
 
-// The current device's scratch address: looked up (and the array zeroed on
-// `s`) at the first call on each device.
-int32_t noalloc_scratch(uint8_t ** out, hipStream_t s) {
+// The current device's scratch address, looked up at the first call on each
+// device.  Nothing is launched: every path of llapis_moe_ffn writes each
+// scratch word before it reads it, so the array needs no clearing (and a
+// first call made under stream capture records no extra node).
+int32_t noalloc_scratch(uint8_t ** out) {
     int dev = 0;
     LL_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_na_mu);
@@ -942,9 +946,6 @@ int32_t noalloc_scratch(uint8_t ** out, hipStream_t s) {
     void * p = nullptr;
     LL_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     if (!p) return fail("llapis_moe_ffn_noalloc: no device address for the scratch array");
-    // the decode path's control block must start at zero: clear the whole
-    // array once, with a kernel (no memset node if the caller is capturing)
-    LL_TRY(launch_zero_i32(static_cast<int *>(p), (int)(LLAPIS_NOALLOC_SCRATCH_BYTES / 4), s));
     g_na_ptr[dev] = static_cast<uint8_t *>(p);
     *out = static_cast<uint8_t *>(p);
     return 0;
@@ -953,8 +954,8 @@ int32_t noalloc_scratch(uint8_t ** out, hipStream_t s) {
 
 extern "C" {
 
-int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int32_t T, float * out, int32_t * ids_out,
-                               float * w_out, void * stream) {
+int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, const float * x_router, int32_t T,
+                               float * out, int32_t * ids_out, float * w_out, void * stream) {
     if (!L) return fail("llapis_moe_ffn_noalloc: null layer");
     if (T <= 0) return 0;
     const uint64_t need = llapis_moe_ffn_workspace_size(L, T);
@@ -963,8 +964,8 @@ int32_t llapis_moe_ffn_noalloc(const llapis_moe_layer * L, const float * x, int3
                     " bytes of scratch, more than the fixed " + std::to_string(LLAPIS_NOALLOC_SCRATCH_BYTES) +
                     " bytes; use llapis_moe_ffn with a workspace");
     uint8_t * ptr = nullptr;
-    if (const int32_t rc = noalloc_scratch(&ptr, (hipStream_t)stream)) return rc;
-    return llapis_moe_ffn(L, x, T, out, ids_out, w_out, ptr, LLAPIS_NOALLOC_SCRATCH_BYTES, stream);
+    if (const int32_t rc = noalloc_scratch(&ptr)) return rc;
+    return llapis_moe_ffn(L, x, x_router, T, out, ids_out, w_out, ptr, LLAPIS_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

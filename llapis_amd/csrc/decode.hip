@@ -71,14 +71,15 @@ __device__ __forceinline__ uint64_t lanes_below() {
 
 // ---------------------------------------------------------------- A
 
-// Router logits of expert e for every token (one workgroup).  Each lane
-// issues all of its row loads (RU float4 per pass) before any arithmetic.
+// Router logits of expert e for every token (one workgroup), from the
+// router's input p.xr.  Each lane issues all of its row loads (RU float4 per
+// pass) before any arithmetic.
 __device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 64]) {
     constexpr int RU = 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d_model, E = p.n_expert, T = p.T, n4 = d / 4;
     const float4 * wrow = reinterpret_cast<const float4 *>(p.router_w + (int64_t)e * d);
-    const float4 * x4 = reinterpret_cast<const float4 *>(p.x);
+    const float4 * x4 = reinterpret_cast<const float4 *>(p.xr);
     const float bias = p.router_b ? p.router_b[e] : 0.0f;     // issued with the row's loads
     float acc[DEC_MAXT];
 #pragma unroll
@@ -115,9 +116,10 @@ __device__ void router_expert(const DecParams & p, int e, float (*s_part)[WG / 6
     }
 }
 
-// Router logits of every token (workgroups e < E, one expert each) and the
-// tokens' gate_up activation quantisation (the workgroups after them: one
-// wave per q8_K 256-block, or per 64 values of q8_1).
+// Router logits of every token (workgroups e < E, one expert each, from the
+// router's input) and the quantisation of the experts' input for gate_up
+// (the workgroups after them: one wave per q8_K 256-block, or per 64 values
+// of q8_1).
 template <int AM>
 __global__ __launch_bounds__(WG) void k_dec_route(const DecParams p) {
     __shared__ float s_part[DEC_MAXT][WG / 64];

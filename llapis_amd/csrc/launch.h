@@ -66,7 +66,8 @@ struct DecCtl {
 
 struct DecParams {
     int d_model, n_ff, n_expert, top_k, k_slots, T;
-    const float * x;
+    const float * x;            // [T][d_model] the experts' input
+    const float * xr;           // [T][d_model] the router's input
     const float * router_w;
     const float * router_b;
     const uint8_t * hot_gu; uint64_t hot_gu_stride;

@@ -306,10 +306,13 @@ class DeviceLayer:
             self._ws = torch.zeros(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
-    def forward(self, x, out=None, ids=None, weights=None, stream=None):
-        """x: [T, d_model] f32 device tensor -> out [T, d_model] (+ ids, weights)."""
+    def forward(self, x, out=None, ids=None, weights=None, stream=None, x_router=None):
+        """x: [T, d_model] f32 device tensor (the experts' input) -> out [T, d_model]
+        (+ ids, weights).  x_router: the router's input, same shape (None: x)."""
         torch = _torch()
         T = x.shape[0]
+        if x_router is not None and (tuple(x_router.shape) != tuple(x.shape) or not x_router.is_contiguous()):
+            raise ValueError("x_router must be a contiguous tensor shaped like x")
         sp = self.layer.spec
         out = out if out is not None else torch.empty(T, sp.d_model, dtype=torch.float32, device=self.device)
         ids = ids if ids is not None else torch.empty(T, sp.top_k, dtype=torch.int32, device=self.device)
@@ -318,7 +321,8 @@ class DeviceLayer:
         ws = self.workspace(T)
         d = self.desc()
         s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
-        check(lib().llapis_moe_ffn(C.byref(d), x.data_ptr(), T, out.data_ptr(), ids.data_ptr(),
+        xr = x_router.data_ptr() if x_router is not None else None
+        check(lib().llapis_moe_ffn(C.byref(d), x.data_ptr(), xr, T, out.data_ptr(), ids.data_ptr(),
                                    weights.data_ptr(), ws.data_ptr(), ws.numel(), s), "llapis_moe_ffn")
         return out, ids, weights
 

@@ -231,7 +231,7 @@ def test_noalloc_refuses_before_any_device_call():
     """A null layer and a call larger than the fixed array are refused on the
     host, with no GPU in the process."""
     lib = _lib.lib()
-    assert lib.llapis_moe_ffn_noalloc(None, None, 1, None, None, None, None) != 0
+    assert lib.llapis_moe_ffn_noalloc(None, None, None, 1, None, None, None, None) != 0
     d = _lib.LlapisMoeLayer(2816, 704, 128, 8, 57, 12, 6, 22, 20, 0, 0, *([None] * 12))
-    assert lib.llapis_moe_ffn_noalloc(C.byref(d), None, 512, None, None, None, None) != 0
+    assert lib.llapis_moe_ffn_noalloc(C.byref(d), None, None, 512, None, None, None, None) != 0
     assert b"bytes of scratch" in lib.llapis_last_error()

@@ -166,3 +166,58 @@ def test_stack_slice_three_layers(gpu, oracle, T, act_mode, gelu_mode):
     # more of its own activations: its chain drifts about twice as far
     assert rel_l2(h_gpu[same], ho[same]) <= (3e-3 if act_mode == la.ACT_Q8_1 else 1e-3)
     assert per[same].max() <= 1e-2 and np.median(per[same]) <= 1e-5
+
+
+def _gemma4_inputs(seed, T):
+    """Gemma4's two MoE inputs from one residual stream h (gemma4.cpp:393-403):
+    the experts read ffn_pre_norm_2(h) = rms_norm(h) * s2, the router reads
+    rms_norm(h) / sqrt(n_embd) * ffn_gate_inp_s.  s2 and ffn_gate_inp_s are
+    seeded per-channel scales; ffn_gate_inp_s carries sqrt(n_embd) so the
+    logits keep the scale the router's bias was tuned for."""
+    d = FULL.d_model
+    h = tokens(seed, T, d)
+    r = _rms_norm_np(h)
+    rng = np.random.default_rng(seed)
+    s2 = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    s_inp = (np.float32(np.sqrt(d)) * rng.uniform(0.5, 1.5, d)).astype(np.float32)
+    x = (r * s2).astype(np.float32)
+    xr = ((r * np.float32(1.0 / np.sqrt(d))).astype(np.float32) * s_inp).astype(np.float32)
+    return x, xr
+
+
+@pytest.mark.parametrize("act_mode,gelu_mode", MODES)
+@pytest.mark.parametrize("T", [4, 512])
+def test_router_input_differs_from_expert_input(gpu, oracle, T, act_mode, gelu_mode):
+    """The fused layer routes on its own router input (x_router) and runs the
+    experts on x, as gemma4's MoE block does (gemma4.cpp:393-403, logits
+    handed to build_moe_ffn as probs_in, llama-graph.cpp:1537-1541): dual
+    K = 57 at 4 tokens (the decode path, token by token) and a 512-token
+    chunk (the prefill path).  The ids equal the oracle's router on x_router
+    (and differ from routing on x, so the second input is really used); the
+    outputs equal the oracle's experts on x with those ids, to the same bars
+    as the single-input workloads."""
+    import torch
+    say(f"workload router input != expert input T={T} act={act_mode}")
+    lay = dual_k57(full_layer(SEED), 7)
+    batches = 3 if T == 4 else 1
+    differ = 0
+    for b in range(batches):
+        x, xr = _gemma4_inputs(5100 + 10 * T + b, T)
+        dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
+        out, ids, w = dl.forward(torch.from_numpy(x).to(gpu), x_router=torch.from_numpy(xr).to(gpu))
+        torch.cuda.synchronize()
+        ids_g, w_g, out_g = ids.cpu().numpy(), w.cpu().numpy(), out.cpu().numpy()
+        ids_o, w_o, _ = oracle.router(xr, lay.router_w, lay.router_b, FULL.top_k)
+        assert np.array_equal(ids_g, ids_o), "routing differs from the oracle's router on x_router"
+        assert np.allclose(w_g, w_o, rtol=1e-5, atol=1e-7)
+        ids_x, _, _ = oracle.router(x, lay.router_w, lay.router_b, FULL.top_k)
+        differ += int((ids_x != ids_o).any(axis=1).sum())
+        out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, oracle_mode(act_mode, T), gelu_mode)
+        if T == 4:
+            per = per_token_rel_l2(out_g, out_o)
+            say(f"  batch {b}: tokens " + " ".join(f"{v:.1e}" for v in per))
+            assert per.max() <= 1e-3, (b, per)
+        else:
+            check_layer_bars(out_g, out_o, say, 0.02 if act_mode == la.ACT_Q8_1 else 0.01)
+    say(f"  {differ} of {batches * T} tokens would route differently on x")
+    assert differ >= max(1, batches * T // 4)
