@@ -396,16 +396,11 @@ int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
 /* Switches for measurement: key 0 = the decode path for <= 4 tokens
  * (default 1; 0 sends those calls down the generic path), key 2 = the MFMA
  * prefill path for > 4 tokens (default 1), key 3 = log2 of the output rows
- * per workgroup of the decode path's down kernel over every group (0..5;
- * -1, the default, picks it from d_model and the token count), key 4 = the
- * decode path's down kernel: 1 by expert group with a combine kernel after
- * it, 0 over every group with the combine in it, -1 (default) by group from
- * two tokens on, key 6 = the one-kernel fires of llapis_moe_dual_compute
- * and of llapis_mul_mat_id (default 1; 0 runs every fire through the
- * island's generic pipeline and every mul_mat_id through the generic
- * matvec), key 7 = the most workgroups of the decode path's gate_up kernel
- * (> 0; 0 or -1, the default, as many as the device holds resident).
- * Other keys are ignored. */
+ * per workgroup of the decode path's down kernel (0..5; -1, the default,
+ * picks it from d_model), key 6 = the one-kernel fires of
+ * llapis_moe_dual_compute and of llapis_mul_mat_id (default 1; 0 runs every
+ * fire through the island's generic pipeline and every mul_mat_id through
+ * the generic matvec).  Other keys are ignored. */
 void llapis_set_tuning(int32_t key, int32_t value);
 
 /* Stage timing of llapis_moe_ffn for measurement (not under stream capture):

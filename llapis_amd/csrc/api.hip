@@ -46,7 +46,7 @@ int32_t fail(const std::string & msg) {
         if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1}, g_fused_fire{1}, g_gu_wgs{-1};
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_fused_fire{1};
 
 // the largest LDS allocation of one workgroup on the current device (cached)
 int max_lds_per_wg() {
@@ -632,28 +632,29 @@ FfnWs ffn_ws(const llapis_moe_layer * L, int32_t T) {
 
 // decode path (T <= DEC_MAXT): control block first
 struct DecWs {
-    uint64_t ctl, logits, ids, w, xq, ya, ydn, total, ctl_bytes;
-    int64_t xq_stride;
+    uint64_t ctl, logits, ids, w, xq, yq, ydn, total, ctl_bytes;
+    int64_t xq_stride, yq_stride;
 };
 DecWs dec_ws(const llapis_moe_layer * L, int32_t T) {
     const uint64_t P = (uint64_t)T * L->top_k;
     DecWs w;
     w.xq_stride = dec_act_bytes(L->d_model);
+    w.yq_stride = dec_act_bytes(L->n_ff);
     w.ctl = 0;
     w.ctl_bytes = dec_ctl_bytes(L);
     w.logits = w.ctl_bytes;
     w.ids = w.logits + al256((uint64_t)T * L->n_expert * 4);
     w.w = w.ids + al256(P * 4);
     w.xq = w.w + al256(P * 4);
-    w.ya = w.xq + al256((uint64_t)T * w.xq_stride);
-    w.ydn = w.ya + al256(P * L->n_ff * 4);
-    w.total = w.ydn + al256(P * L->d_model * 4);
+    w.yq = w.xq + al256((uint64_t)T * w.xq_stride);
+    w.ydn = w.yq + al256(P * w.yq_stride);
+    w.total = w.ydn + (T > 1 ? al256(P * L->d_model * 4) : 0);
     return w;
 }
 
 bool decode_eligible(const llapis_moe_layer * L, int32_t T) {
-    // n_ff <= 1024: the down kernel quantises one 16-byte chunk of each pair's
-    // activation per lane, and 16 lanes hold a row as whole block pairs
+    // n_ff <= 1024 and a multiple of 64: 16 lanes hold a down row as whole
+    // block pairs, and gate_up items are whole 32-blocks
     return g_decode_path.load() && T <= DEC_MAXT && L->top_k <= 16 && L->n_expert <= 256 && L->k_slots <= 256 &&
            (L->d_model % 4) == 0 && L->n_ff <= 1024 && L->n_ff % 64 == 0;
 }
@@ -701,9 +702,7 @@ void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
     if (key == 2) g_prefill = value != 0;
     if (key == 3) g_dn_rows_log2 = value >= 0 && value <= 5 ? value : -1;
-    if (key == 4) g_dn_by_group = value == 0 || value == 1 ? value : -1;
     if (key == 6) g_fused_fire = value != 0;
-    if (key == 7) g_gu_wgs = value > 0 ? value : -1;
 }
 
 uint64_t llapis_moe_ffn_workspace_size(const llapis_moe_layer * L, int32_t n_tokens) {
@@ -762,31 +761,27 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, const float 
         p.ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + dw.ids);
         p.w = w_out ? w_out : reinterpret_cast<float *>(base + dw.w);
         p.xq = base + dw.xq; p.xq_stride = dw.xq_stride;
-        p.ya = reinterpret_cast<float *>(base + dw.ya);
+        p.yq = base + dw.yq; p.yq_stride = dw.yq_stride;
         p.ydn = reinterpret_cast<float *>(base + dw.ydn);
-        // the down kernel by group from two tokens on (one token: 0.4 us
-        // faster over every group, without the combine kernel)
-        p.dn_by_group = g_dn_by_group.load() >= 0 ? g_dn_by_group.load() : (T > 1 ? 1 : 0);
-        p.gu_wgs_max = g_gu_wgs.load();
         p.out = out;
         const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
-        p.w_lds_gu = dev::align16(8 * rbg + 32);
+        p.w_lds_gu = dec_gu_half_bytes(T, rbg);
         // the down rows: a power of two giving about three blocks per CU of
-        // the part (256 CUs on MI355X: 4 rows, 704 blocks at d_model 2816) for
-        // one token, four times that for more (each block re-reads every
-        // pair's activation)
+        // the part (256 CUs on MI355X: 4 rows, 704 blocks at d_model 2816)
         int lg2r = 0;
         while ((1 << lg2r) < DEC_DN_MAXR && (1 << lg2r) * 768 < L->d_model) ++lg2r;
-        if (T > 1) lg2r = std::min(lg2r + 2, 5);
         if (g_dn_rows_log2.load() >= 0) lg2r = g_dn_rows_log2.load();
         p.dn_rows_log2 = lg2r;
         const int lds_max = max_lds_per_wg();
-        if (dec_lds_down(p) + 16 * 1024 <= lds_max && dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) + 16 * 1024 <= lds_max) {
+        // the LDS of the down kernel that will run: every pair's column at one
+        // token, the group's members' columns by group
+        const int dn_lds = T == 1 ? dec_lds_down(p) : std::min(T, DEC_MAXT) * dec_act_bytes(L->n_ff);
+        if (dn_lds + 16 * 1024 <= lds_max && dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) + 16 * 1024 <= lds_max) {
             const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
             hipEvent_t ev[8] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0), prof_ev(pc, 2, 1),
                                 prof_ev(pc, 3, 0), prof_ev(pc, 3, 1),
-                                p.dn_by_group ? prof_ev(pc, 4, 0) : nullptr, p.dn_by_group ? prof_ev(pc, 4, 1) : nullptr};
+                                T > 1 ? prof_ev(pc, 4, 0) : nullptr, T > 1 ? prof_ev(pc, 4, 1) : nullptr};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
                                  src, s, pc >= 0 ? ev : nullptr));
             return 0;

@@ -5,28 +5,25 @@
 //                      and, in the workgroups after those, the tokens'
 //                      activation quantisation.
 //   B  k_dec_gate_up   every workgroup selects the routing from the logits
-//                      (softmax, top-k by a bisection for the k-th largest
-//                      probability, ties to the lower index), groups the
+//                      (softmax, then the top-k largest probabilities taken
+//                      one by one, ties to the lower index), groups the
 //                      routed pairs by expert (the tokens that share an expert
 //                      read its slab once) and resolves each group's tier (the
 //                      residency predicate of moert/cuda/ffn_moe.cu:80-130);
 //                      the first workgroup publishes ids, weights and groups.
-//                      Then its items: an item is one group's 8 gate rows and
-//                      the 8 up rows paired with them (rows i and n_ff + i),
-//                      one row per 16 lanes, the next item's loads in flight;
-//                      the rows are dotted against every member token and the
-//                      item ends with GEGLU of each gate/up pair, stored as
-//                      fp32 down activations.
-//   C  k_dec_down      one token: one workgroup per block of output rows over
-//                      every group; each row's lanes load its block pairs
-//                      straight into registers, dot them against the members'
-//                      down activations (quantised in LDS from B's fp32
-//                      outputs), scale by the expert's .scale and sum each
-//                      token's top_k outputs in k order (llama-graph.cpp:
-//                      1812-1840).
-//      k_dec_down_grp  2-4 tokens: one workgroup per (block of rows, group),
-//      k_dec_combine   the members' activations only, then a combine kernel
-//                      that sums each token's top_k rows in k order.
+//                      Then its item: one group's 32 gate rows and the 32 up
+//                      rows paired with them (rows i and n_ff + i), in four
+//                      passes of 8 + 8 rows, one row per 16 lanes, the next
+//                      passes' loads in flight; the rows are dotted against
+//                      every member token, GEGLU pairs them, and the item ends
+//                      with each member's 32 values quantised (q8_0 / q8_1):
+//                      one block of the pair's down activation, quantised once.
+//   C  k_dec_down      one workgroup per block of output rows over every
+//                      group; each row's lanes load its block pairs straight
+//                      into registers and dot them against the members'
+//                      quantised down columns (copied into LDS), scale by the
+//                      expert's .scale and sum each token's top_k outputs in k
+//                      order (llama-graph.cpp:1812-1840).
 //
 //   k_fire_k256 / k_fire_k32: one GGML_OP_MOE_DUAL fire (gate_up over the
 //   256-value block formats, down over the 32-value ones) as one kernel.
@@ -170,10 +167,9 @@ __device__ __forceinline__ int wave_max_i(int v) {
 
 constexpr int DEC_KMAX = 16;    // top_k of a decode call, at most
 
-// LDS scratch of one wave's selection
+// one wave's scratch for ordering its selected entries
 struct SelScratch {
     int key[DEC_KMAX], idx[DEC_KMAX];
-    int out_idx[DEC_KMAX], out_key[DEC_KMAX];
 };
 
 // Softmax + top-K of one token in one wave, from its logits in registers
@@ -181,12 +177,15 @@ struct SelScratch {
 // graph computes them (soft_max: exp(x - max), the sum in double,
 // probabilities scaled by float(1/sum); argsort_top_k: descending, equal
 // probabilities in index order; weights p / max(sum of the K in double, in
-// order, 6.103515625e-5)).  Probabilities are >= 0, so they are compared as
-// ints.  The K-th largest is found by bisection over its bits (the largest t
-// with at least K probabilities >= t, one ballot count per bit), the entries
-// above it and the lowest-indexed ones equal to it are compacted into LDS in
-// index order, and each of the K lanes ranks its entry against the others.
-// Nothing branches per lane.  ids and weights go to LDS when `wr`.
+// order, 6.103515625e-5)).  Probabilities are >= 0, so they compare as ints.
+// The K-th largest probability is found by bisection over its bits (the
+// largest t with at least K probabilities >= t: one ballot count per step),
+// stopping early once exactly K entries are >= t; the entries above it and
+// the lowest-indexed ones equal to it are taken, and each taken entry's rank
+// (larger first, then the lower index) counts the taken entries before it,
+// read from the lanes.  No cross-lane shuffles in the loops; one LDS round
+// trip orders the K entries.  ids and weights go to LDS when `wr`; entries
+// past the valid ones (K > E) get id -1 and weight 0.
 template <int NJ>
 __device__ __forceinline__ void select_topk(const float (&v)[4], int E, int K, int * s_ids, float * s_w, bool wr,
                                             SelScratch & sc) {
@@ -207,74 +206,101 @@ __device__ __forceinline__ void select_topk(const float (&v)[4], int E, int K, i
     int q[NJ];                  // probabilities as ints; -1: absent
 #pragma unroll
     for (int j = 0; j < NJ; ++j) q[j] = lane + 64 * j < E ? __float_as_int(__fmul_rn(ev[j], inv)) : -1;
-    // the K-th largest probability (they are at most 1.0f: bit 30 is clear)
-    int theta = 0;
-    for (int bit = 29; bit >= 0; --bit) {
-        const int c = theta | (1 << bit);
+    // the threshold (probabilities are at most 1.0f: below 0x40000000)
+    int nv = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) nv += __popcll(__ballot(q[j] >= 0));
+    const int kk = min(K, nv);
+    int lo = 0, hi = 0x40000000;
+    bool exact = nv == kk;              // every valid entry is taken
+    while (!exact && hi - lo > 1) {
+        const int c = lo + ((hi - lo) >> 1);
         int n = 0;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) n += __popcll(__ballot(q[j] >= c));
-        theta = n >= K ? c : theta;
-    }
-    int above = 0;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) above += __popcll(__ballot(q[j] > theta));
-    const int need = K - above;         // entries equal to theta taken, lowest index first
-    const uint64_t below = lanes_below();
-    int eq_before = 0, taken = 0;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const uint64_t eq = __ballot(q[j] == theta);
-        const bool sel = q[j] > theta || (q[j] == theta && eq_before + __popcll(eq & below) < need);
-        const uint64_t sm = __ballot(sel);
-        if (sel) {
-            const int pos = taken + __popcll(sm & below);
-            sc.key[pos] = q[j];
-            sc.idx[pos] = lane + 64 * j;
+        if (n >= kk) {
+            lo = c;
+            exact = n == kk;
+        } else {
+            hi = c;
         }
-        eq_before += __popcll(eq);
-        taken += __popcll(sm);
     }
-    taken = min(taken, K);
+    // the taken entries: those >= lo when exactly kk are; otherwise lo is the
+    // kk-th largest value: those above it, then the lowest-indexed equal ones
+    uint64_t sel[NJ];
+    if (exact) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) sel[j] = __ballot(q[j] >= lo);
+    } else {
+        int need = kk;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            sel[j] = __ballot(q[j] > lo);
+            need -= __popcll(sel[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            uint64_t eq = __ballot(q[j] == lo);
+            while (need > 0 && eq) {
+                const uint64_t b = eq & (~eq + 1);
+                sel[j] |= b;
+                eq ^= b;
+                --need;
+            }
+        }
+    }
+    // ranks of this lane's taken entries
+    int rank[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) rank[j] = 0;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+        uint64_t m = sel[jj];
+        while (m) {
+            const int l = (int)__builtin_ctzll(m);
+            m &= m - 1;
+            const int kq = __builtin_amdgcn_readlane(q[jj], l), ki = l + 64 * jj;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                rank[j] += (kq > q[j] || (kq == q[j] && ki < lane + 64 * j)) ? 1 : 0;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        if ((sel[j] >> lane) & 1) {
+            sc.key[rank[j]] = q[j];
+            sc.idx[rank[j]] = lane + 64 * j;
+        }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // the rank of entry `lane` among the taken ones: larger first, then the
-    // lower index (the entries are in index order)
     const int mine = min(lane, DEC_KMAX - 1);
-    const int kk = lane < taken ? sc.key[mine] : -1, ki = lane < taken ? sc.idx[mine] : -1;
-    int rank = 0;
-    for (int m = 0; m < taken; ++m) {
-        const int km = sc.key[m];
-        rank += (km > kk || (km == kk && m < lane)) ? 1 : 0;
-    }
-    if (lane < taken) {
-        sc.out_idx[rank] = ki;
-        sc.out_key[rank] = kk;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int myid = lane < taken ? sc.out_idx[mine] : -1;
-    const int mysel = lane < taken ? sc.out_key[mine] : 0;
+    const int myid = lane < kk ? sc.idx[mine] : -1;
+    const int mykey = lane < kk ? sc.key[mine] : 0;
     double sum = 0.0;
-    for (int k = 0; k < taken; ++k) sum += (double)__int_as_float(__builtin_amdgcn_readlane(mysel, k));
+    for (int k = 0; k < kk; ++k) sum += (double)__int_as_float(__builtin_amdgcn_readlane(mykey, k));
     float sf = (float)sum;
     if (sf < 6.103515625e-5f) sf = 6.103515625e-5f;
     if (wr && lane < K) {
         s_ids[lane] = myid;
-        s_w[lane] = __int_as_float(mysel) / sf;
+        s_w[lane] = __int_as_float(mykey) / sf;
     }
 }
 
 // Expert groups of the call from the routed ids in LDS (one wave): pairs that
-// share an expert form one group (at most one member per token), in the order
-// of their first pair; each group's tier by the residency predicate, read
-// from es/se/ss (the exp_slot/slot_exp/slot_state mirrors or copies of them).
+// share an expert form one group (at most one member per token: a token's
+// top-k experts are distinct), in the order of their first pair; each
+// group's tier by the residency predicate, read from es/se/ss (the
+// exp_slot/slot_exp/slot_state mirrors or copies of them).  s_first[e] must
+// hold 64 and s_tm[e] 0 for every e < E on entry (s_gid is scratch): the
+// pairs of expert e meet there by LDS atomics (its first pair, the tokens
+// that chose it), so no step loops over the pairs.  A pair with an invalid
+// id forms a group of its own (tier 2).
 __device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo * groups, int * n_groups,
-                             const int32_t * es, const int32_t * se, const int32_t * ss) {
+                             const int32_t * es, const int32_t * se, const int32_t * ss, int * s_first, int * s_tm,
+                             int * s_gid) {
     const int lane = threadIdx.x & 63;
-    const int T = p.T, E = p.n_expert, P = T * p.top_k;
+    const int T = p.T, E = p.n_expert, K = p.top_k, P = T * K;
     const bool live = lane < P;
     const int ex = live ? s_ids[lane] : -1;
     auto tier_of = [&](int e, int * idx) {
@@ -305,24 +331,33 @@ __device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo *
         if (lane == 0) *n_groups = P;
         return;
     }
-    int leader = lane, slot = 0, nmem = 0;
-    for (int q = 0; q < P; ++q) {
-        if (s_ids[q] == ex) {
-            if (q < lane) ++slot;
-            if (q < leader) leader = q;
-            ++nmem;
-        }
+    const bool valid = live && ex >= 0 && ex < E;
+    const int t = live ? lane / K : 0;
+    if (valid) {
+        atomicMin(s_first + ex, lane);
+        atomicOr(s_tm + ex, 1 << t);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int leader = valid ? s_first[ex] : lane;
+    const int tm = valid ? s_tm[ex] : (1 << t);
     const bool is_leader = live && leader == lane;
     const uint64_t lm = __ballot(is_leader);
-    const int gid = __popcll(lm & (leader == 0 ? 0ull : (~0ull >> (64 - leader))));
+    const int gid_lead = __popcll(lm & lanes_below());
     if (is_leader) {
         int idx;
         const int tier = tier_of(ex, &idx);
-        groups[gid].tier = tier;
-        groups[gid].idx = idx;
-        groups[gid].n_mem = min(nmem, min(T, DEC_MAXT));     // one member per token at most
+        groups[gid_lead].tier = tier;
+        groups[gid_lead].idx = idx;
+        groups[gid_lead].n_mem = min(__popc(tm), min(T, DEC_MAXT));
+        if (valid) s_gid[ex] = gid_lead;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int gid = valid ? s_gid[ex] : gid_lead;
+    const int slot = __popc(tm & ((1 << t) - 1));          // tokens before t that chose the expert
     if (live && slot < DEC_MAXT) groups[gid].mem[slot] = lane;
     if (lane == 0) *n_groups = __popcll(lm);
 }
@@ -461,46 +496,177 @@ __device__ __forceinline__ void rows_dot(const uint8_t * sm, int wb, int tier, i
 // ---------------------------------------------------------------- B
 
 constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
-static_assert(TAB_CHUNKS % WG == 0, "codebook chunks per thread");
-constexpr int GU_HALF = 8;              // gate rows of an item (and as many up rows)
-constexpr int GU_LOADS = 4;             // 16-byte loads per thread and half issued ahead (8 rows <= 2048 B)
-constexpr int COL_LOADS = 2;            // quantised token column chunks per thread issued early
 
-// B: the routing, selected by every workgroup from the logits, grouped by
-// expert, each group's tier by the residency predicate; the first workgroup
-// publishes ids, weights and groups.  Then the workgroup's items (group,
-// block j: gate rows 8 j .. 8 j + 7 and the up rows n_ff + 8 j .. paired with
-// them), one row per 16 lanes, the next item's loads in flight while the
-// current one is dotted; each item ends with GEGLU of gate row i with up row
-// i for every member, stored as fp32 down activations.  MT: members a group
-// can have (1 or DEC_MAXT).
+// A gate_up workgroup: 16 waves take the 64 rows of an item (32 gate, 32 up)
+// at once, one row per 16 lanes.
+constexpr int GU_NW = 16;
+constexpr int GU_NT = 64 * GU_NW;
+constexpr int GU_HR = DEC_GU_BLK;             // rows of each half (gate, up) of an item
+// Loads per thread of one half of an item: 32 rows over 1024 threads (Q4_K:
+// 99 chunks of 16 bytes per pair of rows at d_model 2816 -> 4; IQ2_S: at most
+// 57 -> 2, its other two repeat a chunk).  One layout for either format, so
+// the registers stay registers whichever tier an item has.  Chunks past a
+// half's share are loaded when the half is stored.
+constexpr int GU_LH = 4;
+
+// The dots of the staged row at `wb` (one row per 16 lanes) against the
+// members' columns av[c], c < n_mem <= MT; the row sums are complete in lane
+// 0 of the row.  A unit is decoded once for at most two members (3-4 member
+// groups decode it twice: the registers of four columns would halve the
+// waves a CU holds).
+template <int WT, int AM, int MT>
+__device__ __forceinline__ void item_dot(const uint8_t * sm, int wb, int n_mem, int d_in, bool live,
+                                         const ActView * av, float * acc, int grid_off) {
+    constexpr int LPR = Fmt<WT>::LPR;
+    const int lr = threadIdx.x % LPR;
+#pragma unroll
+    for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
+    if (live) {
+        const int U = d_in / Fmt<WT>::UNIT;
+        if (MT == 1 || n_mem == 1) {
+#pragma unroll 1
+            for (int u = lr; u < U; u += LPR) unit_dot_n<WT, AM, 1>(sm, wb, u, av, 1, acc, grid_off);
+        } else {
+#pragma unroll 1
+            for (int u = lr; u < U; u += LPR) unit_dot_n<WT, AM, 2>(sm, wb, u, av, 2, acc, grid_off);
+            if (MT > 2 && n_mem > 2) {
+#pragma unroll 1
+                for (int u = lr; u < U; u += LPR)
+                    unit_dot_n<WT, AM, 2>(sm, wb, u, av + 2, n_mem - 2, acc + 2, grid_off);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < MT; ++c)
+#pragma unroll
+        for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
+}
+
+// the half (h 0: gate rows, 1: up rows) of item (group gi, block j)
+template <int HT, int CT>
+__device__ __forceinline__ Span gu_span(const DecParams & p, const GroupInfo & gi, int j, int h) {
+    return make_span(gi, h * p.n_ff + DEC_GU_BLK * j, GU_HR, p.d_model, HT, CT, p.hot_gu, p.hot_gu_stride,
+                     p.cold_gu, p.cold_gu_stride, p.logits);
+}
+
+// the item's loads, unconditional
+template <int HT, int CT>
+__device__ __forceinline__ void gu_issue(u32x4 (&buf)[2 * GU_LH], const DecParams & p, const GroupInfo & gi, int j) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const Span sp = gu_span<HT, CT>(p, gi, j, h);
+#pragma unroll
+        for (int k = 0; k < GU_LH; ++k) buf[h * GU_LH + k] = sp.src[min((int)threadIdx.x + k * GU_NT, sp.nch - 1)];
+    }
+}
+
+// One gate_up item, its loads issued by gu_issue: gate rows [32 j, 32 j + 32)
+// and the up rows n_ff + 32 j .. paired with them, of group gi's expert
+// (weight type WT), staged through LDS, one row per 16 lanes.  Once the rows
+// are in LDS, the loads of the workgroup's next item (nx, nj; nx.n_mem == 0:
+// none) go into the registers just freed, in flight during this item's dots.
+// GEGLU pairs gate row i with up row i for every member, and each member's
+// 32 values are quantised (q8_0 / q8_1, block j of the pair's down
+// activation) into the pair's down column.
+template <int WT, int HT, int CT, int AM, int MT, int GSRC>
+__device__ __forceinline__ void gu_run(u32x4 (&buf)[2 * GU_LH], const DecParams & p, const GroupInfo & gi, int j,
+                                       uint8_t * smem, const ActView * av,
+                                       int grid_off, float (*s_y)[MT], float (*s_act)[DEC_GU_BLK]) {
+    constexpr int LH = GU_LH;
+    const int T = p.T, K = p.top_k, F = p.n_ff;
+    const int row = threadIdx.x >> 4, hr = row / GU_HR, r = row - hr * GU_HR;     // hr 0: gate rows, 1: up rows
+    const bool live = gi.tier < 2 && gi.n_mem > 0;
+    const Span s0 = gu_span<HT, CT>(p, gi, j, 0), s1 = gu_span<HT, CT>(p, gi, j, 1);
+    __syncthreads();                                      // the previous item is done with LDS
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const Span & sp = h ? s1 : s0;
+        uint8_t * dst = smem + h * p.w_lds_gu;
+#pragma unroll
+        for (int k = 0; k < LH; ++k) {
+            const int i = threadIdx.x + k * GU_NT;
+            if (i < sp.nch) reinterpret_cast<u32x4 *>(dst)[i] = buf[h * LH + k];
+        }
+        for (int i = threadIdx.x + LH * GU_NT; i < sp.nch; i += GU_NT) reinterpret_cast<u32x4 *>(dst)[i] = sp.src[i];
+    }
+    __syncthreads();
+    const int wb = hr ? p.w_lds_gu + s1.off + r * s1.rb : s0.off + r * s0.rb;
+    float acc[MT];
+    item_dot<WT, AM, MT>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
+    if ((threadIdx.x & 15) == 0) {
+#pragma unroll
+        for (int c = 0; c < MT; ++c) s_y[row][c] = acc[c];
+    }
+    __syncthreads();
+    // GEGLU of gate row 32 j + i with its up row, member c
+    if ((int)threadIdx.x < GU_HR * MT) {
+        const int i = threadIdx.x % GU_HR, c = threadIdx.x / GU_HR;
+        s_act[c][i] = geglu1<GSRC>(s_y[i][c], s_y[GU_HR + i][c]);
+    }
+    __syncthreads();
+    // member c's block j, one wave a member (32 lanes)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (live && wave < gi.n_mem) {
+        ActView L;
+        act_layout(F, 0, &L);
+        const int pair = max(0, min(member(gi, wave), T * K - 1));
+        const float v = lane < DEC_GU_BLK ? s_act[wave][lane] : 0.0f;
+        q8_32_put<AM>(p.yq + (int64_t)pair * p.yq_stride, L, v, DEC_GU_BLK * j + (lane & 31), lane < DEC_GU_BLK);
+    }
+}
+
+// the routing's LDS scratch in a gate_up workgroup (at the start of the
+// weight staging area, which the host sizes to hold it: dec_gu_half_bytes)
+struct GuScratch {
+    int32_t res[3][256];
+    int first[256], tm[256];
+    int ids[DEC_PMAX];
+    float w[DEC_PMAX];
+    SelScratch sel[DEC_MAXT];
+};
+
+// B: the routing, selected by every workgroup from the logits (wave t
+// selects token t), grouped by expert, each group's tier by the residency
+// predicate; the first workgroup publishes ids, weights and groups.  Then the
+// workgroup's items: item i is group i / (n_ff / 32) and block j = i mod
+// (n_ff / 32) of its down activation (32 gate rows and the 32 up rows paired
+// with them); workgroup b takes items b, b + gridDim.x, ... (the grid is at
+// most what the device holds resident, so every workgroup runs at once).
+// MT: members a group can have (1 or DEC_MAXT).
 template <int HT, int CT, int AM, int MT, int GSRC>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_gate_up(const DecParams p) {
+__global__ __launch_bounds__(GU_NT) void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     static_assert(Fmt<HT>::LPR == 16 && Fmt<CT>::LPR == 16 && k256<HT>() && k256<CT>(), "gate_up formats");
+    static_assert(GU_NW >= DEC_MAXT && GU_NT >= 256, "a wave per token and a thread per expert");
     constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
-    __shared__ int s_ids[DEC_PMAX];
-    __shared__ float s_w[DEC_PMAX];
-    __shared__ GroupInfo s_grp[DEC_PMAX];
-    __shared__ int32_t s_res[3][256];       // exp_slot, slot_exp, slot_state
+    constexpr int COLL = MT == 1 ? 1 : 2;                 // quantised column chunks per thread issued at once
+    constexpr int TABL = (TAB_CHUNKS + GU_NT - 1) / GU_NT;   // codebook chunks per thread
+    // the routing's scratch lives where the weights are staged later (the
+    // first item starts with a barrier, after every read of it)
+    GuScratch & sr = *reinterpret_cast<GuScratch *>(smem);
+    int * s_ids = sr.ids;
+    float * s_w = sr.w;
+    int32_t (*s_res)[256] = sr.res;           // exp_slot, slot_exp, slot_state
+    int * s_first = sr.first;                 // also each expert's group id, once its first pair is known
+    int * s_tm = sr.tm;
+    SelScratch * s_sel = sr.sel;
+    __shared__ GroupInfo s_grp[DEC_PMAX];     // kept for every item of the workgroup
     __shared__ int s_ng;
-    __shared__ SelScratch s_sel[WG / 64];
-    __shared__ float s_y[2 * GU_HALF][MT];
+    __shared__ float s_y[2 * GU_HR][MT];
+    __shared__ float s_act[MT][DEC_GU_BLK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int T = p.T, K = p.top_k, E = p.n_expert, d_in = p.d_model, F = p.n_ff;
 
-    // 1. every load of the prologue, in the order the data are needed and none
-    //    under a condition: this wave's token's logits, the residency mirrors,
-    //    the IQ2_S codebook, every token's quantised column (the columns are
-    //    contiguous: xq_stride == their size)
+    // 1. the routing's loads, none under a lane condition: the logits of this
+    //    wave's token (waves below T), the residency mirrors
     float lg[4];
-    {
-        const float * lt = p.logits + (int64_t)min(wave, T - 1) * E;
+    if (wave < T) {
+        const float * lt = p.logits + (int64_t)wave * E;
 #pragma unroll
         for (int j = 0; j < 4; ++j) lg[j] = lt[min(lane + 64 * j, E - 1)];
     }
-    int32_t res[3];
-    {
+    int32_t res[3] = {0, 0, 0};
+    if (threadIdx.x < 256) {
         // without hot slots the mirrors may be absent: read a valid dummy
         const int ks = p.k_slots;
         const int32_t * dummy = reinterpret_cast<const int32_t *>(p.logits);
@@ -511,119 +677,91 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         res[0] = es[min((int)threadIdx.x, E - 1)];
         res[1] = se[is];
         res[2] = ss[is];
+        s_first[threadIdx.x] = 64;
+        s_tm[threadIdx.x] = 0;
     }
-    u32x4 tab[TAB_CHUNKS / WG];
-    if (IQ2) {
+
+    // 2. the routing: wave t < T selects token t; then the expert groups
+    if (wave < T) {
+        asm volatile("" ::"v"(lg[2]), "v"(lg[3]));
+        if (E <= 128) select_topk<2>(lg, E, K, s_ids + wave * K, s_w + wave * K, true, s_sel[wave]);
+        else select_topk<4>(lg, E, K, s_ids + wave * K, s_w + wave * K, true, s_sel[wave]);
+    }
+    if (threadIdx.x < 256) {
 #pragma unroll
-        for (int k = 0; k < TAB_CHUNKS / WG; ++k)
-            tab[k] = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_dec)[threadIdx.x + k * WG];
+        for (int i = 0; i < 3; ++i) s_res[i][threadIdx.x] = res[i];
     }
+    __syncthreads();
+    if (wave == 0) build_groups(p, s_ids, s_grp, &s_ng, s_res[0], s_res[1], s_res[2], s_first, s_tm, s_first);
+    __syncthreads();
+    const int ng = max(0, min(s_ng, DEC_PMAX));
+    const int NBLK = F / DEC_GU_BLK, n_items = ng * NBLK;
+    if ((int)blockIdx.x >= n_items) return;   // workgroup-uniform (workgroup 0 always has item 0)
+    auto item = [&](int it, int * jo) {
+        const int g = it / NBLK;
+        *jo = it - g * NBLK;
+        return validate_group(p, s_grp[g], ng, g);
+    };
+
+    // 3. every token's quantised column (contiguous: xq_stride == their
+    //    size), the IQ2_S codebook and the first item's weights, in that
+    //    order; the columns and the codebook then land in LDS (after the two
+    //    halves: at a0), waiting for their own loads only
     ActView tmp;
     const int abytes = act_layout(d_in, 0, &tmp), a16 = abytes / 16;
     const int ncol = min(T, MT) * a16;
     const u32x4 * xq4 = reinterpret_cast<const u32x4 *>(p.xq);
-    u32x4 col[COL_LOADS * MT];
+    u32x4 col[COLL];
 #pragma unroll
-    for (int k = 0; k < COL_LOADS * MT; ++k) col[k] = xq4[min((int)threadIdx.x + k * WG, ncol - 1)];
-
-    // 2. the routing: wave t < T selects token t (a wave past T repeats the
-    //    last token and writes nothing); then the expert groups
-    {
-        asm volatile("" ::"v"(lg[2]), "v"(lg[3]));
-        const int o = min(wave, T - 1) * K;
-        if (E <= 128) select_topk<2>(lg, E, K, s_ids + o, s_w + o, wave < T, s_sel[wave]);
-        else select_topk<4>(lg, E, K, s_ids + o, s_w + o, wave < T, s_sel[wave]);
+    for (int k = 0; k < COLL; ++k) col[k] = xq4[min((int)threadIdx.x + k * GU_NT, ncol - 1)];
+    u32x4 tab[TABL];
+    if (IQ2) {
+#pragma unroll
+        for (int k = 0; k < TABL; ++k)
+            tab[k] = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_dec)[min((int)threadIdx.x + k * GU_NT, TAB_CHUNKS - 1)];
     }
+    int it = blockIdx.x, j;
+    GroupInfo gi = item(it, &j);
+    u32x4 buf[2 * GU_LH];
+    gu_issue<HT, CT>(buf, p, gi, j);
+    const int a0 = 2 * p.w_lds_gu;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) s_res[i][threadIdx.x] = res[i];
-    __syncthreads();
-    if (wave == 0) build_groups(p, s_ids, s_grp, &s_ng, s_res[0], s_res[1], s_res[2]);
-    __syncthreads();
-    const int ng = max(0, min(s_ng, DEC_PMAX));
-    const int NB = F / GU_HALF;
-    int i0, i1;
-    item_range(ng * NB, &i0, &i1);
-
-    // 3. the first item's loads (both halves)
-    auto item_group = [&](int it) {
-        const int g = it / NB;
-        return validate_group(p, s_grp[max(0, min(g, DEC_PMAX - 1))], ng, g);
-    };
-    auto half_span = [&](const GroupInfo & gi, int it, int h) {
-        return make_span(gi, h * F + GU_HALF * (it % NB), GU_HALF, d_in, HT, CT, p.hot_gu, p.hot_gu_stride,
-                         p.cold_gu, p.cold_gu_stride, p.logits);
-    };
-    GroupInfo gcur = item_group(i0);
-    Span sp[2];
-    Regs<GU_LOADS> st[2];
+    for (int k = 0; k < COLL; ++k) {
+        const int i = threadIdx.x + k * GU_NT;
+        if (i < ncol) reinterpret_cast<u32x4 *>(smem + a0)[i] = col[k];
+    }
+    for (int i = threadIdx.x + COLL * GU_NT; i < ncol; i += GU_NT) reinterpret_cast<u32x4 *>(smem + a0)[i] = xq4[i];
+    const int grid_off = align16i(a0 + min(T, DEC_MAXT) * abytes);
+    if (IQ2) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        sp[h] = half_span(gcur, i0, h);
-        span_load(st[h], sp[h]);
+        for (int k = 0; k < TABL; ++k) {
+            const int i = threadIdx.x + k * GU_NT;
+            if (i < TAB_CHUNKS) reinterpret_cast<u32x4 *>(smem + grid_off)[i] = tab[k];
+        }
     }
 
-    // 4. the first workgroup publishes the routing; the codebook and the
-    //    columns land in LDS (after the two halves: at a0)
+    // 4. the first workgroup publishes the routing
     if (blockIdx.x == 0) {
         if ((int)threadIdx.x < T * K) {
             p.ids[threadIdx.x] = s_ids[threadIdx.x];
             p.w[threadIdx.x] = s_w[threadIdx.x];
         }
-        for (int i = threadIdx.x; i < ng; i += WG) p.ctl->groups[i] = s_grp[i];
+        for (int i = threadIdx.x; i < ng; i += GU_NT) p.ctl->groups[i] = s_grp[i];
         if (threadIdx.x == 0) p.ctl->n_groups = ng;
         count_routes(p, s_ids, s_grp, ng);
     }
-    const int a0 = 2 * p.w_lds_gu;
-#pragma unroll
-    for (int k = 0; k < COL_LOADS * MT; ++k) {
-        const int i = threadIdx.x + k * WG;
-        if (i < ncol) reinterpret_cast<u32x4 *>(smem + a0)[i] = col[k];
-    }
-    for (int i = threadIdx.x + COL_LOADS * MT * WG; i < ncol; i += WG) reinterpret_cast<u32x4 *>(smem + a0)[i] = xq4[i];
-    const int grid_off = align16i(a0 + min(T, DEC_MAXT) * abytes);
-    if (IQ2) {
-#pragma unroll
-        for (int k = 0; k < TAB_CHUNKS / WG; ++k)
-            reinterpret_cast<u32x4 *>(smem + grid_off)[threadIdx.x + k * WG] = tab[k];
-    }
 
-    // 5. the items
-    const int row = threadIdx.x >> 4, h = row >> 3;          // h 0: gate rows, 1: up rows
-    for (int it = i0; it < i1; ++it) {
-        const GroupInfo gi = gcur;
+    // 5. the items (gu_run's first barrier orders the LDS stores above)
+    while (true) {
         ActView av[MT];
 #pragma unroll
         for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + max(0, min(member(gi, c) / K, T - 1)) * abytes, &av[c]);
-        __syncthreads();                      // the previous item is done with LDS
-        span_store(st[0], sp[0], smem);
-        span_store(st[1], sp[1], smem + p.w_lds_gu);
-        __syncthreads();
-        // (no array indexed by a per-lane value: that would live in scratch)
-        const int wb = h ? p.w_lds_gu + sp[1].off + (row & 7) * sp[1].rb : sp[0].off + (row & 7) * sp[0].rb;
-        const bool live = sp[0].valid != 0;
-        if (it + 1 < i1) {
-            gcur = item_group(it + 1);
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                sp[k] = half_span(gcur, it + 1, k);
-                span_load(st[k], sp[k]);      // in flight during this item's dots
-            }
-        }
-        float acc[MT];
-        rows_dot<HT, CT, AM, MT>(smem, wb, gi.tier, gi.n_mem, d_in, live, av, acc, grid_off);
-        if ((threadIdx.x & 15) == 0) {
-#pragma unroll
-            for (int c = 0; c < MT; ++c) s_y[row][c] = acc[c];
-        }
-        __syncthreads();
-        // GEGLU of gate row 8 j + i with up row n_ff + 8 j + i, member c
-        if (live && (int)threadIdx.x < GU_HALF * MT) {
-            const int i = threadIdx.x & (GU_HALF - 1), c = threadIdx.x / GU_HALF;
-            if (c < gi.n_mem) {
-                const int pair = max(0, min(member(gi, c), T * K - 1));
-                p.ya[(int64_t)pair * F + GU_HALF * (it % NB) + i] = geglu1<GSRC>(s_y[i][c], s_y[GU_HALF + i][c]);
-            }
-        }
+        if (gi.tier == 0) gu_run<HT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, smem, av, grid_off, s_y, s_act);
+        else gu_run<CT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, smem, av, grid_off, s_y, s_act);
+        it += gridDim.x;
+        if (it >= n_items) break;
+        gi = item(it, &j);
+        gu_issue<HT, CT>(buf, p, gi, j);
     }
 }
 
@@ -631,8 +769,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
 
 constexpr int DN_LPR = 16;      // lanes per row: lane l holds the row's block pair l (blocks 2 l, 2 l + 1)
 constexpr int DN_RPP = WG / DN_LPR;   // rows per pass
-constexpr int DN_QP = 8;        // pairs quantised per pass (fp32 activations in)
-constexpr int DN_GRP_NPS = 2;   // passes of 16 rows of a down-by-group workgroup (4 measured slower)
+constexpr int DN_CL = 8;        // 16-byte chunks of the pairs' down columns per thread loaded first
+constexpr int DN_GRP_NPS = 2;   // passes of 16 rows of a down-by-group workgroup, all in flight
 constexpr int DN_GRP_ROWS = DN_GRP_NPS * DN_RPP;
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -801,16 +939,16 @@ __device__ __forceinline__ void q8_quad(uint8_t * col, const ActView & L, const 
 
 // C: output rows [r0, r0 + R) of every token, r0 = blockIdx.x R, R =
 // 2^dn_rows_log2.  First, with no dependence on anything, the loads of the
-// pairs' down activations (the pairs are 0 .. T top_k - 1 whatever the
-// grouping) and of the groups' records and routing weights (from B's first
-// workgroup); then a table of the groups (tier, members, .scale, where this
-// block's rows start in the pool).  The weights never pass through LDS: each
-// row's lanes load its block pairs straight into registers (lane l: blocks
-// 2 l, 2 l + 1, dword-aligned), the next pass's rows in flight while the
-// current ones are dotted against the members' activations, which are in
-// LDS, quantised here from B's fp32 GEGLU outputs (8 lanes a 32-block).  Each row is scaled by the expert's
-// .scale into s_y[pair][row]; then each (token, row) output is the sum of
-// w_k y_k in k order.  Invalid groups leave their pairs at zero.
+// pairs' quantised down columns (written by B; the pairs are 0 .. T top_k - 1
+// whatever the grouping) and of the groups' records and routing weights
+// (from B's first workgroup); then a table of the groups (tier, members,
+// .scale, where this block's rows start in the pool).  The weights never
+// pass through LDS: each row's lanes load its block pairs straight into
+// registers (lane l: blocks 2 l, 2 l + 1, dword-aligned), the next pass's
+// rows in flight while the current ones are dotted against the members'
+// columns in LDS.  Each row is scaled by the expert's .scale into
+// s_y[pair][row]; then each (token, row) output is the sum of w_k y_k in k
+// order.  Invalid groups leave their pairs at zero.
 template <int HD, int CD, int AM, int MT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_dec_down(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -821,16 +959,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     __shared__ int s_ng;
     const int D = p.d_model, F = p.n_ff, K = p.top_k, T = p.T, P = T * K;
     const int lg2r = p.dn_rows_log2, R = 1 << lg2r, r0 = blockIdx.x << lg2r, nr = max(0, min(R, D - r0));
-    ActView L;
-    const int abytes = act_layout(F, 0, &L);
-    const int F4 = F / 4;                                     // 16-byte chunks of one pair's fp32 activation
+    const int abytes = (int)p.yq_stride;                      // one quantised column, a multiple of 16
     const int NP = F / 64;                                    // block pairs per row
 
-    // 1. the activations' first loads, then the records
-    const u32x4 * ya4 = reinterpret_cast<const u32x4 *>(p.ya);
-    u32x4 act[DN_QP];
+    // 1. the columns' first loads, then the records
+    const u32x4 * yq4 = reinterpret_cast<const u32x4 *>(p.yq);
+    const int nch = P * (abytes / 16);
+    u32x4 col[DN_CL];
 #pragma unroll
-    for (int q = 0; q < DN_QP; ++q) act[q] = ya4[(int64_t)min(q, P - 1) * F4 + min((int)threadIdx.x, F4 - 1)];
+    for (int k = 0; k < DN_CL; ++k) col[k] = yq4[min((int)threadIdx.x + k * WG, nch - 1)];
     {
         const GroupInfo gi_in = p.ctl->groups[min((int)threadIdx.x, DEC_PMAX - 1)];
         const int ngv = p.ctl->n_groups;
@@ -873,37 +1010,33 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const uint8_t * base = d.tier == 0 ? p.hot_dn : p.cold_dn;
         return base + d.row0 + (uint64_t)r * d.rb + (uint64_t)pl * (blk_bytes(d.tier == 0 ? HD : CD) * 2);
     };
-    DnPair cur, nxt;
-    int kc = 0, kn = 0;
     auto load = [&](DnPair & q, int ps, int * kind) {
         const uint8_t * src = pair_src(ps, kind);
         if (*kind == 0) dn_pair_load<HD>(q, src);
         else dn_pair_load<CD>(q, src);
     };
-    if (ng > 0) load(cur, 0, &kc);
-
-    // 2. the activations into LDS
-    {
-        const bool qlane = (int)threadIdx.x < F4;             // F4 <= WG: one chunk of each pair per lane
-        for (int q0 = 0; q0 < P; q0 += DN_QP) {
-            if (q0 > 0) {
+    // every pass's block pairs in flight at once (up to DA passes; later ones
+    // are loaded when they come)
+    constexpr int DA = MT == 1 ? 2 : 8;
+    DnPair w[DA];
+    int kw[DA];
 #pragma unroll
-                for (int q = 0; q < DN_QP; ++q)
-                    act[q] = ya4[(int64_t)min(q0 + q, P - 1) * F4 + min((int)threadIdx.x, F4 - 1)];
-            }
-#pragma unroll
-            for (int q = 0; q < DN_QP; ++q) {
-                const float v[4] = {__uint_as_float(act[q].x), __uint_as_float(act[q].y), __uint_as_float(act[q].z),
-                                    __uint_as_float(act[q].w)};
-                q8_quad<AM>(smem + (q0 + q) * abytes, L, v, threadIdx.x, qlane && q0 + q < P);
-            }
-        }
+    for (int q = 0; q < DA; ++q) {
+        kw[q] = 0;
+        if (q < passes) load(w[q], q, &kw[q]);
     }
+
+    // 2. the columns into LDS
+#pragma unroll
+    for (int k = 0; k < DN_CL; ++k) {
+        const int i = threadIdx.x + k * WG;
+        if (i < nch) reinterpret_cast<u32x4 *>(smem)[i] = col[k];
+    }
+    for (int i = threadIdx.x + DN_CL * WG; i < nch; i += WG) reinterpret_cast<u32x4 *>(smem)[i] = yq4[i];
     __syncthreads();
 
     // 3. the passes: DN_RPP rows each, one row per DN_LPR lanes
-    for (int ps = 0; ps < passes; ++ps) {
-        if (ps + 1 < passes) load(nxt, ps + 1, &kn);
+    auto pass = [&](const DnPair & cur, int kc, int ps) {
         const int k = ps * DN_RPP + lrow, s = min(k >> lg2r, ng - 1), r = k & (R - 1);
         const DnGroup & d = s_gi[s];
         const bool live = k < rows && r < nr && d.n_mem > 0 && lane16 < NP;
@@ -933,8 +1066,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
             for (int c = 0; c < MT; ++c)
                 if (c < d.n_mem) s_y[d.mem[c]][r] = acc[c] * d.scale;
         }
-        cur = nxt;
-        kc = kn;
+    };
+#pragma unroll
+    for (int q = 0; q < DA; ++q)
+        if (q < passes) pass(w[q], kw[q], q);
+    for (int ps = DA; ps < passes; ++ps) {
+        DnPair t;
+        int kt = 0;
+        load(t, ps, &kt);
+        pass(t, kt, ps);
     }
     __syncthreads();
 
@@ -955,8 +1095,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
 // NPS rows, all of them in flight at once: lane l of a row's 16 holds its
 // block pair l), writing the scaled rows y_pair = .scale W a_pair to ydn;
 // workgroups of groups past the call's count return at once.  Only the
-// members' GEGLU outputs are quantised here (one to four columns, where the
-// kernel over every group quantises all T top_k of them in every workgroup).
+// members' quantised columns are read (one to four, where the kernel over
+// every group copies all T top_k of them into every workgroup).
 // k_dec_combine then sums each token's top_k rows.
 template <int HD, int CD, int AM, int MT, int NPS>
 __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
@@ -970,16 +1110,17 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
     if (g >= ng) return;
     const GroupInfo gi = validate_group(p, p.ctl->groups[g], ng, g);
     const int nm = gi.tier < 2 ? gi.n_mem : 0;
-    const int F4 = F / 4, NP = F / 64;
-    ActView L;
-    const int abytes = act_layout(F, 0, &L);
+    const int NP = F / 64;
+    const int abytes = (int)p.yq_stride, a16 = abytes / 16;
 
-    // 1. the members' activations, then every row's block pairs
-    const u32x4 * ya4 = reinterpret_cast<const u32x4 *>(p.ya);
-    u32x4 act[MT];
+    // 1. the members' columns, then every row's block pairs
+    const u32x4 * yq4 = reinterpret_cast<const u32x4 *>(p.yq);
+    u32x4 col[MT];                                          // one chunk of each column per thread (n_ff <= 1024)
 #pragma unroll
-    for (int c = 0; c < MT; ++c)
-        act[c] = ya4[(int64_t)max(0, min(c < nm ? gi.mem[c] : gi.mem[0], P - 1)) * F4 + min((int)threadIdx.x, F4 - 1)];
+    for (int c = 0; c < MT; ++c) {
+        const int pr = max(0, min(c < nm ? gi.mem[c] : gi.mem[0], P - 1));
+        col[c] = yq4[(int64_t)pr * a16 + min((int)threadIdx.x, a16 - 1)];
+    }
     const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
     const int pl = min(lane16, NP - 1);
     const int wt = gi.tier == 0 ? HD : CD;
@@ -995,16 +1136,11 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
         else dn_pair_load<CD>(w[ps], src);
     }
 
-    // 2. the members' q8 columns
-    {
-        const bool qlane = (int)threadIdx.x < F4;
+    // 2. the members' columns into LDS
 #pragma unroll
-        for (int c = 0; c < MT; ++c) {
-            if (c >= max(nm, 1)) break;
-            const float v[4] = {__uint_as_float(act[c].x), __uint_as_float(act[c].y), __uint_as_float(act[c].z),
-                                __uint_as_float(act[c].w)};
-            q8_quad<AM>(smem + c * abytes, L, v, threadIdx.x, qlane && c < nm);
-        }
+    for (int c = 0; c < MT; ++c) {
+        if (c >= max(nm, 1)) break;
+        if ((int)threadIdx.x < a16) reinterpret_cast<u32x4 *>(smem + c * abytes)[threadIdx.x] = col[c];
     }
     __syncthreads();
 
@@ -1043,7 +1179,6 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
                 if (c < nw) p.ydn[(int64_t)max(0, min(gi.mem[c], P - 1)) * D + r0 + r] = acc[c] * scale;
         }
     }
-
 }
 
 // the combine after the down kernel by group (llama-graph.cpp:1812-1840):
@@ -1325,6 +1460,13 @@ int dec_act_bytes(int n) {
     return act_layout(n, 0, &v);
 }
 
+// LDS bytes of one half of a gate_up item (32 rows of the longer gate_up
+// row, plus one dword a funnel read may touch past the end), at least half
+// the routing's scratch, which the two halves hold before the first item
+int dec_gu_half_bytes(int, int row_bytes) {
+    return std::max(align16i(GU_HR * row_bytes + 32), align16i((int)sizeof(GuScratch) / 2 + 16));
+}
+
 // dynamic LDS of B: the two halves of an item, one activation column per
 // token of the call (a group has at most one member per token), the IQ2_S
 // codebook when used
@@ -1334,30 +1476,21 @@ int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
            (iq2 ? (int)sizeof(Iq2sTables) : 0);
 }
 
-// dynamic LDS of C: every pair's down activation
+// dynamic LDS of C: every pair's quantised down column
 int dec_lds_down(const DecParams & p) {
     return p.T * p.top_k * dec_act_bytes(p.n_ff);
 }
 
 namespace {
-// launch with the dispatch's own begin/end timestamps recorded into e0/e1
-// when profiling (e0 != nullptr)
-template <typename F>
-void launch_timed(F k, dim3 grid, int lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const DecParams & p,
-                  int block = WG) {
-    if (e0) hipExtLaunchKernelGGL(k, grid, dim3(block), (uint32_t)lds, s, e0, e1, 0u, p);
-    else hipLaunchKernelGGL(k, grid, dim3(block), lds, s, p);
-}
-
-// resident workgroups of a kernel on the current device (cached per device
-// and instantiation; LDS bytes are part of the key)
+// resident workgroups of a kernel on the current device (cached per device,
+// kernel and LDS bytes; a kernel's block size is fixed)
 template <typename F>
 int resident_wgs(F k, int lds, int block) {
     static std::mutex mu;
     static std::map<std::tuple<int, const void *, int>, int> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    const auto key = std::make_tuple(dev, reinterpret_cast<const void *>(k), lds);   // block is fixed per kernel
+    const auto key = std::make_tuple(dev, reinterpret_cast<const void *>(k), lds);
     std::lock_guard<std::mutex> lk(mu);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
@@ -1368,6 +1501,16 @@ int resident_wgs(F k, int lds, int block) {
     cache[key] = n;
     return n;
 }
+
+// launch with the dispatch's own begin/end timestamps recorded into e0/e1
+// when profiling (e0 != nullptr)
+template <typename F>
+void launch_timed(F k, dim3 grid, int lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const DecParams & p,
+                  int block = WG) {
+    if (e0) hipExtLaunchKernelGGL(k, grid, dim3(block), (uint32_t)lds, s, e0, e1, 0u, p);
+    else hipLaunchKernelGGL(k, grid, dim3(block), lds, s, p);
+}
+
 }  // namespace
 
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int am, int gelu, hipStream_t s,
@@ -1385,19 +1528,21 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         if (err != hipSuccess) return err;
     }
     {
-        // one workgroup per item while they can all be resident; no
-        // workgroup waits on another, so any grid is safe
-        const int items = p.T * p.top_k * (p.n_ff / GU_HALF);   // at most; the groups decide
+        // one workgroup per possible item: every routed pair could be a group
+        // of its own; the workgroups past the call's groups stop after the
+        // routing.  No workgroup waits on another, so any grid is safe.
+        const int groups_max = std::min(p.T * p.top_k, DEC_PMAX);
+        const int items = groups_max * (p.n_ff / DEC_GU_BLK);     // at most; the groups decide
         const int lds = dec_lds_gate_up(p, hgu, cgu);
-        auto go = [&](auto k) {
-            const int cap = resident_wgs(k, lds, WG);
-            int grid = std::max(1, cap > 0 ? std::min(items, cap) : items);
-            if (p.gu_wgs_max > 0) grid = std::min(grid, p.gu_wgs_max);
-            launch_timed(k, dim3(grid), lds, s, e[2], e[3], p);
+        auto go = [&](auto k, int block) {
+            const int cap = resident_wgs(k, lds, block);
+            const int grid = std::max(1, cap > 0 ? std::min(items, cap) : items);
+            launch_timed(k, dim3(grid), lds, s, e[2], e[3], p, block);
         };
 #define LL_GU(A, B, M, G) \
         if (hgu == A && cgu == B && am == M && gelu == G) { \
-            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, G>); else go(k_dec_gate_up<A, B, M, DEC_MAXT, G>); \
+            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, G>, GU_NT); \
+            else go(k_dec_gate_up<A, B, M, DEC_MAXT, G>, GU_NT); \
         } else
 #define LL_GU2(A, B) LL_GU(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_GU(A, B, AM_CPU, SRC_GEGLU_TANH) \
                      LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TANH)
@@ -1409,25 +1554,24 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         if (err != hipSuccess) return err;
     }
     {
+        // one token: the kernel over every group (its 8 columns are 9 KB); more:
+        // by group (each workgroup reads its members' columns only) + combine
         const int lds = dec_lds_down(p);
         const int rows = 1 << p.dn_rows_log2;
         const dim3 grid((p.d_model + rows - 1) / rows);
-        const dim3 ggrid((p.d_model + DN_GRP_ROWS - 1) / DN_GRP_ROWS, p.T * p.top_k);
+        const dim3 ggrid((p.d_model + DN_GRP_ROWS - 1) / DN_GRP_ROWS, std::min(p.T * p.top_k, DEC_PMAX));
         const int glds = std::min(p.T, DEC_MAXT) * dec_act_bytes(p.n_ff);
 #define LL_DN(A, B, M) \
         if (hdn == A && cdn == B && am == M) { \
-            if (p.dn_by_group) { \
-                if (p.T == 1) launch_timed(k_dec_down_grp<A, B, M, 1, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
-                else launch_timed(k_dec_down_grp<A, B, M, DEC_MAXT, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
-            } else if (p.T == 1) launch_timed(k_dec_down<A, B, M, 1>, grid, lds, s, e[4], e[5], p); \
-            else launch_timed(k_dec_down<A, B, M, DEC_MAXT>, grid, lds, s, e[4], e[5], p); \
+            if (p.T == 1) launch_timed(k_dec_down<A, B, M, 1>, grid, lds, s, e[4], e[5], p); \
+            else launch_timed(k_dec_down_grp<A, B, M, DEC_MAXT, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
         } else
 #define LL_DN2(A, B) LL_DN(A, B, AM_CPU) LL_DN(A, B, AM_Q8_1)
         LL_DN2(T_Q5_0, T_IQ4_NL) LL_DN2(T_Q5_0, T_Q5_0) LL_DN2(T_IQ4_NL, T_IQ4_NL) LL_DN2(T_IQ4_NL, T_Q5_0)
         return hipErrorInvalidValue;
 #undef LL_DN2
 #undef LL_DN
-        if (p.dn_by_group) launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
+        if (p.T > 1) launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
     }
     return hipGetLastError();
 }

@@ -55,6 +55,7 @@ struct GroupInfo {
 };
 
 constexpr int DEC_DN_MAXR = 32;  // output rows of one down workgroup, at most
+constexpr int DEC_GU_BLK = 32;   // gate rows of one gate_up item (one q8 block of the down activations)
 
 // control block at the start of the decode workspace: the expert groups the
 // gate_up kernel selected, for the down kernel
@@ -81,24 +82,23 @@ struct DecParams {
     int32_t * ids;              // [T][top_k]
     float * w;                  // [T][top_k]
     uint8_t * xq; int64_t xq_stride;     // quantised tokens
-    float * ya;                 // [P][n_ff] down activations (GEGLU outputs) per routed pair
-    float * ydn;                // [P][d_model] scaled down rows per routed pair (down by group)
-    int dn_by_group;            // 1: the down kernel by group + k_dec_combine, 0: the down kernel over every group
-    int gu_wgs_max;             // > 0: at most this many gate_up workgroups (else as many as are resident)
+    uint8_t * yq; int64_t yq_stride;     // [P] quantised down activations (GEGLU outputs in q8_0 / q8_1)
+    float * ydn;                // [P][d_model] scaled down rows per routed pair (down by group, T > 1)
     float * out;                // [T][d_model]
-    int w_lds_gu;               // LDS bytes of one half of a gate_up item (8 rows)
+    int w_lds_gu;               // LDS bytes of one half of a gate_up pass (dec_gu_half_bytes)
     int dn_rows_log2;           // log2 of the output rows per down workgroup (<= DEC_DN_MAXR)
     int32_t * rc_counts;        // [n_expert] routed pairs per expert, or NULL
     int32_t * rc_hits;          // [2] hot pairs, other pairs (with rc_counts)
 };
 
 int dec_act_bytes(int n);
+int dec_gu_half_bytes(int T, int row_bytes);
 int dec_lds_gate_up(const DecParams & p, int ht, int ct);
 int dec_lds_down(const DecParams & p);
 // ev (optional, profiling): 8 events that receive the begin and end
 // timestamps of the router, gate_up, down and combine kernels (ev[0..1],
-// ev[2..3], ev[4..5], ev[6..7]; the last two stay unrecorded without a
-// combine kernel).
+// ev[2..3], ev[4..5], ev[6..7]; the last two stay unrecorded at one token,
+// which has no combine kernel).
 hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn, int act_mode, int gelu_src,
                          hipStream_t s, hipEvent_t * ev);
 hipError_t launch_zero_i32(int * p, int n, hipStream_t s);

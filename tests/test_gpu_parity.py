@@ -280,14 +280,14 @@ def test_island_fires_match_layer(gpu, oracle, fused, act_mode, T):
 
 @pytest.mark.parametrize("T,n_hot", [(1, 0), (1, 16), (2, 7), (4, 9), (4, 0)])
 @pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
-@pytest.mark.parametrize("down", ["default", "other"])
+@pytest.mark.parametrize("down", [-1, 1, 5])
 def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, down):
-    """The decode path (expert groups, GEGLU in the gate_up epilogue, down
-    activation quantisation in the down kernel, then the combine: in the
-    workgroup over every group, or in a kernel of its own after the down
-    kernel by group) against the generic per-pair path, over several calls
-    on one workspace.  "other" forces the down kernel the token count would
-    not pick (tuning key 4)."""
+    """The decode path (expert groups, GEGLU and the down activation's q8
+    quantisation in the gate_up epilogue, the down kernel over every group
+    with the combine in its workgroup) against the generic per-pair path,
+    over several calls on one workspace.  `down` is log2 of the down
+    kernel's rows per workgroup (tuning key 3; -1: the default, 1: 2 rows,
+    5: 32 rows)."""
     torch = torch_mod()
     say(f"decode vs generic T={T} hot={n_hot} act={act_mode} down={down}")
     spec = FULL16
@@ -295,8 +295,7 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, do
     dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
     lib = la.lib()
     outs = {}
-    if down == "other":
-        lib.llapis_set_tuning(4, 0 if T > 1 else 1)
+    lib.llapis_set_tuning(3, down)
     try:
         for name, dec in (("generic", 0), ("decode", 1)):
             lib.llapis_set_tuning(0, dec)
@@ -308,7 +307,7 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, do
             outs[name] = res
     finally:
         lib.llapis_set_tuning(0, 1)
-        lib.llapis_set_tuning(4, -1)
+        lib.llapis_set_tuning(3, -1)
     for (o, i, w), (og, ig, wg) in zip(outs["decode"], outs["generic"]):
         assert np.array_equal(i, ig)
         assert np.allclose(w, wg, rtol=1e-6, atol=0)
