@@ -397,7 +397,9 @@ int32_t llapis_device_memory_mib(long long * free_mib, long long * total_mib);
  * (default 1; 0 sends those calls down the generic path), key 2 = the MFMA
  * prefill path for > 4 tokens (default 1), key 3 = log2 of the output rows
  * per workgroup of the decode path's down kernel (0..5; -1, the default,
- * picks it from d_model), key 6 = the one-kernel fires of
+ * picks it from d_model), key 4 = the decode path's down kernel for 2-4
+ * tokens (1, the default: by expert group with a combine kernel after it;
+ * 0: over every group with the combine in it), key 6 = the one-kernel fires of
  * llapis_moe_dual_compute and of llapis_mul_mat_id (default 1; 0 runs every
  * fire through the island's generic pipeline and every mul_mat_id through
  * the generic matvec).  Other keys are ignored. */

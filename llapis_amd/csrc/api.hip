@@ -46,7 +46,7 @@ int32_t fail(const std::string & msg) {
         if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_fused_fire{1};
+std::atomic<int> g_decode_path{1}, g_prefill{1}, g_dn_rows_log2{-1}, g_dn_by_group{-1}, g_fused_fire{1};
 
 // the largest LDS allocation of one workgroup on the current device (cached)
 int max_lds_per_wg() {
@@ -702,6 +702,7 @@ void llapis_set_tuning(int32_t key, int32_t value) {
     if (key == 0) g_decode_path = value != 0;
     if (key == 2) g_prefill = value != 0;
     if (key == 3) g_dn_rows_log2 = value >= 0 && value <= 5 ? value : -1;
+    if (key == 4) g_dn_by_group = value == 0 || value == 1 ? value : -1;
     if (key == 6) g_fused_fire = value != 0;
 }
 
@@ -763,6 +764,7 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, const float 
         p.xq = base + dw.xq; p.xq_stride = dw.xq_stride;
         p.yq = base + dw.yq; p.yq_stride = dw.yq_stride;
         p.ydn = reinterpret_cast<float *>(base + dw.ydn);
+        p.dn_by_group = g_dn_by_group.load() >= 0 ? g_dn_by_group.load() : 1;
         p.out = out;
         const int rbg = (int)std::max(rbytes(L->hot_gu_type, L->d_model), rbytes(L->cold_gu_type, L->d_model));
         p.w_lds_gu = dec_gu_half_bytes(T, rbg);
@@ -775,13 +777,14 @@ int32_t llapis_moe_ffn(const llapis_moe_layer * L, const float * x, const float 
         const int lds_max = max_lds_per_wg();
         // the LDS of the down kernel that will run: every pair's column at one
         // token, the group's members' columns by group
-        const int dn_lds = T == 1 ? dec_lds_down(p) : std::min(T, DEC_MAXT) * dec_act_bytes(L->n_ff);
+        const int dn_lds = T == 1 || !p.dn_by_group ? dec_lds_down(p) : std::min(T, DEC_MAXT) * dec_act_bytes(L->n_ff);
         if (dn_lds + 16 * 1024 <= lds_max && dec_lds_gate_up(p, L->hot_gu_type, L->cold_gu_type) + 16 * 1024 <= lds_max) {
             const int pc = prof_slot();
             const int src = L->gelu_mode == LLAPIS_GELU_TANH ? dev::SRC_GEGLU_TANH : dev::SRC_GEGLU_TABLE;
+            const bool comb = T > 1 && p.dn_by_group;
             hipEvent_t ev[8] = {prof_ev(pc, 0, 0), prof_ev(pc, 0, 1), prof_ev(pc, 2, 0), prof_ev(pc, 2, 1),
                                 prof_ev(pc, 3, 0), prof_ev(pc, 3, 1),
-                                T > 1 ? prof_ev(pc, 4, 0) : nullptr, T > 1 ? prof_ev(pc, 4, 1) : nullptr};
+                                comb ? prof_ev(pc, 4, 0) : nullptr, comb ? prof_ev(pc, 4, 1) : nullptr};
             LL_TRY(launch_decode(p, L->hot_gu_type, L->cold_gu_type, L->hot_dn_type, L->cold_dn_type, L->act_mode,
                                  src, s, pc >= 0 ? ev : nullptr));
             return 0;

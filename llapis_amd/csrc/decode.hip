@@ -1555,7 +1555,8 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
     }
     {
         // one token: the kernel over every group (its 8 columns are 9 KB); more:
-        // by group (each workgroup reads its members' columns only) + combine
+        // by group (each workgroup reads its members' columns only) + combine,
+        // or over every group (every pair's column in each workgroup)
         const int lds = dec_lds_down(p);
         const int rows = 1 << p.dn_rows_log2;
         const dim3 grid((p.d_model + rows - 1) / rows);
@@ -1564,6 +1565,7 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
 #define LL_DN(A, B, M) \
         if (hdn == A && cdn == B && am == M) { \
             if (p.T == 1) launch_timed(k_dec_down<A, B, M, 1>, grid, lds, s, e[4], e[5], p); \
+            else if (!p.dn_by_group) launch_timed(k_dec_down<A, B, M, DEC_MAXT>, grid, lds, s, e[4], e[5], p); \
             else launch_timed(k_dec_down_grp<A, B, M, DEC_MAXT, DN_GRP_NPS>, ggrid, glds, s, e[4], e[5], p); \
         } else
 #define LL_DN2(A, B) LL_DN(A, B, AM_CPU) LL_DN(A, B, AM_Q8_1)
@@ -1571,7 +1573,8 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         return hipErrorInvalidValue;
 #undef LL_DN2
 #undef LL_DN
-        if (p.T > 1) launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
+        if (p.T > 1 && p.dn_by_group)
+            launch_timed(k_dec_combine, dim3((p.T * p.d_model + WG - 1) / WG), 0, s, e[6], e[7], p);
     }
     return hipGetLastError();
 }

@@ -84,6 +84,7 @@ struct DecParams {
     uint8_t * xq; int64_t xq_stride;     // quantised tokens
     uint8_t * yq; int64_t yq_stride;     // [P] quantised down activations (GEGLU outputs in q8_0 / q8_1)
     float * ydn;                // [P][d_model] scaled down rows per routed pair (down by group, T > 1)
+    int dn_by_group;            // T > 1: 1 the down kernel by group + k_dec_combine, 0 the kernel over every group
     float * out;                // [T][d_model]
     int w_lds_gu;               // LDS bytes of one half of a gate_up pass (dec_gu_half_bytes)
     int dn_rows_log2;           // log2 of the output rows per down workgroup (<= DEC_DN_MAXR)

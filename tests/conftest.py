@@ -45,5 +45,5 @@ def _library_defaults(request):
     import llapis_amd as la
     lib = la.lib()
     lib.llapis_set_modes(la.ACT_CPU, la.GELU_TABLE)
-    for key, value in ((0, 1), (2, 1), (3, -1), (6, 1)):
+    for key, value in ((0, 1), (2, 1), (3, -1), (4, -1), (6, 1)):
         lib.llapis_set_tuning(key, value)

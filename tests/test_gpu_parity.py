@@ -280,14 +280,15 @@ def test_island_fires_match_layer(gpu, oracle, fused, act_mode, T):
 
 @pytest.mark.parametrize("T,n_hot", [(1, 0), (1, 16), (2, 7), (4, 9), (4, 0)])
 @pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
-@pytest.mark.parametrize("down", [-1, 1, 5])
+@pytest.mark.parametrize("down", ["default", "rows2", "rows32", "every"])
 def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, down):
     """The decode path (expert groups, GEGLU and the down activation's q8
-    quantisation in the gate_up epilogue, the down kernel over every group
-    with the combine in its workgroup) against the generic per-pair path,
-    over several calls on one workspace.  `down` is log2 of the down
-    kernel's rows per workgroup (tuning key 3; -1: the default, 1: 2 rows,
-    5: 32 rows)."""
+    quantisation in the gate_up epilogue; one token: the down kernel over
+    every group with the combine in its workgroup; more: by group, then the
+    combine kernel) against the generic per-pair path, over several calls on
+    one workspace.  rows2 / rows32: 2 or 32 rows per workgroup of the kernel
+    over every group (tuning key 3); every: that kernel for more than one
+    token too (tuning key 4)."""
     torch = torch_mod()
     say(f"decode vs generic T={T} hot={n_hot} act={act_mode} down={down}")
     spec = FULL16
@@ -295,7 +296,8 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, do
     dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
     lib = la.lib()
     outs = {}
-    lib.llapis_set_tuning(3, down)
+    lib.llapis_set_tuning(3, {"rows2": 1, "rows32": 5}.get(down, -1))
+    lib.llapis_set_tuning(4, 0 if down == "every" else -1)
     try:
         for name, dec in (("generic", 0), ("decode", 1)):
             lib.llapis_set_tuning(0, dec)
@@ -308,6 +310,7 @@ def test_decode_path_matches_generic_path(gpu, T, n_hot, act_mode, gelu_mode, do
     finally:
         lib.llapis_set_tuning(0, 1)
         lib.llapis_set_tuning(3, -1)
+        lib.llapis_set_tuning(4, -1)
     for (o, i, w), (og, ig, wg) in zip(outs["decode"], outs["generic"]):
         assert np.array_equal(i, ig)
         assert np.allclose(w, wg, rtol=1e-6, atol=0)
