@@ -3,17 +3,19 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Workload (the headline decode configuration): one MoE FFN layer, d_model 2816,
-128 experts, top-8, n_ff 704, GeGLU; all 128 experts cold (IQ2_S gate_up,
-IQ4_NL down), one token per step.  A step is router -> top-8 -> gate_up ->
-GEGLU -> down -> combine for that token, launched as a captured HIP graph.
-Inputs are resident in HBM before timing starts.  Each step reads a different
-layer replica (and token) so the bytes touched per cycle exceed the 256 MB
-MALL: the HBM rate is HBM, not cache.
+Workload (the headline: decode on the mixed-precision weights): one MoE FFN
+layer, d_model 2816, 128 experts, top-8, n_ff 704, GeGLU; K=57 experts hot
+(Q4_K gate_up, Q5_0 down), chosen from a Zipf(1.1) routing prior, the other 71
+cold (IQ2_S gate_up, IQ4_NL down); the router bias puts ~85 % of the top-8
+picks on the hot set; 4 tokens per step (a depth-3 speculative verify).  A
+step is router -> top-8 -> gate_up -> GEGLU -> down -> combine for those
+tokens, launched as a captured HIP graph.  Inputs are resident in HBM before
+timing starts.  Each step reads a different layer replica (and tokens) so the
+bytes touched per cycle exceed the 256 MB MALL: the HBM rate is HBM, not cache.
 
-Also reported (extra): all-Q4_K decode, the dual-precision K=57 4-token
-decode, the promotion path (expert copies into hot slots, alone and beside
-the decode), and the dual-precision 512-token prefill (grouped MFMA GEMMs; int8
+Also reported (extra): all-IQ2_S and all-Q4_K decode of one token, the
+promotion path (expert copies into hot slots, alone and beside the decode),
+and the dual-precision 512-token prefill (grouped MFMA GEMMs; int8
 TOP/s = 2 x 11 894 784 ops per routed pair, against the int8 peak and against
 the attainable min(peak, arithmetic intensity x HBM)), each with its own
 roofline; the dominant kernel's duration is timed live with HIP events on the
@@ -37,6 +39,13 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E, GB/s
 OPS_PER_PAIR = 2 * (2816 * 1408 + 704 * 2816)   # int8 multiply-adds x 2 per routed pair (gate_up + down)
 INT8_PEAK_TOPS = 5000.0                # MI355X dense int8 MFMA, TOP/s
+HEAD_TOKENS = {"dual": 4, "iq2s": 1, "q4k": 1, "prefill": 512, "prefill_q81": 512, "q4stream": 512}
+HEAD_FORMATS = {
+    "dual": "K=57 hot: Q4_K gate_up / Q5_0 down; 71 cold: IQ2_S gate_up / IQ4_NL down; ~85 % of picks hot",
+    "iq2s": "IQ2_S gate_up / IQ4_NL down", "q4k": "Q4_K gate_up / Q5_0 down",
+    "prefill": "dual K=57, q8_K/q8_0 activations", "prefill_q81": "dual K=57, q8_1 activations",
+    "q4stream": "every expert Q4_K gate_up / Q5_0 down"}
+DOWN_BY_GROUP = True                   # 2-4 token decode: down per expert group + combine (tuning key 4)
 METRIC = "MoE-layer decode tok/s + HBM TB/s (% peak); 512-tok prefill int8 TOPS (% peak)"
 
 
@@ -256,8 +265,9 @@ def run_config(la, torch, name, host_layer, T, steps, warmup, dev, seed=1234, ac
         del wlc
     sb = stage_bytes(sp, n_hot, n_cold, T, pairs)
     dom = max(("gate_up", "down"), key=lambda k: st[k])
-    kernel = ({"gate_up": "k_dec_gate_up", "down": "k_dec_down"} if T <= 4 else
-              {"gate_up": "k_pf_gate_up", "down": "k_pf_down"})[dom]
+    dec_down = "k_dec_down" if T == 1 or not DOWN_BY_GROUP else "k_dec_down_grp"
+    kernel = ({"gate_up": "k_dec_gate_up", "down": dec_down} if T <= 4 else
+              {"gate_up": "k_pf_gate_up" if act == 0 else "k_pf_gate_up_q1", "down": "k_pf_down"})[dom]
     res = {
         "tok_per_s": T * 1e3 / ms_graph,
         "ms_per_step": ms_graph,
@@ -841,9 +851,12 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 20}))
         return
+    global DOWN_BY_GROUP
     for kv in filter(None, args.tune.split(",")):
         k, v = kv.split("=")
         la.lib().llapis_set_tuning(int(k), int(v))
+        if int(k) == 4:
+            DOWN_BY_GROUP = int(v) != 0
     cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
     spec = la.LayerSpec()
     t0 = time.time()
@@ -909,11 +922,18 @@ def main():
     if "stackdyn" in cfgs:
         results["stack_dynamic"] = run_stack_dynamic(la, torch, full, spec, dev, copy_wgs=args.engine_wgs)
 
-    head = results.get("iq2s") or next(iter(v for v in results.values() if "dominant_gbs" in v), None)
-    if head is None:
+    # the headline: the mixed-precision 4-token decode; the single-format
+    # decodes and the prefill stay in extra
+    head_name = next((n for n in ("dual", "iq2s", "q4k") if n in results), None)
+    if head_name is None:
+        head_name = next((n for n, v in results.items() if isinstance(v, dict) and "dominant_gbs" in v), None)
+    if head_name is None:
         print(json.dumps({"extra": results}))
         return
-    workload = "decode_all_iq2s_1tok" if "iq2s" in results else None
+    head = results[head_name]
+    workload = {"dual": "decode_dual_k57_4tok", "iq2s": "decode_all_iq2s_1tok", "q4k": "decode_all_q4k_1tok",
+                "prefill": "prefill_dual_k57_512tok", "prefill_q81": "prefill_dual_k57_512tok_q8_1",
+                "q4stream": "prefill_q4stream_512tok"}.get(head_name)
     roof = {"bound": "hbm", "achieved": head["dominant_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": head["dominant_gbs"] / HBM_PEAK_GBS,
             "traffic": measured_traffic(workload, head["dominant_kernel"]),
@@ -925,11 +945,13 @@ def main():
     log(f"copy of the same {head['dominant_bytes'] / 1e6:.1f} MB per launch: {ceil:.0f} GB/s "
         f"({100 * ceil / HBM_PEAK_GBS:.0f} % of peak); dominant kernel at {100 * head['dominant_gbs'] / ceil:.0f} % of it")
     cpu = None
-    if not args.no_cpu_baseline and "iq2s" in cfgs:
+    if not args.no_cpu_baseline and head_name in ("dual", "iq2s", "q4k"):
         try:
-            cold_only = copy.copy(full)
-            cold_only.residency = la.Residency.from_hot(spec.n_expert, [])
-            layers = {"iq2s": (cold_only, 1, "cold")}
+            layers = {}
+            if "iq2s" in results:
+                cold_only = copy.copy(full)
+                cold_only.residency = la.Residency.from_hot(spec.n_expert, [])
+                layers["iq2s"] = (cold_only, 1, "cold")
             if "q4k" in results:
                 layers["q4k"] = (full, 1, "hot")
             if "dual" in results:
@@ -942,12 +964,16 @@ def main():
                 if g:
                     c["gpu_over_cpu"] = g["tok_per_s"] / c["tok_per_s"]
                     c["effective_gbs"] = g["algo_bytes_step"] / (c["ms_per_step"] * 1e-3) / 1e9
-            h = cb["configs"]["iq2s"]
+            h = cb["configs"][head_name]
+            what = {"dual": "4 tokens on the dual K=57 layer; the reference's ggml CPU graph for the routing "
+                            "and the hot pairs and its CPU cold executor for the cold pairs",
+                    "iq2s": "1 token on the all-IQ2_S layer; the reference's ggml CPU graph",
+                    "q4k": "1 token on the all-Q4_K layer; the reference's ggml CPU graph"}[head_name]
             cpu = {"value": h["tok_per_s"], "unit": "tok/s", "cores": cb["threads"], "kind": "reference",
-                   "sample": f"{h['steps']} decode steps of 1 token on the all-IQ2_S layer, {h['seconds']:.1f} s, "
-                             f"weights rotated over {h['replicas']} replicas of {h['replica_mb']:.0f} MB; the "
-                             f"reference's ggml CPU graph built from its sources for {cb['isa']} "
-                             f"({cb['cpu_model']}, {cb['logical_cpus']} logical CPUs, {cb['threads']} threads)",
+                   "sample": f"{h['steps']} decode steps of {what}, {h['seconds']:.1f} s, weights rotated over "
+                             f"{h['replicas']} replicas of {h['replica_mb']:.0f} MB; built from the reference's "
+                             f"sources for {cb['isa']} ({cb['cpu_model']}, {cb['logical_cpus']} logical CPUs, "
+                             f"{cb['threads']} threads)",
                    "cpu_model": cb["cpu_model"], "isa": cb["isa"], "configs": cb["configs"]}
             log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
         except Exception as e:  # the checker library may be absent; say so
@@ -965,9 +991,11 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": "moe_layer_decode_all_iq2s_1tok", "d_model": spec.d_model, "n_ff": spec.n_ff,
-                   "n_expert": spec.n_expert, "top_k": spec.top_k, "tokens_per_step": 1,
-                   "formats": "IQ2_S gate_up / IQ4_NL down", "replicas": head["replicas"],
+        "config": {"workload": "moe_layer_" + (workload or head_name), "d_model": spec.d_model,
+                   "n_ff": spec.n_ff, "n_expert": spec.n_expert, "top_k": spec.top_k,
+                   "tokens_per_step": HEAD_TOKENS.get(head_name), "formats": HEAD_FORMATS.get(head_name),
+                   "replicas": head["replicas"], "distinct_hot": head["distinct_hot"],
+                   "distinct_cold": head["distinct_cold"],
                    "hbm_gbs_step": head["hbm_gbs_step"], "hbm_frac_step": head["hbm_frac_step"]},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -583,6 +583,24 @@ void orc_router(const float * x, int64_t T, const float * w_r, const float * bia
 
 /* ---------------------------------------------------------------- layer */
 
+static uint64_t g_jitter_seed;
+
+void orc_set_sum_jitter(uint64_t seed) { g_jitter_seed = seed; }
+
+/* splitmix64 finaliser of the seed and a position */
+static uint64_t jitter_hash(uint64_t a, uint64_t b) {
+    uint64_t z = a * 0x9E3779B97F4A7C15ull + b + 0x632BE59BD9B4E5ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static void jitter(float * v, int64_t n, uint64_t where) {
+    if (!g_jitter_seed) return;
+    for (int64_t i = 0; i < n; ++i)
+        v[i] = nextafterf(v[i], (jitter_hash(g_jitter_seed ^ where, (uint64_t)i) & 1) ? INFINITY : -INFINITY);
+}
+
 static int pair_slot(const orc_layer * L, int32_t e) {
     if (e < 0 || e >= L->n_expert || !L->exp_slot) return -1;
     const int s = L->exp_slot[e];
@@ -614,9 +632,11 @@ void orc_moe_experts(const orc_layer * L, const float * x, int64_t T,
             const char * wdn = (const char *)(s >= 0 ? L->hot_dn : L->cold_dn) +
                                (size_t)idx * D * orc_row_size(dnt, F);
             orc_matvec(gut, act_mode, wgu, 2 * F, D, x + t * D, gu);
+            jitter(gu, 2 * F, (uint64_t)(t * K + k) * 2);
             orc_geglu(gu, gu + F, a, F, gelu_mode);
             float * yk = y + k * D;
             orc_matvec(dnt, act_mode, wdn, D, F, a, yk);
+            jitter(yk, D, (uint64_t)(t * K + k) * 2 + 1);
             const float * sc = s >= 0 ? L->s_hot : L->s_cold;
             if (sc) {
                 const float f = sc[idx];

@@ -116,6 +116,13 @@ void orc_moe_experts(const orc_layer * L, const float * x, int64_t T,
                      const int32_t * ids, const float * w, int act_mode, int gelu_mode,
                      float * out, float * y_pairs);
 
+/* A control for chained-layer tests, not part of the restatement: with a
+ * nonzero seed, orc_moe_experts moves every gate_up and down matvec output
+ * one ulp up or down (a seeded coin per token, pair and row) before it is
+ * used -- the last-bit differences another fp32 summation order makes.
+ * 0 (the default) turns it off. */
+void orc_set_sum_jitter(uint64_t seed);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,8 @@ class Oracle:
         lib.orc_geglu.argtypes = [vp, vp, vp, i64, i32]
         lib.orc_router.argtypes = [vp, i64, vp, vp, i64, i64, i64, vp, vp, vp]
         lib.orc_moe_experts.argtypes = [vp, vp, i64, vp, vp, i32, i32, vp, vp]
+        lib.orc_set_sum_jitter.argtypes = [C.c_uint64]
+        lib.orc_set_sum_jitter.restype = None
         lib.orc_fp32_to_fp16.argtypes = [C.c_float]
         lib.orc_fp32_to_fp16.restype = C.c_uint16
         lib.orc_fp16_to_fp32.argtypes = [C.c_uint16]
@@ -92,6 +94,11 @@ class Oracle:
         b = _f32(bias) if bias is not None else None
         self.lib.orc_router(_p(x), T, _p(w_r), _p(b), d, E, top_k, _p(ids), _p(w), _p(probs))
         return ids, w, probs
+
+    def set_sum_jitter(self, seed):
+        """A control for chained-layer tests (0: off): every gate_up and down
+        matvec output moved one ulp up or down by a seeded coin."""
+        self.lib.orc_set_sum_jitter(int(seed))
 
     def moe_experts(self, L, x, ids, w, act_mode=ACT_CPU, gelu_mode=GELU_TABLE):
         """L: a LayerData-like object (see tests/helpers.py) with numpy fields."""
