@@ -497,17 +497,24 @@ __device__ __forceinline__ void rows_dot(const uint8_t * sm, int wb, int tier, i
 
 constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
 
-// A gate_up workgroup: 16 waves take the 64 rows of an item (32 gate, 32 up)
-// at once, one row per 16 lanes.
-constexpr int GU_NW = 16;
-constexpr int GU_NT = 64 * GU_NW;
+// A one-token gate_up workgroup: 16 waves take the 64 rows of an item (32
+// gate, 32 up) at once, one row per 16 lanes, and the device holds one per
+// CU.  With 2-4 tokens a workgroup is 8 waves and takes an item in two
+// steps, its 32 gate rows and then its 32 up rows (one row per 16 lanes), so
+// its LDS holds half an item and a CU holds two workgroups: one's loads are
+// in flight while the other dots.
+template <int MT> constexpr int gu_nw() { return MT == 1 ? 16 : 8; }
+template <int MT> constexpr int gu_nt() { return 64 * gu_nw<MT>(); }
+template <int MT> constexpr int gu_halves() { return MT == 1 ? 2 : 1; }   // halves staged at once
 constexpr int GU_HR = DEC_GU_BLK;             // rows of each half (gate, up) of an item
-// Loads per thread of one half of an item: 32 rows over 1024 threads (Q4_K:
-// 99 chunks of 16 bytes per pair of rows at d_model 2816 -> 4; IQ2_S: at most
-// 57 -> 2, its other two repeat a chunk).  One layout for either format, so
-// the registers stay registers whichever tier an item has.  Chunks past a
-// half's share are loaded when the half is stored.
-constexpr int GU_LH = 4;
+// Loads per thread of one half of an item: 32 rows (Q4_K: 99 chunks of 16
+// bytes per pair of rows at d_model 2816; IQ2_S: at most 57) over 1024
+// threads -> 4, over 512 -> 7.  One layout for either format, so the
+// registers stay registers whichever tier an item has.  Chunks past a half's
+// share are loaded when the half is stored.
+template <int MT> constexpr int gu_lh() { return MT == 1 ? 4 : 7; }
+template <int MT> constexpr int gu_buf() { return gu_halves<MT>() * gu_lh<MT>(); }
+
 
 // The dots of the staged row at `wb` (one row per 16 lanes) against the
 // members' columns av[c], c < n_mem <= MT; the row sums are complete in lane
@@ -549,54 +556,77 @@ __device__ __forceinline__ Span gu_span(const DecParams & p, const GroupInfo & g
                      p.cold_gu, p.cold_gu_stride, p.logits);
 }
 
-// the item's loads, unconditional
-template <int HT, int CT>
-__device__ __forceinline__ void gu_issue(u32x4 (&buf)[2 * GU_LH], const DecParams & p, const GroupInfo & gi, int j) {
+// the loads of an item's halves h0 .. h0 + gu_halves - 1 (0: gate rows,
+// 1: up rows), unconditional
+template <int HT, int CT, int MT>
+__device__ __forceinline__ void gu_issue(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi,
+                                         int j, int h0) {
+    constexpr int LH = gu_lh<MT>(), NT = gu_nt<MT>();
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const Span sp = gu_span<HT, CT>(p, gi, j, h);
+    for (int h = 0; h < gu_halves<MT>(); ++h) {
+        const Span sp = gu_span<HT, CT>(p, gi, j, h0 + h);
 #pragma unroll
-        for (int k = 0; k < GU_LH; ++k) buf[h * GU_LH + k] = sp.src[min((int)threadIdx.x + k * GU_NT, sp.nch - 1)];
+        for (int k = 0; k < LH; ++k) buf[h * LH + k] = sp.src[min((int)threadIdx.x + k * NT, sp.nch - 1)];
     }
 }
 
-// One gate_up item, its loads issued by gu_issue: gate rows [32 j, 32 j + 32)
-// and the up rows n_ff + 32 j .. paired with them, of group gi's expert
-// (weight type WT), staged through LDS, one row per 16 lanes.  Once the rows
-// are in LDS, the loads of the workgroup's next item (nx, nj; nx.n_mem == 0:
-// none) go into the registers just freed, in flight during this item's dots.
-// GEGLU pairs gate row i with up row i for every member, and each member's
-// 32 values are quantised (q8_0 / q8_1, block j of the pair's down
-// activation) into the pair's down column.
-template <int WT, int HT, int CT, int AM, int MT, int GSRC>
-__device__ __forceinline__ void gu_run(u32x4 (&buf)[2 * GU_LH], const DecParams & p, const GroupInfo & gi, int j,
-                                       uint8_t * smem, const ActView * av,
-                                       int grid_off, float (*s_y)[MT], float (*s_act)[DEC_GU_BLK]) {
-    constexpr int LH = GU_LH;
-    const int T = p.T, K = p.top_k, F = p.n_ff;
-    const int row = threadIdx.x >> 4, hr = row / GU_HR, r = row - hr * GU_HR;     // hr 0: gate rows, 1: up rows
-    const bool live = gi.tier < 2 && gi.n_mem > 0;
-    const Span s0 = gu_span<HT, CT>(p, gi, j, 0), s1 = gu_span<HT, CT>(p, gi, j, 1);
-    __syncthreads();                                      // the previous item is done with LDS
+// The staged halves of an item into LDS (half h at smem + h w_lds_gu), once
+// every wave is done with the previous ones
+template <int HT, int CT, int MT>
+__device__ __forceinline__ void gu_store(const u32x4 (&buf)[gu_buf<MT>()], const DecParams & p,
+                                         const GroupInfo & gi, int j, int h0, uint8_t * smem) {
+    constexpr int LH = gu_lh<MT>(), NT = gu_nt<MT>();
+    __syncthreads();
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const Span & sp = h ? s1 : s0;
+    for (int h = 0; h < gu_halves<MT>(); ++h) {
+        const Span sp = gu_span<HT, CT>(p, gi, j, h0 + h);
         uint8_t * dst = smem + h * p.w_lds_gu;
 #pragma unroll
         for (int k = 0; k < LH; ++k) {
-            const int i = threadIdx.x + k * GU_NT;
+            const int i = threadIdx.x + k * NT;
             if (i < sp.nch) reinterpret_cast<u32x4 *>(dst)[i] = buf[h * LH + k];
         }
-        for (int i = threadIdx.x + LH * GU_NT; i < sp.nch; i += GU_NT) reinterpret_cast<u32x4 *>(dst)[i] = sp.src[i];
+        for (int i = threadIdx.x + LH * NT; i < sp.nch; i += NT) reinterpret_cast<u32x4 *>(dst)[i] = sp.src[i];
     }
     __syncthreads();
-    const int wb = hr ? p.w_lds_gu + s1.off + r * s1.rb : s0.off + r * s0.rb;
+}
+
+// The dots of the staged rows: 16 lanes a row, row threadIdx / 16 of the
+// staged halves (h0 + row / 32: gate or up) into s_y[32 (h0 + row / 32) +
+// row % 32]
+template <int WT, int HT, int CT, int AM, int MT>
+__device__ __forceinline__ void gu_dots(const DecParams & p, const GroupInfo & gi, int j, int h0,
+                                        const uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT]) {
+    const int row = threadIdx.x >> 4, hr = row / GU_HR, r = row - hr * GU_HR;
+    const bool live = gi.tier < 2 && gi.n_mem > 0;
+    const Span sp = gu_span<HT, CT>(p, gi, j, h0 + hr);
+    const int wb = hr * p.w_lds_gu + sp.off + r * sp.rb;
     float acc[MT];
     item_dot<WT, AM, MT>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
     if ((threadIdx.x & 15) == 0) {
 #pragma unroll
-        for (int c = 0; c < MT; ++c) s_y[row][c] = acc[c];
+        for (int c = 0; c < MT; ++c) s_y[(h0 + hr) * GU_HR + r][c] = acc[c];
     }
+}
+
+// One step of a gate_up item (group gi, block j: gate rows [32 j, 32 j + 32)
+// and the up rows n_ff + 32 j .. paired with them, of group gi's expert,
+// weight type WT), whose loads are in `buf`: the staged halves h .. h +
+// gu_halves - 1 into LDS, one row per 16 lanes, and their dots.  One token:
+// both halves in one step.  More: the gate rows (h 0), then the up rows (h 1)
+// in the next step (the other workgroup on the CU keeps loads in flight
+// meanwhile).  After the up rows, GEGLU pairs gate row i with up row i for
+// every member, and each member's 32 values are quantised (q8_0 / q8_1, block
+// j of the pair's down activation) into the pair's down column.
+template <int WT, int HT, int CT, int AM, int MT, int GSRC>
+__device__ __forceinline__ void gu_run(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi, int j,
+                                       int h, uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT],
+                                       float (*s_act)[DEC_GU_BLK]) {
+    const int T = p.T, K = p.top_k, F = p.n_ff;
+    const bool live = gi.tier < 2 && gi.n_mem > 0;
+    gu_store<HT, CT, MT>(buf, p, gi, j, h, smem);
+    gu_dots<WT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
+    if (h + gu_halves<MT>() < 2) return;                  // the up rows are still to come
     __syncthreads();
     // GEGLU of gate row 32 j + i with its up row, member c
     if ((int)threadIdx.x < GU_HR * MT) {
@@ -634,10 +664,13 @@ struct GuScratch {
 // most what the device holds resident, so every workgroup runs at once).
 // MT: members a group can have (1 or DEC_MAXT).
 template <int HT, int CT, int AM, int MT, int GSRC>
-__global__ __launch_bounds__(GU_NT) void k_dec_gate_up(const DecParams p) {
+__global__ __launch_bounds__(gu_nt<MT>()) __attribute__((amdgpu_waves_per_eu(4)))
+void k_dec_gate_up(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int GU_NT = gu_nt<MT>();
     static_assert(Fmt<HT>::LPR == 16 && Fmt<CT>::LPR == 16 && k256<HT>() && k256<CT>(), "gate_up formats");
-    static_assert(GU_NW >= DEC_MAXT && GU_NT >= 256, "a wave per token and a thread per expert");
+    static_assert(gu_nw<MT>() >= DEC_MAXT && GU_NT >= 256, "a wave per token and a thread per expert");
+    static_assert(GU_NT / 16 == gu_halves<MT>() * GU_HR, "one row per 16 lanes of the staged halves");
     constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
     constexpr int COLL = MT == 1 ? 1 : 2;                 // quantised column chunks per thread issued at once
     constexpr int TABL = (TAB_CHUNKS + GU_NT - 1) / GU_NT;   // codebook chunks per thread
@@ -720,11 +753,11 @@ __global__ __launch_bounds__(GU_NT) void k_dec_gate_up(const DecParams p) {
         for (int k = 0; k < TABL; ++k)
             tab[k] = reinterpret_cast<const u32x4 *>(&c_iq2s_tab_dec)[min((int)threadIdx.x + k * GU_NT, TAB_CHUNKS - 1)];
     }
-    int it = blockIdx.x, j;
+    int it = blockIdx.x, j, h = 0;
     GroupInfo gi = item(it, &j);
-    u32x4 buf[2 * GU_LH];
-    gu_issue<HT, CT>(buf, p, gi, j);
-    const int a0 = 2 * p.w_lds_gu;
+    u32x4 buf[gu_buf<MT>()];
+    gu_issue<HT, CT, MT>(buf, p, gi, j, 0);
+    const int a0 = gu_halves<MT>() * p.w_lds_gu;
 #pragma unroll
     for (int k = 0; k < COLL; ++k) {
         const int i = threadIdx.x + k * GU_NT;
@@ -756,12 +789,17 @@ __global__ __launch_bounds__(GU_NT) void k_dec_gate_up(const DecParams p) {
         ActView av[MT];
 #pragma unroll
         for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + max(0, min(member(gi, c) / K, T - 1)) * abytes, &av[c]);
-        if (gi.tier == 0) gu_run<HT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, smem, av, grid_off, s_y, s_act);
-        else gu_run<CT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, smem, av, grid_off, s_y, s_act);
-        it += gridDim.x;
-        if (it >= n_items) break;
-        gi = item(it, &j);
-        gu_issue<HT, CT>(buf, p, gi, j);
+        if (gi.tier == 0) gu_run<HT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, h, smem, av, grid_off, s_y, s_act);
+        else gu_run<CT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, h, smem, av, grid_off, s_y, s_act);
+        if (h + gu_halves<MT>() < 2) {
+            h += gu_halves<MT>();
+        } else {
+            it += gridDim.x;
+            if (it >= n_items) break;
+            gi = item(it, &j);
+            h = 0;
+        }
+        gu_issue<HT, CT, MT>(buf, p, gi, j, h);
     }
 }
 
@@ -1463,16 +1501,18 @@ int dec_act_bytes(int n) {
 // LDS bytes of one half of a gate_up item (32 rows of the longer gate_up
 // row, plus one dword a funnel read may touch past the end), at least half
 // the routing's scratch, which the two halves hold before the first item
-int dec_gu_half_bytes(int, int row_bytes) {
-    return std::max(align16i(GU_HR * row_bytes + 32), align16i((int)sizeof(GuScratch) / 2 + 16));
+int dec_gu_half_bytes(int T, int row_bytes) {
+    const int halves = T == 1 ? gu_halves<1>() : gu_halves<DEC_MAXT>();
+    return std::max(align16i(GU_HR * row_bytes + 32), align16i((int)sizeof(GuScratch) / halves + 16));
 }
 
-// dynamic LDS of B: the two halves of an item, one activation column per
-// token of the call (a group has at most one member per token), the IQ2_S
-// codebook when used
+// dynamic LDS of B: the halves of an item staged at once (both with one
+// token, one with more), one activation column per token of the call (a
+// group has at most one member per token), the IQ2_S codebook when used
 int dec_lds_gate_up(const DecParams & p, int ht, int ct) {
     const bool iq2 = ht == T_IQ2_S || ct == T_IQ2_S;
-    return align16i(2 * p.w_lds_gu + std::min(p.T, DEC_MAXT) * dec_act_bytes(p.d_model)) +
+    const int halves = p.T == 1 ? gu_halves<1>() : gu_halves<DEC_MAXT>();
+    return align16i(halves * p.w_lds_gu + std::min(p.T, DEC_MAXT) * dec_act_bytes(p.d_model)) +
            (iq2 ? (int)sizeof(Iq2sTables) : 0);
 }
 
@@ -1541,8 +1581,8 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         };
 #define LL_GU(A, B, M, G) \
         if (hgu == A && cgu == B && am == M && gelu == G) { \
-            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, G>, GU_NT); \
-            else go(k_dec_gate_up<A, B, M, DEC_MAXT, G>, GU_NT); \
+            if (p.T == 1) go(k_dec_gate_up<A, B, M, 1, G>, gu_nt<1>()); \
+            else go(k_dec_gate_up<A, B, M, DEC_MAXT, G>, gu_nt<DEC_MAXT>()); \
         } else
 #define LL_GU2(A, B) LL_GU(A, B, AM_CPU, SRC_GEGLU_TABLE) LL_GU(A, B, AM_CPU, SRC_GEGLU_TANH) \
                      LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TABLE) LL_GU(A, B, AM_Q8_1, SRC_GEGLU_TANH)
