@@ -605,8 +605,13 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
     const _Float16 mo = q == 0 ? (_Float16)(-32768.0f) : q == 1 ? (_Float16)(-1024.0f) : (_Float16)0.0f;
     const h2 mn_mul = h2{mm, mm}, mn_off = h2{mo, mo};
 
-    // one super-block: expand this lane's rows, start the next super-block's
-    // copies and rows, then every 16-token tile against both row tiles
+    // One super-block, K-slice major: the rows' per-super-block words (scales,
+    // mins, IQ2_S index and sign words) first, then the next super-block's
+    // copies and rows, then for each K-slice st (64 values) the expansion of
+    // both row tiles' slice and the MFMAs of every 16-token tile against it,
+    // into int32 accumulators that live across the slices -- so one slice's
+    // expansion (VALU) overlaps the previous slice's MFMAs -- and last the
+    // per-output scaling of every tile.
     auto step = [&](int s, const uint8_t * xb, const _Float16 * mbb, const float * d8b, const uint8_t * wb,
                     uint8_t * xn, _Float16 * mbn, float * d8n, uint8_t * wn) {
         // this wave's copies and rows of super-block s have landed; after the
@@ -614,15 +619,16 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 
-        // ---- B operands of this wave's two 16-row tiles: 4 K-steps of 64,
-        // lane (row l16, quarter q) holds 16 values of each step.  Q4_K: step
-        // st, quarter q = values 64 st + 16 q (sub-block 2 st + q / 2); IQ2_S:
-        // the 16-value group 4 q + st.  The activations are read in the same
-        // order.  The sub-block scales are folded in: Q4_K's 6-bit scale as
-        // 8 sh + sl (q sh, q sl <= 105), IQ2_S's grid (2 ls + 1) as 64 h + l.
-        v4i bh[2][4], bl[2][4];
-        h8 bm[2];
+        // ---- per row tile: Q4_K lane (row l16, quarter q) takes values 64 st
+        // + 16 q of slice st (sub-block 2 st + q / 2); IQ2_S the 16-value group
+        // 4 q + st.  The activations are read in the same order.  The
+        // sub-block scales are folded in: Q4_K's 6-bit scale as 8 sh + sl
+        // (q sh, q sl <= 105), IQ2_S's grid (2 ls + 1) as 64 h + l.
         float dr[2], mr[2];
+        uint32_t sh03[2], sl03[2], sh47[2], sl47[2];         // Q4_K
+        uint2 qs8[2], sg8[2];                                // IQ2_S
+        uint32_t qh2[2], sc2[2];
+        h8 bm[2];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
             if constexpr (Q4) {
@@ -637,22 +643,8 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
                 const uint32_t mn03 = hdr.z & 0x3F3F3F3Fu;
                 const uint32_t sc47 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
                 const uint32_t mn47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-                const uint32_t sh03 = (sc03 >> 3) & 0x07070707u, sl03 = sc03 & 0x07070707u;
-                const uint32_t sh47 = (sc47 >> 3) & 0x07070707u, sl47 = sc47 & 0x07070707u;
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wrw + 16 + 32 * st + 16 * (q & 1));
-                    const uint32_t sel = (st & 1) ? sel_odd : sel_even;
-                    const uint32_t sh2 = __builtin_amdgcn_perm(0u, st < 2 ? sh03 : sh47, sel);
-                    const uint32_t sl2 = __builtin_amdgcn_perm(0u, st < 2 ? sl03 : sl47, sel);
-                    const uint32_t w4v[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t nb = (w4v[i] >> nib_shift) & 0x0F0F0F0Fu;
-                        bh[rs][st][i] = (int)bytes_mul(nb, sh2);
-                        bl[rs][st][i] = (int)bytes_mul(nb, sl2);
-                    }
-                }
+                sh03[rs] = (sc03 >> 3) & 0x07070707u; sl03[rs] = sc03 & 0x07070707u;
+                sh47[rs] = (sc47 >> 3) & 0x07070707u; sl47[rs] = sc47 & 0x07070707u;
                 // mins B operand (16x16x32 f16): k 0..7 = 32 m_j, 8..15 = m_j,
                 // 16..31 = 0; (1024 + m) * mult + off per lane quarter
                 const uint32_t mb4[4] = {magic_lo(mn03), magic_hi(mn03), magic_lo(mn47), magic_hi(mn47)};
@@ -667,28 +659,12 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
                 dr[rs] = h2f((w.d >> w.sh_d) & 0xFFFFu);
                 mr[rs] = 0.0f;
                 // this lane's groups 4q .. 4q + 3: grid entries 8q .. 8q + 7
-                const uint2 qs8 = make_uint2(__builtin_amdgcn_alignbit(w.qs.y, w.qs.x, w.sh_q),
-                                             __builtin_amdgcn_alignbit(w.qs.z, w.qs.y, w.sh_q));
-                const uint2 sg8 = make_uint2(__builtin_amdgcn_alignbit(w.sg.y, w.sg.x, w.sh_q),
-                                             __builtin_amdgcn_alignbit(w.sg.z, w.sg.y, w.sh_q));
-                const uint32_t qh2 = (w.qh >> w.sh_h) & 0xFFFFu;        // 2 bits per entry
-                const uint32_t sc2 = (w.sc >> w.sh_h) & 0xFFFFu;        // 4 bits per group
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const uint32_t qsw = st < 2 ? qs8.x : qs8.y, sgw = st < 2 ? sg8.x : sg8.y;
-                    const int b0 = 16 * (st & 1);                       // bit of entry 2 st in its dword
-                    const uint32_t i0 = __builtin_amdgcn_ubfe(qsw, b0, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st, 2) << 8);
-                    const uint32_t i1 = __builtin_amdgcn_ubfe(qsw, b0 + 8, 8) | (__builtin_amdgcn_ubfe(qh2, 4 * st + 2, 2) << 8);
-                    const uint2 c0 = L.codes[i0], c1 = L.codes[i1];
-                    const uint2 s0 = sign_sel(sgw, b0), s1 = sign_sel(sgw, b0 + 8);
-                    const u32x4 t = L.split[__builtin_amdgcn_ubfe(sc2, 4 * st, 4)];
-                    const uint32_t sel[4] = {c0.x | s0.x, c0.y | s0.y, c1.x | s1.x, c1.y | s1.y};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        bh[rs][st][i] = (int)__builtin_amdgcn_perm(t.y, t.x, sel[i]);
-                        bl[rs][st][i] = (int)__builtin_amdgcn_perm(t.w, t.z, sel[i]);
-                    }
-                }
+                qs8[rs] = make_uint2(__builtin_amdgcn_alignbit(w.qs.y, w.qs.x, w.sh_q),
+                                     __builtin_amdgcn_alignbit(w.qs.z, w.qs.y, w.sh_q));
+                sg8[rs] = make_uint2(__builtin_amdgcn_alignbit(w.sg.y, w.sg.x, w.sh_q),
+                                     __builtin_amdgcn_alignbit(w.sg.z, w.sg.y, w.sh_q));
+                qh2[rs] = (w.qh >> w.sh_h) & 0xFFFFu;               // 2 bits per entry
+                sc2[rs] = (w.sc >> w.sh_h) & 0xFFFFu;               // 4 bits per group
 #pragma unroll
                 for (int j = 0; j < 8; ++j) bm[rs][j] = (_Float16)0.0f;
             }
@@ -700,16 +676,68 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
             load_rows(s + 1);
         }
 
-        // ---- every 16-token tile of the group against both row tiles
+        // ---- slice by slice: expand, then every tile's MFMAs
+        v4i ah[2][NT], al[2][NT];
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs)
+#pragma unroll
+            for (int ts = 0; ts < NT; ++ts) {
+                ah[rs][ts] = v4i{0, 0, 0, 0};
+                al[rs][ts] = v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            v4i bh[2], bl[2];
+#pragma unroll
+            for (int rs = 0; rs < 2; ++rs) {
+                if constexpr (Q4) {
+                    const uint8_t * wrw = wb + (32 * wave + 16 * rs + l16) * 144;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wrw + 16 + 32 * st + 16 * (q & 1));
+                    const uint32_t sel = (st & 1) ? sel_odd : sel_even;
+                    const uint32_t sh2 = __builtin_amdgcn_perm(0u, st < 2 ? sh03[rs] : sh47[rs], sel);
+                    const uint32_t sl2 = __builtin_amdgcn_perm(0u, st < 2 ? sl03[rs] : sl47[rs], sel);
+                    const uint32_t w4v[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t nb = (w4v[i] >> nib_shift) & 0x0F0F0F0Fu;
+                        bh[rs][i] = (int)bytes_mul(nb, sh2);
+                        bl[rs][i] = (int)bytes_mul(nb, sl2);
+                    }
+                } else {
+                    const uint32_t qsw = st < 2 ? qs8[rs].x : qs8[rs].y, sgw = st < 2 ? sg8[rs].x : sg8[rs].y;
+                    const int b0 = 16 * (st & 1);                       // bit of entry 2 st in its dword
+                    const uint32_t i0 = __builtin_amdgcn_ubfe(qsw, b0, 8) | (__builtin_amdgcn_ubfe(qh2[rs], 4 * st, 2) << 8);
+                    const uint32_t i1 = __builtin_amdgcn_ubfe(qsw, b0 + 8, 8) | (__builtin_amdgcn_ubfe(qh2[rs], 4 * st + 2, 2) << 8);
+                    const uint2 c0 = L.codes[i0], c1 = L.codes[i1];
+                    const uint2 s0 = sign_sel(sgw, b0), s1 = sign_sel(sgw, b0 + 8);
+                    const u32x4 t = L.split[__builtin_amdgcn_ubfe(sc2[rs], 4 * st, 4)];
+                    const uint32_t sel[4] = {c0.x | s0.x, c0.y | s0.y, c1.x | s1.x, c1.y | s1.y};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        bh[rs][i] = (int)__builtin_amdgcn_perm(t.y, t.x, sel[i]);
+                        bl[rs][i] = (int)__builtin_amdgcn_perm(t.w, t.z, sel[i]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int ts = 0; ts < NT; ++ts) {
+                const uint8_t * xr = xb + (16 * ts + l16) * 256;
+                const int c = Q4 ? q + 4 * st : 4 * q + st;
+                const v4i a = as_v4i(*reinterpret_cast<const u32x4 *>(xr + 16 * (c ^ l16)));
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs) {
+                    ah[rs][ts] = mfma_i8(a, bh[rs], ah[rs][ts]);
+                    al[rs][ts] = mfma_i8(a, bl[rs], al[rs][ts]);
+                }
+            }
+        }
+
+        // ---- every tile's per-output scaling.  Explicit fmas: every token
+        // column rounds alike.  A pair's column in its group depends on the
+        // bucketing order, and left to itself the compiler contracts some
+        // unrolled columns into an fma and not others.
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) {
-            const uint8_t * xr = xb + (16 * ts + l16) * 256;
-            v4i a[4];
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const int c = Q4 ? q + 4 * st : 4 * q + st;
-                a[st] = as_v4i(*reinterpret_cast<const u32x4 *>(xr + 16 * (c ^ l16)));
-            }
             const f4 d8 = *reinterpret_cast<const f4 *>(d8b + 16 * ts + 4 * q);
             h8 am;
             if constexpr (Q4) {
@@ -721,28 +749,18 @@ __device__ __forceinline__ void pf_gu2_group(const PfParams & p, const PfTile & 
             }
 #pragma unroll
             for (int rs = 0; rs < 2; ++rs) {
-                v4i ah = {0, 0, 0, 0}, al = {0, 0, 0, 0};
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    ah = mfma_i8(a[st], bh[rs][st], ah);
-                    al = mfma_i8(a[st], bl[rs][st], al);
-                }
-                // explicit fmas: every token column rounds alike.  A pair's
-                // column in its group depends on the bucketing order, and left
-                // to itself the compiler contracts some unrolled columns into
-                // an fma and not others.
                 if constexpr (Q4) {
                     const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float sf = (float)(8 * ah[r] + al[r]);
+                        const float sf = (float)(8 * ah[rs][ts][r] + al[rs][ts][r]);
                         const float t = __builtin_fmaf(dr[rs], sf, -(mr[rs] * m[r]));
                         y[rs][ts][r] = __builtin_fmaf(d8[r], t, y[rs][ts][r]);
                     }
                 } else {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float sf = (float)(64 * ah[r] + al[r]);
+                        const float sf = (float)(64 * ah[rs][ts][r] + al[rs][ts][r]);
                         y[rs][ts][r] = __builtin_fmaf(d8[r], dr[rs] * sf, y[rs][ts][r]);
                     }
                 }
