@@ -461,7 +461,8 @@ class Stack:
     per-layer device copies of the one quantised layer (distinct memory, the
     same bytes).  Attention is omitted: each layer is h += moe(rms_norm(h)),
     the MoE input normalised as the model's is (without the norm the
-    residual stream grows until q8 scales overflow fp16)."""
+    residual stream grows until q8 scales overflow fp16); the residual add
+    and the next layer's norm run as one kernel."""
 
     def __init__(self, la, torch, full, spec, n_layers, dev):
         self.la, self.torch, self.spec = la, torch, spec
@@ -517,21 +518,22 @@ class Stack:
 
     def run(self, h, xn, out, ws, stream, T, moe=True):
         """h [T, d_model] (the residual stream) is updated in place through
-        every layer; out is scratch (xn is unused: the norm's output is the
-        layer's input).  moe=False runs only the glue
-        (norm and add) to time it on its own."""
+        every layer; xn holds each layer's input rms_norm(h), out its MoE
+        output.  The glue between layers is one kernel (h += out, then the
+        next input's norm: llapis_residual_rmsnorm).  moe=False runs only the
+        glue, to time it on its own."""
         torch = self.torch
         sp = self.spec
         ids = torch.empty(T, sp.top_k, dtype=torch.int32, device=h.device)
         w = torch.empty(T, sp.top_k, device=h.device)
+        self.la.residual_rmsnorm(h, None, xn, eps=1e-6, stream=stream)
         for d in self.descs:
-            xl = torch.nn.functional.rms_norm(h, (sp.d_model,), eps=1e-6)   # the layer's input, no extra copy
             if moe:
-                rc = self.fn(C.byref(d), xl.data_ptr(), None, T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                rc = self.fn(C.byref(d), xn.data_ptr(), None, T, out.data_ptr(), ids.data_ptr(), w.data_ptr(),
                              ws.data_ptr(), ws.numel(), stream)
                 if rc != 0:
                     raise RuntimeError(self.la.lib().llapis_last_error().decode())
-            h.add_(out)
+            self.la.residual_rmsnorm(h, out, xn, eps=1e-6, stream=stream)
 
 
 def run_stack(la, torch, full, spec, dev, n_layers=30, decode_steps=50, prefill_tokens=11200):

@@ -118,6 +118,17 @@ int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float 
 int32_t llapis_moe_combine(const float * y, const float * weights, int32_t n_tokens, int32_t top_k, int32_t d,
                            float * out, void * stream);
 
+/* The glue between two layers of a residual stream, in one kernel: h += add
+ * (when add is not NULL; h [n_tokens][d] updated in place), then
+ * x = h / sqrt(mean(h^2) + eps) per token (ggml_rms_norm without a weight:
+ * the sum of squares in fp32 in a fixed order, an IEEE square root and
+ * division).  Not part of the MoE operator: the residual add and the next
+ * block's input norm a model runs between its blocks (llama-graph.cpp
+ * build_norm, ggml_add), here for a stack of MoE layers that skips
+ * attention. */
+int32_t llapis_residual_rmsnorm(float * h, const float * add, int32_t n_tokens, int32_t d, float eps, float * x,
+                                void * stream);
+
 /* One dual-precision MoE FFN layer: build_moe_ffn's merged gate_up path for
  * gemma4-style MoE (llama-graph.cpp:1507-1850) with each routed pair computed
  * at its tier.  Pools are device slabs (see the note at the top):

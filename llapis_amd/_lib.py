@@ -249,6 +249,7 @@ SIGNATURES = {
     "llapis_router_topk": (i32, [vp, i32, vp, vp, i32, i32, i32, vp, vp, vp, vp]),
     "llapis_geglu": (i32, [vp, i32, i32, vp, i32, vp]),
     "llapis_moe_combine": (i32, [vp, vp, i32, i32, i32, vp, vp]),
+    "llapis_residual_rmsnorm": (i32, [vp, vp, i32, i32, C.c_float, vp, vp]),
     "llapis_moe_ffn_workspace_size": (u64, [C.POINTER(LlapisMoeLayer), i32]),
     "llapis_moe_ffn": (i32, [C.POINTER(LlapisMoeLayer), vp, vp, i32, vp, vp, vp, vp, u64, vp]),
     "llapis_moe_ffn_workspace_init": (i32, [C.POINTER(LlapisMoeLayer), vp, u64, vp]),

@@ -527,6 +527,15 @@ int32_t llapis_geglu(const float * gate_up, int32_t n_ff, int32_t n_cols, float 
     return 0;
 }
 
+int32_t llapis_residual_rmsnorm(float * h, const float * add, int32_t n_tokens, int32_t d, float eps, float * x,
+                                void * stream) {
+    if (n_tokens <= 0) return 0;
+    if (!h || !x) return fail("llapis_residual_rmsnorm: null pointer");
+    if (d <= 0 || d > 4096) return fail("llapis_residual_rmsnorm: need 0 < d <= 4096");
+    LL_TRY(launch_residual_rmsnorm(h, add, n_tokens, d, eps, x, (hipStream_t)stream));
+    return 0;
+}
+
 int32_t llapis_moe_combine(const float * y, const float * weights, int32_t n_tokens, int32_t top_k, int32_t d,
                            float * out, void * stream) {
     if (n_tokens <= 0 || d <= 0) return 0;

@@ -191,6 +191,7 @@ hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, 
 hipError_t launch_topk_parts(const float * parts, const float * bias, int T, int E, int K, float * probs, int32_t * ids,
                              float * w, hipStream_t s);
 hipError_t launch_combine(const float * y, const float * w, int T, int K, int D, float * out, hipStream_t s);
+hipError_t launch_residual_rmsnorm(float * h, const float * add, int T, int d, float eps, float * x, hipStream_t s);
 hipError_t launch_geglu(const float * gu, int F, int n_cols, float * out, int mode, hipStream_t s);
 
 hipError_t launch_partition(const int32_t * ids, int n_used, int ids_s1, int n_pairs, const int32_t * exp_slot,

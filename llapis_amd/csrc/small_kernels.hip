@@ -191,6 +191,50 @@ __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, 
     if (lane < K) w[(int64_t)t * K + lane] = sel / sf;
 }
 
+// h += add (add may be null), then x = h * (1 / sqrt(mean(h^2) + eps)); one
+// workgroup per token, every load issued before the first sum; the squares
+// summed per thread in element order, then over the wave, then the four
+// waves in order
+constexpr int RMS_PER_THREAD = 16;               // d <= 4096
+__global__ __launch_bounds__(WG) void k_residual_rmsnorm(float * __restrict__ h, const float * __restrict__ add,
+                                                          int d, float eps, float * __restrict__ x) {
+    __shared__ float s_part[WG / 64];
+    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float * ht = h + (int64_t)t * d;
+    const float * at = add ? add + (int64_t)t * d : nullptr;
+    float v[RMS_PER_THREAD];
+#pragma unroll
+    for (int j = 0; j < RMS_PER_THREAD; ++j) {
+        const int i = threadIdx.x + j * WG;
+        v[j] = i < d ? ht[i] : 0.0f;
+    }
+    if (at) {
+#pragma unroll
+        for (int j = 0; j < RMS_PER_THREAD; ++j) {
+            const int i = threadIdx.x + j * WG;
+            if (i < d) {
+                v[j] = v[j] + at[i];
+                ht[i] = v[j];
+            }
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RMS_PER_THREAD; ++j) ss = __builtin_fmaf(v[j], v[j], ss);
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) s_part[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < WG / 64; ++q) tot += s_part[q];
+    const float inv = 1.0f / __fsqrt_rn(tot / (float)d + eps);
+#pragma unroll
+    for (int j = 0; j < RMS_PER_THREAD; ++j) {
+        const int i = threadIdx.x + j * WG;
+        if (i < d) x[(int64_t)t * d + i] = v[j] * inv;
+    }
+}
+
 // out[t][r] = ((w0 y0 + w1 y1) + w2 y2) + ...   (llama-graph.cpp:1812-1840:
 // ggml_mul by the weights, then the views added in order)
 __global__ __launch_bounds__(WG) void k_combine(const float * __restrict__ y, const float * __restrict__ w, int K, int D,
@@ -377,6 +421,12 @@ hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, 
 hipError_t launch_topk_parts(const float * parts, const float * bias, int T, int E, int K, float * probs, int32_t * ids,
                              float * w, hipStream_t s) {
     hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, s, probs, E, K, ids, w, parts, T, bias);
+    return hipGetLastError();
+}
+
+hipError_t launch_residual_rmsnorm(float * h, const float * add, int T, int d, float eps, float * x, hipStream_t s) {
+    if (d <= 0 || d > RMS_PER_THREAD * WG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_residual_rmsnorm, dim3(T), dim3(WG), 0, s, h, add, d, eps, x);
     return hipGetLastError();
 }
 

@@ -416,6 +416,22 @@ def combine(y, weights):
     return out
 
 
+def residual_rmsnorm(h, add=None, x=None, eps=1e-6, stream=None):
+    """h += add (in place, when add is given), then x = rms_norm(h) per row
+    (no weight); returns x.  The glue between two layers of a residual
+    stream, one kernel."""
+    torch = _torch()
+    T, d = h.shape
+    if not h.is_contiguous() or (add is not None and (not add.is_contiguous() or add.shape != h.shape)):
+        raise ValueError("residual_rmsnorm: h and add must be contiguous [T, d]")
+    if x is None:
+        x = torch.empty_like(h)
+    s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    check(lib().llapis_residual_rmsnorm(h.data_ptr(), None if add is None else add.data_ptr(), T, d, eps,
+                                        x.data_ptr(), s), "llapis_residual_rmsnorm")
+    return x
+
+
 def geglu(gate_up, n_ff, gelu_mode=L.GELU_TABLE):
     torch = _torch()
     n_cols = gate_up.numel() // (2 * n_ff)

@@ -175,6 +175,33 @@ def test_combine_is_the_k_order_sum(gpu, K):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("T,d,with_add", [(1, 2816, True), (5, 2816, False), (530, 2816, True), (3, 4096, True),
+                                           (2, 7, True)])
+def test_residual_rmsnorm(gpu, T, d, with_add):
+    """llapis_residual_rmsnorm: h += add bit for bit (one fp32 rounding per
+    element), then x = h / sqrt(mean(h^2) + eps) within 2e-6 of the float64
+    value per element (the fp32 sum of squares runs in the kernel's order);
+    the same call twice gives the same bits."""
+    torch = torch_mod()
+    say(f"residual rmsnorm T={T} d={d} add={with_add}")
+    rng = np.random.default_rng(70 + T + d)
+    h = (rng.standard_normal((T, d)) * 3).astype(np.float32)
+    a = rng.standard_normal((T, d)).astype(np.float32) if with_add else None
+    hd = torch.from_numpy(h).to(gpu)
+    ad = torch.from_numpy(a).to(gpu) if with_add else None
+    x = la.residual_rmsnorm(hd, ad, eps=1e-6)
+    torch.cuda.synchronize()
+    hs = (h + a).astype(np.float32) if with_add else h
+    assert np.array_equal(hd.cpu().numpy(), hs)
+    h64 = hs.astype(np.float64)
+    want = h64 / np.sqrt(np.mean(h64 * h64, axis=1, keepdims=True) + 1e-6)
+    got = x.cpu().numpy()
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) <= 2e-6
+    x2 = la.residual_rmsnorm(torch.from_numpy(hs).to(gpu), None, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(x, x2)
+
+
 def test_geglu_table_exhaustive(gpu, oracle):
     """Table mode depends on g only through fp16(g): every fp16 value of
     magnitude below 10 (and inputs just inside +-10, which round to fp16
