@@ -609,26 +609,50 @@ __device__ __forceinline__ void gu_dots(const DecParams & p, const GroupInfo & g
     }
 }
 
-// One step of a gate_up item (group gi, block j: gate rows [32 j, 32 j + 32)
-// and the up rows n_ff + 32 j .. paired with them, of group gi's expert,
-// weight type WT), whose loads are in `buf`: the staged halves h .. h +
-// gu_halves - 1 into LDS, one row per 16 lanes, and their dots.  One token:
-// both halves in one step.  More: the gate rows (h 0), then the up rows (h 1)
-// in the next step (the other workgroup on the CU keeps loads in flight
-// meanwhile).  After the up rows, GEGLU pairs gate row i with up row i for
-// every member, and each member's 32 values are quantised (q8_0 / q8_1, block
-// j of the pair's down activation) into the pair's down column.
-template <int WT, int HT, int CT, int AM, int MT, int GSRC>
-__device__ __forceinline__ void gu_run(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi, int j,
-                                       int h, uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT],
-                                       float (*s_act)[DEC_GU_BLK]) {
+// One token: wave w of the 16 stages and dots rows 4 (w mod 8) .. + 3 of the
+// item's gate (w < 8) or up (w >= 8) half, in its own LDS region of
+// w_lds_gu / 8 bytes: the load unit copies the four rows' chunks into it
+// (global_load_lds, no registers), so a wave waits only for its own rows and
+// needs no barrier before its dots, and it can start its rows of the next
+// item as soon as its dots are done.
+template <int HT, int CT>
+__device__ __forceinline__ Span gu_wave_span(const DecParams & p, const GroupInfo & gi, int j) {
+    const int wave = threadIdx.x >> 6;
+    return make_span(gi, (wave >> 3) * p.n_ff + DEC_GU_BLK * j + 4 * (wave & 7), 4, p.d_model, HT, CT, p.hot_gu,
+                     p.hot_gu_stride, p.cold_gu, p.cold_gu_stride, p.logits);
+}
+template <int HT, int CT>
+__device__ __forceinline__ void gu_wave_load(const DecParams & p, const GroupInfo & gi, int j, uint8_t * smem) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const Span sp = gu_wave_span<HT, CT>(p, gi, j);
+    uint8_t * dst = smem + wave * (p.w_lds_gu / 8);
+    for (int k = 0; 64 * k < sp.nch; ++k) {                // wave-uniform bound
+        const int c = 64 * k + lane;
+        if (c < sp.nch) lds_dma16(sp.src + c, dst + 1024 * k);
+    }
+}
+template <int WT, int HT, int CT, int AM>
+__device__ __forceinline__ void gu_wave_dots(const DecParams & p, const GroupInfo & gi, int j, const uint8_t * smem,
+                                             const ActView * av, int grid_off, float (*s_y)[1]) {
+    const int row = threadIdx.x >> 4, wave = threadIdx.x >> 6;
+    const bool live = gi.tier < 2 && gi.n_mem > 0;
+    const Span sp = gu_wave_span<HT, CT>(p, gi, j);
+    const int wb = wave * (p.w_lds_gu / 8) + sp.off + (row & 3) * sp.rb;
+    float acc[1];
+    item_dot<WT, AM, 1>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
+    if ((threadIdx.x & 15) == 0) s_y[row][0] = acc[0];
+}
+
+// GEGLU of the item's gate rows with its up rows for every member (s_y: row
+// i of the gate half at i, of the up half at 32 + i), and each member's 32
+// values quantised (q8_0 / q8_1, block j of the pair's down activation) into
+// the pair's down column
+template <int AM, int MT, int GSRC>
+__device__ __forceinline__ void gu_epilogue(const DecParams & p, const GroupInfo & gi, int j, float (*s_y)[MT],
+                                            float (*s_act)[DEC_GU_BLK]) {
     const int T = p.T, K = p.top_k, F = p.n_ff;
     const bool live = gi.tier < 2 && gi.n_mem > 0;
-    gu_store<HT, CT, MT>(buf, p, gi, j, h, smem);
-    gu_dots<WT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
-    if (h + gu_halves<MT>() < 2) return;                  // the up rows are still to come
     __syncthreads();
-    // GEGLU of gate row 32 j + i with its up row, member c
     if ((int)threadIdx.x < GU_HR * MT) {
         const int i = threadIdx.x % GU_HR, c = threadIdx.x / GU_HR;
         s_act[c][i] = geglu1<GSRC>(s_y[i][c], s_y[GU_HR + i][c]);
@@ -645,13 +669,30 @@ __device__ __forceinline__ void gu_run(u32x4 (&buf)[gu_buf<MT>()], const DecPara
     }
 }
 
+// One step of a gate_up item (group gi, block j: gate rows [32 j, 32 j + 32)
+// and the up rows n_ff + 32 j .. paired with them, of group gi's expert,
+// weight type WT), whose loads are in `buf`: the staged halves h .. h +
+// gu_halves - 1 into LDS, one row per 16 lanes, and their dots.  One token:
+// both halves in one step.  More: the gate rows (h 0), then the up rows (h 1)
+// in the next step (the other workgroup on the CU keeps loads in flight
+// meanwhile).  After the up rows, GEGLU pairs gate row i with up row i for
+// every member, and each member's 32 values are quantised (q8_0 / q8_1, block
+// j of the pair's down activation) into the pair's down column.
+template <int WT, int HT, int CT, int AM, int MT, int GSRC>
+__device__ __forceinline__ void gu_run(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi, int j,
+                                       int h, uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT],
+                                       float (*s_act)[DEC_GU_BLK]) {
+    gu_store<HT, CT, MT>(buf, p, gi, j, h, smem);
+    gu_dots<WT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
+    if (h + gu_halves<MT>() < 2) return;                  // the up rows are still to come
+    gu_epilogue<AM, MT, GSRC>(p, gi, j, s_y, s_act);
+}
+
 // the routing's LDS scratch in a gate_up workgroup (at the start of the
 // weight staging area, which the host sizes to hold it: dec_gu_half_bytes)
 struct GuScratch {
     int32_t res[3][256];
     int first[256], tm[256];
-    int ids[DEC_PMAX];
-    float w[DEC_PMAX];
     SelScratch sel[DEC_MAXT];
 };
 
@@ -677,8 +718,8 @@ void k_dec_gate_up(const DecParams p) {
     // the routing's scratch lives where the weights are staged later (the
     // first item starts with a barrier, after every read of it)
     GuScratch & sr = *reinterpret_cast<GuScratch *>(smem);
-    int * s_ids = sr.ids;
-    float * s_w = sr.w;
+    __shared__ int s_ids[DEC_PMAX];           // the routing, kept past the scratch's reuse
+    __shared__ float s_w[DEC_PMAX];
     int32_t (*s_res)[256] = sr.res;           // exp_slot, slot_exp, slot_state
     int * s_first = sr.first;                 // also each expert's group id, once its first pair is known
     int * s_tm = sr.tm;
@@ -756,7 +797,8 @@ void k_dec_gate_up(const DecParams p) {
     int it = blockIdx.x, j, h = 0;
     GroupInfo gi = item(it, &j);
     u32x4 buf[gu_buf<MT>()];
-    gu_issue<HT, CT, MT>(buf, p, gi, j, 0);
+    if constexpr (MT == 1) gu_wave_load<HT, CT>(p, gi, j, smem);   // the scratch is dead: after the barrier above
+    else gu_issue<HT, CT, MT>(buf, p, gi, j, 0);
     const int a0 = gu_halves<MT>() * p.w_lds_gu;
 #pragma unroll
     for (int k = 0; k < COLL; ++k) {
@@ -785,6 +827,29 @@ void k_dec_gate_up(const DecParams p) {
     }
 
     // 5. the items (gu_run's first barrier orders the LDS stores above)
+    if constexpr (MT == 1) {
+        __syncthreads();                                  // the columns and the codebook
+        while (true) {
+            ActView av[1];
+            act_layout(d_in, a0, &av[0]);
+            __builtin_amdgcn_s_waitcnt(0);                // this wave's rows have landed
+            if (gi.tier == 0) gu_wave_dots<HT, HT, CT, AM>(p, gi, j, smem, av, grid_off, s_y);
+            else gu_wave_dots<CT, HT, CT, AM>(p, gi, j, smem, av, grid_off, s_y);
+            const int nit = it + (int)gridDim.x;
+            int nj = 0;
+            GroupInfo nx = gi;
+            if (nit < n_items) {
+                nx = item(nit, &nj);
+                gu_wave_load<HT, CT>(p, nx, nj, smem);    // in flight during the epilogue
+            }
+            gu_epilogue<AM, 1, GSRC>(p, gi, j, s_y, s_act);
+            if (nit >= n_items) break;
+            it = nit;
+            gi = nx;
+            j = nj;
+        }
+        return;
+    }
     while (true) {
         ActView av[MT];
 #pragma unroll
@@ -1503,7 +1568,11 @@ int dec_act_bytes(int n) {
 // the routing's scratch, which the two halves hold before the first item
 int dec_gu_half_bytes(int T, int row_bytes) {
     const int halves = T == 1 ? gu_halves<1>() : gu_halves<DEC_MAXT>();
-    return std::max(align16i(GU_HR * row_bytes + 32), align16i((int)sizeof(GuScratch) / halves + 16));
+    // one token: eight waves' regions of 4 rows each (plus a dword a funnel
+    // read may touch past a span's end)
+    const int rows = T == 1 ? 8 * align16i(4 * row_bytes + 32) : align16i(GU_HR * row_bytes + 32);
+    const int b = std::max(rows, align16i((int)sizeof(GuScratch) / halves + 16));
+    return T == 1 ? (b + 127) / 128 * 128 : b;        // eight 16-aligned regions
 }
 
 // dynamic LDS of B: the halves of an item staged at once (both with one

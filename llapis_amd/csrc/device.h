@@ -450,6 +450,19 @@ template <> struct Fmt<T_IQ2_S>  { static constexpr int UNIT = 64; static conste
 template <> struct Fmt<T_Q5_0>   { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
 template <> struct Fmt<T_IQ4_NL> { static constexpr int UNIT = 32; static constexpr int LPR = 8; };
 
+typedef const void __attribute__((address_space(1))) * gptr_t;
+typedef void __attribute__((address_space(3))) * lptr_t;
+
+// 16 (or 4) bytes per lane from global memory into LDS at dst + 16 lane
+// (4 lane): the load unit writes LDS itself, tracked by the vector memory
+// counter (dst is the wave's base: the same in every lane)
+__device__ __forceinline__ void lds_dma16(const void * src, void * dst) {
+    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void * src, void * dst) {
+    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 4, 0, 0);
+}
+
 __device__ __forceinline__ u32x4 lds128(const uint8_t * smem, int off) {   // off % 16 == 0
     return *reinterpret_cast<const u32x4 *>(smem + off);
 }

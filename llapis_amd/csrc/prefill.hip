@@ -429,19 +429,6 @@ struct Gu2Lds {
     int * tok; int * pair;
 };
 
-typedef const void __attribute__((address_space(1))) * gptr_t;
-typedef void __attribute__((address_space(3))) * lptr_t;
-
-// 16 (or 4) bytes per lane from global memory into LDS at dst + 16 lane
-// (4 lane): the load unit writes LDS itself, tracked by the vector memory
-// counter
-__device__ __forceinline__ void lds_dma16(const void * src, void * dst) {
-    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 16, 0, 0);
-}
-__device__ __forceinline__ void lds_dma4(const void * src, void * dst) {
-    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 4, 0, 0);
-}
-
 // one lane's bytes of one IQ2_S super-block of a 16-row tile
 struct Iq2Raw {
     uint32_t d;                 // dword holding d
