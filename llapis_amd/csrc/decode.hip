@@ -501,20 +501,12 @@ constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
 // gate, 32 up) at once, one row per 16 lanes, and the device holds one per
 // CU.  With 2-4 tokens a workgroup is 8 waves and takes an item in two
 // steps, its 32 gate rows and then its 32 up rows (one row per 16 lanes), so
-// its LDS holds half an item and a CU holds two workgroups: one's loads are
-// in flight while the other dots.
+// its LDS holds half an item and a CU holds two workgroups.  Either way wave
+// w stages four rows in an LDS region of its own.
 template <int MT> constexpr int gu_nw() { return MT == 1 ? 16 : 8; }
 template <int MT> constexpr int gu_nt() { return 64 * gu_nw<MT>(); }
 template <int MT> constexpr int gu_halves() { return MT == 1 ? 2 : 1; }   // halves staged at once
 constexpr int GU_HR = DEC_GU_BLK;             // rows of each half (gate, up) of an item
-// Loads per thread of one half of an item: 32 rows (Q4_K: 99 chunks of 16
-// bytes per pair of rows at d_model 2816; IQ2_S: at most 57) over 1024
-// threads -> 4, over 512 -> 7.  One layout for either format, so the
-// registers stay registers whichever tier an item has.  Chunks past a half's
-// share are loaded when the half is stored.
-template <int MT> constexpr int gu_lh() { return MT == 1 ? 4 : 7; }
-template <int MT> constexpr int gu_buf() { return gu_halves<MT>() * gu_lh<MT>(); }
-
 
 // The dots of the staged row at `wb` (one row per 16 lanes) against the
 // members' columns av[c], c < n_mem <= MT; the row sums are complete in lane
@@ -556,91 +548,50 @@ __device__ __forceinline__ Span gu_span(const DecParams & p, const GroupInfo & g
                      p.cold_gu, p.cold_gu_stride, p.logits);
 }
 
-// the loads of an item's halves h0 .. h0 + gu_halves - 1 (0: gate rows,
-// 1: up rows), unconditional
+// Wave w stages and dots four rows of an item: rows 4 (w mod 8) .. + 3 of the
+// gate half (0) or the up half (1) -- one token: half w / 8, the 16 waves
+// cover both; more: the step's half h -- in an LDS region of its own,
+// w_lds_gu / 8 bytes at w w_lds_gu / 8.  The load unit copies the rows'
+// chunks into it (global_load_lds, no registers), so a wave waits only for
+// its own rows and needs no barrier before its dots, and it starts its rows
+// of the next step as soon as its dots are done.
+template <int MT>
+__device__ __forceinline__ int gu_wave_half(int h) {
+    return gu_halves<MT>() == 2 ? (int)(threadIdx.x >> 9) : h;
+}
 template <int HT, int CT, int MT>
-__device__ __forceinline__ void gu_issue(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi,
-                                         int j, int h0) {
-    constexpr int LH = gu_lh<MT>(), NT = gu_nt<MT>();
-#pragma unroll
-    for (int h = 0; h < gu_halves<MT>(); ++h) {
-        const Span sp = gu_span<HT, CT>(p, gi, j, h0 + h);
-#pragma unroll
-        for (int k = 0; k < LH; ++k) buf[h * LH + k] = sp.src[min((int)threadIdx.x + k * NT, sp.nch - 1)];
-    }
-}
-
-// The staged halves of an item into LDS (half h at smem + h w_lds_gu), once
-// every wave is done with the previous ones
-template <int HT, int CT, int MT>
-__device__ __forceinline__ void gu_store(const u32x4 (&buf)[gu_buf<MT>()], const DecParams & p,
-                                         const GroupInfo & gi, int j, int h0, uint8_t * smem) {
-    constexpr int LH = gu_lh<MT>(), NT = gu_nt<MT>();
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < gu_halves<MT>(); ++h) {
-        const Span sp = gu_span<HT, CT>(p, gi, j, h0 + h);
-        uint8_t * dst = smem + h * p.w_lds_gu;
-#pragma unroll
-        for (int k = 0; k < LH; ++k) {
-            const int i = threadIdx.x + k * NT;
-            if (i < sp.nch) reinterpret_cast<u32x4 *>(dst)[i] = buf[h * LH + k];
-        }
-        for (int i = threadIdx.x + LH * NT; i < sp.nch; i += NT) reinterpret_cast<u32x4 *>(dst)[i] = sp.src[i];
-    }
-    __syncthreads();
-}
-
-// The dots of the staged rows: 16 lanes a row, row threadIdx / 16 of the
-// staged halves (h0 + row / 32: gate or up) into s_y[32 (h0 + row / 32) +
-// row % 32]
-template <int WT, int HT, int CT, int AM, int MT>
-__device__ __forceinline__ void gu_dots(const DecParams & p, const GroupInfo & gi, int j, int h0,
-                                        const uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT]) {
-    const int row = threadIdx.x >> 4, hr = row / GU_HR, r = row - hr * GU_HR;
-    const bool live = gi.tier < 2 && gi.n_mem > 0;
-    const Span sp = gu_span<HT, CT>(p, gi, j, h0 + hr);
-    const int wb = hr * p.w_lds_gu + sp.off + r * sp.rb;
-    float acc[MT];
-    item_dot<WT, AM, MT>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
-    if ((threadIdx.x & 15) == 0) {
-#pragma unroll
-        for (int c = 0; c < MT; ++c) s_y[(h0 + hr) * GU_HR + r][c] = acc[c];
-    }
-}
-
-// One token: wave w of the 16 stages and dots rows 4 (w mod 8) .. + 3 of the
-// item's gate (w < 8) or up (w >= 8) half, in its own LDS region of
-// w_lds_gu / 8 bytes: the load unit copies the four rows' chunks into it
-// (global_load_lds, no registers), so a wave waits only for its own rows and
-// needs no barrier before its dots, and it can start its rows of the next
-// item as soon as its dots are done.
-template <int HT, int CT>
-__device__ __forceinline__ Span gu_wave_span(const DecParams & p, const GroupInfo & gi, int j) {
+__device__ __forceinline__ Span gu_wave_span(const DecParams & p, const GroupInfo & gi, int j, int h) {
     const int wave = threadIdx.x >> 6;
-    return make_span(gi, (wave >> 3) * p.n_ff + DEC_GU_BLK * j + 4 * (wave & 7), 4, p.d_model, HT, CT, p.hot_gu,
-                     p.hot_gu_stride, p.cold_gu, p.cold_gu_stride, p.logits);
+    return make_span(gi, gu_wave_half<MT>(h) * p.n_ff + DEC_GU_BLK * j + 4 * (wave & 7), 4, p.d_model, HT, CT,
+                     p.hot_gu, p.hot_gu_stride, p.cold_gu, p.cold_gu_stride, p.logits);
 }
-template <int HT, int CT>
-__device__ __forceinline__ void gu_wave_load(const DecParams & p, const GroupInfo & gi, int j, uint8_t * smem) {
+template <int HT, int CT, int MT>
+__device__ __forceinline__ void gu_wave_load(const DecParams & p, const GroupInfo & gi, int j, int h, uint8_t * smem) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const Span sp = gu_wave_span<HT, CT>(p, gi, j);
+    const Span sp = gu_wave_span<HT, CT, MT>(p, gi, j, h);
     uint8_t * dst = smem + wave * (p.w_lds_gu / 8);
     for (int k = 0; 64 * k < sp.nch; ++k) {                // wave-uniform bound
         const int c = 64 * k + lane;
         if (c < sp.nch) lds_dma16(sp.src + c, dst + 1024 * k);
     }
 }
-template <int WT, int HT, int CT, int AM>
-__device__ __forceinline__ void gu_wave_dots(const DecParams & p, const GroupInfo & gi, int j, const uint8_t * smem,
-                                             const ActView * av, int grid_off, float (*s_y)[1]) {
-    const int row = threadIdx.x >> 4, wave = threadIdx.x >> 6;
+// the four rows' dots against the members' columns into s_y[32 half + 4 (w
+// mod 8) + row]
+template <int WT, int HT, int CT, int AM, int MT>
+__device__ __forceinline__ void gu_wave_dots(const DecParams & p, const GroupInfo & gi, int j, int h,
+                                             const uint8_t * smem, const ActView * av, int grid_off,
+                                             float (*s_y)[MT]) {
+    const int wave = threadIdx.x >> 6, r = (threadIdx.x >> 4) & 3;
     const bool live = gi.tier < 2 && gi.n_mem > 0;
-    const Span sp = gu_wave_span<HT, CT>(p, gi, j);
-    const int wb = wave * (p.w_lds_gu / 8) + sp.off + (row & 3) * sp.rb;
-    float acc[1];
-    item_dot<WT, AM, 1>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
-    if ((threadIdx.x & 15) == 0) s_y[row][0] = acc[0];
+    const Span sp = gu_wave_span<HT, CT, MT>(p, gi, j, h);
+    const int wb = wave * (p.w_lds_gu / 8) + sp.off + r * sp.rb;
+    float acc[MT];
+    item_dot<WT, AM, MT>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
+    if ((threadIdx.x & 15) == 0) {
+        const int y = GU_HR * gu_wave_half<MT>(h) + 4 * (wave & 7) + r;
+#pragma unroll
+        for (int c = 0; c < MT; ++c) s_y[y][c] = acc[c];
+    }
 }
 
 // GEGLU of the item's gate rows with its up rows for every member (s_y: row
@@ -667,25 +618,6 @@ __device__ __forceinline__ void gu_epilogue(const DecParams & p, const GroupInfo
         const float v = lane < DEC_GU_BLK ? s_act[wave][lane] : 0.0f;
         q8_32_put<AM>(p.yq + (int64_t)pair * p.yq_stride, L, v, DEC_GU_BLK * j + (lane & 31), lane < DEC_GU_BLK);
     }
-}
-
-// One step of a gate_up item (group gi, block j: gate rows [32 j, 32 j + 32)
-// and the up rows n_ff + 32 j .. paired with them, of group gi's expert,
-// weight type WT), whose loads are in `buf`: the staged halves h .. h +
-// gu_halves - 1 into LDS, one row per 16 lanes, and their dots.  One token:
-// both halves in one step.  More: the gate rows (h 0), then the up rows (h 1)
-// in the next step (the other workgroup on the CU keeps loads in flight
-// meanwhile).  After the up rows, GEGLU pairs gate row i with up row i for
-// every member, and each member's 32 values are quantised (q8_0 / q8_1, block
-// j of the pair's down activation) into the pair's down column.
-template <int WT, int HT, int CT, int AM, int MT, int GSRC>
-__device__ __forceinline__ void gu_run(u32x4 (&buf)[gu_buf<MT>()], const DecParams & p, const GroupInfo & gi, int j,
-                                       int h, uint8_t * smem, const ActView * av, int grid_off, float (*s_y)[MT],
-                                       float (*s_act)[DEC_GU_BLK]) {
-    gu_store<HT, CT, MT>(buf, p, gi, j, h, smem);
-    gu_dots<WT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
-    if (h + gu_halves<MT>() < 2) return;                  // the up rows are still to come
-    gu_epilogue<AM, MT, GSRC>(p, gi, j, s_y, s_act);
 }
 
 // the routing's LDS scratch in a gate_up workgroup (at the start of the
@@ -796,9 +728,8 @@ void k_dec_gate_up(const DecParams p) {
     }
     int it = blockIdx.x, j, h = 0;
     GroupInfo gi = item(it, &j);
-    u32x4 buf[gu_buf<MT>()];
-    if constexpr (MT == 1) gu_wave_load<HT, CT>(p, gi, j, smem);   // the scratch is dead: after the barrier above
-    else gu_issue<HT, CT, MT>(buf, p, gi, j, 0);
+    // the first step's rows (the routing's scratch is dead: the barrier above)
+    gu_wave_load<HT, CT, MT>(p, gi, j, 0, smem);
     const int a0 = gu_halves<MT>() * p.w_lds_gu;
 #pragma unroll
     for (int k = 0; k < COLL; ++k) {
@@ -826,45 +757,33 @@ void k_dec_gate_up(const DecParams p) {
         count_routes(p, s_ids, s_grp, ng);
     }
 
-    // 5. the items (gu_run's first barrier orders the LDS stores above)
-    if constexpr (MT == 1) {
-        __syncthreads();                                  // the columns and the codebook
-        while (true) {
-            ActView av[1];
-            act_layout(d_in, a0, &av[0]);
-            __builtin_amdgcn_s_waitcnt(0);                // this wave's rows have landed
-            if (gi.tier == 0) gu_wave_dots<HT, HT, CT, AM>(p, gi, j, smem, av, grid_off, s_y);
-            else gu_wave_dots<CT, HT, CT, AM>(p, gi, j, smem, av, grid_off, s_y);
-            const int nit = it + (int)gridDim.x;
-            int nj = 0;
-            GroupInfo nx = gi;
-            if (nit < n_items) {
-                nx = item(nit, &nj);
-                gu_wave_load<HT, CT>(p, nx, nj, smem);    // in flight during the epilogue
-            }
-            gu_epilogue<AM, 1, GSRC>(p, gi, j, s_y, s_act);
-            if (nit >= n_items) break;
-            it = nit;
-            gi = nx;
-            j = nj;
-        }
-        return;
-    }
+    // 5. the steps: (item, half) -- one token: both halves in one step.  A
+    //    wave dots its rows once they have landed, starts its rows of the
+    //    next step, and after an item's up rows the workgroup's epilogue runs
+    //    (its barriers order s_y and s_act between the waves)
+    __syncthreads();                                      // the columns and the codebook
     while (true) {
         ActView av[MT];
 #pragma unroll
         for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + max(0, min(member(gi, c) / K, T - 1)) * abytes, &av[c]);
-        if (gi.tier == 0) gu_run<HT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, h, smem, av, grid_off, s_y, s_act);
-        else gu_run<CT, HT, CT, AM, MT, GSRC>(buf, p, gi, j, h, smem, av, grid_off, s_y, s_act);
-        if (h + gu_halves<MT>() < 2) {
-            h += gu_halves<MT>();
-        } else {
-            it += gridDim.x;
-            if (it >= n_items) break;
-            gi = item(it, &j);
-            h = 0;
+        __builtin_amdgcn_s_waitcnt(0);                    // this wave's rows have landed
+        if (gi.tier == 0) gu_wave_dots<HT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
+        else gu_wave_dots<CT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
+        const bool last = h + gu_halves<MT>() >= 2;       // the item's up rows are done
+        int nit = it, nj = j, nh = h + gu_halves<MT>();
+        GroupInfo nx = gi;
+        if (last) {
+            nit = it + (int)gridDim.x;
+            nh = 0;
+            if (nit < n_items) nx = item(nit, &nj);
         }
-        gu_issue<HT, CT, MT>(buf, p, gi, j, h);
+        if (nit < n_items) gu_wave_load<HT, CT, MT>(p, nx, nj, nh, smem);   // in flight meanwhile
+        if (last) gu_epilogue<AM, MT, GSRC>(p, gi, j, s_y, s_act);
+        if (nit >= n_items) break;
+        it = nit;
+        j = nj;
+        h = nh;
+        gi = nx;
     }
 }
 
@@ -1568,11 +1487,11 @@ int dec_act_bytes(int n) {
 // the routing's scratch, which the two halves hold before the first item
 int dec_gu_half_bytes(int T, int row_bytes) {
     const int halves = T == 1 ? gu_halves<1>() : gu_halves<DEC_MAXT>();
-    // one token: eight waves' regions of 4 rows each (plus a dword a funnel
-    // read may touch past a span's end)
-    const int rows = T == 1 ? 8 * align16i(4 * row_bytes + 32) : align16i(GU_HR * row_bytes + 32);
+    // eight waves' regions of 4 rows each (plus a dword a funnel read may
+    // touch past a span's end), at least the routing's scratch over the halves
+    const int rows = 8 * align16i(4 * row_bytes + 32);
     const int b = std::max(rows, align16i((int)sizeof(GuScratch) / halves + 16));
-    return T == 1 ? (b + 127) / 128 * 128 : b;        // eight 16-aligned regions
+    return (b + 127) / 128 * 128;                     // eight 16-aligned regions
 }
 
 // dynamic LDS of B: the halves of an item staged at once (both with one
