@@ -575,48 +575,43 @@ __device__ __forceinline__ void gu_wave_load(const DecParams & p, const GroupInf
         if (c < sp.nch) lds_dma16(sp.src + c, dst + 1024 * k);
     }
 }
-// the four rows' dots against the members' columns into s_y[32 half + 4 (w
-// mod 8) + row]
+// the four rows' dots against the members' columns: acc[c], complete in
+// every lane of the row
 template <int WT, int HT, int CT, int AM, int MT>
 __device__ __forceinline__ void gu_wave_dots(const DecParams & p, const GroupInfo & gi, int j, int h,
-                                             const uint8_t * smem, const ActView * av, int grid_off,
-                                             float (*s_y)[MT]) {
+                                             const uint8_t * smem, const ActView * av, int grid_off, float * acc) {
     const int wave = threadIdx.x >> 6, r = (threadIdx.x >> 4) & 3;
     const bool live = gi.tier < 2 && gi.n_mem > 0;
     const Span sp = gu_wave_span<HT, CT, MT>(p, gi, j, h);
     const int wb = wave * (p.w_lds_gu / 8) + sp.off + r * sp.rb;
-    float acc[MT];
     item_dot<WT, AM, MT>(smem, wb, gi.n_mem, p.d_model, live, av, acc, grid_off);
-    if ((threadIdx.x & 15) == 0) {
-        const int y = GU_HR * gu_wave_half<MT>(h) + 4 * (wave & 7) + r;
-#pragma unroll
-        for (int c = 0; c < MT; ++c) s_y[y][c] = acc[c];
-    }
 }
 
-// GEGLU of the item's gate rows with its up rows for every member (s_y: row
-// i of the gate half at i, of the up half at 32 + i), and each member's 32
-// values quantised (q8_0 / q8_1, block j of the pair's down activation) into
-// the pair's down column
+// the row of s_y the lane's row sums go to: 32 half + 4 (w mod 8) + row
+template <int MT>
+__device__ __forceinline__ int gu_y_row(int h) {
+    return GU_HR * gu_wave_half<MT>(h) + 4 * ((threadIdx.x >> 6) & 7) + ((threadIdx.x >> 4) & 3);
+}
+
+// Each member's 32 GEGLU values (s_y: the gate rows at i -- one token: their
+// GELU factors, geglu_factor --, the up rows at 32 + i) quantised (q8_0 / q8_1, block j of the
+// pair's down activation) into the pair's down column: wave c takes member c
+// (32 lanes).  One barrier: s_y is kept per item parity, so the next item's
+// rows cannot overwrite what a slower wave still reads.
 template <int AM, int MT, int GSRC>
-__device__ __forceinline__ void gu_epilogue(const DecParams & p, const GroupInfo & gi, int j, float (*s_y)[MT],
-                                            float (*s_act)[DEC_GU_BLK]) {
+__device__ __forceinline__ void gu_epilogue(const DecParams & p, const GroupInfo & gi, int j,
+                                            const float (*s_y)[MT]) {
     const int T = p.T, K = p.top_k, F = p.n_ff;
-    const bool live = gi.tier < 2 && gi.n_mem > 0;
-    __syncthreads();
-    if ((int)threadIdx.x < GU_HR * MT) {
-        const int i = threadIdx.x % GU_HR, c = threadIdx.x / GU_HR;
-        s_act[c][i] = geglu1<GSRC>(s_y[i][c], s_y[GU_HR + i][c]);
-    }
-    __syncthreads();
-    // member c's block j, one wave a member (32 lanes)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (live && wave < gi.n_mem) {
+    __syncthreads();
+    if (gi.tier < 2 && wave < gi.n_mem) {
         ActView L;
         act_layout(F, 0, &L);
         const int pair = max(0, min(member(gi, wave), T * K - 1));
-        const float v = lane < DEC_GU_BLK ? s_act[wave][lane] : 0.0f;
-        q8_32_put<AM>(p.yq + (int64_t)pair * p.yq_stride, L, v, DEC_GU_BLK * j + (lane & 31), lane < DEC_GU_BLK);
+        const int i = lane & 31;
+        const float f = MT == 1 ? s_y[i][wave] : geglu_factor<GSRC>(s_y[i][wave]);
+        const float v = lane < DEC_GU_BLK ? geglu_apply<GSRC>(f, s_y[GU_HR + i][wave]) : 0.0f;
+        q8_32_put<AM>(p.yq + (int64_t)pair * p.yq_stride, L, v, DEC_GU_BLK * j + i, lane < DEC_GU_BLK);
     }
 }
 
@@ -658,8 +653,7 @@ void k_dec_gate_up(const DecParams p) {
     SelScratch * s_sel = sr.sel;
     __shared__ GroupInfo s_grp[DEC_PMAX];     // kept for every item of the workgroup
     __shared__ int s_ng;
-    __shared__ float s_y[2 * GU_HR][MT];
-    __shared__ float s_act[MT][DEC_GU_BLK];
+    __shared__ float s_y[2][2 * GU_HR][MT];   // by item parity (the epilogue has one barrier)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int T = p.T, K = p.top_k, E = p.n_expert, d_in = p.d_model, F = p.n_ff;
 
@@ -760,15 +754,28 @@ void k_dec_gate_up(const DecParams p) {
     // 5. the steps: (item, half) -- one token: both halves in one step.  A
     //    wave dots its rows once they have landed, starts its rows of the
     //    next step, and after an item's up rows the workgroup's epilogue runs
-    //    (its barriers order s_y and s_act between the waves)
+    //    (its barrier orders s_y between the waves)
     __syncthreads();                                      // the columns and the codebook
+    int par = 0;
     while (true) {
         ActView av[MT];
 #pragma unroll
         for (int c = 0; c < MT; ++c) act_layout(d_in, a0 + max(0, min(member(gi, c) / K, T - 1)) * abytes, &av[c]);
         __builtin_amdgcn_s_waitcnt(0);                    // this wave's rows have landed
-        if (gi.tier == 0) gu_wave_dots<HT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
-        else gu_wave_dots<CT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, s_y);
+        float acc[MT];
+        if (gi.tier == 0) gu_wave_dots<HT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, acc);
+        else gu_wave_dots<CT, HT, CT, AM, MT>(p, gi, j, h, smem, av, grid_off, acc);
+        // one token: a gate row's sum becomes its GELU factor at once (the
+        // table read is in flight while the up waves finish); 2-4 tokens:
+        // the sums, the epilogue takes the factors
+        if ((threadIdx.x & 15) == 0) {
+            if (MT == 1 && gu_wave_half<MT>(h) == 0) {
+                s_y[par][gu_y_row<MT>(h)][0] = geglu_factor<GSRC>(acc[0]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < MT; ++c) s_y[par][gu_y_row<MT>(h)][c] = acc[c];
+            }
+        }
         const bool last = h + gu_halves<MT>() >= 2;       // the item's up rows are done
         int nit = it, nj = j, nh = h + gu_halves<MT>();
         GroupInfo nx = gi;
@@ -778,7 +785,10 @@ void k_dec_gate_up(const DecParams p) {
             if (nit < n_items) nx = item(nit, &nj);
         }
         if (nit < n_items) gu_wave_load<HT, CT, MT>(p, nx, nj, nh, smem);   // in flight meanwhile
-        if (last) gu_epilogue<AM, MT, GSRC>(p, gi, j, s_y, s_act);
+        if (last) {
+            gu_epilogue<AM, MT, GSRC>(p, gi, j, s_y[par]);
+            par ^= 1;
+        }
         if (nit >= n_items) break;
         it = nit;
         j = nj;

@@ -130,6 +130,25 @@ __device__ __forceinline__ float geglu1(float g, float u) {
     return __fmul_rn((float)__builtin_bit_cast(_Float16, y), u);
 }
 
+// GEGLU in two parts, for a gate value known before its up value: the
+// factor f of g (the table entry, g itself at or above 10, NaN for the zero
+// below -10) and then the product; geglu_apply(geglu_factor(g), u) ==
+// geglu1(g, u) bit for bit
+template <int SRC>
+__device__ __forceinline__ float geglu_factor(float g) {
+    if (SRC == SRC_GEGLU_TANH || SRC == SRC_GEGLU_TANH_COH) return gelu_tanh(g);
+    if (g <= -10.0f) return __builtin_nanf("");
+    if (g >= 10.0f) return g;
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)g);
+    const uint32_t mag = min(h & 0x7FFFu, (uint32_t)LLAPIS_GELU_TAB_SPAN - 1u);
+    return (float)__builtin_bit_cast(_Float16, gelu_f16_table[mag + (h >> 15) * LLAPIS_GELU_TAB_SPAN]);
+}
+template <int SRC>
+__device__ __forceinline__ float geglu_apply(float f, float u) {
+    if (SRC == SRC_GEGLU_TANH || SRC == SRC_GEGLU_TANH_COH) return __fmul_rn(f, u);
+    return f != f ? 0.0f : __fmul_rn(f, u);
+}
+
 // ----------------------------------------------- wave reductions (wave64)
 
 __device__ __forceinline__ float wave_max(float v) {
