@@ -839,7 +839,8 @@ __device__ __forceinline__ void dn_pair_load(DnPair & q, const uint8_t * src) {
 }
 
 // the member activation's 32-block b from LDS: 32 int8 values, its scale
-// (and q8_1 sum)
+// and its sum (q8_1: of the values, stored as fp16; q8_0: of the int8
+// values, exact)
 struct Act32 {
     u32x4 lo, hi;
     float d, s;
@@ -851,72 +852,83 @@ __device__ __forceinline__ Act32 act32(const uint8_t * smem, const ActView & av,
     a.lo = lds128(smem, ao);
     a.hi = lds128(smem, ao + 16);
     a.d = reinterpret_cast<const float *>(smem + av.d32)[b];
-    a.s = AM == AM_CPU ? 0.0f : reinterpret_cast<const float *>(smem + av.s32)[b];
+    a.s = reinterpret_cast<const float *>(smem + av.s32)[b];
     return a;
+}
+
+// A block of a down row's pair, decoded once for every member's column: its
+// 32 weights as int8 (v[2 i]: values 4 i .. 4 i + 3, v[2 i + 1]: 16 + 4 i ..;
+// Q5_0: q in 0 .. 31, IQ4_NL: the table values) and its scale
+struct DnBlk {
+    uint32_t v[8];
+    float d;
+};
+// bit j of the nibble n4 / 16 (n4 = nibble << 4) at bit 4 of byte j
+__device__ __forceinline__ uint32_t q5_hi4(uint32_t n4) { return __umul24(n4, 0x204081u) & 0x10101010u; }
+template <int T>
+__device__ __forceinline__ DnBlk dn_block(const DnPair & q, int h) {
+    DnBlk b;
+    uint32_t d16, qs[4];
+    if (T == T_Q5_0) {
+        uint32_t qh;
+        if (h == 0) {
+            d16 = q.w[0] & 0xFFFF;
+            qh = __builtin_amdgcn_alignbit(q.w[1], q.w[0], 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[2 + i], q.w[1 + i], 16);
+        } else {
+            d16 = q.w[5] >> 16;
+            qh = q.w[6];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qs[i] = q.w[7 + i];
+        }
+        // the fifth bits: value 4 i + j from qh bit 4 i + j, value 16 + 4 i + j from bit 16 + 4 i + j
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo4 = (i == 0 ? qh << 4 : qh >> (4 * i - 4)) & 0xF0u;
+            const uint32_t hi4 = (qh >> (12 + 4 * i)) & 0xF0u;
+            b.v[2 * i] = (qs[i] & 0x0F0F0F0Fu) | q5_hi4(lo4);
+            b.v[2 * i + 1] = ((qs[i] >> 4) & 0x0F0F0F0Fu) | q5_hi4(hi4);
+        }
+    } else {
+        if (h == 0) {
+            d16 = q.w[0] & 0xFFFF;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[1 + i], q.w[i], 16);
+        } else {
+            d16 = q.w[4] >> 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qs[i] = q.w[5 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            b.v[2 * i] = iq4nl_lookup(qs[i] & 0x0F0F0F0Fu);
+            b.v[2 * i + 1] = iq4nl_lookup((qs[i] >> 4) & 0x0F0F0F0Fu);
+        }
+    }
+    b.d = h2f(d16);
+    return b;
 }
 
 // Q5_0 . q8_0 (ggml-cpu/quants.c:314-352):  d_w d8 sum (q - 16) a
 // Q5_0 . q8_1 (ggml-cuda/vecdotq.cuh:172-198): d_w (d8 sum q a - 16 s8)
-// block h (0, 1) of the pair
-template <int AM>
-__device__ __forceinline__ float q5_0_block(const DnPair & q, int h, const Act32 & a) {
-    uint32_t d16, qh, qs[4];
-    if (h == 0) {
-        d16 = q.w[0] & 0xFFFF;
-        qh = __builtin_amdgcn_alignbit(q.w[1], q.w[0], 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[2 + i], q.w[1 + i], 16);
-    } else {
-        d16 = q.w[5] >> 16;
-        qh = q.w[6];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = q.w[7 + i];
-    }
-    const uint32_t al[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w}, ah[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
-    int sumi = 0, suma = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t vh0 = qh >> (4 * i), vh1 = qh >> (16 + 4 * i);
-        uint32_t v0 = qs[i] & 0x0F0F0F0Fu;
-        v0 |= (vh0 << 4) & 0x10u; v0 |= (vh0 << 11) & 0x1000u; v0 |= (vh0 << 18) & 0x100000u; v0 |= (vh0 << 25) & 0x10000000u;
-        uint32_t v1 = (qs[i] >> 4) & 0x0F0F0F0Fu;
-        v1 |= (vh1 << 4) & 0x10u; v1 |= (vh1 << 11) & 0x1000u; v1 |= (vh1 << 18) & 0x100000u; v1 |= (vh1 << 25) & 0x10000000u;
-        sumi = dot4((int)v0, (int)al[i], sumi);
-        sumi = dot4((int)v1, (int)ah[i], sumi);
-        if (AM == AM_CPU) {
-            suma = dot4(0x01010101, (int)al[i], suma);
-            suma = dot4(0x01010101, (int)ah[i], suma);
-        }
-    }
-    const float d = h2f(d16);
-    if (AM == AM_CPU) return __fmul_rn(d * a.d, (float)(sumi - 16 * suma));
-    return d * ((float)sumi * a.d - 16.0f * a.s);
-}
-
 // IQ4_NL . q8_0 (ggml-cpu/quants.c:1203-1228) and . q8_1 (vecdotq.cuh:1270-1289):
 //   d_w d8 sum kvalues[q] a
-template <int AM>
-__device__ __forceinline__ float iq4nl_block(const DnPair & q, int h, const Act32 & a) {
-    uint32_t d16, qs[4];
-    if (h == 0) {
-        d16 = q.w[0] & 0xFFFF;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbit(q.w[1 + i], q.w[i], 16);
-    } else {
-        d16 = q.w[4] >> 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = q.w[5 + i];
-    }
+template <int AM, int T>
+__device__ __forceinline__ float dn_dot(const DnBlk & b, const Act32 & a) {
     const uint32_t al[4] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w}, ah[4] = {a.hi.x, a.hi.y, a.hi.z, a.hi.w};
     int sumi = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        sumi = dot4((int)iq4nl_lookup(qs[i] & 0x0F0F0F0Fu), (int)al[i], sumi);
-        sumi = dot4((int)iq4nl_lookup((qs[i] >> 4) & 0x0F0F0F0Fu), (int)ah[i], sumi);
+        sumi = dot4((int)b.v[2 * i], (int)al[i], sumi);
+        sumi = dot4((int)b.v[2 * i + 1], (int)ah[i], sumi);
     }
-    const float d = h2f(d16);
-    if (AM == AM_CPU) return __fmul_rn(a.d * d, (float)sumi);
-    return (d * a.d) * (float)sumi;
+    if (T == T_Q5_0) {
+        if (AM == AM_CPU) return __fmul_rn(b.d * a.d, (float)(sumi - 16 * (int)a.s));
+        return b.d * ((float)sumi * a.d - 16.0f * a.s);
+    }
+    if (AM == AM_CPU) return __fmul_rn(a.d * b.d, (float)sumi);
+    return (b.d * a.d) * (float)sumi;
 }
 
 // max over each group of 8 lanes (lanes 8 m .. 8 m + 7), in every lane of it
@@ -947,6 +959,11 @@ __device__ __forceinline__ void q8_quad(uint8_t * col, const ActView & L, const 
             q[j] = r > 127 ? 127 : (r < -128 ? -128 : r);
         }
         dstore = round_to_half(amax / 127.f);
+        int qs = q[0] + q[1] + q[2] + q[3];                 // the block's sum of q (exact)
+        qs += __builtin_amdgcn_update_dpp(0, qs, 0xB1, 0xF, 0xF, false);
+        qs += __builtin_amdgcn_update_dpp(0, qs, 0x4E, 0xF, 0xF, false);
+        qs += __shfl_xor(qs, 4, 8);
+        sstore = (float)qs;
     } else {
         const float d = amax / 127.0f;
         float s = __fadd_rn(__fadd_rn(v[0], v[1]), __fadd_rn(v[2], v[3]));
@@ -964,7 +981,7 @@ __device__ __forceinline__ void q8_quad(uint8_t * col, const ActView & L, const 
         *reinterpret_cast<uint32_t *>(col + L.q + qpos(4 * c4)) = w;
         if ((c4 & 7) == 0) {
             reinterpret_cast<float *>(col + L.d32)[c4 >> 3] = dstore;
-            if (AM != AM_CPU) reinterpret_cast<float *>(col + L.s32)[c4 >> 3] = sstore;
+            reinterpret_cast<float *>(col + L.s32)[c4 >> 3] = sstore;
         }
     }
 }
@@ -1077,15 +1094,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
         if (live) {
 #pragma unroll
-            for (int c = 0; c < MT; ++c) {
-                if (c >= d.n_mem) break;
-                ActView av;
-                act_layout(F, max(0, min(d.mem[c], P - 1)) * abytes, &av);
+            for (int h = 0; h < 2; ++h) {
+                const DnBlk bk = kc == 0 ? dn_block<HD>(cur, h) : dn_block<CD>(cur, h);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int c = 0; c < MT; ++c) {
+                    if (c >= d.n_mem) break;
+                    ActView av;
+                    act_layout(F, max(0, min(d.mem[c], P - 1)) * abytes, &av);
                     const Act32 a = act32<AM>(smem, av, 2 * lane16 + h);
-                    acc[c] += kc == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(cur, h, a) : iq4nl_block<AM>(cur, h, a))
-                                      : (CD == T_Q5_0 ? q5_0_block<AM>(cur, h, a) : iq4nl_block<AM>(cur, h, a));
+                    acc[c] += kc == 0 ? dn_dot<AM, HD>(bk, a) : dn_dot<AM, CD>(bk, a);
                 }
             }
         }
@@ -1187,15 +1204,15 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
         for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
         if (lane16 < NP) {
 #pragma unroll
-            for (int c = 0; c < MT; ++c) {
-                if (c >= nm) break;
-                ActView av;
-                act_layout(F, c * abytes, &av);
+            for (int h = 0; h < 2; ++h) {
+                const DnBlk bk = gi.tier == 0 ? dn_block<HD>(w[ps], h) : dn_block<CD>(w[ps], h);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int c = 0; c < MT; ++c) {
+                    if (c >= nm) break;
+                    ActView av;
+                    act_layout(F, c * abytes, &av);
                     const Act32 a = act32<AM>(smem, av, 2 * lane16 + h);
-                    acc[c] += gi.tier == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a))
-                                           : (CD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a));
+                    acc[c] += gi.tier == 0 ? dn_dot<AM, HD>(bk, a) : dn_dot<AM, CD>(bk, a);
                 }
             }
         }
@@ -1469,8 +1486,7 @@ __global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const Act32 a = act32<AM>(smem, L, 2 * lane16 + h);
-                acc += tier == 0 ? (HD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a))
-                                 : (CD == T_Q5_0 ? q5_0_block<AM>(w[ps], h, a) : iq4nl_block<AM>(w[ps], h, a));
+                acc += tier == 0 ? dn_dot<AM, HD>(dn_block<HD>(w[ps], h), a) : dn_dot<AM, CD>(dn_block<CD>(w[ps], h), a);
             }
         }
 #pragma unroll

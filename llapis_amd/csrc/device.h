@@ -198,6 +198,16 @@ __device__ __forceinline__ float half_max_dpp(float v) {
     const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
     return (threadIdx.x & 32) ? fmaxf(r2, r3) : fmaxf(r0, r1);
 }
+// integer sum over each 32-lane half of the wave, in every lane of it
+__device__ __forceinline__ int half_sum_dpp_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);   // row (16-lane) sum in every lane
+    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += dpp_f<0xB1>(0.0f, v);
     v += dpp_f<0x4E>(0.0f, v);
@@ -322,6 +332,9 @@ __device__ __forceinline__ void q8_32_put(uint8_t * base, const ActView & L, flo
         qi = (int)rintf(__fmul_rn(v, id));
         qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
         dstore = round_to_half(d);
+        // the block's sum of q (exact), for the q8_0 dots' - 16 sum a term
+        const int qs = half_sum_dpp_i(live ? qi : 0);
+        if (live && (lane & 31) == 0) s32[pos >> 5] = (float)qs;
     } else {
         float s = v;
         for (int o = 16; o >= 1; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, 32));
