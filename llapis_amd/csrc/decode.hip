@@ -802,8 +802,11 @@ void k_dec_gate_up(const DecParams p) {
 constexpr int DN_LPR = 16;      // lanes per row: lane l holds the row's block pair l (blocks 2 l, 2 l + 1)
 constexpr int DN_RPP = WG / DN_LPR;   // rows per pass
 constexpr int DN_CL = 8;        // 16-byte chunks of the pairs' down columns per thread loaded first
-constexpr int DN_GRP_NPS = 2;   // passes of 16 rows of a down-by-group workgroup, all in flight
-constexpr int DN_GRP_ROWS = DN_GRP_NPS * DN_RPP;
+constexpr int DN_GRP_NPS = 2;   // passes of a down-by-group workgroup (dn_grp_rpp rows each), all in flight
+// down by group: a row's NP = n_ff / 64 block pairs take NP consecutive
+// lanes, so a pass covers WG / NP rows (23 at n_ff 704, where 16 lanes a row
+// would leave 5 of them idle)
+__host__ __device__ inline int dn_grp_rpp(int n_ff) { return WG / (n_ff / 64); }
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
 // per-group state of the down kernel, in LDS.  The slab is kept as a byte
@@ -1140,9 +1143,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(1, 4))) void
 }
 
 // C by group (more than one token): workgroup (b, g) computes output rows
-// [b R, b R + R) of group g's expert for the group's members only (R = 16
-// NPS rows, all of them in flight at once: lane l of a row's 16 holds its
-// block pair l), writing the scaled rows y_pair = .scale W a_pair to ydn;
+// [b R, b R + R) of group g's expert for the group's members only (R = NPS
+// passes of dn_grp_rpp rows, all of them in flight at once: lane l of a
+// row's NP holds its block pair l), writing the scaled rows y_pair = .scale
+// W a_pair to ydn;
 // workgroups of groups past the call's count return at once.  Only the
 // members' quantised columns are read (one to four, where the kernel over
 // every group copies all T top_k of them into every workgroup).
@@ -1151,8 +1155,9 @@ template <int HD, int CD, int AM, int MT, int NPS>
 __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     static_assert(!k256<HD>() && !k256<CD>(), "down formats");
-    constexpr int R = NPS * DN_RPP;
+    __shared__ float s_red[NPS][WG][MT];      // the lanes' partial row sums
     const int D = p.d_model, F = p.n_ff, K = p.top_k, T = p.T, P = T * K;
+    const int RPP = dn_grp_rpp(F), R = NPS * RPP;
     const int b = blockIdx.x, r0 = b * R, nr = max(0, min(R, D - r0));
     const int g = blockIdx.y;
     const int ng = max(0, min(p.ctl->n_groups, P));
@@ -1170,8 +1175,9 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
         const int pr = max(0, min(c < nm ? gi.mem[c] : gi.mem[0], P - 1));
         col[c] = yq4[(int64_t)pr * a16 + min((int)threadIdx.x, a16 - 1)];
     }
-    const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
-    const int pl = min(lane16, NP - 1);
+    // lane: row lrow of each pass, block pair pl (lanes past RPP rows idle)
+    const int lrow = threadIdx.x / NP, pl = threadIdx.x - lrow * NP;
+    const bool lane_live = lrow < RPP;
     const int wt = gi.tier == 0 ? HD : CD;
     const int rbytes = (F / 32) * blk_bytes(wt);
     const uint8_t * slab = gi.tier == 0 ? p.hot_dn + (uint64_t)gi.idx * p.hot_dn_stride
@@ -1179,7 +1185,7 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
     DnPair w[NPS];
 #pragma unroll
     for (int ps = 0; ps < NPS; ++ps) {
-        const int r = min(ps * DN_RPP + lrow, max(nr - 1, 0));
+        const int r = min(ps * RPP + min(lrow, RPP - 1), max(nr - 1, 0));
         const uint8_t * src = slab + (uint64_t)(r0 + r) * rbytes + (uint64_t)pl * (2 * blk_bytes(wt));
         if (gi.tier == 0) dn_pair_load<HD>(w[ps], src);
         else dn_pair_load<CD>(w[ps], src);
@@ -1193,16 +1199,15 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
     }
     __syncthreads();
 
-    // 3. the rows: dot, reduce over the row's 16 lanes, scale, store
-    const float scale = gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f)
-                                     : (gi.tier == 1 ? (p.s_cold ? p.s_cold[gi.idx] : 1.0f) : 0.0f);
+    // 3. the rows: each lane dots its block pair, the row's NP partial sums
+    //    meet in LDS and one thread a row adds them in pair order, scales
+    //    and stores
 #pragma unroll
     for (int ps = 0; ps < NPS; ++ps) {
-        const int r = ps * DN_RPP + lrow;
         float acc[MT];
 #pragma unroll
         for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
-        if (lane16 < NP) {
+        if (lane_live) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const DnBlk bk = gi.tier == 0 ? dn_block<HD>(w[ps], h) : dn_block<CD>(w[ps], h);
@@ -1211,22 +1216,31 @@ __global__ __launch_bounds__(WG) void k_dec_down_grp(const DecParams p) {
                     if (c >= nm) break;
                     ActView av;
                     act_layout(F, c * abytes, &av);
-                    const Act32 a = act32<AM>(smem, av, 2 * lane16 + h);
+                    const Act32 a = act32<AM>(smem, av, 2 * pl + h);
                     acc[c] += gi.tier == 0 ? dn_dot<AM, HD>(bk, a) : dn_dot<AM, CD>(bk, a);
                 }
             }
         }
 #pragma unroll
+        for (int c = 0; c < MT; ++c) s_red[ps][threadIdx.x][c] = acc[c];
+    }
+    __syncthreads();
+    const float scale = gi.tier == 0 ? (p.s_hot ? p.s_hot[gi.idx] : 1.0f)
+                                     : (gi.tier == 1 ? (p.s_cold ? p.s_cold[gi.idx] : 1.0f) : 0.0f);
+    // an invalid id's members get zero rows
+    const int nw = gi.tier < 2 ? nm : max(0, min(gi.n_mem, MT));
+    for (int i = threadIdx.x; i < NPS * RPP; i += WG) {
+        const int ps = i / RPP, lr = i - ps * RPP, r = ps * RPP + lr;
+        if (r >= nr) continue;
+        float sum[MT];
+#pragma unroll
+        for (int c = 0; c < MT; ++c) sum[c] = 0.0f;
+        for (int j = 0; j < NP; ++j)
+#pragma unroll
+            for (int c = 0; c < MT; ++c) sum[c] += s_red[ps][lr * NP + j][c];
+#pragma unroll
         for (int c = 0; c < MT; ++c)
-#pragma unroll
-            for (int o = DN_LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, DN_LPR);
-        if (lane16 == 0 && r < nr) {
-            // an invalid id's members get zero rows
-            const int nw = gi.tier < 2 ? nm : max(0, min(gi.n_mem, MT));
-#pragma unroll
-            for (int c = 0; c < MT; ++c)
-                if (c < nw) p.ydn[(int64_t)max(0, min(gi.mem[c], P - 1)) * D + r0 + r] = acc[c] * scale;
-        }
+            if (c < nw) p.ydn[(int64_t)max(0, min(gi.mem[c], P - 1)) * D + r0 + r] = sum[c] * scale;
     }
 }
 
@@ -1614,7 +1628,8 @@ hipError_t launch_decode(const DecParams & p, int hgu, int cgu, int hdn, int cdn
         const int lds = dec_lds_down(p);
         const int rows = 1 << p.dn_rows_log2;
         const dim3 grid((p.d_model + rows - 1) / rows);
-        const dim3 ggrid((p.d_model + DN_GRP_ROWS - 1) / DN_GRP_ROWS, std::min(p.T * p.top_k, DEC_PMAX));
+        const int grows = DN_GRP_NPS * dn_grp_rpp(p.n_ff);
+        const dim3 ggrid((p.d_model + grows - 1) / grows, std::min(p.T * p.top_k, DEC_PMAX));
         const int glds = std::min(p.T, DEC_MAXT) * dec_act_bytes(p.n_ff);
 #define LL_DN(A, B, M) \
         if (hdn == A && cdn == B && am == M) { \
