@@ -526,6 +526,10 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
         m1  = ((s8b >> sh1) >> 4 & 0xF) | (((s47 >> sh1) >> 6 & 3) << 4);
     }
     const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+    // the integer sums below are formed in fp32: every product and partial
+    // sum is an integer below 2^24, so exact (and fp32 multiplies are full
+    // rate, where 32-bit integer ones are not)
+    const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)m0, fm1 = (float)m1;
     const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     uint32_t lo[8], hi[8];
 #pragma unroll
@@ -550,9 +554,10 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
         if (AM == AM_CPU) {
             const float dK = reinterpret_cast<const float *>(smem + av[c].dK)[sb];
             const int * bs = reinterpret_cast<const int *>(smem + av[c].bsum) + sb * 16 + 4 * qq;
-            const int sumi = __mul24(sc0, dot1) + __mul24(sc1, dot2);
-            const int summ = __mul24(m0, bs[0] + bs[1]) + __mul24(m1, bs[2] + bs[3]);
-            acc[c] += __fmul_rn(d * dK, (float)sumi) - __fmul_rn(dmin * dK, (float)summ);
+            // |dot| <= 32 * 15 * 128, sc and m <= 63, |bs| <= 16 * 128
+            const float sumi = __fmaf_rn(fsc0, (float)dot1, __fmul_rn(fsc1, (float)dot2));
+            const float summ = __fmaf_rn(fm0, (float)(bs[0] + bs[1]), __fmul_rn(fm1, (float)(bs[2] + bs[3])));
+            acc[c] += __fmul_rn(d * dK, sumi) - __fmul_rn(dmin * dK, summ);
         } else {
             int sq0 = 0, sq1 = 0;
 #pragma unroll
@@ -561,8 +566,8 @@ __device__ __forceinline__ void q4k_unit(const uint8_t * smem, int wb, int u, co
                 sq1 = dot4(0x01010101, (int)ahi[i], sq1);
             }
             const float * d32 = reinterpret_cast<const float *>(smem + av[c].d32) + (sb * 256 + 64 * qq) / 32;
-            const float sd = d32[0] * (float)__mul24(dot1, sc0) + d32[1] * (float)__mul24(dot2, sc1);
-            const float sm = d32[0] * (float)__mul24(sq0, m0) + d32[1] * (float)__mul24(sq1, m1);
+            const float sd = d32[0] * __fmul_rn((float)dot1, fsc0) + d32[1] * __fmul_rn((float)dot2, fsc1);
+            const float sm = d32[0] * __fmul_rn((float)sq0, fm0) + d32[1] * __fmul_rn((float)sq1, fm1);
             acc[c] += d * sd - dmin * sm;
         }
     }
@@ -599,7 +604,7 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
     for (int c = 0; c < NC; ++c) {
         if (c >= nc) break;
         const int ao = av[c].q + sb * 272 + 64 * qq;         // qpos(64 u)
-        int bsum = 0;
+        float bsum = 0.0f;          // an integer below 2^24 (|s| <= 16 * 43 * 128, scales <= 31): exact in fp32
         float accf = 0.0f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -613,7 +618,8 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
                 s[l >> 1] = dot4((int)g1[g], (int)a.y, s[l >> 1]);
             }
             if (AM == AM_CPU) {
-                bsum += __mul24(2 * (int)(scb & 15) + 1, s[0]) + __mul24(2 * (int)(scb >> 4) + 1, s[1]);
+                bsum = __fadd_rn(bsum, __fmaf_rn((float)(2 * (int)(scb & 15) + 1), (float)s[0],
+                                                 __fmul_rn((float)(2 * (int)(scb >> 4) + 1), (float)s[1])));
             } else {
                 const int sumi = (__mul24(s[0], (int)(scb & 15)) + __mul24(s[1], (int)(scb >> 4)) + (s[0] + s[1]) / 2) / 4;
                 const float d8 = reinterpret_cast<const float *>(smem + av[c].d32)[(sb * 256 + 64 * qq + 32 * h) / 32];
@@ -622,7 +628,7 @@ __device__ __forceinline__ void iq2s_unit(const uint8_t * smem, int wb, int u, c
         }
         if (AM == AM_CPU) {
             const float dK = reinterpret_cast<const float *>(smem + av[c].dK)[sb];
-            acc[c] += 0.125f * __fmul_rn(d * dK, (float)bsum);
+            acc[c] += 0.125f * __fmul_rn(d * dK, bsum);
         } else {
             acc[c] += accf;
         }
