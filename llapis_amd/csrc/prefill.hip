@@ -64,7 +64,7 @@ typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 __constant__ Iq2sTables c_iq2s_tab_pf = make_iq2s_tables();
 
-constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged weight row (Q4_K 144, IQ2_S <= 96)
+constexpr int PF_WROW_GU = 144;           // LDS pitch of a staged Q4_K super-block row
 
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -117,12 +117,6 @@ __device__ __forceinline__ uint32_t magic_hi(uint32_t x) { return __builtin_amdg
 
 __device__ __forceinline__ bool tile_valid(const PfParams & p, const PfTile & t) {
     return (t.tier == 0 && t.idx >= 0 && t.idx < p.k_slots) || (t.tier == 1 && t.idx >= 0 && t.idx < p.n_expert);
-}
-
-// 16-byte chunks covering [ps, ps + len) of a slab; they stay inside the
-// slab because slabs are whole 16-byte chunks
-__device__ __forceinline__ int chunk_count(uint64_t ps, int len) {
-    return (int)(((ps + len + 15) >> 4) - (ps >> 4));
 }
 
 // ------------------------------------------------------------ IQ2_S tables
@@ -885,29 +879,38 @@ constexpr Iq2sHalf make_iq2s_half() {
 __constant__ Iq2sHalf c_iq2s_half = make_iq2s_half();
 
 constexpr int PF_XH = 512 + 8;            // halfs per staged token row of one super-block: 256 hi, 256 lo, pad
-constexpr int PF_TOK1 = 32;               // pairs per gate_up group in the q8_1 mode
-constexpr int GU1_XREG = 8;               // activation chunks per thread per super-block (32 tokens x 64)
+constexpr int PF_TOK1Q4 = 48;             // pairs per gate_up group in the q8_1 mode, Q4_K expert
+constexpr int PF_TOK1IQ2 = 32;            // IQ2_S expert (its tables take the room of 16 tokens)
+constexpr int GU1_XREG = 4;               // activation chunks per thread per super-block and 16-token tile (16 x 64)
 
+// The LDS of one workgroup.  An IQ2_S group (its rows go straight to
+// registers) keeps its tables in the room it leaves: the grid selectors and
+// Iq2sHalf past 32 tokens' activations, the sign masks in the row buffer.
 struct GuSmemQ1 {
-    uint8_t w[PF_ROWS * PF_WROW_GU];      // raw super-block rows: Q4_K at 144 r, IQ2_S at 96 r + offset
-    _Float16 x[PF_TOK1 * PF_XH];          // the tokens' d q of this super-block, exact hi and lo parts
-    _Float16 mb[PF_TOK1 * 16];            // their per-32 mins terms u = d sum(q), {hi_0..7, lo_0..7}
-    u32x4 csel[1024];                     // IQ2_S grid: v_perm selectors (lo byte c, hi byte 4 + c) per value pair
-    u32x4 sgnh[256];                      // IQ2_S sign byte: 0x8000 per negative value, per value pair
-    uint2 lsT[16];                        // Iq2sHalf
-    int poff[PF_ROWS];
-    int tok[PF_TOK1], pair[PF_TOK1];
+    uint8_t w[PF_ROWS * PF_WROW_GU];      // Q4_K: the 128 rows of one super-block, [row][144]
+    _Float16 x[PF_TOK1Q4 * PF_XH];        // the tokens' d q of this super-block, exact hi and lo parts
+    _Float16 mb[PF_TOK1Q4 * 16];          // their per-32 mins terms u = d sum(q), {hi_0..7, lo_0..7}, Q4_K
+    int tok[PF_TOK1Q4], pair[PF_TOK1Q4];
+    // IQ2_S grid: v_perm selectors (lo byte c, hi byte 4 + c) per value pair
+    __device__ u32x4 * csel() { return reinterpret_cast<u32x4 *>(x + PF_TOK1IQ2 * PF_XH); }
+    __device__ uint2 * lsT() { return reinterpret_cast<uint2 *>(csel() + 1024); }       // Iq2sHalf
+    // IQ2_S sign byte: 0x8000 per negative value, per value pair
+    __device__ u32x4 * sgnh() { return reinterpret_cast<u32x4 *>(w); }
 };
 static_assert(sizeof(GuSmemQ1) <= 80 * 1024, "two workgroups per CU");
-static_assert(PF_ROWS * GU_STP * 4 <= (int)sizeof(GuSmemQ1::x), "epilogue staging fits the activation buffer");
+static_assert(PF_ROWS * GU_STP * 4 <= PF_TOK1IQ2 * PF_XH * 2, "epilogue staging stays below the IQ2_S tables");
+static_assert((PF_TOK1Q4 - PF_TOK1IQ2) * PF_XH * 2 >= 1024 * 16 + 16 * 8 && (PF_TOK1IQ2 * PF_XH * 2) % 16 == 0,
+              "IQ2_S grid selectors and Iq2sHalf past 32 tokens");
+static_assert(PF_ROWS * PF_WROW_GU >= 256 * 16, "IQ2_S sign masks in the row buffer");
 
+template <int NT>
 struct GuStageQ1 {
     u32x4 w[GU_WREG];
-    u32x4 x[GU1_XREG];
+    u32x4 x[NT * GU1_XREG];
     u32x4 mb;
 };
 
-// One (group of <= 32 pairs, row block) of the gate_up GEMM in the q8_1 activation mode
+// One (group of <= 48 pairs, row block) of the gate_up GEMM in the q8_1 activation mode
 // (ggml-cuda's arithmetic, vecdotq.cuh:504-522 / 864-907): the activation
 // scale is per 32 values, so it is carried by the activation operand -- each
 // value d q as exact fp16 hi + lo parts, two v_mfma_f32_16x16x32_f16 per
@@ -920,18 +923,19 @@ struct GuStageQ1 {
 template <int WT, int GSRC, int NT>
 __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const PfTile & tile, GuSmemQ1 & sm,
                                                     const int rb, const int n) {
-    static_assert(PF_ROWS * 9 <= GU_WREG * WG && PF_TOK1 * 64 == GU1_XREG * WG, "staging shape");
+    static_assert(PF_ROWS * 9 <= GU_WREG * WG && 16 * 64 == GU1_XREG * WG, "staging shape");
     constexpr int NTOK = 16 * NT;
     constexpr bool q4 = WT == T_Q4_K;
     static_assert(q4 || WT == T_IQ2_S, "gate_up formats");
+    constexpr int CAP = q4 ? PF_TOK1Q4 : PF_TOK1IQ2;
+    static_assert(NTOK <= CAP, "group fits the LDS");
     const int F = p.n_ff, D = p.d_model, NSB = D / 256, K = p.top_k;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     constexpr int bb = q4 ? 144 : 82;
-    constexpr int nwc = q4 ? 9 : 6;
     const uint64_t rbytes = (uint64_t)NSB * bb;
     const uint8_t * W = tile.tier == 0 ? p.hot_gu + (uint64_t)tile.idx * p.hot_gu_stride
                                        : p.cold_gu + (uint64_t)tile.idx * p.cold_gu_stride;
-    if (tid < PF_TOK1) {
+    if (tid < NTOK) {
         const int qp = p.sorted[tile.begin + min(tid, n - 1)];
         sm.pair[tid] = qp;
         sm.tok[tid] = qp / K;
@@ -946,65 +950,73 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
             v.y = __builtin_amdgcn_perm(0u, c.x, 0x03030202u) + 0x04000400u;
             v.z = __builtin_amdgcn_perm(0u, c.y, 0x01010000u) + 0x04000400u;
             v.w = __builtin_amdgcn_perm(0u, c.y, 0x03030202u) + 0x04000400u;
-            sm.csel[i] = v;
+            sm.csel()[i] = v;
         }
         u32x4 sg;
         sg.x = ((tid & 1) ? 0x8000u : 0u) | ((tid & 2) ? 0x80000000u : 0u);
         sg.y = ((tid & 4) ? 0x8000u : 0u) | ((tid & 8) ? 0x80000000u : 0u);
         sg.z = ((tid & 16) ? 0x8000u : 0u) | ((tid & 32) ? 0x80000000u : 0u);
         sg.w = ((tid & 64) ? 0x8000u : 0u) | ((tid & 128) ? 0x80000000u : 0u);
-        sm.sgnh[tid] = sg;                                      // WG == 256 sign bytes
-        if (tid < 16) sm.lsT[tid] = make_uint2(c_iq2s_half.t[tid][0], c_iq2s_half.t[tid][1]);
+        sm.sgnh()[tid] = sg;                                    // WG == 256 sign bytes
+        if (tid < 16) sm.lsT()[tid] = make_uint2(c_iq2s_half.t[tid][0], c_iq2s_half.t[tid][1]);
     }
     __syncthreads();
 
+    // Q4_K rows: 128 rows x 9 chunks of one super-block, [row][144] in LDS
     uint32_t wrow[GU_WREG], wdst[GU_WREG];
 #pragma unroll
     for (int k = 0; k < GU_WREG; ++k) {
         const int i = tid + WG * k;
-        const int r = i / nwc, c = i - nwc * r;
+        const int r = i / 9, c = i - 9 * r;
         const int gi = min(64 * rb + (r & 63), F - 1);
         const int row = r < 64 ? gi : F + gi;
         wrow[k] = r < PF_ROWS ? (uint32_t)((uint64_t)row * rbytes) : ~0u;
-        wdst[k] = (uint32_t)(r * (q4 ? 144 : 96) + 16 * c) | ((uint32_t)c << 16);
+        wdst[k] = (uint32_t)(r * 144 + 16 * c) | ((uint32_t)c << 16);
     }
     const int tok_m = tid < 2 * NTOK ? sm.tok[tid >> 1] * NSB * 16 + 8 * (tid & 1) : 0;
-
-    GuStageQ1 g;
-    auto fetch = [&](int s) {
+    // IQ2_S rows go straight to registers (as k_pf_gate_up's): local row
+    // 32 wave + 16 rs + l16 is gate row 64 rb + r (r < 64) or up row
+    // F + 64 rb + r - 64, clamped into the slab
+    uint32_t voff[2], rowpar[2];
 #pragma unroll
-        for (int k = 0; k < GU_WREG; ++k) {
-            g.w[k] = u32x4{0, 0, 0, 0};
-            if (wrow[k] != ~0u) {
-                const uint32_t ps = wrow[k] + (uint32_t)(bb * s);
-                const int c = (int)(wdst[k] >> 16);
-                if (q4 || c < chunk_count(ps, 82))
-                    g.w[k] = *reinterpret_cast<const u32x4 *>(W + (ps & ~15u) + 16 * c);
+    for (int rs = 0; rs < 2; ++rs) {
+        const int r = 32 * wave + 16 * rs + l16;
+        const int gi = min(64 * rb + (r & 63), F - 1);
+        voff[rs] = (uint32_t)((uint64_t)(r < 64 ? gi : F + gi) * rbytes);
+        rowpar[rs] = (voff[rs] >> 1) & 1u;                      // row start mod 4, halved (slabs are 16-aligned)
+    }
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(W), 0, (int)(2u * (uint32_t)F * (uint32_t)rbytes), 0x00020000);
+    Iq2Raw wi[q4 ? 1 : 2];
+
+    GuStageQ1<NT> g;
+    auto fetch = [&](int s) {
+        if constexpr (q4) {
+#pragma unroll
+            for (int k = 0; k < GU_WREG; ++k) {
+                g.w[k] = u32x4{0, 0, 0, 0};
+                if (wrow[k] != ~0u) g.w[k] = *reinterpret_cast<const u32x4 *>(W + wrow[k] + (uint32_t)(bb * s) + 16 * (wdst[k] >> 16));
             }
         }
 #pragma unroll
-        for (int k = 0; k < NT * GU1_XREG / 2; ++k) {
+        for (int k = 0; k < NT * GU1_XREG; ++k) {
             const int i = tid + WG * k, j = i >> 6, c = i & 63;
             g.x[k] = *reinterpret_cast<const u32x4 *>(p.xh + ((int64_t)sm.tok[j] * NSB + s) * 512 + 8 * c);
         }
         if (q4 && tid < 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
     };
     auto store = [&](int s) {
+        if constexpr (q4) {
 #pragma unroll
-        for (int k = 0; k < GU_WREG; ++k)
-            if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(sm.w + (wdst[k] & 0xFFFF)) = g.w[k];
+            for (int k = 0; k < GU_WREG; ++k)
+                if (wrow[k] != ~0u) *reinterpret_cast<u32x4 *>(sm.w + (wdst[k] & 0xFFFF)) = g.w[k];
+        }
 #pragma unroll
-        for (int k = 0; k < NT * GU1_XREG / 2; ++k) {
+        for (int k = 0; k < NT * GU1_XREG; ++k) {
             const int i = tid + WG * k, j = i >> 6, c = i & 63;
             *reinterpret_cast<u32x4 *>(sm.x + j * PF_XH + 8 * c) = g.x[k];
         }
         if (q4 && tid < 2 * NTOK) *reinterpret_cast<u32x4 *>(sm.mb + 16 * (tid >> 1) + 8 * (tid & 1)) = g.mb;
-        if (tid < PF_ROWS) {
-            const int r = tid;
-            const int gi = min(64 * rb + (r & 63), F - 1);
-            const uint64_t ps = (uint64_t)(r < 64 ? gi : F + gi) * rbytes + (uint64_t)bb * s;
-            sm.poff[r] = q4 ? r * 144 : r * 96 + (int)(ps & 15);
-        }
     };
 
     f4 y[2][NT];
@@ -1018,6 +1030,10 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
     const h2 m1024 = h2{(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
 
     fetch(0);
+    if constexpr (!q4) {
+#pragma unroll
+        for (int rs = 0; rs < 2; ++rs) iq2_raw_load(wi[rs], wr, voff[rs], rowpar[rs], 0, q);
+    }
 #pragma unroll 1
     for (int s = 0; s < NSB; ++s) {
         if (s) __syncthreads();
@@ -1025,15 +1041,18 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
         __syncthreads();
         if (s + 1 < NSB) fetch(s + 1);
 
-        // ---- per row tile: the super-block's header
+        // ---- per row tile: the super-block's header (Q4_K from LDS, IQ2_S
+        // from the registers its loads landed in; then the next super-block's
+        // IQ2_S loads are issued)
         int wo[2];
         float dr[2], mr[2];
         h2 scp[2][4];
-        uint2 qh8[2], sc8[2];
+        uint2 qs8[2], sg8[2];
+        uint32_t qh2[2], sc2[2];
         h8 bm[2];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            wo[rs] = sm.poff[32 * wave + 16 * rs + l16];
+            wo[rs] = (32 * wave + 16 * rs + l16) * 144;
             if constexpr (q4) {
                 const u32x4 hdr = *reinterpret_cast<const u32x4 *>(sm.w + wo[rs]);
                 dr[rs] = h2f(hdr.x & 0xFFFF);
@@ -1056,16 +1075,30 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
                     bm[rs][2 * i + 1] = mv.y;
                 }
             } else {
-                dr[rs] = h2f(lds16(sm.w, wo[rs]));
+                // this lane's grid entries 8 q .. 8 q + 7 (values 64 q .. 64 q + 63)
+                const Iq2Raw & w = wi[rs];
+                dr[rs] = h2f((w.d >> w.sh_d) & 0xFFFFu);
                 mr[rs] = 0.0f;
-                qh8[rs] = lds64u(sm.w, wo[rs] + 66);
-                sc8[rs] = lds64u(sm.w, wo[rs] + 74);
+                qs8[rs] = make_uint2(__builtin_amdgcn_alignbit(w.qs.y, w.qs.x, w.sh_q),
+                                     __builtin_amdgcn_alignbit(w.qs.z, w.qs.y, w.sh_q));
+                sg8[rs] = make_uint2(__builtin_amdgcn_alignbit(w.sg.y, w.sg.x, w.sh_q),
+                                     __builtin_amdgcn_alignbit(w.sg.z, w.sg.y, w.sh_q));
+                qh2[rs] = (w.qh >> w.sh_h) & 0xFFFFu;               // 2 bits per entry
+                sc2[rs] = (w.sc >> w.sh_h) & 0xFFFFu;               // 4 bits per two entries
+            }
+        }
+        if constexpr (!q4) {
+            if (s + 1 < NSB) {
+#pragma unroll
+                for (int rs = 0; rs < 2; ++rs) iq2_raw_load(wi[rs], wr, voff[rs], rowpar[rs], s + 1, q);
             }
         }
 
-        // ---- per 32-block j: B (lane (row l16, quarter q): values
-        // 8 q .. 8 q + 7 of block j, exact fp16 integers, scale folded in),
-        // then hi and lo of every token tile into the chained accumulators
+        // ---- per step j: B (lane (row l16, quarter q): Q4_K values 8 q ..
+        // 8 q + 7 of block j, IQ2_S grid entry 8 q + j; exact fp16 integers,
+        // scale folded in), then hi and lo of the same values of every token
+        // tile into the chained accumulators (the super-block's K order is
+        // free: the activation scales are in the parts)
         f4 acc[2][NT];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs)
@@ -1091,16 +1124,14 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
                     hv[2] = h2bits(__builtin_elementwise_fma(as_h2(magic_lo(n1)), sc2, off));
                     hv[3] = h2bits(__builtin_elementwise_fma(as_h2(magic_hi(n1)), sc2, off));
                 } else {
-                    // group 4 j + q: codebook entry, signs, 4-bit scale of its 16
-                    const uint32_t qsw = lds32u(sm.w, wo[rs] + 2 + 4 * j);
-                    const uint32_t sgw = lds32u(sm.w, wo[rs] + 34 + 4 * j);
-                    const uint32_t qhj = __builtin_amdgcn_ubfe(j < 4 ? qh8[rs].x : qh8[rs].y, 8 * (j & 3) + 2 * q, 2);
-                    const uint32_t idx = __builtin_amdgcn_ubfe(qsw, 8 * q, 8) | (qhj << 8);
-                    const uint32_t ls =
-                        __builtin_amdgcn_ubfe(j < 4 ? sc8[rs].x : sc8[rs].y, 8 * (j & 3) + 4 * (q >> 1), 4);
-                    const u32x4 sel = sm.csel[idx];
-                    const u32x4 sg = sm.sgnh[__builtin_amdgcn_ubfe(sgw, 8 * q, 8)];
-                    const uint2 t = sm.lsT[ls];
+                    // grid entry 8 q + j: its index, signs, the 4-bit scale of its 16 values
+                    const uint32_t qsw = j < 4 ? qs8[rs].x : qs8[rs].y, sgw = j < 4 ? sg8[rs].x : sg8[rs].y;
+                    const uint32_t idx = __builtin_amdgcn_ubfe(qsw, 8 * (j & 3), 8) |
+                                         (__builtin_amdgcn_ubfe(qh2[rs], 2 * j, 2) << 8);
+                    const uint32_t ls = __builtin_amdgcn_ubfe(sc2[rs], 4 * (j >> 1), 4);
+                    const u32x4 sel = sm.csel()[idx];
+                    const u32x4 sg = sm.sgnh()[__builtin_amdgcn_ubfe(sgw, 8 * (j & 3), 8)];
+                    const uint2 t = sm.lsT()[ls];
                     hv[0] = __builtin_amdgcn_perm(t.y, t.x, sel.x) | sg.x;
                     hv[1] = __builtin_amdgcn_perm(t.y, t.x, sel.y) | sg.y;
                     hv[2] = __builtin_amdgcn_perm(t.y, t.x, sel.z) | sg.z;
@@ -1110,7 +1141,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
             }
 #pragma unroll
             for (int ts = 0; ts < NT; ++ts) {
-                const _Float16 * xr = sm.x + (16 * ts + l16) * PF_XH + 32 * j + 8 * q;
+                const _Float16 * xr = sm.x + (16 * ts + l16) * PF_XH + (q4 ? 32 * j + 8 * q : 64 * q + 8 * j);
                 h8 ah, al;
                 __builtin_memcpy(&ah, xr, 16);
                 __builtin_memcpy(&al, xr + 256, 16);
@@ -1163,7 +1194,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
             const float gv = stg[(32 * blk + i) * GU_STP + tk];
             const float uv = stg[(64 + 32 * blk + i) * GU_STP + tk];
             const float v = geglu1<GSRC>(gv, uv);
-            const int64_t qp = sm.pair[min(j, PF_TOK1 - 1)];
+            const int64_t qp = sm.pair[min(j, NTOK - 1)];
             q8_store32<AM_Q8_1>(v, p.ah + qp * F + fi + i, p.al + qp * F + fi + i, nullptr, live);
         }
     }
@@ -1172,17 +1203,20 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
 template <int HT, int CT, int GSRC>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_pf_gate_up_q1(const PfParams p) {
     __shared__ __align__(16) GuSmemQ1 sm;
-    // the gate_up groups of this mode hold <= PF_TOK1 pairs; workgroups are
-    // dealt to the XCDs as k_pf_gate_up's (all row blocks of a group on one)
+    // the gate_up groups of this mode hold <= PF_TOK1Q4 pairs of a Q4_K
+    // expert, <= PF_TOK1IQ2 of an IQ2_S one; workgroups are dealt to the XCDs
+    // as k_pf_gate_up's (all row blocks of a group on one)
     const int RB = (p.n_ff + 63) / 64;
     const int i = blockIdx.x, k = i >> 3;
     const int g = 8 * (k / RB) + (i & 7), rb = k - (k / RB) * RB;
     if (g >= *p.n_gtiles) return;
     const PfTile tile = p.gtiles[g];
-    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > PF_TOK1) return;
+    const bool q4 = (tile.tier == 0 ? HT : CT) == T_Q4_K;
+    if (!tile_valid(p, tile) || tile.n <= 0 || tile.n > (q4 ? PF_TOK1Q4 : PF_TOK1IQ2)) return;
     const int n = tile.n;
-    if ((tile.tier == 0 ? HT : CT) == T_Q4_K) {
-        if (n > 16) pf_gate_up_group_q1<T_Q4_K, GSRC, 2>(p, tile, sm, rb, n);
+    if (q4) {
+        if (n > 32) pf_gate_up_group_q1<T_Q4_K, GSRC, 3>(p, tile, sm, rb, n);
+        else if (n > 16) pf_gate_up_group_q1<T_Q4_K, GSRC, 2>(p, tile, sm, rb, n);
         else pf_gate_up_group_q1<T_Q4_K, GSRC, 1>(p, tile, sm, rb, n);
     } else {
         if (n > 16) pf_gate_up_group_q1<T_IQ2_S, GSRC, 2>(p, tile, sm, rb, n);
@@ -1508,13 +1542,15 @@ void launch_gu(int gelu, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const PfPa
 // pairs per gate_up group of an expert in format t (the Q4_K kernel holds
 // 128 tokens' activations in LDS; IQ2_S's tables take the room of half)
 int gate_up_cap(int t) { return t == T_Q4_K ? G2_TOKQ4 : G2_TOKIQ2; }
+// in the q8_1 mode (1 KB of activation parts per token and super-block)
+int gate_up_cap_q1(int t) { return t == T_Q4_K ? PF_TOK1Q4 : PF_TOK1IQ2; }
 }  // namespace
 
 hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cdn, int gelu, hipStream_t s,
                           hipEvent_t * ev) {
     PfParams p = p0;
-    p.gcap[0] = p.act_mode == AM_Q8_1 ? PF_TOK1 : gate_up_cap(hgu);
-    p.gcap[1] = p.act_mode == AM_Q8_1 ? PF_TOK1 : gate_up_cap(cgu);
+    p.gcap[0] = p.act_mode == AM_Q8_1 ? gate_up_cap_q1(hgu) : gate_up_cap(hgu);
+    p.gcap[1] = p.act_mode == AM_Q8_1 ? gate_up_cap_q1(cgu) : gate_up_cap(cgu);
     hipEvent_t e[4] = {};
     if (ev)
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
