@@ -326,6 +326,7 @@ __device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo *
             groups[lane].tier = tier_of(ex, &idx);
             groups[lane].idx = idx;
             groups[lane].n_mem = 1;
+            groups[lane].ord = lane;
             groups[lane].mem[0] = lane;
         }
         if (lane == 0) *n_groups = P;
@@ -345,12 +346,26 @@ __device__ void build_groups(const DecParams & p, const int * s_ids, GroupInfo *
     const bool is_leader = live && leader == lane;
     const uint64_t lm = __ballot(is_leader);
     const int gid_lead = __popcll(lm & lanes_below());
+    // the groups in order of first appearance; .ord lists them in order of
+    // their dot passes, cheapest first (invalid ids: none; a hot expert's
+    // Q4_K dots take about half an IQ2_S expert's; a pass per two members),
+    // ties in order of first appearance
+    int idx = 0, tier = 2, key = 0;
+    const int nm = min(__popc(tm), min(T, DEC_MAXT));
     if (is_leader) {
-        int idx;
-        const int tier = tier_of(ex, &idx);
+        tier = tier_of(ex, &idx);
+        key = tier == 2 ? 0 : (tier == 1 ? 2 : 1) * ((nm + 1) / 2);
+    }
+    int rank = 0;
+    for (int k = 0; k <= 2 * ((DEC_MAXT + 1) / 2); ++k) {
+        const uint64_t b = __ballot(is_leader && key == k);
+        rank += k < key ? __popcll(b) : (k == key ? __popcll(b & lanes_below()) : 0);
+    }
+    if (is_leader) {
         groups[gid_lead].tier = tier;
         groups[gid_lead].idx = idx;
-        groups[gid_lead].n_mem = min(__popc(tm), min(T, DEC_MAXT));
+        groups[gid_lead].n_mem = nm;
+        groups[rank].ord = gid_lead;
         if (valid) s_gid[ex] = gid_lead;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -697,9 +712,16 @@ void k_dec_gate_up(const DecParams p) {
     const int ng = max(0, min(s_ng, DEC_PMAX));
     const int NBLK = F / DEC_GU_BLK, n_items = ng * NBLK;
     if ((int)blockIdx.x >= n_items) return;   // workgroup-uniform (workgroup 0 always has item 0)
-    auto item = [&](int it, int * jo) {
-        const int g = it / NBLK;
-        *jo = it - g * NBLK;
+    // workgroup b takes the items at positions b, b + grid, ...; with more
+    // items than workgroups, positions past the grid (second items) take the
+    // cheapest items and the first workgroups (the ones with a second item)
+    // the next cheapest (the groups taken in .ord order, cheapest first)
+    const int G = (int)gridDim.x, shift = max(0, n_items - G);
+    auto item = [&](int pos, int * jo) {
+        const int it = pos >= G ? pos - G : pos + shift;
+        const int k = it / NBLK;
+        const int g = max(0, min(s_grp[k].ord, ng - 1));
+        *jo = it - k * NBLK;
         return validate_group(p, s_grp[g], ng, g);
     };
 

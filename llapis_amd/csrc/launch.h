@@ -50,7 +50,7 @@ struct GroupInfo {
     int tier;                   // 0 hot (idx = slot), 1 cold (idx = expert), 2 invalid id
     int idx;
     int n_mem;
-    int pad;
+    int ord;                    // the gate_up kernel's item order: group ord is the (this entry's index)-th cheapest
     int mem[DEC_MAXT];          // routed-pair indices, one per member token
 };
 
