@@ -1226,59 +1226,18 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
 // ------------------------------------------------------------------ down
 
-// 8 values (8 u .. 8 u + 7 of 32-block `blk` at LDS byte offset b, 2-aligned)
-// as exact fp16 integers: Q5_0 q - 16 (ggml-quants.c:442), IQ4_NL kvalues[q]
-// (:2653); the block scale d_w out
-template <int T>
-__device__ __forceinline__ h8 down_frag(const uint8_t * sw, int b, int u, float & d) {
-    d = h2f(lds16(sw, b));
-    uint32_t h[4];
-    if constexpr (T == T_Q5_0) {
-        // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
-        const uint2 qs = lds64u(sw, b + 6 + 8 * (u & 1));
-        const uint32_t qh = __builtin_amdgcn_ubfe(lds32u(sw, b + 2), 8 * u, 8);
-        const int sh = 4 * (u >> 1);
-        uint32_t x[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t nib = ((i ? qs.y : qs.x) >> sh) & 0x0F0F0F0Fu;
-            const uint32_t hb = (qh >> (4 * i)) & 15u;
-            x[i] = nib | (((hb * 0x00204081u) & 0x01010101u) << 4);   // bit k -> bit 4 of byte k
-        }
-        const h2 off = h2{(_Float16)(-1040.0f), (_Float16)(-1040.0f)};
-        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
-        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
-        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
-        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
-    } else {
-        // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
-        const uint2 qs = lds64u(sw, b + 2 + 8 * (u & 1));
-        const int sh = 4 * (u >> 1);
-        const h2 off = h2{(_Float16)(-1152.0f), (_Float16)(-1152.0f)};
-        uint32_t x[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) x[i] = iq4nl_lookup(((i ? qs.y : qs.x) >> sh) & 0x0F0F0F0Fu) ^ 0x80808080u;
-        h[0] = h2bits(as_h2(magic_lo(x[0])) + off);
-        h[1] = h2bits(as_h2(magic_hi(x[0])) + off);
-        h[2] = h2bits(as_h2(magic_lo(x[1])) + off);
-        h[3] = h2bits(as_h2(magic_hi(x[1])) + off);
-    }
-    h8 o;
-    __builtin_memcpy(&o, h, 16);
-    return o;
-}
-
 // One (group, 128-row block) of the down GEMM with NT 16-token tiles.  Wave
 // w owns rows 32 w .. 32 w + 31 as two 16-row MFMA tiles.  K (n_ff) runs in
-// chunks of two 32-blocks.  The load unit copies the next chunk's activation
-// parts into LDS while the current one is used (two buffers, separately
-// declared, one barrier per chunk): a pair's chunk is 16 slots of 16 bytes
-// (slots 0..7 the high parts of its 64 values, 8..15 the low parts), slot s
-// at s ^ (pair & 15), so the 16 pairs of an MFMA fragment read 16 distinct
-// slots.  Each lane loads its rows' chunk (44 bytes of Q5_0, 36 of IQ4_NL)
-// straight into registers, the next chunk in flight during the current
-// one's MFMAs.
-constexpr int D2_XB = PF_TOK * 256;                // activations of one chunk: [pair slot][16][16 bytes]
+// chunks of two 32-blocks, CPS chunks a step (groups of up to 32 pairs take
+// two: a small group's step is short, and each step waits for its loads).
+// The load unit copies the next step's activation parts into LDS while the
+// current one's are used (two buffers, separately declared, one barrier per
+// step): a pair's chunk is 16 slots of 16 bytes (slots 0..7 the high parts
+// of its 64 values, 8..15 the low parts), slot s at s ^ (pair & 15), so the
+// 16 pairs of an MFMA fragment read 16 distinct slots.  Each lane loads its
+// rows' window of the step (44 bytes of Q5_0, 36 of IQ4_NL a chunk) straight
+// into registers, the next step's in flight during the current one's MFMAs.
+constexpr int D2_XB = PF_TOK * 256;                // activations of one step: [chunk][pair slot][16][16 bytes]
 
 struct Dn2Lds {
     uint8_t * x0; uint8_t * x1;
@@ -1350,55 +1309,62 @@ __device__ __forceinline__ h8 down_frag_r(const DnWin & w, int u, float & d) {
     return o;
 }
 
-template <int WT, int NT>
+template <int WT, int NT, int CPS>
 __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile & tile, const Dn2Lds & L,
                                                const int rb) {
     static_assert(WT == T_Q5_0 || WT == T_IQ4_NL, "down formats");
     constexpr int NTOK = 16 * NT;
+    static_assert(NTOK * 256 * CPS <= D2_XB, "a step's chunks fit an activation buffer");
     constexpr int BS = WT == T_Q5_0 ? 22 : 18;
-    const int D = p.d_model, F = p.n_ff, NB = F / 32, NC = (NB + 1) / 2;
+    constexpr int CW = BS / 2;                                  // dwords of a chunk (two blocks)
+    constexpr int NW = (4 * CW * CPS + 3 + 15) / 16;            // 16-byte loads of a step's row window
+    const int D = p.d_model, F = p.n_ff, NB = F / 32, NC = (NB + 1) / 2, NS = (NC + CPS - 1) / CPS;
     const int r0 = rb * PF_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, l16 = lane & 15;
     const uint32_t rbytes = (uint32_t)(NB * BS);
     const uint8_t * W = tile.tier == 0 ? p.hot_dn + (uint64_t)tile.idx * p.hot_dn_stride
                                        : p.cold_dn + (uint64_t)tile.idx * p.cold_dn_stride;
-    // the slab as a buffer: a last chunk of one block reads past its row
-    // (unused bytes; past the slab they read as zero)
+    // the slab as a buffer: a last chunk of one block (and a step's window)
+    // reads past its row (unused bytes; past the slab they read as zero)
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), 0,
                                                                          (int)((uint32_t)D * rbytes), 0x00020000);
     if (tid < NTOK) L.pair[tid] = p.sorted[tile.begin + min(tid, tile.n - 1)];
     __syncthreads();
 
-    auto copy_in = [&](int c, uint8_t * xb) {
+    // step s: chunks CPS s .. CPS s + CPS - 1, chunk c of the step at xb + c NTOK 256
+    auto copy_in = [&](int s, uint8_t * xb) {
         const _Float16 * ah = p.ah;
         const _Float16 * al = p.al;
         asm volatile("" : "+s"(ah), "+s"(al));
         // wave w moves pair blocks w NT + k (four pair slots each); a last
         // chunk of one block reads its second block's slots from inside the row
 #pragma unroll
-        for (int k = 0; k < NT; ++k) {
-            const int j = 4 * (wave * NT + k) + (lane >> 4);
-            const int sg = (lane & 15) ^ (j & 15);
-            const uint32_t off = (uint32_t)(L.pair[j] * F + min(64 * c + 8 * (sg & 7), F - 8));
-            lds_dma16((sg < 8 ? ah : al) + off, xb + 1024 * (wave * NT + k));
+        for (int cc = 0; cc < CPS; ++cc) {
+            const int c = min(CPS * s + cc, NC - 1);
+#pragma unroll
+            for (int k = 0; k < NT; ++k) {
+                const int j = 4 * (wave * NT + k) + (lane >> 4);
+                const int sg = (lane & 15) ^ (j & 15);
+                const uint32_t off = (uint32_t)(L.pair[j] * F + min(64 * c + 8 * (sg & 7), F - 8));
+                lds_dma16((sg < 8 ? ah : al) + off, xb + NTOK * 256 * cc + 1024 * (wave * NT + k));
+            }
         }
     };
     uint32_t voff[2];
 #pragma unroll
     for (int rs = 0; rs < 2; ++rs) voff[rs] = (uint32_t)min(r0 + 32 * wave + 16 * rs + l16, D - 1) * rbytes;
-    // raw windows: from the dword at or below the chunk's start (a row of an
-    // odd block count starts 2 bytes into a dword), 48 bytes
-    u32x4 wr0[2], wr1[2], wr2[2];
+    // raw windows: from the dword at or below the step's start (a row of an
+    // odd block count starts 2 bytes into a dword), NW x 16 bytes
+    u32x4 wraw[2][NW];
     uint32_t wsh[2];
-    auto load_rows = [&](int c) {
+    auto load_rows = [&](int s) {
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const uint32_t st = voff[rs] + (uint32_t)(2 * BS * c);
+            const uint32_t st = voff[rs] + (uint32_t)(2 * BS * CPS * s);
             const uint32_t v0 = st & ~3u;
             wsh[rs] = 8u * (st & 3u);
-            wr0[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0, 0, 0);
-            wr1[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0 + 16, 0, 0);
-            wr2[rs] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0 + 32, 0, 0);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) wraw[rs][k] = __builtin_amdgcn_raw_buffer_load_b128(wr, v0 + 16 * k, 0, 0);
         }
     };
 
@@ -1408,58 +1374,77 @@ __device__ __forceinline__ void pf_down2_group(const PfParams & p, const PfTile 
 #pragma unroll
         for (int ts = 0; ts < NT; ++ts) y[rs][ts] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto step = [&](int c, const uint8_t * xb, uint8_t * xn) {
+    auto step = [&](int s, const uint8_t * xb, uint8_t * xn) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        // this chunk's rows out of the registers the loads land in, the next
-        // chunk's copies and loads in flight during the MFMAs
-        DnWin wc[2];
+        // this step's rows out of the registers the loads land in, the next
+        // step's copies and loads in flight during the MFMAs
+        DnWin wc[CPS][2];
 #pragma unroll
         for (int rs = 0; rs < 2; ++rs) {
-            const uint32_t r[12] = {wr0[rs].x, wr0[rs].y, wr0[rs].z, wr0[rs].w, wr1[rs].x, wr1[rs].y,
-                                    wr1[rs].z, wr1[rs].w, wr2[rs].x, wr2[rs].y, wr2[rs].z, wr2[rs].w};
-            uint32_t t[11];
+            uint32_t r[4 * NW];
 #pragma unroll
-            for (int i = 0; i < 11; ++i) t[i] = __builtin_amdgcn_alignbit(r[i + 1], r[i], wsh[rs]);
-            wc[rs].a = u32x4{t[0], t[1], t[2], t[3]};
-            wc[rs].b = u32x4{t[4], t[5], t[6], t[7]};
-            wc[rs].e = u32x3{t[8], t[9], t[10]};
-        }
-        if (c + 1 < NC) {
-            copy_in(c + 1, xn);
-            load_rows(c + 1);
-        }
-        const int cb = min(2, NB - 2 * c);
-        auto block = [&](auto bc) {
-            constexpr int B = decltype(bc)::value;
-            // B operand: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block B
-            h8 bw[2];
-            float dw[2];
-#pragma unroll
-            for (int rs = 0; rs < 2; ++rs) bw[rs] = down_frag_r<WT, B>(wc[rs], q, dw[rs]);
-#pragma unroll
-            for (int ts = 0; ts < NT; ++ts) {
-                const uint8_t * xr = xb + (16 * ts + l16) * 256;
-                h8 ah, al;
-                __builtin_memcpy(&ah, xr + 16 * ((4 * B + q) ^ l16), 16);
-                __builtin_memcpy(&al, xr + 16 * ((8 + 4 * B + q) ^ l16), 16);
-#pragma unroll
-                for (int rs = 0; rs < 2; ++rs) {
-                    const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) y[rs][ts][r] = __builtin_fmaf(dw[rs], sb[r], y[rs][ts][r]);
-                }
+            for (int k = 0; k < NW; ++k) {
+                r[4 * k] = wraw[rs][k].x;
+                r[4 * k + 1] = wraw[rs][k].y;
+                r[4 * k + 2] = wraw[rs][k].z;
+                r[4 * k + 3] = wraw[rs][k].w;
             }
-        };
-        block(std::integral_constant<int, 0>{});
-        if (cb > 1) block(std::integral_constant<int, 1>{});
+#pragma unroll
+            for (int cc = 0; cc < CPS; ++cc) {
+                uint32_t t[11];
+#pragma unroll
+                for (int i = 0; i < 11; ++i) {
+                    const int a = min(CW * cc + i, 4 * NW - 2);
+                    t[i] = __builtin_amdgcn_alignbit(r[a + 1], r[a], wsh[rs]);
+                }
+                wc[cc][rs].a = u32x4{t[0], t[1], t[2], t[3]};
+                wc[cc][rs].b = u32x4{t[4], t[5], t[6], t[7]};
+                wc[cc][rs].e = u32x3{t[8], t[9], t[10]};
+            }
+        }
+        if (s + 1 < NS) {
+            copy_in(s + 1, xn);
+            load_rows(s + 1);
+        }
+#pragma unroll
+        for (int cc = 0; cc < CPS; ++cc) {
+            const int c = CPS * s + cc;
+            if (c < NC) {                                       // workgroup-uniform
+                const int cb = min(2, NB - 2 * c);
+                const uint8_t * xc = xb + NTOK * 256 * cc;
+                auto block = [&](auto bc) {
+                    constexpr int B = decltype(bc)::value;
+                    // B operand: lane (row l16, quarter q) holds values 8 q .. 8 q + 7 of block B
+                    h8 bw[2];
+                    float dw[2];
+#pragma unroll
+                    for (int rs = 0; rs < 2; ++rs) bw[rs] = down_frag_r<WT, B>(wc[cc][rs], q, dw[rs]);
+#pragma unroll
+                    for (int ts = 0; ts < NT; ++ts) {
+                        const uint8_t * xr = xc + (16 * ts + l16) * 256;
+                        h8 ah, al;
+                        __builtin_memcpy(&ah, xr + 16 * ((4 * B + q) ^ l16), 16);
+                        __builtin_memcpy(&al, xr + 16 * ((8 + 4 * B + q) ^ l16), 16);
+#pragma unroll
+                        for (int rs = 0; rs < 2; ++rs) {
+                            const f4 sb = mfma_f16(al, bw[rs], mfma_f16(ah, bw[rs], f4{0.0f, 0.0f, 0.0f, 0.0f}));
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) y[rs][ts][r] = __builtin_fmaf(dw[rs], sb[r], y[rs][ts][r]);
+                        }
+                    }
+                };
+                block(std::integral_constant<int, 0>{});
+                if (cb > 1) block(std::integral_constant<int, 1>{});
+            }
+        }
     };
 
     copy_in(0, L.x0);
     load_rows(0);
-    for (int c = 0; c < NC; c += 2) {
-        step(c, L.x0, L.x1);
-        if (c + 1 < NC) step(c + 1, L.x1, L.x0);
+    for (int s = 0; s < NS; s += 2) {
+        step(s, L.x0, L.x1);
+        if (s + 1 < NS) step(s + 1, L.x1, L.x0);
     }
     const float sc = tile.tier == 0 ? (p.s_hot ? p.s_hot[tile.idx] : 1.0f) : (p.s_cold ? p.s_cold[tile.idx] : 1.0f);
 #pragma unroll
@@ -1496,21 +1481,21 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     static_assert(PF_TOK == 96, "six tile counts");
     if ((tile.tier == 0 ? HT : CT) == T_Q5_0) {
         switch (nt) {
-        case 1: pf_down2_group<T_Q5_0, 1>(p, tile, sm, rb); break;
-        case 2: pf_down2_group<T_Q5_0, 2>(p, tile, sm, rb); break;
-        case 3: pf_down2_group<T_Q5_0, 3>(p, tile, sm, rb); break;
-        case 4: pf_down2_group<T_Q5_0, 4>(p, tile, sm, rb); break;
-        case 5: pf_down2_group<T_Q5_0, 5>(p, tile, sm, rb); break;
-        default: pf_down2_group<T_Q5_0, 6>(p, tile, sm, rb); break;
+        case 1: pf_down2_group<T_Q5_0, 1, 2>(p, tile, sm, rb); break;
+        case 2: pf_down2_group<T_Q5_0, 2, 2>(p, tile, sm, rb); break;
+        case 3: pf_down2_group<T_Q5_0, 3, 1>(p, tile, sm, rb); break;
+        case 4: pf_down2_group<T_Q5_0, 4, 1>(p, tile, sm, rb); break;
+        case 5: pf_down2_group<T_Q5_0, 5, 1>(p, tile, sm, rb); break;
+        default: pf_down2_group<T_Q5_0, 6, 1>(p, tile, sm, rb); break;
         }
     } else {
         switch (nt) {
-        case 1: pf_down2_group<T_IQ4_NL, 1>(p, tile, sm, rb); break;
-        case 2: pf_down2_group<T_IQ4_NL, 2>(p, tile, sm, rb); break;
-        case 3: pf_down2_group<T_IQ4_NL, 3>(p, tile, sm, rb); break;
-        case 4: pf_down2_group<T_IQ4_NL, 4>(p, tile, sm, rb); break;
-        case 5: pf_down2_group<T_IQ4_NL, 5>(p, tile, sm, rb); break;
-        default: pf_down2_group<T_IQ4_NL, 6>(p, tile, sm, rb); break;
+        case 1: pf_down2_group<T_IQ4_NL, 1, 2>(p, tile, sm, rb); break;
+        case 2: pf_down2_group<T_IQ4_NL, 2, 2>(p, tile, sm, rb); break;
+        case 3: pf_down2_group<T_IQ4_NL, 3, 1>(p, tile, sm, rb); break;
+        case 4: pf_down2_group<T_IQ4_NL, 4, 1>(p, tile, sm, rb); break;
+        case 5: pf_down2_group<T_IQ4_NL, 5, 1>(p, tile, sm, rb); break;
+        default: pf_down2_group<T_IQ4_NL, 6, 1>(p, tile, sm, rb); break;
         }
     }
 }

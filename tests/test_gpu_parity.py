@@ -80,6 +80,40 @@ def test_mul_mat_id_vs_oracle(gpu, oracle, wtype, d_in, d_out, act_mode, fused):
     la.lib().llapis_set_modes(la.ACT_CPU, la.GELU_TABLE)
 
 
+@pytest.mark.parametrize("wtype,d_in,d_out", [(la.Q4_K, 512, 33), (la.IQ2_S, 768, 24), (la.Q5_0, 96, 40)])
+@pytest.mark.parametrize("n_ids", [11, 80])
+def test_mul_mat_id_repeated_and_invalid_ids(gpu, oracle, wtype, d_in, d_out, n_ids):
+    """The fire kernels with experts used by several channels (three and
+    five, and apart), an invalid id (its channel gets zeros) and more than 64
+    channels: every channel against the oracle."""
+    torch = torch_mod()
+    say(f"mul_mat_id repeated ids type={wtype} d_in={d_in} n_ids={n_ids}")
+    la.lib().llapis_set_tuning(6, 1)
+    n_pool = 4
+    rs = la.row_size(wtype, d_in)
+    w = np.concatenate([la.quantize(wtype, la.synth_normal(300 + e, d_out * d_in, 0, 0.02).reshape(d_out, d_in),
+                                    np.ones(d_in, np.float32) if wtype in (la.IQ2_S, la.IQ4_NL) else None)
+                        for e in range(n_pool)])
+    base = [1, 1, 3, 1, 0, 2, 3, 2, 3, 3, 3]
+    ids = np.array([base[i % len(base)] if i != 6 else n_pool + 5 for i in range(n_ids)], np.int32)
+    b = la.synth_normal(17, d_in * n_ids).reshape(n_ids, d_in)
+    dev = {k: torch.from_numpy(v).to(gpu) for k, v in dict(w=w, ids=ids, b=b).items()}
+    y = torch.full((n_ids, d_out), float("nan"), device=gpu)
+    call = L.MoertMmCall(L.MM_W_HOT, 0, None, 0, dev["b"].data_ptr(), n_ids, dev["ids"].data_ptr(), n_ids,
+                         y.data_ptr(), None, None)
+    s = torch.cuda.current_stream().cuda_stream
+    L.check(la.lib().llapis_mul_mat_id(C.byref(call), wtype, dev["w"].data_ptr(), n_pool, d_in, d_out, s), "mm")
+    torch.cuda.synchronize()
+    yg = y.cpu().numpy()
+    for i in range(n_ids):
+        if ids[i] >= n_pool:
+            assert (yg[i] == 0).all(), i
+            continue
+        slab = w[ids[i] * rs * d_out:(ids[i] + 1) * rs * d_out]
+        yo = oracle.matvec(wtype, la.ACT_CPU, slab, d_out, d_in, b[i])
+        assert rel_l2(yg[i], yo) <= 2e-6, (i, rel_l2(yg[i], yo))
+
+
 def test_mul_mat_id_refuses_unaligned_slab(gpu):
     """An expert slab that is not a whole number of 16-byte chunks is refused
     on the host (the kernel streams slabs in 128-bit loads)."""
