@@ -990,20 +990,28 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
     Iq2Raw wi[q4 ? 1 : 2];
 
     GuStageQ1<NT> g;
+    // buffer loads: a lane's offset in its register (fixed over the
+    // super-blocks), the super-block's in the scalar offset
+    const __amdgpu_buffer_rsrc_t xr4 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16 *>(p.xh), 0, (int)((uint32_t)p.T * (uint32_t)NSB * 1024u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t mr4 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16 *>(p.xm), 0, (int)((uint32_t)p.T * (uint32_t)NSB * 32u), 0x00020000);
     auto fetch = [&](int s) {
         if constexpr (q4) {
 #pragma unroll
             for (int k = 0; k < GU_WREG; ++k) {
                 g.w[k] = u32x4{0, 0, 0, 0};
-                if (wrow[k] != ~0u) g.w[k] = *reinterpret_cast<const u32x4 *>(W + wrow[k] + (uint32_t)(bb * s) + 16 * (wdst[k] >> 16));
+                if (wrow[k] != ~0u)
+                    g.w[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, wrow[k] + 16 * (wdst[k] >> 16), bb * s, 0);
             }
         }
 #pragma unroll
         for (int k = 0; k < NT * GU1_XREG; ++k) {
             const int i = tid + WG * k, j = i >> 6, c = i & 63;
-            g.x[k] = *reinterpret_cast<const u32x4 *>(p.xh + ((int64_t)sm.tok[j] * NSB + s) * 512 + 8 * c);
+            g.x[k] = __builtin_amdgcn_raw_buffer_load_b128(xr4, (uint32_t)sm.tok[j] * (uint32_t)(NSB * 1024) + 16u * (uint32_t)c,
+                                                           1024 * s, 0);
         }
-        if (q4 && tid < 2 * NTOK) g.mb = *reinterpret_cast<const u32x4 *>(p.xm + tok_m + 16 * s);
+        if (q4 && tid < 2 * NTOK) g.mb = __builtin_amdgcn_raw_buffer_load_b128(mr4, 2u * (uint32_t)tok_m, 32 * s, 0);
     };
     auto store = [&](int s) {
         if constexpr (q4) {
@@ -1162,7 +1170,7 @@ __device__ __forceinline__ void pf_gate_up_group_q1(const PfParams & p, const Pf
                     const f4 m = mfma_f16(am, bm[rs], f4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        y[rs][ts][r] = __fadd_rn(y[rs][ts][r], __builtin_fmaf(dr[rs], acc[rs][ts][r], -(mr[rs] * m[r])));
+                        y[rs][ts][r] = __builtin_fmaf(-mr[rs], m[r], __builtin_fmaf(dr[rs], acc[rs][ts][r], y[rs][ts][r]));
                 }
             } else {
 #pragma unroll
