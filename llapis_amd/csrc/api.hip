@@ -702,7 +702,8 @@ PfWs pf_ws(const llapis_moe_layer * L, int32_t T) {
 
 bool prefill_eligible(const llapis_moe_layer * L, int32_t T) {
     return g_prefill.load() && T > DEC_MAXT && L->top_k >= 1 &&
-           L->top_k <= PF_MAX_PAIRS && L->n_expert <= 256 && L->n_ff <= PF_MAX_FF && L->d_model % 256 == 0 &&
+           L->top_k <= PF_MAX_PAIRS && L->n_expert <= 256 && L->k_slots <= 256 && L->n_ff <= PF_MAX_FF &&
+           L->d_model % 256 == 0 &&
            L->n_ff % 32 == 0;
 }
 }  // namespace

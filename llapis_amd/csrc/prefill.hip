@@ -162,12 +162,21 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     constexpr int PER = PF_MAX_PAIRS / WG;
     __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_gf[256], s_gr[256], s_hot;
     const int P = p.T * p.top_k, E = p.n_expert;
+    __shared__ int s_se[256], s_ss[256];
     int ev[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int q = threadIdx.x + WG * k;
         const int v = q < P ? p.ids[q] : -1;
         ev[k] = (v >= 0 && v < E) ? v : 256;     // 256: invalid id
+    }
+    // the residency mirrors in the same round of loads (a thread per expert
+    // and per slot), looked up in LDS
+    const int e0 = threadIdx.x, ks = p.k_slots;
+    const int sl = ks > 0 && e0 < E ? p.exp_slot[e0] : -1;
+    if (ks > 0 && e0 < ks) {
+        s_se[e0] = p.slot_exp[e0];
+        s_ss[e0] = p.slot_state[e0];
     }
     for (int i = threadIdx.x; i < 257; i += WG) {
         s_cnt[i] = 0;
@@ -179,16 +188,12 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
     for (int k = 0; k < PER; ++k)
         if (threadIdx.x + WG * k < P) atomicAdd(&s_cnt[ev[k]], 1);
     __syncthreads();
-    const int e0 = threadIdx.x;
     int n_e = 0, tier = 1, idx = e0;
     if (e0 < E) {
         n_e = s_cnt[e0];
-        if (p.k_slots > 0) {
-            const int sl = p.exp_slot[e0];
-            if (sl >= 0 && sl < p.k_slots && p.slot_state[sl] == 2 && p.slot_exp[sl] == e0) {
-                tier = 0;
-                idx = sl;
-            }
+        if (sl >= 0 && sl < ks && s_ss[sl] == 2 && s_se[sl] == e0) {
+            tier = 0;
+            idx = sl;
         }
     }
     const int nt_e = (n_e + PF_TOK - 1) / PF_TOK;
