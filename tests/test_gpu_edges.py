@@ -3,7 +3,8 @@ expert counts that are not a multiple of the wave width, top_k at its limits
 (1 and 16), and placement masks whose slots are FILLING or FREE or whose
 mapping is stale or out of range (ffn_moe.cu:80-130 with policy.h:46: only a
 READY slot whose slot_exp points back at the expert is hot).  Each case runs
-the decode path (1 and 3 tokens) and the prefill path (40 tokens)."""
+the decode path (1 and 3 tokens) and the prefill path (40 tokens), in the
+CPU-parity activation mode and in the q8_1 mode."""
 import copy
 
 import numpy as np
@@ -11,7 +12,7 @@ import pytest
 
 import llapis_amd as la
 from llapis_amd import LayerSpec
-from helpers import layer, rel_l2, tokens
+from helpers import check_layer_bars, layer, oracle_mode, rel_l2, tokens
 from test_gpu_parity import check_flip_tolerant, say, torch_mod
 
 pytestmark = pytest.mark.gpu
@@ -45,14 +46,15 @@ def mixed_mask_layer(spec, seed):
     return lay
 
 
+@pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
 @pytest.mark.parametrize("T", [1, 3, 40])
 @pytest.mark.parametrize("spec_name", list(EDGE_SPECS))
-def test_shapes_and_placement_states(gpu, oracle, spec_name, T):
+def test_shapes_and_placement_states(gpu, oracle, spec_name, T, act_mode, gelu_mode):
     torch = torch_mod()
     spec = EDGE_SPECS[spec_name]
-    say(f"edges {spec_name} T={T}")
+    say(f"edges {spec_name} T={T} act={act_mode}")
     lay = mixed_mask_layer(spec, 700 + spec.n_expert)
-    dl = la.DeviceLayer(lay, gpu)
+    dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
     x = tokens(710 + T, T, spec.d_model)
     out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
     torch.cuda.synchronize()
@@ -60,13 +62,15 @@ def test_shapes_and_placement_states(gpu, oracle, spec_name, T):
     ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, spec.top_k)
     assert np.array_equal(ids_g, ids_o)
     assert np.allclose(w_g, w_o, rtol=1e-5, atol=1e-7)
-    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g)
+    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, oracle_mode(act_mode, T), gelu_mode)
     if T <= 4:
         err = rel_l2(out.cpu().numpy(), out_o)
         say(f"  rel_l2 vs oracle = {err:.3e}")
         assert err <= 1e-4
-    else:
+    elif act_mode == la.ACT_CPU:
         check_flip_tolerant(out.cpu().numpy(), out_o)
+    else:
+        check_layer_bars(out.cpu().numpy(), out_o, say, 0.02)
 
 
 def test_zero_tokens_is_a_no_op(gpu):
