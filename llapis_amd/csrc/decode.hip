@@ -1470,26 +1470,32 @@ __global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
     if ((threadIdx.x & 15) == 0 && row < nr) f.dst[(int64_t)p * f.d_out + r0 + row] = live ? acc[0] : 0.0f;
 }
 
-// down fire (Q5_0 / IQ4_NL weights, d_in a multiple of 64, <= 1024): 32 rows
-// of one pair per workgroup, each row's block pairs loaded straight into
-// registers (as the decode path's down kernels do), the pair's column
-// quantised here (q8_0, or q8_1), y = .scale W a.
+// down fire (Q5_0 / IQ4_NL weights, d_in a multiple of 64, <= 1024): two
+// passes of WG / (d_in / 64) rows of one pair per workgroup (23 rows a pass
+// at n_ff 704), a row's block pairs on consecutive lanes and loaded straight
+// into registers (as the decode path's down kernels do), the row's partial
+// sums added in LDS in pair order; the pair's column quantised here (q8_0,
+// or q8_1), y = .scale W a.
 template <int HD, int CD, int AM>
 __global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int32_t s_m[3][256];
-    constexpr int NPS = 2, R = NPS * DN_RPP;
-    const int p = blockIdx.y, F = f.d_in, D = f.d_out, r0 = blockIdx.x * R, nr = max(0, min(R, D - r0));
+    constexpr int NPS = 2;
+    __shared__ float s_red[NPS][WG];          // the lanes' partial row sums
+    const int p = blockIdx.y, F = f.d_in, D = f.d_out;
+    const int NP = F / 64, RPP = dn_grp_rpp(F), R = NPS * RPP;
+    const int r0 = blockIdx.x * R, nr = max(0, min(R, D - r0));
     if (f.n_live && p >= *f.n_live) return;
-    const int F4 = F / 4, NP = F / 64;
+    const int F4 = F / 4;
     // 1. the pair's column (fp32), then its tier
     const u32x4 a4 = reinterpret_cast<const u32x4 *>(f.cur + (f.cur_shared ? 0 : (int64_t)p * F))[min((int)threadIdx.x, F4 - 1)];
     int e;
     const FireRes rs = fire_resolve(f, p, s_m, &e);
     if (f.kind == 0) fire_count(f, e, rs);
-    // 2. the rows' block pairs
-    const int lrow = threadIdx.x / DN_LPR, lane16 = threadIdx.x % DN_LPR;
-    const int pl = min(lane16, NP - 1);
+    // 2. the rows' block pairs: lane -> row lrow of each pass, block pair pl
+    //    (lanes past RPP rows idle)
+    const int lrow = threadIdx.x / NP, pl = threadIdx.x - lrow * NP;
+    const bool lane_live = lrow < RPP;
     const int tier = rs.tier < 2 ? rs.tier : 1, idx = rs.tier < 2 ? rs.idx : 0;
     const int wt = tier == 0 ? HD : CD;
     const int rbytes = (F / 32) * blk_bytes(wt);
@@ -1497,7 +1503,7 @@ __global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
     DnPair w[NPS];
 #pragma unroll
     for (int ps = 0; ps < NPS; ++ps) {
-        const int r = min(ps * DN_RPP + lrow, max(nr - 1, 0));
+        const int r = min(ps * RPP + min(lrow, RPP - 1), max(nr - 1, 0));
         const uint8_t * src = slab + (uint64_t)(r0 + r) * rbytes + (uint64_t)pl * (2 * blk_bytes(wt));
         if (tier == 0) dn_pair_load<HD>(w[ps], src);
         else dn_pair_load<CD>(w[ps], src);
@@ -1513,21 +1519,27 @@ __global__ __launch_bounds__(WG) void k_fire_k32(const FireParams f) {
     const float scale = f.kind == 1 ? (rs.tier == 0 ? (f.s_hot ? f.s_hot[rs.idx] : 1.0f)
                                                     : (rs.tier == 1 ? (f.s_cold ? f.s_cold[rs.idx] : 1.0f) : 0.0f))
                                     : (rs.tier < 2 ? 1.0f : 0.0f);
-    // 4. the rows
+    // 4. each lane dots its block pair; the row's NP partial sums meet in LDS
+    //    and one thread a row adds them in pair order, scales and stores
 #pragma unroll
     for (int ps = 0; ps < NPS; ++ps) {
-        const int r = ps * DN_RPP + lrow;
         float acc = 0.0f;
-        if (lane16 < NP && rs.tier < 2) {
+        if (lane_live && rs.tier < 2) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const Act32 a = act32<AM>(smem, L, 2 * lane16 + h);
+                const Act32 a = act32<AM>(smem, L, 2 * pl + h);
                 acc += tier == 0 ? dn_dot<AM, HD>(dn_block<HD>(w[ps], h), a) : dn_dot<AM, CD>(dn_block<CD>(w[ps], h), a);
             }
         }
-#pragma unroll
-        for (int o = DN_LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, DN_LPR);
-        if (lane16 == 0 && r < nr) f.dst[(int64_t)p * D + r0 + r] = acc * scale;
+        s_red[ps][threadIdx.x] = acc;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NPS * RPP; i += WG) {
+        const int ps = i / RPP, lr = i - ps * RPP, r = ps * RPP + lr;
+        if (r >= nr) continue;
+        float sum = 0.0f;
+        for (int j = 0; j < NP; ++j) sum += s_red[ps][lr * NP + j];
+        f.dst[(int64_t)p * D + r0 + r] = sum * scale;
     }
 }
 
@@ -1690,7 +1702,8 @@ hipError_t launch_fire(const FireParams & f, int ht, int ct, int am, hipStream_t
 #undef LL_F2
 #undef LL_F
     } else {
-        const dim3 grid((f.d_out + 2 * DN_RPP - 1) / (2 * DN_RPP), P);
+        const int rows = 2 * dn_grp_rpp(f.d_in);              // k_fire_k32's two passes
+        const dim3 grid((f.d_out + rows - 1) / rows, P);
 #define LL_F(A, B, M) if (ht == A && ct == B && am == M) hipLaunchKernelGGL((k_fire_k32<A, B, M>), grid, dim3(WG), lds, s, f); else
 #define LL_F2(A, B) LL_F(A, B, AM_CPU) LL_F(A, B, AM_Q8_1)
         LL_F2(T_Q5_0, T_IQ4_NL) LL_F2(T_Q5_0, T_Q5_0) LL_F2(T_IQ4_NL, T_IQ4_NL) LL_F2(T_IQ4_NL, T_Q5_0)
