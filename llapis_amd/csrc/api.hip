@@ -140,7 +140,7 @@ int32_t llapis_mul_mat_id(const moert_mm_call * c, int32_t w_type, const void * 
         f.hot_stride = f.cold_stride = eb;
         f.dst = static_cast<float *>(c->y);
         f.n_live = c->ne_live;
-        f.w_lds = dev::align16(16 * (int)rb + 32);
+        f.w_lds = dev::align16(dev::fire_gu_rows(d_in) * (int)rb + 32);
         if (fire_lds(f, w_type, w_type) + 16 * 1024 <= max_lds_per_wg()) {
             LL_TRY(launch_fire(f, w_type, w_type, g_act_mode.load(), (hipStream_t)stream));
             return 0;
@@ -477,7 +477,7 @@ int32_t llapis_moe_dual_compute(const llapis_moe_dual_op * op, void * workspace,
             f.rc_hits = g_rc.dev + (size_t)g_rc.nl * g_rc.ne + (size_t)a.il * 2;
         }
         const int rb = (int)std::max(rbytes(w_hot->type, a.d_in), rbytes(w_cold->type, a.d_in));
-        f.w_lds = dev::align16(16 * rb + 32);
+        f.w_lds = dev::align16(dev::fire_gu_rows(a.d_in) * rb + 32);
         if (fire_lds(f, w_hot->type, w_cold->type) + 16 * 1024 <= max_lds_per_wg()) {
             LL_TRY(launch_fire(f, w_hot->type, w_cold->type, g_act_mode.load(), (hipStream_t)stream));
             dir_gate_after_fire(a.il, a.kind, (hipStream_t)stream);

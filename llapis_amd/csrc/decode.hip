@@ -1351,8 +1351,7 @@ __device__ __forceinline__ void fire_count(const FireParams & f, int e, const Fi
     }
 }
 
-constexpr int FIRE_GU_ROWS = 16;        // output rows per workgroup, 256-value block formats
-constexpr int FIRE_GU_LOADS = 7;        // 16-byte weight chunks per thread in flight (16 Q4_K rows of 2816)
+constexpr int FIRE_GU_LOADS = 9;        // 16-byte weight chunks per thread in flight (23 Q4_K rows of 2816)
 constexpr int FIRE_XV = 12;             // fp32 input values per lane (d_in <= 3072)
 
 // q8_K of 256-block b held as v[j] = x[256 b + lane + 64 j] by one wave
@@ -1403,7 +1402,7 @@ __global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr bool IQ2 = HT == T_IQ2_S || CT == T_IQ2_S;
     __shared__ int32_t s_m[3][256];
-    const int p = blockIdx.y, d_in = f.d_in, r0 = blockIdx.x * FIRE_GU_ROWS;
+    const int p = blockIdx.y, d_in = f.d_in, NPL = fire_gu_lanes(d_in), RW = WG / NPL, r0 = blockIdx.x * RW;
     if (f.n_live && p >= *f.n_live) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = p / f.n_used;
@@ -1429,7 +1428,7 @@ __global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
     gi.tier = rs.tier;
     gi.idx = rs.idx;
     gi.n_mem = 1;
-    const int nr = min(FIRE_GU_ROWS, f.d_out - r0);
+    const int nr = min(RW, f.d_out - r0);
     const Span sp = make_span(gi, r0, nr, d_in, HT, CT, f.hot, f.hot_stride, f.cold, f.cold_stride, f.ids);
     Regs<FIRE_GU_LOADS> st;
     span_load(st, sp);
@@ -1462,12 +1461,27 @@ __global__ __launch_bounds__(WG) void k_fire_k256(const FireParams f) {
     }
     span_store(st, sp, smem);
     __syncthreads();
-    // 4. one row per 16 lanes
-    const int row = threadIdx.x >> 4;
+    // 4. NPL lanes a row, units lr, lr + NPL, ...; the row's partial sums
+    //    meet in LDS and one thread a row adds them in lane order
+    __shared__ float s_red[WG];
+    const int row = threadIdx.x / NPL, lr = threadIdx.x - row * NPL;
     const bool live = sp.valid != 0 && row < nr;
-    float acc[1];
-    rows_dot<HT, CT, AM, 1>(smem, sp.off + row * sp.rb, gi.tier, 1, d_in, live, av, acc, grid_off);
-    if ((threadIdx.x & 15) == 0 && row < nr) f.dst[(int64_t)p * f.d_out + r0 + row] = live ? acc[0] : 0.0f;
+    float acc = 0.0f;
+    if (live) {
+        const int U = d_in / 64, wb = sp.off + row * sp.rb;
+        if (gi.tier == 0) {
+            for (int u = lr; u < U; u += NPL) unit_dot_n<HT, AM, 1>(smem, wb, u, av, 1, &acc, grid_off);
+        } else {
+            for (int u = lr; u < U; u += NPL) unit_dot_n<CT, AM, 1>(smem, wb, u, av, 1, &acc, grid_off);
+        }
+    }
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        float sum = 0.0f;
+        for (int j = 0; j < NPL; ++j) sum += s_red[threadIdx.x * NPL + j];
+        f.dst[(int64_t)p * f.d_out + r0 + threadIdx.x] = sp.valid != 0 ? sum : 0.0f;
+    }
 }
 
 // down fire (Q5_0 / IQ4_NL weights, d_in a multiple of 64, <= 1024): two
@@ -1694,7 +1708,8 @@ hipError_t launch_fire(const FireParams & f, int ht, int ct, int am, hipStream_t
     const int P = f.n_used * f.n_tokens;
     const int lds = fire_lds(f, ht, ct);
     if (k256_type(ht)) {
-        const dim3 grid((f.d_out + FIRE_GU_ROWS - 1) / FIRE_GU_ROWS, P);
+        const int rows = fire_gu_rows(f.d_in);
+        const dim3 grid((f.d_out + rows - 1) / rows, P);
 #define LL_F(A, B, M) if (ht == A && ct == B && am == M) hipLaunchKernelGGL((k_fire_k256<A, B, M>), grid, dim3(WG), lds, s, f); else
 #define LL_F2(A, B) LL_F(A, B, AM_CPU) LL_F(A, B, AM_Q8_1)
         LL_F2(T_Q4_K, T_IQ2_S) LL_F2(T_Q4_K, T_Q4_K) LL_F2(T_IQ2_S, T_IQ2_S) LL_F2(T_IQ2_S, T_Q4_K)

@@ -63,6 +63,18 @@ struct LdsLayout {
 
 LL_HD inline int align16(int x) { return (x + 15) & ~15; }
 
+// The gate_up fire's lanes per row: the largest divisor of the row's
+// 64-value units (d_in / 64) up to 16, so that every lane takes as many
+// units (11 lanes of 4 units at d_in 2816); its rows per workgroup: as many
+// as fit WG lanes (23).
+LL_HD inline int fire_gu_lanes(int d_in) {
+    const int u = d_in / 64;
+    int l = 16;
+    while (l > 1 && u % l) --l;
+    return l;
+}
+LL_HD inline int fire_gu_rows(int d_in) { return WG / fire_gu_lanes(d_in); }
+
 LL_HD inline LdsLayout lds_layout(int w_bytes, int d_in, bool iq2_tables) {
     LdsLayout L;
     L.w = 0;
