@@ -470,44 +470,6 @@ __device__ __forceinline__ void span_store(const Regs<N> & s, const Span & sp, u
     for (int i = threadIdx.x + N * WG; i < sp.nch; i += WG) *reinterpret_cast<u32x4 *>(dst + 16 * i) = sp.src[i];
 }
 
-// the workgroup's items: a contiguous range
-__device__ __forceinline__ void item_range(int n_items, int * i0, int * i1) {
-    *i0 = (int)((int64_t)blockIdx.x * n_items / gridDim.x);
-    *i1 = (int)((int64_t)(blockIdx.x + 1) * n_items / gridDim.x);
-}
-
-// Dots of the rows of a span staged at `sm` (one row per LPR lanes) against
-// the members' columns av[c], c < n_mem <= MT; the row sums are complete in
-// lane lr == 0 of the row.  Tier decides the format.
-template <int HT, int CT, int AM, int MT>
-__device__ __forceinline__ void rows_dot(const uint8_t * sm, int wb, int tier, int n_mem, int d_in, bool live,
-                                         const ActView * av, float * acc, int grid_off) {
-    constexpr int LPR = Fmt<HT>::LPR;
-    const int lr = threadIdx.x % LPR;
-#pragma unroll
-    for (int c = 0; c < MT; ++c) acc[c] = 0.0f;
-    if (live) {
-        const int U = d_in / Fmt<HT>::UNIT;
-        if (tier == 0) {
-            if (MT == 1 || n_mem == 1) {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, 1>(sm, wb, u, av, n_mem, acc, grid_off);
-            } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<HT, AM, MT>(sm, wb, u, av, n_mem, acc, grid_off);
-            }
-        } else {
-            if (MT == 1 || n_mem == 1) {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, 1>(sm, wb, u, av, n_mem, acc, grid_off);
-            } else {
-                for (int u = lr; u < U; u += LPR) unit_dot_n<CT, AM, MT>(sm, wb, u, av, n_mem, acc, grid_off);
-            }
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < MT; ++c)
-#pragma unroll
-        for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
-}
-
 // ---------------------------------------------------------------- B
 
 constexpr int TAB_CHUNKS = (int)(sizeof(Iq2sTables) / 16);
@@ -554,13 +516,6 @@ __device__ __forceinline__ void item_dot(const uint8_t * sm, int wb, int n_mem, 
     for (int c = 0; c < MT; ++c)
 #pragma unroll
         for (int o = LPR / 2; o >= 1; o >>= 1) acc[c] += __shfl_xor(acc[c], o, LPR);
-}
-
-// the half (h 0: gate rows, 1: up rows) of item (group gi, block j)
-template <int HT, int CT>
-__device__ __forceinline__ Span gu_span(const DecParams & p, const GroupInfo & gi, int j, int h) {
-    return make_span(gi, h * p.n_ff + DEC_GU_BLK * j, GU_HR, p.d_model, HT, CT, p.hot_gu, p.hot_gu_stride,
-                     p.cold_gu, p.cold_gu_stride, p.logits);
 }
 
 // Wave w stages and dots four rows of an item: rows 4 (w mod 8) .. + 3 of the

@@ -90,9 +90,6 @@ LL_HD inline LdsLayout lds_layout(int w_bytes, int d_in, bool iq2_tables) {
 
 #if defined(__HIPCC__)
 
-__device__ __forceinline__ uint32_t lds32(const uint8_t * smem, int off) {       // off % 4 == 0
-    return *reinterpret_cast<const uint32_t *>(smem + off);
-}
 // a dword at an even (2-aligned) byte offset
 __device__ __forceinline__ uint32_t lds32u(const uint8_t * smem, int off) {
     const int a = off & ~3;
@@ -162,11 +159,6 @@ __device__ __forceinline__ float geglu_apply(float f, float u) {
 }
 
 // ----------------------------------------------- wave reductions (wave64)
-
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
 // DPP lane moves (quad perms, row mirrors, row broadcasts): cross-lane data
 // without LDS round trips.  CTRL: 0xB1 quad_perm [1,0,3,2], 0x4E quad_perm
@@ -246,10 +238,6 @@ __device__ __forceinline__ int row16_sum(int v) {
     v += dpp_i<0x4E>(0, v);
     v += dpp_i<0x141>(0, v);
     v += dpp_i<0x140>(0, v);
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
@@ -402,16 +390,6 @@ __device__ __forceinline__ void act_batch_quant(uint8_t * base, const ActView & 
         const bool live = pos < d_in;
         const float v = SRC == SRC_PLAIN ? b.g[j] : (live ? geglu1<SRC>(b.g[j], b.u[j]) : 0.0f);
         q8_32_put<AM>(base, L, v, pos, live);
-    }
-}
-
-// the batches after the first (d_in > Q8_BATCH * WG)
-template <int SRC, int AM>
-__device__ __forceinline__ void quantize_q8_32_rest(uint8_t * base, const ActView & L, const ActSrc & src, int d_in) {
-    for (int at0 = (threadIdx.x >> 6) * 64 + Q8_BATCH * WG; at0 < d_in; at0 += Q8_BATCH * WG) {
-        ActBatch b;
-        act_batch_load<SRC>(b, src, d_in, at0);
-        act_batch_quant<SRC, AM>(base, L, b, d_in, at0);
     }
 }
 

@@ -88,9 +88,6 @@ __device__ __forceinline__ uint32_t bytes_mul(uint32_t x, uint32_t s2) {
     __builtin_memcpy(&r, &c, 4);
     return r;
 }
-__device__ __forceinline__ uint32_t lds16(const uint8_t * smem, int off) {   // off even
-    return *reinterpret_cast<const uint16_t *>(smem + off);
-}
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2 as_h2(uint32_t u) {
     h2 v;
@@ -101,14 +98,6 @@ __device__ __forceinline__ uint32_t h2bits(h2 v) {
     uint32_t u;
     __builtin_memcpy(&u, &v, 4);
     return u;
-}
-// 8 bytes at a 2-aligned LDS offset (two dwords)
-__device__ __forceinline__ uint2 lds64u(const uint8_t * smem, int off) {
-    const int a = off & ~3, sh = (off & 3) * 8;
-    const uint32_t w0 = *reinterpret_cast<const uint32_t *>(smem + a);
-    const uint32_t w1 = *reinterpret_cast<const uint32_t *>(smem + a + 4);
-    const uint32_t w2 = *reinterpret_cast<const uint32_t *>(smem + a + 8);
-    return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
 }
 // four small unsigned bytes -> two packed fp16 pairs of (1024 + byte):
 // bytes {0, 1} and {2, 3}
