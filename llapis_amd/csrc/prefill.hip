@@ -1,17 +1,20 @@
 // prefill.hip -- the MoE layer for long token batches (prefill chunks) on
 // gfx950 int8 matrix cores (v_mfma_i32_16x16x64_i8).
 //
-//   k_pf_bucket    routed pairs grouped by expert (a counting sort with LDS
+//   k_pf_prep      one kernel for two independent jobs: its workgroup 0
+//                  buckets, the others quantise the tokens.
+//     pf_bucket    routed pairs grouped by expert (a counting sort with LDS
 //                  atomics) and cut into groups two ways over the same sorted
 //                  list: down groups of <= PF_TOK pairs and gate_up groups
 //                  (their sizes set per tier by the host), each tagged with
 //                  its tier by the residency predicate (ggml-cuda/mmid.cu:
 //                  28-116 groups the same way; moert/cuda/ffn_moe.cu:80-130 is
 //                  the predicate).
-//   k_pf_quant_x   each token quantised once to q8_K (the CPU path's
+//     pf_quant_x   each token quantised once to q8_K (the CPU path's
 //                  activation format for 256-blocks): int8 values, the
 //                  per-256 scale, and the per-32 sums split as 32 hi + lo
-//                  (both exact in fp16) for the Q4_K mins term.
+//                  (both exact in fp16) for the Q4_K mins term
+//                  (pf_quant_x1: q8_1, as exact fp16 parts).
 //   k_pf_gate_up   grouped GEMM per (group, 64 gate rows + the 64 matching up
 //                  rows), on groups of its own (<= 48 pairs of a Q4_K expert,
 //                  <= 64 of an IQ2_S one), the full groups first, every row
@@ -147,7 +150,7 @@ __constant__ Iq2sSplit c_iq2s_split = make_iq2s_split();
 // next slot of its expert.  The order of pairs inside an expert's range is
 // not fixed, and need not be: each pair's output column is computed on its
 // own.
-__global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
+__device__ __forceinline__ void pf_bucket(const PfParams & p) {
     constexpr int PER = PF_MAX_PAIRS / WG;
     __shared__ int s_cnt[257], s_fill[257], s_off[257], s_nt[257], s_gf[256], s_gr[256], s_hot;
     const int P = p.T * p.top_k, E = p.n_expert;
@@ -266,11 +269,11 @@ __global__ __launch_bounds__(WG) void k_pf_bucket(const PfParams p) {
 // One wave per (token, 256-block): q8_K exactly as the CPU path; the int8
 // values, the scale, and the 8 per-32 sums as {hi_0..hi_7, lo_0..lo_7} with
 // sum = 32 hi + lo, 0 <= lo < 32 (each part exact in fp16).
-__global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
+__device__ __forceinline__ void pf_quant_x(const PfParams & p, int blk) {
     __shared__ __align__(16) uint8_t scratch[WG / 64][512];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int NSB = p.d_model / 256;
-    const int job = blockIdx.x * (WG / 64) + wave;
+    const int job = blk * (WG / 64) + wave;
     const bool live = job < p.T * NSB;
     const int t = live ? job / NSB : 0, s = live ? job % NSB : 0;
     ActView L;
@@ -305,10 +308,10 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x(const PfParams p) {
 // [token][256-block] {256 hi, 256 lo}; and per 32-block u = d sum(q) (the
 // Q4_K mins term of vecdotq.cuh's q4_K . q8_1) as exact hi + lo,
 // [token][256-block] {hi_0..hi_7, lo_0..lo_7}.
-__global__ __launch_bounds__(WG) void k_pf_quant_x1(const PfParams p) {
+__device__ __forceinline__ void pf_quant_x1(const PfParams & p, int blk) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int D = p.d_model, per = D / 64;
-    const int job = blockIdx.x * (WG / 64) + wave;
+    const int job = blk * (WG / 64) + wave;
     if (job >= p.T * per) return;                        // whole waves leave
     const int t = job / per, pos = 64 * (job - t * per) + lane;
     const float v = p.x[(int64_t)t * D + pos];
@@ -334,6 +337,16 @@ __global__ __launch_bounds__(WG) void k_pf_quant_x1(const PfParams p) {
         xm[j] = h;
         xm[8 + j] = l;
     }
+}
+
+// Workgroup 0 buckets the pairs; the others quantise the tokens (neither
+// depends on the other), so the quantisation runs while the one bucketing
+// workgroup does and the chunk has one kernel boundary fewer.
+template <int AM>
+__global__ __launch_bounds__(WG) void k_pf_prep(const PfParams p) {
+    if (blockIdx.x == 0) pf_bucket(p);
+    else if (AM == AM_Q8_1) pf_quant_x1(p, blockIdx.x - 1);
+    else pf_quant_x(p, blockIdx.x - 1);
 }
 
 // -------------------------------------------------------------- gate_up
@@ -1542,10 +1555,9 @@ hipError_t launch_prefill(const PfParams & p0, int hgu, int cgu, int hdn, int cd
     if (ev)
         for (int i = 0; i < 4; ++i) e[i] = ev[i];
     const int NSB = p.d_model / 256;
-    hipLaunchKernelGGL(k_pf_bucket, dim3(1), dim3(WG), 0, s, p);
     if (p.act_mode == AM_Q8_1)
-        hipLaunchKernelGGL(k_pf_quant_x1, dim3((p.T * (p.d_model / 64) + 3) / 4), dim3(WG), 0, s, p);
-    else hipLaunchKernelGGL(k_pf_quant_x, dim3((p.T * NSB + 3) / 4), dim3(WG), 0, s, p);
+        hipLaunchKernelGGL(k_pf_prep<AM_Q8_1>, dim3(1 + (p.T * (p.d_model / 64) + 3) / 4), dim3(WG), 0, s, p);
+    else hipLaunchKernelGGL(k_pf_prep<AM_CPU>, dim3(1 + (p.T * NSB + 3) / 4), dim3(WG), 0, s, p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     {
