@@ -124,6 +124,67 @@ __global__ __launch_bounds__(WG) void k_router_mfma(const float * __restrict__ x
         }
 }
 
+// The same tiles and the same MFMA sequence (so the same partial sums, bit
+// for bit) with the whole K split staged at once: every thread issues all of
+// its loads of x and W_r (kc / 16 of each) before the first wait, the
+// workgroup stores them to LDS and meets at one barrier, instead of one
+// load round trip per 16-k slice.  kc <= RKC_MAX (d <= 3072 at RSPLIT 16).
+// The row pitch is 4 mod 32 floats, so the 8 rows of a 16-byte read's lane
+// group fall in different banks.
+constexpr int RKC_MAX = 192, RPITCH = RKC_MAX + 4;
+
+__global__ __launch_bounds__(WG) void k_router_mfma_st(const float * __restrict__ x, int T,
+                                                       const float * __restrict__ w_r, int d, int E, int kc,
+                                                       float * __restrict__ parts) {
+    typedef float f16v __attribute__((ext_vector_type(16)));
+    constexpr int NJ = RKC_MAX / RK;
+    __shared__ __align__(16) float s_x[RT * RPITCH], s_w[RT * RPITCH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 31, h = lane >> 5;
+    const int t0 = blockIdx.x * RT, e0 = blockIdx.y * RT, sp = blockIdx.z;
+    const int nk = kc / RK;
+    const int lr = tid >> 2, lc = 4 * (tid & 3);
+    const float * xs = x + (int64_t)min(t0 + lr, T - 1) * d + sp * kc + lc;
+    const float * ws = w_r + (int64_t)min(e0 + lr, E - 1) * d + sp * kc + lc;
+    // slices past the split (j >= nk) reload its last one into LDS room that
+    // no MFMA reads: no branch, so the values stay in registers
+    float4 gx[NJ], gw[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) gx[j] = *reinterpret_cast<const float4 *>(xs + RK * min(j, nk - 1));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) gw[j] = *reinterpret_cast<const float4 *>(ws + RK * min(j, nk - 1));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        *reinterpret_cast<float4 *>(&s_x[lr * RPITCH + RK * j + lc]) = gx[j];
+        *reinterpret_cast<float4 *>(&s_w[lr * RPITCH + RK * j + lc]) = gw[j];
+    }
+    __syncthreads();
+    const int xo = (32 * (wave >> 1) + r) * RPITCH + 8 * h, wo = (32 * (wave & 1) + r) * RPITCH + 8 * h;
+    f16v acc = {};
+    for (int j = 0; j < nk; ++j) {
+        const float4 xa = *reinterpret_cast<const float4 *>(&s_x[xo + RK * j]);
+        const float4 xb = *reinterpret_cast<const float4 *>(&s_x[xo + RK * j + 4]);
+        const float4 wa = *reinterpret_cast<const float4 *>(&s_w[wo + RK * j]);
+        const float4 wb = *reinterpret_cast<const float4 *>(&s_w[wo + RK * j + 4]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, wa.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, wa.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.z, wa.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.w, wa.w, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.x, wb.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.y, wb.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.z, wb.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xb.w, wb.w, acc, 0, 0, 0);
+    }
+    const int e = e0 + 32 * (wave & 1) + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 32 * (wave >> 1) + 8 * i + 4 * h + j;
+            if (t < T && e < E) parts[((int64_t)sp * T + t) * E + e] = acc[4 * i + j];
+        }
+}
+
 // In place: logits -> probabilities (ggml soft_max: exp(x - max), sum in
 // double, scaled by float(1/sum); ops.cpp:5344-5450), then top-K by
 // descending p with ties to the lower index (argsort_top_k), weights
@@ -414,7 +475,9 @@ int router_parts_floats(int T, int E) { return RSPLIT * T * E; }
 hipError_t launch_router_mfma(const float * x, int T, const float * w_r, int d, int E, float * parts, hipStream_t s) {
     if (d % (16 * RSPLIT) != 0 || T <= 0 || E <= 0) return hipErrorInvalidValue;
     dim3 grid((T + RT - 1) / RT, (E + RT - 1) / RT, RSPLIT);
-    hipLaunchKernelGGL(k_router_mfma, grid, dim3(WG), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
+    if (d / RSPLIT <= RKC_MAX)
+        hipLaunchKernelGGL(k_router_mfma_st, grid, dim3(WG), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
+    else hipLaunchKernelGGL(k_router_mfma, grid, dim3(WG), 0, s, x, T, w_r, d, E, d / RSPLIT, parts);
     return hipGetLastError();
 }
 

@@ -73,6 +73,32 @@ def test_shapes_and_placement_states(gpu, oracle, spec_name, T, act_mode, gelu_m
         check_layer_bars(out.cpu().numpy(), out_o, say, 0.02)
 
 
+@pytest.mark.parametrize("act_mode,gelu_mode", [(la.ACT_CPU, la.GELU_TABLE), (la.ACT_Q8_1, la.GELU_TANH)])
+def test_prefill_wide_model(gpu, oracle, act_mode, gelu_mode):
+    """d_model 4096 at 40 tokens: the router's 16 K splits are 256 values
+    each, past what the staged router kernel holds (192), so the chunk's
+    logits come from the slice-by-slice kernel; 16 super-blocks a row in
+    the grouped GEMMs."""
+    torch = torch_mod()
+    spec = LayerSpec(d_model=4096, n_ff=64, n_expert=16, top_k=2)
+    T = 40
+    say(f"wide d_model=4096 T={T} act={act_mode}")
+    lay = mixed_mask_layer(spec, 730)
+    dl = la.DeviceLayer(lay, gpu, act_mode, gelu_mode)
+    x = tokens(731, T, spec.d_model)
+    out, ids, w = dl.forward(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    ids_g, w_g = ids.cpu().numpy(), w.cpu().numpy()
+    ids_o, w_o, _ = oracle.router(x, lay.router_w, lay.router_b, spec.top_k)
+    assert np.array_equal(ids_g, ids_o)
+    assert np.allclose(w_g, w_o, rtol=1e-5, atol=1e-7)
+    out_o, _ = oracle.moe_experts(lay, x, ids_g, w_g, oracle_mode(act_mode, T), gelu_mode)
+    if act_mode == la.ACT_CPU:
+        check_flip_tolerant(out.cpu().numpy(), out_o)
+    else:
+        check_layer_bars(out.cpu().numpy(), out_o, say, 0.02)
+
+
 def test_zero_tokens_is_a_no_op(gpu):
     """n_tokens = 0: nothing is launched, nothing is written, status 0."""
     torch = torch_mod()
