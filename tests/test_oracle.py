@@ -25,8 +25,12 @@ How each oracle function is pinned:
       q4_K, q5_0, iq4_nl: equal to the float64 dot of the dequantised operands
       (their q8_1 formulas are exact integer sums times scales); iq2_s: within
       the truncation bound of its integer formula (at most one unit of
-      d*d8 per 32 values).  Parity with the reference's CUDA code itself is
-      unpinned (no CUDA compiler here).
+      d*d8 per 32 values).  Known answers worked out by hand from the
+      reference's integer formulas on blocks built field by field pin the
+      two forms that differ from the dequantised dot: iq2_s's divisions
+      truncate toward zero (where floor, rounding or exact arithmetic give
+      other values), q5_0 uses the block's stored sum s.  The reference's
+      CUDA code itself is not run (no CUDA compiler here).
   orc_vec_dot q8_1 matrix-core mode (ACT_Q8_1_MMA: the prefill's sums)
       every format equal to the float64 dot of the dequantised operands: its
       IQ2_S keeps the per-16 scale exact and its Q5_0 uses (q - 16) against
@@ -269,6 +273,107 @@ def test_vec_dot_equals_dequantised_dot(oracle, name, mode):
             assert abs(got - exact) <= bound, (r, got, exact, bound)
         else:
             assert abs(got - exact) <= 3e-6 * scale, (r, got, exact)
+
+
+# Known answers for the two q8_1-mode formulas that are not the dot of the
+# dequantised operands, worked out by hand from the reference's integer
+# arithmetic on blocks built field by field (every scale a power of two, so
+# the float steps are exact):
+#   vec_dot_iq2_s_q8_1 (vecdotq.cuh:1061-1102): per 32-block
+#       sumi = (s0 ls0 + s1 ls1 + (s0 + s1) / 2) / 4 in C integer division
+#       (truncation toward zero), times d d8;
+#   vec_dot_q5_0_q8_1_impl (vecdotq.cuh:172-198): d5 (d8 sum(q5 q8) - 16 s8)
+#       with q5 in 0..31 and s8 the q8_1 block's stored sum, not d8 sum(q8).
+
+def _q8_1_row(d8, s8, q):
+    """q8_1 blocks [d fp16][s fp16][32 x int8] from per-block d8, s8 and the
+    int8 values q (n values)."""
+    nb = len(q) // 32
+    a = np.zeros((nb, 36), np.uint8)
+    a[:, 0:2] = np.asarray(d8, np.float16).reshape(nb, 1).view(np.uint8)
+    a[:, 2:4] = np.asarray(s8, np.float16).reshape(nb, 1).view(np.uint8)
+    a[:, 4:36] = np.asarray(q, np.int8).reshape(nb, 32).view(np.uint8)
+    return a.ravel()
+
+
+def _iq2s_super_block(d, groups, scales):
+    """One block_iq2_s {d fp16, qs[64], qh[8], scales[8]}: groups maps the
+    8-value group l (0..31) to (grid index, sign byte); scales[ib] =
+    (ls0, ls1) of 32-block ib."""
+    b = np.zeros(82, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    for l, (idx, sg) in groups.items():
+        b[2 + l] = idx & 0xFF
+        b[2 + 32 + l] = sg
+        b[2 + 64 + l // 4] |= ((idx >> 8) & 3) << (2 * (l % 4))
+    for ib, (ls0, ls1) in scales.items():
+        b[2 + 64 + 8 + ib] = ls0 | (ls1 << 4)
+    return b
+
+
+def _grid_index_with_first(oracle, v):
+    """The first IQ2_S grid index whose value 0 is v (d = 1, ls = 0: the
+    dequantised value is v / 8)."""
+    for idx in range(1024):
+        w = _iq2s_super_block(1.0, {0: (idx, 0)}, {})
+        if oracle.dequantize(IQ2_S, w, 256)[0] == v / 8.0:
+            return idx
+    raise AssertionError(f"no grid entry starts with {v}")
+
+
+def test_iq2s_q8_1_truncates_toward_zero(oracle):
+    i25, i43 = _grid_index_with_first(oracle, 25), _grid_index_with_first(oracle, 43)
+    d8 = np.ones(8, np.float32)
+
+    def dot(groups, scales, q, d8=d8):
+        return oracle.vec_dot(IQ2_S, ACT_Q8_1, 256, _iq2s_super_block(1.0, groups, scales),
+                              _q8_1_row(d8, np.zeros(8), q))
+
+    q = np.zeros(256, np.int64)
+    q[0] = -1
+    # s0 = -25, ls0 = 3: (-75 + (-25)/2) / 4 = (-75 - 12) / 4 = -87 / 4 = -21
+    # (floor division would give -22, rounding -22, exact arithmetic -21.875)
+    assert dot({0: (i25, 0)}, {0: (3, 0)}, q) == -21.0
+    q[0] = 1
+    assert dot({0: (i25, 0)}, {0: (3, 0)}, q) == 21.0            # 87 / 4
+    assert dot({0: (i25, 0x01)}, {0: (3, 0)}, q) == -21.0         # sign bit 0: value -25
+    # s0 = -25 (ls0 3), s1 = 43 (ls1 5, group 2 = values 16..23):
+    # (-75 + 215 + 18/2) / 4 = 149 / 4 = 37
+    q[0], q[16] = -1, 1
+    groups = {0: (i25, 0), 2: (i43, 0)}
+    assert dot(groups, {0: (3, 5)}, q) == 37.0
+    # plus 32-block 1 at d8 = 1/2: s0 = 75 (q = 3), ls = 0: (75 / 2) / 4 = 37 / 4 = 9
+    q[32] = 3
+    groups[4] = (i25, 0)
+    d8b = d8.copy()
+    d8b[1] = 0.5
+    assert dot(groups, {0: (3, 5)}, q, d8b) == 37.0 + 4.5
+
+
+def test_q5_0_q8_1_uses_the_stored_sum(oracle):
+    # q5 values: 16 everywhere (weight 0) but value 0 = 31 and value 17 = 5
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    qh = 1 << 0                                   # value 0's fifth bit
+    for j in range(16):
+        if j != 0:
+            qh |= 1 << j                          # 16 = 0b10000
+        if j != 1:
+            qh |= 1 << (j + 16)
+    b[2:6] = np.array([qh], np.uint32).view(np.uint8)
+    lo = np.zeros(16, np.int64)
+    hi = np.zeros(16, np.int64)
+    lo[0] = 15                                    # 15 + 16 = 31
+    hi[1] = 5                                     # value 17: fifth bit clear
+    b[6:22] = (lo | (hi << 4)).astype(np.uint8)
+    assert np.array_equal(oracle.dequantize(Q5_0, b, 32)[[0, 17, 5]], [15.0, -11.0, 0.0])
+    q = np.zeros(32, np.int64)
+    q[0], q[17] = 2, -3
+    # sum(q5 q8) = 31*2 + 5*(-3) = 47; stored s8 = 7 (not d8 sum q8 = -1):
+    # 1 * (47 - 16 * 7) = -65 (the (q5 - 16) form would give 63)
+    assert oracle.vec_dot(Q5_0, ACT_Q8_1, 32, b, _q8_1_row([1.0], [7.0], q)) == -65.0
+    # and with s8 = d8 sum(q8) the two forms agree
+    assert oracle.vec_dot(Q5_0, ACT_Q8_1, 32, b, _q8_1_row([1.0], [-1.0], q)) == 63.0
 
 
 # ------------------------------------------------------------ geglu
