@@ -197,21 +197,35 @@ __global__ __launch_bounds__(64) void k_topk(float * __restrict__ probs, int E, 
     const int lane = threadIdx.x, t = blockIdx.x;
     float * row = probs + (int64_t)t * E;
     float v[4];
+    if (parts) {
+        // every partial of the token's experts in flight before the first
+        // sum (the 64-expert quarters are wave-uniform), then the sums in
+        // split order
+        float pv[4][RSPLIT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j;
-        if (e >= E) {
-            v[j] = -INFINITY;
-        } else if (parts) {
-            float pv[RSPLIT];
+        for (int j = 0; j < 4; ++j)
+            if (64 * j < E) {
+                const int e = min(lane + 64 * j, E - 1);
 #pragma unroll
-            for (int q = 0; q < RSPLIT; ++q) pv[q] = parts[((int64_t)q * T + t) * E + e];
-            float a = pv[0];
+                for (int q = 0; q < RSPLIT; ++q) pv[j][q] = parts[((int64_t)q * T + t) * E + e];
+            }
 #pragma unroll
-            for (int q = 1; q < RSPLIT; ++q) a += pv[q];
-            v[j] = bias ? a + bias[e] : a;
-        } else {
-            v[j] = row[e];
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            if (e >= E) {
+                v[j] = -INFINITY;
+            } else {
+                float a = pv[j][0];
+#pragma unroll
+                for (int q = 1; q < RSPLIT; ++q) a += pv[j][q];
+                v[j] = bias ? a + bias[e] : a;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j;
+            v[j] = e < E ? row[e] : -INFINITY;
         }
     }
     const float mx = wave_max_dpp(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
